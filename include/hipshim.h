@@ -1,0 +1,84 @@
+/* C ABI of the HIP runtime shim used by hip_runtime (ctypes).
+ *
+ * The shim is the MI355X replacement for the CuPy objects the reference's CUDA
+ * runtime drives from Python: cupy.RawKernel JIT + launch
+ * (reference cuda_runtime/cuda_executor.py:38-51, 166-168), cupy.cuda.Device and
+ * its synchronize() (cuda_runtime/cuda_backend.py:97-101, 148-150), and the
+ * host<->device copies behind CUDABuffer.from_numpy/to_numpy
+ * (cuda_runtime/cuda_backend.py:52-91). Device memory itself is allocated by
+ * PyTorch-ROCm; the shim only receives raw device pointers and never frees them.
+ *
+ * Conventions: every entry point returns 0 on success or a hipError_t /
+ * hiprtcResult value (hiprtc results offset by 10000) and never aborts; the text
+ * of the last failure on the calling thread is available from hs_last_error().
+ * Handles are opaque pointers. Nothing here is thread-safe per stream.
+ */
+#ifndef HIPSHIM_H
+#define HIPSHIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One prebuilt kernel launch: function, grid, block, dynamic LDS and the packed
+ * kernarg segment (the by-value argument struct). */
+typedef struct hs_launch_rec {
+  void* fn;
+  uint32_t grid[3];
+  uint32_t block[3];
+  uint32_t lds_bytes;
+  uint32_t kernarg_size;
+  const void* kernarg;
+} hs_launch_rec;
+
+/* Select the device and create its primary context (replaces cp.cuda.Device(id)). */
+int hs_init(int device);
+int hs_device_count(int* count);
+const char* hs_last_error(void);
+
+/* Code objects (replace cupy.RawKernel's NVRTC module + function lookup). */
+int hs_module_load(const void* image, size_t size, void** module);
+int hs_module_unload(void* module);
+int hs_module_function(void* module, const char* name, void** fn);
+
+/* Runtime compilation of generated kernels with hiprtc (replaces NVRTC). The
+ * returned image and log are malloc'd; release them with hs_free_host. */
+int hs_rtc_compile(const char* source, const char* name, const char* arch, const char* include_dir,
+                   void** image, size_t* image_size, char** log);
+void hs_free_host(void* p);
+
+/* Launches: one kernel, a prebuilt list replayed in one call, or a list captured
+ * once into a HIP graph and relaunched (the reference's per-step Python dispatch
+ * loop, cuda_executor.py:166-168, becomes one call per step). */
+int hs_launch(void* fn, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t by, uint32_t bz,
+              uint32_t lds_bytes, void* stream, const void* kernarg, size_t kernarg_size);
+int hs_replay(const hs_launch_rec* recs, size_t n, void* stream);
+int hs_graph_capture(const hs_launch_rec* recs, size_t n, void* stream, void** graph_exec);
+int hs_graph_launch(void* graph_exec, void* stream);
+int hs_graph_destroy(void* graph_exec);
+
+/* Streams, events and copies. A NULL stream is the legacy default stream. */
+int hs_stream_create(void** stream);
+int hs_stream_destroy(void* stream);
+int hs_stream_sync(void* stream);
+int hs_device_sync(void);
+int hs_event_create(void** event);
+int hs_event_destroy(void* event);
+int hs_event_record(void* event, void* stream);
+int hs_event_sync(void* event);
+int hs_event_elapsed_ms(void* start, void* stop, float* ms);
+int hs_memcpy_htod(void* dst, const void* src, size_t n, void* stream);
+int hs_memcpy_dtoh(void* dst, const void* src, size_t n, void* stream);
+int hs_memcpy_dtod(void* dst, const void* src, size_t n, void* stream);
+
+/* sizeof() of the kernel argument struct with the given name (e.g. "LinearArgs"),
+ * or 0 when unknown; lets the host check its ctypes mirrors. */
+size_t hs_argsize(const char* struct_name);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HIPSHIM_H */

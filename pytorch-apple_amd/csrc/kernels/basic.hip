@@ -1,0 +1,223 @@
+// Bandwidth-bound utility kernels for gfx950: strided copy/cast, fill, RMSNorm,
+// embedding gather, rotary tables, in-place index_copy, masked softmax, last-dim
+// mean and argmax, and a plain batched matmul for shapes no pattern claims.
+// All arithmetic is fp32 with one rounding to the output dtype per IR op, the
+// rounding points of ATen on the CPU.
+#include "common.h"
+
+// ---------------------------------------------------------------- copy / cast / fill
+
+extern "C" __global__ void __launch_bounds__(256) k_copy(const CopyArgs a) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+    long long rem = i, so = 0, dof = 0;
+    for (int d = a.ndim - 1; d >= 0; --d) {
+      const long long c = rem % a.shape[d];
+      rem /= a.shape[d];
+      so += c * a.sstride[d];
+      dof += c * a.dstride[d];
+    }
+    if (a.sdtype == a.ddtype && (a.sdtype == HS_I64 || a.sdtype == HS_F64)) {
+      ((long long*)a.dst)[dof] = ((const long long*)a.src)[so];
+    } else if (a.sdtype == a.ddtype && (a.sdtype == HS_BF16 || a.sdtype == HS_F16)) {
+      ((uint16_t*)a.dst)[dof] = ((const uint16_t*)a.src)[so];
+    } else if (a.ddtype == HS_I64 || a.ddtype == HS_I32) {
+      const long long v = (a.sdtype == HS_I64 || a.sdtype == HS_I32 || a.sdtype == HS_U8)
+                              ? ld_i(a.src, so, a.sdtype) : (long long)ld_f(a.src, so, a.sdtype);
+      if (a.ddtype == HS_I64) ((long long*)a.dst)[dof] = v; else ((int*)a.dst)[dof] = (int)v;
+    } else {
+      st_f(a.dst, dof, a.ddtype, ld_f(a.src, so, a.sdtype));
+    }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) k_fill(const FillArgs a) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
+    if (a.dtype == HS_I64) ((long long*)a.out)[i] = (long long)a.value;
+    else if (a.dtype == HS_F64) ((double*)a.out)[i] = a.value;
+    else st_f(a.out, i, a.dtype, (float)a.value);
+  }
+}
+
+// ---------------------------------------------------------------- RMSNorm
+
+// One 256-thread workgroup per row:
+//   h = f32(x); r = rsqrt(mean(h*h) + eps); n = round_n(h*r); out = round_out(w * n)
+extern "C" __global__ void __launch_bounds__(256) k_rmsnorm(const RMSNormArgs a) {
+  __shared__ float red[4];
+  const long long row = blockIdx.x;
+  if (row >= a.rows) return;
+  const void* x = (const char*)a.x + row * a.ldx * (a.x_dtype == HS_F32 ? 4 : 2);
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < a.cols; c += 256) {
+    const float h = ld_f(x, c, a.x_dtype);
+    ss += h * h;
+  }
+  ss = block_sum256(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+  void* out = (char*)a.out + row * a.ldo * (a.out_dtype == HS_F32 ? 4 : 2);
+  for (int c = threadIdx.x; c < a.cols; c += 256) {
+    const float n = round_to(ld_f(x, c, a.x_dtype) * r, a.n_dtype);
+    st_f(out, c, a.out_dtype, ld_f(a.w, c, a.w_dtype) * n);
+  }
+}
+
+// ---------------------------------------------------------------- embedding gather (bit-exact)
+
+extern "C" __global__ void __launch_bounds__(256) k_embedding(const EmbeddingArgs a) {
+  const long long s = blockIdx.x;
+  if (s >= a.n_ids) return;
+  const long long id = ld_i(a.ids, s, a.ids_dtype);
+  char* dst = (char*)a.out + s * a.row_bytes;
+  const bool ok = id >= 0 && id < a.vocab;
+  const char* src = (const char*)a.w + (ok ? id : 0) * a.row_bytes;
+  if ((a.row_bytes & 15) == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0) {
+    const long long nv = a.row_bytes >> 4;
+    for (long long i = threadIdx.x; i < nv; i += blockDim.x) {
+      uint4 v = ok ? ((const uint4*)src)[i] : make_uint4(0, 0, 0, 0);
+      ((uint4*)dst)[i] = v;
+    }
+  } else {
+    for (long long i = threadIdx.x; i < a.row_bytes; i += blockDim.x) dst[i] = ok ? src[i] : 0;
+  }
+}
+
+// ---------------------------------------------------------------- rotary tables
+
+// cos/sin[s, j] = cos/sin(inv_freq[j % half] * float(pos[s])) * scaling, rounded to out_dtype
+extern "C" __global__ void __launch_bounds__(256) k_rope_table(const RopeTableArgs a) {
+  const long long s = blockIdx.x;
+  const int j = threadIdx.x;
+  if (s >= a.S || j >= 2 * a.half) return;
+  const float p = (float)ld_i(a.pos, s, a.pos_dtype);
+  const float f = a.inv_freq[j % a.half] * p;
+  st_f(a.cos_out, s * 2 * a.half + j, a.out_dtype, cosf(f) * a.scaling);
+  st_f(a.sin_out, s * 2 * a.half + j, a.out_dtype, sinf(f) * a.scaling);
+}
+
+// ---------------------------------------------------------------- index_copy (in place, bit-exact)
+
+// dst[o, index[j], i] = src[o, j, i]; indices outside [0, dim_size) are skipped.
+extern "C" __global__ void __launch_bounds__(256) k_index_copy(const IndexCopyArgs a) {
+  const long long total = a.outer * a.nidx * a.inner;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const long long i = t % a.inner;
+    const long long j = (t / a.inner) % a.nidx;
+    const long long o = t / (a.inner * a.nidx);
+    const long long idx = ld_i(a.index, j, a.idx_dtype);
+    if (idx < 0 || idx >= a.dim_size) continue;
+    const long long so = o * a.src_so + j * a.src_sj + i * a.src_si;
+    const long long dof = (o * a.dim_size + idx) * a.inner + i;
+    if (a.elem_bytes == 2) ((uint16_t*)a.dst)[dof] = ((const uint16_t*)a.src)[so];
+    else if (a.elem_bytes == 4) ((uint32_t*)a.dst)[dof] = ((const uint32_t*)a.src)[so];
+    else ((uint64_t*)a.dst)[dof] = ((const uint64_t*)a.src)[so];
+  }
+}
+
+// ---------------------------------------------------------------- softmax over the last dim
+
+// a = round_add(x + mask) (when masked), then out = exp(a - max) / sum, fp32 inside.
+extern "C" __global__ void __launch_bounds__(256) k_softmax(const SoftmaxArgs a) {
+  __shared__ float red[4];
+  const long long row = blockIdx.x;
+  if (row >= a.rows) return;
+  long long rem = row, xo = 0, mo = 0;
+  for (int d = a.nlead - 1; d >= 0; --d) {
+    const long long c = rem % a.lead_shape[d];
+    rem /= a.lead_shape[d];
+    xo += c * a.x_lead_stride[d];
+    mo += c * a.mask_lead_stride[d];
+  }
+  auto val = [&](long long c) -> float {
+    float v = ld_f(a.x, xo + c, a.x_dtype);
+    if (a.has_mask) v = round_to(v + ld_f(a.mask, mo + c * a.mask_col_stride, a.mask_dtype), a.add_dtype);
+    return v;
+  };
+  float m = -INFINITY;
+  for (long long c = threadIdx.x; c < a.cols; c += 256) m = fmaxf(m, val(c));
+  m = block_max256(m, red);
+  float s = 0.f;
+  for (long long c = threadIdx.x; c < a.cols; c += 256) s += expf(val(c) - m);
+  s = block_sum256(s, red);
+  const float inv = 1.0f / s;
+  for (long long c = threadIdx.x; c < a.cols; c += 256)
+    st_f(a.out, row * a.cols + c, a.out_dtype, expf(val(c) - m) * inv);
+}
+
+// ---------------------------------------------------------------- last-dim mean / argmax
+
+extern "C" __global__ void __launch_bounds__(256) k_mean_last(const ReduceLastArgs a) {
+  __shared__ float red[4];
+  const long long row = blockIdx.x;
+  if (row >= a.rows) return;
+  float s = 0.f;
+  for (long long c = threadIdx.x; c < a.cols; c += 256) s += ld_f(a.x, row * a.cols + c, a.x_dtype);
+  s = block_sum256(s, red);
+  if (threadIdx.x == 0) st_f(a.out, row, a.out_dtype, s / (float)a.cols);
+}
+
+// first index of the maximum (np.argmax / torch.argmax tie rule); NaN counts as maximum
+extern "C" __global__ void __launch_bounds__(256) k_argmax(const ReduceLastArgs a) {
+  __shared__ float sv[256];
+  __shared__ long long si[256];
+  const long long row = blockIdx.x;
+  if (row >= a.rows) return;
+  float best = -INFINITY;
+  long long bi = -1;
+  for (long long c = threadIdx.x; c < a.cols; c += 256) {
+    const float v = ld_f(a.x, row * a.cols + c, a.x_dtype);
+    if (bi < 0 || v > best || (v != v && best == best)) { best = v; bi = c; }
+  }
+  sv[threadIdx.x] = best;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      const float v2 = sv[threadIdx.x + o];
+      const long long i2 = si[threadIdx.x + o];
+      const float v1 = sv[threadIdx.x];
+      const long long i1 = si[threadIdx.x];
+      bool take = false;
+      if (i2 >= 0) {
+        if (i1 < 0) take = true;
+        else if (v1 != v1) take = (v2 != v2) && i2 < i1;
+        else if (v2 != v2) take = true;
+        else take = v2 > v1 || (v2 == v1 && i2 < i1);
+      }
+      if (take) { sv[threadIdx.x] = v2; si[threadIdx.x] = i2; }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (a.out_dtype == HS_I64) ((long long*)a.out)[row] = si[0];
+    else ((int*)a.out)[row] = (int)si[0];
+  }
+}
+
+// ---------------------------------------------------------------- generic batched matmul
+
+// One output element per thread, fp32 accumulation, one rounding. For shapes that
+// no fused kernel claims (e.g. unpatterned attention); not a performance path.
+extern "C" __global__ void __launch_bounds__(256) k_bmm(const BmmArgs a) {
+  long long nb = 1;
+  for (int d = 0; d < a.nbatch; ++d) nb *= a.batch_shape[d];
+  const long long total = nb * a.M * a.N;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+    const long long n = t % a.N;
+    const long long m = (t / a.N) % a.M;
+    long long b = t / (a.N * a.M), ao = 0, bo = 0;
+    for (int d = a.nbatch - 1; d >= 0; --d) {
+      const long long c = b % a.batch_shape[d];
+      b /= a.batch_shape[d];
+      ao += c * a.a_bstride[d];
+      bo += c * a.b_bstride[d];
+    }
+    float acc = 0.f;
+    for (long long k = 0; k < a.K; ++k)
+      acc += ld_f(a.a, ao + m * a.a_sm + k * a.a_sk, a.a_dtype) * ld_f(a.b, bo + k * a.b_sk + n * a.b_sn, a.b_dtype);
+    st_f(a.c, t, a.c_dtype, acc);
+  }
+}

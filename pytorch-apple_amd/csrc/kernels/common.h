@@ -1,0 +1,276 @@
+// Shared definitions for the gfx950 kernels: dtype codes, bf16/fp16 helpers,
+// wave64 reductions and the by-value argument structs of every kernel.
+//
+// Every kernel takes exactly one argument, a struct passed by value, so its
+// kernarg segment is the struct's C layout. The host packs the same layout with
+// ctypes; hs_argsize() in the shim reports sizeof() of each struct so the host
+// can check the two agree. Fields are ordered 8-byte first, then 4-byte, so no
+// implicit padding appears between them.
+#pragma once
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+#endif
+#include <stdint.h>
+
+#define HS_MAXD 6
+
+enum HsDtype { HS_F32 = 0, HS_F16 = 1, HS_BF16 = 2, HS_I64 = 3, HS_I32 = 4, HS_U8 = 5, HS_F64 = 6 };
+
+// ---------------------------------------------------------------- argument structs
+
+struct CopyArgs {            // dst[idx(dshape, dstride)] = cast(src[idx(dshape, sstride)])
+  void* dst;
+  const void* src;
+  long long n;
+  long long shape[HS_MAXD];
+  long long sstride[HS_MAXD];
+  long long dstride[HS_MAXD];
+  int ndim;
+  int sdtype;
+  int ddtype;
+  int pad;
+};
+
+struct FillArgs {
+  void* out;
+  long long n;
+  double value;
+  int dtype;
+  int pad;
+};
+
+struct RMSNormArgs {          // out = w * round_n(x * rsqrt(mean(x^2) + eps)), one row per workgroup
+  const void* x;
+  const void* w;
+  void* out;
+  long long rows;
+  long long ldx;
+  long long ldo;
+  int cols;
+  float eps;
+  int x_dtype;
+  int w_dtype;
+  int n_dtype;
+  int out_dtype;
+};
+
+struct EmbeddingArgs {        // out[s, :] = w[ids[s], :]
+  const void* w;
+  const void* ids;
+  void* out;
+  long long n_ids;
+  long long vocab;
+  long long row_bytes;
+  int ids_dtype;
+  int pad;
+};
+
+struct RopeTableArgs {        // cos/sin[s, j] for j < 2*half from inv_freq[j % half] * pos[s]
+  const float* inv_freq;
+  const void* pos;
+  void* cos_out;
+  void* sin_out;
+  long long S;
+  int half;
+  int pos_dtype;
+  int out_dtype;
+  float scaling;
+};
+
+struct IndexCopyArgs {        // dst[o, index[j], i] = src[o*s_o + j*s_j + i*s_i]
+  void* dst;
+  const void* src;
+  const void* index;
+  long long outer;
+  long long dim_size;
+  long long inner;
+  long long nidx;
+  long long src_so;
+  long long src_sj;
+  long long src_si;
+  int idx_dtype;
+  int elem_bytes;
+};
+
+struct SoftmaxArgs {          // out[row] = softmax(round_a(x[row] + mask[row'])) along the last dim
+  const void* x;
+  const void* mask;
+  void* out;
+  long long rows;
+  long long cols;
+  long long lead_shape[5];
+  long long x_lead_stride[5];
+  long long mask_lead_stride[5];
+  long long mask_col_stride;
+  int nlead;
+  int x_dtype;
+  int mask_dtype;
+  int add_dtype;
+  int out_dtype;
+  int has_mask;
+};
+
+struct ReduceLastArgs {       // mean / argmax over the last dim of a [rows, cols] contiguous view
+  const void* x;
+  void* out;
+  long long rows;
+  long long cols;
+  int x_dtype;
+  int out_dtype;
+};
+
+struct BmmArgs {              // c[b, m, n] = sum_k a[b, m, k] * b[b, k, n] (strided, broadcast batch)
+  const void* a;
+  const void* b;
+  void* c;
+  long long batch_shape[4];
+  long long a_bstride[4];
+  long long b_bstride[4];
+  long long M;
+  long long N;
+  long long K;
+  long long a_sm, a_sk, b_sk, b_sn;
+  int nbatch;
+  int a_dtype;
+  int b_dtype;
+  int c_dtype;
+};
+
+struct LinearArgs {           // out[m, n] = round(x[m, :] . w[n, :] + bias[n])   (bf16/fp16, K % 8 == 0)
+  const void* x;
+  const void* w;
+  const void* bias;
+  void* out;
+  const void* resid;          // optional residual: out = round(resid + round(linear))
+  long long M;
+  long long ldx;
+  long long ldo;
+  long long ldr;
+  int N;
+  int K;
+  int dtype;                  // HS_BF16 or HS_F16 for x, w, bias, out and resid alike
+  int has_bias;
+  int has_resid;
+  int pad;
+};
+
+struct FusedArgs {            // generated elementwise chains: out[i] = chain(in0..in7 at strided offsets)
+  void* out;
+  const void* in[8];
+  long long n;
+};
+
+struct DecodeAttnArgs {       // GQA decode attention over static caches, split over KV tiles
+  const void* q;              // [H, D] (query heads contiguous, D contiguous)
+  const void* k;              // [KVH, S, D]
+  const void* v;              // [KVH, S, D]
+  const void* mask;           // [S] with stride mask_stride (broadcast over heads)
+  void* out;                  // [H, D]
+  float* scores;              // scratch [H, S]
+  float* stats;               // scratch [H, ntiles, 2]
+  float* part;                // scratch [KVH, ntiles, G, D]
+  int* counters;              // scratch [KVH], zero between launches
+  long long S;
+  long long q_head_stride;
+  long long kv_head_stride;
+  long long mask_stride;
+  int H;
+  int KVH;
+  int D;
+  int ntiles;
+  float scale;
+  int mask_dtype;             // HS_BF16 / HS_F16 / HS_F32, or -1 for no mask
+  int add_dtype;              // dtype of scores + mask in the model (rounding point)
+  int dtype;                  // q/k/v/out dtype (HS_BF16 or HS_F16)
+};
+
+#ifdef __HIPCC__
+// ---------------------------------------------------------------- device helpers
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {   // round to nearest even, quiet NaN
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+// value of element i of a typed buffer, as float
+__device__ __forceinline__ float ld_f(const void* p, long long i, int dt) {
+  switch (dt) {
+    case HS_F32: return ((const float*)p)[i];
+    case HS_F16: return f16_to_f32(((const uint16_t*)p)[i]);
+    case HS_BF16: return bf16_to_f32(((const uint16_t*)p)[i]);
+    case HS_I64: return (float)((const long long*)p)[i];
+    case HS_I32: return (float)((const int*)p)[i];
+    case HS_U8: return (float)((const unsigned char*)p)[i];
+    case HS_F64: return (float)((const double*)p)[i];
+  }
+  return 0.f;
+}
+
+__device__ __forceinline__ long long ld_i(const void* p, long long i, int dt) {
+  switch (dt) {
+    case HS_I64: return ((const long long*)p)[i];
+    case HS_I32: return ((const int*)p)[i];
+    case HS_U8: return ((const unsigned char*)p)[i];
+    case HS_F32: return (long long)((const float*)p)[i];
+  }
+  return 0;
+}
+
+// round a float to the storage precision of dt (identity for fp32)
+__device__ __forceinline__ float round_to(float f, int dt) {
+  if (dt == HS_BF16) return bf16_to_f32(f32_to_bf16(f));
+  if (dt == HS_F16) return f16_to_f32(f32_to_f16(f));
+  return f;
+}
+
+__device__ __forceinline__ void st_f(void* p, long long i, int dt, float f) {
+  switch (dt) {
+    case HS_F32: ((float*)p)[i] = f; break;
+    case HS_F16: ((uint16_t*)p)[i] = f32_to_f16(f); break;
+    case HS_BF16: ((uint16_t*)p)[i] = f32_to_bf16(f); break;
+    case HS_I64: ((long long*)p)[i] = (long long)f; break;
+    case HS_I32: ((int*)p)[i] = (int)f; break;
+    case HS_U8: ((unsigned char*)p)[i] = (unsigned char)(f != 0.f); break;
+    case HS_F64: ((double*)p)[i] = (double)f; break;
+  }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// sum over a 256-thread workgroup; every thread gets the result
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  __syncthreads();
+  if (l == 0) red[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+#endif

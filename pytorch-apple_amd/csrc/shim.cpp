@@ -1,0 +1,254 @@
+// HIP runtime shim: the C ABI declared in include/hipshim.h.
+#include "../../include/hipshim.h"
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels/common.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail_hip(hipError_t e, const char* what) {
+  g_err = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  return (int)e;
+}
+
+#define HS_CHECK(call)                                  \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return fail_hip(e_, #call);   \
+  } while (0)
+
+int launch_one(const hs_launch_rec& r, hipStream_t s) {
+  size_t sz = r.kernarg_size;
+  void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(r.kernarg), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
+                 HIP_LAUNCH_PARAM_END};
+  HS_CHECK(hipModuleLaunchKernel((hipFunction_t)r.fn, r.grid[0], r.grid[1], r.grid[2], r.block[0], r.block[1],
+                                 r.block[2], r.lds_bytes, s, nullptr, cfg));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hs_last_error(void) { return g_err.c_str(); }
+
+int hs_device_count(int* count) {
+  HS_CHECK(hipGetDeviceCount(count));
+  return 0;
+}
+
+int hs_init(int device) {
+  int n = 0;
+  HS_CHECK(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) {
+    g_err = "hs_init: device " + std::to_string(device) + " out of range (" + std::to_string(n) + " devices)";
+    return (int)hipErrorInvalidDevice;
+  }
+  HS_CHECK(hipSetDevice(device));
+  HS_CHECK(hipFree(nullptr));
+  return 0;
+}
+
+int hs_module_load(const void* image, size_t size, void** module) {
+  (void)size;
+  hipModule_t m = nullptr;
+  HS_CHECK(hipModuleLoadData(&m, image));
+  *module = m;
+  return 0;
+}
+
+int hs_module_unload(void* module) {
+  HS_CHECK(hipModuleUnload((hipModule_t)module));
+  return 0;
+}
+
+int hs_module_function(void* module, const char* name, void** fn) {
+  hipFunction_t f = nullptr;
+  hipError_t e = hipModuleGetFunction(&f, (hipModule_t)module, name);
+  if (e != hipSuccess) return fail_hip(e, (std::string("hipModuleGetFunction ") + name).c_str());
+  *fn = f;
+  return 0;
+}
+
+int hs_rtc_compile(const char* source, const char* name, const char* arch, const char* include_dir, void** image,
+                   size_t* image_size, char** log) {
+  *image = nullptr;
+  *image_size = 0;
+  if (log) *log = nullptr;
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, source, name, 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS) {
+    g_err = std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r);
+    return 10000 + (int)r;
+  }
+  std::string arch_opt = std::string("--offload-arch=") + (arch ? arch : "gfx950");
+  std::string inc_opt = std::string("-I") + (include_dir ? include_dir : ".");
+  std::vector<const char*> opts = {arch_opt.c_str(), inc_opt.c_str(), "-O3", "-std=c++17", "-mllvm",
+                                   "-amdgpu-early-inline-all=true"};
+  r = hiprtcCompileProgram(prog, (int)opts.size(), opts.data());
+  size_t log_size = 0;
+  hiprtcGetProgramLogSize(prog, &log_size);
+  if (log && log_size > 1) {
+    *log = (char*)malloc(log_size + 1);
+    hiprtcGetProgramLog(prog, *log);
+    (*log)[log_size] = 0;
+  }
+  if (r != HIPRTC_SUCCESS) {
+    g_err = std::string("hiprtcCompileProgram: ") + hiprtcGetErrorString(r);
+    hiprtcDestroyProgram(&prog);
+    return 10000 + (int)r;
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  void* buf = malloc(n);
+  hiprtcGetCode(prog, (char*)buf);
+  hiprtcDestroyProgram(&prog);
+  *image = buf;
+  *image_size = n;
+  return 0;
+}
+
+void hs_free_host(void* p) { free(p); }
+
+int hs_launch(void* fn, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t by, uint32_t bz,
+              uint32_t lds_bytes, void* stream, const void* kernarg, size_t kernarg_size) {
+  hs_launch_rec r{fn, {gx, gy, gz}, {bx, by, bz}, lds_bytes, (uint32_t)kernarg_size, kernarg};
+  return launch_one(r, (hipStream_t)stream);
+}
+
+int hs_replay(const hs_launch_rec* recs, size_t n, void* stream) {
+  for (size_t i = 0; i < n; ++i) {
+    int rc = launch_one(recs[i], (hipStream_t)stream);
+    if (rc) {
+      g_err = "launch " + std::to_string(i) + ": " + g_err;
+      return rc;
+    }
+  }
+  return 0;
+}
+
+int hs_graph_capture(const hs_launch_rec* recs, size_t n, void* stream, void** graph_exec) {
+  hipStream_t s = (hipStream_t)stream;
+  HS_CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = 0;
+  for (size_t i = 0; i < n && rc == 0; ++i) rc = launch_one(recs[i], s);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(s, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return fail_hip(e, "hipStreamEndCapture");
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return fail_hip(e, "hipGraphInstantiate");
+  *graph_exec = ex;
+  return 0;
+}
+
+int hs_graph_launch(void* graph_exec, void* stream) {
+  HS_CHECK(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
+  return 0;
+}
+
+int hs_graph_destroy(void* graph_exec) {
+  HS_CHECK(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+  return 0;
+}
+
+int hs_stream_create(void** stream) {
+  hipStream_t s;
+  HS_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *stream = s;
+  return 0;
+}
+
+int hs_stream_destroy(void* stream) {
+  HS_CHECK(hipStreamDestroy((hipStream_t)stream));
+  return 0;
+}
+
+int hs_stream_sync(void* stream) {
+  HS_CHECK(hipStreamSynchronize((hipStream_t)stream));
+  return 0;
+}
+
+int hs_device_sync(void) {
+  HS_CHECK(hipDeviceSynchronize());
+  return 0;
+}
+
+int hs_event_create(void** event) {
+  hipEvent_t e;
+  HS_CHECK(hipEventCreate(&e));
+  *event = e;
+  return 0;
+}
+
+int hs_event_destroy(void* event) {
+  HS_CHECK(hipEventDestroy((hipEvent_t)event));
+  return 0;
+}
+
+int hs_event_record(void* event, void* stream) {
+  HS_CHECK(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+  return 0;
+}
+
+int hs_event_sync(void* event) {
+  HS_CHECK(hipEventSynchronize((hipEvent_t)event));
+  return 0;
+}
+
+int hs_event_elapsed_ms(void* start, void* stop, float* ms) {
+  HS_CHECK(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+  return 0;
+}
+
+int hs_memcpy_htod(void* dst, const void* src, size_t n, void* stream) {
+  HS_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, (hipStream_t)stream));
+  return 0;
+}
+
+int hs_memcpy_dtoh(void* dst, const void* src, size_t n, void* stream) {
+  HS_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, (hipStream_t)stream));
+  HS_CHECK(hipStreamSynchronize((hipStream_t)stream));
+  return 0;
+}
+
+int hs_memcpy_dtod(void* dst, const void* src, size_t n, void* stream) {
+  HS_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+  return 0;
+}
+
+size_t hs_argsize(const char* s) {
+#define HS_SZ(T) \
+  if (!strcmp(s, #T)) return sizeof(T);
+  HS_SZ(CopyArgs)
+  HS_SZ(FillArgs)
+  HS_SZ(RMSNormArgs)
+  HS_SZ(EmbeddingArgs)
+  HS_SZ(RopeTableArgs)
+  HS_SZ(IndexCopyArgs)
+  HS_SZ(SoftmaxArgs)
+  HS_SZ(ReduceLastArgs)
+  HS_SZ(BmmArgs)
+  HS_SZ(LinearArgs)
+  HS_SZ(DecodeAttnArgs)
+  HS_SZ(FusedArgs)
+#undef HS_SZ
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,641 @@
+"""Subgraph analyzer: IR graph → ordered launch steps over views and arena storages.
+
+Counterpart of the reference's ``analyze_subgraph`` (`cuda_compiler/subgraph_analyzer.py:797-981`).
+The algorithm keeps the reference's shape — pattern pre-passes first, then one
+walk over the nodes in topological order that classifies each op and greedily
+grows elementwise chains — with MI355X-specific choices:
+
+* pattern pre-passes (`patterns.py`) claim RMSNorm chains (reference cs:667-756),
+  add+softmax (cs:759-789) and the whole GQA decode-attention chain (the span of
+  cs:85-160 plus the scale/mask/softmax steps between the two matmuls);
+* shape ops never launch: they map a ``TView`` to a ``TView`` (``views.py``);
+* a chain grows while the new elementwise node reads the chain's current tail, the
+  tail has exactly one consumer and the output shape is unchanged (the reference's
+  rule, cs:984-1013); operands may broadcast (stride 0), fixing defect D3;
+* chains are emitted lazily, when something first needs their value, so the step
+  list is already in dependency order (the reference re-sorts with Kahn's
+  algorithm afterwards, cs:1047-1091);
+* an ``index_copy`` whose target is a graph input read by nothing else updates that
+  input in place (the reference copies the whole cache every step, defect D7).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+from hip_compiler import views as V
+from hip_compiler.codegen import MAX_CHAIN_INPUTS, ChainOp, generate_chain
+from hip_compiler.op_classify import OpCategory, classify_op
+from hip_compiler.program import (DTYPE_CODE, ELEM_SIZE, FLOAT_DTYPES, LaunchStep, Ref, Storage, TView,
+                                  contiguous_strides, numel)
+from npu_compiler.ir_reader import IRGraph, OpNode
+
+HS_BF16, HS_F16 = DTYPE_CODE["bfloat16"], DTYPE_CODE["float16"]
+
+
+def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
+    return (max(1, min(cap, (int(n) + block - 1) // block)), 1, 1)
+
+
+@dataclass
+class _Chain:
+    ops: list[ChainOp] = field(default_factory=list)
+    ext: list[TView] = field(default_factory=list)
+    ext_names: list[str] = field(default_factory=list)
+    node_names: list[str] = field(default_factory=list)
+    tail: str = ""
+    shape: tuple[int, ...] = ()
+    dtype: str = "float32"
+
+
+class Lowering:
+    """Lowers one IR graph; ``steps``, ``storages`` and ``views`` are the result."""
+
+    def __init__(self, graph: IRGraph, inplace_inputs: bool = True):
+        self.g = graph
+        self.inplace_inputs = inplace_inputs
+        self.steps: list[LaunchStep] = []
+        self.storages: dict[str, Storage] = {}
+        self.views: dict[str, TView] = {}
+        self.kernel_sources: dict[str, str] = {}
+        self.consumers: dict[str, list[OpNode]] = {}
+        self.producer: dict[str, OpNode] = {}
+        for n in graph.nodes:
+            for t in n.inputs:
+                self.consumers.setdefault(t.name, []).append(n)
+            for t in n.outputs:
+                self.producer[t.name] = n
+        self.chains: dict[str, _Chain] = {}
+        self.claimed: dict[str, object] = {}     # node name -> pattern emitter (at its last node) or None
+        self.graph_output_names = {o.name for o in graph.graph_outputs}
+        self.mutated_inputs: set[str] = set()
+        self._uid = 0
+        for spec in graph.graph_inputs:
+            self._external(spec.name, spec.shape, spec.dtype, "input")
+        for ph, sd in graph.weight_name_mapping.items():
+            w = next((w for w in graph.weights if w.name == sd), None)
+            if w is not None:
+                self._external(ph, w.shape, w.dtype, "weight")
+        for w in graph.weights:
+            if w.name not in self.views:
+                self._external(w.name, w.shape, w.dtype, "weight")
+
+    # ------------------------------------------------------------------ storages and views
+
+    def _external(self, name: str, shape, dtype: str, kind: str) -> None:
+        shape = tuple(int(s) for s in shape)
+        self.storages[name] = Storage(name, kind, numel(shape) * ELEM_SIZE[dtype], dtype)
+        self.views[name] = TView(name, 0, shape, contiguous_strides(shape), dtype)
+
+    def new_storage(self, name: str, shape, dtype: str, kind: str = "arena") -> TView:
+        shape = tuple(int(s) for s in shape)
+        key = name
+        while key in self.storages:
+            self._uid += 1
+            key = f"{name}#{self._uid}"
+        self.storages[key] = Storage(key, kind, max(numel(shape) * ELEM_SIZE[dtype], 1), dtype)
+        return TView(key, 0, shape, contiguous_strides(shape), dtype)
+
+    def scratch(self, name: str, nbytes: int, persistent: bool = False) -> Ref:
+        key = name
+        while key in self.storages:
+            self._uid += 1
+            key = f"{name}#{self._uid}"
+        self.storages[key] = Storage(key, "persistent" if persistent else "arena", max(int(nbytes), 4), "uint8",
+                                     zero_init=persistent)
+        return Ref(key, 0)
+
+    @staticmethod
+    def ref(v: TView) -> Ref:
+        return Ref(v.storage, v.offset * ELEM_SIZE[v.dtype])
+
+    def view(self, name: str) -> TView:
+        if name in self.chains:
+            self.flush_chain(name)
+        if name not in self.views:
+            raise KeyError(f"tensor {name} has no value (producer not lowered)")
+        return self.views[name]
+
+    def contiguous(self, name: str, v: TView | None = None) -> TView:
+        """A contiguous view with the value of ``name`` (copying when needed)."""
+        v = v or self.view(name)
+        if v.is_contiguous():
+            return v
+        out = self.new_storage(name + ".c", v.shape, v.dtype)
+        self.emit_copy(v, out, [name], [name + ".c"])
+        return out
+
+    def emit(self, step: LaunchStep) -> None:
+        self.steps.append(step)
+
+    def emit_copy(self, src: TView, dst: TView, ins: list[str], outs: list[str]) -> None:
+        nd = len(src.shape)
+        if nd > 6:
+            raise NotImplementedError("copy of rank > 6")
+        shape = list(src.shape) + [1] * (6 - nd)
+        ss = list(src.strides) + [0] * (6 - nd)
+        ds = list(dst.strides) + [0] * (6 - nd)
+        n = src.numel
+        self.emit(LaunchStep(
+            kind="copy", kernel="k_copy", module="basic", arg_struct="CopyArgs",
+            args=dict(dst=self.ref(dst), src=self.ref(src), n=n, shape=shape, sstride=ss, dstride=ds,
+                      ndim=max(nd, 1), sdtype=DTYPE_CODE[src.dtype], ddtype=DTYPE_CODE[dst.dtype]),
+            grid=grid1d(n), inputs=ins, outputs=outs, params={"total": n}))
+
+    # ------------------------------------------------------------------ elementwise chains
+
+    def flush_chain(self, tail: str) -> None:
+        ch = self.chains.pop(tail)
+        out = self.new_storage(tail, ch.shape, ch.dtype)
+        name, src = generate_chain(ch.ops, ch.ext, ch.shape, ch.dtype)
+        self.kernel_sources[name] = src
+        n = numel(ch.shape)
+        ptrs = [self.ref(v) for v in ch.ext] + [None] * (MAX_CHAIN_INPUTS - len(ch.ext))
+        self.emit(LaunchStep(
+            kind="fused", kernel=name, module=name, arg_struct="FusedArgs",
+            args=dict(out=self.ref(out), **{"in": ptrs}, n=n), grid=grid1d(n),
+            inputs=list(ch.ext_names), outputs=[tail],
+            params={"total": n, "ops": [o.op_type for o in ch.ops], "nodes": list(ch.node_names)}))
+        self.views[tail] = out
+
+    def flush_chains_reading(self, storage: str) -> None:
+        for tail in [t for t, ch in self.chains.items() if any(v.storage == storage for v in ch.ext)]:
+            if tail in self.chains:
+                self.flush_chain(tail)
+
+    def lower_elementwise(self, node: OpNode) -> None:
+        out = node.outputs[0]
+        shape = tuple(out.shape)
+        if node.op_type == "aten.to.dtype" or node.op_type == "aten._to_copy.default":
+            src = node.inputs[0]
+            if src.dtype == out.dtype and src.name not in self.chains:
+                self.views[out.name] = self.view(src.name)
+                return
+        ext_inputs = [t for t in node.inputs]
+        # extend an open chain whose tail this node reads (single consumer, same shape)
+        chain = None
+        for t in ext_inputs:
+            ch = self.chains.get(t.name)
+            if ch is not None and len(self.consumers.get(t.name, [])) == 1 and ch.shape == shape:
+                new_ext = {x.name for x in ext_inputs if x.name != t.name and x.name not in ch.ext_names}
+                if len(ch.ext) + len(new_ext) <= MAX_CHAIN_INPUTS:
+                    chain = ch
+                    break
+        if chain is None:
+            chain = _Chain(shape=shape)
+        else:
+            del self.chains[chain.tail]
+        operands = []
+        for t in ext_inputs:
+            if t.name == chain.tail and chain.ops:
+                operands.append(("val", len(chain.ops) - 1))
+                continue
+            if t.name in chain.ext_names:
+                operands.append(("ext", chain.ext_names.index(t.name)))
+                continue
+            v = self.view(t.name)
+            try:
+                v = V.broadcast_to(v, shape)
+            except Exception as e:  # pragma: no cover - malformed IR
+                raise ValueError(f"{node.name}: cannot broadcast {t.name} {v.shape} to {shape}") from e
+            chain.ext.append(v)
+            chain.ext_names.append(t.name)
+            operands.append(("ext", len(chain.ext) - 1))
+        attrs = dict(node.attrs)
+        if node.op_type in ("aten.add.Tensor", "aten.add_.Tensor", "aten.sub.Tensor", "aten.mul.Tensor",
+                            "aten.mul_.Tensor", "aten.div.Tensor") and len(operands) == 1:
+            operands.append(("scalar", float(attrs.get("other", 0.0))))
+        chain.ops.append(ChainOp(node.op_type, operands, out.dtype, attrs))
+        chain.node_names.append(node.name)
+        chain.tail = out.name
+        chain.dtype = out.dtype
+        self.chains[out.name] = chain
+
+    # ------------------------------------------------------------------ generic lowering per op
+
+    def lower_alias(self, node: OpNode) -> None:
+        op = node.op_type
+        out = node.outputs[0]
+        if op == "<built-in function getitem>":
+            idx = int(node.attrs.get("index", 0))
+            src = node.inputs[idx] if idx < len(node.inputs) else node.inputs[0]
+            self.views[out.name] = self.view(src.name)
+            return
+        v = self.view(node.inputs[0].name)
+        a = node.attrs
+        if op in ("aten.transpose.int",):
+            nv = V.transpose(v, int(a.get("dim0", 0)), int(a.get("dim1", 1)))
+        elif op == "aten.t.default":
+            nv = V.transpose(v, 0, 1) if len(v.shape) == 2 else v
+        elif op == "aten.permute.default":
+            nv = V.permute(v, a.get("dims"))
+        elif op == "aten.expand.default":
+            nv = V.expand(v, out.shape)
+        elif op == "aten.slice.Tensor":
+            nv = V.slice_(v, int(a.get("dim", 0)), a.get("start", 0), a.get("end", V.INT64_MAX), int(a.get("step", 1)))
+        elif op == "aten.select.int":
+            nv = V.select(v, int(a.get("dim", 0)), int(a.get("index", 0)))
+        elif op in ("aten.alias.default", "aten.detach.default", "aten.detach_.default", "aten.dropout.default"):
+            nv = v
+        elif op == "aten.contiguous.default":
+            nv = v if v.is_contiguous() else None
+        else:  # reshape / view / flatten / unsqueeze / squeeze
+            nv = V.restride(v, out.shape)
+        if nv is None:
+            nv = V.restride(self.contiguous(node.inputs[0].name, v), out.shape)
+        if tuple(nv.shape) != tuple(out.shape):
+            raise ValueError(f"{node.name}: view shape {nv.shape} != declared {out.shape}")
+        self.views[out.name] = nv
+
+    def lower_linear(self, node: OpNode) -> None:
+        x_t, w_t = node.inputs[0], node.inputs[1]
+        b_t = node.inputs[2] if len(node.inputs) > 2 else None
+        out = node.outputs[0]
+        self.emit_linear(x_t.name, w_t.name, b_t.name if b_t else None, out.name, tuple(out.shape), out.dtype,
+                         resid=None, node_names=[node.name])
+
+    def emit_linear(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, out_dtype: str,
+                    resid: str | None, node_names: list[str]) -> None:
+        x = self.contiguous(x_name)
+        w = self.contiguous(w_name)
+        K = x.shape[-1]
+        N = w.shape[0]
+        M = x.numel // K if K else 0
+        ok = (x.dtype == w.dtype == out_dtype and x.dtype in ("bfloat16", "float16") and K % 8 == 0
+              and (x.offset * 2) % 16 == 0 and (w.offset * 2) % 16 == 0)
+        if b_name is not None:
+            ok = ok and self.view(b_name).dtype == out_dtype
+        if not ok:
+            self.emit_linear_generic(x, w, b_name, out_name, out_shape, out_dtype, node_names)
+            if resid is not None:
+                raise NotImplementedError("residual epilogue on the generic path")
+            return
+        o = self.new_storage(out_name, out_shape, out_dtype)
+        bias = self.contiguous(b_name) if b_name is not None else None
+        r = self.contiguous(resid) if resid is not None else None
+        mb, rpw = (1, 4) if M <= 1 else (4, 2)
+        kname = f"k_linear_{'bf16' if out_dtype == 'bfloat16' else 'f16'}_m{mb}"
+        self.emit(LaunchStep(
+            kind="gemm", kernel=kname, module="linear", arg_struct="LinearArgs",
+            args=dict(x=self.ref(x), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
+                      resid=self.ref(r) if r else None, M=M, ldx=K, ldo=N, ldr=N, N=N, K=K,
+                      dtype=DTYPE_CODE[out_dtype], has_bias=int(bias is not None), has_resid=int(r is not None)),
+            grid=((N + 4 * rpw - 1) // (4 * rpw), (M + mb - 1) // mb, 1),
+            inputs=[x_name, w_name] + ([b_name] if b_name else []) + ([resid] if resid else []),
+            outputs=[out_name], params={"M": M, "N": N, "K": K, "has_bias": bias is not None,
+                                        "transpose_b": True, "nodes": node_names}))
+        self.views[out_name] = o
+
+    def emit_linear_generic(self, x: TView, w: TView, b_name, out_name, out_shape, out_dtype, node_names) -> None:
+        K = x.shape[-1]
+        M = x.numel // K
+        N = w.shape[0]
+        xm = V.restride(x, (M, K))
+        wt = V.transpose(w, 0, 1)  # [K, N]
+        tmp_name = out_name if b_name is None else out_name + ".mm"
+        o = self.new_storage(tmp_name, (M, N), out_dtype)
+        self.emit_bmm(xm, wt, o, [], [out_name])
+        res = V.restride(o, out_shape)
+        self.views[tmp_name] = res
+        if b_name is not None:
+            self.chains.pop(tmp_name, None)
+            ch = _Chain(shape=tuple(out_shape), dtype=out_dtype)
+            ch.ext = [res, V.broadcast_to(self.view(b_name), tuple(out_shape))]
+            ch.ext_names = [tmp_name, b_name]
+            ch.ops = [ChainOp("aten.add.Tensor", [("ext", 0), ("ext", 1)], out_dtype, {})]
+            ch.tail = out_name
+            ch.node_names = list(node_names)
+            self.chains[out_name] = ch
+            self.flush_chain(out_name)
+        else:
+            self.views[out_name] = res
+
+    def emit_bmm(self, a: TView, b: TView, c: TView, ins: list[str], outs: list[str]) -> None:
+        """c[..., M, N] = a[..., M, K] @ b[..., K, N] with broadcast batch dims (generic kernel)."""
+        M, K = a.shape[-2], a.shape[-1]
+        N = b.shape[-1]
+        batch = tuple(c.shape[:-2])
+        if len(batch) > 4:
+            raise NotImplementedError("matmul batch rank > 4")
+        ab = V.broadcast_to(a.with_(shape=a.shape[:-2], strides=a.strides[:-2]), batch) if batch else None
+        bb = V.broadcast_to(b.with_(shape=b.shape[:-2], strides=b.strides[:-2]), batch) if batch else None
+        pad = 4 - len(batch)
+        self.emit(LaunchStep(
+            kind="gemm_batched", kernel="k_bmm", module="basic", arg_struct="BmmArgs",
+            args=dict(a=self.ref(a), b=self.ref(b), c=self.ref(c),
+                      batch_shape=list(batch) + [1] * pad,
+                      a_bstride=(list(ab.strides) if ab else []) + [0] * pad,
+                      b_bstride=(list(bb.strides) if bb else []) + [0] * pad,
+                      M=M, N=N, K=K, a_sm=a.strides[-2], a_sk=a.strides[-1], b_sk=b.strides[-2],
+                      b_sn=b.strides[-1], nbatch=len(batch), a_dtype=DTYPE_CODE[a.dtype],
+                      b_dtype=DTYPE_CODE[b.dtype], c_dtype=DTYPE_CODE[c.dtype]),
+            grid=grid1d(c.numel), inputs=ins, outputs=outs,
+            params={"batch": numel(batch), "M": M, "N": N, "K": K}))
+
+    def lower_matmul(self, node: OpNode) -> None:
+        a = self.view(node.inputs[0].name)
+        b = self.view(node.inputs[1].name)
+        out = node.outputs[0]
+        sq_a = len(a.shape) == 1
+        sq_b = len(b.shape) == 1
+        if sq_a:
+            a = a.with_(shape=(1,) + a.shape, strides=(0,) + a.strides)
+        if sq_b:
+            b = b.with_(shape=b.shape + (1,), strides=b.strides + (0,))
+        full = tuple(out.shape)
+        if sq_a:
+            full = full[:-1] + (1, full[-1]) if len(full) else (1, 1)
+        if sq_b:
+            full = full + (1,)
+        o = self.new_storage(out.name, full, out.dtype)
+        self.emit_bmm(a, b, o, [t.name for t in node.inputs], [out.name])
+        self.views[out.name] = V.restride(o, out.shape)
+
+    def lower_addmm(self, node: OpNode) -> None:
+        bias, m1, m2 = (t.name for t in node.inputs[:3])
+        out = node.outputs[0]
+        beta = float(node.attrs.get("beta", 1))
+        alpha = float(node.attrs.get("alpha", 1))
+        w2 = self.view(m2)
+        if beta == 1 and alpha == 1 and len(w2.shape) == 2 and w2.strides == (1, w2.shape[0]):
+            # mat2 is W^T of a contiguous W[N, K]
+            wname = m2 + ".T"
+            self.views[wname] = V.transpose(w2, 0, 1)
+            self.emit_linear(m1, wname, bias, out.name, tuple(out.shape), out.dtype, None, [node.name])
+            return
+        a, b = self.view(m1), self.view(m2)
+        o = self.new_storage(out.name + ".mm", out.shape, out.dtype)
+        self.emit_bmm(a, b, o, [m1, m2], [out.name + ".mm"])
+        self.views[out.name + ".mm"] = o
+        ch = _Chain(shape=tuple(out.shape), dtype=out.dtype)
+        ch.ext = [o, V.broadcast_to(self.view(bias), tuple(out.shape))]
+        ch.ext_names = [out.name + ".mm", bias]
+        ch.ops = [ChainOp("aten.mul.Tensor", [("ext", 0), ("scalar", alpha)], out.dtype, {}),
+                  ChainOp("aten.add.Tensor", [("val", 0), ("ext", 1)], out.dtype, {"alpha": beta})]
+        ch.tail = out.name
+        ch.node_names = [node.name]
+        self.chains[out.name] = ch
+
+    def emit_softmax(self, x_name: str, mask_name: str | None, add_dtype: str, out_name: str, out_shape,
+                     out_dtype: str, node_names: list[str]) -> None:
+        x = self.view(x_name)
+        if x.strides[-1] != 1:
+            x = self.contiguous(x_name, x)
+        shape = tuple(x.shape)
+        cols = shape[-1]
+        rows = x.numel // cols if cols else 0
+        lead = list(shape[:-1])
+        if len(lead) > 5:
+            raise NotImplementedError("softmax rank > 6")
+        xs = list(x.strides[:-1])
+        margs = dict(mask=None, mask_lead_stride=[0] * 5, mask_col_stride=0, mask_dtype=0, has_mask=0)
+        if mask_name is not None:
+            m = V.broadcast_to(self.view(mask_name), shape)
+            margs = dict(mask=self.ref(m), mask_lead_stride=list(m.strides[:-1]) + [0] * (5 - len(lead)),
+                         mask_col_stride=m.strides[-1], mask_dtype=DTYPE_CODE[m.dtype], has_mask=1)
+        o = self.new_storage(out_name, out_shape, out_dtype)
+        self.emit(LaunchStep(
+            kind="softmax", kernel="k_softmax", module="basic", arg_struct="SoftmaxArgs",
+            args=dict(x=self.ref(x), out=self.ref(o), rows=rows, cols=cols,
+                      lead_shape=lead + [1] * (5 - len(lead)), x_lead_stride=xs + [0] * (5 - len(lead)),
+                      nlead=len(lead), x_dtype=DTYPE_CODE[x.dtype], add_dtype=DTYPE_CODE[add_dtype],
+                      out_dtype=DTYPE_CODE[out_dtype], **margs),
+            grid=(max(rows, 1), 1, 1), inputs=[x_name] + ([mask_name] if mask_name else []), outputs=[out_name],
+            params={"rows": rows, "cols": cols, "masked": mask_name is not None, "nodes": node_names}))
+        self.views[out_name] = o
+
+    def lower_softmax(self, node: OpNode) -> None:
+        x = node.inputs[0]
+        out = node.outputs[0]
+        dim = int(node.attrs.get("dim", -1)) % len(x.shape)
+        if dim != len(x.shape) - 1:
+            v = self.view(x.name)
+            perm = [d for d in range(len(x.shape)) if d != dim] + [dim]
+            pv = V.permute(v, perm)
+            self.views[x.name + ".perm"] = pv
+            self.emit_softmax(x.name + ".perm", None, x.dtype, out.name + ".perm", pv.shape, out.dtype, [node.name])
+            inv = [perm.index(d) for d in range(len(perm))]
+            self.views[out.name] = V.permute(self.views[out.name + ".perm"], inv)
+            return
+        self.emit_softmax(x.name, None, x.dtype, out.name, tuple(out.shape), out.dtype, [node.name])
+
+    def lower_mean(self, node: OpNode) -> None:
+        x = node.inputs[0]
+        out = node.outputs[0]
+        nd = len(x.shape)
+        dims = node.attrs.get("dim", None)
+        dims = list(range(nd)) if dims is None else ([dims] if isinstance(dims, int) else list(dims))
+        dims = sorted(d % nd for d in dims)
+        keep = [d for d in range(nd) if d not in dims]
+        v = self.view(x.name)
+        pv = V.permute(v, keep + dims)
+        pv = self.contiguous(x.name, pv) if not pv.is_contiguous() else pv
+        cols = numel([x.shape[d] for d in dims])
+        rows = pv.numel // cols
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        self.emit(LaunchStep(
+            kind="reduction", kernel="k_mean_last", module="basic", arg_struct="ReduceLastArgs",
+            args=dict(x=self.ref(pv), out=self.ref(o), rows=rows, cols=cols, x_dtype=DTYPE_CODE[pv.dtype],
+                      out_dtype=DTYPE_CODE[out.dtype]),
+            grid=(max(rows, 1), 1, 1), inputs=[x.name], outputs=[out.name], params={"rows": rows, "cols": cols}))
+        self.views[out.name] = o
+
+    def lower_argmax(self, node: OpNode) -> None:
+        x = node.inputs[0]
+        out = node.outputs[0]
+        v = self.view(x.name)
+        dim = node.attrs.get("dim", None)
+        if dim is None:
+            pv = self.contiguous(x.name, v)
+            pv = V.restride(pv, (1, pv.numel))
+        else:
+            dim = int(dim) % len(x.shape)
+            perm = [d for d in range(len(x.shape)) if d != dim] + [dim]
+            pv = V.permute(v, perm)
+            if not pv.is_contiguous():
+                pv = self.contiguous(x.name, pv)
+        cols = pv.shape[-1]
+        rows = pv.numel // cols
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        self.emit(LaunchStep(
+            kind="reduction", kernel="k_argmax", module="basic", arg_struct="ReduceLastArgs",
+            args=dict(x=self.ref(pv), out=self.ref(o), rows=rows, cols=cols, x_dtype=DTYPE_CODE[pv.dtype],
+                      out_dtype=DTYPE_CODE[out.dtype]),
+            grid=(max(rows, 1), 1, 1), inputs=[x.name], outputs=[out.name], params={"rows": rows, "cols": cols}))
+        self.views[out.name] = o
+
+    def lower_embedding(self, node: OpNode) -> None:
+        w_t, idx_t = node.inputs[0], node.inputs[1]
+        out = node.outputs[0]
+        w = self.contiguous(w_t.name)
+        ids = self.contiguous(idx_t.name)
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        n = ids.numel
+        self.emit(LaunchStep(
+            kind="special", kernel="k_embedding", module="basic", arg_struct="EmbeddingArgs",
+            args=dict(w=self.ref(w), ids=self.ref(ids), out=self.ref(o), n_ids=n, vocab=w.shape[0],
+                      row_bytes=numel(w.shape[1:]) * ELEM_SIZE[w.dtype], ids_dtype=DTYPE_CODE[ids.dtype]),
+            grid=(max(n, 1), 1, 1), inputs=[w_t.name, idx_t.name], outputs=[out.name],
+            params={"seq_len": n, "embed_dim": numel(w.shape[1:])}))
+        self.views[out.name] = o
+
+    def lower_rope_table(self, node: OpNode) -> None:
+        inv_t, pos_t = node.inputs[0], node.inputs[1]
+        cos_s, sin_s = node.outputs[0], node.outputs[1]
+        inv = self.contiguous(inv_t.name)
+        pos = self.contiguous(pos_t.name)
+        if inv.dtype != "float32":
+            raise NotImplementedError("rotary inv_freq must be float32")
+        half = inv.numel
+        S = pos.numel
+        c = self.new_storage(cos_s.name, cos_s.shape, cos_s.dtype)
+        s = self.new_storage(sin_s.name, sin_s.shape, sin_s.dtype)
+        self.emit(LaunchStep(
+            kind="special", kernel="k_rope_table", module="basic", arg_struct="RopeTableArgs",
+            args=dict(inv_freq=self.ref(inv), pos=self.ref(pos), cos_out=self.ref(c), sin_out=self.ref(s), S=S,
+                      half=half, pos_dtype=DTYPE_CODE[pos.dtype], out_dtype=DTYPE_CODE[cos_s.dtype],
+                      scaling=float(node.attrs.get("attention_scaling", 1.0))),
+            grid=(max(S, 1), 1, 1), block=(max(64, ((2 * half + 63) // 64) * 64), 1, 1),
+            inputs=[inv_t.name, pos_t.name], outputs=[cos_s.name, sin_s.name],
+            params={"seq_len": S, "head_dim": 2 * half}))
+        self.views[cos_s.name] = c
+        self.views[sin_s.name] = s
+
+    def _collapse(self, shape, strides) -> int | None:
+        """Single stride covering ``shape`` as one flattened dim, or None."""
+        st = None
+        expect = None
+        for s, t in zip(reversed(shape), reversed(strides)):
+            if s == 1:
+                continue
+            if st is None:
+                st, expect = t, t * s
+            elif t != expect:
+                return None
+            else:
+                expect = t * s
+        return st if st is not None else 0
+
+    def lower_index_copy(self, node: OpNode) -> None:
+        self_t, idx_t, src_t = node.inputs[0], node.inputs[1], node.inputs[2]
+        out = node.outputs[0]
+        dim = int(node.attrs.get("dim", 0)) % len(self_t.shape)
+        tv = self.view(self_t.name)
+        st = self.storages[tv.storage]
+        inplace = (self.inplace_inputs and st.kind == "input" and len(self.consumers.get(self_t.name, [])) == 1
+                   and tv.is_contiguous() and tv.offset == 0 and tv.numel * tv.itemsize == st.nbytes
+                   and self_t.name not in self.graph_output_names)
+        if inplace:
+            self.flush_chains_reading(tv.storage)
+            dst = tv
+            self.mutated_inputs.add(tv.storage)
+        else:
+            dst = self.new_storage(out.name, out.shape, out.dtype)
+            self.emit_copy(tv, dst, [self_t.name], [out.name])
+        src = self.view(src_t.name)
+        shape = list(tv.shape)
+        outer = numel(shape[:dim])
+        inner = numel(shape[dim + 1:])
+        nidx = src.shape[dim]
+        so = self._collapse(src.shape[:dim], src.strides[:dim])
+        si = self._collapse(src.shape[dim + 1:], src.strides[dim + 1:])
+        if so is None or si is None or (inner > 1 and si == 0):
+            src = self.contiguous(src_t.name, src)
+            so = self._collapse(src.shape[:dim], src.strides[:dim])
+            si = self._collapse(src.shape[dim + 1:], src.strides[dim + 1:])
+        sj = src.strides[dim]
+        idx = self.contiguous(idx_t.name)
+        total = outer * nidx * inner
+        self.emit(LaunchStep(
+            kind="special", kernel="k_index_copy", module="basic", arg_struct="IndexCopyArgs",
+            args=dict(dst=self.ref(dst), src=self.ref(src), index=self.ref(idx), outer=outer, dim_size=shape[dim],
+                      inner=inner, nidx=nidx, src_so=so if outer > 1 else 0, src_sj=sj, src_si=si if inner > 1 else 0,
+                      idx_dtype=DTYPE_CODE[idx.dtype], elem_bytes=ELEM_SIZE[dst.dtype]),
+            grid=grid1d(total), inputs=[self_t.name, idx_t.name, src_t.name], outputs=[out.name],
+            params={"outer_size": outer, "dim_size": shape[dim], "inner_size": inner, "num_indices": nidx,
+                    "inplace": inplace}))
+        self.views[out.name] = dst
+
+    def lower_full(self, node: OpNode) -> None:
+        out = node.outputs[0]
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        n = o.numel
+        self.emit(LaunchStep(
+            kind="special", kernel="k_fill", module="basic", arg_struct="FillArgs",
+            args=dict(out=self.ref(o), n=n, value=float(node.attrs.get("fill_value", 0.0)),
+                      dtype=DTYPE_CODE[out.dtype]),
+            grid=grid1d(n), inputs=[], outputs=[out.name], params={"total": n}))
+        self.views[out.name] = o
+
+    def lower_cat(self, node: OpNode) -> None:
+        out = node.outputs[0]
+        nd = len(out.shape)
+        dim = int(node.attrs.get("dim", 0)) % nd
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        pos = 0
+        for t in node.inputs:
+            if len(t.shape) == 1 and t.shape[0] == 0:
+                continue
+            v = self.view(t.name)
+            n = v.shape[dim]
+            dst = V.slice_(o, dim, pos, pos + n)
+            self.emit_copy(v, dst.with_(dtype=out.dtype), [t.name], [out.name])
+            pos += n
+        self.views[out.name] = o
+
+    # ------------------------------------------------------------------ driver
+
+    def run(self, patterns) -> None:
+        for pat in patterns:
+            pat(self)
+        for node in self.g.nodes:
+            if node.name in self.claimed:
+                emitter = self.claimed[node.name]
+                if emitter is not None:
+                    emitter()
+                continue
+            self.lower_node(node)
+        for o in self.g.graph_outputs:
+            self.view(o.name)
+
+    def lower_node(self, node: OpNode) -> None:
+        op = node.op_type
+        cat = classify_op(op)
+        if cat == OpCategory.NOOP:
+            return
+        if cat == OpCategory.ELEMENTWISE:
+            return self.lower_elementwise(node)
+        if cat == OpCategory.SHAPE_ALIAS:
+            return self.lower_alias(node)
+        table = {
+            "aten.linear.default": self.lower_linear,
+            "aten.matmul.default": self.lower_matmul,
+            "aten.mm.default": self.lower_matmul,
+            "aten.bmm.default": self.lower_matmul,
+            "aten.addmm.default": self.lower_addmm,
+            "aten.softmax.int": self.lower_softmax,
+            "aten._softmax.default": self.lower_softmax,
+            "aten.mean.dim": self.lower_mean,
+            "aten.argmax.default": self.lower_argmax,
+            "aten.embedding.default": self.lower_embedding,
+            "wrap_with_set_grad_enabled": self.lower_rope_table,
+            "aten.index_copy.default": self.lower_index_copy,
+            "aten.full.default": self.lower_full,
+            "aten.cat.default": self.lower_cat,
+        }
+        fn = table.get(op)
+        if fn is None:
+            raise NotImplementedError(f"HIP backend has no lowering for {op} (node {node.name})")
+        fn(node)
+
+
+def analyze_subgraph(graph: IRGraph, inplace_inputs: bool = True, fuse: bool = True) -> Lowering:
+    from hip_compiler.patterns import DEFAULT_PATTERNS
+
+    low = Lowering(graph, inplace_inputs=inplace_inputs)
+    low.run(DEFAULT_PATTERNS if fuse else [])
+    return low
+
+
+__all__ = ["Lowering", "analyze_subgraph", "grid1d", "math"]

@@ -1,0 +1,204 @@
+"""HIP executor: runs a HIPProgram as one prebuilt launch list (or one HIP graph).
+
+Counterpart of the reference's ``CUDAExecutor`` (`cuda_runtime/cuda_executor.py:54-176`).
+Init-time work: load code objects (AOT ``.hsaco`` and hiprtc-compiled chains),
+allocate the arena (zero-filled once), pack every step's argument struct with
+concrete arena pointers, and record where external buffers (graph inputs and
+weights) must be patched in. ``run()`` resolves the external pointers; when they
+are the same as in the previous call the captured HIP graph is relaunched as-is
+(one host call per step, instead of the reference's one Python dispatch per IR
+step), otherwise the affected kernargs are re-packed and the graph re-captured.
+
+Returned outputs alias executor-owned storage and stay valid until the next
+``run()``, as in the reference (`cuda_executor.py:153-176`); outputs that are
+graph inputs updated in place (KV caches) are the input buffers themselves.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch
+
+from hip_compiler.program import ELEM_SIZE, HIPProgram, Ref
+from hip_runtime import _shim
+from hip_runtime.hip_backend import _TORCH_OF_IR, HIPBuffer
+from hip_runtime.kernels import STRUCTS, ModuleCache
+
+_MODULES: dict[int, ModuleCache] = {}
+
+
+def module_cache(device_index: int) -> ModuleCache:
+    mc = _MODULES.get(device_index)
+    if mc is None:
+        mc = _MODULES[device_index] = ModuleCache()
+    return mc
+
+
+class HIPExecutor:
+    def __init__(self, program: HIPProgram, backend=None, use_graph: bool | None = None):
+        self.program = program
+        self.device = backend.device if backend is not None else torch.device("cuda", torch.cuda.current_device())
+        if use_graph is None:
+            use_graph = os.environ.get("HIPRT_NO_GRAPH", "0") != "1"
+        self.use_graph = use_graph
+        mods = module_cache(self.device.index or 0)
+        gen = {ks.kernel_name: ks.source_code for ks in program.kernel_sources}
+        for st in program.steps:
+            if st.module in gen:
+                mods.ensure_generated(st.module, gen[st.module])
+            else:
+                mods.ensure_builtin(st.module)
+        self.arena = torch.zeros(max(program.arena_bytes, 256), dtype=torch.uint8, device=self.device)
+        base = self.arena.data_ptr()
+        storages = program.storages
+        self._ext_names: list[str] = sorted({r.storage for st in program.steps for r in _refs(st.args)
+                                             if storages[r.storage].kind in ("input", "weight")})
+        self._structs = []
+        self._fixups: list[tuple[object, str, int, str, int]] = []   # (struct, field, index, storage, byte_off)
+        n = len(program.steps)
+        self._recs = (_shim.LaunchRec * max(n, 1))()
+        for i, st in enumerate(program.steps):
+            s = STRUCTS[st.arg_struct]()
+            for k, v in st.args.items():
+                if isinstance(v, (list, tuple)):
+                    arr = getattr(s, k)
+                    for j, x in enumerate(v):
+                        self._set(s, k, j, x, arr, base, storages)
+                else:
+                    self._set(s, k, -1, v, None, base, storages)
+            self._structs.append(s)
+            r = self._recs[i]
+            r.fn = mods.function(st.module, st.kernel)
+            r.grid[:] = [int(g) for g in st.grid]
+            r.block[:] = [int(b) for b in st.block]
+            r.lds_bytes = int(st.lds)
+            r.kernarg_size = C.sizeof(s)
+            r.kernarg = C.addressof(s)
+        self._n = n
+        self._ext_key: tuple | None = None
+        self._graph = None
+        self._capture_stream = None
+        self._out_cache: dict[str, HIPBuffer] = {}
+        for spec in program.output_specs:
+            v = program.output_views[spec.name]
+            st = storages[v.storage]
+            if st.kind in ("arena", "persistent"):
+                off = st.offset + v.offset * ELEM_SIZE[v.dtype]
+                t = self.arena[off:off + v.numel * ELEM_SIZE[v.dtype]].view(_TORCH_OF_IR[v.dtype]).view(v.shape)
+                self._out_cache[spec.name] = HIPBuffer(t, tuple(spec.shape))
+
+    # ------------------------------------------------------------------ kernarg packing
+
+    def _set(self, s, field, idx, v, arr, base, storages) -> None:
+        if isinstance(v, Ref):
+            st = storages[v.storage]
+            if st.kind in ("arena", "persistent"):
+                val = base + st.offset + v.byte_offset
+            else:
+                self._fixups.append((s, field, idx, v.storage, v.byte_offset))
+                val = 0
+        elif v is None:
+            val = 0
+        else:
+            val = v
+        if idx < 0:
+            setattr(s, field, val)
+        else:
+            arr[idx] = val
+
+    def _patch(self, ptrs: dict[str, int]) -> None:
+        for s, field, idx, storage, off in self._fixups:
+            val = ptrs[storage] + off
+            if idx < 0:
+                setattr(s, field, val)
+            else:
+                getattr(s, field)[idx] = val
+
+    # ------------------------------------------------------------------ execution
+
+    def _resolve(self, inputs: dict, weights: dict) -> dict[str, int]:
+        ptrs: dict[str, int] = {}
+        wmap = self.program.weight_name_mapping
+        for name in self._ext_names:
+            buf = inputs.get(name)
+            if buf is None:
+                buf = weights.get(name)
+            if buf is None and name in wmap:
+                buf = weights.get(wmap[name])
+            if buf is None:
+                raise KeyError(f"HIPExecutor: no buffer for '{name}' (graph input or weight)")
+            t = buf.native_handle if isinstance(buf, HIPBuffer) else buf
+            if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+                raise TypeError(f"HIPExecutor: '{name}' must be a device buffer, got {type(buf).__name__}")
+            spec_st = self.program.storages[name]
+            if t.numel() * t.element_size() < spec_st.nbytes:
+                raise ValueError(f"HIPExecutor: '{name}' holds {t.numel() * t.element_size()} bytes, "
+                                 f"program needs {spec_st.nbytes}")
+            ptrs[name] = t.data_ptr()
+        return ptrs
+
+    def launch(self, inputs: dict, weights: dict, stream: int | None = None) -> None:
+        """Enqueue the whole program on ``stream`` (default: torch's current stream)."""
+        ptrs = self._resolve(inputs, weights)
+        key = tuple(ptrs[n] for n in self._ext_names)
+        if key != self._ext_key:
+            self._patch(ptrs)
+            self._ext_key = key
+            if self._graph is not None:
+                _shim.check(_shim.lib().hs_graph_destroy(self._graph), "graph destroy")
+                self._graph = None
+        if stream is None:
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+        if self._n == 0:
+            return
+        if self.use_graph:
+            if self._graph is None:
+                if self._capture_stream is None:
+                    cs = C.c_void_p()
+                    _shim.check(_shim.lib().hs_stream_create(C.byref(cs)), "stream create")
+                    self._capture_stream = cs.value
+                g = C.c_void_p()
+                _shim.check(_shim.lib().hs_graph_capture(self._recs, self._n, self._capture_stream, C.byref(g)),
+                            "graph capture")
+                self._graph = g.value
+            _shim.check(_shim.lib().hs_graph_launch(self._graph, stream), "graph launch")
+        else:
+            _shim.check(_shim.lib().hs_replay(self._recs, self._n, stream), "replay")
+
+    def run(self, inputs: dict, weights: dict) -> dict[str, HIPBuffer]:
+        self.launch(inputs, weights)
+        out: dict[str, HIPBuffer] = {}
+        for spec in self.program.output_specs:
+            b = self._out_cache.get(spec.name)
+            if b is None:
+                v = self.program.output_views[spec.name]
+                src = inputs.get(v.storage)
+                if isinstance(src, HIPBuffer) and tuple(src.shape) == tuple(spec.shape):
+                    b = src
+                else:
+                    t = src.native_handle if isinstance(src, HIPBuffer) else src
+                    b = HIPBuffer(t.reshape(-1)[:v.numel].view(tuple(spec.shape)), tuple(spec.shape))
+            out[spec.name] = b
+        return out
+
+    def __del__(self):
+        try:
+            lib = _shim.lib()
+            if self._graph is not None:
+                lib.hs_graph_destroy(self._graph)
+            if self._capture_stream is not None:
+                lib.hs_stream_destroy(self._capture_stream)
+        except Exception:
+            pass
+
+
+def _refs(args: dict):
+    for v in args.values():
+        if isinstance(v, Ref):
+            yield v
+        elif isinstance(v, (list, tuple)):
+            for x in v:
+                if isinstance(x, Ref):
+                    yield x
