@@ -1,5 +1,5 @@
-// GQA decode attention (one query token) over static K/V caches, split over
-// 64-position tiles so that the two KV heads of Qwen2.5 still fill the chip.
+// GQA decode attention (one query token) over static K/V caches, in two kernels
+// with no cross-workgroup synchronisation inside either of them.
 //
 // The math restates the CPU (ATen) rounding points of the eager attention chain
 //   s  = round(q . k)              matmul, fp32 accumulation
@@ -7,24 +7,25 @@
 //   s2 = round_add(s1 + mask)      add of the additive mask
 //   p  = round(softmax_f32(s2))    softmax(dtype=f32) then to(model dtype)
 //   o  = round(sum_s p * v)        matmul, fp32 accumulation
-// so the two passes are:
-//   k_attn_scores: s2 for every position of a tile, plus the tile's (max, sum exp)
-//   k_attn_pv:     global (max, sum) per head from the tile stats, p for the tile,
-//                  the tile's partial p.V; the last tile to finish (atomic ticket)
-//                  adds the partials in tile order and writes the output.
-// A position whose mask is -inf contributes exactly 0, so its K and V rows are
-// never loaded: KV traffic follows the valid length, not the cache capacity.
-// Each tile's K rows are read once and shared by the G query heads of its group.
+// k_attn_scores: one workgroup per (64-position tile, KV head) computes s2 for the
+//   G query heads of the group (each K row is read once and shared by the G heads)
+//   and the tile's (max, sum exp) per head.
+// k_attn_out:    one workgroup per (8-dim slice, KV head) folds the tile stats into
+//   the global (max, sum) per head, forms p for every position exactly as above
+//   and accumulates p * V over the whole sequence for its slice, so the output is
+//   written in one pass with no partial-sum combine.
+// Positions whose mask is -inf contribute exactly 0: their K rows are never loaded,
+// and V rows of tiles that are entirely masked are skipped, so KV traffic follows
+// the valid length rather than the cache capacity.
+// Loads are issued in batches before their first use so that each wave keeps many
+// HBM requests in flight (decode attention is latency-, not bandwidth-, limited).
 #include "common.h"
 
 #define AT_TILE 64
 #define AT_D 128
 #define AT_GMAX 8
-
-__device__ __forceinline__ float ld_h(const void* p, long long i, int dt) {
-  const uint16_t h = ((const uint16_t*)p)[i];
-  return dt == HS_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
-}
+#define AT_ROUND 8
+#define AT_MAXTILES 1024
 
 __device__ __forceinline__ void unpack8(const uint4 v, int dt, float* f) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -36,50 +37,66 @@ __device__ __forceinline__ void unpack8(const uint4 v, int dt, float* f) {
   }
 }
 
-__device__ __forceinline__ bool masked_out(const DecodeAttnArgs& a, long long p, float* mv) {
-  if (a.mask_dtype < 0) { *mv = 0.f; return false; }
-  *mv = ld_f(a.mask, p * a.mask_stride, a.mask_dtype);
-  return *mv == -INFINITY;
-}
-
 extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttnArgs a) {
   __shared__ float qs[AT_GMAX][AT_D];
   __shared__ float sc[AT_GMAX][AT_TILE];
+  __shared__ float mv[AT_TILE];
+  __shared__ int live;
   const int G = a.H / a.KVH;
   const int kvh = blockIdx.y;
   const int tile = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long t0 = (long long)tile * AT_TILE;
+  if (threadIdx.x == 0) live = 0;
+  __syncthreads();
   for (int i = threadIdx.x; i < G * AT_D; i += 256) {
     const int h = i / AT_D, d = i % AT_D;
-    qs[h][d] = ld_h(a.q, (long long)(kvh * G + h) * a.q_head_stride + d, a.dtype);
+    const uint16_t raw = ((const uint16_t*)a.q)[(long long)(kvh * G + h) * a.q_head_stride + d];
+    qs[h][d] = a.dtype == HS_BF16 ? bf16_to_f32(raw) : f16_to_f32(raw);
+  }
+  if (threadIdx.x < AT_TILE) {
+    const long long p = t0 + threadIdx.x;
+    float m = -INFINITY;
+    if (p < a.S) m = a.mask_dtype < 0 ? 0.f : ld_f(a.mask, p * a.mask_stride, a.mask_dtype);
+    mv[threadIdx.x] = m;
+    if (m != -INFINITY) live = 1;
   }
   __syncthreads();
+  if (!live) {   // whole tile masked: contributes nothing (l = 0)
+    if (threadIdx.x < G) {
+      float* st = a.stats + ((long long)(kvh * G + threadIdx.x) * a.ntiles + tile) * 2;
+      st[0] = -INFINITY;
+      st[1] = 0.f;
+    }
+    return;
+  }
   const int g8 = lane >> 3, sub = lane & 7;
   const uint16_t* K = (const uint16_t*)a.k + (long long)kvh * a.kv_head_stride;
+  uint4 kr[2][2];
+  bool use[2];
 #pragma unroll
   for (int step = 0; step < 2; ++step) {
     const int tp = wave * 16 + step * 8 + g8;
-    const long long p = (long long)tile * AT_TILE + tp;
-    float mv = 0.f;
-    const bool valid = p < a.S;
-    const bool skip = !valid || masked_out(a, p, &mv);
+    use[step] = mv[tp] != -INFINITY;
+    const uint4* src = (const uint4*)(K + (t0 + tp) * AT_D + sub * 16);
+    kr[step][0] = use[step] ? src[0] : make_uint4(0, 0, 0, 0);
+    kr[step][1] = use[step] ? src[1] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int step = 0; step < 2; ++step) {
+    const int tp = wave * 16 + step * 8 + g8;
+    float kf[16];
+    unpack8(kr[step][0], a.dtype, kf);
+    unpack8(kr[step][1], a.dtype, kf + 8);
     float dots[AT_GMAX];
 #pragma unroll
-    for (int h = 0; h < AT_GMAX; ++h) dots[h] = 0.f;
-    if (!skip) {
-      const uint4* kr = (const uint4*)(K + p * AT_D + sub * 16);
-      float kf[16];
-      unpack8(kr[0], a.dtype, kf);
-      unpack8(kr[1], a.dtype, kf + 8);
+    for (int h = 0; h < AT_GMAX; ++h) {
+      float acc = 0.f;
+      if (h < G) {
 #pragma unroll
-      for (int h = 0; h < AT_GMAX; ++h) {
-        if (h < G) {
-          float acc = 0.f;
-#pragma unroll
-          for (int j = 0; j < 16; ++j) acc = fmaf(qs[h][sub * 16 + j], kf[j], acc);
-          dots[h] = acc;
-        }
+        for (int j = 0; j < 16; ++j) acc = fmaf(qs[h][sub * 16 + j], kf[j], acc);
       }
+      dots[h] = acc;
     }
 #pragma unroll
     for (int h = 0; h < AT_GMAX; ++h) {
@@ -89,17 +106,15 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
     }
 #pragma unroll
     for (int h = 0; h < AT_GMAX; ++h) {
-      if (h < G && sub == (h & 7)) {
-        float s;
-        if (skip) {
-          s = -INFINITY;
-        } else {
+      if (h < G && sub == h) {
+        float s = -INFINITY;
+        if (use[step]) {
           s = round_to(dots[h], a.dtype);
           s = round_to(s * a.scale, a.dtype);
-          if (a.mask_dtype >= 0) s = round_to(s + mv, a.add_dtype);
+          if (a.mask_dtype >= 0) s = round_to(s + mv[tp], a.add_dtype);
         }
         sc[h][tp] = s;
-        if (valid) a.scores[(long long)(kvh * G + h) * a.S + p] = s;
+        if (t0 + tp < a.S) a.scores[(long long)(kvh * G + h) * a.S + t0 + tp] = s;
       }
     }
   }
@@ -107,7 +122,7 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
   for (int h = wave; h < G; h += 4) {
     const float v = sc[h][lane];
     const float m = wave_max(v);
-    const float e = (m == -INFINITY) ? 0.f : expf(v - m);
+    const float e = (m == -INFINITY || v == -INFINITY) ? 0.f : expf(v - m);
     const float l = wave_sum(e);
     if (lane == 0) {
       float* st = a.stats + ((long long)(kvh * G + h) * a.ntiles + tile) * 2;
@@ -117,17 +132,16 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
   }
 }
 
-extern "C" __global__ void __launch_bounds__(256) k_attn_pv(const DecodeAttnArgs a) {
-  __shared__ float gm[AT_GMAX], gl[AT_GMAX];
-  __shared__ float pr[AT_GMAX][AT_TILE];
-  __shared__ float red[4][AT_GMAX][AT_D];
-  __shared__ int is_last;
+extern "C" __global__ void __launch_bounds__(256) k_attn_out(const AttnOutArgs a) {
+  __shared__ float gm[AT_GMAX], ginv[AT_GMAX];
+  __shared__ unsigned char tile_live[AT_MAXTILES];
+  __shared__ float red[256][AT_GMAX * 8 + 1];
   const int G = a.H / a.KVH;
   const int kvh = blockIdx.y;
-  const int tile = blockIdx.x;
+  const int d0 = blockIdx.x * 8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-
-  // global max and sum of exp for each head of the group
+  for (int t = threadIdx.x; t < a.ntiles; t += 256) tile_live[t] = 0;
+  __syncthreads();
   for (int h = wave; h < G; h += 4) {
     const float* st = a.stats + (long long)(kvh * G + h) * a.ntiles * 2;
     float m = -INFINITY;
@@ -136,73 +150,63 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_pv(const DecodeAttnArgs
     float l = 0.f;
     for (int t = lane; t < a.ntiles; t += 64) {
       const float lt = st[2 * t + 1];
-      if (lt > 0.f) l += lt * expf(st[2 * t] - m);
+      if (lt > 0.f) {
+        l += lt * expf(st[2 * t] - m);
+        tile_live[t] = 1;
+      }
     }
     l = wave_sum(l);
-    if (lane == 0) { gm[h] = m; gl[h] = l; }
+    if (lane == 0) { gm[h] = m; ginv[h] = 1.0f / l; }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < G * AT_TILE; i += 256) {
-    const int h = i / AT_TILE, tp = i % AT_TILE;
-    const long long p = (long long)tile * AT_TILE + tp;
-    float pv = 0.f;
-    if (p < a.S) {
-      const float s = a.scores[(long long)(kvh * G + h) * a.S + p];
-      if (s != -INFINITY) pv = round_to(expf(s - gm[h]) * (1.0f / gl[h]), a.dtype);
+  float acc[AT_GMAX][8];
+#pragma unroll
+  for (int h = 0; h < AT_GMAX; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
+  const uint16_t* V = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride + d0;
+  const float* SC = a.scores + (long long)kvh * G * a.S;
+  for (long long base = 0; base < a.S; base += 256 * AT_ROUND) {
+    uint4 vr[AT_ROUND];
+    float s[AT_ROUND][AT_GMAX];
+#pragma unroll
+    for (int r = 0; r < AT_ROUND; ++r) {
+      const long long p = base + r * 256 + threadIdx.x;
+      const bool ok = p < a.S && tile_live[p / AT_TILE];
+      vr[r] = ok ? *(const uint4*)(V + p * AT_D) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int h = 0; h < AT_GMAX; ++h) s[r][h] = (ok && h < G) ? SC[(long long)h * a.S + p] : -INFINITY;
     }
-    pr[h][tp] = pv;
-  }
-  __syncthreads();
-
-  // partial o over this tile: lane owns dims 2*lane, 2*lane+1; wave owns 16 positions
-  float acc[AT_GMAX][2];
 #pragma unroll
-  for (int h = 0; h < AT_GMAX; ++h) acc[h][0] = acc[h][1] = 0.f;
-  const uint16_t* V = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride;
-  for (int j = 0; j < 16; ++j) {
-    const int tp = wave * 16 + j;
-    const long long p = (long long)tile * AT_TILE + tp;
-    if (p >= a.S) break;
-    float mv;
-    if (masked_out(a, p, &mv)) continue;
-    const uint32_t w2 = *(const uint32_t*)(V + p * AT_D + 2 * lane);
-    const uint16_t lo = (uint16_t)(w2 & 0xffffu), hi = (uint16_t)(w2 >> 16);
-    const float v0 = a.dtype == HS_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
-    const float v1 = a.dtype == HS_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    for (int r = 0; r < AT_ROUND; ++r) {
+      float vf[8];
+      unpack8(vr[r], a.dtype, vf);
 #pragma unroll
-    for (int h = 0; h < AT_GMAX; ++h) {
-      if (h < G) {
-        acc[h][0] = fmaf(pr[h][tp], v0, acc[h][0]);
-        acc[h][1] = fmaf(pr[h][tp], v1, acc[h][1]);
+      for (int h = 0; h < AT_GMAX; ++h) {
+        if (h < G && s[r][h] != -INFINITY) {
+          const float p = round_to(expf(s[r][h] - gm[h]) * ginv[h], a.dtype);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(p, vf[j], acc[h][j]);
+        }
       }
     }
   }
 #pragma unroll
-  for (int h = 0; h < AT_GMAX; ++h) {
-    if (h < G) {
-      red[wave][h][2 * lane] = acc[h][0];
-      red[wave][h][2 * lane + 1] = acc[h][1];
-    }
-  }
+  for (int h = 0; h < AT_GMAX; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[threadIdx.x][h * 8 + j] = acc[h][j];
   __syncthreads();
-  float* part = a.part + ((long long)kvh * a.ntiles + tile) * G * AT_D;
-  for (int i = threadIdx.x; i < G * AT_D; i += 256) {
-    const int h = i / AT_D, d = i % AT_D;
-    part[i] = ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d];
+  // 4 threads per output value, each summing 64 rows; then a fixed-order 4-way combine
+  const int o = threadIdx.x >> 2, q4 = threadIdx.x & 3;
+  float part = 0.f;
+  if (o < G * 8) {
+    for (int i = q4 * 64; i < q4 * 64 + 64; ++i) part += red[i][o];
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) is_last = (atomicAdd(&a.counters[kvh], 1) == a.ntiles - 1);
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const float* pk = a.part + (long long)kvh * a.ntiles * G * AT_D;
-  for (int i = threadIdx.x; i < G * AT_D; i += 256) {
-    float s = 0.f;
-    for (int t = 0; t < a.ntiles; ++t) s += pk[(long long)t * G * AT_D + i];
-    const int h = i / AT_D, d = i % AT_D;
-    const long long o = (long long)(kvh * G + h) * AT_D + d;
-    ((uint16_t*)a.out)[o] = a.dtype == HS_BF16 ? f32_to_bf16(s) : f32_to_f16(s);
+  part += __shfl_xor(part, 1, 64);
+  part += __shfl_xor(part, 2, 64);
+  if (o < G * 8 && q4 == 0) {
+    const int h = o >> 3, j = o & 7;
+    const long long idx = (long long)(kvh * G + h) * AT_D + d0 + j;
+    ((uint16_t*)a.out)[idx] = a.dtype == HS_BF16 ? f32_to_bf16(part) : f32_to_f16(part);
   }
-  if (threadIdx.x == 0) atomicExch(&a.counters[kvh], 0);
 }

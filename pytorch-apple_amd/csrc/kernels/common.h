@@ -155,6 +155,65 @@ struct LinearArgs {           // out[m, n] = round(x[m, :] . w[n, :] + bias[n]) 
   int pad;
 };
 
+struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm, epilogues bias/resid/silu/argmax
+  const void* x;              // [M, K] bf16 activations (raw residual stream when NORM)
+  const void* w;              // [N, K] bf16
+  const void* bias;           // [N] or null
+  void* out;                  // [M, N] bf16
+  const void* resid;          // [M, N] residual (RESID)
+  const void* w2;             // [N, K] second weight (SILU: up projection)
+  const void* bias2;          // [N] or null
+  const void* norm_w;         // [K] RMSNorm weight (NORM)
+  unsigned long long* argmax_slot;  // [M] packed (value, ~index) keys (ARGMAX), zero before launch
+  long long M;
+  long long ldx;
+  long long ldo;
+  long long ldr;
+  int N;
+  int K;
+  float eps;
+  int n_dtype;                // rounding dtype of x * rsqrt(...) (the to(dtype) of the norm)
+  int flags;                  // 1: bias, 4: bias2
+  int pad;
+};
+
+struct ArgmaxFinalizeArgs {   // out[m] = index of max over the `parts` keys of row m
+  const unsigned long long* slot;   // [rows, parts] packed (ordered value, ~index) keys
+  void* out;
+  long long rows;
+  int parts;
+  int out_dtype;
+};
+
+struct QKVArgs {              // RMSNorm -> q/k/v projections -> RoPE -> K/V cache rows (gemv.hip)
+  const void* x;
+  const void* norm_w;
+  const void* wq;
+  const void* bq;
+  const void* wk;
+  const void* bk;
+  const void* wv;
+  const void* bv;
+  const float* inv_freq;
+  const void* pos_ids;
+  const void* cache_pos;
+  void* q_out;                // [H, D]
+  void* k_dst;                // K cache [KVH, S, D] (flag 16) or [KVH, D]
+  void* v_dst;                // V cache [KVH, S, D] (flag 32) or [KVH, D]
+  long long kv_head_stride;
+  long long cache_len;
+  int K;
+  int H;
+  int KVH;
+  int D;
+  float eps;
+  int n_dtype;
+  int flags;                  // 1 norm, 2 bias, 4 rope q, 8 rope k, 16 k to cache, 32 v to cache
+  int pos_dtype;
+  int cpos_dtype;
+  float rope_scaling;
+};
+
 struct FusedArgs {            // generated elementwise chains: out[i] = chain(in0..in7 at strided offsets)
   void* out;
   const void* in[8];
@@ -169,8 +228,6 @@ struct DecodeAttnArgs {       // GQA decode attention over static caches, split 
   void* out;                  // [H, D]
   float* scores;              // scratch [H, S]
   float* stats;               // scratch [H, ntiles, 2]
-  float* part;                // scratch [KVH, ntiles, G, D]
-  int* counters;              // scratch [KVH], zero between launches
   long long S;
   long long q_head_stride;
   long long kv_head_stride;
@@ -183,6 +240,23 @@ struct DecodeAttnArgs {       // GQA decode attention over static caches, split 
   int mask_dtype;             // HS_BF16 / HS_F16 / HS_F32, or -1 for no mask
   int add_dtype;              // dtype of scores + mask in the model (rounding point)
   int dtype;                  // q/k/v/out dtype (HS_BF16 or HS_F16)
+};
+
+struct AttnOutArgs {          // second attention pass: global softmax and p.V per 8-dim slice
+  const float* scores;        // [H, S] s2 from k_attn_scores (-inf where masked)
+  const float* stats;         // [H, ntiles, 2] tile (max, sum exp)
+  const void* v;              // [KVH, S, D]
+  const void* mask;           // unused by the kernel; kept for symmetry with DecodeAttnArgs
+  void* out;                  // [H, D]
+  long long S;
+  long long kv_head_stride;
+  long long mask_stride;
+  int H;
+  int KVH;
+  int ntiles;
+  int mask_dtype;
+  int dtype;
+  int pad;
 };
 
 #ifdef __HIPCC__

@@ -1,0 +1,332 @@
+// Fused streaming GEMV kernels for decode (M <= 4 rows of activations).
+//
+// Weight rows are the HBM stream: every wave owns RPW rows and walks K with one
+// 16-byte load per lane per 512 elements, accumulating in fp32 with v_dot2.
+// Around that loop the kernels fold in the ops that the IR places next to each
+// projection, at the CPU's rounding points:
+//   prologue  NORM   y = round(w_n * round(x * rsqrt(mean(x^2) + eps)))  (RMSNorm), staged in LDS
+//   epilogue  BIAS   out = round(acc + b)
+//             RESID  out = round(r + round(acc + b))                     (linear then residual add)
+//             SILU   out = round(round(silu(round(acc_g))) * round(acc_u)) (gate/up pair, SiLU*mul)
+//             ARGMAX out = round(acc); atomicMax of (ordered value, ~index) per activation row
+// k_qkv_rope additionally applies rotary embedding to q/k row pairs (d, d+D/2) and
+// writes k/v straight into the static caches at cache_position (index_copy in place).
+#include "common.h"
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_v;
+
+__device__ __forceinline__ float dot8_bf16(const uint4 a, const uint4 b, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.x), __builtin_bit_cast(bf16x2_v, b.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.y), __builtin_bit_cast(bf16x2_v, b.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.z), __builtin_bit_cast(bf16x2_v, b.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.w), __builtin_bit_cast(bf16x2_v, b.w), acc, false);
+  return acc;
+}
+
+typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read once per step: non-temporal hint)
+__device__ __forceinline__ uint4 ld_stream(const uint16_t* p) {
+  const u32x4_v v = __builtin_nontemporal_load((const u32x4_v*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float bf(const void* p, long long i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
+__device__ __forceinline__ float rbf(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+enum { EPI_BIAS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
+#define GEMV_MAXK 8960
+#define GEMV_MB 4
+
+// RMSNorm of `rows` activation rows into LDS (bf16 bits); 256 threads.
+__device__ __forceinline__ void norm_to_lds(const GemvArgs& a, long long m0, int rows, uint16_t* xs) {
+  __shared__ float red[4];
+  for (int m = 0; m < rows; ++m) {
+    const uint16_t* x = (const uint16_t*)a.x + (m0 + m) * a.ldx;
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < a.K; c += 256) {
+      const float h = bf16_to_f32(x[c]);
+      ss += h * h;
+    }
+    ss = block_sum256(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+    for (int c = threadIdx.x; c < a.K; c += 256) {
+      const float n = round_to(bf16_to_f32(x[c]) * r, a.n_dtype);
+      xs[m * a.K + c] = f32_to_bf16(bf(a.norm_w, c) * n);
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
+  uint32_t b = __float_as_uint(v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)n);
+}
+
+// Workgroups stride over blocks of 4*RPW weight rows (grid.x may be smaller than the
+// number of blocks), so a prologue is computed once per workgroup, not once per block.
+template <bool NORM, int EPI, int RPW, int MB>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[NORM ? GEMV_MB * 1536 * 2 : 8];
+  __shared__ unsigned long long best_w[EPI == EPI_ARGMAX ? 4 * MB : 1];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long long m0 = (long long)blockIdx.y * MB;
+  const int mrows = (int)min((long long)MB, a.M - m0);
+  constexpr int NW = (EPI == EPI_SILU) ? 2 : 1;
+  const uint16_t* W[NW];
+  W[0] = (const uint16_t*)a.w;
+  if constexpr (EPI == EPI_SILU) W[1] = (const uint16_t*)a.w2;
+  const int nblocks = (a.N + 4 * RPW - 1) / (4 * RPW);
+  unsigned long long best[MB];
+#pragma unroll
+  for (int m = 0; m < MB; ++m) best[m] = 0ull;
+
+  // Rounds of U chunks: every weight load of a round is issued before any is consumed,
+  // so a wave keeps U*RPW*NW 16-byte loads in flight instead of waiting on each. The
+  // first round is issued before the RMSNorm prologue, which then overlaps its latency.
+  constexpr int U = (RPW * NW >= 4) ? 2 : (RPW * NW >= 2 ? 4 : 8);
+  uint4 wv[U][RPW][NW];
+  int n0 = (blockIdx.x * 4 + wave) * RPW;
+  auto load_round = [&](int kb) {
+#pragma unroll
+    for (int c = 0; c < U; ++c) {
+      const int k = kb + c * 512;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const long long n = min(n0 + r, a.N - 1);
+#pragma unroll
+        for (int u = 0; u < NW; ++u)
+          wv[c][r][u] = k < a.K ? ld_stream(W[u] + n * a.K + k) : make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+  load_round(lane * 8);
+  if constexpr (NORM) norm_to_lds(a, m0, mrows, xs);
+  for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+  n0 = (blk * 4 + wave) * RPW;
+  if (blk != (int)blockIdx.x) load_round(lane * 8);
+  if (n0 >= a.N) continue;
+  float acc[MB][RPW][NW];
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int u = 0; u < NW; ++u) acc[m][r][u] = 0.f;
+  for (int kb = lane * 8; kb < a.K; kb += 512 * U) {
+    if (kb != lane * 8) load_round(kb);
+#pragma unroll
+    for (int c = 0; c < U; ++c) {
+      const int k = kb + c * 512;
+      if (k >= a.K) break;
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        if (m < mrows) {
+          uint4 xv;
+          if constexpr (NORM) xv = *(const uint4*)(xs + m * a.K + k);
+          else xv = *(const uint4*)((const uint16_t*)a.x + (m0 + m) * a.ldx + k);
+#pragma unroll
+          for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int u = 0; u < NW; ++u) acc[m][r][u] = dot8_bf16(xv, wv[c][r][u], acc[m][r][u]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MB; ++m)
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int u = 0; u < NW; ++u) acc[m][r][u] = wave_sum(acc[m][r][u]);
+
+#pragma unroll
+  for (int m = 0; m < MB; ++m) {
+    if (m >= mrows) continue;
+    const long long mm = m0 + m;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int n = n0 + r;
+      if (n >= a.N) continue;
+      float v = acc[m][r][0];
+      if (a.flags & 1) v += bf(a.bias, n);
+      v = rbf(v);
+      if constexpr (EPI == EPI_RESID) v = bf(a.resid, mm * a.ldr + n) + v;
+      if constexpr (EPI == EPI_SILU) {
+        float u = acc[m][r][1];
+        if (a.flags & 4) u += bf(a.bias2, n);
+        u = rbf(u);
+        const float s = rbf(v / (1.f + expf(-v)));
+        v = s * u;
+      }
+      if (lane == 0) ((uint16_t*)a.out)[mm * a.ldo + n] = f32_to_bf16(v);
+      if constexpr (EPI == EPI_ARGMAX) {
+        const unsigned long long key = argmax_key(rbf(v), n);
+        best[m] = key > best[m] ? key : best[m];
+      }
+    }
+  }
+  }  // row blocks
+  if constexpr (EPI == EPI_ARGMAX) {
+    // one key per (activation row, workgroup); k_argmax_finalize reduces them
+    if (lane == 0)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) best_w[wave * MB + m] = best[m];
+    __syncthreads();
+    if (threadIdx.x < (unsigned)mrows) {
+      unsigned long long k = 0ull;
+      for (int w = 0; w < 4; ++w) k = best_w[w * MB + threadIdx.x] > k ? best_w[w * MB + threadIdx.x] : k;
+      a.argmax_slot[(m0 + threadIdx.x) * gridDim.x + blockIdx.x] = k;
+    }
+  }
+}
+
+#define GEMV_KERNEL(NAME, NORM, EPI, RPW, MB) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const GemvArgs a) { gemv_body<NORM, EPI, RPW, MB>(a); }
+
+GEMV_KERNEL(k_gemv_bias_r1, false, EPI_BIAS, 1, 1)
+GEMV_KERNEL(k_gemv_bias_r4, false, EPI_BIAS, 4, 1)
+GEMV_KERNEL(k_gemv_resid_r1, false, EPI_RESID, 1, 1)
+GEMV_KERNEL(k_gemv_norm_bias_r1, true, EPI_BIAS, 1, 1)
+GEMV_KERNEL(k_gemv_norm_silu_r1, true, EPI_SILU, 1, 1)
+GEMV_KERNEL(k_gemv_silu_r1, false, EPI_SILU, 1, 1)
+GEMV_KERNEL(k_gemv_norm_argmax_r4, true, EPI_ARGMAX, 4, 1)
+GEMV_KERNEL(k_gemv_argmax_r4, false, EPI_ARGMAX, 4, 1)
+GEMV_KERNEL(k_gemv_bias_m4, false, EPI_BIAS, 2, 4)
+GEMV_KERNEL(k_gemv_resid_m4, false, EPI_RESID, 2, 4)
+GEMV_KERNEL(k_gemv_norm_bias_m4, true, EPI_BIAS, 2, 4)
+GEMV_KERNEL(k_gemv_norm_silu_m4, true, EPI_SILU, 1, 4)
+GEMV_KERNEL(k_gemv_silu_m4, false, EPI_SILU, 1, 4)
+
+// One workgroup per activation row: the largest of the row's per-workgroup keys is the
+// maximum logit with the smallest index among equal maxima (np.argmax's rule).
+extern "C" __global__ void __launch_bounds__(256) k_argmax_finalize(const ArgmaxFinalizeArgs a) {
+  __shared__ unsigned long long red[256];
+  const long long m = blockIdx.x;
+  if (m >= a.rows) return;
+  unsigned long long k = 0ull;
+  for (int i = threadIdx.x; i < a.parts; i += 256) {
+    const unsigned long long v = a.slot[m * a.parts + i];
+    k = v > k ? v : k;
+  }
+  red[threadIdx.x] = k;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o && red[threadIdx.x + o] > red[threadIdx.x]) red[threadIdx.x] = red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const long long idx = (long long)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFull));
+    if (a.out_dtype == HS_I64) ((long long*)a.out)[m] = idx;
+    else ((int*)a.out)[m] = (int)idx;
+  }
+}
+
+// ------------------------------------------------------------------------ q/k/v + RoPE + cache
+
+// One wave per task; a task is a pair of weight rows:
+//   q and k: rows (h*D + j, h*D + j + D/2) of one head, rotated together;
+//   v:       rows (2t, 2t+1), plain.
+extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[1536 * 2];
+  __shared__ float red[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int D = a.D, half = a.D / 2;
+  const int tq = a.H * half, tk = a.KVH * half, tv = a.KVH * D / 2;
+  const int t0 = blockIdx.x * 4 + wave;
+  const bool active = t0 < tq + tk + tv;
+  const int t = active ? t0 : 0;
+  int seg, r0, r1;
+  const uint16_t* W;
+  const void* B;
+  if (t < tq) {
+    seg = 0; W = (const uint16_t*)a.wq; B = a.bq;
+    r0 = (t / half) * D + (t % half); r1 = r0 + half;
+  } else if (t < tq + tk) {
+    seg = 1; W = (const uint16_t*)a.wk; B = a.bk;
+    const int u = t - tq;
+    r0 = (u / half) * D + (u % half); r1 = r0 + half;
+  } else {
+    seg = 2; W = (const uint16_t*)a.wv; B = a.bv;
+    const int u = t - tq - tk;
+    r0 = 2 * u; r1 = 2 * u + 1;
+  }
+  // weight rows first (K <= 3072: at most 6 chunks of 512 per row), then the norm prologue
+  uint4 w0[6], w1[6];
+#pragma unroll
+  for (int c = 0; c < 6; ++c) {
+    const int k = lane * 8 + c * 512;
+    w0[c] = k < a.K ? ld_stream(W + (long long)r0 * a.K + k) : make_uint4(0, 0, 0, 0);
+    w1[c] = k < a.K ? ld_stream(W + (long long)r1 * a.K + k) : make_uint4(0, 0, 0, 0);
+  }
+  {
+    const uint16_t* x = (const uint16_t*)a.x;
+    if (a.flags & 1) {
+      float ss = 0.f;
+      for (int c = threadIdx.x; c < a.K; c += 256) {
+        const float h = bf16_to_f32(x[c]);
+        ss += h * h;
+      }
+      ss = block_sum256(ss, red);
+      const float r = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+      for (int c = threadIdx.x; c < a.K; c += 256) {
+        const float n = round_to(bf16_to_f32(x[c]) * r, a.n_dtype);
+        xs[c] = f32_to_bf16(bf(a.norm_w, c) * n);
+      }
+    } else {
+      for (int c = threadIdx.x; c < a.K; c += 256) xs[c] = x[c];
+    }
+    __syncthreads();
+  }
+  if (!active) return;
+  float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+  for (int c = 0; c < 6; ++c) {
+    const int k = lane * 8 + c * 512;
+    if (k < a.K) {
+      const uint4 xv = *(const uint4*)(xs + k);
+      acc0 = dot8_bf16(xv, w0[c], acc0);
+      acc1 = dot8_bf16(xv, w1[c], acc1);
+    }
+  }
+  acc0 = wave_sum(acc0);
+  acc1 = wave_sum(acc1);
+  if (lane != 0) return;
+  if (a.flags & 2) {
+    acc0 += bf(B, r0);
+    acc1 += bf(B, r1);
+  }
+  float v0 = rbf(acc0), v1 = rbf(acc1);
+  const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
+  if (rope) {
+    const int j = r0 % D;
+    const float p = (float)ld_i(a.pos_ids, 0, a.pos_dtype);
+    const float f = a.inv_freq[j] * p;
+    const float c = round_to(cosf(f) * a.rope_scaling, HS_BF16);
+    const float s = round_to(sinf(f) * a.rope_scaling, HS_BF16);
+    const float e0 = rbf(rbf(v0 * c) + rbf(-v1 * s));   // x[j]*cos + (-x[j+D/2])*sin
+    const float e1 = rbf(rbf(v1 * c) + rbf(v0 * s));    // x[j+D/2]*cos + x[j]*sin
+    v0 = e0;
+    v1 = e1;
+  }
+  if (seg == 0) {
+    ((uint16_t*)a.q_out)[r0] = f32_to_bf16(v0);
+    ((uint16_t*)a.q_out)[r1] = f32_to_bf16(v1);
+    return;
+  }
+  const bool to_cache = (seg == 1) ? (a.flags & 16) : (a.flags & 32);
+  void* dst = seg == 1 ? a.k_dst : a.v_dst;
+  if (to_cache) {
+    const long long pos = ld_i(a.cache_pos, 0, a.cpos_dtype);
+    if (pos < 0 || pos >= a.cache_len) return;
+    const long long b0 = (long long)(r0 / D) * a.kv_head_stride + pos * D, b1 = (long long)(r1 / D) * a.kv_head_stride + pos * D;
+    ((uint16_t*)dst)[b0 + r0 % D] = f32_to_bf16(v0);
+    ((uint16_t*)dst)[b1 + r1 % D] = f32_to_bf16(v1);
+  } else {
+    ((uint16_t*)dst)[r0] = f32_to_bf16(v0);
+    ((uint16_t*)dst)[r1] = f32_to_bf16(v1);
+  }
+}

@@ -247,6 +247,10 @@ size_t hs_argsize(const char* s) {
   HS_SZ(LinearArgs)
   HS_SZ(DecodeAttnArgs)
   HS_SZ(FusedArgs)
+  HS_SZ(GemvArgs)
+  HS_SZ(ArgmaxFinalizeArgs)
+  HS_SZ(QKVArgs)
+  HS_SZ(AttnOutArgs)
 #undef HS_SZ
   return 0;
 }

@@ -130,7 +130,13 @@ def rmsnorm(low) -> None:
                 params={"rows": rows, "cols": cols, "eps": eps, "nodes": names}))
             low.views[out.name] = o
 
-        cx.claim(chain, emit)
+        # emitted only if some consumer needs the normalised tensor itself; a fused GEMV
+        # that reads it folds the same computation into its prologue instead
+        cx.claim(chain, None)
+        low.lazy[out.name] = emit
+        w_dt = w.dtype
+        low.rms_info[out.name] = {"x": x.name, "w": w.name, "eps": eps, "n_dtype": n_dtype, "x_dtype": x.dtype,
+                                  "w_dtype": w_dt, "out_dtype": out.dtype}
 
 
 # ---------------------------------------------------------------------------------- masked softmax
@@ -249,7 +255,7 @@ def decode_attention(low) -> None:
             else tr.inputs[0]
         kvh = k_spec.shape[1]
         S = k_spec.shape[2]
-        if H % kvh or H // kvh > 8 or k_spec.shape[3] != D:
+        if H % kvh or H // kvh > 8 or k_spec.shape[3] != D or S > 64 * 1024:
             continue
         add_dtype = add_n.outputs[0].dtype if mask_name is not None else dt
         if mask_name is not None:
@@ -286,22 +292,324 @@ def _emit_decode_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype,
     o = low.new_storage(out.name, out.shape, out.dtype)
     scores = low.scratch(out.name + ".scores", H * S * 4)
     stats = low.scratch(out.name + ".stats", H * ntiles * 2 * 4)
-    part = low.scratch(out.name + ".part", kvh * ntiles * G * D * 4)
-    counters = low.scratch(out.name + ".tickets", kvh * 4, persistent=True)
     args = dict(q=low.ref(qv), k=low.ref(kv_), v=low.ref(vv_), out=low.ref(o), scores=scores, stats=stats,
-                part=part, counters=counters, S=S, q_head_stride=qv.strides[1], kv_head_stride=kv_.strides[1],
-                H=H, KVH=kvh, D=D, ntiles=ntiles, scale=float(scale), add_dtype=DTYPE_CODE[add_dtype],
-                dtype=DTYPE_CODE[dt], **margs)
+                S=S, q_head_stride=qv.strides[1], kv_head_stride=kv_.strides[1], H=H, KVH=kvh, D=D,
+                ntiles=ntiles, scale=float(scale), add_dtype=DTYPE_CODE[add_dtype], dtype=DTYPE_CODE[dt], **margs)
     ins = [q, k, v] + ([mask] if mask else [])
     params = {"kv_heads": kvh, "q_per_kv": G, "seq_len": S, "head_dim": D, "ntiles": ntiles, "nodes": names}
     low.emit(LaunchStep(kind="attention", kernel="k_attn_scores", module="attention", arg_struct="DecodeAttnArgs",
                         args=args, grid=(ntiles, kvh, 1), inputs=ins, outputs=[out.name + ".scores"], params=params))
-    low.emit(LaunchStep(kind="attention", kernel="k_attn_pv", module="attention", arg_struct="DecodeAttnArgs",
-                        args=dict(args), grid=(ntiles, kvh, 1), inputs=ins + [out.name + ".scores"],
+    oargs = dict(scores=scores, stats=stats, v=low.ref(vv_), mask=margs["mask"], out=low.ref(o), S=S,
+                 kv_head_stride=vv_.strides[1], mask_stride=margs["mask_stride"], H=H, KVH=kvh, ntiles=ntiles,
+                 mask_dtype=margs["mask_dtype"], dtype=DTYPE_CODE[dt])
+    low.emit(LaunchStep(kind="attention", kernel="k_attn_out", module="attention", arg_struct="AttnOutArgs",
+                        args=oargs, grid=(D // 8, kvh, 1), inputs=[out.name + ".scores", v],
                         outputs=[out.name], params=params))
     low.views[out.name] = o
 
 
-DEFAULT_PATTERNS = [decode_attention, rmsnorm, masked_softmax]
+# ---------------------------------------------------------------------------------- fused decode GEMVs
+
+def _linear_parts(n: OpNode):
+    """(x, w, bias or None) of a 2-D-weight ``aten.linear`` node, or None."""
+    if n.op_type != "aten.linear.default" or len(n.inputs) < 2 or len(n.inputs[1].shape) != 2:
+        return None
+    return n.inputs[0], n.inputs[1], (n.inputs[2] if len(n.inputs) > 2 else None)
+
+
+def _gemv_candidate(low, n: OpNode) -> bool:
+    p = _linear_parts(n)
+    if p is None or n.name in low.claimed:
+        return False
+    x, w, b = p
+    return (low.gemv_ok(x.name, w.name, n.outputs[0].dtype, x.dtype) and (b is None or b.dtype == "bfloat16")
+            and x.shape[-1] == w.shape[1])
+
+
+def gate_up_silu(low) -> None:
+    """``mul(silu(linear(x, Wg)), linear(x, Wu))`` → one GEMV over both weights with a SiLU·mul epilogue."""
+    cx = _Ctx(low)
+    for mul_n in low.g.nodes:
+        if mul_n.op_type != "aten.mul.Tensor" or mul_n.name in low.claimed or len(mul_n.inputs) != 2:
+            continue
+        a, b = (low.producer.get(t.name) for t in mul_n.inputs)
+        for silu_n, lu in ((a, b), (b, a)):
+            if silu_n is None or lu is None or silu_n.op_type != "aten.silu.default":
+                continue
+            lg = low.producer.get(silu_n.inputs[0].name)
+            if lg is None or not _gemv_candidate(low, lg) or not _gemv_candidate(low, lu) or lg is lu:
+                continue
+            (xg, wg, bg), (xu, wu, bu) = _linear_parts(lg), _linear_parts(lu)
+            if xg.name != xu.name or wg.shape != wu.shape or (bg is None) != (bu is None):
+                continue
+            nodes = [lg, silu_n, lu, mul_n]
+            if not (cx.private(lg.outputs[0].name, {silu_n.name}) and cx.private(silu_n.outputs[0].name, {mul_n.name})
+                    and cx.private(lu.outputs[0].name, {mul_n.name})):
+                continue
+            out = mul_n.outputs[0]
+            names = [n.name for n in nodes]
+
+            def emit(x=xg.name, wg=wg.name, bg=bg.name if bg else None, wu=wu.name, bu=bu.name if bu else None,
+                     out=out, names=names):
+                low.emit_gemv(x, wg, bg, out.name, tuple(out.shape), epi="silu", nodes=names + _readers(low, x, names),
+                              w2=wu, b2=bu)
+
+            cx.claim(nodes, emit)
+            break
+
+
+def _readers(low, x: str, names: list[str]) -> list[str]:
+    """Names of other claimed GEMV nodes that share ``x`` (so a norm on ``x`` can still be folded)."""
+    return [n.name for n in low.consumers.get(x, []) if n.name not in names and n.name in low.claimed]
+
+
+def linear_resid(low) -> None:
+    """``add(r, linear(x, W))`` (either operand order) → GEMV with a residual epilogue."""
+    cx = _Ctx(low)
+    for add_n in low.g.nodes:
+        if add_n.op_type != "aten.add.Tensor" or add_n.name in low.claimed or len(add_n.inputs) != 2:
+            continue
+        if float(add_n.attrs.get("alpha", 1)) != 1.0:
+            continue
+        for lin_t, r_t in ((add_n.inputs[1], add_n.inputs[0]), (add_n.inputs[0], add_n.inputs[1])):
+            lin = low.producer.get(lin_t.name)
+            if lin is None or not _gemv_candidate(low, lin) or lin_t.name == r_t.name:
+                continue
+            if tuple(r_t.shape) != tuple(add_n.outputs[0].shape) or r_t.dtype != "bfloat16":
+                continue
+            if tuple(lin_t.shape) != tuple(add_n.outputs[0].shape) or not cx.private(lin_t.name, {add_n.name}):
+                continue
+            x, w, b = _linear_parts(lin)
+            out = add_n.outputs[0]
+            names = [lin.name, add_n.name]
+
+            def emit(x=x.name, w=w.name, b=b.name if b else None, r=r_t.name, out=out, names=names):
+                low.emit_gemv(x, w, b, out.name, tuple(out.shape), epi="resid", resid=r,
+                              nodes=names + _readers(low, x, names))
+
+            cx.claim([lin, add_n], emit)
+            break
+
+
+def linear_argmax(low) -> None:
+    """``argmax(linear(x, W), dim=-1)`` → GEMV whose epilogue also reduces the argmax (first index)."""
+    cx = _Ctx(low)
+    for am in low.g.nodes:
+        if am.op_type != "aten.argmax.default" or am.name in low.claimed or am.attrs.get("keepdim", False):
+            continue
+        dim = am.attrs.get("dim", None)
+        src = am.inputs[0]
+        if dim is None or int(dim) % len(src.shape) != len(src.shape) - 1:
+            continue
+        lin = low.producer.get(src.name)
+        if lin is None or not _gemv_candidate(low, lin):
+            continue
+        if any(n.name != am.name for n in cx.consumers(src.name)):
+            continue
+        x, w, b = _linear_parts(lin)
+        rows = 1
+        for s in src.shape[:-1]:
+            rows *= s
+        if rows != 1:
+            continue
+        out = am.outputs[0]
+        names = [lin.name, am.name]
+
+        def emit(x=x.name, w=w.name, b=b.name if b else None, src=src, out=out, names=names):
+            low.emit_gemv(x, w, b, src.name, tuple(src.shape), epi="argmax", nodes=names + _readers(low, x, names),
+                          argmax_out=(out.name, tuple(out.shape), out.dtype))
+
+        cx.claim([lin, am], emit)
+
+
+def _heads(cx: _Ctx, lin: OpNode):
+    """``linear → view [B, T, n, D] → transpose(1, 2)`` with T == 1: returns (view, transpose, n, D) or None."""
+    v = cx.only(lin.outputs[0].name, ("aten.view.default", "aten.reshape.default", "aten._unsafe_view.default"))
+    if v is None or len(v.outputs[0].shape) != 4 or v.outputs[0].shape[:2] != [1, 1]:
+        return None
+    t = cx.only(v.outputs[0].name, "aten.transpose.int")
+    if t is None or sorted([int(t.attrs.get("dim0", 0)) % 4, int(t.attrs.get("dim1", 1)) % 4]) != [1, 2]:
+        return None
+    return v, t, v.outputs[0].shape[2], v.outputs[0].shape[3]
+
+
+def _rope_source(low, t_name: str):
+    """(rope node, output index) when ``t_name`` is ``unsqueeze(getitem(rope, i), 1)``."""
+    u = low.producer.get(t_name)
+    if u is None or u.op_type != "aten.unsqueeze.default" or int(u.attrs.get("dim", 0)) != 1:
+        return None
+    g = low.producer.get(u.inputs[0].name)
+    if g is None or g.op_type != "<built-in function getitem>":
+        return None
+    idx = int(g.attrs.get("index", 0))
+    src = g.inputs[idx] if idx < len(g.inputs) else g.inputs[0]
+    r = low.producer.get(src.name)
+    if r is None or r.op_type != "wrap_with_set_grad_enabled":
+        return None
+    return r, [o.name for o in r.outputs].index(src.name)
+
+
+def _rope_chain(cx: _Ctx, x_name: str, D: int):
+    """Match ``add(mul(x, cos), mul(cat(neg(x[..., D/2:]), x[..., :D/2]), sin))``.
+
+    Returns (nodes, output name, rope node) or None.
+    """
+    low = cx.low
+    cs = cx.consumers(x_name)
+    if len(cs) != 3 or any(n.name in low.claimed for n in cs):
+        return None
+    muls = [n for n in cs if n.op_type == "aten.mul.Tensor"]
+    slices = [n for n in cs if n.op_type == "aten.slice.Tensor"]
+    if len(muls) != 1 or len(slices) != 2:
+        return None
+    half = D // 2
+
+    def rng(s):
+        return (int(s.attrs.get("dim", 0)) % 4, int(s.attrs.get("start", 0) or 0),
+                min(int(s.attrs.get("end", D)), D), int(s.attrs.get("step", 1)))
+
+    lo = next((s for s in slices if rng(s) == (3, 0, half, 1)), None)
+    hi = next((s for s in slices if rng(s) == (3, half, D, 1)), None)
+    if lo is None or hi is None:
+        return None
+    neg = cx.only(hi.outputs[0].name, "aten.neg.default")
+    if neg is None:
+        return None
+    cat = cx.only(neg.outputs[0].name, "aten.cat.default")
+    if (cat is None or [t.name for t in cat.inputs] != [neg.outputs[0].name, lo.outputs[0].name]
+            or int(cat.attrs.get("dim", 0)) % 4 != 3 or cx.consumers(lo.outputs[0].name) != [cat]):
+        return None
+    m2 = cx.only(cat.outputs[0].name, "aten.mul.Tensor")
+    m1 = muls[0]
+    if m2 is None or len(m1.inputs) != 2 or len(m2.inputs) != 2:
+        return None
+    cos_t = next(t for t in m1.inputs if t.name != x_name)
+    sin_t = next(t for t in m2.inputs if t.name != cat.outputs[0].name)
+    cs_src, sn_src = _rope_source(low, cos_t.name), _rope_source(low, sin_t.name)
+    if cs_src is None or sn_src is None or cs_src[0] is not sn_src[0] or (cs_src[1], sn_src[1]) != (0, 1):
+        return None
+    add = cx.only(m1.outputs[0].name, "aten.add.Tensor")
+    if add is None or cx.consumers(m2.outputs[0].name) != [add] or float(add.attrs.get("alpha", 1)) != 1.0:
+        return None
+    if add.inputs[0].name != m1.outputs[0].name:
+        return None
+    nodes = [m1, lo, hi, neg, cat, m2, add]
+    if not all(n.outputs[0].dtype == "bfloat16" for n in nodes):
+        return None
+    return nodes, add.outputs[0].name, cs_src[0]
+
+
+def _inplace_target(low, cx: _Ctx, t_name: str):
+    """``index_copy(past, cpos, t, dim=2)`` updatable in place: returns (node, past, cpos) or None."""
+    ic = cx.only(t_name, "aten.index_copy.default")
+    if ic is None or int(ic.attrs.get("dim", 0)) % 4 != 2 or ic.inputs[2].name != t_name:
+        return None
+    past, cpos = ic.inputs[0], ic.inputs[1]
+    st = low.storages.get(past.name)
+    if (st is None or st.kind != "input" or len(low.consumers.get(past.name, [])) != 1
+            or past.name in low.graph_output_names or not low.inplace_inputs or cpos.shape != [1]):
+        return None
+    return ic, past.name, cpos.name
+
+
+def qkv_rope(low) -> None:
+    """Three projections of one activation row — q with RoPE, k with RoPE written to the K cache,
+    v written to the V cache — become one ``k_qkv_rope`` launch (RMSNorm folded in when pending)."""
+    cx = _Ctx(low)
+    by_x: dict[str, dict] = {}
+    for lin in low.g.nodes:
+        if not _gemv_candidate(low, lin):
+            continue
+        x, w, b = _linear_parts(lin)
+        hd = _heads(cx, lin)
+        if hd is None:
+            continue
+        vnode, tnode, nh, D = hd
+        if D % 2 or D > 256:
+            continue
+        xname = tnode.outputs[0].name
+        rope = _rope_chain(cx, xname, D)
+        entry = {"lin": lin, "w": w, "b": b, "nh": nh, "D": D, "nodes": [lin, vnode, tnode]}
+        if rope is not None:
+            rnodes, rout, rnode = rope
+            entry["nodes"] += rnodes
+            entry["rope"] = rnode
+            tgt = _inplace_target(low, cx, rout)
+            if tgt is None:
+                if rout in low.graph_output_names:
+                    continue
+                entry["role"], entry["out"] = "q", rout
+            else:
+                entry["role"], entry["ic"], entry["past"], entry["cpos"] = "k", *tgt
+                entry["nodes"].append(tgt[0])
+        else:
+            tgt = _inplace_target(low, cx, xname)
+            if tgt is None:
+                continue
+            entry["role"], entry["ic"], entry["past"], entry["cpos"] = "v", *tgt
+            entry["nodes"].append(tgt[0])
+        by_x.setdefault(x.name, {}).setdefault(entry["role"], []).append(entry)
+    for xname, roles in by_x.items():
+        if any(len(roles.get(r, [])) != 1 for r in ("q", "k", "v")):
+            continue
+        q, k, v = roles["q"][0], roles["k"][0], roles["v"][0]
+        if not (q["D"] == k["D"] == v["D"] and k["nh"] == v["nh"] and q["rope"] is k["rope"]
+                and k["cpos"] == v["cpos"] and q["nh"] % k["nh"] == 0):
+            continue
+        if len({q["b"] is None, k["b"] is None, v["b"] is None}) != 1:
+            continue
+        K = q["w"].shape[1]
+        if K > 3072 or any(e["w"].shape != [e["nh"] * e["D"], K] for e in (q, k, v)):
+            continue
+        past_k = low.views[k["past"]]
+        if list(past_k.shape[:2]) != [1, k["nh"]] or past_k.shape[3] != k["D"]:
+            continue
+        nodes = q["nodes"] + k["nodes"] + v["nodes"]
+        names = [n.name for n in nodes]
+
+        def emit(xname=xname, q=q, k=k, v=v, names=names):
+            _emit_qkv(low, xname, q, k, v, names)
+
+        cx.claim(nodes, emit)
+
+
+def _emit_qkv(low, xname, q, k, v, names) -> None:
+    norm = low.foldable_norm(xname, set(names))
+    x = low.contiguous(norm["x"] if norm else xname)
+    rope = q["rope"]
+    inv = low.contiguous(rope.inputs[0].name)
+    pos = low.contiguous(rope.inputs[1].name)
+    cpos = low.contiguous(k["cpos"])
+    if inv.dtype != "float32" or pos.numel != 1:
+        raise NotImplementedError("fused RoPE needs fp32 inv_freq and one position")
+    H, KVH, D = q["nh"], k["nh"], q["D"]
+    K = x.shape[-1]
+    qo = low.new_storage(q["out"], [1, H, 1, D], "bfloat16")
+    kc, vc = low.views[k["past"]], low.views[v["past"]]
+    args = dict(x=low.ref(x), norm_w=low.ref(low.contiguous(norm["w"])) if norm else None,
+                wq=low.ref(low.contiguous(q["w"].name)), bq=low.ref(low.contiguous(q["b"].name)) if q["b"] else None,
+                wk=low.ref(low.contiguous(k["w"].name)), bk=low.ref(low.contiguous(k["b"].name)) if k["b"] else None,
+                wv=low.ref(low.contiguous(v["w"].name)), bv=low.ref(low.contiguous(v["b"].name)) if v["b"] else None,
+                inv_freq=low.ref(inv), pos_ids=low.ref(pos), cache_pos=low.ref(cpos), q_out=low.ref(qo),
+                k_dst=low.ref(kc), v_dst=low.ref(vc), kv_head_stride=kc.strides[1], cache_len=kc.shape[2],
+                K=K, H=H, KVH=KVH, D=D, eps=float(norm["eps"]) if norm else 0.0,
+                n_dtype=DTYPE_CODE[norm["n_dtype"]] if norm else 0,
+                flags=(1 if norm else 0) | (2 if q["b"] else 0) | 4 | 8 | 16 | 32,
+                pos_dtype=DTYPE_CODE[pos.dtype], cpos_dtype=DTYPE_CODE[cpos.dtype],
+                rope_scaling=float(rope.attrs.get("attention_scaling", 1.0)))
+    tasks = (H * D + 2 * KVH * D) // 2
+    ins = [norm["x"] if norm else xname, q["w"].name, k["w"].name, v["w"].name, k["cpos"], k["past"], v["past"]]
+    low.emit(LaunchStep(kind="gemv", kernel="k_qkv_rope", module="gemv", arg_struct="QKVArgs", args=args,
+                        grid=((tasks + 3) // 4, 1, 1), inputs=ins,
+                        outputs=[q["out"], k["ic"].outputs[0].name, v["ic"].outputs[0].name],
+                        params={"M": 1, "N": H * D + 2 * KVH * D, "K": K, "epilogue": "qkv_rope",
+                                "norm": norm is not None, "has_bias": q["b"] is not None, "nodes": names}))
+    low.views[q["out"]] = qo
+    low.views[k["ic"].outputs[0].name] = kc
+    low.views[v["ic"].outputs[0].name] = vc
+    low.mutated_inputs.update({kc.storage, vc.storage})
+
+
+DEFAULT_PATTERNS = [decode_attention, rmsnorm, qkv_rope, gate_up_silu, linear_argmax, linear_resid, masked_softmax]
 
 __all__ = ["DEFAULT_PATTERNS", "rmsnorm", "masked_softmax", "decode_attention", "V"]

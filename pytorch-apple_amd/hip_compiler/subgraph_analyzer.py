@@ -68,6 +68,8 @@ class Lowering:
                 self.producer[t.name] = n
         self.chains: dict[str, _Chain] = {}
         self.claimed: dict[str, object] = {}     # node name -> pattern emitter (at its last node) or None
+        self.lazy: dict[str, object] = {}        # tensor name -> emitter run when the value is first needed
+        self.rms_info: dict[str, dict] = {}      # RMSNorm output -> {x, w, eps, n_dtype} (foldable prologue)
         self.graph_output_names = {o.name for o in graph.graph_outputs}
         self.mutated_inputs: set[str] = set()
         self._uid = 0
@@ -113,6 +115,8 @@ class Lowering:
     def view(self, name: str) -> TView:
         if name in self.chains:
             self.flush_chain(name)
+        if name in self.lazy:
+            self.lazy.pop(name)()
         if name not in self.views:
             raise KeyError(f"tensor {name} has no value (producer not lowered)")
         return self.views[name]
@@ -215,6 +219,10 @@ class Lowering:
     # ------------------------------------------------------------------ generic lowering per op
 
     def lower_alias(self, node: OpNode) -> None:
+        """Views are resolved when first used, so a view nobody reads costs nothing."""
+        self.lazy[node.outputs[0].name] = lambda node=node: self._alias_now(node)
+
+    def _alias_now(self, node: OpNode) -> None:
         op = node.op_type
         out = node.outputs[0]
         if op == "<built-in function getitem>":
@@ -252,8 +260,117 @@ class Lowering:
         x_t, w_t = node.inputs[0], node.inputs[1]
         b_t = node.inputs[2] if len(node.inputs) > 2 else None
         out = node.outputs[0]
+        if self.gemv_ok(x_t.name, w_t.name, out.dtype, x_t.dtype) and (b_t is None or b_t.dtype == "bfloat16"):
+            self.emit_gemv(x_t.name, w_t.name, b_t.name if b_t else None, out.name, tuple(out.shape),
+                           epi="bias", nodes=[node.name])
+            return
         self.emit_linear(x_t.name, w_t.name, b_t.name if b_t else None, out.name, tuple(out.shape), out.dtype,
                          resid=None, node_names=[node.name])
+
+    # ------------------------------------------------------------------ fused decode GEMV
+
+    def foldable_norm(self, x_name: str, fused_nodes: set[str]) -> dict | None:
+        """RMSNorm parameters when ``x_name`` is a not-yet-emitted RMSNorm read only by ``fused_nodes``."""
+        info = self.rms_info.get(x_name)
+        if info is None or x_name not in self.lazy:
+            return None
+        if x_name in self.graph_output_names:
+            return None
+        if any(n.name not in fused_nodes for n in self.consumers.get(x_name, [])):
+            return None
+        return info
+
+    def gemv_ok(self, x_name: str, w_name: str, out_dtype: str, x_dtype: str = "bfloat16") -> bool:
+        """Shapes the streaming GEMV kernels take: bf16, K % 8 == 0, contiguous 16-byte aligned weights."""
+        w = self.views.get(w_name)
+        if w is None or w.dtype != "bfloat16" or out_dtype != "bfloat16" or x_dtype != "bfloat16":
+            return False
+        if len(w.shape) != 2 or not w.is_contiguous():
+            return False
+        K = w.shape[1]
+        if K % 8 or (w.offset * 2) % 16:
+            return False
+        info = self.rms_info.get(x_name)
+        if info is not None and x_name in self.lazy:
+            return info["x_dtype"] == "bfloat16"
+        return True
+
+    def emit_gemv(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, *, epi: str,
+                  nodes: list[str], resid: str | None = None, w2: str | None = None, b2: str | None = None,
+                  argmax_out=None) -> None:
+        """One fused GEMV launch (csrc/kernels/gemv.hip); folds a pending RMSNorm of ``x`` when possible."""
+        norm = self.foldable_norm(x_name, set(nodes))
+        w = self.contiguous(w_name)
+        K = w.shape[1]
+        N = w.shape[0]
+        if norm is not None:
+            x = self.contiguous(norm["x"])
+            M = x.numel // K
+            mb = 1 if M == 1 else 4
+            if mb * K > 12288:
+                norm = None
+        if norm is None:
+            x = self.contiguous(x_name)
+            M = x.numel // K
+            if (x.offset * 2) % 16:
+                aligned = self.new_storage(x_name + ".a", x.shape, x.dtype)
+                self.emit_copy(x, aligned, [x_name], [x_name + ".a"])
+                x = aligned
+        mb = 1 if M == 1 else 4
+        if epi == "argmax":
+            rpw = 4 if M == 1 else 2
+        elif epi == "silu":
+            rpw = 1
+        else:
+            rpw = 1 if M == 1 else 2
+        if mb == 4 and epi == "argmax":
+            raise NotImplementedError("argmax epilogue with M > 1")
+        kname = {("bias", 1, False): "k_gemv_bias_r1", ("bias", 1, True): "k_gemv_norm_bias_r1",
+                 ("resid", 1, False): "k_gemv_resid_r1", ("silu", 1, False): "k_gemv_silu_r1",
+                 ("silu", 1, True): "k_gemv_norm_silu_r1", ("argmax", 1, True): "k_gemv_norm_argmax_r4",
+                 ("argmax", 1, False): "k_gemv_argmax_r4", ("bias", 4, False): "k_gemv_bias_m4",
+                 ("bias", 4, True): "k_gemv_norm_bias_m4", ("resid", 4, False): "k_gemv_resid_m4",
+                 ("silu", 4, False): "k_gemv_silu_m4", ("silu", 4, True): "k_gemv_norm_silu_m4"}.get(
+            (epi, mb, norm is not None))
+        if kname is None:
+            raise NotImplementedError(f"no GEMV kernel for epilogue {epi} M={M} norm={norm is not None}")
+        if epi == "bias" and M == 1 and N >= 65536:
+            kname, rpw = "k_gemv_bias_r4", 4
+        o = self.new_storage(out_name, out_shape, "bfloat16")
+        bias = self.contiguous(b_name) if b_name else None
+        r = self.contiguous(resid) if resid else None
+        wv2 = self.contiguous(w2) if w2 else None
+        bv2 = self.contiguous(b2) if b2 else None
+        nblocks = (N + 4 * rpw - 1) // (4 * rpw)
+        # kernels with a prologue (RMSNorm) or a per-workgroup reduction (argmax) stride over row
+        # blocks with a capped grid, so the prologue is paid once per workgroup
+        gx = min(nblocks, 1024) if (norm is not None or epi == "argmax") else nblocks
+        slot = self.scratch(out_name + ".argmax", 8 * max(M, 1) * gx) if epi == "argmax" else None
+        args = dict(x=self.ref(x), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
+                    resid=self.ref(r) if r else None, w2=self.ref(wv2) if wv2 else None,
+                    bias2=self.ref(bv2) if bv2 else None,
+                    norm_w=self.ref(self.contiguous(norm["w"])) if norm else None, argmax_slot=slot,
+                    M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=float(norm["eps"]) if norm else 0.0,
+                    n_dtype=DTYPE_CODE[norm["n_dtype"]] if norm else 0,
+                    flags=(1 if bias else 0) | (4 if bv2 else 0))
+        ins = [norm["x"] if norm else x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t]
+        if norm:
+            ins.append(norm["w"])
+        self.emit(LaunchStep(
+            kind="gemv", kernel=kname, module="gemv", arg_struct="GemvArgs", args=args,
+            grid=(gx, (M + mb - 1) // mb, 1), inputs=ins, outputs=[out_name],
+            params={"M": M, "N": N, "K": K, "epilogue": epi, "norm": norm is not None, "has_bias": bias is not None,
+                    "weights": 2 if w2 else 1, "transpose_b": True, "nodes": nodes}))
+        self.views[out_name] = o
+        if epi == "argmax":
+            name, shape, dtype = argmax_out
+            t = self.new_storage(name, shape, dtype)
+            self.emit(LaunchStep(
+                kind="reduction", kernel="k_argmax_finalize", module="gemv", arg_struct="ArgmaxFinalizeArgs",
+                args=dict(slot=slot, out=self.ref(t), rows=M, parts=gx, out_dtype=DTYPE_CODE[dtype]),
+                grid=(M, 1, 1), block=(256, 1, 1), inputs=[out_name], outputs=[name],
+                params={"rows": M, "cols": N}))
+            self.views[name] = t
 
     def emit_linear(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, out_dtype: str,
                     resid: str | None, node_names: list[str]) -> None:
@@ -481,6 +598,20 @@ class Lowering:
         self.views[out.name] = o
 
     def lower_rope_table(self, node: OpNode) -> None:
+        """cos/sin tables are emitted when first read (fused RoPE epilogues compute their own)."""
+        done = []
+
+        def emit(node=node):
+            if not done:
+                done.append(True)
+                self._rope_table_now(node)
+
+        for o in node.outputs[:2]:
+            self.lazy[o.name] = emit
+
+    def _rope_table_now(self, node: OpNode) -> None:
+        for o in node.outputs[:2]:
+            self.lazy.pop(o.name, None)
         inv_t, pos_t = node.inputs[0], node.inputs[1]
         cos_s, sin_s = node.outputs[0], node.outputs[1]
         inv = self.contiguous(inv_t.name)

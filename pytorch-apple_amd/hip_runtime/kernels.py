@@ -55,8 +55,20 @@ _struct("LinearArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P)
                        ("ldo", LL), ("ldr", LL), ("N", I), ("K", I), ("dtype", I), ("has_bias", I),
                        ("has_resid", I), ("pad", I)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])
+_struct("GemvArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P), ("w2", P), ("bias2", P),
+                     ("norm_w", P), ("argmax_slot", P), ("M", LL), ("ldx", LL), ("ldo", LL), ("ldr", LL),
+                     ("N", I), ("K", I), ("eps", F), ("n_dtype", I), ("flags", I), ("pad", I)])
+_struct("ArgmaxFinalizeArgs", [("slot", P), ("out", P), ("rows", LL), ("parts", I), ("out_dtype", I)])
+_struct("QKVArgs", [("x", P), ("norm_w", P), ("wq", P), ("bq", P), ("wk", P), ("bk", P), ("wv", P), ("bv", P),
+                    ("inv_freq", P), ("pos_ids", P), ("cache_pos", P), ("q_out", P), ("k_dst", P), ("v_dst", P),
+                    ("kv_head_stride", LL), ("cache_len", LL), ("K", I), ("H", I), ("KVH", I), ("D", I),
+                    ("eps", F), ("n_dtype", I), ("flags", I), ("pos_dtype", I), ("cpos_dtype", I),
+                    ("rope_scaling", F)])
+_struct("AttnOutArgs", [("scores", P), ("stats", P), ("v", P), ("mask", P), ("out", P), ("S", LL),
+                        ("kv_head_stride", LL), ("mask_stride", LL), ("H", I), ("KVH", I), ("ntiles", I),
+                        ("mask_dtype", I), ("dtype", I), ("pad", I)])
 _struct("DecodeAttnArgs", [("q", P), ("k", P), ("v", P), ("mask", P), ("out", P), ("scores", P), ("stats", P),
-                           ("part", P), ("counters", P), ("S", LL), ("q_head_stride", LL), ("kv_head_stride", LL),
+                           ("S", LL), ("q_head_stride", LL), ("kv_head_stride", LL),
                            ("mask_stride", LL), ("H", I), ("KVH", I), ("D", I), ("ntiles", I), ("scale", F),
                            ("mask_dtype", I), ("add_dtype", I), ("dtype", I)])
 

@@ -32,13 +32,13 @@ def close(got, ref, rtol=RTOL):
     return err / scale
 
 
-def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=()):
+def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True):
     from hip_compiler import compile_subgraph, is_hip_op_supported
     from npu_compiler import partition
     from npu_runtime import DAGExecutor
 
     fn = supported or (lambda op, a=None: is_hip_op_supported(op, a) and op not in force_cpu)
-    ex = DAGExecutor(partition(ir, fn), backend, compile_fn=compile_subgraph)
+    ex = DAGExecutor(partition(ir, fn), backend, compile_fn=lambda sub: compile_subgraph(sub, fuse=fuse))
     ex.load_weights(weights)
     out = ex.execute(inputs)
     return {k: (v if isinstance(v, np.ndarray) else v.to_numpy()) for k, v in out.items()}, ex
@@ -96,12 +96,14 @@ def test_attention_block_cfg2(backend):
     ref = run_cpu(ir, x, w)
     orc = run_ir(ir, x, w)
     for k in got:
+        close(got[k], ref[k])
+        close(got[k], orc[k])
         if k.startswith("index_copy"):
-            assert np.array_equal(got[k], ref[k]), k      # KV update is bit-exact
-            assert np.array_equal(got[k], orc[k]), k
-        else:
-            close(got[k], ref[k])
-            close(got[k], orc[k])
+            # rows other than the written position are untouched copies of the input: bit-exact
+            keep = np.ones(got[k].shape[2], bool)
+            keep[int(x["cache_position"][0])] = False
+            src = x["past_key_0"] if k == "index_copy" else x["past_value_0"]
+            assert np.array_equal(got[k][:, :, keep], src[:, :, keep])
 
 
 @pytest.mark.parametrize("valid", [1, 10, 64, 65, 1000])
@@ -174,7 +176,8 @@ def mini_cfg(layers=2):
                       vocab=4096)
 
 
-def test_decode_step_mini_model(backend):
+@pytest.mark.parametrize("fuse", [True, False])
+def test_decode_step_mini_model(backend, fuse):
     from irgen.qwen import build_decode_ir
     from irgen.workloads import decode_inputs, make_weights
     from oracle.numpy_ref import run_ir
@@ -183,7 +186,7 @@ def test_decode_step_mini_model(backend):
     ir = build_decode_ir(256, cfg, argmax=True)
     w = host(make_weights(ir, cfg))
     x = host(decode_inputs(256, 200, cfg))
-    got, ex = run_hip(ir, x, w, backend)
+    got, ex = run_hip(ir, x, w, backend, fuse=fuse)
     assert_all_npu(ex)
     ref = run_cpu(ir, x, w)
     orc = run_ir(ir, x, w)
@@ -192,7 +195,7 @@ def test_decode_step_mini_model(backend):
     close(got[logits], orc[logits])
     assert int(got["next_token"].reshape(-1)[0]) == int(np.argmax(f32(ref[logits]).reshape(-1)))
     for o in ir["graph_outputs"][1:-1]:
-        assert np.array_equal(got[o["name"]], ref[o["name"]]), o["name"]
+        close(got[o["name"]], ref[o["name"]])
 
 
 def test_greedy_loop_device_resident(backend):
@@ -233,4 +236,86 @@ def test_greedy_loop_device_resident(backend):
             dev_in[i] = o_dev[o]
             cpu_in[i] = o_cpu[o]
     for i in kv_names:
-        assert np.array_equal(dev_in[i].to_numpy(), cpu_in[i]), i
+        # cached K/V rows come out of a floating-point linear (+RoPE): bf16 tolerance, not bit-exact
+        close(dev_in[i].to_numpy(), cpu_in[i])
+
+
+@pytest.mark.parametrize("case", ["single_1d", "multi_1d", "kv_dim2", "dim0_2d", "kv_bf16_dim2"])
+def test_index_copy_kats(backend, case):
+    """Known-answer vectors of tests/test_index_copy.py:23-117 through the HIP path (bit-exact)."""
+    from irgen.builder import IRBuilder
+    from oracle.numpy_ref import index_copy
+
+    rng = np.random.default_rng(0)
+    if case == "single_1d":
+        dst, idx, src, dim, dt = np.array([10, 20, 30, 40, 50], np.float32), [2], np.array([99], np.float32), 0, "float32"
+    elif case == "multi_1d":
+        dst, idx, src, dim, dt = np.arange(8, dtype=np.float32), [1, 3, 5], np.array([100, 200, 300], np.float32), 0, "float32"
+    elif case == "kv_dim2":
+        dst, idx, src, dim, dt = (rng.standard_normal((1, 2, 8, 4)).astype(np.float32), [5],
+                                  rng.standard_normal((1, 2, 1, 4)).astype(np.float32), 2, "float32")
+    elif case == "dim0_2d":
+        dst, idx = np.arange(12, dtype=np.float32).reshape(4, 3), [1, 3]
+        src, dim, dt = np.array([[100, 101, 102], [300, 301, 302]], np.float32), 0, "float32"
+    else:
+        dst = rng.integers(0, 65535, (1, 2, 1025, 128)).astype(np.uint16)
+        src = rng.integers(0, 65535, (1, 2, 1, 128)).astype(np.uint16)
+        idx, dim, dt = [1024], 2, "bfloat16"
+    b = IRBuilder("ic")
+    d = b.input("dst", list(dst.shape), dt)
+    i = b.input("idx", [len(idx)], "int64")
+    s = b.input("src", list(src.shape), dt)
+    b.output(b.op("aten.index_copy.default", [d, i, s], {"dim": dim}))
+    ir = b.to_dict()
+    ins = {"dst": dst, "idx": np.array(idx, np.int64), "src": src}
+    got, _ = run_hip(ir, ins, {}, backend)
+    exp = index_copy(dst, dim, np.array(idx), src)
+    assert np.array_equal(got["index_copy"], exp)
+    assert np.array_equal(got["index_copy"], run_cpu(ir, ins, {})["index_copy"])
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_mlp_block_unfused_generic_path(backend, tokens):
+    """The generic lowering (no pattern fusion) stays correct: rmsnorm kernel, linear kernels, chains."""
+    from irgen.qwen import build_mlp_ir
+    from irgen.workloads import make_weights, mlp_inputs
+
+    ir = build_mlp_ir(tokens)
+    w = host(make_weights(ir, norm_std=0.02))
+    x = host(mlp_inputs(tokens))
+    got, _ = run_hip(ir, x, w, backend, fuse=False)
+    ref = run_cpu(ir, x, w)
+    (name,) = got
+    close(got[name], ref[name])
+
+
+def test_attention_block_unfused_generic_path(backend):
+    from irgen.qwen import build_attention_ir
+    from irgen.workloads import attention_inputs, make_weights
+
+    ir = build_attention_ir(300)
+    w = host(make_weights(ir))
+    x = host(attention_inputs(300))
+    got, _ = run_hip(ir, x, w, backend, fuse=False)
+    ref = run_cpu(ir, x, w)
+    for k in got:
+        close(got[k], ref[k])
+
+
+def test_full_decode_step_real_dims(backend):
+    """cfg3 shapes (hidden 1536, vocab 151936, GQA 12/2, head 128) with 2 layers, vs the CPU fallback."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(layers=2)
+    ir = build_decode_ir(2048, cfg, argmax=True)
+    w = host(make_weights(ir, cfg))
+    x = host(decode_inputs(2048, 1984, cfg))
+    got, ex = run_hip(ir, x, w, backend)
+    assert_all_npu(ex)
+    ref = run_cpu(ir, x, w)
+    logits = ir["graph_outputs"][0]["name"]
+    close(got[logits], ref[logits])
+    assert int(got["next_token"].reshape(-1)[0]) == int(np.argmax(f32(ref[logits]).reshape(-1)))
+    for o in ir["graph_outputs"][1:-1]:
+        close(got[o["name"]], ref[o["name"]])
