@@ -78,9 +78,10 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
   for (int step = 0; step < 2; ++step) {
     const int tp = wave * 16 + step * 8 + g8;
     use[step] = mv[tp] != -INFINITY;
-    const uint4* src = (const uint4*)(K + (t0 + tp) * AT_D + sub * 16);
-    kr[step][0] = use[step] ? src[0] : make_uint4(0, 0, 0, 0);
-    kr[step][1] = use[step] ? src[1] : make_uint4(0, 0, 0, 0);
+    // unconditional load; masked rows read the tile's first row instead (valid, discarded)
+    const uint4* src = (const uint4*)(K + (t0 + (use[step] ? tp : 0)) * AT_D + sub * 16);
+    kr[step][0] = src[0];
+    kr[step][1] = src[1];
   }
 #pragma unroll
   for (int step = 0; step < 2; ++step) {
@@ -132,6 +133,224 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
   }
 }
 
+// ------------------------------------------------------------------ split-S flash decoding
+//
+// k_attn_flash: one workgroup per (split of `spl` positions, KV head). The q rows of
+// the G heads and the split's mask are staged first; then every K and V row of the
+// split is requested at once (8 lanes x 32 B per K row, 16 lanes x 16 B per V row),
+// scores are formed with the model's rounding points (as in k_attn_scores), the
+// split's (max m, sum l) per head computed, and sum_s exp(s - m) v_s accumulated.
+// The partials are combined either by k_attn_combine or inside the next GEMV's
+// prologue (gemv.hip): o = sum_t e^(m_t - M) o_t / sum_t e^(m_t - M) l_t. Compared
+// with the CPU chain, only the bf16 rounding of the probabilities is not repeated.
+#define FL_SPL 128
+
+typedef __attribute__((ext_vector_type(2))) __bf16 fl_bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 fl_f16x2;
+
+template <int DT>
+__device__ __forceinline__ float fl_dot2(uint32_t a, uint32_t b, float acc) {
+  if constexpr (DT == HS_BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(fl_bf16x2, a), __builtin_bit_cast(fl_bf16x2, b), acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(fl_f16x2, a), __builtin_bit_cast(fl_f16x2, b), acc, false);
+}
+
+template <int DT>
+__device__ __forceinline__ void flash_body(const FlashArgs& a) {
+  __shared__ float mv[FL_SPL];
+  __shared__ float sc[AT_GMAX][FL_SPL];
+  __shared__ float red[4][AT_GMAX][AT_D];
+  __shared__ int live;
+  const int G = a.H / a.KVH;
+  const int split = blockIdx.x, kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long p0 = (long long)split * a.spl;
+  const int npos = (int)min((long long)a.spl, a.S - p0);
+  const int pw = a.spl >> 2;                       // positions per wave
+  const int g8 = lane >> 3, sub = lane & 7;        // K: 8 lanes per row, 16 dims each
+  const int g16 = lane >> 4, dv = (lane & 15) * 8; // V: 16 lanes per row, 8 dims each
+  float* ml = a.part_ml + ((long long)(kvh * a.nsplit + split) * G) * 2;
+  float* po = a.part_o + ((long long)(kvh * a.nsplit + split) * G) * AT_D;
+  // q (this lane's 16 dims of each head, kept packed) and the split's mask, in one round trip
+  uint4 qr[AT_GMAX][2];
+#pragma unroll
+  for (int h = 0; h < AT_GMAX; ++h) {
+    const int hh = h < G ? h : 0;
+    const uint4* src = (const uint4*)((const uint16_t*)a.q + (long long)(kvh * G + hh) * a.q_head_stride + sub * 16);
+    qr[h][0] = src[0];
+    qr[h][1] = src[1];
+  }
+  if (threadIdx.x == 0) live = 0;
+  __syncthreads();
+  if ((int)threadIdx.x < a.spl) {
+    float m = -INFINITY;
+    if ((int)threadIdx.x < npos)
+      m = a.mask_dtype < 0 ? 0.f : ld_f(a.mask, (p0 + threadIdx.x) * a.mask_stride, a.mask_dtype);
+    mv[threadIdx.x] = m;
+    if (m != -INFINITY) live = 1;
+  }
+  __syncthreads();
+  if (!live) {   // fully masked split: l = 0 and zero partials (combines read them unconditionally)
+    if (threadIdx.x < G) {
+      ml[threadIdx.x * 2] = -INFINITY;
+      ml[threadIdx.x * 2 + 1] = 0.f;
+    }
+    for (int i = threadIdx.x; i < G * AT_D; i += 256) po[i] = 0.f;
+    return;
+  }
+  const uint16_t* K = (const uint16_t*)a.k + (long long)kvh * a.kv_head_stride + p0 * AT_D;
+  const uint16_t* V = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride + p0 * AT_D;
+  // Every K and V load is issued unconditionally; a masked or out-of-split row reads row 0
+  // of the split instead (valid memory) and is discarded, so all loads stay in flight.
+  uint4 kr[FL_SPL / 32][2];
+  uint4 vr[FL_SPL / 16];
+#pragma unroll
+  for (int st = 0; st < FL_SPL / 32; ++st) {
+    const int tp = wave * pw + st * 8 + g8;
+    const int row = (st * 8 < pw && mv[tp] != -INFINITY) ? tp : 0;
+    const uint4* src = (const uint4*)(K + (long long)row * AT_D + sub * 16);
+    kr[st][0] = src[0];
+    kr[st][1] = src[1];
+  }
+#pragma unroll
+  for (int st = 0; st < FL_SPL / 16; ++st) {
+    const int tp = wave * pw + st * 4 + g16;
+    const int row = (st * 4 < pw && mv[tp] != -INFINITY) ? tp : 0;
+    vr[st] = *(const uint4*)(V + (long long)row * AT_D + dv);
+  }
+  // scores (packed dot products on the raw bf16/fp16 data) with the model's rounding points
+#pragma unroll
+  for (int st = 0; st < FL_SPL / 32; ++st) {
+    if (st * 8 >= pw) break;
+    const int tp = wave * pw + st * 8 + g8;
+    const uint32_t kw[8] = {kr[st][0].x, kr[st][0].y, kr[st][0].z, kr[st][0].w,
+                            kr[st][1].x, kr[st][1].y, kr[st][1].z, kr[st][1].w};
+    float dots[AT_GMAX];
+#pragma unroll
+    for (int h = 0; h < AT_GMAX; ++h) {
+      const uint32_t qw[8] = {qr[h][0].x, qr[h][0].y, qr[h][0].z, qr[h][0].w,
+                              qr[h][1].x, qr[h][1].y, qr[h][1].z, qr[h][1].w};
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fl_dot2<DT>(qw[j], kw[j], acc);
+      acc += __shfl_xor(acc, 4, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      acc += __shfl_xor(acc, 1, 64);
+      dots[h] = acc;
+    }
+    if (sub < G) {
+      float d = dots[0];
+#pragma unroll
+      for (int h = 1; h < AT_GMAX; ++h) d = (sub == h) ? dots[h] : d;
+      float s = -INFINITY;
+      const float m = mv[tp];
+      if (m != -INFINITY) {
+        s = round_to(d, DT);
+        s = round_to(s * a.scale, DT);
+        if (a.mask_dtype >= 0) s = round_to(s + m, a.add_dtype);
+      }
+      sc[sub][tp] = s;
+    }
+  }
+  __syncthreads();
+  // split max / sum per head; sc becomes exp(s - m)
+  for (int h = wave; h < G; h += 4) {
+    float m = -INFINITY;
+    for (int i = lane; i < a.spl; i += 64) m = fmaxf(m, sc[h][i]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int i = lane; i < a.spl; i += 64) {
+      const float s = sc[h][i];
+      const float e = (s == -INFINITY) ? 0.f : expf(s - m);
+      sc[h][i] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      ml[h * 2] = m;
+      ml[h * 2 + 1] = l;
+    }
+  }
+  __syncthreads();
+  float acc[AT_GMAX][8];
+#pragma unroll
+  for (int h = 0; h < AT_GMAX; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
+#pragma unroll
+  for (int st = 0; st < FL_SPL / 16; ++st) {
+    if (st * 4 >= pw) break;
+    const int tp = wave * pw + st * 4 + g16;
+    if (mv[tp] == -INFINITY) continue;   // p = 0 for every head; the loaded row is a stand-in
+    float vf[8];
+    unpack8(vr[st], DT, vf);
+#pragma unroll
+    for (int h = 0; h < AT_GMAX; ++h) {
+      if (h < G) {
+        const float p = sc[h][tp];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(p, vf[j], acc[h][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < AT_GMAX; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[h][j] += __shfl_xor(acc[h][j], 16, 64);
+      acc[h][j] += __shfl_xor(acc[h][j], 32, 64);
+    }
+  if (lane < 16) {
+#pragma unroll
+    for (int h = 0; h < AT_GMAX; ++h)
+      if (h < G)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[wave][h][dv + j] = acc[h][j];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * AT_D; i += 256) {
+    const int h = i / AT_D, d = i % AT_D;
+    po[i] = ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d];
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(256) k_attn_flash(const FlashArgs a) { flash_body<HS_BF16>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_attn_flash_f16(const FlashArgs a) { flash_body<HS_F16>(a); }
+
+// out[h, d] = round(sum_t e^(m_t - M) o_t[d] * (1 / sum_t e^(m_t - M) l_t)); one workgroup per head
+extern "C" __global__ void __launch_bounds__(128) k_attn_combine(const CombineArgs a) {
+  __shared__ float w[1024], lv[1024];
+  __shared__ float inv_l;
+  const int h = blockIdx.x;
+  const int G = a.H / a.KVH, kvh = h / G, g = h % G;
+  const float* ml = a.part_ml + ((long long)kvh * a.nsplit * G + g) * 2;
+  for (int t = threadIdx.x; t < a.nsplit; t += 128) {   // all (m, l) loads in flight at once
+    w[t] = ml[(long long)t * G * 2];
+    lv[t] = ml[(long long)t * G * 2 + 1];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = -INFINITY;
+    for (int t = 0; t < a.nsplit; ++t)
+      if (lv[t] > 0.f) M = fmaxf(M, w[t]);
+    float L = 0.f;
+    for (int t = 0; t < a.nsplit; ++t) {
+      const float e = lv[t] > 0.f ? expf(w[t] - M) : 0.f;
+      w[t] = e;
+      L += e * lv[t];
+    }
+    inv_l = 1.0f / L;
+  }
+  __syncthreads();
+  const int d = threadIdx.x;
+  float s = 0.f;
+  for (int t = 0; t < a.nsplit; ++t)   // dead splits hold zero partials and weight 0
+    s += w[t] * a.part_o[(((long long)kvh * a.nsplit + t) * G + g) * AT_D + d];
+  const float o = s * inv_l;
+  ((uint16_t*)a.out)[(long long)h * AT_D + d] = a.dtype == HS_BF16 ? f32_to_bf16(o) : f32_to_f16(o);
+}
+
 extern "C" __global__ void __launch_bounds__(256) k_attn_out(const AttnOutArgs a) {
   __shared__ float gm[AT_GMAX], ginv[AT_GMAX];
   __shared__ unsigned char tile_live[AT_MAXTILES];
@@ -173,9 +392,13 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_out(const AttnOutArgs a
     for (int r = 0; r < AT_ROUND; ++r) {
       const long long p = base + r * 256 + threadIdx.x;
       const bool ok = p < a.S && tile_live[p / AT_TILE];
-      vr[r] = ok ? *(const uint4*)(V + p * AT_D) : make_uint4(0, 0, 0, 0);
+      const long long pc = ok ? p : 0;   // unconditional loads from a valid row, masked afterwards
+      vr[r] = *(const uint4*)(V + pc * AT_D);
 #pragma unroll
-      for (int h = 0; h < AT_GMAX; ++h) s[r][h] = (ok && h < G) ? SC[(long long)h * a.S + p] : -INFINITY;
+      for (int h = 0; h < AT_GMAX; ++h) {
+        const float raw = SC[(long long)(h < G ? h : 0) * a.S + pc];
+        s[r][h] = (ok && h < G) ? raw : -INFINITY;
+      }
     }
 #pragma unroll
     for (int r = 0; r < AT_ROUND; ++r) {

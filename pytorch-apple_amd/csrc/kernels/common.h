@@ -164,7 +164,9 @@ struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm,
   const void* w2;             // [N, K] second weight (SILU: up projection)
   const void* bias2;          // [N] or null
   const void* norm_w;         // [K] RMSNorm weight (NORM)
-  unsigned long long* argmax_slot;  // [M] packed (value, ~index) keys (ARGMAX), zero before launch
+  unsigned long long* argmax_slot;  // [M, grid.x] packed (value, ~index) keys per workgroup (ARGMAX)
+  const float* attn_o;        // ATTN prologue: split partials of the decode attention feeding x
+  const float* attn_ml;
   long long M;
   long long ldx;
   long long ldo;
@@ -174,7 +176,9 @@ struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm,
   float eps;
   int n_dtype;                // rounding dtype of x * rsqrt(...) (the to(dtype) of the norm)
   int flags;                  // 1: bias, 4: bias2
-  int pad;
+  int attn_heads;             // ATTN prologue: H, KVH, nsplit (x = heads * 128 values)
+  int attn_kvh;
+  int attn_splits;
 };
 
 struct ArgmaxFinalizeArgs {   // out[m] = index of max over the `parts` keys of row m
@@ -240,6 +244,37 @@ struct DecodeAttnArgs {       // GQA decode attention over static caches, split 
   int mask_dtype;             // HS_BF16 / HS_F16 / HS_F32, or -1 for no mask
   int add_dtype;              // dtype of scores + mask in the model (rounding point)
   int dtype;                  // q/k/v/out dtype (HS_BF16 or HS_F16)
+};
+
+struct FlashArgs {            // split-S decode attention: per-split (max, sum, unnormalised p.V)
+  const void* q;              // [H, D]
+  const void* k;              // [KVH, S, D]
+  const void* v;              // [KVH, S, D]
+  const void* mask;           // [S] (stride mask_stride), broadcast over heads
+  float* part_o;              // [KVH, nsplit, G, D] sum_s exp(s - m) v_s over the split
+  float* part_ml;             // [KVH, nsplit, G, 2] (m, l) of the split; l = 0 when fully masked
+  long long S;
+  long long q_head_stride;
+  long long kv_head_stride;
+  long long mask_stride;
+  int H;
+  int KVH;
+  int nsplit;
+  int spl;                    // positions per split (multiple of 64, <= 256)
+  float scale;
+  int mask_dtype;             // -1: no mask
+  int add_dtype;
+  int dtype;
+};
+
+struct CombineArgs {          // out[h, d] = round(sum_t e^(m_t - M) o_t[d] / sum_t e^(m_t - M) l_t)
+  const float* part_o;
+  const float* part_ml;
+  void* out;                  // [H, D]
+  int H;
+  int KVH;
+  int nsplit;
+  int dtype;
 };
 
 struct AttnOutArgs {          // second attention pass: global softmax and p.V per 8-dim slice

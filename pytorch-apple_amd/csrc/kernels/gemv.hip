@@ -66,10 +66,58 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
 
 // Workgroups stride over blocks of 4*RPW weight rows (grid.x may be smaller than the
 // number of blocks), so a prologue is computed once per workgroup, not once per block.
-template <bool NORM, int EPI, int RPW, int MB>
+// x = the decode attention output, combined from its split partials (see attention.hip):
+// x[h*128 + d] = round(sum_t e^(m_t - M_h) o_t[d] / sum_t e^(m_t - M_h) l_t)
+__device__ __forceinline__ void attn_to_lds(const GemvArgs& a, uint16_t* xs) {
+  __shared__ float wt[16][128];
+  __shared__ float lt[16][128];
+  __shared__ float inv_l[16];
+  const int H = a.attn_heads, T = a.attn_splits, G = a.attn_heads / a.attn_kvh;
+  // (m, l) of every (head, split) fetched in parallel: layout [kvh][t][g][2]
+  for (int i = threadIdx.x; i < H * T; i += 256) {
+    const int h = i / T, t = i % T, kvh = h / G, g = h % G;
+    const float* ml = a.attn_ml + (((long long)kvh * T + t) * G + g) * 2;
+    wt[h][t] = ml[0];
+    lt[h][t] = ml[1];
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < H) {
+    const int h = threadIdx.x;
+    float M = -INFINITY;
+    for (int t = 0; t < T; ++t)
+      if (lt[h][t] > 0.f) M = fmaxf(M, wt[h][t]);
+    float L = 0.f;
+    for (int t = 0; t < T; ++t) {
+      const float e = lt[h][t] > 0.f ? expf(wt[h][t] - M) : 0.f;
+      wt[h][t] = e;
+      L += e * lt[h][t];
+    }
+    inv_l[h] = 1.0f / L;
+  }
+  __syncthreads();
+  // x = sum_t w_t o_t / L; dead splits carry zero partials and zero weight, so the loads
+  // are unconditional and a thread's T loads are all in flight together
+  for (int i = threadIdx.x; i < H * 128; i += 256) {
+    const int h = i >> 7, d = i & 127, kvh = h / G, g = h % G;
+    const float* po = a.attn_o + (((long long)kvh * T) * G + g) * 128 + d;
+    float s = 0.f;
+    for (int t = 0; t < T; ++t) s += wt[h][t] * po[(long long)t * G * 128];
+    xs[i] = f32_to_bf16(s * inv_l[h]);
+  }
+  __syncthreads();
+}
+
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ATTN = 2 };
+
+// KS > 1: the 4 waves of a workgroup share the same RPW rows and split K (chunk c goes to
+// wave c % 4); the per-wave partial sums are added in LDS. Used for long rows (K = 8960),
+// so that each wave's loads for a row fit in one round.
+template <int PRO, int EPI, int RPW, int MB, int KS = 1>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[NORM ? GEMV_MB * 1536 * 2 : 8];
+  constexpr bool NORM = PRO != PRO_NONE;   // x comes from LDS
+  __shared__ __attribute__((aligned(16))) uint16_t xs[NORM ? MB * 3072 : 8];
   __shared__ unsigned long long best_w[EPI == EPI_ARGMAX ? 4 * MB : 1];
+  __shared__ float kred[KS > 1 ? 4 * MB * RPW * 2 : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const long long m0 = (long long)blockIdx.y * MB;
@@ -78,7 +126,9 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   const uint16_t* W[NW];
   W[0] = (const uint16_t*)a.w;
   if constexpr (EPI == EPI_SILU) W[1] = (const uint16_t*)a.w2;
-  const int nblocks = (a.N + 4 * RPW - 1) / (4 * RPW);
+  constexpr int ROWS_WG = KS > 1 ? RPW : 4 * RPW;
+  const int nblocks = (a.N + ROWS_WG - 1) / ROWS_WG;
+  const int kstart = (KS > 1 ? wave * 512 : 0) + lane * 8;
   unsigned long long best[MB];
 #pragma unroll
   for (int m = 0; m < MB; ++m) best[m] = 0ull;
@@ -86,13 +136,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   // Rounds of U chunks: every weight load of a round is issued before any is consumed,
   // so a wave keeps U*RPW*NW 16-byte loads in flight instead of waiting on each. The
   // first round is issued before the RMSNorm prologue, which then overlaps its latency.
-  constexpr int U = (RPW * NW >= 4) ? 2 : (RPW * NW >= 2 ? 4 : 8);
+  constexpr int U = 12 / (RPW * NW) > 0 ? 12 / (RPW * NW) : 1;   // 12 x 16 B loads per lane per round
   uint4 wv[U][RPW][NW];
-  int n0 = (blockIdx.x * 4 + wave) * RPW;
+  int n0 = KS > 1 ? blockIdx.x * RPW : (blockIdx.x * 4 + wave) * RPW;
   auto load_round = [&](int kb) {
 #pragma unroll
     for (int c = 0; c < U; ++c) {
-      const int k = kb + c * 512;
+      const int k = kb + c * 512 * KS;
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
         const long long n = min(n0 + r, a.N - 1);
@@ -102,12 +152,24 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
       }
     }
   };
-  load_round(lane * 8);
-  if constexpr (NORM) norm_to_lds(a, m0, mrows, xs);
+  load_round(kstart);
+  if constexpr (PRO == PRO_NORM) norm_to_lds(a, m0, mrows, xs);
+  if constexpr (PRO == PRO_ATTN) attn_to_lds(a, xs);
   for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
-  n0 = (blk * 4 + wave) * RPW;
-  if (blk != (int)blockIdx.x) load_round(lane * 8);
+  n0 = KS > 1 ? blk * RPW : (blk * 4 + wave) * RPW;
+  if (blk != (int)blockIdx.x) load_round(kstart);
   if (n0 >= a.N) continue;
+  // epilogue operands are fetched now so their latency hides behind the weight stream
+  float bpre[RPW], b2pre[RPW], rpre[MB][RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int n = min(n0 + r, a.N - 1);
+    bpre[r] = (a.flags & 1) ? bf(a.bias, n) : 0.f;
+    b2pre[r] = (EPI == EPI_SILU && (a.flags & 4)) ? bf(a.bias2, n) : 0.f;
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+      rpre[m][r] = (EPI == EPI_RESID && m < mrows) ? bf(a.resid, (m0 + m) * a.ldr + n) : 0.f;
+  }
   float acc[MB][RPW][NW];
 #pragma unroll
   for (int m = 0; m < MB; ++m)
@@ -115,11 +177,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
       for (int u = 0; u < NW; ++u) acc[m][r][u] = 0.f;
-  for (int kb = lane * 8; kb < a.K; kb += 512 * U) {
-    if (kb != lane * 8) load_round(kb);
+  for (int kb = kstart; kb < a.K; kb += 512 * U * KS) {
+    if (kb != kstart) load_round(kb);
 #pragma unroll
     for (int c = 0; c < U; ++c) {
-      const int k = kb + c * 512;
+      const int k = kb + c * 512 * KS;
       if (k >= a.K) break;
 #pragma unroll
       for (int m = 0; m < MB; ++m) {
@@ -141,6 +203,26 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     for (int r = 0; r < RPW; ++r)
 #pragma unroll
       for (int u = 0; u < NW; ++u) acc[m][r][u] = wave_sum(acc[m][r][u]);
+  if constexpr (KS > 1) {   // add the four waves' K-partials (fixed order)
+    if (lane == 0)
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+          for (int u = 0; u < NW; ++u) kred[((wave * MB + m) * RPW + r) * NW + u] = acc[m][r][u];
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MB; ++m)
+#pragma unroll
+      for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int u = 0; u < NW; ++u) {
+          const int o = (m * RPW + r) * NW + u, st = MB * RPW * NW;
+          acc[m][r][u] = ((kred[o] + kred[st + o]) + kred[2 * st + o]) + kred[3 * st + o];
+        }
+    __syncthreads();
+  }
 
 #pragma unroll
   for (int m = 0; m < MB; ++m) {
@@ -151,17 +233,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
       const int n = n0 + r;
       if (n >= a.N) continue;
       float v = acc[m][r][0];
-      if (a.flags & 1) v += bf(a.bias, n);
+      if (a.flags & 1) v += bpre[r];
       v = rbf(v);
-      if constexpr (EPI == EPI_RESID) v = bf(a.resid, mm * a.ldr + n) + v;
+      if constexpr (EPI == EPI_RESID) v = rpre[m][r] + v;
       if constexpr (EPI == EPI_SILU) {
         float u = acc[m][r][1];
-        if (a.flags & 4) u += bf(a.bias2, n);
+        if (a.flags & 4) u += b2pre[r];
         u = rbf(u);
         const float s = rbf(v / (1.f + expf(-v)));
         v = s * u;
       }
-      if (lane == 0) ((uint16_t*)a.out)[mm * a.ldo + n] = f32_to_bf16(v);
+      if (lane == 0 && (KS == 1 || wave == 0)) ((uint16_t*)a.out)[mm * a.ldo + n] = f32_to_bf16(v);
       if constexpr (EPI == EPI_ARGMAX) {
         const unsigned long long key = argmax_key(rbf(v), n);
         best[m] = key > best[m] ? key : best[m];
@@ -185,6 +267,11 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
 
 #define GEMV_KERNEL(NAME, NORM, EPI, RPW, MB) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const GemvArgs a) { gemv_body<NORM, EPI, RPW, MB>(a); }
+#define GEMV_KERNEL_KS(NAME, NORM, EPI, RPW, MB) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const GemvArgs a) { gemv_body<NORM, EPI, RPW, MB, 4>(a); }
+
+GEMV_KERNEL_KS(k_gemv_resid_ks_r2, false, EPI_RESID, 2, 1)
+GEMV_KERNEL_KS(k_gemv_bias_ks_r2, false, EPI_BIAS, 2, 1)
 
 GEMV_KERNEL(k_gemv_bias_r1, false, EPI_BIAS, 1, 1)
 GEMV_KERNEL(k_gemv_bias_r4, false, EPI_BIAS, 4, 1)
@@ -199,6 +286,8 @@ GEMV_KERNEL(k_gemv_resid_m4, false, EPI_RESID, 2, 4)
 GEMV_KERNEL(k_gemv_norm_bias_m4, true, EPI_BIAS, 2, 4)
 GEMV_KERNEL(k_gemv_norm_silu_m4, true, EPI_SILU, 1, 4)
 GEMV_KERNEL(k_gemv_silu_m4, false, EPI_SILU, 1, 4)
+GEMV_KERNEL(k_gemv_attn_bias_r4, PRO_ATTN, EPI_BIAS, 4, 1)
+GEMV_KERNEL(k_gemv_attn_resid_r4, PRO_ATTN, EPI_RESID, 4, 1)
 
 // One workgroup per activation row: the largest of the row's per-workgroup keys is the
 // maximum logit with the smallest index among equal maxima (np.argmax's rule).
@@ -254,7 +343,12 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
     const int u = t - tq - tk;
     r0 = 2 * u; r1 = 2 * u + 1;
   }
-  // weight rows first (K <= 3072: at most 6 chunks of 512 per row), then the norm prologue
+  // epilogue operands (bias, positions, rotary frequency) are fetched up front
+  const float b0 = (a.flags & 2) ? bf(B, r0) : 0.f, b1 = (a.flags & 2) ? bf(B, r1) : 0.f;
+  const long long pos_v = ld_i(a.pos_ids, 0, a.pos_dtype);
+  const long long cpos_v = ld_i(a.cache_pos, 0, a.cpos_dtype);
+  const float invf = a.inv_freq[(r0 % D) % half];
+  // weight rows next (K <= 3072: at most 6 chunks of 512 per row), then the norm prologue
   uint4 w0[6], w1[6];
 #pragma unroll
   for (int c = 0; c < 6; ++c) {
@@ -295,16 +389,12 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   acc0 = wave_sum(acc0);
   acc1 = wave_sum(acc1);
   if (lane != 0) return;
-  if (a.flags & 2) {
-    acc0 += bf(B, r0);
-    acc1 += bf(B, r1);
-  }
+  acc0 += b0;
+  acc1 += b1;
   float v0 = rbf(acc0), v1 = rbf(acc1);
   const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
   if (rope) {
-    const int j = r0 % D;
-    const float p = (float)ld_i(a.pos_ids, 0, a.pos_dtype);
-    const float f = a.inv_freq[j] * p;
+    const float f = invf * (float)pos_v;
     const float c = round_to(cosf(f) * a.rope_scaling, HS_BF16);
     const float s = round_to(sinf(f) * a.rope_scaling, HS_BF16);
     const float e0 = rbf(rbf(v0 * c) + rbf(-v1 * s));   // x[j]*cos + (-x[j+D/2])*sin
@@ -320,11 +410,11 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   const bool to_cache = (seg == 1) ? (a.flags & 16) : (a.flags & 32);
   void* dst = seg == 1 ? a.k_dst : a.v_dst;
   if (to_cache) {
-    const long long pos = ld_i(a.cache_pos, 0, a.cpos_dtype);
-    if (pos < 0 || pos >= a.cache_len) return;
-    const long long b0 = (long long)(r0 / D) * a.kv_head_stride + pos * D, b1 = (long long)(r1 / D) * a.kv_head_stride + pos * D;
-    ((uint16_t*)dst)[b0 + r0 % D] = f32_to_bf16(v0);
-    ((uint16_t*)dst)[b1 + r1 % D] = f32_to_bf16(v1);
+    if (cpos_v < 0 || cpos_v >= a.cache_len) return;
+    const long long o0 = (long long)(r0 / D) * a.kv_head_stride + cpos_v * D;
+    const long long o1 = (long long)(r1 / D) * a.kv_head_stride + cpos_v * D;
+    ((uint16_t*)dst)[o0 + r0 % D] = f32_to_bf16(v0);
+    ((uint16_t*)dst)[o1 + r1 % D] = f32_to_bf16(v1);
   } else {
     ((uint16_t*)dst)[r0] = f32_to_bf16(v0);
     ((uint16_t*)dst)[r1] = f32_to_bf16(v1);

@@ -251,6 +251,8 @@ size_t hs_argsize(const char* s) {
   HS_SZ(ArgmaxFinalizeArgs)
   HS_SZ(QKVArgs)
   HS_SZ(AttnOutArgs)
+  HS_SZ(FlashArgs)
+  HS_SZ(CombineArgs)
 #undef HS_SZ
   return 0;
 }

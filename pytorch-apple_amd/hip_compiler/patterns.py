@@ -269,9 +269,56 @@ def decode_attention(low) -> None:
 
         def emit(q=q_t.name, k=k_name, v=v_name, mask=mask_name, out=out, scale=scale, H=H, kvh=kvh, S=S,
                  add_dtype=add_dtype, dt=dt, names=[n.name for n in nodes]):
-            _emit_decode_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names)
+            if low.exact_attention:
+                _emit_decode_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names)
+            else:
+                _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names)
 
         cx.claim(nodes, emit)
+
+
+def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names) -> None:
+    """Split-S partials now; the combine is emitted lazily (or folded into the next GEMV)."""
+    D = 128
+    G = H // kvh
+    qv = low.view(q)
+    if qv.strides[-1] != 1:
+        qv = low.contiguous(q, qv)
+    kv_ = low.contiguous(k)
+    vv_ = low.contiguous(v)
+    if (kv_.offset * 2) % 16 or (vv_.offset * 2) % 16:
+        raise NotImplementedError("attention caches must be 16-byte aligned")
+    spl = 128 if S >= 1024 else 64
+    nsplit = (S + spl - 1) // spl
+    margs = dict(mask=None, mask_stride=0, mask_dtype=-1)
+    if mask is not None:
+        mv = low.view(mask)
+        margs = dict(mask=low.ref(mv), mask_stride=mv.strides[-1], mask_dtype=DTYPE_CODE[mv.dtype])
+    part_o = low.scratch(out.name + ".part_o", kvh * nsplit * G * D * 4)
+    part_ml = low.scratch(out.name + ".part_ml", kvh * nsplit * G * 2 * 4)
+    args = dict(q=low.ref(qv), k=low.ref(kv_), v=low.ref(vv_), part_o=part_o, part_ml=part_ml, S=S,
+                q_head_stride=qv.strides[1], kv_head_stride=kv_.strides[1], H=H, KVH=kvh, nsplit=nsplit, spl=spl,
+                scale=float(scale), add_dtype=DTYPE_CODE[add_dtype], dtype=DTYPE_CODE[dt], **margs)
+    ins = [q, k, v] + ([mask] if mask else [])
+    params = {"kv_heads": kvh, "q_per_kv": G, "seq_len": S, "head_dim": D, "nsplit": nsplit, "spl": spl,
+              "nodes": names}
+    low.emit(LaunchStep(kind="attention", kernel="k_attn_flash" if dt == "bfloat16" else "k_attn_flash_f16",
+                        module="attention", arg_struct="FlashArgs",
+                        args=args, grid=(nsplit, kvh, 1), inputs=ins, outputs=[out.name + ".partials"],
+                        params=params))
+
+    def combine():
+        o = low.new_storage(out.name, out.shape, out.dtype)
+        low.emit(LaunchStep(kind="attention", kernel="k_attn_combine", module="attention", arg_struct="CombineArgs",
+                            args=dict(part_o=part_o, part_ml=part_ml, out=low.ref(o), H=H, KVH=kvh, nsplit=nsplit,
+                                      dtype=DTYPE_CODE[dt]),
+                            grid=(H, 1, 1), block=(D, 1, 1), inputs=[out.name + ".partials"], outputs=[out.name],
+                            params=params))
+        low.views[out.name] = o
+
+    low.lazy[out.name] = combine
+    low.attn_info[out.name] = {"part_o": part_o, "part_ml": part_ml, "H": H, "KVH": kvh, "nsplit": nsplit,
+                               "shape": list(out.shape), "out": out.name}
 
 
 def _emit_decode_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names) -> None:

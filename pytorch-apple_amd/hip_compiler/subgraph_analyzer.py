@@ -22,6 +22,7 @@ grows elementwise chains — with MI355X-specific choices:
 from __future__ import annotations
 
 import math
+import os
 from dataclasses import dataclass, field
 
 from hip_compiler import views as V
@@ -38,6 +39,30 @@ def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
     return (max(1, min(cap, (int(n) + block - 1) // block)), 1, 1)
 
 
+def apply_alias(node: OpNode, v: TView) -> TView | None:
+    """The view a shape op produces from ``v`` (getitem excluded), or None when it needs a copy."""
+    op = node.op_type
+    out = node.outputs[0]
+    a = node.attrs
+    if op in ("aten.transpose.int",):
+        return V.transpose(v, int(a.get("dim0", 0)), int(a.get("dim1", 1)))
+    if op == "aten.t.default":
+        return V.transpose(v, 0, 1) if len(v.shape) == 2 else v
+    if op == "aten.permute.default":
+        return V.permute(v, a.get("dims"))
+    if op == "aten.expand.default":
+        return V.expand(v, out.shape)
+    if op == "aten.slice.Tensor":
+        return V.slice_(v, int(a.get("dim", 0)), a.get("start", 0), a.get("end", V.INT64_MAX), int(a.get("step", 1)))
+    if op == "aten.select.int":
+        return V.select(v, int(a.get("dim", 0)), int(a.get("index", 0)))
+    if op in ("aten.alias.default", "aten.detach.default", "aten.detach_.default", "aten.dropout.default"):
+        return v
+    if op == "aten.contiguous.default":
+        return v if v.is_contiguous() else None
+    return V.restride(v, out.shape)   # reshape / view / flatten / unsqueeze / squeeze
+
+
 @dataclass
 class _Chain:
     ops: list[ChainOp] = field(default_factory=list)
@@ -52,9 +77,13 @@ class _Chain:
 class Lowering:
     """Lowers one IR graph; ``steps``, ``storages`` and ``views`` are the result."""
 
-    def __init__(self, graph: IRGraph, inplace_inputs: bool = True):
+    def __init__(self, graph: IRGraph, inplace_inputs: bool = True, exact_attention: bool = False):
         self.g = graph
         self.inplace_inputs = inplace_inputs
+        self.exact_attention = exact_attention
+        # fold the split-attention combine into the following projection's prologue (1) or
+        # emit it as its own small kernel (0); HIPRT_FOLD_ATTN overrides for measurements
+        self.fold_attn_combine = os.environ.get("HIPRT_FOLD_ATTN", "0") == "1"
         self.steps: list[LaunchStep] = []
         self.storages: dict[str, Storage] = {}
         self.views: dict[str, TView] = {}
@@ -70,6 +99,7 @@ class Lowering:
         self.claimed: dict[str, object] = {}     # node name -> pattern emitter (at its last node) or None
         self.lazy: dict[str, object] = {}        # tensor name -> emitter run when the value is first needed
         self.rms_info: dict[str, dict] = {}      # RMSNorm output -> {x, w, eps, n_dtype} (foldable prologue)
+        self.attn_info: dict[str, dict] = {}     # split decode attention output -> partials (foldable prologue)
         self.graph_output_names = {o.name for o in graph.graph_outputs}
         self.mutated_inputs: set[str] = set()
         self._uid = 0
@@ -231,25 +261,7 @@ class Lowering:
             self.views[out.name] = self.view(src.name)
             return
         v = self.view(node.inputs[0].name)
-        a = node.attrs
-        if op in ("aten.transpose.int",):
-            nv = V.transpose(v, int(a.get("dim0", 0)), int(a.get("dim1", 1)))
-        elif op == "aten.t.default":
-            nv = V.transpose(v, 0, 1) if len(v.shape) == 2 else v
-        elif op == "aten.permute.default":
-            nv = V.permute(v, a.get("dims"))
-        elif op == "aten.expand.default":
-            nv = V.expand(v, out.shape)
-        elif op == "aten.slice.Tensor":
-            nv = V.slice_(v, int(a.get("dim", 0)), a.get("start", 0), a.get("end", V.INT64_MAX), int(a.get("step", 1)))
-        elif op == "aten.select.int":
-            nv = V.select(v, int(a.get("dim", 0)), int(a.get("index", 0)))
-        elif op in ("aten.alias.default", "aten.detach.default", "aten.detach_.default", "aten.dropout.default"):
-            nv = v
-        elif op == "aten.contiguous.default":
-            nv = v if v.is_contiguous() else None
-        else:  # reshape / view / flatten / unsqueeze / squeeze
-            nv = V.restride(v, out.shape)
+        nv = apply_alias(node, v)
         if nv is None:
             nv = V.restride(self.contiguous(node.inputs[0].name, v), out.shape)
         if tuple(nv.shape) != tuple(out.shape):
@@ -280,6 +292,36 @@ class Lowering:
             return None
         return info
 
+    def foldable_attn(self, x_name: str, fused_nodes: set[str]) -> dict | None:
+        """Split-attention partials when ``x_name`` is a pure, order-preserving view of a decode
+        attention output that nothing else reads and that has not been combined yet."""
+        if any(n.name not in fused_nodes for n in self.consumers.get(x_name, [])):
+            return None
+        chain: list[OpNode] = []
+        name = x_name
+        while name not in self.attn_info:
+            prod = self.producer.get(name)
+            if (prod is None or classify_op(prod.op_type) != OpCategory.SHAPE_ALIAS
+                    or prod.op_type in ("<built-in function getitem>", "aten.expand.default", "aten.slice.Tensor",
+                                        "aten.select.int")):
+                return None
+            if len(self.consumers.get(prod.inputs[0].name, [])) != 1 or prod.inputs[0].name in self.graph_output_names:
+                return None
+            chain.append(prod)
+            name = prod.inputs[0].name
+        info = self.attn_info[name]
+        if name not in self.lazy or name in self.graph_output_names:
+            return None
+        shape = tuple(info["shape"])
+        v = TView("virtual", 0, shape, contiguous_strides(shape), "bfloat16")
+        for node in reversed(chain):
+            v = apply_alias(node, v)
+            if v is None:
+                return None
+        if not (v.is_contiguous() and v.offset == 0):
+            return None
+        return info
+
     def gemv_ok(self, x_name: str, w_name: str, out_dtype: str, x_dtype: str = "bfloat16") -> bool:
         """Shapes the streaming GEMV kernels take: bf16, K % 8 == 0, contiguous 16-byte aligned weights."""
         w = self.views.get(w_name)
@@ -300,6 +342,7 @@ class Lowering:
                   argmax_out=None) -> None:
         """One fused GEMV launch (csrc/kernels/gemv.hip); folds a pending RMSNorm of ``x`` when possible."""
         norm = self.foldable_norm(x_name, set(nodes))
+        attn = None
         w = self.contiguous(w_name)
         K = w.shape[1]
         N = w.shape[0]
@@ -307,9 +350,16 @@ class Lowering:
             x = self.contiguous(norm["x"])
             M = x.numel // K
             mb = 1 if M == 1 else 4
-            if mb * K > 12288:
+            if K > 3072:   # the normalised rows are staged in LDS: MB x 3072 bf16
                 norm = None
-        if norm is None:
+        if norm is None and self.fold_attn_combine:
+            attn = self.foldable_attn(x_name, set(nodes))
+            if attn is not None and (K != attn["H"] * 128 or attn["H"] > 16 or attn["nsplit"] > 128
+                                     or epi not in ("bias", "resid")):
+                attn = None
+        if attn is not None:
+            x, M = None, 1
+        elif norm is None:
             x = self.contiguous(x_name)
             M = x.numel // K
             if (x.offset * 2) % 16:
@@ -325,42 +375,57 @@ class Lowering:
             rpw = 1 if M == 1 else 2
         if mb == 4 and epi == "argmax":
             raise NotImplementedError("argmax epilogue with M > 1")
-        kname = {("bias", 1, False): "k_gemv_bias_r1", ("bias", 1, True): "k_gemv_norm_bias_r1",
-                 ("resid", 1, False): "k_gemv_resid_r1", ("silu", 1, False): "k_gemv_silu_r1",
-                 ("silu", 1, True): "k_gemv_norm_silu_r1", ("argmax", 1, True): "k_gemv_norm_argmax_r4",
-                 ("argmax", 1, False): "k_gemv_argmax_r4", ("bias", 4, False): "k_gemv_bias_m4",
-                 ("bias", 4, True): "k_gemv_norm_bias_m4", ("resid", 4, False): "k_gemv_resid_m4",
-                 ("silu", 4, False): "k_gemv_silu_m4", ("silu", 4, True): "k_gemv_norm_silu_m4"}.get(
-            (epi, mb, norm is not None))
+        pro = "attn" if attn is not None else ("norm" if norm is not None else "")
+        kname = {("bias", 1, ""): "k_gemv_bias_r1", ("bias", 1, "norm"): "k_gemv_norm_bias_r1",
+                 ("resid", 1, ""): "k_gemv_resid_r1", ("silu", 1, ""): "k_gemv_silu_r1",
+                 ("silu", 1, "norm"): "k_gemv_norm_silu_r1", ("argmax", 1, "norm"): "k_gemv_norm_argmax_r4",
+                 ("argmax", 1, ""): "k_gemv_argmax_r4", ("bias", 4, ""): "k_gemv_bias_m4",
+                 ("bias", 4, "norm"): "k_gemv_norm_bias_m4", ("resid", 4, ""): "k_gemv_resid_m4",
+                 ("silu", 4, ""): "k_gemv_silu_m4", ("silu", 4, "norm"): "k_gemv_norm_silu_m4",
+                 ("bias", 1, "attn"): "k_gemv_attn_bias_r4", ("resid", 1, "attn"): "k_gemv_attn_resid_r4"}.get(
+            (epi, mb, pro))
         if kname is None:
-            raise NotImplementedError(f"no GEMV kernel for epilogue {epi} M={M} norm={norm is not None}")
-        if epi == "bias" and M == 1 and N >= 65536:
+            raise NotImplementedError(f"no GEMV kernel for epilogue {epi} M={M} prologue={pro!r}")
+        rows_per_wg = None
+        if attn is not None:
+            rpw = 4
+        if epi == "bias" and M == 1 and N >= 65536 and pro == "":
             kname, rpw = "k_gemv_bias_r4", 4
+        elif epi in ("bias", "resid") and M == 1 and pro == "" and K >= 4096:
+            # long rows: the four waves of a workgroup split K, two rows per workgroup
+            kname, rpw, rows_per_wg = f"k_gemv_{epi}_ks_r2", 2, 2
         o = self.new_storage(out_name, out_shape, "bfloat16")
         bias = self.contiguous(b_name) if b_name else None
         r = self.contiguous(resid) if resid else None
         wv2 = self.contiguous(w2) if w2 else None
         bv2 = self.contiguous(b2) if b2 else None
-        nblocks = (N + 4 * rpw - 1) // (4 * rpw)
+        rows_per_wg = rows_per_wg or 4 * rpw
+        nblocks = (N + rows_per_wg - 1) // rows_per_wg
         # kernels with a prologue (RMSNorm) or a per-workgroup reduction (argmax) stride over row
-        # blocks with a capped grid, so the prologue is paid once per workgroup
+        # blocks with a capped grid, so the prologue is paid once per workgroup (measured: the
+        # norm+gate/up GEMV takes 13.6 us strided vs 17.1 us with one workgroup per block); the
+        # others get one workgroup per row block so that all weight loads are in flight at once
         gx = min(nblocks, 1024) if (norm is not None or epi == "argmax") else nblocks
         slot = self.scratch(out_name + ".argmax", 8 * max(M, 1) * gx) if epi == "argmax" else None
-        args = dict(x=self.ref(x), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
-                    resid=self.ref(r) if r else None, w2=self.ref(wv2) if wv2 else None,
+        args = dict(x=self.ref(x) if x is not None else None, w=self.ref(w), bias=self.ref(bias) if bias else None,
+                    out=self.ref(o), resid=self.ref(r) if r else None, w2=self.ref(wv2) if wv2 else None,
                     bias2=self.ref(bv2) if bv2 else None,
                     norm_w=self.ref(self.contiguous(norm["w"])) if norm else None, argmax_slot=slot,
+                    attn_o=attn["part_o"] if attn else None, attn_ml=attn["part_ml"] if attn else None,
                     M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=float(norm["eps"]) if norm else 0.0,
                     n_dtype=DTYPE_CODE[norm["n_dtype"]] if norm else 0,
-                    flags=(1 if bias else 0) | (4 if bv2 else 0))
-        ins = [norm["x"] if norm else x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t]
+                    flags=(1 if bias else 0) | (4 if bv2 else 0),
+                    attn_heads=attn["H"] if attn else 0, attn_kvh=attn["KVH"] if attn else 0,
+                    attn_splits=attn["nsplit"] if attn else 0)
+        ins = [norm["x"] if norm else (attn["out"] + ".partials" if attn else x_name), w_name] + \
+            [t for t in (b_name, resid, w2, b2) if t]
         if norm:
             ins.append(norm["w"])
         self.emit(LaunchStep(
             kind="gemv", kernel=kname, module="gemv", arg_struct="GemvArgs", args=args,
             grid=(gx, (M + mb - 1) // mb, 1), inputs=ins, outputs=[out_name],
-            params={"M": M, "N": N, "K": K, "epilogue": epi, "norm": norm is not None, "has_bias": bias is not None,
-                    "weights": 2 if w2 else 1, "transpose_b": True, "nodes": nodes}))
+            params={"M": M, "N": N, "K": K, "epilogue": epi, "norm": norm is not None, "prologue": pro,
+                    "has_bias": bias is not None, "weights": 2 if w2 else 1, "transpose_b": True, "nodes": nodes}))
         self.views[out_name] = o
         if epi == "argmax":
             name, shape, dtype = argmax_out
@@ -761,10 +826,11 @@ class Lowering:
         fn(node)
 
 
-def analyze_subgraph(graph: IRGraph, inplace_inputs: bool = True, fuse: bool = True) -> Lowering:
+def analyze_subgraph(graph: IRGraph, inplace_inputs: bool = True, fuse: bool = True,
+                     exact_attention: bool = False) -> Lowering:
     from hip_compiler.patterns import DEFAULT_PATTERNS
 
-    low = Lowering(graph, inplace_inputs=inplace_inputs)
+    low = Lowering(graph, inplace_inputs=inplace_inputs, exact_attention=exact_attention)
     low.run(DEFAULT_PATTERNS if fuse else [])
     return low
 

@@ -56,8 +56,14 @@ _struct("LinearArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P)
                        ("has_resid", I), ("pad", I)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])
 _struct("GemvArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P), ("w2", P), ("bias2", P),
-                     ("norm_w", P), ("argmax_slot", P), ("M", LL), ("ldx", LL), ("ldo", LL), ("ldr", LL),
-                     ("N", I), ("K", I), ("eps", F), ("n_dtype", I), ("flags", I), ("pad", I)])
+                     ("norm_w", P), ("argmax_slot", P), ("attn_o", P), ("attn_ml", P), ("M", LL), ("ldx", LL),
+                     ("ldo", LL), ("ldr", LL), ("N", I), ("K", I), ("eps", F), ("n_dtype", I), ("flags", I),
+                     ("attn_heads", I), ("attn_kvh", I), ("attn_splits", I)])
+_struct("FlashArgs", [("q", P), ("k", P), ("v", P), ("mask", P), ("part_o", P), ("part_ml", P), ("S", LL),
+                      ("q_head_stride", LL), ("kv_head_stride", LL), ("mask_stride", LL), ("H", I), ("KVH", I),
+                      ("nsplit", I), ("spl", I), ("scale", F), ("mask_dtype", I), ("add_dtype", I), ("dtype", I)])
+_struct("CombineArgs", [("part_o", P), ("part_ml", P), ("out", P), ("H", I), ("KVH", I), ("nsplit", I),
+                        ("dtype", I)])
 _struct("ArgmaxFinalizeArgs", [("slot", P), ("out", P), ("rows", LL), ("parts", I), ("out_dtype", I)])
 _struct("QKVArgs", [("x", P), ("norm_w", P), ("wq", P), ("bq", P), ("wk", P), ("bk", P), ("wv", P), ("bv", P),
                     ("inv_freq", P), ("pos_ids", P), ("cache_pos", P), ("q_out", P), ("k_dst", P), ("v_dst", P),

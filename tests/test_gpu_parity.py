@@ -32,13 +32,14 @@ def close(got, ref, rtol=RTOL):
     return err / scale
 
 
-def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True):
+def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True, exact=False):
     from hip_compiler import compile_subgraph, is_hip_op_supported
     from npu_compiler import partition
     from npu_runtime import DAGExecutor
 
     fn = supported or (lambda op, a=None: is_hip_op_supported(op, a) and op not in force_cpu)
-    ex = DAGExecutor(partition(ir, fn), backend, compile_fn=lambda sub: compile_subgraph(sub, fuse=fuse))
+    ex = DAGExecutor(partition(ir, fn), backend,
+                     compile_fn=lambda sub: compile_subgraph(sub, fuse=fuse, exact_attention=exact))
     ex.load_weights(weights)
     out = ex.execute(inputs)
     return {k: (v if isinstance(v, np.ndarray) else v.to_numpy()) for k, v in out.items()}, ex
@@ -83,7 +84,8 @@ def test_mlp_block_cfg1(backend, tokens):
         close(got[name], run_ir(ir, x, w)[name])
 
 
-def test_attention_block_cfg2(backend):
+@pytest.mark.parametrize("exact", [False, True])
+def test_attention_block_cfg2(backend, exact):
     from irgen.qwen import build_attention_ir
     from irgen.workloads import attention_inputs, make_weights
     from oracle.numpy_ref import run_ir
@@ -91,7 +93,7 @@ def test_attention_block_cfg2(backend):
     ir = build_attention_ir(1025)
     w = host(make_weights(ir))
     x = host(attention_inputs(1025))
-    got, ex = run_hip(ir, x, w, backend)
+    got, ex = run_hip(ir, x, w, backend, exact=exact)
     assert_all_npu(ex)
     ref = run_cpu(ir, x, w)
     orc = run_ir(ir, x, w)
@@ -106,8 +108,9 @@ def test_attention_block_cfg2(backend):
             assert np.array_equal(got[k][:, :, keep], src[:, :, keep])
 
 
+@pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("valid", [1, 10, 64, 65, 1000])
-def test_decode_attention_kernel_vs_closed_form(backend, valid):
+def test_decode_attention_kernel_vs_closed_form(backend, valid, exact):
     """The fused split-KV kernel against the closed form of tests/test_extended_kernels.py:621-640."""
     from irgen.qwen import QwenConfig, build_attention_ir
     from irgen.workloads import attention_inputs, decode_mask, make_weights
@@ -122,7 +125,7 @@ def test_decode_attention_kernel_vs_closed_form(backend, valid):
     x["position_ids"][:] = valid - 1
     x["cache_position"][:] = valid - 1
     x = host(x)
-    got, _ = run_hip(ir, x, w, backend)
+    got, _ = run_hip(ir, x, w, backend, exact=exact)
     orc = run_ir(ir, x, w)
     for k in got:
         if not k.startswith("index_copy"):
