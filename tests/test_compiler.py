@@ -1,0 +1,150 @@
+"""Structure of compiled HIP programs (no GPU): step lists, fusion decisions, views, arena,
+codegen and the op support table. Counterpart of the reference's CPU-only compiler tests
+(tests/test_cuda_compiler.py:53-530)."""
+
+import numpy as np
+import pytest
+
+from hip_compiler import compile_subgraph, get_hip_supported_ops, is_hip_op_supported
+from hip_compiler import views as V
+from hip_compiler.program import ELEM_SIZE, Ref, TView, contiguous_strides
+from irgen.qwen import QwenConfig, build_attention_ir, build_decode_ir, build_mlp_ir
+from npu_compiler import partition
+
+
+def kernels(p):
+    return [s.kernel for s in p.steps]
+
+
+def test_mlp_block_fused_and_generic_step_lists():
+    fused = compile_subgraph(build_mlp_ir(1))
+    assert kernels(fused) == ["k_gemv_norm_silu_r1", "k_gemv_resid_ks_r2"]
+    gen = compile_subgraph(build_mlp_ir(16), fuse=False)
+    kinds = [s.kind for s in gen.steps]
+    # the reference's expected list: [RMSNorm, gemm gate, gemm up, fused(silu, mul), gemm down, fused(add)]
+    assert kinds.count("gemv") == 3 and kinds.count("fused") >= 2
+    assert "rmsnorm" not in kinds  # generic lowering: the norm becomes a chain + mean reduction
+    chains = [s.params["ops"] for s in gen.steps if s.kind == "fused"]
+    assert ["aten.silu.default", "aten.mul.Tensor"] in chains
+    assert ["aten.add.Tensor"] in chains
+
+
+def test_rmsnorm_pattern_alone_is_one_kernel():
+    p = compile_subgraph(build_mlp_ir(128))
+    assert [s.params.get("norm") for s in p.steps if s.kind == "gemv"][0] is True
+    eps = [s.args["eps"] for s in p.steps if s.kind == "gemv"][0]
+    assert abs(eps - 1e-6) < 1e-12
+
+
+def test_attention_block_is_four_launches_with_inplace_cache():
+    p = compile_subgraph(build_attention_ir(1025))
+    assert kernels(p) == ["k_qkv_rope", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
+    assert set(p.stats["mutated_inputs"]) == {"past_key_0", "past_value_0"}
+    assert p.output_views["index_copy"].storage == "past_key_0"
+    exact = compile_subgraph(build_attention_ir(1025), exact_attention=True)
+    assert kernels(exact) == ["k_qkv_rope", "k_attn_scores", "k_attn_out", "k_gemv_bias_r1"]
+    gen = compile_subgraph(build_attention_ir(1025), fuse=False)
+    assert "k_index_copy" in kernels(gen) and "k_bmm" in kernels(gen)
+
+
+def test_decode_step_launch_count_and_cache_aliasing():
+    cfg = QwenConfig(layers=3)
+    p = compile_subgraph(build_decode_ir(256, cfg, argmax=True))
+    assert len(p.steps) == 1 + 6 * cfg.layers + 2      # embedding, 6 per layer, lm_head+argmax, finalize
+    assert kernels(p)[0] == "k_embedding" and kernels(p)[-2:] == ["k_gemv_norm_argmax_r4", "k_argmax_finalize"]
+    assert len(p.stats["mutated_inputs"]) == 2 * cfg.layers
+    assert not any(s.kernel in ("k_rope_table", "k_rmsnorm", "k_copy") for s in p.steps)
+
+
+def test_not_inplace_when_cache_input_has_another_reader():
+    ir = build_attention_ir(64)
+    # make the K cache also a graph output read directly: in-place update is no longer allowed
+    ir["graph_outputs"].append({"name": "past_key_0", "shape": [1, 2, 64, 128], "dtype": "bfloat16"})
+    p = compile_subgraph(ir)
+    assert "past_key_0" not in p.stats["mutated_inputs"]
+
+
+def test_every_decode_op_is_supported_and_partitions_to_one_device_partition():
+    ir = build_decode_ir(128, QwenConfig(layers=2), argmax=True)
+    assert all(is_hip_op_supported(n["op_type"], n.get("attrs")) for n in ir["nodes"])
+    plan = partition(ir, is_hip_op_supported)
+    assert len(plan.steps) == 1 and plan.steps[0].target == "npu"
+    assert not is_hip_op_supported("aten.conv2d.default")
+    assert not is_hip_op_supported("aten.dropout.default", {"p": 0.1, "train": True})
+    assert "aten.index_copy.default" in get_hip_supported_ops()
+
+
+def _intervals(p):
+    out = []
+    for s in p.storages.values():
+        if s.kind in ("arena", "persistent") and s.first >= 0:
+            size = (s.nbytes + 255) // 256 * 256
+            out.append((s.first, s.last, s.offset, s.offset + size, s.kind))
+    return out
+
+
+@pytest.mark.parametrize("build", [lambda: build_decode_ir(256, QwenConfig(layers=2), argmax=True),
+                                   lambda: build_mlp_ir(16), lambda: build_attention_ir(300)])
+@pytest.mark.parametrize("fuse", [True, False])
+def test_arena_live_ranges_never_share_bytes(build, fuse):
+    p = compile_subgraph(build(), fuse=fuse)
+    iv = _intervals(p)
+    for i, a in enumerate(iv):
+        assert a[3] <= p.arena_bytes
+        for b in iv[i + 1:]:
+            live_overlap = not (a[1] < b[0] or b[1] < a[0]) or "persistent" in (a[4], b[4])
+            if live_overlap:
+                assert a[3] <= b[2] or b[3] <= a[2]
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_steps_read_only_already_written_arena_storage(fuse):
+    p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True), fuse=fuse)
+    out_fields = {"dst", "out", "c", "cos_out", "sin_out", "q_out", "k_dst", "v_dst", "part_o", "part_ml",
+                  "scores", "stats", "argmax_slot"}
+    written = set()
+    for s in p.steps:
+        outs = {v.storage for k, v in s.args.items() if k in out_fields and isinstance(v, Ref)}
+        for k, v in s.args.items():
+            refs = [v] if isinstance(v, Ref) else [x for x in v if isinstance(x, Ref)] if isinstance(v, (list, tuple)) \
+                else []
+            for r in refs:
+                if k in out_fields or p.storages[r.storage].kind != "arena":
+                    continue
+                assert r.storage in written or r.storage in outs, (s.kernel, k, r)
+        written |= outs
+
+
+def test_view_arithmetic():
+    v = TView("s", 0, (1, 12, 1, 128), contiguous_strides((1, 12, 1, 128)), "bfloat16")
+    t = V.transpose(v, 1, 2)
+    assert t.shape == (1, 1, 12, 128)
+    r = V.restride(t, (1, 1, 1536))
+    assert r is not None and r.is_contiguous()
+    m = TView("m", 0, (4, 6), contiguous_strides((4, 6)), "float32")
+    assert V.restride(V.transpose(m, 0, 1), (24,)) is None        # needs a copy
+    e = V.expand(TView("c", 0, (1, 1, 1, 128), (128, 128, 128, 1), "bfloat16"), (1, 12, 1, 128))
+    assert e.strides[1] == 0
+    s = V.slice_(m, 1, 2, 5)
+    assert s.offset == 2 and s.shape == (4, 3) and s.strides == (6, 1)
+    assert V.slice_(m, 1, 3, 9223372036854775807).shape == (4, 3)
+
+
+def test_generated_chain_reads_broadcast_operands_with_zero_stride():
+    from hip_compiler.codegen import ChainOp, generate_chain
+
+    out = (1, 12, 1, 128)
+    x = TView("x", 0, out, contiguous_strides(out), "bfloat16")
+    c = V.broadcast_to(TView("c", 0, (1, 1, 1, 128), contiguous_strides((1, 1, 1, 128)), "bfloat16"), out)
+    name, src = generate_chain([ChainOp("aten.mul.Tensor", [("ext", 0), ("ext", 1)], "bfloat16")], [x, c], out,
+                               "bfloat16")
+    assert "c1 * 128LL" in src                     # x walks heads
+    assert "ld_f(a.in[1], c3 * 1LL, 2)" in src       # cos broadcast over heads: only the dim term
+    assert name.startswith("fused_ew_")
+
+
+def test_output_views_are_whole_contiguous_storages():
+    p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True))
+    for name, v in p.output_views.items():
+        st = p.storages[v.storage]
+        assert v.offset == 0 and v.is_contiguous() and v.numel * ELEM_SIZE[v.dtype] == st.nbytes

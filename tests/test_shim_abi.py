@@ -1,0 +1,65 @@
+"""The C-ABI library: it loads, exports every entry point include/hipshim.h declares, agrees
+with the host's ctypes mirrors on every kernel-argument struct, and reports errors instead
+of aborting. No kernel is launched here."""
+
+import ctypes as C
+import os
+import re
+
+import pytest
+import torch
+
+from hip_runtime import _shim
+from hip_runtime.kernels import STRUCTS, check_layouts
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "hipshim.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(hs_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_entry_point():
+    lib = _shim.lib()
+    names = declared_symbols()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_shim.EXPORTED)
+
+
+def test_kernel_argument_layouts_match():
+    assert check_layouts() == {}
+    assert _shim.lib().hs_argsize(b"NoSuchStruct") == 0
+    assert C.sizeof(STRUCTS["GemvArgs"]) % 8 == 0
+
+
+def test_init_reports_errors_without_aborting():
+    lib = _shim.lib()
+    rc = lib.hs_init(12345)
+    assert rc != 0
+    assert b"out of range" in lib.hs_last_error() or lib.hs_last_error()
+    if not torch.cuda.is_available():
+        assert lib.hs_init(0) != 0
+
+
+def test_runtime_compile_of_a_generated_kernel_without_a_device():
+    from hip_compiler import compile_subgraph
+    from irgen.qwen import build_mlp_ir
+
+    p = compile_subgraph(build_mlp_ir(4), fuse=False)
+    ks = p.kernel_sources[0]
+    image = _shim.rtc_compile(ks.source_code, ks.kernel_name)
+    assert image[:4] == b"\x7fELF" or image[:24].startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    with pytest.raises(_shim.HIPShimError):
+        _shim.rtc_compile("this is not C++", "broken")
+
+
+def test_backend_fails_loudly_without_a_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    from hip_runtime import HIPBackend
+
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        HIPBackend().allocate_zeros((2, 2))
