@@ -1,19 +1,21 @@
-"""Benchmark: Qwen2.5-1.5B-architecture bf16 decode on one MI355X (BASELINE cfg3).
+"""Benchmark: Qwen2.5-1.5B-architecture bf16 decode on one MI355X (the headline workload).
 
 A step is one decode step of the full 28-layer model (random-init bf16 weights
 N(0, 0.02), tied embeddings) at batch 1 over static KV caches of length 2048,
 run through ``DAGExecutor`` + the HIP backend, with the greedy next token computed
 on the device and fed back as the next step's ``input_ids`` (no host sync inside
-the timed region). Timed steps walk cache positions 1984..1984+K-1 (the
-BASELINE's 64-step window for K=64); warmup steps run over the same positions
-first, so the timed steps see exactly the caches a cold run would.
+the timed region). Timed steps walk cache positions 1984..1984+K-1 (a 64-step
+window ending at the cache length for K=64); every run (warmup, timed, parity)
+starts from the same first token at position 1984, and each step writes its
+cache row before reading it, so every run sees the caches a cold run would.
 
 Printed JSON line: tok/s (whole job), ms/step, a ``roofline`` object for the
-dominant kernel (the streaming linear kernel: algorithmic bytes per launch over
-its average launch time, measured here with HIP events on the launch stream),
-the step-level fraction of HBM peak, and a ``cpu_baseline`` measured on this
-host's cores with the CPU fallback (DAGExecutor over an all-CPU plan, ATen bf16)
-on a bounded sample of the same workload.
+dominant kernel (algorithmic bytes per launch over its average launch time,
+measured with HIP events on the launch stream), the step-level fraction of HBM
+peak, the rate with host-side per-step inputs, and a ``cpu_baseline`` measured on
+this host's cores with the CPU fallback (DAGExecutor over an all-CPU plan, ATen
+bf16) over the same 64-step greedy loop, with a teacher-forced top-1 comparison
+of the two paths.
 """
 
 from __future__ import annotations
@@ -32,7 +34,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "Qwen2.5-1.5B-arch bf16 decode tok/s @ctx2048; achieved HBM GB/s vs peak"
-PUBLISHED_TOKS = 30.0   # reference CUDA path, RTX 3090 Ti, position 2048 (docs/benchmarks.md:98)
+PUBLISHED_TOKS = 30.0   # reference CUDA path, RTX 3090 Ti, cache position 2048 (docs/benchmarks.md:98)
 
 
 def log(*a):
@@ -82,8 +84,50 @@ def time_kernel_subset(ex, indices, repeats, stream) -> float:
     return ms.value / (repeats * len(indices))
 
 
-def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int) -> dict:
-    """CPU fallback (all-CPU plan through DAGExecutor, ATen bf16) on ``steps`` decode steps."""
+def time_in_step(ex, indices, replays, stream) -> float:
+    """Average ms of the launches ``indices`` inside full replays of the step's launch list:
+    every launch of the step runs in order, and HIP events on ``stream`` bracket each selected
+    launch, so the kernel is timed with the caches and neighbours it has in a real step."""
+    from hip_runtime import _shim
+
+    lib = _shim.lib()
+    recs = ex._recs
+    sel = set(indices)
+    n = len(recs)
+    evs = [C.c_void_p() for _ in range(2 * len(indices))]
+    for e in evs:
+        _shim.check(lib.hs_event_create(C.byref(e)))
+    total = 0.0
+    for _ in range(replays):
+        j, k = 0, 0
+        while j < n:
+            if j in sel:
+                _shim.check(lib.hs_event_record(evs[2 * k], stream))
+                one = (_shim.LaunchRec * 1)(recs[j])
+                _shim.check(lib.hs_replay(one, 1, stream))
+                _shim.check(lib.hs_event_record(evs[2 * k + 1], stream))
+                j, k = j + 1, k + 1
+                continue
+            e = j
+            while e < n and e not in sel:
+                e += 1
+            chunk = (_shim.LaunchRec * (e - j))(*recs[j:e])
+            _shim.check(lib.hs_replay(chunk, e - j, stream))
+            j = e
+        _shim.check(lib.hs_event_sync(evs[-1]))
+        ms = C.c_float()
+        for k in range(len(indices)):
+            _shim.check(lib.hs_event_elapsed_ms(evs[2 * k], evs[2 * k + 1], C.byref(ms)))
+            total += ms.value
+    for e in evs:
+        lib.hs_event_destroy(e)
+    return total / (replays * len(indices))
+
+
+def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int, warmup: int = 3):
+    """CPU fallback (all-CPU plan through DAGExecutor, ATen bf16): ``warmup`` untimed steps, then
+    ``steps`` timed greedy decode steps from the same starting state. Returns the baseline record,
+    the greedy tokens and the logits (float32) of the timed steps."""
     import numpy as np
     import torch
 
@@ -94,28 +138,103 @@ def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int) -> dict:
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
     w = {k: v.detach().cpu() for k, v in weights_dev.items()}
-    x = {k: v.detach().cpu() for k, v in inputs_dev.items()}
+    x = {k: to_host(v.detach().cpu()) for k, v in inputs_dev.items()}
     ex = DAGExecutor(partition(ir, lambda *_: False), None)
     ex.load_weights(w)
-    ins = {k: to_host(v) for k, v in x.items()}
-    times = []
-    start = int(ins["cache_position"][0])
-    for s in range(steps + 1):
-        pos = start + s
-        ins["attention_mask"] = to_host(decode_mask(ins["attention_mask"].shape[-1], pos))
-        ins["position_ids"] = np.array([[pos]], np.int64)
-        ins["cache_position"] = np.array([pos], np.int64)
-        t0 = time.perf_counter()
-        out = ex.execute(ins)
-        times.append(time.perf_counter() - t0)
-        ins["input_ids"] = out["next_token"]
-        for i, o in zip([g["name"] for g in ir["graph_inputs"][4:]], [o["name"] for o in ir["graph_outputs"][1:-1]]):
-            ins[i] = out[o]
-    med = statistics.median(times[1:])
-    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": n, "kind": "port",
-            "sample": f"{steps} decode steps (after 1 warmup) of the full 28-layer model at positions "
-                      f"{start}..{start + steps}, DAGExecutor all-CPU plan (ATen bf16), median step "
-                      f"{med * 1e3:.1f} ms"}
+    kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
+    kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
+    start = int(x["cache_position"][0])
+    S = x["attention_mask"].shape[-1]
+
+    lname = ir["graph_outputs"][0]["name"]
+
+    def loop(n_steps, times=None, tokens=None, logits=None):
+        # every step writes its cache row before reading it, so re-running positions from the same
+        # first token reproduces a cold run exactly
+        ins = dict(x)
+        for s in range(n_steps):
+            pos = start + s
+            ins["attention_mask"] = to_host(decode_mask(S, pos))
+            ins["position_ids"] = np.array([[pos]], np.int64)
+            ins["cache_position"] = np.array([pos], np.int64)
+            t0 = time.perf_counter()
+            out = ex.execute(ins)
+            if times is not None:
+                times.append(time.perf_counter() - t0)
+            ins["input_ids"] = out["next_token"]
+            if tokens is not None:
+                tokens.append(int(np.asarray(out["next_token"]).reshape(-1)[0]))
+                logits.append(torch.from_numpy(np.asarray(out[lname]).view(np.int16)).view(torch.bfloat16)
+                              .float().reshape(-1).numpy())
+            for i, o in zip(kv_in, kv_out):
+                ins[i] = out[o]
+
+    loop(warmup)
+    times, tokens, logits = [], [], []
+    loop(steps, times, tokens, logits)
+    med = statistics.median(times)
+    total = sum(times)
+    rec = {"value": round(steps / total, 4), "unit": "tok/s", "cores": n, "kind": "port",
+           "sample": f"the same greedy loop: {steps} decode steps of the full 28-layer model at positions "
+                     f"{start}..{start + steps - 1} after {warmup} untimed warmup steps, DAGExecutor with an "
+                     f"all-CPU plan (ATen bf16, {n} threads); {total:.1f} s total, median step "
+                     f"{med * 1e3:.1f} ms"}
+    return rec, tokens, logits
+
+
+def run_copy_probe(device_index: int, stream, mib: int = 512, repeats: int = 3) -> float:
+    """Launch the library's plain copy kernel (``k_copy``) over ``mib`` MiB of bf16, ``repeats`` times.
+
+    Its known traffic (``mib`` MiB read, ``mib`` MiB written per launch) calibrates the
+    FETCH_SIZE / WRITE_SIZE counters that give the ``traffic`` figure. Returns the average
+    launch time in ms."""
+    import torch
+
+    from hip_runtime import _shim
+    from hip_runtime.hip_executor import module_cache
+    from hip_runtime.kernels import STRUCTS
+
+    n = mib * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device=f"cuda:{device_index}")
+    dst = torch.empty_like(src)
+    a = STRUCTS["CopyArgs"]()
+    a.dst, a.src, a.n, a.ndim = dst.data_ptr(), src.data_ptr(), n, 1
+    a.shape[0], a.sstride[0], a.dstride[0] = n, 1, 1
+    a.sdtype = a.ddtype = 2
+    mods = module_cache(device_index)
+    mods.ensure_builtin("basic")
+    fn = mods.function("basic", "k_copy")
+    lib = _shim.lib()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    _shim.check(lib.hs_event_create(C.byref(e0)))
+    _shim.check(lib.hs_event_create(C.byref(e1)))
+    _shim.check(lib.hs_event_record(e0, stream))
+    for _ in range(repeats):
+        _shim.check(lib.hs_launch(fn, 4096, 1, 1, 256, 1, 1, 0, stream, C.byref(a), C.sizeof(a)), "k_copy")
+    _shim.check(lib.hs_event_record(e1, stream))
+    _shim.check(lib.hs_event_sync(e1))
+    ms = C.c_float()
+    _shim.check(lib.hs_event_elapsed_ms(e0, e1, C.byref(ms)))
+    lib.hs_event_destroy(e0)
+    lib.hs_event_destroy(e1)
+    if not torch.equal(dst[:4096], src[:4096]):
+        raise RuntimeError("copy probe produced wrong data")
+    return ms.value / repeats
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_ctx2048_hbm_traffic.md")
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of ``kernel`` from the committed FETCH_SIZE / WRITE_SIZE summary
+    (lines ``traffic_bytes_per_launch <kernel> <bytes>``), or None when it has no entry."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        parts = line.strip().strip("`").split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+            return int(parts[2])
+    return None
 
 
 def main() -> int:
@@ -125,13 +244,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--max-cache-len", type=int, default=2048)
     ap.add_argument("--start-pos", type=int, default=1984)
-    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=64)
+    ap.add_argument("--cpu-warmup", type=int, default=3)
+    ap.add_argument("--kernel-repeats", type=int, default=10,
+                    help="replays per kernel family / per step in the per-kernel timing")
+    ap.add_argument("--copy-probe-mib", type=int, default=512,
+                    help="size of the k_copy calibration launches run after timing (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=28)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 (multi-GPU sharding is "
-                                   "described in DESIGN.md, not implemented)"}))
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (sharding across "
+                                   "GPUs is a design note, not implemented)"}))
         return 2
 
     import torch
@@ -139,7 +263,7 @@ def main() -> int:
     from hip_compiler import compile_subgraph, is_hip_op_supported
     from hip_runtime import HIPBackend
     from irgen.qwen import QwenConfig, build_decode_ir
-    from irgen.workloads import decode_inputs, decode_mask, make_weights
+    from irgen.workloads import decode_inputs, decode_mask, make_weights, to_host
     from npu_compiler import partition
     from npu_runtime import DAGExecutor
 
@@ -164,24 +288,42 @@ def main() -> int:
 
     kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
     kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
-    masks = [decode_mask(S, p).to(dev) for p in range(start, start + max(args.steps, args.warmup))]
+    masks = [decode_mask(S, p).to(dev) for p in range(start, S)]
     pos_ids = [torch.tensor([[p]], dtype=torch.int64, device=dev) for p in range(start, S)]
     cpos = [torch.tensor([p], dtype=torch.int64, device=dev) for p in range(start, S)]
     from hip_runtime import HIPBuffer
 
     state = {k: backend.allocate_buffer(v) for k, v in x0.items()}
+    first_token = state["input_ids"]
     mask_t, pos_t, cpos_t = (state[k].native_handle for k in ("attention_mask", "position_ids", "cache_position"))
 
-    def run(n_steps):
-        st = state
+    host_steps = None
+
+    lname = ir["graph_outputs"][0]["name"]
+
+    def run(n_steps, host=False, feed=None, record=None):
+        # every run starts from the same first token at position `start`; each step writes its
+        # cache row before reading it, so every run repeats the cold run exactly.
+        # feed: per-step host input_ids (teacher forcing); record: list that gets (token, logits)
+        st = dict(state)
+        st["input_ids"] = first_token
         for s in range(n_steps):
-            # per-step inputs are refreshed in place (device copies on the launch stream), so the
-            # executor's pointers stay fixed and its captured graph is relaunched as-is
-            mask_t.copy_(masks[s])
-            pos_t.copy_(pos_ids[s])
-            cpos_t.copy_(cpos[s])
+            if feed is not None and s > 0:
+                st["input_ids"] = feed[s]
+            if host:
+                # host-side per-step inputs (numpy), uploaded by DAGExecutor every step
+                st.update(host_steps[s])
+            else:
+                # per-step inputs are refreshed in place (device copies on the launch stream), so
+                # the executor's pointers stay fixed and its captured graph is relaunched as-is
+                mask_t.copy_(masks[s])
+                pos_t.copy_(pos_ids[s])
+                cpos_t.copy_(cpos[s])
             out = ex.execute(st)
             st["input_ids"] = out["next_token"]
+            if record is not None:
+                record.append((int(out["next_token"].native_handle.reshape(-1)[0].item()),
+                               out[lname].native_handle.float().reshape(-1).cpu().numpy()))
             for i, o in zip(kv_in, kv_out):
                 st[i] = out[o]
         return st
@@ -201,7 +343,18 @@ def main() -> int:
     step_gbs = sbytes / (ms * 1e-3) / 1e9
     log(f"{toks:.1f} tok/s, {ms:.3f} ms/step, step roofline {step_gbs:.0f} GB/s")
 
-    # dominant kernel: the streaming linear kernel (most algorithmic bytes per step)
+    # the same loop with the per-step mask / position inputs handed over as host arrays
+    # (PCIe-inclusive rate; reported beside the headline, never as it)
+    host_steps = [{"attention_mask": to_host(masks[s].cpu()), "position_ids": pos_ids[s].cpu().numpy(),
+                   "cache_position": cpos[s].cpu().numpy()} for s in range(args.steps)]
+    run(min(args.warmup, args.steps), host=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(args.steps, host=True)
+    torch.cuda.synchronize()
+    host_toks = args.steps / (time.perf_counter() - t0)
+    log(f"host-input loop: {host_toks:.1f} tok/s")
+
     stream = torch.cuda.current_stream(dev).cuda_stream
     # per kernel family: average launch time over its launches in one step (HIP events, launch stream)
     fams: dict[str, list[int]] = {}
@@ -209,7 +362,7 @@ def main() -> int:
         fams.setdefault(s.kernel, []).append(i)
     per_kernel = {}
     for kname, idx in sorted(fams.items()):
-        us = time_kernel_subset(hexec, idx, 10, stream) * 1e3
+        us = time_kernel_subset(hexec, idx, args.kernel_repeats, stream) * 1e3
         entry = {"launches_per_step": len(idx), "avg_us": round(us, 3)}
         if program.steps[idx[0]].kind == "gemv":
             b = sum(gemv_launch_bytes(program.steps[i]) for i in idx) / len(idx)
@@ -217,19 +370,51 @@ def main() -> int:
             entry["bytes_per_launch"] = int(b)
         per_kernel[kname] = entry
         log(f"  {kname}: {entry}")
+    # dominant kernel: the linear-layer family with the most time per step
     dom = max((k for k in per_kernel if "GBs" in per_kernel[k]),
               key=lambda k: per_kernel[k]["avg_us"] * per_kernel[k]["launches_per_step"])
-    avg_ms = per_kernel[dom]["avg_us"] * 1e-3
-    achieved = per_kernel[dom]["GBs"]
     lin = fams[dom]
-    lin_bytes = per_kernel[dom]["bytes_per_launch"] * len(lin)
+    avg_ms = per_kernel[dom]["avg_us"] * 1e-3
+    dom_bytes = per_kernel[dom]["bytes_per_launch"]
+    achieved = dom_bytes / (avg_ms * 1e-3) / 1e9
+    # the same launches bracketed one by one by events inside full step replays: this also counts
+    # each launch's dispatch latency, so it is an upper bound on the kernel's duration
+    in_step_ms = time_in_step(hexec, lin, args.kernel_repeats, stream)
+    log(f"dominant {dom}: {avg_ms * 1e3:.2f} us per launch ({achieved:.0f} GB/s); "
+        f"{in_step_ms * 1e3:.2f} us with per-launch events inside the step")
+    traffic = measured_traffic(dom)
+
+    probe = None
+    if args.copy_probe_mib > 0:
+        pm = run_copy_probe(0, stream, args.copy_probe_mib)
+        probe = {"kernel": "k_copy", "mib": args.copy_probe_mib, "avg_ms": round(pm, 4),
+                 "GBs": round(2 * args.copy_probe_mib * (1 << 20) / (pm * 1e-3) / 1e9, 1)}
+        log(f"copy probe: {probe}")
 
     cpu = None
     if not args.no_cpu_baseline:
+        import numpy as np
+
         log("cpu baseline")
         x_cpu = decode_inputs(S, start, cfg, device="cuda")
-        cpu = cpu_baseline(ir, weights, x_cpu, cfg, args.cpu_steps)
+        cpu, cpu_tokens, cpu_logits = cpu_baseline(ir, weights, x_cpu, cfg, args.cpu_steps, args.cpu_warmup)
         log(f"cpu: {cpu['value']} tok/s on {cpu['cores']} cores")
+        # untimed parity pass: the device loop teacher-forced with the CPU's tokens, so every step
+        # compares the two paths on the same context
+        n_check = min(args.cpu_steps, len(masks))
+        feed = [None] + [np.array([[t]], np.int64) for t in cpu_tokens[:n_check - 1]]
+        rec = []
+        run(n_check, feed=feed, record=rec)
+        agree = sum(int(g == c) for (g, _), c in zip(rec, cpu_tokens))
+        rel = max(float(np.abs(gl - cl).max() / np.abs(cl).max()) for (_, gl), cl in zip(rec, cpu_logits))
+        # a disagreement is a near tie when the CPU logits of the two tokens differ by less than the
+        # step's largest GPU-vs-CPU logit difference
+        ties = sum(1 for (g, gl), c, cl in zip(rec, cpu_tokens, cpu_logits)
+                   if g != c and cl[c] - cl[g] <= np.abs(gl - cl).max())
+        cpu["parity"] = {"steps": n_check, "top1_agree": agree, "disagree_near_ties": ties,
+                         "logits_max_rel_err": round(rel, 4),
+                         "mode": "device loop teacher-forced with the CPU greedy tokens"}
+        log(f"parity: {cpu['parity']}")
 
     line = {
         "metric": METRIC, "value": round(toks, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -239,12 +424,15 @@ def main() -> int:
                                f"positions {start}..{start + args.steps - 1}, device-side greedy argmax",
                    "layers": cfg.layers, "hidden": cfg.hidden, "vocab": cfg.vocab, "max_cache_len": S,
                    "launches_per_step": len(program.steps), "compile_s": round(compile_s, 2),
+                   "host_input_tok_s": round(host_toks, 2),
                    "vs_baseline_ref": "reference CUDA path on RTX 3090 Ti, 30.0 tok/s at position 2048"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 3),
-                     "launches_per_step": len(lin), "bytes_per_launch": lin_bytes // len(lin)},
+                     "traffic": traffic, "avg_launch_us": round(avg_ms * 1e3, 3),
+                     "in_step_event_us": round(in_step_ms * 1e3, 3),
+                     "launches_per_step": len(lin), "bytes_per_launch": dom_bytes},
         "kernels": per_kernel,
+        "copy_probe": probe,
         "step_roofline": {"bytes_per_step": sbytes, "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,

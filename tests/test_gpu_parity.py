@@ -322,3 +322,49 @@ def test_full_decode_step_real_dims(backend):
     assert int(got["next_token"].reshape(-1)[0]) == int(np.argmax(f32(ref[logits]).reshape(-1)))
     for o in ir["graph_outputs"][1:-1]:
         close(got[o["name"]], ref[o["name"]])
+
+
+def test_full_model_logits_as_close_to_fp32_as_the_cpu_path(backend):
+    """The full 28-layer cfg3 step: bf16 paths vs the same IR evaluated in float32 (plain ATen fp32).
+
+    Two bf16 implementations that sum in different orders drift apart over 28 layers by about
+    the distance each has from the fp32 result (3-4% of the largest logit with random weights),
+    so the full-depth bar is: the HIP path is as close to the fp32 result as the CPU fallback
+    is (logits and the rows written into the KV caches), the next token matches, and the first
+    layer's cache rows match the CPU path's within 2e-2."""
+    import dataclasses
+
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(layers=28)
+    S, pos = 2048, 1984
+    ir = build_decode_ir(S, cfg, argmax=True)
+    w = host(make_weights(ir, cfg, device="cuda"))
+    x = host(decode_inputs(S, pos, cfg, device="cuda"))
+    got, ex = run_hip(ir, x, w, backend)
+    assert_all_npu(ex)
+    ref = run_cpu(ir, x, w)
+    ir32 = build_decode_ir(S, dataclasses.replace(cfg, dtype="float32"), argmax=True)
+    up = {k: f32(v) if np.asarray(v).dtype == np.uint16 else v for k, v in w.items()}
+    x32 = {k: f32(v) if np.asarray(v).dtype == np.uint16 else v for k, v in x.items()}
+    truth = run_cpu(ir32, x32, up)
+    lg = ir["graph_outputs"][0]["name"]
+    t = np.asarray(truth[lg], np.float32).reshape(-1)
+    err_hip = np.abs(f32(got[lg]).reshape(-1) - t).max() / np.abs(t).max()
+    err_cpu = np.abs(f32(ref[lg]).reshape(-1) - t).max() / np.abs(t).max()
+    print(f"logits vs fp32: hip {err_hip:.4f}, cpu fallback {err_cpu:.4f}")
+    assert err_hip <= 1.25 * err_cpu + 5e-3
+    assert int(got["next_token"].reshape(-1)[0]) == int(np.asarray(ref["next_token"]).reshape(-1)[0])
+    # the rows written into the caches at `pos`: the first layer's (no drift yet) within 2e-2 of the
+    # CPU path; over all layers, no further from the fp32 result than the CPU path's rows are
+    kv = [o["name"] for o in ir["graph_outputs"][1:-1]]
+    for name in kv[:2]:
+        close(f32(got[name])[:, :, pos], f32(ref[name])[:, :, pos])
+    def rms(a):
+        return float(np.sqrt(np.mean(np.square(a))))
+    d_hip = [f32(got[n])[:, :, pos] - np.asarray(truth[n], np.float32)[:, :, pos] for n in kv]
+    d_cpu = [f32(ref[n])[:, :, pos] - np.asarray(truth[n], np.float32)[:, :, pos] for n in kv]
+    r_hip, r_cpu = rms(np.concatenate(d_hip)), rms(np.concatenate(d_cpu))
+    print(f"cache rows vs fp32 (rms): hip {r_hip:.5f}, cpu fallback {r_cpu:.5f}")
+    assert r_hip <= 1.25 * r_cpu + 1e-4
