@@ -135,15 +135,26 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
 
 // ------------------------------------------------------------------ split-S flash decoding
 //
-// k_attn_flash: one workgroup per (split of `spl` positions, KV head). The q rows of
-// the G heads and the split's mask are staged first; then every K and V row of the
-// split is requested at once (8 lanes x 32 B per K row, 16 lanes x 16 B per V row),
-// scores are formed with the model's rounding points (as in k_attn_scores), the
-// split's (max m, sum l) per head computed, and sum_s exp(s - m) v_s accumulated.
-// The partials are combined either by k_attn_combine or inside the next GEMV's
-// prologue (gemv.hip): o = sum_t e^(m_t - M) o_t / sum_t e^(m_t - M) l_t. Compared
-// with the CPU chain, only the bf16 rounding of the probabilities is not repeated.
-#define FL_SPL 128
+// k_attn_flash: grid (nsplit, KVH, G), 256 threads. Workgroup (t, kvh, g) handles query
+// head kvh*G + g over the FL_SPL = 64 positions of split t, 16 per wave. Spreading the
+// heads of a GQA group over workgroups (rather than serving all G heads from one K/V
+// read) gives G times more workgroups for the same split size; the G reads of a K/V
+// tile happen together and are served by the caches, and the work per wave stays small,
+// which is what decode attention is limited by (latency, not bytes).
+// Per wave: each lane holds a quarter (32 dims) of one position's K row (4 lanes per
+// position), the split's mask value for it and the matching quarter of q; scores are
+// summed across the quad with DPP, rounded at the model's points (as in k_attn_scores),
+// and the wave's (max, sum) come from DPP row rotations plus 4 lane reads. For P.V each
+// lane owns 2 of the 128 dims over the wave's 16 positions, taking p from the owning
+// lane with readlane. The 4 waves are merged in LDS into the split's partials
+//   m_t = max s, l_t = sum exp(s - m_t), o_t = sum exp(s - m_t) v   (fp32).
+// A wave whose 16 positions are all masked loads no K or V rows.
+// The partials are combined by k_attn_combine (or in the prologue of the next GEMV,
+// gemv.hip): o = sum_t e^(m_t - M) o_t / sum_t e^(m_t - M) l_t. Compared with the CPU
+// chain, only the bf16 rounding of the probabilities is not repeated.
+#define FL_SPL 64
+#define FL_PW 16
+#define FL_WAVES 4
 
 typedef __attribute__((ext_vector_type(2))) __bf16 fl_bf16x2;
 typedef __attribute__((ext_vector_type(2))) _Float16 fl_f16x2;
@@ -156,198 +167,169 @@ __device__ __forceinline__ float fl_dot2(uint32_t a, uint32_t b, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(fl_f16x2, a), __builtin_bit_cast(fl_f16x2, b), acc, false);
 }
 
+// cross-lane moves: DPP (quad permutes, rotations within a row of 16) and readlane
+#define FL_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xf, 0xf, false))
+#define FL_RL(v, l) __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, (v)), (l)))
+#define FL_QUAD_XOR1 0xB1
+#define FL_QUAD_XOR2 0x4E
+#define FL_ROW_ROR4 0x124
+#define FL_ROW_ROR8 0x128
+
+// max / sum over all 64 lanes (every lane gets the result)
+__device__ __forceinline__ float fl_wave_max(float m) {
+  m = fmaxf(m, FL_DPP(m, FL_QUAD_XOR1));
+  m = fmaxf(m, FL_DPP(m, FL_QUAD_XOR2));
+  m = fmaxf(m, FL_DPP(m, FL_ROW_ROR4));
+  m = fmaxf(m, FL_DPP(m, FL_ROW_ROR8));
+  return fmaxf(fmaxf(FL_RL(m, 0), FL_RL(m, 16)), fmaxf(FL_RL(m, 32), FL_RL(m, 48)));
+}
+__device__ __forceinline__ float fl_wave_sum(float l) {
+  l += FL_DPP(l, FL_QUAD_XOR1);
+  l += FL_DPP(l, FL_QUAD_XOR2);
+  l += FL_DPP(l, FL_ROW_ROR4);
+  l += FL_DPP(l, FL_ROW_ROR8);
+  return (FL_RL(l, 0) + FL_RL(l, 16)) + (FL_RL(l, 32) + FL_RL(l, 48));
+}
+
 template <int DT>
 __device__ __forceinline__ void flash_body(const FlashArgs& a) {
-  __shared__ float mv[FL_SPL];
-  __shared__ float sc[AT_GMAX][FL_SPL];
-  __shared__ float red[4][AT_GMAX][AT_D];
-  __shared__ int live;
+  __shared__ float osh[FL_WAVES][AT_D];
+  __shared__ float msh[FL_WAVES], lsh[FL_WAVES];
   const int G = a.H / a.KVH;
-  const int split = blockIdx.x, kvh = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const long long p0 = (long long)split * a.spl;
-  const int npos = (int)min((long long)a.spl, a.S - p0);
-  const int pw = a.spl >> 2;                       // positions per wave
-  const int g8 = lane >> 3, sub = lane & 7;        // K: 8 lanes per row, 16 dims each
-  const int g16 = lane >> 4, dv = (lane & 15) * 8; // V: 16 lanes per row, 8 dims each
-  float* ml = a.part_ml + ((long long)(kvh * a.nsplit + split) * G) * 2;
-  float* po = a.part_o + ((long long)(kvh * a.nsplit + split) * G) * AT_D;
-  // q (this lane's 16 dims of each head, kept packed) and the split's mask, in one round trip
-  uint4 qr[AT_GMAX][2];
+  const int split = blockIdx.x, kvh = blockIdx.y, g = blockIdx.z;
+  const long long p0 = (long long)split * FL_SPL + wave * FL_PW;   // this wave's first position
+  const int kq = lane >> 2, kc = lane & 3;                         // K: position p0 + kq, dims kc*32..+32
+  const long long last = a.S - 1;
+  const uint16_t* Kb = (const uint16_t*)a.k + (long long)kvh * a.kv_head_stride;
+  const uint16_t* Vb = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride;
+  float mval = -INFINITY;
+  if (p0 + kq <= last) mval = a.mask_dtype < 0 ? 0.f : ld_f(a.mask, (p0 + kq) * a.mask_stride, a.mask_dtype);
+  uint4 qr[4];
+  const uint4* qs = (const uint4*)((const uint16_t*)a.q + (long long)(kvh * G + g) * a.q_head_stride + kc * 32);
 #pragma unroll
-  for (int h = 0; h < AT_GMAX; ++h) {
-    const int hh = h < G ? h : 0;
-    const uint4* src = (const uint4*)((const uint16_t*)a.q + (long long)(kvh * G + hh) * a.q_head_stride + sub * 16);
-    qr[h][0] = src[0];
-    qr[h][1] = src[1];
-  }
-  if (threadIdx.x == 0) live = 0;
-  __syncthreads();
-  if ((int)threadIdx.x < a.spl) {
-    float m = -INFINITY;
-    if ((int)threadIdx.x < npos)
-      m = a.mask_dtype < 0 ? 0.f : ld_f(a.mask, (p0 + threadIdx.x) * a.mask_stride, a.mask_dtype);
-    mv[threadIdx.x] = m;
-    if (m != -INFINITY) live = 1;
-  }
-  __syncthreads();
-  if (!live) {   // fully masked split: l = 0 and zero partials (combines read them unconditionally)
-    if (threadIdx.x < G) {
-      ml[threadIdx.x * 2] = -INFINITY;
-      ml[threadIdx.x * 2 + 1] = 0.f;
+  for (int j = 0; j < 4; ++j) qr[j] = qs[j];
+  const bool live = __ballot(mval != -INFINITY) != 0ull;   // wave-uniform
+  float m_w = -INFINITY, l_w = 0.f, acc0 = 0.f, acc1 = 0.f;
+  if (live) {
+    uint4 kr[4];
+    uint32_t vr[FL_PW];
+    const uint4* ks = (const uint4*)(Kb + min(p0 + kq, last) * AT_D + kc * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kr[j] = ks[j];
+#pragma unroll
+    for (int t = 0; t < FL_PW; ++t) vr[t] = *(const uint32_t*)(Vb + min(p0 + t, last) * AT_D + 2 * lane);
+    float d = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      d = fl_dot2<DT>(qr[j].x, kr[j].x, d);
+      d = fl_dot2<DT>(qr[j].y, kr[j].y, d);
+      d = fl_dot2<DT>(qr[j].z, kr[j].z, d);
+      d = fl_dot2<DT>(qr[j].w, kr[j].w, d);
     }
-    for (int i = threadIdx.x; i < G * AT_D; i += 256) po[i] = 0.f;
-    return;
-  }
-  const uint16_t* K = (const uint16_t*)a.k + (long long)kvh * a.kv_head_stride + p0 * AT_D;
-  const uint16_t* V = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride + p0 * AT_D;
-  // Every K and V load is issued unconditionally; a masked or out-of-split row reads row 0
-  // of the split instead (valid memory) and is discarded, so all loads stay in flight.
-  uint4 kr[FL_SPL / 32][2];
-  uint4 vr[FL_SPL / 16];
-#pragma unroll
-  for (int st = 0; st < FL_SPL / 32; ++st) {
-    const int tp = wave * pw + st * 8 + g8;
-    const int row = (st * 8 < pw && mv[tp] != -INFINITY) ? tp : 0;
-    const uint4* src = (const uint4*)(K + (long long)row * AT_D + sub * 16);
-    kr[st][0] = src[0];
-    kr[st][1] = src[1];
-  }
-#pragma unroll
-  for (int st = 0; st < FL_SPL / 16; ++st) {
-    const int tp = wave * pw + st * 4 + g16;
-    const int row = (st * 4 < pw && mv[tp] != -INFINITY) ? tp : 0;
-    vr[st] = *(const uint4*)(V + (long long)row * AT_D + dv);
-  }
-  // scores (packed dot products on the raw bf16/fp16 data) with the model's rounding points
-#pragma unroll
-  for (int st = 0; st < FL_SPL / 32; ++st) {
-    if (st * 8 >= pw) break;
-    const int tp = wave * pw + st * 8 + g8;
-    const uint32_t kw[8] = {kr[st][0].x, kr[st][0].y, kr[st][0].z, kr[st][0].w,
-                            kr[st][1].x, kr[st][1].y, kr[st][1].z, kr[st][1].w};
-    float dots[AT_GMAX];
-#pragma unroll
-    for (int h = 0; h < AT_GMAX; ++h) {
-      const uint32_t qw[8] = {qr[h][0].x, qr[h][0].y, qr[h][0].z, qr[h][0].w,
-                              qr[h][1].x, qr[h][1].y, qr[h][1].z, qr[h][1].w};
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fl_dot2<DT>(qw[j], kw[j], acc);
-      acc += __shfl_xor(acc, 4, 64);
-      acc += __shfl_xor(acc, 2, 64);
-      acc += __shfl_xor(acc, 1, 64);
-      dots[h] = acc;
+    d += FL_DPP(d, FL_QUAD_XOR1);
+    d += FL_DPP(d, FL_QUAD_XOR2);
+    float s = -INFINITY;
+    if (mval != -INFINITY) {
+      s = round_to(d, DT);
+      s = round_to(s * a.scale, DT);
+      if (a.mask_dtype >= 0) s = round_to(s + mval, a.add_dtype);
     }
-    if (sub < G) {
-      float d = dots[0];
+    // the 4 lanes of a quad hold the same position: reduce over quads only
+    float m = fmaxf(s, FL_DPP(s, FL_ROW_ROR4));
+    m = fmaxf(m, FL_DPP(m, FL_ROW_ROR8));
+    m = fmaxf(fmaxf(FL_RL(m, 0), FL_RL(m, 16)), fmaxf(FL_RL(m, 32), FL_RL(m, 48)));
+    const float e = (s == -INFINITY) ? 0.f : __expf(s - m);
+    float l = e + FL_DPP(e, FL_ROW_ROR4);
+    l += FL_DPP(l, FL_ROW_ROR8);
+    l_w = (FL_RL(l, 0) + FL_RL(l, 16)) + (FL_RL(l, 32) + FL_RL(l, 48));
+    m_w = m;
 #pragma unroll
-      for (int h = 1; h < AT_GMAX; ++h) d = (sub == h) ? dots[h] : d;
-      float s = -INFINITY;
-      const float m = mv[tp];
-      if (m != -INFINITY) {
-        s = round_to(d, DT);
-        s = round_to(s * a.scale, DT);
-        if (a.mask_dtype >= 0) s = round_to(s + m, a.add_dtype);
+    for (int t = 0; t < FL_PW; ++t) {
+      float v0, v1;
+      if constexpr (DT == HS_BF16) {
+        v0 = bf16_to_f32((uint16_t)(vr[t] & 0xffffu));
+        v1 = bf16_to_f32((uint16_t)(vr[t] >> 16));
+      } else {
+        v0 = f16_to_f32((uint16_t)(vr[t] & 0xffffu));
+        v1 = f16_to_f32((uint16_t)(vr[t] >> 16));
       }
-      sc[sub][tp] = s;
+      const float p = FL_RL(e, 4 * t);
+      acc0 = fmaf(p, v0, acc0);
+      acc1 = fmaf(p, v1, acc1);
     }
+  }
+  osh[wave][2 * lane] = acc0;
+  osh[wave][2 * lane + 1] = acc1;
+  if (lane == 0) {
+    msh[wave] = m_w;
+    lsh[wave] = l_w;
   }
   __syncthreads();
-  // split max / sum per head; sc becomes exp(s - m)
-  for (int h = wave; h < G; h += 4) {
-    float m = -INFINITY;
-    for (int i = lane; i < a.spl; i += 64) m = fmaxf(m, sc[h][i]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int i = lane; i < a.spl; i += 64) {
-      const float s = sc[h][i];
-      const float e = (s == -INFINITY) ? 0.f : expf(s - m);
-      sc[h][i] = e;
-      l += e;
+  if (threadIdx.x < AT_D) {
+    const int dd = threadIdx.x;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < FL_WAVES; ++w) M = fmaxf(M, msh[w]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < FL_WAVES; ++w) {
+      const float f = (lsh[w] > 0.f) ? __expf(msh[w] - M) : 0.f;
+      o = fmaf(f, osh[w][dd], o);
+      L = fmaf(f, lsh[w], L);
     }
-    l = wave_sum(l);
-    if (lane == 0) {
-      ml[h * 2] = m;
-      ml[h * 2 + 1] = l;
+    const long long part = (long long)(kvh * a.nsplit + split) * G + g;
+    a.part_o[part * AT_D + dd] = o;
+    if (dd == 0) {
+      a.part_ml[part * 2] = M;
+      a.part_ml[part * 2 + 1] = L;
     }
-  }
-  __syncthreads();
-  float acc[AT_GMAX][8];
-#pragma unroll
-  for (int h = 0; h < AT_GMAX; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[h][j] = 0.f;
-#pragma unroll
-  for (int st = 0; st < FL_SPL / 16; ++st) {
-    if (st * 4 >= pw) break;
-    const int tp = wave * pw + st * 4 + g16;
-    if (mv[tp] == -INFINITY) continue;   // p = 0 for every head; the loaded row is a stand-in
-    float vf[8];
-    unpack8(vr[st], DT, vf);
-#pragma unroll
-    for (int h = 0; h < AT_GMAX; ++h) {
-      if (h < G) {
-        const float p = sc[h][tp];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[h][j] = fmaf(p, vf[j], acc[h][j]);
-      }
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < AT_GMAX; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      acc[h][j] += __shfl_xor(acc[h][j], 16, 64);
-      acc[h][j] += __shfl_xor(acc[h][j], 32, 64);
-    }
-  if (lane < 16) {
-#pragma unroll
-    for (int h = 0; h < AT_GMAX; ++h)
-      if (h < G)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) red[wave][h][dv + j] = acc[h][j];
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < G * AT_D; i += 256) {
-    const int h = i / AT_D, d = i % AT_D;
-    po[i] = ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d];
   }
 }
 
 extern "C" __global__ void __launch_bounds__(256) k_attn_flash(const FlashArgs a) { flash_body<HS_BF16>(a); }
 extern "C" __global__ void __launch_bounds__(256) k_attn_flash_f16(const FlashArgs a) { flash_body<HS_F16>(a); }
 
-// out[h, d] = round(sum_t e^(m_t - M) o_t[d] * (1 / sum_t e^(m_t - M) l_t)); one workgroup per head
+// out[h, d] = round(sum_t e^(m_t - M) o_t[d] / sum_t e^(m_t - M) l_t); one workgroup of 128
+// threads per head. Splits are folded in chunks of 64: lane t of every wave loads split t's
+// (m, l), so each wave forms the chunk's weights itself (no LDS, no barrier) and thread d
+// takes them with readlane while its 64 partial loads are already in flight.
+#define CB_CHUNK 64
 extern "C" __global__ void __launch_bounds__(128) k_attn_combine(const CombineArgs a) {
-  __shared__ float w[1024], lv[1024];
-  __shared__ float inv_l;
   const int h = blockIdx.x;
   const int G = a.H / a.KVH, kvh = h / G, g = h % G;
+  const int d = threadIdx.x, lane = threadIdx.x & 63;
   const float* ml = a.part_ml + ((long long)kvh * a.nsplit * G + g) * 2;
-  for (int t = threadIdx.x; t < a.nsplit; t += 128) {   // all (m, l) loads in flight at once
-    w[t] = ml[(long long)t * G * 2];
-    lv[t] = ml[(long long)t * G * 2 + 1];
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float M = -INFINITY;
-    for (int t = 0; t < a.nsplit; ++t)
-      if (lv[t] > 0.f) M = fmaxf(M, w[t]);
-    float L = 0.f;
-    for (int t = 0; t < a.nsplit; ++t) {
-      const float e = lv[t] > 0.f ? expf(w[t] - M) : 0.f;
-      w[t] = e;
-      L += e * lv[t];
+  const float* po = a.part_o + ((long long)kvh * a.nsplit * G + g) * AT_D + d;
+  float M = -INFINITY, L = 0.f, acc = 0.f;
+  for (int c0 = 0; c0 < a.nsplit; c0 += CB_CHUNK) {
+    const int n = min(CB_CHUNK, a.nsplit - c0);
+    float ot[CB_CHUNK];
+#pragma unroll
+    for (int i = 0; i < CB_CHUNK; ++i) ot[i] = po[(long long)(c0 + min(i, n - 1)) * G * AT_D];
+    float m = -INFINITY, l = 0.f;
+    if (lane < n) {
+      m = ml[(long long)(c0 + lane) * G * 2];
+      l = ml[(long long)(c0 + lane) * G * 2 + 1];
     }
-    inv_l = 1.0f / L;
+    if (!(l > 0.f)) m = -INFINITY;   // fully masked split
+    const float Mn = fmaxf(M, fl_wave_max(m));
+    const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
+    const float f = (m == -INFINITY) ? 0.f : __expf(m - Mn);
+    L = L * r + fl_wave_sum(f * l);
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < CB_CHUNK; i += 4) {
+      if (i < n) s0 = fmaf(FL_RL(f, i), ot[i], s0);
+      if (i + 1 < n) s1 = fmaf(FL_RL(f, i + 1), ot[i + 1], s1);
+      if (i + 2 < n) s2 = fmaf(FL_RL(f, i + 2), ot[i + 2], s2);
+      if (i + 3 < n) s3 = fmaf(FL_RL(f, i + 3), ot[i + 3], s3);
+    }
+    acc = acc * r + ((s0 + s1) + (s2 + s3));
+    M = Mn;
   }
-  __syncthreads();
-  const int d = threadIdx.x;
-  float s = 0.f;
-  for (int t = 0; t < a.nsplit; ++t)   // dead splits hold zero partials and weight 0
-    s += w[t] * a.part_o[(((long long)kvh * a.nsplit + t) * G + g) * AT_D + d];
-  const float o = s * inv_l;
+  const float o = acc / L;
   ((uint16_t*)a.out)[(long long)h * AT_D + d] = a.dtype == HS_BF16 ? f32_to_bf16(o) : f32_to_f16(o);
 }
 

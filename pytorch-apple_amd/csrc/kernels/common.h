@@ -260,7 +260,7 @@ struct FlashArgs {            // split-S decode attention: per-split (max, sum, 
   int H;
   int KVH;
   int nsplit;
-  int spl;                    // positions per split (multiple of 64, <= 256)
+  int spl;                    // positions per split: 64 (FL_SPL)
   float scale;
   int mask_dtype;             // -1: no mask
   int add_dtype;

@@ -288,7 +288,7 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     vv_ = low.contiguous(v)
     if (kv_.offset * 2) % 16 or (vv_.offset * 2) % 16:
         raise NotImplementedError("attention caches must be 16-byte aligned")
-    spl = 128 if S >= 1024 else 64
+    spl = 64                     # FL_SPL of k_attn_flash
     nsplit = (S + spl - 1) // spl
     margs = dict(mask=None, mask_stride=0, mask_dtype=-1)
     if mask is not None:
@@ -304,7 +304,7 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
               "nodes": names}
     low.emit(LaunchStep(kind="attention", kernel="k_attn_flash" if dt == "bfloat16" else "k_attn_flash_f16",
                         module="attention", arg_struct="FlashArgs",
-                        args=args, grid=(nsplit, kvh, 1), inputs=ins, outputs=[out.name + ".partials"],
+                        args=args, grid=(nsplit, kvh, G), inputs=ins, outputs=[out.name + ".partials"],
                         params=params))
 
     def combine():
