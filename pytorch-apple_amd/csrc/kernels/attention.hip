@@ -167,31 +167,6 @@ __device__ __forceinline__ float fl_dot2(uint32_t a, uint32_t b, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(fl_f16x2, a), __builtin_bit_cast(fl_f16x2, b), acc, false);
 }
 
-// cross-lane moves: DPP (quad permutes, rotations within a row of 16) and readlane
-#define FL_DPP(v, ctrl) \
-  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xf, 0xf, false))
-#define FL_RL(v, l) __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, (v)), (l)))
-#define FL_QUAD_XOR1 0xB1
-#define FL_QUAD_XOR2 0x4E
-#define FL_ROW_ROR4 0x124
-#define FL_ROW_ROR8 0x128
-
-// max / sum over all 64 lanes (every lane gets the result)
-__device__ __forceinline__ float fl_wave_max(float m) {
-  m = fmaxf(m, FL_DPP(m, FL_QUAD_XOR1));
-  m = fmaxf(m, FL_DPP(m, FL_QUAD_XOR2));
-  m = fmaxf(m, FL_DPP(m, FL_ROW_ROR4));
-  m = fmaxf(m, FL_DPP(m, FL_ROW_ROR8));
-  return fmaxf(fmaxf(FL_RL(m, 0), FL_RL(m, 16)), fmaxf(FL_RL(m, 32), FL_RL(m, 48)));
-}
-__device__ __forceinline__ float fl_wave_sum(float l) {
-  l += FL_DPP(l, FL_QUAD_XOR1);
-  l += FL_DPP(l, FL_QUAD_XOR2);
-  l += FL_DPP(l, FL_ROW_ROR4);
-  l += FL_DPP(l, FL_ROW_ROR8);
-  return (FL_RL(l, 0) + FL_RL(l, 16)) + (FL_RL(l, 32) + FL_RL(l, 48));
-}
-
 template <int DT>
 __device__ __forceinline__ void flash_body(const FlashArgs& a) {
   __shared__ float osh[FL_WAVES][AT_D];
@@ -228,8 +203,8 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
       d = fl_dot2<DT>(qr[j].z, kr[j].z, d);
       d = fl_dot2<DT>(qr[j].w, kr[j].w, d);
     }
-    d += FL_DPP(d, FL_QUAD_XOR1);
-    d += FL_DPP(d, FL_QUAD_XOR2);
+    d += HS_DPP(d, HS_QUAD_XOR1);
+    d += HS_DPP(d, HS_QUAD_XOR2);
     float s = -INFINITY;
     if (mval != -INFINITY) {
       s = round_to(d, DT);
@@ -237,13 +212,13 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
       if (a.mask_dtype >= 0) s = round_to(s + mval, a.add_dtype);
     }
     // the 4 lanes of a quad hold the same position: reduce over quads only
-    float m = fmaxf(s, FL_DPP(s, FL_ROW_ROR4));
-    m = fmaxf(m, FL_DPP(m, FL_ROW_ROR8));
-    m = fmaxf(fmaxf(FL_RL(m, 0), FL_RL(m, 16)), fmaxf(FL_RL(m, 32), FL_RL(m, 48)));
+    float m = fmaxf(s, HS_DPP(s, HS_ROW_ROR4));
+    m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
+    m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
     const float e = (s == -INFINITY) ? 0.f : __expf(s - m);
-    float l = e + FL_DPP(e, FL_ROW_ROR4);
-    l += FL_DPP(l, FL_ROW_ROR8);
-    l_w = (FL_RL(l, 0) + FL_RL(l, 16)) + (FL_RL(l, 32) + FL_RL(l, 48));
+    float l = e + HS_DPP(e, HS_ROW_ROR4);
+    l += HS_DPP(l, HS_ROW_ROR8);
+    l_w = (HS_RL(l, 0) + HS_RL(l, 16)) + (HS_RL(l, 32) + HS_RL(l, 48));
     m_w = m;
 #pragma unroll
     for (int t = 0; t < FL_PW; ++t) {
@@ -255,7 +230,7 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
         v0 = f16_to_f32((uint16_t)(vr[t] & 0xffffu));
         v1 = f16_to_f32((uint16_t)(vr[t] >> 16));
       }
-      const float p = FL_RL(e, 4 * t);
+      const float p = HS_RL(e, 4 * t);
       acc0 = fmaf(p, v0, acc0);
       acc1 = fmaf(p, v1, acc1);
     }
@@ -314,17 +289,17 @@ extern "C" __global__ void __launch_bounds__(128) k_attn_combine(const CombineAr
       l = ml[(long long)(c0 + lane) * G * 2 + 1];
     }
     if (!(l > 0.f)) m = -INFINITY;   // fully masked split
-    const float Mn = fmaxf(M, fl_wave_max(m));
+    const float Mn = fmaxf(M, wave_max(m));
     const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
     const float f = (m == -INFINITY) ? 0.f : __expf(m - Mn);
-    L = L * r + fl_wave_sum(f * l);
+    L = L * r + wave_sum(f * l);
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
     for (int i = 0; i < CB_CHUNK; i += 4) {
-      if (i < n) s0 = fmaf(FL_RL(f, i), ot[i], s0);
-      if (i + 1 < n) s1 = fmaf(FL_RL(f, i + 1), ot[i + 1], s1);
-      if (i + 2 < n) s2 = fmaf(FL_RL(f, i + 2), ot[i + 2], s2);
-      if (i + 3 < n) s3 = fmaf(FL_RL(f, i + 3), ot[i + 3], s3);
+      if (i < n) s0 = fmaf(HS_RL(f, i), ot[i], s0);
+      if (i + 1 < n) s1 = fmaf(HS_RL(f, i + 1), ot[i + 1], s1);
+      if (i + 2 < n) s2 = fmaf(HS_RL(f, i + 2), ot[i + 2], s2);
+      if (i + 3 < n) s3 = fmaf(HS_RL(f, i + 3), ot[i + 3], s3);
     }
     acc = acc * r + ((s0 + s1) + (s2 + s3));
     M = Mn;

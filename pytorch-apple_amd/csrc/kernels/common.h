@@ -352,16 +352,31 @@ __device__ __forceinline__ void st_f(void* p, long long i, int dt, float f) {
   }
 }
 
+// Cross-lane moves without LDS: DPP (quad permutes, rotations within a row of 16 lanes)
+// and readlane. They need every lane of the wave active, which holds at every call site.
+#define HS_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (v)), (ctrl), 0xf, 0xf, false))
+#define HS_RL(v, l) __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, (v)), (l)))
+#define HS_QUAD_XOR1 0xB1
+#define HS_QUAD_XOR2 0x4E
+#define HS_ROW_ROR4 0x124
+#define HS_ROW_ROR8 0x128
+
+// sum / max over the 64 lanes of a wave; every lane gets the result
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += HS_DPP(v, HS_QUAD_XOR1);
+  v += HS_DPP(v, HS_QUAD_XOR2);
+  v += HS_DPP(v, HS_ROW_ROR4);
+  v += HS_DPP(v, HS_ROW_ROR8);
+  return (HS_RL(v, 0) + HS_RL(v, 16)) + (HS_RL(v, 32) + HS_RL(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, HS_DPP(v, HS_QUAD_XOR1));
+  v = fmaxf(v, HS_DPP(v, HS_QUAD_XOR2));
+  v = fmaxf(v, HS_DPP(v, HS_ROW_ROR4));
+  v = fmaxf(v, HS_DPP(v, HS_ROW_ROR8));
+  return fmaxf(fmaxf(HS_RL(v, 0), HS_RL(v, 16)), fmaxf(HS_RL(v, 32), HS_RL(v, 48)));
 }
 
 // sum over a 256-thread workgroup; every thread gets the result

@@ -38,24 +38,86 @@ enum { EPI_BIAS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 #define GEMV_MAXK 8960
 #define GEMV_MB 4
 
-// RMSNorm of `rows` activation rows into LDS (bf16 bits); 256 threads.
-__device__ __forceinline__ void norm_to_lds(const GemvArgs& a, long long m0, int rows, uint16_t* xs) {
-  __shared__ float red[4];
-  for (int m = 0; m < rows; ++m) {
-    const uint16_t* x = (const uint16_t*)a.x + (m0 + m) * a.ldx;
-    float ss = 0.f;
-    for (int c = threadIdx.x; c < a.K; c += 256) {
-      const float h = bf16_to_f32(x[c]);
-      ss += h * h;
+// RMSNorm (norm = true) or a plain copy of `rows` <= ROWS activation rows of length K into LDS
+// as bf16 bits (row m at xs + m*K); 256 threads, K % 8 == 0, K <= 4096, 16-byte aligned rows.
+// x and the norm weight are fetched with 16-byte loads, all in one round; the sums of squares
+// are reduced with DPP plus one LDS exchange.
+template <int ROWS>
+__device__ __forceinline__ void rows_to_lds(const uint16_t* x, long long ldx, int rows, const uint16_t* w, int K,
+                                            float eps, int n_dtype, bool norm, uint16_t* xs) {
+  __shared__ float red[4][ROWS];
+  const int K8 = K >> 3;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint4 xv[ROWS][2], wn[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int i = threadIdx.x + c * 256;
+    wn[c] = (norm && i < K8) ? *(const uint4*)(w + 8 * i) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int m = 0; m < ROWS; ++m)
+      xv[m][c] = (m < rows && i < K8) ? *(const uint4*)(x + m * ldx + 8 * i) : make_uint4(0, 0, 0, 0);
+  }
+  if (!norm) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int i = threadIdx.x + c * 256;
+#pragma unroll
+      for (int m = 0; m < ROWS; ++m)
+        if (m < rows && i < K8) *(uint4*)(xs + m * K + 8 * i) = xv[m][c];
     }
-    ss = block_sum256(ss, red);
-    const float r = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-    for (int c = threadIdx.x; c < a.K; c += 256) {
-      const float n = round_to(bf16_to_f32(x[c]) * r, a.n_dtype);
-      xs[m * a.K + c] = f32_to_bf16(bf(a.norm_w, c) * n);
+    __syncthreads();
+    return;
+  }
+  float ss[ROWS];
+#pragma unroll
+  for (int m = 0; m < ROWS; ++m) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const uint32_t q[4] = {xv[m][c].x, xv[m][c].y, xv[m][c].z, xv[m][c].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_to_f32((uint16_t)(q[j] & 0xffffu)), hi = bf16_to_f32((uint16_t)(q[j] >> 16));
+        acc = fmaf(lo, lo, acc);
+        acc = fmaf(hi, hi, acc);
+      }
+    }
+    ss[m] = wave_sum(acc);
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int m = 0; m < ROWS; ++m) red[wave][m] = ss[m];
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < ROWS; ++m) {
+    if (m >= rows) break;
+    const float tot = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
+    const float r = 1.0f / sqrtf(tot / (float)K + eps);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int i = threadIdx.x + c * 256;
+      if (i >= K8) continue;
+      const uint32_t q[4] = {xv[m][c].x, xv[m][c].y, xv[m][c].z, xv[m][c].w};
+      const uint32_t g[4] = {wn[c].x, wn[c].y, wn[c].z, wn[c].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float n0 = round_to(bf16_to_f32((uint16_t)(q[j] & 0xffffu)) * r, n_dtype);
+        const float n1 = round_to(bf16_to_f32((uint16_t)(q[j] >> 16)) * r, n_dtype);
+        const uint16_t y0 = f32_to_bf16(bf16_to_f32((uint16_t)(g[j] & 0xffffu)) * n0);
+        const uint16_t y1 = f32_to_bf16(bf16_to_f32((uint16_t)(g[j] >> 16)) * n1);
+        o[j] = (uint32_t)y0 | ((uint32_t)y1 << 16);
+      }
+      *(uint4*)(xs + m * K + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
     }
   }
   __syncthreads();
+}
+
+template <int MB>
+__device__ __forceinline__ void norm_to_lds(const GemvArgs& a, long long m0, int rows, uint16_t* xs) {
+  rows_to_lds<MB>((const uint16_t*)a.x + m0 * a.ldx, a.ldx, rows, (const uint16_t*)a.norm_w, a.K, a.eps, a.n_dtype,
+                  true, xs);
 }
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
@@ -153,7 +215,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     }
   };
   load_round(kstart);
-  if constexpr (PRO == PRO_NORM) norm_to_lds(a, m0, mrows, xs);
+  if constexpr (PRO == PRO_NORM) norm_to_lds<MB>(a, m0, mrows, xs);
   if constexpr (PRO == PRO_ATTN) attn_to_lds(a, xs);
   for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
   n0 = KS > 1 ? blk * RPW : (blk * 4 + wave) * RPW;
@@ -319,8 +381,7 @@ extern "C" __global__ void __launch_bounds__(256) k_argmax_finalize(const Argmax
 //   q and k: rows (h*D + j, h*D + j + D/2) of one head, rotated together;
 //   v:       rows (2t, 2t+1), plain.
 extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t xs[1536 * 2];
-  __shared__ float red[4];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[3072];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int D = a.D, half = a.D / 2;
@@ -356,25 +417,7 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
     w0[c] = k < a.K ? ld_stream(W + (long long)r0 * a.K + k) : make_uint4(0, 0, 0, 0);
     w1[c] = k < a.K ? ld_stream(W + (long long)r1 * a.K + k) : make_uint4(0, 0, 0, 0);
   }
-  {
-    const uint16_t* x = (const uint16_t*)a.x;
-    if (a.flags & 1) {
-      float ss = 0.f;
-      for (int c = threadIdx.x; c < a.K; c += 256) {
-        const float h = bf16_to_f32(x[c]);
-        ss += h * h;
-      }
-      ss = block_sum256(ss, red);
-      const float r = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-      for (int c = threadIdx.x; c < a.K; c += 256) {
-        const float n = round_to(bf16_to_f32(x[c]) * r, a.n_dtype);
-        xs[c] = f32_to_bf16(bf(a.norm_w, c) * n);
-      }
-    } else {
-      for (int c = threadIdx.x; c < a.K; c += 256) xs[c] = x[c];
-    }
-    __syncthreads();
-  }
+  rows_to_lds<1>((const uint16_t*)a.x, 0, 1, (const uint16_t*)a.norm_w, a.K, a.eps, a.n_dtype, (a.flags & 1) != 0, xs);
   if (!active) return;
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
@@ -395,8 +438,10 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
   if (rope) {
     const float f = invf * (float)pos_v;
-    const float c = round_to(cosf(f) * a.rope_scaling, HS_BF16);
-    const float s = round_to(sinf(f) * a.rope_scaling, HS_BF16);
+    float sf, cf;
+    sincosf(f, &sf, &cf);
+    const float c = round_to(cf * a.rope_scaling, HS_BF16);
+    const float s = round_to(sf * a.rope_scaling, HS_BF16);
     const float e0 = rbf(rbf(v0 * c) + rbf(-v1 * s));   // x[j]*cos + (-x[j+D/2])*sin
     const float e1 = rbf(rbf(v1 * c) + rbf(v0 * s));    // x[j+D/2]*cos + x[j]*sin
     v0 = e0;

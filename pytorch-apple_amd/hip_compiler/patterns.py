@@ -631,9 +631,13 @@ def _emit_qkv(low, xname, q, k, v, names) -> None:
         raise NotImplementedError("fused RoPE needs fp32 inv_freq and one position")
     H, KVH, D = q["nh"], k["nh"], q["D"]
     K = x.shape[-1]
+    if K % 8 or K > 3072:
+        raise NotImplementedError("fused q/k/v needs hidden % 8 == 0 and <= 3072 (staged in LDS)")
+    x = low.aligned16(x, norm["x"] if norm else xname)
+    nw = low.aligned16(low.contiguous(norm["w"]), norm["w"]) if norm else None
     qo = low.new_storage(q["out"], [1, H, 1, D], "bfloat16")
     kc, vc = low.views[k["past"]], low.views[v["past"]]
-    args = dict(x=low.ref(x), norm_w=low.ref(low.contiguous(norm["w"])) if norm else None,
+    args = dict(x=low.ref(x), norm_w=low.ref(nw) if norm else None,
                 wq=low.ref(low.contiguous(q["w"].name)), bq=low.ref(low.contiguous(q["b"].name)) if q["b"] else None,
                 wk=low.ref(low.contiguous(k["w"].name)), bk=low.ref(low.contiguous(k["b"].name)) if k["b"] else None,
                 wv=low.ref(low.contiguous(v["w"].name)), bv=low.ref(low.contiguous(v["b"].name)) if v["b"] else None,

@@ -163,6 +163,17 @@ class Lowering:
     def emit(self, step: LaunchStep) -> None:
         self.steps.append(step)
 
+    def aligned16(self, v: TView, name: str) -> TView:
+        """``v`` (contiguous) if it starts on a 16-byte boundary, else a fresh aligned copy of it."""
+        if (v.offset * ELEM_SIZE[v.dtype]) % 16 == 0:
+            return v
+        if name + ".a16" in self.views:
+            return self.views[name + ".a16"]
+        aligned = self.new_storage(name + ".a16", v.shape, v.dtype)
+        self.emit_copy(v, aligned, [name], [name + ".a16"])
+        self.views[name + ".a16"] = aligned
+        return aligned
+
     def emit_copy(self, src: TView, dst: TView, ins: list[str], outs: list[str]) -> None:
         nd = len(src.shape)
         if nd > 6:
@@ -347,7 +358,7 @@ class Lowering:
         K = w.shape[1]
         N = w.shape[0]
         if norm is not None:
-            x = self.contiguous(norm["x"])
+            x = self.aligned16(self.contiguous(norm["x"]), norm["x"])
             M = x.numel // K
             mb = 1 if M == 1 else 4
             if K > 3072:   # the normalised rows are staged in LDS: MB x 3072 bf16
@@ -360,12 +371,8 @@ class Lowering:
         if attn is not None:
             x, M = None, 1
         elif norm is None:
-            x = self.contiguous(x_name)
+            x = self.aligned16(self.contiguous(x_name), x_name)
             M = x.numel // K
-            if (x.offset * 2) % 16:
-                aligned = self.new_storage(x_name + ".a", x.shape, x.dtype)
-                self.emit_copy(x, aligned, [x_name], [x_name + ".a"])
-                x = aligned
         mb = 1 if M == 1 else 4
         if epi == "argmax":
             rpw = 4 if M == 1 else 2
@@ -410,7 +417,8 @@ class Lowering:
         args = dict(x=self.ref(x) if x is not None else None, w=self.ref(w), bias=self.ref(bias) if bias else None,
                     out=self.ref(o), resid=self.ref(r) if r else None, w2=self.ref(wv2) if wv2 else None,
                     bias2=self.ref(bv2) if bv2 else None,
-                    norm_w=self.ref(self.contiguous(norm["w"])) if norm else None, argmax_slot=slot,
+                    norm_w=self.ref(self.aligned16(self.contiguous(norm["w"]), norm["w"])) if norm else None,
+                    argmax_slot=slot,
                     attn_o=attn["part_o"] if attn else None, attn_ml=attn["part_ml"] if attn else None,
                     M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=float(norm["eps"]) if norm else 0.0,
                     n_dtype=DTYPE_CODE[norm["n_dtype"]] if norm else 0,
