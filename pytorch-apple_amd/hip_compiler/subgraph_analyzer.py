@@ -365,7 +365,7 @@ class Lowering:
                 norm = None
         if norm is None and self.fold_attn_combine:
             attn = self.foldable_attn(x_name, set(nodes))
-            if attn is not None and (K != attn["H"] * 128 or attn["H"] > 16 or attn["nsplit"] > 128
+            if attn is not None and (K != attn["H"] * 128 or attn["H"] > 12 or attn["nsplit"] > 32
                                      or epi not in ("bias", "resid")):
                 attn = None
         if attn is not None:
