@@ -155,6 +155,27 @@ struct LinearArgs {           // out[m, n] = round(x[m, :] . w[n, :] + bias[n]) 
   int pad;
 };
 
+struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M, K], w [N, K], K % 32 == 0
+  const void* x;              // [M, K] (row stride ldx), 16-byte aligned rows
+  const void* w;              // [N, K] contiguous
+  const void* w2;             // second weight (SiLU * mul epilogue: w = gate, w2 = up) or null
+  const void* bias;           // [N] or null
+  const void* bias2;          // [N] or null (for w2)
+  const void* resid;          // [M, N] (row stride ldr) or null
+  void* out;                  // [M, N] (row stride ldo)
+  float* part;                // split-K: fp32 partial sums [ksplit, NW, M, N], reduced by k_gemm_reduce_*
+  long long M;
+  long long ldx;
+  long long ldo;
+  long long ldr;
+  int N;
+  int K;
+  int flags;                  // 1: bias, 2: bias2
+  int ksplit;                 // 1: epilogue in the GEMM; > 1: grid.z splits K into chunks of kchunk
+  int kchunk;                 // K elements per split (multiple of 32)
+  int nw;                     // weights (1, or 2 for SiLU * mul); read by the reduce kernel
+};
+
 struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm, epilogues bias/resid/silu/argmax
   const void* x;              // [M, K] bf16 activations (raw residual stream when NORM)
   const void* w;              // [N, K] bf16

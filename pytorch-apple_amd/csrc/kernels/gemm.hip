@@ -1,0 +1,235 @@
+// MFMA GEMM for prefill-shaped linears (M >= 64): out[m, n] = epi(sum_k x[m, k] w[n, k]).
+//
+// Both operands are K-contiguous ([M, K] activations, [N, K] weights as the model stores
+// them), which is exactly the register layout of the gfx950 MFMA
+// v_mfma_f32_32x32x16_{bf16,f16}: lane l holds 8 consecutive k of row (or column) l % 32
+// at k offset 8 * (l / 32), and the 32x32 fp32 result sits in 16 registers per lane,
+// element 4q + r at row 8q + 4(l / 32) + r, column l % 32.
+// Workgroup tile BM x BN (BN columns per weight), K step 32, 256 threads as 2 x 2
+// waves of (BM / 2) x (BN / 2). Tiles are double-buffered in LDS through registers: the
+// global loads of step k+1 are in flight while step k is multiplied, then stored to the
+// other buffer, one barrier per step. LDS rows are padded (40 elements) so the 16-byte
+// fragment reads of 32 consecutive rows spread over the banks.
+// Epilogues (fp32 accumulator, ATen's rounding points):
+//   BIAS  out = round(acc + b)
+//   RESID out = round(r + round(acc + b))
+//   SILU  out = round(round(silu(round(acc_g + b_g))) * round(acc_u + b_u))   (NW = 2)
+// Rows past M and columns past N are computed from clamped (valid) addresses and not stored.
+#include "common.h"
+
+typedef __attribute__((ext_vector_type(8))) __bf16 gm_bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 gm_f16x8;
+typedef __attribute__((ext_vector_type(16))) float gm_f32x16;
+
+enum { GE_BIAS = 0, GE_RESID = 1, GE_SILU = 2 };
+#define GM_BK 32
+#define GM_LDS_K 40   // padded row length in LDS (elements)
+
+template <int DT>
+__device__ __forceinline__ gm_f32x16 gm_mfma(const uint4 a, const uint4 b, gm_f32x16 c) {
+  if constexpr (DT == HS_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(gm_bf16x8, a), __builtin_bit_cast(gm_bf16x8, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(gm_f16x8, a), __builtin_bit_cast(gm_f16x8, b),
+                                                  c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float gm_ld(const void* p, long long i) {
+  const uint16_t h = ((const uint16_t*)p)[i];
+  return DT == HS_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+
+template <int DT>
+__device__ __forceinline__ float gm_round(float f) {
+  return DT == HS_BF16 ? bf16_to_f32(f32_to_bf16(f)) : f16_to_f32(f32_to_f16(f));
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t gm_pack(float f) {
+  return DT == HS_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
+}
+
+template <int DT, int EPI, int NW, int BM, int BN>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a) {
+  constexpr int BNT = BN * NW;            // weight rows staged per step (BN columns per weight)
+  constexpr int TI = BM / 64;             // 32-row MFMA tiles per wave
+  constexpr int TJ = BN / 64;             // 32-column MFMA tiles per wave and weight
+  constexpr int A_LD = BM * GM_BK / 8 / 256;    // 16-byte A loads per thread per step
+  constexpr int B_LD = BNT * GM_BK / 8 / 256;   // 16-byte B loads per thread per step
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][GM_LDS_K];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BNT][GM_LDS_K];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const long long m_base = (long long)blockIdx.y * BM;
+  const int n_base = blockIdx.x * BN;
+  const uint16_t* X = (const uint16_t*)a.x;
+  const uint16_t* W[2] = {(const uint16_t*)a.w, (const uint16_t*)(NW == 2 ? a.w2 : a.w)};
+
+  // global -> register staging of one K step
+  uint4 ra[A_LD], rb[B_LD];
+  auto load_step = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+      const long long m = min(m_base + row, a.M - 1);
+      ra[i] = *(const uint4*)(X + m * a.ldx + k0 + col);
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+      const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
+      rb[i] = *(const uint4*)(W[u] + (long long)n * a.K + k0 + col);
+    }
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+      *(uint4*)&As[buf][row][col] = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+      *(uint4*)&Bs[buf][row][col] = rb[i];
+    }
+  };
+
+  gm_f32x16 acc[NW][TI][TJ];
+#pragma unroll
+  for (int u = 0; u < NW; ++u)
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[u][i][j][e] = 0.f;
+
+  // split K: workgroup z covers [z * kchunk, (z + 1) * kchunk)
+  const int kbeg = blockIdx.z * a.kchunk;
+  const int nsteps = min(a.kchunk, a.K - kbeg) / GM_BK;
+  X += kbeg;
+  W[0] += kbeg;
+  W[1] += kbeg;
+  load_step(0);
+  store_step(0);
+  __syncthreads();
+  const int fr = lane & 31, fk = (lane >> 5) * 8;   // fragment row/column and k offset of this lane
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nsteps) load_step((s + 1) * GM_BK);
+#pragma unroll
+    for (int ks = 0; ks < GM_BK / 16; ++ks) {
+      uint4 af[TI], bfr[NW][TJ];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) af[i] = *(const uint4*)&As[buf][wr * (BM / 2) + i * 32 + fr][ks * 16 + fk];
+#pragma unroll
+      for (int u = 0; u < NW; ++u)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          bfr[u][j] = *(const uint4*)&Bs[buf][u * BN + wc * (BN / 2) + j * 32 + fr][ks * 16 + fk];
+#pragma unroll
+      for (int u = 0; u < NW; ++u)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) acc[u][i][j] = gm_mfma<DT>(af[i], bfr[u][j], acc[u][i][j]);
+    }
+    if (s + 1 < nsteps) store_step(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (a.ksplit > 1) {   // raw fp32 partial sums; k_gemm_reduce_* applies the epilogue
+#pragma unroll
+    for (int u = 0; u < NW; ++u)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int n = n_base + wc * (BN / 2) + j * 32 + fr;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            if (m < a.M) a.part[(((long long)blockIdx.z * NW + u) * a.M + m) * a.N + n] = acc[u][i][j][e];
+          }
+      }
+    return;
+  }
+  // epilogue
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int n = n_base + wc * (BN / 2) + j * 32 + fr;
+    if (n >= a.N) continue;
+    const float b0 = (a.flags & 1) ? gm_ld<DT>(a.bias, n) : 0.f;
+    const float b1 = (EPI == GE_SILU && (a.flags & 2)) ? gm_ld<DT>(a.bias2, n) : 0.f;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (m >= a.M) continue;
+        float v = gm_round<DT>(acc[0][i][j][e] + b0);
+        if constexpr (EPI == GE_RESID) v = gm_round<DT>(gm_ld<DT>(a.resid, m * a.ldr + n) + v);
+        if constexpr (EPI == GE_SILU) {
+          const float up = gm_round<DT>(acc[NW - 1][i][j][e] + b1);
+          const float sg = gm_round<DT>(v / (1.f + expf(-v)));
+          v = gm_round<DT>(sg * up);
+        }
+        ((uint16_t*)a.out)[m * a.ldo + n] = gm_pack<DT>(v);
+      }
+    }
+  }
+}
+
+// Split-K reduction and epilogue: one thread per output element (fixed summation order).
+template <int DT, int EPI>
+__device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
+  const long long total = a.M * a.N;
+  const long long plane = total;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const long long m = i / a.N;
+    const int n = (int)(i % a.N);
+    float g = 0.f, up = 0.f;
+    for (int z = 0; z < a.ksplit; ++z) {
+      g += a.part[((long long)z * a.nw) * plane + i];
+      if constexpr (EPI == GE_SILU) up += a.part[((long long)z * a.nw + 1) * plane + i];
+    }
+    float v = gm_round<DT>(g + ((a.flags & 1) ? gm_ld<DT>(a.bias, n) : 0.f));
+    if constexpr (EPI == GE_RESID) v = gm_round<DT>(gm_ld<DT>(a.resid, m * a.ldr + n) + v);
+    if constexpr (EPI == GE_SILU) {
+      const float u = gm_round<DT>(up + ((a.flags & 2) ? gm_ld<DT>(a.bias2, n) : 0.f));
+      const float sg = gm_round<DT>(v / (1.f + expf(-v)));
+      v = gm_round<DT>(sg * u);
+    }
+    ((uint16_t*)a.out)[m * a.ldo + n] = gm_pack<DT>(v);
+  }
+}
+
+#define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); }
+#define GEMM_REDUCE(NAME, DT, EPI) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_reduce_body<DT, EPI>(a); }
+
+// k_gemm_<dtype>_<epilogue>_m<BM>n<BN>: BN columns per weight
+GEMM_KERNEL(k_gemm_bf16_bias_m128n128, HS_BF16, GE_BIAS, 1, 128, 128)
+GEMM_KERNEL(k_gemm_bf16_bias_m64n128, HS_BF16, GE_BIAS, 1, 64, 128)
+GEMM_KERNEL(k_gemm_bf16_bias_m64n64, HS_BF16, GE_BIAS, 1, 64, 64)
+GEMM_KERNEL(k_gemm_bf16_resid_m128n128, HS_BF16, GE_RESID, 1, 128, 128)
+GEMM_KERNEL(k_gemm_bf16_resid_m64n128, HS_BF16, GE_RESID, 1, 64, 128)
+GEMM_KERNEL(k_gemm_bf16_resid_m64n64, HS_BF16, GE_RESID, 1, 64, 64)
+GEMM_KERNEL(k_gemm_bf16_silu_m128n64, HS_BF16, GE_SILU, 2, 128, 64)
+GEMM_KERNEL(k_gemm_bf16_silu_m64n64, HS_BF16, GE_SILU, 2, 64, 64)
+GEMM_KERNEL(k_gemm_f16_bias_m128n128, HS_F16, GE_BIAS, 1, 128, 128)
+GEMM_KERNEL(k_gemm_f16_bias_m64n128, HS_F16, GE_BIAS, 1, 64, 128)
+GEMM_KERNEL(k_gemm_f16_bias_m64n64, HS_F16, GE_BIAS, 1, 64, 64)
+GEMM_KERNEL(k_gemm_f16_resid_m128n128, HS_F16, GE_RESID, 1, 128, 128)
+GEMM_KERNEL(k_gemm_f16_resid_m64n128, HS_F16, GE_RESID, 1, 64, 128)
+GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64)
+GEMM_REDUCE(k_gemm_reduce_bf16_bias, HS_BF16, GE_BIAS)
+GEMM_REDUCE(k_gemm_reduce_bf16_resid, HS_BF16, GE_RESID)
+GEMM_REDUCE(k_gemm_reduce_bf16_silu, HS_BF16, GE_SILU)
+GEMM_REDUCE(k_gemm_reduce_f16_bias, HS_F16, GE_BIAS)
+GEMM_REDUCE(k_gemm_reduce_f16_resid, HS_F16, GE_RESID)

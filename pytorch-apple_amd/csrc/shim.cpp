@@ -245,6 +245,7 @@ size_t hs_argsize(const char* s) {
   HS_SZ(ReduceLastArgs)
   HS_SZ(BmmArgs)
   HS_SZ(LinearArgs)
+  HS_SZ(GemmArgs)
   HS_SZ(DecodeAttnArgs)
   HS_SZ(FusedArgs)
   HS_SZ(GemvArgs)

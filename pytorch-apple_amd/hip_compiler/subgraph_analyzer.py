@@ -35,6 +35,13 @@ from npu_compiler.ir_reader import IRGraph, OpNode
 HS_BF16, HS_F16 = DTYPE_CODE["bfloat16"], DTYPE_CODE["float16"]
 
 
+# linears with at least this many activation rows use the MFMA GEMM (weights read once per
+# column tile) instead of the streaming GEMV (weights re-read per block of 4 rows)
+GEMM_MIN_M = 16
+GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
+GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
+
+
 def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
     return (max(1, min(cap, (int(n) + block - 1) // block)), 1, 1)
 
@@ -351,7 +358,14 @@ class Lowering:
     def emit_gemv(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, *, epi: str,
                   nodes: list[str], resid: str | None = None, w2: str | None = None, b2: str | None = None,
                   argmax_out=None) -> None:
-        """One fused GEMV launch (csrc/kernels/gemv.hip); folds a pending RMSNorm of ``x`` when possible."""
+        """One fused GEMV launch (csrc/kernels/gemv.hip); folds a pending RMSNorm of ``x`` when possible.
+        Prefill-shaped calls (M >= GEMM_MIN_M) go to the MFMA GEMM instead."""
+        w_view = self.view(w_name)
+        n_out = numel(out_shape) // w_view.shape[0] if w_view.shape[0] else 0
+        if epi in ("bias", "resid", "silu") and n_out >= GEMM_MIN_M and w_view.shape[1] % 32 == 0:
+            self.emit_gemm(x_name, w_name, b_name, out_name, out_shape, "bfloat16", epi=epi, nodes=nodes,
+                           resid=resid, w2=w2, b2=b2)
+            return
         norm = self.foldable_norm(x_name, set(nodes))
         attn = None
         w = self.contiguous(w_name)
@@ -445,6 +459,52 @@ class Lowering:
                 params={"rows": M, "cols": N}))
             self.views[name] = t
 
+    def emit_gemm(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, dtype: str, *,
+                  epi: str, nodes: list[str], resid: str | None = None, w2: str | None = None,
+                  b2: str | None = None) -> None:
+        """MFMA GEMM (csrc/kernels/gemm.hip) for M >= GEMM_MIN_M: out = epi(x . W^T); a pending
+        RMSNorm of ``x`` is materialised first (it is cheap next to the GEMM)."""
+        w = self.aligned16(self.contiguous(w_name), w_name)
+        N, K = w.shape
+        x = self.aligned16(self.contiguous(x_name), x_name)
+        M = x.numel // K
+        o = self.new_storage(out_name, out_shape, dtype)
+        bias = self.contiguous(b_name) if b_name else None
+        r = self.contiguous(resid) if resid else None
+        wv2 = self.aligned16(self.contiguous(w2), w2) if w2 else None
+        bv2 = self.contiguous(b2) if b2 else None
+        nw = 2 if epi == "silu" else 1
+        # the largest tile that still gives >= 256 workgroups; below that, split K as well
+        tiles = [(128, 64), (64, 64)] if nw == 2 else [(128, 128), (64, 128), (64, 64)]
+        for bm, bn in tiles:
+            ntiles = ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
+            if ntiles >= GEMM_TARGET_WGS:
+                break
+        ksplit, kchunk = 1, K
+        if ntiles < GEMM_TARGET_WGS:
+            ksplit = max(1, min((GEMM_TARGET_WGS + ntiles - 1) // ntiles, K // GEMM_MIN_KCHUNK))
+            kchunk = ((K // 32 + ksplit - 1) // ksplit) * 32
+            ksplit = (K + kchunk - 1) // kchunk
+        dt = "bf16" if dtype == "bfloat16" else "f16"
+        part = self.scratch(out_name + ".kpart", ksplit * nw * M * N * 4) if ksplit > 1 else None
+        args = dict(x=self.ref(x), w=self.ref(w), w2=self.ref(wv2) if wv2 else None,
+                    bias=self.ref(bias) if bias else None, bias2=self.ref(bv2) if bv2 else None,
+                    resid=self.ref(r) if r else None, out=self.ref(o), part=part, M=M, ldx=K, ldo=N, ldr=N,
+                    N=N, K=K, flags=(1 if bias else 0) | (2 if bv2 else 0), ksplit=ksplit, kchunk=kchunk, nw=nw)
+        ins = [x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t]
+        params = {"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None, "weights": nw,
+                  "transpose_b": True, "nodes": nodes, "mfma": True, "tile": (bm, bn), "ksplit": ksplit}
+        self.emit(LaunchStep(
+            kind="gemm", kernel=f"k_gemm_{dt}_{epi}_m{bm}n{bn}", module="gemm", arg_struct="GemmArgs", args=args,
+            grid=((N + bn - 1) // bn, (M + bm - 1) // bm, ksplit), inputs=ins,
+            outputs=[out_name + ".kpart" if ksplit > 1 else out_name], params=params))
+        if ksplit > 1:
+            self.emit(LaunchStep(
+                kind="gemm", kernel=f"k_gemm_reduce_{dt}_{epi}", module="gemm", arg_struct="GemmArgs",
+                args=dict(args), grid=grid1d(M * N), inputs=[out_name + ".kpart"] + ins[2:], outputs=[out_name],
+                params=dict(params, reduce=True)))
+        self.views[out_name] = o
+
     def emit_linear(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, out_dtype: str,
                     resid: str | None, node_names: list[str]) -> None:
         x = self.contiguous(x_name)
@@ -460,6 +520,10 @@ class Lowering:
             self.emit_linear_generic(x, w, b_name, out_name, out_shape, out_dtype, node_names)
             if resid is not None:
                 raise NotImplementedError("residual epilogue on the generic path")
+            return
+        if M >= GEMM_MIN_M and K % 32 == 0:
+            self.emit_gemm(x_name, w_name, b_name, out_name, out_shape, out_dtype,
+                           epi="resid" if resid is not None else "bias", nodes=node_names, resid=resid)
             return
         o = self.new_storage(out_name, out_shape, out_dtype)
         bias = self.contiguous(b_name) if b_name is not None else None

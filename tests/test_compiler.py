@@ -19,7 +19,7 @@ def kernels(p):
 def test_mlp_block_fused_and_generic_step_lists():
     fused = compile_subgraph(build_mlp_ir(1))
     assert kernels(fused) == ["k_gemv_norm_silu_r1", "k_gemv_resid_ks_r2"]
-    gen = compile_subgraph(build_mlp_ir(16), fuse=False)
+    gen = compile_subgraph(build_mlp_ir(4), fuse=False)
     kinds = [s.kind for s in gen.steps]
     # the reference's expected list: [RMSNorm, gemm gate, gemm up, fused(silu, mul), gemm down, fused(add)]
     assert kinds.count("gemv") == 3 and kinds.count("fused") >= 2
@@ -27,10 +27,32 @@ def test_mlp_block_fused_and_generic_step_lists():
     chains = [s.params["ops"] for s in gen.steps if s.kind == "fused"]
     assert ["aten.silu.default", "aten.mul.Tensor"] in chains
     assert ["aten.add.Tensor"] in chains
+    # prefill-shaped rows: the linears go to the MFMA GEMM (gate, up, down), fused or not
+    gen16 = compile_subgraph(build_mlp_ir(16), fuse=False)
+    assert sum(1 for s in gen16.steps if s.kind == "gemm" and not s.params.get("reduce")) == 3
+
+
+def test_prefill_mlp_is_norm_plus_two_mfma_gemms():
+    p = compile_subgraph(build_mlp_ir(512))
+    main = [s for s in p.steps if s.kind == "gemm" and not s.params.get("reduce")]
+    assert kernels(p)[0] == "k_rmsnorm" and abs(p.steps[0].args["eps"] - 1e-6) < 1e-12
+    assert [s.params["epilogue"] for s in main] == ["silu", "resid"]
+    assert main[0].params["weights"] == 2 and main[0].args["w2"] is not None
+    for s in main:   # every workgroup covers a whole K range; splits tile K exactly
+        g = s.grid
+        assert g[2] == s.args["ksplit"] and s.args["kchunk"] % 32 == 0
+        assert (g[2] - 1) * s.args["kchunk"] < s.args["K"] <= g[2] * s.args["kchunk"]
+        bm, bn = s.params["tile"]
+        assert g[0] * bn >= s.args["N"] and g[1] * bm >= s.args["M"]
+    # split-K launches are followed by their reduction, which applies the epilogue
+    for i, s in enumerate(p.steps):
+        if s.kind == "gemm" and s.args["ksplit"] > 1 and not s.params.get("reduce"):
+            assert p.steps[i + 1].kernel.startswith("k_gemm_reduce_")
+            assert p.steps[i + 1].args["part"] == s.args["part"]
 
 
 def test_rmsnorm_pattern_alone_is_one_kernel():
-    p = compile_subgraph(build_mlp_ir(128))
+    p = compile_subgraph(build_mlp_ir(4))
     assert [s.params.get("norm") for s in p.steps if s.kind == "gemv"][0] is True
     eps = [s.args["eps"] for s in p.steps if s.kind == "gemv"][0]
     assert abs(eps - 1e-6) < 1e-12
@@ -101,7 +123,7 @@ def test_arena_live_ranges_never_share_bytes(build, fuse):
 def test_steps_read_only_already_written_arena_storage(fuse):
     p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True), fuse=fuse)
     out_fields = {"dst", "out", "c", "cos_out", "sin_out", "q_out", "k_dst", "v_dst", "part_o", "part_ml",
-                  "scores", "stats", "argmax_slot"}
+                  "scores", "stats", "argmax_slot", "part"}
     written = set()
     for s in p.steps:
         outs = {v.storage for k, v in s.args.items() if k in out_fields and isinstance(v, Ref)}
