@@ -171,13 +171,16 @@ def build_attention_ir(kv_len: int, cfg: QWEN2_5_1_5B.__class__ = QWEN2_5_1_5B) 
     return b.to_dict()
 
 
-def build_decode_ir(max_cache_len: int, cfg: QwenConfig = QWEN2_5_1_5B, argmax: bool = False) -> dict:
-    """cfg3: one full decode step over static caches of length ``max_cache_len``."""
-    b = IRBuilder("Qwen2.5_Decode")
-    ids = b.input("input_ids", [1, 1], "int64")
-    mask = b.input("attention_mask", [1, 1, 1, max_cache_len], cfg.dtype)
-    pos = b.input("position_ids", [1, 1], "int64")
-    cpos = b.input("cache_position", [1], "int64")
+def build_decode_ir(max_cache_len: int, cfg: QwenConfig = QWEN2_5_1_5B, argmax: bool = False,
+                    tokens: int = 1) -> dict:
+    """cfg3: one full decode step over static caches of length ``max_cache_len``; with
+    ``tokens`` > 1 the same graph is a prefill of that many tokens (cfg4: ``tokens`` =
+    ``max_cache_len`` = 512, causal mask [1, 1, T, S] as an input)."""
+    b = IRBuilder("Qwen2.5_Decode" if tokens == 1 else "Qwen2.5_Prefill")
+    ids = b.input("input_ids", [1, tokens], "int64")
+    mask = b.input("attention_mask", [1, 1, tokens, max_cache_len], cfg.dtype)
+    pos = b.input("position_ids", [1, tokens], "int64")
+    cpos = b.input("cache_position", [tokens], "int64")
     caches = []
     for li in range(cfg.layers):
         caches.append((b.input(f"past_key_{li}", [1, cfg.kv_heads, max_cache_len, cfg.head_dim], cfg.dtype),

@@ -90,3 +90,24 @@ def decode_inputs(max_cache_len: int, start_pos: int, cfg: QwenConfig = QWEN2_5_
                                               device=device).to(dt)
             d[f"past_{kind}_{li}"] = t
     return d
+
+
+def prefill_inputs(tokens: int, max_cache_len: int | None = None, cfg: QwenConfig = QWEN2_5_1_5B,
+                   token_seed: int = 2, device: str = "cpu") -> dict[str, torch.Tensor]:
+    """cfg4: ``tokens`` prompt ids ~U[0, vocab) at positions 0..T-1, causal mask [1, 1, T, S]
+    (0 on and below the diagonal, -inf above and past T), empty (zero) static caches of length S."""
+    S = max_cache_len or tokens
+    dt = _TD[cfg.dtype]
+    g = torch.Generator().manual_seed(token_seed)
+    mask = torch.full((tokens, S), float("-inf"))
+    mask[:, :tokens] = torch.triu(torch.full((tokens, tokens), float("-inf")), diagonal=1)
+    d: dict[str, torch.Tensor] = {
+        "input_ids": torch.randint(0, cfg.vocab, (1, tokens), generator=g).to(device),
+        "attention_mask": mask.to(dt).reshape(1, 1, tokens, S).to(device),
+        "position_ids": torch.arange(tokens, dtype=torch.int64).reshape(1, tokens).to(device),
+        "cache_position": torch.arange(tokens, dtype=torch.int64).to(device),
+    }
+    for li in range(cfg.layers):
+        for kind in ("key", "value"):
+            d[f"past_{kind}_{li}"] = torch.zeros((1, cfg.kv_heads, S, cfg.head_dim), dtype=dt, device=device)
+    return d

@@ -368,3 +368,75 @@ def test_full_model_logits_as_close_to_fp32_as_the_cpu_path(backend):
     r_hip, r_cpu = rms(np.concatenate(d_hip)), rms(np.concatenate(d_cpu))
     print(f"cache rows vs fp32 (rms): hip {r_hip:.5f}, cpu fallback {r_cpu:.5f}")
     assert r_hip <= 1.25 * r_cpu + 1e-4
+
+
+def _linear_ir(M, N, K, epi, dtype="bfloat16"):
+    """One linear (+ residual add, or the gate/up SiLU * mul pair) as an IR graph."""
+    from irgen.builder import IRBuilder
+
+    b = IRBuilder("linear")
+    x = b.input("x", [M, K], dtype)
+    w = b.weight("w", [N, K], dtype)
+    bias = b.weight("b", [N], dtype)
+    y = b.op("aten.linear.default", [x, w, bias])
+    if epi == "resid":
+        r = b.input("r", [M, N], dtype)
+        y = b.op("aten.add.Tensor", [r, y])
+    elif epi == "silu":
+        w2 = b.weight("w2", [N, K], dtype)
+        u = b.op("aten.linear.default", [x, w2])
+        y = b.op("aten.mul.Tensor", [b.op("aten.silu.default", [y]), u])
+    b.output(y)
+    return b.to_dict()
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(16, 200, 96, "bias"), (77, 1000, 1536, "resid"), (300, 136, 8960, "resid"),
+                                       (512, 1536, 1536, "bias"), (128, 640, 1536, "silu"), (33, 96, 64, "silu")])
+def test_mfma_gemm_vs_fp32_matmul(backend, M, N, K, epi):
+    """The MFMA GEMM (tiles, split-K, epilogues) against x @ W.T in float32 (test_cuda_executor.py:209-243's
+    closed form), within bf16 rounding of the output, and against the CPU fallback."""
+    ir = _linear_ir(M, N, K, epi)
+    g = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = {"w": (0.05 * torch.randn(N, K, generator=g)).bfloat16(), "b": (0.1 * torch.randn(N, generator=g)).bfloat16()}
+    ins = {"x": x}
+    if epi == "resid":
+        ins["r"] = torch.randn(M, N, generator=g).bfloat16()
+    if epi == "silu":
+        w["w2"] = (0.05 * torch.randn(N, K, generator=g)).bfloat16()
+    got, ex = run_hip(ir, host(ins), host(w), backend)
+    (prog,) = ex.npu_programs.values()
+    assert any(s.kernel.startswith("k_gemm_") for s in prog.steps)
+    ref = run_cpu(ir, host(ins), host(w))
+    (name,) = got
+    close(got[name], ref[name])
+    y = x.float() @ w["w"].float().T + w["b"].float()
+    if epi == "resid":
+        y = ins["r"].float() + y.bfloat16().float()
+    if epi == "silu":
+        gs = y.bfloat16().float()
+        y = (gs * torch.sigmoid(gs)).bfloat16().float() * (x.float() @ w["w2"].float().T).bfloat16().float()
+    close(got[name], y.numpy(), rtol=2e-2)
+
+
+def test_prefill_two_layers_real_dims(backend):
+    """cfg4 shapes (hidden 1536, 12/2 heads, vocab 151936) at T = 128 with 2 layers: logits, greedy
+    tokens and the caches written, vs the CPU fallback."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import make_weights, prefill_inputs
+
+    cfg = QwenConfig(layers=2)
+    T = 128
+    ir = build_decode_ir(T, cfg, argmax=True, tokens=T)
+    w = host(make_weights(ir, cfg, device="cuda"))
+    x = host(prefill_inputs(T, T, cfg))
+    got, ex = run_hip(ir, x, w, backend)
+    assert_all_npu(ex)
+    ref = run_cpu(ir, x, w)
+    logits = ir["graph_outputs"][0]["name"]
+    close(got[logits], ref[logits])
+    tok_g = np.asarray(got["next_token"]).reshape(-1)
+    tok_c = np.asarray(ref["next_token"]).reshape(-1)
+    assert (tok_g == tok_c).mean() >= 0.95
+    for o in ir["graph_outputs"][1:-1]:
+        close(got[o["name"]], ref[o["name"]])
