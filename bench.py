@@ -252,7 +252,12 @@ def main() -> int:
                     help="size of the k_copy calibration launches run after timing (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
+                    help="decode: the headline (cfg3); prefill: 512-token prefill (cfg4), MFMA utilisation")
+    ap.add_argument("--prefill-tokens", type=int, default=512)
     args = ap.parse_args()
+    if args.workload == "prefill" and args.gpus == 1:
+        return main_prefill(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (sharding across "
                                    "GPUs is a design note, not implemented)"}))
@@ -435,6 +440,114 @@ def main() -> int:
         "copy_probe": probe,
         "step_roofline": {"bytes_per_step": sbytes, "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+
+
+def main_prefill(args) -> int:
+    """cfg4: full 28-layer prefill of T tokens (causal mask, empty static caches of length T).
+
+    A step is one prefill; ``value`` is prompt tokens per second. The roofline is MFMA: the
+    GEMM kernels' linear FLOPs (2 M N K per weight) over their measured time, against the
+    dense bf16 peak; the step-level figure divides all linear FLOPs by the step time."""
+    import torch
+
+    from hip_compiler import compile_subgraph, is_hip_op_supported
+    from hip_runtime import HIPBackend
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import make_weights, prefill_inputs
+    from npu_compiler import partition
+    from npu_runtime import DAGExecutor
+
+    cfg = QwenConfig(layers=args.layers)
+    T = args.prefill_tokens
+    steps = args.steps if args.steps != 64 else 10
+    warm = args.warmup if args.warmup != 8 else 2
+    log(f"prefill T={T}: building IR and compiling")
+    t0 = time.time()
+    ir = build_decode_ir(T, cfg, argmax=True, tokens=T)
+    backend = HIPBackend(0)
+    ex = DAGExecutor(partition(ir, is_hip_op_supported), backend, compile_fn=compile_subgraph)
+    compile_s = time.time() - t0
+    weights = make_weights(ir, cfg, device="cuda")
+    ex.load_weights(weights)
+    x0 = prefill_inputs(T, T, cfg, device="cuda")
+    state = {k: backend.allocate_buffer(v) for k, v in x0.items()}
+    (program,) = ex.npu_programs.values()
+    (hexec,) = ex._npu_executors.values()
+    log(f"program: {len(program.steps)} launches, arena {program.arena_bytes / 1e6:.1f} MB")
+    for _ in range(warm):
+        ex.execute(state)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ex.execute(state)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / steps
+    toks = T * steps / elapsed
+    gemms = [i for i, s in enumerate(program.steps) if s.kernel.startswith("k_gemm_") and not s.params.get("reduce")]
+    flops = sum(2.0 * s.args["M"] * s.args["N"] * s.args["K"] * s.params.get("weights", 1)
+                for s in (program.steps[i] for i in gemms))
+    stream = torch.cuda.current_stream().cuda_stream
+    fams: dict[str, list[int]] = {}
+    for i, s in enumerate(program.steps):
+        fams.setdefault(s.kernel, []).append(i)
+    per_kernel = {}
+    gemm_ms = 0.0
+    for kname, idx in sorted(fams.items()):
+        us = time_kernel_subset(hexec, idx, max(1, args.kernel_repeats // 5), stream) * 1e3
+        e = {"launches_per_step": len(idx), "avg_us": round(us, 2)}
+        if kname.startswith("k_gemm_") and "reduce" not in kname:
+            f = sum(2.0 * program.steps[i].args["M"] * program.steps[i].args["N"] * program.steps[i].args["K"]
+                    * program.steps[i].params.get("weights", 1) for i in idx) / len(idx)
+            e["TFLOPs"] = round(f / (us * 1e-6) / 1e12, 1)
+            gemm_ms += us * len(idx) * 1e-3
+        per_kernel[kname] = e
+        log(f"  {kname}: {e}")
+    dom = max((k for k in per_kernel if "TFLOPs" in per_kernel[k]),
+              key=lambda k: per_kernel[k]["avg_us"] * per_kernel[k]["launches_per_step"])
+    dflops = per_kernel[dom]["TFLOPs"]
+    gemm_tf = flops / (gemm_ms * 1e-3) / 1e12
+    step_tf = flops / (ms * 1e-3) / 1e12
+    log(f"{toks:.0f} tok/s, {ms:.2f} ms/prefill; GEMMs {gemm_tf:.0f} TFLOP/s over {gemm_ms:.2f} ms")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from irgen.workloads import to_host
+
+        n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n)
+        cex = DAGExecutor(partition(ir, lambda *_: False), None)
+        cex.load_weights({k: v.detach().cpu() for k, v in weights.items()})
+        ins = {k: to_host(v.detach().cpu()) for k, v in x0.items()}
+        cex.execute(ins)
+        t0 = time.perf_counter()
+        cex.execute(ins)
+        cs = time.perf_counter() - t0
+        cpu = {"value": round(T / cs, 2), "unit": "tok/s", "cores": n, "kind": "port",
+               "sample": f"one {T}-token prefill of the full {cfg.layers}-layer model after one warmup, "
+                         f"DAGExecutor all-CPU plan (ATen bf16, {n} threads): {cs:.2f} s"}
+        log(f"cpu: {cpu}")
+    line = {
+        "metric": "Qwen2.5-1.5B-arch bf16 prefill tok/s @512; MFMA TFLOP/s vs dense bf16 peak",
+        "value": round(toks, 1), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"cfg4: Qwen2.5-1.5B-arch prefill, batch 1, {T} tokens, causal mask, "
+                               "logits for every position, device-side argmax",
+                   "layers": cfg.layers, "launches_per_step": len(program.steps), "compile_s": round(compile_s, 2)},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": dflops, "peak": MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(dflops / MFMA_PEAK_TFLOPS, 4), "traffic": None},
+        "gemm_roofline": {"linear_flops_per_step": flops, "gemm_ms": round(gemm_ms, 3),
+                          "achieved": round(gemm_tf, 1), "frac": round(gemm_tf / MFMA_PEAK_TFLOPS, 4)},
+        "step_roofline": {"achieved": round(step_tf, 1), "unit": "TFLOP/s",
+                          "frac": round(step_tf / MFMA_PEAK_TFLOPS, 4)},
+        "kernels": per_kernel,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

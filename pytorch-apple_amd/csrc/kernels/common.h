@@ -157,7 +157,7 @@ struct LinearArgs {           // out[m, n] = round(x[m, :] . w[n, :] + bias[n]) 
 
 struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M, K], w [N, K], K % 32 == 0
   const void* x;              // [M, K] (row stride ldx), 16-byte aligned rows
-  const void* w;              // [N, K] contiguous
+  const void* w;              // [N, K] (row stride ldw); the _kn kernels take w as [K, N] (row stride ldw)
   const void* w2;             // second weight (SiLU * mul epilogue: w = gate, w2 = up) or null
   const void* bias;           // [N] or null
   const void* bias2;          // [N] or null (for w2)
@@ -166,8 +166,14 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   float* part;                // split-K: fp32 partial sums [ksplit, NW, M, N], reduced by k_gemm_reduce_*
   long long M;
   long long ldx;
+  long long ldw;
   long long ldo;
   long long ldr;
+  long long sx;               // batched: element offsets of batch b: x + b*sx, w + (b / bdiv)*sw, out + b*so
+  long long sw;
+  long long so;
+  int batch;                  // grid.z = batch * ksplit
+  int bdiv;
   int N;
   int K;
   int flags;                  // 1: bias, 2: bias2

@@ -15,6 +15,9 @@
 //   RESID out = round(r + round(acc + b))
 //   SILU  out = round(round(silu(round(acc_g + b_g))) * round(acc_u + b_u))   (NW = 2)
 // Rows past M and columns past N are computed from clamped (valid) addresses and not stored.
+// Batched use (grid.z = batch * ksplit): batch b reads x + b*sx and w + (b / bdiv)*sw (the
+// GQA head -> KV head map) and writes out + b*so. The _kn kernels take w as [K, N]
+// (N-contiguous, e.g. V in P.V) and transpose it while staging into LDS.
 #include "common.h"
 
 typedef __attribute__((ext_vector_type(8))) __bf16 gm_bf16x8;
@@ -51,7 +54,7 @@ __device__ __forceinline__ uint16_t gm_pack(float f) {
   return DT == HS_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
 }
 
-template <int DT, int EPI, int NW, int BM, int BN>
+template <int DT, int EPI, int NW, int BM, int BN, bool KN = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr int BNT = BN * NW;            // weight rows staged per step (BN columns per weight)
   constexpr int TI = BM / 64;             // 32-row MFMA tiles per wave
@@ -64,8 +67,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const int wr = wave >> 1, wc = wave & 1;
   const long long m_base = (long long)blockIdx.y * BM;
   const int n_base = blockIdx.x * BN;
-  const uint16_t* X = (const uint16_t*)a.x;
-  const uint16_t* W[2] = {(const uint16_t*)a.w, (const uint16_t*)(NW == 2 ? a.w2 : a.w)};
+  const int bz = blockIdx.z / a.ksplit, kz = blockIdx.z % a.ksplit;   // batch, K split
+  const uint16_t* X = (const uint16_t*)a.x + bz * a.sx;
+  const long long wofs = (long long)(bz / a.bdiv) * a.sw;
+  const uint16_t* W[2] = {(const uint16_t*)a.w + wofs, (const uint16_t*)(NW == 2 ? a.w2 : a.w) + wofs};
+  uint16_t* OUT = (uint16_t*)a.out + bz * a.so;
 
   // global -> register staging of one K step
   uint4 ra[A_LD], rb[B_LD];
@@ -78,9 +84,16 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
-      const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
-      rb[i] = *(const uint4*)(W[u] + (long long)n * a.K + k0 + col);
+      const int c = tid + 256 * i;
+      if constexpr (KN) {   // w is [K, N]: 16-byte chunks along n, BNT / 8 chunks per k row (NW == 1)
+        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;
+        const int n = min(n_base + nc, a.N - 8);
+        rb[i] = *(const uint4*)(W[0] + (long long)(k0 + kr) * a.ldw + n);
+      } else {
+        const int row = c >> 2, col = (c & 3) * 8;
+        const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
+        rb[i] = *(const uint4*)(W[u] + (long long)n * a.ldw + k0 + col);
+      }
     }
   };
   auto store_step = [&](int buf) {
@@ -91,8 +104,19 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
-      *(uint4*)&Bs[buf][row][col] = rb[i];
+      const int c = tid + 256 * i;
+      if constexpr (KN) {   // transpose into the [n][k] layout the fragments are read from
+        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;
+        const uint32_t q[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          Bs[buf][nc + 2 * j][kr] = (uint16_t)(q[j] & 0xffffu);
+          Bs[buf][nc + 2 * j + 1][kr] = (uint16_t)(q[j] >> 16);
+        }
+      } else {
+        const int row = c >> 2, col = (c & 3) * 8;
+        *(uint4*)&Bs[buf][row][col] = rb[i];
+      }
     }
   };
 
@@ -107,11 +131,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         for (int e = 0; e < 16; ++e) acc[u][i][j][e] = 0.f;
 
   // split K: workgroup z covers [z * kchunk, (z + 1) * kchunk)
-  const int kbeg = blockIdx.z * a.kchunk;
+  const int kbeg = kz * a.kchunk;
   const int nsteps = min(a.kchunk, a.K - kbeg) / GM_BK;
   X += kbeg;
-  W[0] += kbeg;
-  W[1] += kbeg;
+  if constexpr (KN) {
+    W[0] += (long long)kbeg * a.ldw;
+  } else {
+    W[0] += kbeg;
+    W[1] += kbeg;
+  }
   load_step(0);
   store_step(0);
   __syncthreads();
@@ -152,7 +180,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-            if (m < a.M) a.part[(((long long)blockIdx.z * NW + u) * a.M + m) * a.N + n] = acc[u][i][j][e];
+            if (m < a.M) a.part[(((long long)kz * NW + u) * a.M + m) * a.N + n] = acc[u][i][j][e];
           }
       }
     return;
@@ -177,7 +205,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
           const float sg = gm_round<DT>(v / (1.f + expf(-v)));
           v = gm_round<DT>(sg * up);
         }
-        ((uint16_t*)a.out)[m * a.ldo + n] = gm_pack<DT>(v);
+        OUT[m * a.ldo + n] = gm_pack<DT>(v);
       }
     }
   }
@@ -210,6 +238,10 @@ __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
 
 #define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); }
+#define GEMM_KERNEL_KN(NAME, DT, BM, BN) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { \
+    gemm_body<DT, GE_BIAS, 1, BM, BN, true>(a);                             \
+  }
 #define GEMM_REDUCE(NAME, DT, EPI) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_reduce_body<DT, EPI>(a); }
 
@@ -233,3 +265,8 @@ GEMM_REDUCE(k_gemm_reduce_bf16_resid, HS_BF16, GE_RESID)
 GEMM_REDUCE(k_gemm_reduce_bf16_silu, HS_BF16, GE_SILU)
 GEMM_REDUCE(k_gemm_reduce_f16_bias, HS_F16, GE_BIAS)
 GEMM_REDUCE(k_gemm_reduce_f16_resid, HS_F16, GE_RESID)
+// batched matmuls (attention at prefill): B given as [K, N] (row-major, N % 8 == 0)
+GEMM_KERNEL_KN(k_gemm_bf16_bias_m64n64_kn, HS_BF16, 64, 64)
+GEMM_KERNEL_KN(k_gemm_bf16_bias_m128n128_kn, HS_BF16, 128, 128)
+GEMM_KERNEL_KN(k_gemm_f16_bias_m64n64_kn, HS_F16, 64, 64)
+GEMM_KERNEL_KN(k_gemm_f16_bias_m128n128_kn, HS_F16, 128, 128)

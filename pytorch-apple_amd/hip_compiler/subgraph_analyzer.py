@@ -489,7 +489,8 @@ class Lowering:
         part = self.scratch(out_name + ".kpart", ksplit * nw * M * N * 4) if ksplit > 1 else None
         args = dict(x=self.ref(x), w=self.ref(w), w2=self.ref(wv2) if wv2 else None,
                     bias=self.ref(bias) if bias else None, bias2=self.ref(bv2) if bv2 else None,
-                    resid=self.ref(r) if r else None, out=self.ref(o), part=part, M=M, ldx=K, ldo=N, ldr=N,
+                    resid=self.ref(r) if r else None, out=self.ref(o), part=part, M=M, ldx=K, ldw=K, ldo=N, ldr=N,
+                    sx=0, sw=0, so=0, batch=1, bdiv=1,
                     N=N, K=K, flags=(1 if bias else 0) | (2 if bv2 else 0), ksplit=ksplit, kchunk=kchunk, nw=nw)
         ins = [x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t]
         params = {"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None, "weights": nw,
@@ -603,8 +604,65 @@ class Lowering:
         if sq_b:
             full = full + (1,)
         o = self.new_storage(out.name, full, out.dtype)
+        if not (sq_a or sq_b) and self.emit_batched_gemm(a, b, o, [t.name for t in node.inputs], [out.name]):
+            self.views[out.name] = V.restride(o, out.shape)
+            return
         self.emit_bmm(a, b, o, [t.name for t in node.inputs], [out.name])
         self.views[out.name] = V.restride(o, out.shape)
+
+    @staticmethod
+    def _linear_batch_stride(shape, strides) -> int | None:
+        """s such that the batch element with flat index b starts at b * s, or None."""
+        s, span = None, 1
+        for n, st in zip(reversed(shape), reversed(strides)):
+            if n > 1:
+                if s is None:
+                    s = st // span if span else 0
+                    if s * span != st:
+                        return None
+                elif st != s * span:
+                    return None
+            span *= n
+        return s or 0
+
+    def emit_batched_gemm(self, a: TView, b: TView, c: TView, ins: list[str], outs: list[str]) -> bool:
+        """Batched c = a @ b on the MFMA GEMM when the layout allows it (bf16/fp16, K % 32 == 0,
+        K-contiguous a, b either [N, K]- or [K, N]-contiguous, batch offsets linear in the flat
+        batch index); returns False to leave the matmul to the generic kernel."""
+        M, K, N = a.shape[-2], a.shape[-1], b.shape[-1]
+        dt = c.dtype
+        if not (a.dtype == b.dtype == dt and dt in ("bfloat16", "float16") and K % 32 == 0 and M * N >= 4096):
+            return False
+        if a.strides[-1] != 1 or a.strides[-2] % 8 or (a.offset * 2) % 16 or (b.offset * 2) % 16:
+            return False
+        if b.strides[-2] == 1 and b.strides[-1] % 8 == 0:
+            kn, ldw = False, b.strides[-1]
+        elif b.strides[-1] == 1 and b.strides[-2] % 8 == 0 and N % 8 == 0:
+            kn, ldw = True, b.strides[-2]
+        else:
+            return False
+        batch = tuple(c.shape[:-2])
+        nb = numel(batch)
+        ab = V.broadcast_to(a.with_(shape=a.shape[:-2], strides=a.strides[:-2]), batch) if batch else None
+        bb = V.broadcast_to(b.with_(shape=b.shape[:-2], strides=b.strides[:-2]), batch) if batch else None
+        sx = self._linear_batch_stride(batch, ab.strides) if batch else 0
+        sw = self._linear_batch_stride(batch, bb.strides) if batch else 0
+        if sx is None or sw is None or sx % 8 or sw % 8:
+            return False
+        tiles = [(128, 128), (64, 64)]
+        for bm, bn in tiles:
+            if ((M + bm - 1) // bm) * ((N + bn - 1) // bn) * nb >= GEMM_TARGET_WGS:
+                break
+        name = f"k_gemm_{'bf16' if dt == 'bfloat16' else 'f16'}_bias_m{bm}n{bn}" + ("_kn" if kn else "")
+        args = dict(x=self.ref(a), w=self.ref(b), w2=None, bias=None, bias2=None, resid=None, out=self.ref(c),
+                    part=None, M=M, ldx=a.strides[-2], ldw=ldw, ldo=N, ldr=N, sx=sx, sw=sw, so=M * N, batch=nb,
+                    bdiv=1, N=N, K=K, flags=0, ksplit=1, kchunk=K, nw=1)
+        self.emit(LaunchStep(
+            kind="gemm", kernel=name, module="gemm", arg_struct="GemmArgs", args=args,
+            grid=((N + bn - 1) // bn, (M + bm - 1) // bm, nb), inputs=ins, outputs=outs,
+            params={"M": M, "N": N, "K": K, "batch": nb, "epilogue": "bias", "weights": 1, "mfma": True,
+                    "tile": (bm, bn), "ksplit": 1, "b_layout": "kn" if kn else "nk"}))
+        return True
 
     def lower_addmm(self, node: OpNode) -> None:
         bias, m1, m2 = (t.name for t in node.inputs[:3])

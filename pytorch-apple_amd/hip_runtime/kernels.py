@@ -55,8 +55,9 @@ _struct("LinearArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P)
                        ("ldo", LL), ("ldr", LL), ("N", I), ("K", I), ("dtype", I), ("has_bias", I),
                        ("has_resid", I), ("pad", I)])
 _struct("GemmArgs", [("x", P), ("w", P), ("w2", P), ("bias", P), ("bias2", P), ("resid", P), ("out", P),
-                     ("part", P), ("M", LL), ("ldx", LL), ("ldo", LL), ("ldr", LL), ("N", I), ("K", I),
-                     ("flags", I), ("ksplit", I), ("kchunk", I), ("nw", I)])
+                     ("part", P), ("M", LL), ("ldx", LL), ("ldw", LL), ("ldo", LL), ("ldr", LL), ("sx", LL),
+                     ("sw", LL), ("so", LL), ("batch", I), ("bdiv", I), ("N", I), ("K", I), ("flags", I),
+                     ("ksplit", I), ("kchunk", I), ("nw", I)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])
 _struct("GemvArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P), ("w2", P), ("bias2", P),
                      ("norm_w", P), ("argmax_slot", P), ("attn_o", P), ("attn_ml", P), ("M", LL), ("ldx", LL),

@@ -440,3 +440,32 @@ def test_prefill_two_layers_real_dims(backend):
     assert (tok_g == tok_c).mean() >= 0.95
     for o in ir["graph_outputs"][1:-1]:
         close(got[o["name"]], ref[o["name"]])
+
+
+@pytest.mark.parametrize("transposed_b", [False, True])
+def test_batched_matmul_on_mfma(backend, transposed_b):
+    """matmul over [2, 3] batches (attention-shaped) on the MFMA GEMM, b given as [K, N] or as the
+    transpose of an [N, K] tensor, vs float32 torch.matmul."""
+    from irgen.builder import IRBuilder
+
+    B0, B1, M, K, N = 2, 3, 96, 64, 80
+    b_ = IRBuilder("bmm")
+    a = b_.input("a", [B0, B1, M, K], "bfloat16")
+    if transposed_b:
+        bt = b_.input("b", [B0, B1, N, K], "bfloat16")
+        bb = b_.op("aten.transpose.int", [bt], {"dim0": 2, "dim1": 3})
+    else:
+        bb = b_.input("b", [B0, B1, K, N], "bfloat16")
+    b_.output(b_.op("aten.matmul.default", [a, bb]))
+    ir = b_.to_dict()
+    g = torch.Generator().manual_seed(5)
+    ta = torch.randn(B0, B1, M, K, generator=g).bfloat16()
+    tb = torch.randn(B0, B1, N, K, generator=g).bfloat16() if transposed_b else \
+        torch.randn(B0, B1, K, N, generator=g).bfloat16()
+    got, ex = run_hip(ir, host({"a": ta, "b": tb}), {}, backend)
+    (prog,) = ex.npu_programs.values()
+    assert [s.kernel for s in prog.steps if s.kind == "gemm"] == \
+        ["k_gemm_bf16_bias_m64n64" + ("" if transposed_b else "_kn")]
+    ref = ta.float() @ (tb.float().transpose(2, 3) if transposed_b else tb.float())
+    (name,) = got
+    close(got[name], ref.numpy())
