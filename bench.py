@@ -492,8 +492,10 @@ def main_prefill(args) -> int:
     ms = elapsed * 1e3 / steps
     toks = T * steps / elapsed
     gemms = [i for i, s in enumerate(program.steps) if s.kernel.startswith("k_gemm_") and not s.params.get("reduce")]
-    flops = sum(2.0 * s.args["M"] * s.args["N"] * s.args["K"] * s.params.get("weights", 1)
-                for s in (program.steps[i] for i in gemms))
+    def gflops(st):
+        return 2.0 * st.args["M"] * st.args["N"] * st.args["K"] * st.params.get("weights", 1) * st.args.get("batch", 1)
+
+    flops = sum(gflops(program.steps[i]) for i in gemms)
     stream = torch.cuda.current_stream().cuda_stream
     fams: dict[str, list[int]] = {}
     for i, s in enumerate(program.steps):
@@ -504,8 +506,7 @@ def main_prefill(args) -> int:
         us = time_kernel_subset(hexec, idx, max(1, args.kernel_repeats // 5), stream) * 1e3
         e = {"launches_per_step": len(idx), "avg_us": round(us, 2)}
         if kname.startswith("k_gemm_") and "reduce" not in kname:
-            f = sum(2.0 * program.steps[i].args["M"] * program.steps[i].args["N"] * program.steps[i].args["K"]
-                    * program.steps[i].params.get("weights", 1) for i in idx) / len(idx)
+            f = sum(gflops(program.steps[i]) for i in idx) / len(idx)
             e["TFLOPs"] = round(f / (us * 1e-6) / 1e12, 1)
             gemm_ms += us * len(idx) * 1e-3
         per_kernel[kname] = e

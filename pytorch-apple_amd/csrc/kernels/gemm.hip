@@ -70,55 +70,55 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const int bz = blockIdx.z / a.ksplit, kz = blockIdx.z % a.ksplit;   // batch, K split
   const uint16_t* X = (const uint16_t*)a.x + bz * a.sx;
   const long long wofs = (long long)(bz / a.bdiv) * a.sw;
-  const uint16_t* W[2] = {(const uint16_t*)a.w + wofs, (const uint16_t*)(NW == 2 ? a.w2 : a.w) + wofs};
+  // two named pointers (a runtime-indexed pointer array would live in scratch memory)
+  const uint16_t* W0 = (const uint16_t*)a.w + wofs;
+  const uint16_t* W1 = (const uint16_t*)(NW == 2 ? a.w2 : a.w) + wofs;
   uint16_t* OUT = (uint16_t*)a.out + bz * a.so;
 
-  // global -> register staging of one K step
+  // global -> register staging of one K step, and register -> LDS (plain loops on local
+  // arrays: lambdas capturing the arrays by reference put them in scratch memory)
   uint4 ra[A_LD], rb[B_LD];
-  auto load_step = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
-      const long long m = min(m_base + row, a.M - 1);
-      ra[i] = *(const uint4*)(X + m * a.ldx + k0 + col);
-    }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-      const int c = tid + 256 * i;
-      if constexpr (KN) {   // w is [K, N]: 16-byte chunks along n, BNT / 8 chunks per k row (NW == 1)
-        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;
-        const int n = min(n_base + nc, a.N - 8);
-        rb[i] = *(const uint4*)(W[0] + (long long)(k0 + kr) * a.ldw + n);
-      } else {
-        const int row = c >> 2, col = (c & 3) * 8;
-        const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
-        rb[i] = *(const uint4*)(W[u] + (long long)n * a.ldw + k0 + col);
-      }
-    }
-  };
-  auto store_step = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
-      *(uint4*)&As[buf][row][col] = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-      const int c = tid + 256 * i;
-      if constexpr (KN) {   // transpose into the [n][k] layout the fragments are read from
-        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;
-        const uint32_t q[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          Bs[buf][nc + 2 * j][kr] = (uint16_t)(q[j] & 0xffffu);
-          Bs[buf][nc + 2 * j + 1][kr] = (uint16_t)(q[j] >> 16);
-        }
-      } else {
-        const int row = c >> 2, col = (c & 3) * 8;
-        *(uint4*)&Bs[buf][row][col] = rb[i];
-      }
-    }
-  };
+#define GM_LOAD_STEP(k0)                                                                  \
+  do {                                                                                    \
+    _Pragma("unroll") for (int i = 0; i < A_LD; ++i) {                                    \
+      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;                       \
+      const long long m = min(m_base + row, a.M - 1);                                     \
+      ra[i] = *(const uint4*)(X + m * a.ldx + (k0) + col);                                \
+    }                                                                                     \
+    _Pragma("unroll") for (int i = 0; i < B_LD; ++i) {                                    \
+      const int c = tid + 256 * i;                                                        \
+      if constexpr (KN) {                                                                 \
+        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;                           \
+        const int n = min(n_base + nc, a.N - 8);                                          \
+        rb[i] = *(const uint4*)(W0 + (long long)((k0) + kr) * a.ldw + n);                 \
+      } else {                                                                            \
+        const int row = c >> 2, col = (c & 3) * 8;                                        \
+        const int u = row / BN, n = min(n_base + row % BN, a.N - 1);                      \
+        rb[i] = *(const uint4*)((u == 0 ? W0 : W1) + (long long)n * a.ldw + (k0) + col);  \
+      }                                                                                   \
+    }                                                                                     \
+  } while (0)
+#define GM_STORE_STEP(buf)                                                                \
+  do {                                                                                    \
+    _Pragma("unroll") for (int i = 0; i < A_LD; ++i) {                                    \
+      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;                       \
+      *(uint4*)&As[buf][row][col] = ra[i];                                                \
+    }                                                                                     \
+    _Pragma("unroll") for (int i = 0; i < B_LD; ++i) {                                    \
+      const int c = tid + 256 * i;                                                        \
+      if constexpr (KN) { /* transpose into the [n][k] layout the fragments are read from */ \
+        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;                           \
+        const uint32_t q[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};                       \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                   \
+          Bs[buf][nc + 2 * j][kr] = (uint16_t)(q[j] & 0xffffu);                           \
+          Bs[buf][nc + 2 * j + 1][kr] = (uint16_t)(q[j] >> 16);                           \
+        }                                                                                 \
+      } else {                                                                            \
+        const int row = c >> 2, col = (c & 3) * 8;                                        \
+        *(uint4*)&Bs[buf][row][col] = rb[i];                                              \
+      }                                                                                   \
+    }                                                                                     \
+  } while (0)
 
   gm_f32x16 acc[NW][TI][TJ];
 #pragma unroll
@@ -135,18 +135,18 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const int nsteps = min(a.kchunk, a.K - kbeg) / GM_BK;
   X += kbeg;
   if constexpr (KN) {
-    W[0] += (long long)kbeg * a.ldw;
+    W0 += (long long)kbeg * a.ldw;
   } else {
-    W[0] += kbeg;
-    W[1] += kbeg;
+    W0 += kbeg;
+    W1 += kbeg;
   }
-  load_step(0);
-  store_step(0);
+  GM_LOAD_STEP(0);
+  GM_STORE_STEP(0);
   __syncthreads();
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // fragment row/column and k offset of this lane
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
-    if (s + 1 < nsteps) load_step((s + 1) * GM_BK);
+    if (s + 1 < nsteps) GM_LOAD_STEP((s + 1) * GM_BK);
 #pragma unroll
     for (int ks = 0; ks < GM_BK / 16; ++ks) {
       uint4 af[TI], bfr[NW][TJ];
@@ -164,7 +164,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 #pragma unroll
           for (int j = 0; j < TJ; ++j) acc[u][i][j] = gm_mfma<DT>(af[i], bfr[u][j], acc[u][i][j]);
     }
-    if (s + 1 < nsteps) store_step(buf ^ 1);
+    if (s + 1 < nsteps) GM_STORE_STEP(buf ^ 1);
     __syncthreads();
   }
 
@@ -211,6 +211,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   }
 }
 
+#undef GM_LOAD_STEP
+#undef GM_STORE_STEP
+
 // Split-K reduction and epilogue: one thread per output element (fixed summation order).
 template <int DT, int EPI>
 __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
@@ -236,12 +239,13 @@ __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
   }
 }
 
+// up to 2 waves per SIMD: the 64 accumulator registers plus staging and fragments need
+// more than the default register budget, which would otherwise spill the staging to scratch
+#define GM_ATTRS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
 #define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN) \
-  extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); }
+  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); }
 #define GEMM_KERNEL_KN(NAME, DT, BM, BN) \
-  extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { \
-    gemm_body<DT, GE_BIAS, 1, BM, BN, true>(a);                             \
-  }
+  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, true>(a); }
 #define GEMM_REDUCE(NAME, DT, EPI) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_reduce_body<DT, EPI>(a); }
 
