@@ -182,6 +182,47 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   int nw;                     // weights (1, or 2 for SiLU * mul); read by the reduce kernel
 };
 
+struct ConvArgs {             // implicit-GEMM conv2d (conv.hip), NCHW activations, OIHW weights, groups 1
+  const void* x;              // [N, Cin, H, W]
+  const void* w;              // [Cout, Cin, KH, KW]
+  const void* bias;           // [Cout] or null
+  const void* bn_w;           // batch-norm (inference) of the conv output: weight, bias, running stats [Cout]
+  const void* bn_b;
+  const void* bn_mean;
+  const void* bn_var;
+  const void* resid;          // [N, Cout, Ho, Wo] added after the batch norm, or null
+  void* out;                  // [N, Cout, Ho, Wo]
+  long long M;                // N * Ho * Wo
+  int N, Cin, H, W, Cout, Ho, Wo, KH, KW, sh, sw, ph, pw;
+  int K;                      // Cin * KH * KW
+  float eps;
+  int flags;                  // 1 bias, 2 batch norm, 4 residual add, 8 ReLU
+};
+
+struct PoolArgs {             // NCHW max pooling (pool.hip)
+  const void* x;
+  void* out;
+  long long planes;           // N * C
+  int H, W, Ho, Wo, kh, kw, sh, sw, ph, pw;
+  int dtype;
+  int pad;
+};
+
+struct BatchNormArgs {        // inference batch norm over NCHW (channel = dim 1), optional ReLU
+  const void* x;
+  const void* w;
+  const void* b;
+  const void* mean;
+  const void* var;
+  void* out;
+  long long n;                // N * C * HW
+  long long hw;
+  int C;
+  float eps;
+  int dtype;
+  int relu;
+};
+
 struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm, epilogues bias/resid/silu/argmax
   const void* x;              // [M, K] bf16 activations (raw residual stream when NORM)
   const void* w;              // [N, K] bf16

@@ -1,0 +1,236 @@
+// conv2d as an implicit GEMM on MFMA (gfx950 v_mfma_f32_32x32x16_{f16,bf16}), NCHW / OIHW.
+//
+//   C[m, co] = sum_k A[m, k] B[co, k]   m = (n, ho, wo), k = (ci, kh, kw), K = Cin*KH*KW
+//   A[m, k]  = x[n, ci, ho*sh - ph + kh, wo*sw - pw + kw]   (0 outside the image)
+//   B[co, k] = w[co, ci, kh, kw]                            (OIHW rows are K-contiguous)
+// Workgroup tile 128 pixels x 128 output channels, K step 32, 256 threads as 2 x 2 waves
+// of 64 x 64 (the same fragment layout as gemm.hip). A is gathered straight from the
+// NCHW activations: thread t owns pixel t % 128 and 16 consecutive k of the step, so a
+// wave's loads for one k walk 64 neighbouring pixels (contiguous for stride 1); the k ->
+// (ci, kh, kw) decomposition is advanced incrementally, not divided per element. B rows
+// are read with 16-byte loads when K % 8 == 0 (every conv but a 3-channel stem).
+// Epilogue per (pixel, channel), the CPU path's rounding points:
+//   v = round(acc (+ bias));  batch norm: v = round(v * a_c + b_c), a_c = w_c / sqrt(var_c + eps),
+//   b_c = bias_c - mean_c * a_c;  residual: v = round(v + r);  ReLU: v = max(v, 0).
+#include "common.h"
+
+typedef __attribute__((ext_vector_type(8))) __bf16 cv_bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 cv_f16x8;
+typedef __attribute__((ext_vector_type(16))) float cv_f32x16;
+
+#define CV_BM 128
+#define CV_BN 128
+#define CV_BK 32
+#define CV_LDS_K 40
+
+template <int DT>
+__device__ __forceinline__ cv_f32x16 cv_mfma(const uint4 a, const uint4 b, cv_f32x16 c) {
+  if constexpr (DT == HS_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(cv_bf16x8, a), __builtin_bit_cast(cv_bf16x8, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(cv_f16x8, a), __builtin_bit_cast(cv_f16x8, b),
+                                                  c, 0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float cv_f(uint16_t h) {
+  return DT == HS_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+}
+template <int DT>
+__device__ __forceinline__ uint16_t cv_h(float f) {
+  return DT == HS_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
+}
+template <int DT>
+__device__ __forceinline__ float cv_round(float f) {
+  return cv_f<DT>(cv_h<DT>(f));
+}
+
+template <int DT, bool BVEC>
+__device__ __forceinline__ void conv_body(const ConvArgs& a) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][CV_BM][CV_LDS_K];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][CV_BN][CV_LDS_K];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const long long m_base = (long long)blockIdx.y * CV_BM;
+  const int n_base = blockIdx.x * CV_BN;
+  const uint16_t* X = (const uint16_t*)a.x;
+  const uint16_t* Wt = (const uint16_t*)a.w;
+  const int HW = a.H * a.W, KHW = a.KH * a.KW;
+
+  // this thread's A pixel and k range within a step
+  const int am = tid & (CV_BM - 1), akg = tid >> 7;   // akg: which 16 of the 32 k
+  const long long mg = m_base + am;
+  const bool mvalid = mg < a.M;
+  const int HoWo = a.Ho * a.Wo;
+  const long long mn = mvalid ? mg / HoWo : 0;
+  const int mp = mvalid ? (int)(mg - mn * HoWo) : 0;
+  const int hi0 = (mp / a.Wo) * a.sh - a.ph, wi0 = (mp % a.Wo) * a.sw - a.pw;
+  const uint16_t* Xn = X + mn * (long long)a.Cin * HW;
+
+  uint32_t ra[8];    // 16 gathered A values, packed in pairs
+  uint4 rb[2];       // B: 2 x 16 bytes (BVEC) ...
+  uint32_t rbs[16];  // ... or 16 gathered values packed in pairs
+  auto load_a = [&](int k0, uint32_t (&dst)[8]) {
+    int k = k0 + akg * 16;
+    int ci = k / KHW, r = k - ci * KHW, kh = r / a.KW, kw = r - kh * a.KW;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      uint16_t v = 0;
+      const int hi = hi0 + kh, wi = wi0 + kw;
+      if (mvalid && k < a.K && hi >= 0 && hi < a.H && wi >= 0 && wi < a.W) v = Xn[(long long)ci * HW + hi * a.W + wi];
+      if (j & 1) dst[j >> 1] |= (uint32_t)v << 16;
+      else dst[j >> 1] = v;
+      ++k;
+      if (++kw == a.KW) {
+        kw = 0;
+        if (++kh == a.KH) { kh = 0; ++ci; }
+      }
+    }
+  };
+  // B staging: thread t -> channel row (t >> 2) and (t >> 2) + 64, 8 consecutive k at (t & 3) * 8
+  auto load_b = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = (tid >> 2) + 64 * i, col = (tid & 3) * 8;
+      const int co = min(n_base + row, a.Cout - 1);
+      const int k = k0 + col;
+      if constexpr (BVEC) {
+        rb[i] = k < a.K ? *(const uint4*)(Wt + (long long)co * a.K + k) : make_uint4(0, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const uint16_t lo = (k + j < a.K) ? Wt[(long long)co * a.K + k + j] : 0;
+          const uint16_t hi = (k + j + 1 < a.K) ? Wt[(long long)co * a.K + k + j + 1] : 0;
+          rbs[i * 4 + j / 2] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+      }
+    }
+  };
+  auto store = [&](int buf) {
+    *(uint4*)&As[buf][am][akg * 16] = make_uint4(ra[0], ra[1], ra[2], ra[3]);
+    *(uint4*)&As[buf][am][akg * 16 + 8] = make_uint4(ra[4], ra[5], ra[6], ra[7]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = (tid >> 2) + 64 * i, col = (tid & 3) * 8;
+      if constexpr (BVEC) *(uint4*)&Bs[buf][row][col] = rb[i];
+      else *(uint4*)&Bs[buf][row][col] = make_uint4(rbs[i * 4], rbs[i * 4 + 1], rbs[i * 4 + 2], rbs[i * 4 + 3]);
+    }
+  };
+
+  cv_f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nsteps = (a.K + CV_BK - 1) / CV_BK;
+  load_a(0, ra);
+  load_b(0);
+  store(0);
+  __syncthreads();
+  const int fr = lane & 31, fk = (lane >> 5) * 8;
+  for (int s = 0; s < nsteps; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nsteps) {
+      load_a((s + 1) * CV_BK, ra);
+      load_b((s + 1) * CV_BK);
+    }
+#pragma unroll
+    for (int ks = 0; ks < CV_BK / 16; ++ks) {
+      uint4 af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const uint4*)&As[buf][wr * 64 + i * 32 + fr][ks * 16 + fk];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bfr[j] = *(const uint4*)&Bs[buf][wc * 64 + j * 32 + fr][ks * 16 + fk];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = cv_mfma<DT>(af[i], bfr[j], acc[i][j]);
+    }
+    if (s + 1 < nsteps) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int co = n_base + wc * 64 + j * 32 + fr;
+    if (co >= a.Cout) continue;
+    const float bias = (a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[co]) : 0.f;
+    float al = 1.f, be = 0.f;
+    if (a.flags & 2) {
+      const float g = cv_f<DT>(((const uint16_t*)a.bn_w)[co]), bb = cv_f<DT>(((const uint16_t*)a.bn_b)[co]);
+      const float mu = cv_f<DT>(((const uint16_t*)a.bn_mean)[co]), var = cv_f<DT>(((const uint16_t*)a.bn_var)[co]);
+      al = g / sqrtf(var + a.eps);
+      be = bb - mu * al;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const long long m = m_base + wr * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        if (m >= a.M) continue;
+        const long long n = m / HoWo;
+        const long long o = (n * a.Cout + co) * HoWo + (m - n * HoWo);
+        float v = cv_round<DT>(acc[i][j][e] + bias);
+        if (a.flags & 2) v = cv_round<DT>(v * al + be);
+        if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
+        if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
+        ((uint16_t*)a.out)[o] = cv_h<DT>(v);
+      }
+    }
+  }
+}
+
+#define CV_ATTRS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+extern "C" __global__ void CV_ATTRS k_conv_f16(const ConvArgs a) { conv_body<HS_F16, true>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_f16_g(const ConvArgs a) { conv_body<HS_F16, false>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_bf16(const ConvArgs a) { conv_body<HS_BF16, true>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_bf16_g(const ConvArgs a) { conv_body<HS_BF16, false>(a); }
+
+// ---------------------------------------------------------------- pooling / batch norm
+
+// max over the window; positions outside the image are skipped (ATen's -inf padding)
+extern "C" __global__ void __launch_bounds__(256) k_maxpool2d(const PoolArgs a) {
+  const long long total = a.planes * a.Ho * a.Wo;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+    const int wo = (int)(i % a.Wo);
+    const int ho = (int)((i / a.Wo) % a.Ho);
+    const long long pl = i / ((long long)a.Wo * a.Ho);
+    const uint16_t* x = (const uint16_t*)a.x + pl * a.H * a.W;
+    float best = -INFINITY;
+    bool nan = false;
+    for (int kh = 0; kh < a.kh; ++kh) {
+      const int hi = ho * a.sh - a.ph + kh;
+      if (hi < 0 || hi >= a.H) continue;
+      for (int kw = 0; kw < a.kw; ++kw) {
+        const int wi = wo * a.sw - a.pw + kw;
+        if (wi < 0 || wi >= a.W) continue;
+        const float v = a.dtype == HS_BF16 ? bf16_to_f32(x[hi * a.W + wi]) : f16_to_f32(x[hi * a.W + wi]);
+        nan |= v != v;
+        best = fmaxf(best, v);
+      }
+    }
+    if (nan) best = NAN;
+    ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(best) : f32_to_f16(best);
+  }
+}
+
+// out = round(x * a_c + b_c) (+ ReLU), a_c = w_c / sqrt(var_c + eps), b_c = bias_c - mean_c * a_c
+extern "C" __global__ void __launch_bounds__(256) k_batchnorm(const BatchNormArgs a) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (long long)gridDim.x * 256) {
+    const int c = (int)((i / a.hw) % a.C);
+    auto f = [&](const void* p, long long j) {
+      const uint16_t h = ((const uint16_t*)p)[j];
+      return a.dtype == HS_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+    };
+    const float al = f(a.w, c) / sqrtf(f(a.var, c) + a.eps);
+    const float be = f(a.b, c) - f(a.mean, c) * al;
+    float v = f(a.x, i) * al + be;
+    if (a.relu) v = v != v ? v : fmaxf(v, 0.f);
+    ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+  }
+}

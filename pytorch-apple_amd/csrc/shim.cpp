@@ -246,6 +246,9 @@ size_t hs_argsize(const char* s) {
   HS_SZ(BmmArgs)
   HS_SZ(LinearArgs)
   HS_SZ(GemmArgs)
+  HS_SZ(ConvArgs)
+  HS_SZ(PoolArgs)
+  HS_SZ(BatchNormArgs)
   HS_SZ(DecodeAttnArgs)
   HS_SZ(FusedArgs)
   HS_SZ(GemvArgs)

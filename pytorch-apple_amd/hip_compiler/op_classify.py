@@ -30,6 +30,10 @@ _TABLE: dict[str, OpCategory] = {
     "aten.addmm.default": OpCategory.ANCHOR_BLAS,
     "aten.mm.default": OpCategory.ANCHOR_BLAS,
     "aten.bmm.default": OpCategory.ANCHOR_BLAS,
+    "aten.conv2d.default": OpCategory.ANCHOR_BLAS,
+    "aten.batch_norm.default": OpCategory.REDUCTION,
+    "aten.max_pool2d.default": OpCategory.REDUCTION,
+    "aten.adaptive_avg_pool2d.default": OpCategory.REDUCTION,
     "aten.softmax.int": OpCategory.REDUCTION,
     "aten._softmax.default": OpCategory.REDUCTION,
     "aten.mean.dim": OpCategory.REDUCTION,

@@ -14,6 +14,9 @@ from hip_compiler.codegen import EW_OPS
 _HIP_SUPPORTED_OPS: set[str] = {
     # GEMM-shaped
     "aten.linear.default", "aten.matmul.default", "aten.addmm.default", "aten.mm.default", "aten.bmm.default",
+    # convolution networks
+    "aten.conv2d.default", "aten.batch_norm.default", "aten.max_pool2d.default",
+    "aten.adaptive_avg_pool2d.default",
     # reductions
     "aten.softmax.int", "aten._softmax.default", "aten.mean.dim", "aten.argmax.default",
     # specials
@@ -34,6 +37,18 @@ def is_hip_op_supported(op_type: str, attrs: dict | None = None) -> bool:
     attrs = attrs or {}
     if op_type == "aten.dropout.default" and attrs.get("train", False) and attrs.get("p", 0.0) != 0.0:
         return False
+    def pair(v, default):
+        v = attrs.get(v, default)
+        return [v, v] if isinstance(v, int) else list(v or default)
+
+    if op_type == "aten.conv2d.default":
+        return int(attrs.get("groups", 1)) == 1 and pair("dilation", [1, 1]) == [1, 1]
+    if op_type == "aten.batch_norm.default":
+        return not attrs.get("training", False)
+    if op_type == "aten.max_pool2d.default":
+        return pair("dilation", [1, 1]) == [1, 1] and not attrs.get("ceil_mode", False)
+    if op_type == "aten.adaptive_avg_pool2d.default":
+        return pair("output_size", [1, 1]) == [1, 1]
     if op_type == "aten.mean.dim":
         dims = attrs.get("dim", [-1])
         if dims is None:

@@ -661,6 +661,42 @@ def _emit_qkv(low, xname, q, k, v, names) -> None:
     low.mutated_inputs.update({kc.storage, vc.storage})
 
 
-DEFAULT_PATTERNS = [decode_attention, rmsnorm, qkv_rope, gate_up_silu, linear_argmax, linear_resid, masked_softmax]
+# ------------------------------------------------------------------ conv + BN (+ add) (+ ReLU)
+
+def conv_bn_act(low) -> None:
+    """``conv2d -> batch_norm [-> add(., r)] [-> relu]`` with private intermediates -> one implicit-GEMM
+    launch whose epilogue applies the inference batch norm, the residual add and the ReLU
+    (the Conv+BN+ReLU and Add+ReLU fusions of the reference's ResNet path)."""
+    cx = _Ctx(low)
+    for conv in low.g.nodes:
+        if conv.op_type != "aten.conv2d.default" or conv.name in low.claimed:
+            continue
+        if len(conv.outputs[0].shape) != 4 or conv.outputs[0].dtype not in ("float16", "bfloat16"):
+            continue
+        bn = cx.only(conv.outputs[0].name, "aten.batch_norm.default")
+        if bn is None or bn.attrs.get("training", False) or not cx.private(conv.outputs[0].name, {bn.name}):
+            continue
+        if bn.inputs[0].name != conv.outputs[0].name or any(t.dtype != conv.outputs[0].dtype for t in bn.inputs[1:5]):
+            continue
+        nodes, tail, resid, relu = [conv, bn], bn.outputs[0], None, False
+        add = cx.only(tail.name, ("aten.add.Tensor",))
+        if (add is not None and len(add.inputs) == 2 and float(add.attrs.get("alpha", 1)) == 1.0
+                and cx.private(tail.name, {add.name})):
+            other = add.inputs[1] if add.inputs[0].name == tail.name else add.inputs[0]
+            if (other.name != tail.name and tuple(other.shape) == tuple(tail.shape) and other.dtype == tail.dtype
+                    and add.outputs[0].dtype == tail.dtype):
+                nodes, tail, resid = nodes + [add], add.outputs[0], other.name
+        r = cx.only(tail.name, ("aten.relu.default", "aten.relu_.default"))
+        if r is not None and cx.private(tail.name, {r.name}):
+            nodes, tail, relu = nodes + [r], r.outputs[0], True
+
+        def emit(conv=conv, bn=bn, resid=resid, relu=relu, out=tail.name, names=[n.name for n in nodes]):
+            low.emit_conv(conv, out, bn=bn, resid=resid, relu=relu, nodes=names)
+
+        cx.claim(nodes, emit)
+
+
+DEFAULT_PATTERNS = [decode_attention, rmsnorm, qkv_rope, gate_up_silu, linear_argmax, linear_resid, masked_softmax,
+                    conv_bn_act]
 
 __all__ = ["DEFAULT_PATTERNS", "rmsnorm", "masked_softmax", "decode_attention", "V"]

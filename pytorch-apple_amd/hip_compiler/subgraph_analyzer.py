@@ -753,6 +753,99 @@ class Lowering:
             grid=(max(rows, 1), 1, 1), inputs=[x.name], outputs=[out.name], params={"rows": rows, "cols": cols}))
         self.views[out.name] = o
 
+    # ------------------------------------------------------------------ convolution network ops
+
+    def emit_conv(self, conv: OpNode, out_name: str, *, bn: OpNode | None = None, resid: str | None = None,
+                  relu: bool = False, nodes: list[str] | None = None) -> None:
+        """conv2d (+ batch norm) (+ residual add) (+ ReLU) as one implicit-GEMM launch (conv.hip)."""
+        x = self.contiguous(conv.inputs[0].name)
+        w = self.contiguous(conv.inputs[1].name)
+        has_bias = len(conv.inputs) > 2
+        N, Cin, H, W = x.shape
+        Cout, _, KH, KW = w.shape
+        out_t = conv.outputs[0]
+        Ho, Wo = out_t.shape[2], out_t.shape[3]
+        st = conv.attrs.get("stride", [1, 1])
+        pd = conv.attrs.get("padding", [0, 0])
+        st = [st, st] if isinstance(st, int) else list(st)
+        pd = [pd, pd] if isinstance(pd, int) else list(pd)
+        K = Cin * KH * KW
+        dt = x.dtype
+        o = self.new_storage(out_name, [N, Cout, Ho, Wo], dt)
+        bnv = [self.contiguous(t.name) for t in bn.inputs[1:5]] if bn is not None else [None] * 4
+        rv = self.contiguous(resid) if resid else None
+        flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
+        vec = K % 8 == 0 and (w.offset * 2) % 16 == 0
+        kname = f"k_conv_{'bf16' if dt == 'bfloat16' else 'f16'}" + ("" if vec else "_g")
+        M = N * Ho * Wo
+        ins = [conv.inputs[0].name, conv.inputs[1].name] + ([conv.inputs[2].name] if has_bias else []) + \
+            ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
+        self.emit(LaunchStep(
+            kind="conv", kernel=kname, module="conv", arg_struct="ConvArgs",
+            args=dict(x=self.ref(x), w=self.ref(w), bias=self.ref(self.contiguous(conv.inputs[2].name)) if has_bias
+                      else None, bn_w=self.ref(bnv[0]) if bn is not None else None,
+                      bn_b=self.ref(bnv[1]) if bn is not None else None,
+                      bn_mean=self.ref(bnv[2]) if bn is not None else None,
+                      bn_var=self.ref(bnv[3]) if bn is not None else None,
+                      resid=self.ref(rv) if rv is not None else None, out=self.ref(o), M=M, N=N, Cin=Cin, H=H, W=W,
+                      Cout=Cout, Ho=Ho, Wo=Wo, KH=KH, KW=KW, sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], K=K,
+                      eps=float(bn.attrs.get("eps", 1e-5)) if bn is not None else 0.0, flags=flags),
+            grid=((Cout + 127) // 128, (M + 127) // 128, 1), inputs=ins, outputs=[out_name],
+            params={"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
+                    "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
+                    "nodes": nodes or [conv.name]}))
+        self.views[out_name] = o
+
+    def lower_conv2d(self, node: OpNode) -> None:
+        self.emit_conv(node, node.outputs[0].name)
+
+    def lower_batch_norm(self, node: OpNode) -> None:
+        x = self.contiguous(node.inputs[0].name)
+        out = node.outputs[0]
+        ps = [self.contiguous(t.name) for t in node.inputs[1:5]]
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        hw = numel(x.shape[2:]) if len(x.shape) > 2 else 1
+        self.emit(LaunchStep(
+            kind="elementwise", kernel="k_batchnorm", module="conv", arg_struct="BatchNormArgs",
+            args=dict(x=self.ref(x), w=self.ref(ps[0]), b=self.ref(ps[1]), mean=self.ref(ps[2]), var=self.ref(ps[3]),
+                      out=self.ref(o), n=x.numel, hw=hw, C=x.shape[1], eps=float(node.attrs.get("eps", 1e-5)),
+                      dtype=DTYPE_CODE[x.dtype], relu=0),
+            grid=grid1d(x.numel), inputs=[t.name for t in node.inputs], outputs=[out.name], params={}))
+        self.views[out.name] = o
+
+    def lower_max_pool2d(self, node: OpNode) -> None:
+        x = self.contiguous(node.inputs[0].name)
+        out = node.outputs[0]
+        ks = node.attrs.get("kernel_size", [2, 2])
+        ks = [ks, ks] if isinstance(ks, int) else list(ks)
+        st = node.attrs.get("stride", None) or ks
+        st = [st, st] if isinstance(st, int) else list(st)
+        pd = node.attrs.get("padding", [0, 0])
+        pd = [pd, pd] if isinstance(pd, int) else list(pd)
+        N, C, H, W = x.shape
+        Ho, Wo = out.shape[2], out.shape[3]
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        self.emit(LaunchStep(
+            kind="reduction", kernel="k_maxpool2d", module="conv", arg_struct="PoolArgs",
+            args=dict(x=self.ref(x), out=self.ref(o), planes=N * C, H=H, W=W, Ho=Ho, Wo=Wo, kh=ks[0], kw=ks[1],
+                      sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], dtype=DTYPE_CODE[x.dtype], pad=0),
+            grid=grid1d(N * C * Ho * Wo), inputs=[node.inputs[0].name], outputs=[out.name], params={}))
+        self.views[out.name] = o
+
+    def lower_adaptive_avg_pool2d(self, node: OpNode) -> None:
+        """Global average pooling (output 1 x 1): the mean over H*W of each (n, c) plane."""
+        x = self.contiguous(node.inputs[0].name)
+        out = node.outputs[0]
+        N, C, H, W = x.shape
+        o = self.new_storage(out.name, out.shape, out.dtype)
+        self.emit(LaunchStep(
+            kind="reduction", kernel="k_mean_last", module="basic", arg_struct="ReduceLastArgs",
+            args=dict(x=self.ref(x), out=self.ref(o), rows=N * C, cols=H * W, x_dtype=DTYPE_CODE[x.dtype],
+                      out_dtype=DTYPE_CODE[out.dtype]),
+            grid=(max(N * C, 1), 1, 1), inputs=[node.inputs[0].name], outputs=[out.name],
+            params={"rows": N * C, "cols": H * W}))
+        self.views[out.name] = o
+
     def lower_argmax(self, node: OpNode) -> None:
         x = node.inputs[0]
         out = node.outputs[0]
@@ -949,6 +1042,10 @@ class Lowering:
             "aten.index_copy.default": self.lower_index_copy,
             "aten.full.default": self.lower_full,
             "aten.cat.default": self.lower_cat,
+            "aten.conv2d.default": self.lower_conv2d,
+            "aten.batch_norm.default": self.lower_batch_norm,
+            "aten.max_pool2d.default": self.lower_max_pool2d,
+            "aten.adaptive_avg_pool2d.default": self.lower_adaptive_avg_pool2d,
         }
         fn = table.get(op)
         if fn is None:

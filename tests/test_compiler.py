@@ -91,7 +91,10 @@ def test_every_decode_op_is_supported_and_partitions_to_one_device_partition():
     assert all(is_hip_op_supported(n["op_type"], n.get("attrs")) for n in ir["nodes"])
     plan = partition(ir, is_hip_op_supported)
     assert len(plan.steps) == 1 and plan.steps[0].target == "npu"
-    assert not is_hip_op_supported("aten.conv2d.default")
+    assert is_hip_op_supported("aten.conv2d.default", {"groups": 1, "dilation": [1, 1]})
+    assert not is_hip_op_supported("aten.conv2d.default", {"groups": 32})       # grouped conv -> CPU
+    assert not is_hip_op_supported("aten.batch_norm.default", {"training": True})
+    assert not is_hip_op_supported("aten.adaptive_avg_pool2d.default", {"output_size": [7, 7]})
     assert not is_hip_op_supported("aten.dropout.default", {"p": 0.1, "train": True})
     assert "aten.index_copy.default" in get_hip_supported_ops()
 
@@ -170,3 +173,16 @@ def test_output_views_are_whole_contiguous_storages():
     for name, v in p.output_views.items():
         st = p.storages[v.storage]
         assert v.offset == 0 and v.is_contiguous() and v.numel * ELEM_SIZE[v.dtype] == st.nbytes
+
+
+def test_resnet50_compiles_to_fused_convs():
+    from irgen.resnet import build_resnet50_ir
+
+    ir = build_resnet50_ir(32, 224)
+    plan = partition(ir, is_hip_op_supported)
+    assert len(plan.steps) == 1 and plan.steps[0].target == "npu"
+    p = compile_subgraph(ir)
+    convs = [s for s in p.steps if s.kind == "conv"]
+    assert len(convs) == 53 and len(p.steps) <= 57          # every BN / add / ReLU folded into a conv
+    assert sum(1 for s in convs if s.args["flags"] & 4) == 16 and all(s.args["flags"] & 2 for s in convs)
+    assert convs[0].kernel.endswith("_g") and convs[0].args["K"] == 147   # 3-channel stem: gathered weights

@@ -469,3 +469,75 @@ def test_batched_matmul_on_mfma(backend, transposed_b):
     ref = ta.float() @ (tb.float().transpose(2, 3) if transposed_b else tb.float())
     (name,) = got
     close(got[name], ref.numpy())
+
+
+def _conv_ir(N, Cin, H, W, Cout, k, stride, pad, bn=True, add=False, relu=True, dtype="float16"):
+    from irgen.builder import IRBuilder
+
+    b = IRBuilder("conv")
+    x = b.input("x", [N, Cin, H, W], dtype)
+    w = b.weight("w", [Cout, Cin, k, k], dtype)
+    y = b.op("aten.conv2d.default", [x, w], {"stride": [stride, stride], "padding": [pad, pad],
+                                             "dilation": [1, 1], "groups": 1})
+    if bn:
+        ps = [b.weight(n, [Cout], dtype) for n in ("g", "beta", "mu", "var")]
+        y = b.op("aten.batch_norm.default", [y] + ps, {"training": False, "momentum": 0.1, "eps": 1e-5,
+                                                       "cudnn_enabled": True})
+    if add:
+        r = b.input("r", list(y.shape), dtype)
+        y = b.op("aten.add.Tensor", [y, r])
+    if relu:
+        y = b.op("aten.relu.default", [y])
+    b.output(y)
+    return b.to_dict()
+
+
+@pytest.mark.parametrize("N,Cin,H,W,Cout,k,stride,pad,add", [
+    (2, 3, 33, 40, 64, 7, 2, 3, False),      # stem shape: K = 147 (gathered weights), odd sizes
+    (3, 64, 14, 14, 256, 1, 1, 0, True),     # 1x1 expand + residual add + ReLU
+    (2, 128, 15, 15, 128, 3, 2, 1, False),   # 3x3 stride 2
+    (1, 256, 7, 9, 200, 1, 2, 0, False),     # strided 1x1 (downsample), Cout not a tile multiple
+])
+def test_conv_bn_act_vs_fp32_conv(backend, N, Cin, H, W, Cout, k, stride, pad, add):
+    """Implicit-GEMM conv (+BN +add +ReLU) vs torch.nn.functional.conv2d in float32 on the same fp16
+    values (the rounding of the conv output before BN is mirrored), and vs the CPU fallback."""
+    ir = _conv_ir(N, Cin, H, W, Cout, k, stride, pad, add=add)
+    g = torch.Generator().manual_seed(Cin + Cout)
+    x = torch.randn(N, Cin, H, W, generator=g).half()
+    w = {"w": ((2.0 / (Cin * k * k)) ** 0.5 * torch.randn(Cout, Cin, k, k, generator=g)).half(),
+         "g": (1 + 0.1 * torch.randn(Cout, generator=g)).half(), "beta": (0.1 * torch.randn(Cout, generator=g)).half(),
+         "mu": (0.1 * torch.randn(Cout, generator=g)).half(), "var": (0.5 + torch.rand(Cout, generator=g)).half()}
+    ins = {"x": x}
+    yshape = [N, Cout, (H + 2 * pad - k) // stride + 1, (W + 2 * pad - k) // stride + 1]
+    if add:
+        ins["r"] = torch.randn(yshape, generator=g).half()
+    got, ex = run_hip(ir, host(ins), host(w), backend)
+    (prog,) = ex.npu_programs.values()
+    assert [s.kind for s in prog.steps] == ["conv"]
+    (name,) = got
+    ref = run_cpu(ir, host(ins), host(w))
+    close(got[name], ref[name])
+    y = torch.nn.functional.conv2d(x.float(), w["w"].float(), stride=stride, padding=pad).half().float()
+    a = w["g"].float() / torch.sqrt(w["var"].float() + 1e-5)
+    y = (y * a[None, :, None, None] + (w["beta"].float() - w["mu"].float() * a)[None, :, None, None]).half().float()
+    if add:
+        y = (y + ins["r"].float()).half().float()
+    close(got[name], torch.relu(y).numpy())
+
+
+def test_resnet50_small_images_top5(backend):
+    """cfg5's network (all 53 convs with BN / add / ReLU fused, max-pool, global pool, fc) at batch 2 on
+    96 x 96 images vs the CPU fallback: logits within 2e-2 and the same top-5 classes."""
+    from irgen.resnet import build_resnet50_ir, resnet_inputs, resnet_weights
+
+    ir = build_resnet50_ir(2, 96)
+    w = host(resnet_weights(ir))
+    x = host(resnet_inputs(2, 96))
+    got, ex = run_hip(ir, x, w, backend)
+    assert_all_npu(ex)
+    ref = run_cpu(ir, x, w)
+    (name,) = got
+    close(got[name], ref[name])
+    g, r = f32(got[name]), f32(ref[name])
+    for i in range(2):
+        assert set(np.argsort(-g[i])[:5]) == set(np.argsort(-r[i])[:5])
