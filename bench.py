@@ -252,12 +252,16 @@ def main() -> int:
                     help="size of the k_copy calibration launches run after timing (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=28)
-    ap.add_argument("--workload", choices=("decode", "prefill"), default="decode",
-                    help="decode: the headline (cfg3); prefill: 512-token prefill (cfg4), MFMA utilisation")
+    ap.add_argument("--workload", choices=("decode", "prefill", "resnet50"), default="decode",
+                    help="decode: the headline (cfg3); prefill: 512-token prefill (cfg4); resnet50: batch-32 "
+                         "ResNet-50 inference (cfg5); the last two report MFMA utilisation")
+    ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--prefill-tokens", type=int, default=512)
     args = ap.parse_args()
     if args.workload == "prefill" and args.gpus == 1:
         return main_prefill(args)
+    if args.workload == "resnet50" and args.gpus == 1:
+        return main_resnet(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (sharding across "
                                    "GPUs is a design note, not implemented)"}))
@@ -547,6 +551,112 @@ def main_prefill(args) -> int:
         "gemm_roofline": {"linear_flops_per_step": flops, "gemm_ms": round(gemm_ms, 3),
                           "achieved": round(gemm_tf, 1), "frac": round(gemm_tf / MFMA_PEAK_TFLOPS, 4)},
         "step_roofline": {"achieved": round(step_tf, 1), "unit": "TFLOP/s",
+                          "frac": round(step_tf / MFMA_PEAK_TFLOPS, 4)},
+        "kernels": per_kernel,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def main_resnet(args) -> int:
+    """cfg5: ResNet-50 inference, fp16, batch 32 at 224 x 224 (He-normal convs, inference batch norm
+    with random running statistics). A step is one forward pass; ``value`` is images per second.
+    The roofline is MFMA: the convolutions' FLOPs (2 N Ho Wo Cout Cin KH KW each) over their
+    measured time, against the dense fp16 peak."""
+    import torch
+
+    from hip_compiler import compile_subgraph, is_hip_op_supported
+    from hip_runtime import HIPBackend
+    from irgen.resnet import build_resnet50_ir, resnet_inputs, resnet_weights
+    from npu_compiler import partition
+    from npu_runtime import DAGExecutor
+
+    B = args.batch
+    steps = args.steps if args.steps != 64 else 20
+    warm = args.warmup if args.warmup != 8 else 3
+    t0 = time.time()
+    ir = build_resnet50_ir(B, 224)
+    backend = HIPBackend(0)
+    ex = DAGExecutor(partition(ir, is_hip_op_supported), backend, compile_fn=compile_subgraph)
+    compile_s = time.time() - t0
+    weights = resnet_weights(ir, device="cuda")
+    ex.load_weights(weights)
+    x0 = resnet_inputs(B, 224, device="cuda")
+    state = {k: backend.allocate_buffer(v) for k, v in x0.items()}
+    (program,) = ex.npu_programs.values()
+    (hexec,) = ex._npu_executors.values()
+    log(f"resnet50 batch {B}: {len(program.steps)} launches, arena {program.arena_bytes / 1e6:.1f} MB")
+    for _ in range(warm):
+        ex.execute(state)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ex.execute(state)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed * 1e3 / steps
+    ips = B * steps / elapsed
+
+    def cflops(st):
+        if st.kind == "conv":
+            return 2.0 * st.args["M"] * st.args["Cout"] * st.args["K"]
+        if st.kernel.startswith("k_gemm_") and not st.params.get("reduce"):
+            return 2.0 * st.args["M"] * st.args["N"] * st.args["K"]
+        return 0.0
+
+    flops = sum(cflops(s) for s in program.steps)
+    stream = torch.cuda.current_stream().cuda_stream
+    fams: dict[str, list[int]] = {}
+    for i, s in enumerate(program.steps):
+        fams.setdefault(s.kernel, []).append(i)
+    per_kernel, conv_ms, conv_flops = {}, 0.0, 0.0
+    for kname, idx in sorted(fams.items()):
+        us = time_kernel_subset(hexec, idx, max(1, args.kernel_repeats // 5), stream) * 1e3
+        e = {"launches_per_step": len(idx), "avg_us": round(us, 2)}
+        f = sum(cflops(program.steps[i]) for i in idx)
+        if f:
+            e["TFLOPs"] = round(f / len(idx) / (us * 1e-6) / 1e12, 1)
+        if kname.startswith("k_conv_"):
+            conv_ms += us * len(idx) * 1e-3
+            conv_flops += f
+        per_kernel[kname] = e
+        log(f"  {kname}: {e}")
+    # per conv launch (every conv has its own shape): time each inside the family replay
+    conv_tf = conv_flops / (conv_ms * 1e-3) / 1e12
+    step_tf = flops / (ms * 1e-3) / 1e12
+    log(f"{ips:.0f} images/s, {ms:.2f} ms/batch; convs {conv_tf:.0f} TFLOP/s over {conv_ms:.2f} ms")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from irgen.workloads import to_host
+
+        n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n)
+        cb = min(B, 8)
+        cir = build_resnet50_ir(cb, 224)
+        cex = DAGExecutor(partition(cir, lambda *_: False), None)
+        cex.load_weights({k: v.detach().cpu() for k, v in weights.items()})
+        ins = {"x": to_host(x0["x"][:cb].detach().cpu())}
+        cex.execute(ins)
+        t0 = time.perf_counter()
+        cex.execute(ins)
+        cs = time.perf_counter() - t0
+        cpu = {"value": round(cb / cs, 2), "unit": "images/s", "cores": n, "kind": "port",
+               "sample": f"one forward pass of batch {cb} (the first {cb} images of the same input) after one "
+                         f"warmup, DAGExecutor all-CPU plan (ATen fp16, {n} threads): {cs:.2f} s"}
+        log(f"cpu: {cpu}")
+    line = {
+        "metric": "ResNet-50 fp16 inference images/s @batch32 224x224; MFMA TFLOP/s vs dense fp16 peak",
+        "value": round(ips, 1), "unit": "images/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": f"cfg5: ResNet-50 (torchvision v1.5 layout), batch {B}, 3 x 224 x 224, "
+                               "inference batch norm fused into the convolutions",
+                   "launches_per_step": len(program.steps), "compile_s": round(compile_s, 2)},
+        "roofline": {"bound": "mfma", "kernel": "k_conv_f16 (all 52 launches)", "achieved": round(conv_tf, 1),
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(conv_tf / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "step_roofline": {"flops_per_step": flops, "achieved": round(step_tf, 1), "unit": "TFLOP/s",
                           "frac": round(step_tf / MFMA_PEAK_TFLOPS, 4)},
         "kernels": per_kernel,
         "cpu_baseline": cpu,
