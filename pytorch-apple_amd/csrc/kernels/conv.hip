@@ -46,7 +46,8 @@ __device__ __forceinline__ float cv_round(float f) {
   return cv_f<DT>(cv_h<DT>(f));
 }
 
-template <int DT, bool BVEC>
+// KS: 1 = 1x1 kernel without padding (A is one strided plane read per k), 3 = 3x3, 0 = any
+template <int DT, bool BVEC, int KS = 0>
 __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[2][CV_BM][CV_LDS_K];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][CV_BN][CV_LDS_K];
@@ -56,35 +57,61 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   const int n_base = blockIdx.x * CV_BN;
   const uint16_t* X = (const uint16_t*)a.x;
   const uint16_t* Wt = (const uint16_t*)a.w;
-  const int HW = a.H * a.W, KHW = a.KH * a.KW;
+  const int HW = a.H * a.W;
 
-  // this thread's A pixel and k range within a step
-  const int am = tid & (CV_BM - 1), akg = tid >> 7;   // akg: which 16 of the 32 k
-  const long long mg = m_base + am;
-  const bool mvalid = mg < a.M;
+  // this thread's A pixel and k range within a step. The 16 k of a thread are the same for
+  // the whole wave (akg = wave / 2), so their (ci, kh, kw) decomposition is scalar work, and
+  // each element costs one vector add, a validity test and the load.
+  const int am = tid & (CV_BM - 1);
+  const int akg = __builtin_amdgcn_readfirstlane(tid >> 7);
+  const int M32 = (int)a.M;
+  const int mg = min((int)m_base + am, M32 - 1);   // rows past M read a valid pixel; never stored
   const int HoWo = a.Ho * a.Wo;
-  const long long mn = mvalid ? mg / HoWo : 0;
-  const int mp = mvalid ? (int)(mg - mn * HoWo) : 0;
+  const int mn = mg / HoWo, mp = mg - mn * HoWo;
   const int hi0 = (mp / a.Wo) * a.sh - a.ph, wi0 = (mp % a.Wo) * a.sw - a.pw;
-  const uint16_t* Xn = X + mn * (long long)a.Cin * HW;
+  const int pix = mn * a.Cin * HW + hi0 * a.W + wi0;   // element offset of (n, ci = 0, hi0, wi0); < 2^31
+  // 3x3: bit kh * 3 + kw set when the tap (kh, kw) of this pixel is inside the image
+  unsigned tapmask = 0;
+  if constexpr (KS == 3) {
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+      for (int kw = 0; kw < 3; ++kw)
+        if ((unsigned)(hi0 + kh) < (unsigned)a.H && (unsigned)(wi0 + kw) < (unsigned)a.W)
+          tapmask |= 1u << (kh * 3 + kw);
+  }
 
   uint32_t ra[8];    // 16 gathered A values, packed in pairs
   uint4 rb[2];       // B: 2 x 16 bytes (BVEC) ...
   uint32_t rbs[16];  // ... or 16 gathered values packed in pairs
   auto load_a = [&](int k0, uint32_t (&dst)[8]) {
-    int k = k0 + akg * 16;
-    int ci = k / KHW, r = k - ci * KHW, kh = r / a.KW, kw = r - kh * a.KW;
+    const int kb = __builtin_amdgcn_readfirstlane(k0 + akg * 16);
+    if constexpr (KS == 1) {   // K % 32 == 0 and no padding (the host checks): every element is in range
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      uint16_t v = 0;
-      const int hi = hi0 + kh, wi = wi0 + kw;
-      if (mvalid && k < a.K && hi >= 0 && hi < a.H && wi >= 0 && wi < a.W) v = Xn[(long long)ci * HW + hi * a.W + wi];
-      if (j & 1) dst[j >> 1] |= (uint32_t)v << 16;
-      else dst[j >> 1] = v;
-      ++k;
-      if (++kw == a.KW) {
-        kw = 0;
-        if (++kh == a.KH) { kh = 0; ++ci; }
+      for (int j = 0; j < 16; ++j) {
+        const uint16_t v = X[pix + (kb + j) * HW];
+        if (j & 1) dst[j >> 1] |= (uint32_t)v << 16;
+        else dst[j >> 1] = v;
+      }
+    } else {
+      const int KWr = KS == 3 ? 3 : a.KW, KHr = KS == 3 ? 3 : a.KH;
+      int ci = kb / (KHr * KWr), r = kb - ci * (KHr * KWr), kh = r / KWr, kw = r - kh * KWr;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int k = kb + j;
+        const int tap = kh * KWr + kw;
+        const int so = ci * HW + kh * a.W + kw;   // scalar part of the offset
+        bool ok;
+        if constexpr (KS == 3) ok = k < a.K && ((tapmask >> tap) & 1u);
+        else ok = k < a.K && (unsigned)(hi0 + kh) < (unsigned)a.H && (unsigned)(wi0 + kw) < (unsigned)a.W;
+        const uint16_t ld = X[ok ? pix + so : 0];   // padded taps read element 0 (in bounds), then 0
+        const uint16_t v = ok ? ld : (uint16_t)0;
+        if (j & 1) dst[j >> 1] |= (uint32_t)v << 16;
+        else dst[j >> 1] = v;
+        if (++kw == KWr) {
+          kw = 0;
+          if (++kh == KHr) { kh = 0; ++ci; }
+        }
       }
     }
   };
@@ -154,29 +181,39 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
     __syncthreads();
   }
 
-  // epilogue
+  // epilogue: per-channel batch-norm factors first, then (image, pixel) of each row once
+  // (M < 2^31, so 32-bit division; the same row serves both channel tiles)
+  float bias[2], al[2], be[2];
+  int cos_[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int co = n_base + wc * 64 + j * 32 + fr;
-    if (co >= a.Cout) continue;
-    const float bias = (a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[co]) : 0.f;
-    float al = 1.f, be = 0.f;
+    cos_[j] = co;
+    const int cc = min(co, a.Cout - 1);
+    bias[j] = (a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[cc]) : 0.f;
+    al[j] = 1.f;
+    be[j] = 0.f;
     if (a.flags & 2) {
-      const float g = cv_f<DT>(((const uint16_t*)a.bn_w)[co]), bb = cv_f<DT>(((const uint16_t*)a.bn_b)[co]);
-      const float mu = cv_f<DT>(((const uint16_t*)a.bn_mean)[co]), var = cv_f<DT>(((const uint16_t*)a.bn_var)[co]);
-      al = g / sqrtf(var + a.eps);
-      be = bb - mu * al;
+      const float g = cv_f<DT>(((const uint16_t*)a.bn_w)[cc]), bb = cv_f<DT>(((const uint16_t*)a.bn_b)[cc]);
+      const float mu = cv_f<DT>(((const uint16_t*)a.bn_mean)[cc]), var = cv_f<DT>(((const uint16_t*)a.bn_var)[cc]);
+      al[j] = g / sqrtf(var + a.eps);
+      be[j] = bb - mu * al[j];
     }
+  }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < 2; ++i) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const long long m = m_base + wr * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-        if (m >= a.M) continue;
-        const long long n = m / HoWo;
-        const long long o = (n * a.Cout + co) * HoWo + (m - n * HoWo);
-        float v = cv_round<DT>(acc[i][j][e] + bias);
-        if (a.flags & 2) v = cv_round<DT>(v * al + be);
+    for (int e = 0; e < 16; ++e) {
+      const int m = (int)m_base + wr * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+      if (m >= M32) continue;
+      const int n = m / HoWo;
+      const long long pix = (long long)n * a.Cout * HoWo + (m - n * HoWo);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (cos_[j] >= a.Cout) continue;
+        const long long o = pix + (long long)cos_[j] * HoWo;
+        float v = cv_round<DT>(acc[i][j][e] + bias[j]);
+        if (a.flags & 2) v = cv_round<DT>(v * al[j] + be[j]);
         if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
         if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
         ((uint16_t*)a.out)[o] = cv_h<DT>(v);
@@ -188,8 +225,12 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
 #define CV_ATTRS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
 extern "C" __global__ void CV_ATTRS k_conv_f16(const ConvArgs a) { conv_body<HS_F16, true>(a); }
 extern "C" __global__ void CV_ATTRS k_conv_f16_g(const ConvArgs a) { conv_body<HS_F16, false>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_f16_1x1(const ConvArgs a) { conv_body<HS_F16, true, 1>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_f16_3x3(const ConvArgs a) { conv_body<HS_F16, true, 3>(a); }
 extern "C" __global__ void CV_ATTRS k_conv_bf16(const ConvArgs a) { conv_body<HS_BF16, true>(a); }
 extern "C" __global__ void CV_ATTRS k_conv_bf16_g(const ConvArgs a) { conv_body<HS_BF16, false>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_bf16_1x1(const ConvArgs a) { conv_body<HS_BF16, true, 1>(a); }
+extern "C" __global__ void CV_ATTRS k_conv_bf16_3x3(const ConvArgs a) { conv_body<HS_BF16, true, 3>(a); }
 
 // ---------------------------------------------------------------- pooling / batch norm
 

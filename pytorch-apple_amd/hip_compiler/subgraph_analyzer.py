@@ -777,7 +777,13 @@ class Lowering:
         flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
         vec = K % 8 == 0 and (w.offset * 2) % 16 == 0
         kname = f"k_conv_{'bf16' if dt == 'bfloat16' else 'f16'}" + ("" if vec else "_g")
+        if vec and KH == KW == 1 and pd == [0, 0] and K % 32 == 0:
+            kname += "_1x1"
+        elif vec and KH == KW == 3:
+            kname += "_3x3"
         M = N * Ho * Wo
+        if M + 256 >= 2 ** 31 or x.numel >= 2 ** 31:
+            raise NotImplementedError("conv2d with 2^31 or more input elements or output pixels")
         ins = [conv.inputs[0].name, conv.inputs[1].name] + ([conv.inputs[2].name] if has_bias else []) + \
             ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
         self.emit(LaunchStep(
