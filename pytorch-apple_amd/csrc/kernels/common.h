@@ -8,10 +8,23 @@
 // implicit padding appears between them.
 #pragma once
 
-#ifdef __HIPCC__
+// hiprtc (generated kernels) provides the HIP device definitions and fixed-width
+// integer types itself, so the headers are only included for hipcc builds
+#if defined(__HIPCC__) && !defined(__HIPCC_RTC__)
 #include <hip/hip_runtime.h>
 #endif
+#ifdef __HIPCC_RTC__
+typedef signed char int8_t;
+typedef unsigned char uint8_t;
+typedef short int16_t;
+typedef unsigned short uint16_t;
+typedef int int32_t;
+typedef unsigned int uint32_t;
+typedef long long int64_t;
+typedef unsigned long long uint64_t;
+#else
 #include <stdint.h>
+#endif
 
 #define HS_MAXD 6
 

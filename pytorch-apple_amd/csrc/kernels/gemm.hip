@@ -75,49 +75,60 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const uint16_t* W1 = (const uint16_t*)(NW == 2 ? a.w2 : a.w) + wofs;
   uint16_t* OUT = (uint16_t*)a.out + bz * a.so;
 
-  // global -> register staging of one K step, and register -> LDS (plain loops on local
-  // arrays: lambdas capturing the arrays by reference put them in scratch memory)
-  uint4 ra[A_LD], rb[B_LD];
-#define GM_LOAD_STEP(k0)                                                                  \
-  do {                                                                                    \
-    _Pragma("unroll") for (int i = 0; i < A_LD; ++i) {                                    \
-      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;                       \
-      const long long m = min(m_base + row, a.M - 1);                                     \
-      ra[i] = *(const uint4*)(X + m * a.ldx + (k0) + col);                                \
-    }                                                                                     \
-    _Pragma("unroll") for (int i = 0; i < B_LD; ++i) {                                    \
-      const int c = tid + 256 * i;                                                        \
-      if constexpr (KN) {                                                                 \
-        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;                           \
-        const int n = min(n_base + nc, a.N - 8);                                          \
-        rb[i] = *(const uint4*)(W0 + (long long)((k0) + kr) * a.ldw + n);                 \
-      } else {                                                                            \
-        const int row = c >> 2, col = (c & 3) * 8;                                        \
-        const int u = row / BN, n = min(n_base + row % BN, a.N - 1);                      \
-        rb[i] = *(const uint4*)((u == 0 ? W0 : W1) + (long long)n * a.ldw + (k0) + col);  \
-      }                                                                                   \
-    }                                                                                     \
+  // global -> register staging of one K step, and register -> LDS. The staging lives in
+  // named registers (A_LD, B_LD <= 2): a small per-thread array would be promoted to LDS by
+  // the compiler, doubling the LDS traffic of the main loop.
+  static_assert(A_LD >= 1 && A_LD <= 2 && B_LD >= 1 && B_LD <= 2, "staging registers");
+  uint4 ra0, ra1, rb0, rb1;
+  auto a_ld = [&](int i, int k0) -> uint4 {
+    const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+    const long long m = min(m_base + row, a.M - 1);
+    return *(const uint4*)(X + m * a.ldx + k0 + col);
+  };
+  auto b_ld = [&](int i, int k0) -> uint4 {
+    const int c = tid + 256 * i;
+    if constexpr (KN) {   // w is [K, N]: 16-byte chunks along n, BNT / 8 chunks per k row (NW == 1)
+      const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;
+      const int n = min(n_base + nc, a.N - 8);
+      return *(const uint4*)(W0 + (long long)(k0 + kr) * a.ldw + n);
+    } else {
+      const int row = c >> 2, col = (c & 3) * 8;
+      const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
+      return *(const uint4*)((u == 0 ? W0 : W1) + (long long)n * a.ldw + k0 + col);
+    }
+  };
+  auto a_st = [&](int buf, int i, uint4 v) {
+    const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+    *(uint4*)&As[buf][row][col] = v;
+  };
+  auto b_st = [&](int buf, int i, uint4 v) {
+    const int c = tid + 256 * i;
+    if constexpr (KN) {   // transpose into the [n][k] layout the fragments are read from
+      const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;
+      const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        Bs[buf][nc + 2 * j][kr] = (uint16_t)(q[j] & 0xffffu);
+        Bs[buf][nc + 2 * j + 1][kr] = (uint16_t)(q[j] >> 16);
+      }
+    } else {
+      const int row = c >> 2, col = (c & 3) * 8;
+      *(uint4*)&Bs[buf][row][col] = v;
+    }
+  };
+#define GM_LOAD_STEP(k0)                  \
+  do {                                    \
+    ra0 = a_ld(0, (k0));                  \
+    if (A_LD > 1) ra1 = a_ld(1, (k0));    \
+    rb0 = b_ld(0, (k0));                  \
+    if (B_LD > 1) rb1 = b_ld(1, (k0));    \
   } while (0)
-#define GM_STORE_STEP(buf)                                                                \
-  do {                                                                                    \
-    _Pragma("unroll") for (int i = 0; i < A_LD; ++i) {                                    \
-      const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;                       \
-      *(uint4*)&As[buf][row][col] = ra[i];                                                \
-    }                                                                                     \
-    _Pragma("unroll") for (int i = 0; i < B_LD; ++i) {                                    \
-      const int c = tid + 256 * i;                                                        \
-      if constexpr (KN) { /* transpose into the [n][k] layout the fragments are read from */ \
-        const int kr = c / (BNT / 8), nc = (c % (BNT / 8)) * 8;                           \
-        const uint32_t q[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};                       \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                   \
-          Bs[buf][nc + 2 * j][kr] = (uint16_t)(q[j] & 0xffffu);                           \
-          Bs[buf][nc + 2 * j + 1][kr] = (uint16_t)(q[j] >> 16);                           \
-        }                                                                                 \
-      } else {                                                                            \
-        const int row = c >> 2, col = (c & 3) * 8;                                        \
-        *(uint4*)&Bs[buf][row][col] = rb[i];                                              \
-      }                                                                                   \
-    }                                                                                     \
+#define GM_STORE_STEP(buf)                \
+  do {                                    \
+    a_st((buf), 0, ra0);                  \
+    if (A_LD > 1) a_st((buf), 1, ra1);    \
+    b_st((buf), 0, rb0);                  \
+    if (B_LD > 1) b_st((buf), 1, rb1);    \
   } while (0)
 
   gm_f32x16 acc[NW][TI][TJ];
