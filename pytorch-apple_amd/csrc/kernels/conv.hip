@@ -70,6 +70,10 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   const int mn = mg / HoWo, mp = mg - mn * HoWo;
   const int hi0 = (mp / a.Wo) * a.sh - a.ph, wi0 = (mp % a.Wo) * a.sw - a.pw;
   const int pix = mn * a.Cin * HW + hi0 * a.W + wi0;   // element offset of (n, ci = 0, hi0, wi0); < 2^31
+  // byte offsets from the (uniform) tensor base: 32-bit unsigned, so every load is
+  // base + one vector add (the input is < 4 GiB; the host checks)
+  const char* Xb = (const char*)a.x;
+  const uint32_t HWb = (uint32_t)HW * 2u;
   // 3x3: bit kh * 3 + kw set when the tap (kh, kw) of this pixel is inside the image
   unsigned tapmask = 0;
   if constexpr (KS == 3) {
@@ -87,9 +91,10 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   auto load_a = [&](int k0, uint32_t (&dst)[8]) {
     const int kb = __builtin_amdgcn_readfirstlane(k0 + akg * 16);
     if constexpr (KS == 1) {   // K % 32 == 0 and no padding (the host checks): every element is in range
+      const uint32_t o0 = (uint32_t)pix * 2u + (uint32_t)kb * HWb;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const uint16_t v = X[pix + (kb + j) * HW];
+        const uint16_t v = *(const uint16_t*)(Xb + (o0 + (uint32_t)j * HWb));
         if (j & 1) dst[j >> 1] |= (uint32_t)v << 16;
         else dst[j >> 1] = v;
       }
@@ -104,7 +109,8 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
         bool ok;
         if constexpr (KS == 3) ok = k < a.K && ((tapmask >> tap) & 1u);
         else ok = k < a.K && (unsigned)(hi0 + kh) < (unsigned)a.H && (unsigned)(wi0 + kw) < (unsigned)a.W;
-        const uint16_t ld = X[ok ? pix + so : 0];   // padded taps read element 0 (in bounds), then 0
+        // padded taps read element 0 (in bounds) and are replaced by 0
+        const uint16_t ld = *(const uint16_t*)(Xb + (ok ? (uint32_t)(pix + so) * 2u : 0u));
         const uint16_t v = ok ? ld : (uint16_t)0;
         if (j & 1) dst[j >> 1] |= (uint32_t)v << 16;
         else dst[j >> 1] = v;
@@ -175,45 +181,49 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = cv_mfma<DT>(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = cv_mfma<DT>(bfr[j], af[i], acc[i][j]);   // D[channel][pixel]
     }
     if (s + 1 < nsteps) store(buf ^ 1);
     __syncthreads();
   }
 
-  // epilogue: per-channel batch-norm factors first, then (image, pixel) of each row once
-  // (M < 2^31, so 32-bit division; the same row serves both channel tiles)
-  float bias[2], al[2], be[2];
-  int cos_[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int co = n_base + wc * 64 + j * 32 + fr;
-    cos_[j] = co;
-    const int cc = min(co, a.Cout - 1);
-    bias[j] = (a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[cc]) : 0.f;
-    al[j] = 1.f;
-    be[j] = 0.f;
+  // epilogue. The MFMA operands are swapped (weights as the row operand), so each
+  // accumulator register holds one channel for 32 consecutive pixels across the lanes:
+  // stores (and residual loads) of a register are 64 contiguous bytes in NCHW.
+  // Per-channel factors of the tile are computed once into LDS.
+  __shared__ float s_al[CV_BN], s_be[CV_BN];
+  if (tid < CV_BN) {
+    const int cc = min(n_base + tid, a.Cout - 1);
+    const float bias = (a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[cc]) : 0.f;
+    float al = 1.f, be = 0.f;
     if (a.flags & 2) {
       const float g = cv_f<DT>(((const uint16_t*)a.bn_w)[cc]), bb = cv_f<DT>(((const uint16_t*)a.bn_b)[cc]);
       const float mu = cv_f<DT>(((const uint16_t*)a.bn_mean)[cc]), var = cv_f<DT>(((const uint16_t*)a.bn_var)[cc]);
-      al[j] = g / sqrtf(var + a.eps);
-      be[j] = bb - mu * al[j];
+      al = g / sqrtf(var + a.eps);
+      be = bb - mu * al;
     }
+    s_al[tid] = al;
+    s_be[tid] = be;
+    ((float*)&Bs[0][0][0])[tid] = bias;   // Bs is free after the main loop
   }
+  __syncthreads();
+  const float* s_bias = (const float*)&Bs[0][0][0];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
+    const int m = (int)m_base + wr * 64 + i * 32 + fr;
+    if (m >= M32) continue;
+    const int n = m / HoWo;
+    const long long pixo = (long long)n * a.Cout * HoWo + (m - n * HoWo);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int m = (int)m_base + wr * 64 + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
-      if (m >= M32) continue;
-      const int n = m / HoWo;
-      const long long pix = (long long)n * a.Cout * HoWo + (m - n * HoWo);
+    for (int j = 0; j < 2; ++j) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (cos_[j] >= a.Cout) continue;
-        const long long o = pix + (long long)cos_[j] * HoWo;
-        float v = cv_round<DT>(acc[i][j][e] + bias[j]);
-        if (a.flags & 2) v = cv_round<DT>(v * al[j] + be[j]);
+      for (int e = 0; e < 16; ++e) {
+        const int cl = wc * 64 + j * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        const int co = n_base + cl;
+        if (co >= a.Cout) continue;
+        const long long o = pixo + (long long)co * HoWo;
+        float v = cv_round<DT>(acc[i][j][e] + s_bias[cl]);
+        if (a.flags & 2) v = cv_round<DT>(v * s_al[cl] + s_be[cl]);
         if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
         if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
         ((uint16_t*)a.out)[o] = cv_h<DT>(v);

@@ -782,7 +782,7 @@ class Lowering:
         elif vec and KH == KW == 3:
             kname += "_3x3"
         M = N * Ho * Wo
-        if M + 256 >= 2 ** 31 or x.numel >= 2 ** 31:
+        if M + 256 >= 2 ** 31 or x.numel * 2 >= 2 ** 32:
             raise NotImplementedError("conv2d with 2^31 or more input elements or output pixels")
         ins = [conv.inputs[0].name, conv.inputs[1].name] + ([conv.inputs[2].name] if has_bias else []) + \
             ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
