@@ -419,6 +419,16 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   }
   rows_to_lds<1>((const uint16_t*)a.x, 0, 1, (const uint16_t*)a.norm_w, a.K, a.eps, a.n_dtype, (a.flags & 1) != 0, xs);
   if (!active) return;
+  // rotary factors now: they depend only on the position, so this runs while the weight
+  // loads are still in flight instead of after the dot products
+  const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
+  float rc = 1.f, rs = 0.f;
+  if (rope) {
+    float sf, cf;
+    sincosf(invf * (float)pos_v, &sf, &cf);
+    rc = round_to(cf * a.rope_scaling, HS_BF16);
+    rs = round_to(sf * a.rope_scaling, HS_BF16);
+  }
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
   for (int c = 0; c < 6; ++c) {
@@ -435,13 +445,8 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   acc0 += b0;
   acc1 += b1;
   float v0 = rbf(acc0), v1 = rbf(acc1);
-  const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
   if (rope) {
-    const float f = invf * (float)pos_v;
-    float sf, cf;
-    sincosf(f, &sf, &cf);
-    const float c = round_to(cf * a.rope_scaling, HS_BF16);
-    const float s = round_to(sf * a.rope_scaling, HS_BF16);
+    const float c = rc, s = rs;
     const float e0 = rbf(rbf(v0 * c) + rbf(-v1 * s));   // x[j]*cos + (-x[j+D/2])*sin
     const float e1 = rbf(rbf(v1 * c) + rbf(v0 * s));    // x[j+D/2]*cos + x[j]*sin
     v0 = e0;
