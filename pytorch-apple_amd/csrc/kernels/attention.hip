@@ -135,8 +135,9 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
 
 // ------------------------------------------------------------------ split-S flash decoding
 //
-// k_attn_flash: grid (nsplit, KVH, G), 256 threads. Workgroup (t, kvh, g) handles query
-// head kvh*G + g over the FL_SPL = 64 positions of split t, 16 per wave. Spreading the
+// k_attn_flash: grid (nsplit, KVH, G), 256 threads (k_attn_flash_w16: 1024). Workgroup
+// (t, kvh, g) handles query head kvh*G + g over the 16 * W positions of split t (W = 4 or
+// 16 waves), 16 per wave. Spreading the
 // heads of a GQA group over workgroups (rather than serving all G heads from one K/V
 // read) gives G times more workgroups for the same split size; the G reads of a K/V
 // tile happen together and are served by the caches, and the work per wave stays small,
@@ -148,13 +149,12 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_scores(const DecodeAttn
 // lane owns 2 of the 128 dims over the wave's 16 positions, taking p from the owning
 // lane with readlane. The 4 waves are merged in LDS into the split's partials
 //   m_t = max s, l_t = sum exp(s - m_t), o_t = sum exp(s - m_t) v   (fp32).
-// A wave whose 16 positions are all masked loads no K or V rows.
+// A wave whose 16 positions are all masked skips the arithmetic (its K/V loads are issued
+// with the mask's, before the mask is known).
 // The partials are combined by k_attn_combine (or in the prologue of the next GEMV,
 // gemv.hip): o = sum_t e^(m_t - M) o_t / sum_t e^(m_t - M) l_t. Compared with the CPU
 // chain, only the bf16 rounding of the probabilities is not repeated.
-#define FL_SPL 64
-#define FL_PW 16
-#define FL_WAVES 4
+#define FL_PW 16      // positions per wave; a split is FL_PW * W positions (W waves)
 
 typedef __attribute__((ext_vector_type(2))) __bf16 fl_bf16x2;
 typedef __attribute__((ext_vector_type(2))) _Float16 fl_f16x2;
@@ -167,34 +167,38 @@ __device__ __forceinline__ float fl_dot2(uint32_t a, uint32_t b, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(fl_f16x2, a), __builtin_bit_cast(fl_f16x2, b), acc, false);
 }
 
-template <int DT>
+template <int DT, int W>
 __device__ __forceinline__ void flash_body(const FlashArgs& a) {
-  __shared__ float osh[FL_WAVES][AT_D];
-  __shared__ float msh[FL_WAVES], lsh[FL_WAVES];
+  __shared__ float osh[W][AT_D];
+  __shared__ float msh[W], lsh[W];
   const int G = a.H / a.KVH;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, g = blockIdx.z;
-  const long long p0 = (long long)split * FL_SPL + wave * FL_PW;   // this wave's first position
+  const long long p0 = (long long)split * (FL_PW * W) + wave * FL_PW;   // this wave's first position
   const int kq = lane >> 2, kc = lane & 3;                         // K: position p0 + kq, dims kc*32..+32
   const long long last = a.S - 1;
   const uint16_t* Kb = (const uint16_t*)a.k + (long long)kvh * a.kv_head_stride;
   const uint16_t* Vb = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride;
-  float mval = -INFINITY;
-  if (p0 + kq <= last) mval = a.mask_dtype < 0 ? 0.f : ld_f(a.mask, (p0 + kq) * a.mask_stride, a.mask_dtype);
-  uint4 qr[4];
+  // every load is issued up front with no branch: the mask value as raw bits, q, and the
+  // wave's K and V rows (positions clamped to the cache; a masked position's rows are read
+  // but weigh nothing), so one memory latency covers them all
+  const void* mptr = a.mask_dtype < 0 ? a.q : a.mask;   // a.q: valid dummy address
+  const FRaw mraw = ld_f_raw(mptr, min(p0 + kq, last) * a.mask_stride, a.mask_dtype);
+  uint4 qr[4], kr[4];
+  uint32_t vr[FL_PW];
   const uint4* qs = (const uint4*)((const uint16_t*)a.q + (long long)(kvh * G + g) * a.q_head_stride + kc * 32);
 #pragma unroll
   for (int j = 0; j < 4; ++j) qr[j] = qs[j];
+  const uint4* ks = (const uint4*)(Kb + min(p0 + kq, last) * AT_D + kc * 32);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kr[j] = ks[j];
+#pragma unroll
+  for (int t = 0; t < FL_PW; ++t) vr[t] = *(const uint32_t*)(Vb + min(p0 + t, last) * AT_D + 2 * lane);
+  const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
+  const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
   const bool live = __ballot(mval != -INFINITY) != 0ull;   // wave-uniform
   float m_w = -INFINITY, l_w = 0.f, acc0 = 0.f, acc1 = 0.f;
   if (live) {
-    uint4 kr[4];
-    uint32_t vr[FL_PW];
-    const uint4* ks = (const uint4*)(Kb + min(p0 + kq, last) * AT_D + kc * 32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kr[j] = ks[j];
-#pragma unroll
-    for (int t = 0; t < FL_PW; ++t) vr[t] = *(const uint32_t*)(Vb + min(p0 + t, last) * AT_D + 2 * lane);
     float d = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -246,10 +250,10 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
     const int dd = threadIdx.x;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < FL_WAVES; ++w) M = fmaxf(M, msh[w]);
+    for (int w = 0; w < W; ++w) M = fmaxf(M, msh[w]);
     float o = 0.f, L = 0.f;
 #pragma unroll
-    for (int w = 0; w < FL_WAVES; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float f = (lsh[w] > 0.f) ? __expf(msh[w] - M) : 0.f;
       o = fmaf(f, osh[w][dd], o);
       L = fmaf(f, lsh[w], L);
@@ -263,8 +267,11 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
   }
 }
 
-extern "C" __global__ void __launch_bounds__(256) k_attn_flash(const FlashArgs a) { flash_body<HS_BF16>(a); }
-extern "C" __global__ void __launch_bounds__(256) k_attn_flash_f16(const FlashArgs a) { flash_body<HS_F16>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_attn_flash(const FlashArgs a) { flash_body<HS_BF16, 4>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_attn_flash_f16(const FlashArgs a) { flash_body<HS_F16, 4>(a); }
+// 16 waves, 256 positions per split: 4x fewer partials, for a combine folded into the next GEMV
+extern "C" __global__ void __launch_bounds__(1024) k_attn_flash_w16(const FlashArgs a) { flash_body<HS_BF16, 16>(a); }
+extern "C" __global__ void __launch_bounds__(1024) k_attn_flash_w16_f16(const FlashArgs a) { flash_body<HS_F16, 16>(a); }
 
 // out[h, d] = round(sum_t e^(m_t - M) o_t[d] / sum_t e^(m_t - M) l_t); one workgroup of 128
 // threads per head. Splits are folded in chunks of 64: lane t of every wave loads split t's

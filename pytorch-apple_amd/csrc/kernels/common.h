@@ -414,6 +414,36 @@ __device__ __forceinline__ long long ld_i(const void* p, long long i, int dt) {
   return 0;
 }
 
+// Branch-free loads for values needed late in a kernel: the raw words are loaded with no
+// dtype switch (so no wait follows the load) and decoded where the value is used.
+// Integer element i of an int64 or int32 tensor: two 32-bit words (int64: its halves;
+// int32: the element's word twice).
+struct IRaw {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ IRaw ld_i_raw(const void* p, long long i, int dt) {
+  const bool wide = dt == HS_I64;
+  const uint32_t* w = (const uint32_t*)((const char*)p + i * (wide ? 8 : 4));
+  return IRaw{w[0], w[wide ? 1 : 0]};
+}
+__device__ __forceinline__ long long ld_i_decode(IRaw r, int dt) {
+  return dt == HS_I64 ? (long long)(((unsigned long long)r.hi << 32) | r.lo) : (long long)(int)r.lo;
+}
+// Float element i of an fp32, fp16 or bf16 tensor: two 16-bit halves (fp32: low and high
+// half; 16-bit types: the element twice).
+struct FRaw {
+  uint16_t lo, hi;
+};
+__device__ __forceinline__ FRaw ld_f_raw(const void* p, long long i, int dt) {
+  const bool wide = dt == HS_F32;
+  const uint16_t* h = (const uint16_t*)((const char*)p + i * (wide ? 4 : 2));
+  return FRaw{h[0], h[wide ? 1 : 0]};
+}
+__device__ __forceinline__ float ld_f_decode(FRaw r, int dt) {
+  if (dt == HS_F32) return __uint_as_float(((uint32_t)r.hi << 16) | r.lo);
+  return dt == HS_BF16 ? bf16_to_f32(r.lo) : f16_to_f32(r.lo);
+}
+
 // round a float to the storage precision of dt (identity for fp32)
 __device__ __forceinline__ float round_to(float f, int dt) {
   if (dt == HS_BF16) return bf16_to_f32(f32_to_bf16(f));

@@ -40,30 +40,43 @@ enum { EPI_BIAS = 0, EPI_RESID = 1, EPI_SILU = 2, EPI_ARGMAX = 3 };
 
 // RMSNorm (norm = true) or a plain copy of `rows` <= ROWS activation rows of length K into LDS
 // as bf16 bits (row m at xs + m*K); 256 threads, K % 8 == 0, K <= 4096, 16-byte aligned rows.
-// x and the norm weight are fetched with 16-byte loads, all in one round; the sums of squares
-// are reduced with DPP plus one LDS exchange.
+// Two halves: rows_fetch issues the 16-byte loads of x and the norm weight (one round), and
+// rows_finish reduces the sums of squares (DPP plus one LDS exchange) and writes LDS. A kernel
+// issues its weight loads between the two, so the norm runs while the weights stream in.
 template <int ROWS>
-__device__ __forceinline__ void rows_to_lds(const uint16_t* x, long long ldx, int rows, const uint16_t* w, int K,
-                                            float eps, int n_dtype, bool norm, uint16_t* xs) {
-  __shared__ float red[4][ROWS];
-  const int K8 = K >> 3;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct RowsPre {
   uint4 xv[ROWS][2], wn[2];
+};
+
+template <int ROWS>
+__device__ __forceinline__ void rows_fetch(RowsPre<ROWS>& p, const uint16_t* x, long long ldx, int rows,
+                                           const uint16_t* w, int K, bool norm) {
+  const int K8 = K >> 3;
+  const uint16_t* wsrc = norm ? w : x;   // a valid address either way; unused without the norm
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int i = threadIdx.x + c * 256;
-    wn[c] = (norm && i < K8) ? *(const uint4*)(w + 8 * i) : make_uint4(0, 0, 0, 0);
+    const bool in = i < K8;
+    p.wn[c] = in ? *(const uint4*)(wsrc + 8 * i) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int m = 0; m < ROWS; ++m)
-      xv[m][c] = (m < rows && i < K8) ? *(const uint4*)(x + m * ldx + 8 * i) : make_uint4(0, 0, 0, 0);
+      p.xv[m][c] = in ? *(const uint4*)(x + min(m, rows - 1) * ldx + 8 * i) : make_uint4(0, 0, 0, 0);
   }
+}
+
+template <int ROWS>
+__device__ __forceinline__ void rows_finish(const RowsPre<ROWS>& p, int rows, int K, float eps, int n_dtype,
+                                            bool norm, uint16_t* xs) {
+  __shared__ float red[4][ROWS];
+  const int K8 = K >> 3;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (!norm) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const int i = threadIdx.x + c * 256;
 #pragma unroll
       for (int m = 0; m < ROWS; ++m)
-        if (m < rows && i < K8) *(uint4*)(xs + m * K + 8 * i) = xv[m][c];
+        if (m < rows && i < K8) *(uint4*)(xs + m * K + 8 * i) = p.xv[m][c];
     }
     __syncthreads();
     return;
@@ -74,7 +87,7 @@ __device__ __forceinline__ void rows_to_lds(const uint16_t* x, long long ldx, in
     float acc = 0.f;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const uint32_t q[4] = {xv[m][c].x, xv[m][c].y, xv[m][c].z, xv[m][c].w};
+      const uint32_t q[4] = {p.xv[m][c].x, p.xv[m][c].y, p.xv[m][c].z, p.xv[m][c].w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float lo = bf16_to_f32((uint16_t)(q[j] & 0xffffu)), hi = bf16_to_f32((uint16_t)(q[j] >> 16));
@@ -97,8 +110,8 @@ __device__ __forceinline__ void rows_to_lds(const uint16_t* x, long long ldx, in
     for (int c = 0; c < 2; ++c) {
       const int i = threadIdx.x + c * 256;
       if (i >= K8) continue;
-      const uint32_t q[4] = {xv[m][c].x, xv[m][c].y, xv[m][c].z, xv[m][c].w};
-      const uint32_t g[4] = {wn[c].x, wn[c].y, wn[c].z, wn[c].w};
+      const uint32_t q[4] = {p.xv[m][c].x, p.xv[m][c].y, p.xv[m][c].z, p.xv[m][c].w};
+      const uint32_t g[4] = {p.wn[c].x, p.wn[c].y, p.wn[c].z, p.wn[c].w};
       uint32_t o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -114,12 +127,6 @@ __device__ __forceinline__ void rows_to_lds(const uint16_t* x, long long ldx, in
   __syncthreads();
 }
 
-template <int MB>
-__device__ __forceinline__ void norm_to_lds(const GemvArgs& a, long long m0, int rows, uint16_t* xs) {
-  rows_to_lds<MB>((const uint16_t*)a.x + m0 * a.ldx, a.ldx, rows, (const uint16_t*)a.norm_w, a.K, a.eps, a.n_dtype,
-                  true, xs);
-}
-
 __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
   uint32_t b = __float_as_uint(v);
   b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
@@ -130,41 +137,55 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
 // number of blocks), so a prologue is computed once per workgroup, not once per block.
 // x = the decode attention output, combined from its split partials (see attention.hip):
 // x[h*128 + d] = round(sum_t e^(m_t - M_h) o_t[d] / sum_t e^(m_t - M_h) l_t)
-__device__ __forceinline__ void attn_to_lds(const GemvArgs& a, uint16_t* xs) {
-  __shared__ float wt[16][128];
-  __shared__ float lt[16][128];
-  __shared__ float inv_l[16];
+// Wave w combines heads w, w+4, w+8, w+12; lane d holds dims d and d+64 of each. attn_fetch
+// loads every partial the wave needs (its heads' o_t, and lane t's (m_t, l_t)) in one round,
+// issued before the weight loads; attn_finish combines them while the weights stream in.
+// At most ATTN_MAXT splits and 16 heads (checked on the host).
+#define ATTN_MAXT 8
+struct AttnPre {
+  float o0[4][ATTN_MAXT], o1[4][ATTN_MAXT], m[4], l[4];
+};
+
+__device__ __forceinline__ void attn_fetch(const GemvArgs& a, AttnPre& p) {
   const int H = a.attn_heads, T = a.attn_splits, G = a.attn_heads / a.attn_kvh;
-  // (m, l) of every (head, split) fetched in parallel: layout [kvh][t][g][2]
-  for (int i = threadIdx.x; i < H * T; i += 256) {
-    const int h = i / T, t = i % T, kvh = h / G, g = h % G;
-    const float* ml = a.attn_ml + (((long long)kvh * T + t) * G + g) * 2;
-    wt[h][t] = ml[0];
-    lt[h][t] = ml[1];
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < H) {
-    const int h = threadIdx.x;
-    float M = -INFINITY;
-    for (int t = 0; t < T; ++t)
-      if (lt[h][t] > 0.f) M = fmaxf(M, wt[h][t]);
-    float L = 0.f;
-    for (int t = 0; t < T; ++t) {
-      const float e = lt[h][t] > 0.f ? expf(wt[h][t] - M) : 0.f;
-      wt[h][t] = e;
-      L += e * lt[h][t];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (wave + 4 * j >= H) break;   // wave-uniform
+    const int h = wave + 4 * j, kvh = h / G, g = h % G;
+    const float* po = a.attn_o + ((long long)kvh * T * G + g) * 128 + lane;
+#pragma unroll
+    for (int t = 0; t < ATTN_MAXT; ++t) {   // splits past T repeat the last one (weight 0 below)
+      const long long off = (long long)min(t, T - 1) * G * 128;
+      p.o0[j][t] = po[off];
+      p.o1[j][t] = po[off + 64];
     }
-    inv_l[h] = 1.0f / L;
+    const float* ml = a.attn_ml + (((long long)kvh * T + min(lane, T - 1)) * G + g) * 2;
+    p.m[j] = ml[0];
+    p.l[j] = ml[1];
   }
-  __syncthreads();
-  // x = sum_t w_t o_t / L; dead splits carry zero partials and zero weight, so the loads
-  // are unconditional and a thread's T loads are all in flight together
-  for (int i = threadIdx.x; i < H * 128; i += 256) {
-    const int h = i >> 7, d = i & 127, kvh = h / G, g = h % G;
-    const float* po = a.attn_o + (((long long)kvh * T) * G + g) * 128 + d;
-    float s = 0.f;
-    for (int t = 0; t < T; ++t) s += wt[h][t] * po[(long long)t * G * 128];
-    xs[i] = f32_to_bf16(s * inv_l[h]);
+}
+
+__device__ __forceinline__ void attn_finish(const GemvArgs& a, const AttnPre& p, uint16_t* xs) {
+  const int H = a.attn_heads, T = a.attn_splits;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = wave + 4 * j;
+    if (h >= H) break;   // wave-uniform
+    const float mj = (lane < T && p.l[j] > 0.f) ? p.m[j] : -INFINITY;   // dead splits weigh 0
+    const float M = wave_max(mj);
+    const float f = (mj == -INFINITY) ? 0.f : __expf(mj - M);
+    const float L = wave_sum(f * p.l[j]);
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int t = 0; t < ATTN_MAXT; ++t) {
+      const float ft = HS_RL(f, t);
+      s0 = fmaf(ft, p.o0[j][t], s0);
+      s1 = fmaf(ft, p.o1[j][t], s1);
+    }
+    xs[h * 128 + lane] = f32_to_bf16(s0 / L);
+    xs[h * 128 + 64 + lane] = f32_to_bf16(s1 / L);
   }
   __syncthreads();
 }
@@ -196,8 +217,10 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   for (int m = 0; m < MB; ++m) best[m] = 0ull;
 
   // Rounds of U chunks: every weight load of a round is issued before any is consumed,
-  // so a wave keeps U*RPW*NW 16-byte loads in flight instead of waiting on each. The
-  // first round is issued before the RMSNorm prologue, which then overlaps its latency.
+  // so a wave keeps U*RPW*NW 16-byte loads in flight instead of waiting on each. Behind a
+  // prologue the loads carry no branch: chunks past K re-read the row's last 16 bytes (one
+  // address for the whole wave), so the number of loads after the prologue's is fixed and
+  // the prologue waits for its own loads only. Without one, chunks past K are skipped.
   constexpr int U = 12 / (RPW * NW) > 0 ? 12 / (RPW * NW) : 1;   // 12 x 16 B loads per lane per round
   uint4 wv[U][RPW][NW];
   int n0 = KS > 1 ? blockIdx.x * RPW : (blockIdx.x * 4 + wave) * RPW;
@@ -209,28 +232,44 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
       for (int r = 0; r < RPW; ++r) {
         const long long n = min(n0 + r, a.N - 1);
 #pragma unroll
-        for (int u = 0; u < NW; ++u)
-          wv[c][r][u] = k < a.K ? ld_stream(W[u] + n * a.K + k) : make_uint4(0, 0, 0, 0);
+        for (int u = 0; u < NW; ++u) {
+          if constexpr (PRO != PRO_NONE)   // unconditional (offset clamped; the dot loop skips k >= K)
+            wv[c][r][u] = ld_stream(W[u] + n * a.K + min(k, a.K - 8));
+          else
+            wv[c][r][u] = k < a.K ? ld_stream(W[u] + n * a.K + k) : make_uint4(0, 0, 0, 0);
+        }
       }
     }
   };
+  // prologue loads first, then the first weight round; the prologue's math then runs while
+  // the weights are in flight (loads complete in issue order)
+  RowsPre<MB> rpre_x;
+  AttnPre apre;
+  if constexpr (PRO == PRO_NORM)
+    rows_fetch<MB>(rpre_x, (const uint16_t*)a.x + m0 * a.ldx, a.ldx, mrows, (const uint16_t*)a.norm_w, a.K, true);
+  if constexpr (PRO == PRO_ATTN) attn_fetch(a, apre);
   load_round(kstart);
-  if constexpr (PRO == PRO_NORM) norm_to_lds<MB>(a, m0, mrows, xs);
-  if constexpr (PRO == PRO_ATTN) attn_to_lds(a, xs);
+  if constexpr (PRO == PRO_NORM) rows_finish<MB>(rpre_x, mrows, a.K, a.eps, a.n_dtype, true, xs);
+  if constexpr (PRO == PRO_ATTN) attn_finish(a, apre, xs);
+  // absent epilogue operands read a valid dummy address (the weights), so the loads carry no
+  // branch and no wait; their flags are applied where the values are used
+  const uint16_t* bias_p = (a.flags & 1) ? (const uint16_t*)a.bias : W[0];
+  const uint16_t* bias2_p = (EPI == EPI_SILU && (a.flags & 4)) ? (const uint16_t*)a.bias2 : W[0];
+  const uint16_t* resid_p = EPI == EPI_RESID ? (const uint16_t*)a.resid : W[0];
   for (int blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
   n0 = KS > 1 ? blk * RPW : (blk * 4 + wave) * RPW;
   if (blk != (int)blockIdx.x) load_round(kstart);
   if (n0 >= a.N) continue;
   // epilogue operands are fetched now so their latency hides behind the weight stream
-  float bpre[RPW], b2pre[RPW], rpre[MB][RPW];
+  uint16_t bpre[RPW], b2pre[RPW], rpre[MB][RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const int n = min(n0 + r, a.N - 1);
-    bpre[r] = (a.flags & 1) ? bf(a.bias, n) : 0.f;
-    b2pre[r] = (EPI == EPI_SILU && (a.flags & 4)) ? bf(a.bias2, n) : 0.f;
+    bpre[r] = bias_p[n];
+    b2pre[r] = bias2_p[n];
 #pragma unroll
     for (int m = 0; m < MB; ++m)
-      rpre[m][r] = (EPI == EPI_RESID && m < mrows) ? bf(a.resid, (m0 + m) * a.ldr + n) : 0.f;
+      rpre[m][r] = resid_p[EPI == EPI_RESID ? (m0 + min(m, mrows - 1)) * a.ldr + n : n];
   }
   float acc[MB][RPW][NW];
 #pragma unroll
@@ -295,12 +334,12 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
       const int n = n0 + r;
       if (n >= a.N) continue;
       float v = acc[m][r][0];
-      if (a.flags & 1) v += bpre[r];
+      if (a.flags & 1) v += bf16_to_f32(bpre[r]);
       v = rbf(v);
-      if constexpr (EPI == EPI_RESID) v = rpre[m][r] + v;
+      if constexpr (EPI == EPI_RESID) v = bf16_to_f32(rpre[m][r]) + v;
       if constexpr (EPI == EPI_SILU) {
         float u = acc[m][r][1];
-        if (a.flags & 4) u += b2pre[r];
+        if (a.flags & 4) u += bf16_to_f32(b2pre[r]);
         u = rbf(u);
         const float s = rbf(v / (1.f + expf(-v)));
         v = s * u;
@@ -404,21 +443,30 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
     const int u = t - tq - tk;
     r0 = 2 * u; r1 = 2 * u + 1;
   }
-  // epilogue operands (bias, positions, rotary frequency) are fetched up front
-  const float b0 = (a.flags & 2) ? bf(B, r0) : 0.f, b1 = (a.flags & 2) ? bf(B, r1) : 0.f;
-  const long long pos_v = ld_i(a.pos_ids, 0, a.pos_dtype);
-  const long long cpos_v = ld_i(a.cache_pos, 0, a.cpos_dtype);
+  // Loads in issue order: the activation row and norm weight (the prologue) and the rotary
+  // operands, the weight rows (K <= 3072: at most 6 chunks of 512 per row), then the bias as
+  // raw bits with no branch. Loads complete in order, so the norm and the rotary factors
+  // wait only for their own loads and are computed while the weights stream in.
+  const bool norm = (a.flags & 1) != 0;
+  RowsPre<1> xp;
+  rows_fetch<1>(xp, (const uint16_t*)a.x, 0, 1, (const uint16_t*)a.norm_w, a.K, norm);
+  const IRaw pos_r = ld_i_raw(a.pos_ids, 0, a.pos_dtype);
+  const IRaw cpos_r = ld_i_raw(a.cache_pos, 0, a.cpos_dtype);
   const float invf = a.inv_freq[(r0 % D) % half];
-  // weight rows next (K <= 3072: at most 6 chunks of 512 per row), then the norm prologue
   uint4 w0[6], w1[6];
 #pragma unroll
-  for (int c = 0; c < 6; ++c) {
-    const int k = lane * 8 + c * 512;
-    w0[c] = k < a.K ? ld_stream(W + (long long)r0 * a.K + k) : make_uint4(0, 0, 0, 0);
-    w1[c] = k < a.K ? ld_stream(W + (long long)r1 * a.K + k) : make_uint4(0, 0, 0, 0);
+  for (int c = 0; c < 6; ++c) {   // no branch: chunks past K re-read the row's last 16 bytes
+    const int k = min(lane * 8 + c * 512, a.K - 8);
+    w0[c] = ld_stream(W + (long long)r0 * a.K + k);
+    w1[c] = ld_stream(W + (long long)r1 * a.K + k);
   }
-  rows_to_lds<1>((const uint16_t*)a.x, 0, 1, (const uint16_t*)a.norm_w, a.K, a.eps, a.n_dtype, (a.flags & 1) != 0, xs);
+  const uint16_t* Bp = (a.flags & 2) ? (const uint16_t*)B : W;   // W: a valid dummy address
+  const uint16_t b0r = Bp[r0], b1r = Bp[r1];
+  rows_finish<1>(xp, 1, a.K, a.eps, a.n_dtype, norm, xs);
   if (!active) return;
+  const long long pos_v = ld_i_decode(pos_r, a.pos_dtype);
+  const long long cpos_v = ld_i_decode(cpos_r, a.cpos_dtype);
+  const float b0 = (a.flags & 2) ? bf16_to_f32(b0r) : 0.f, b1 = (a.flags & 2) ? bf16_to_f32(b1r) : 0.f;
   // rotary factors now: they depend only on the position, so this runs while the weight
   // loads are still in flight instead of after the dot products
   const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));

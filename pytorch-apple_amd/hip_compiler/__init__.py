@@ -30,7 +30,8 @@ def _infer_compute_dtype(graph: IRGraph) -> str:
 
 
 def compile_subgraph(ir_dict: dict, compute_dtype: str | None = None, *, inplace_inputs: bool = True,
-                     fuse: bool = True, exact_attention: bool = False) -> HIPProgram:
+                     fuse: bool = True, exact_attention: bool = False,
+                     fold_attention: bool | None = None) -> HIPProgram:
     """Compile one IR dict (a whole graph or one device partition) into a HIPProgram.
 
     ``inplace_inputs``: let ``index_copy`` update a graph-input cache in place when nothing else
@@ -38,14 +39,17 @@ def compile_subgraph(ir_dict: dict, compute_dtype: str | None = None, *, inplace
     ``exact_attention``: decode attention repeats every CPU rounding point, including the bf16
     rounding of the softmax probabilities (two kernels and a combine-free output pass) instead of
     the default split-S kernel whose combine folds into the following projection.
+    ``fold_attention``: combine the split-S partials in the prologue of the projection that reads
+    the attention output (True) or in a kernel of their own (False); None = the default.
     """
     return compile_graph(load_ir_from_dict(ir_dict), compute_dtype, inplace_inputs=inplace_inputs, fuse=fuse,
-                         exact_attention=exact_attention)
+                         exact_attention=exact_attention, fold_attention=fold_attention)
 
 
 def compile_graph(graph: IRGraph, compute_dtype: str | None = None, *, inplace_inputs: bool = True,
-                  fuse: bool = True, exact_attention: bool = False) -> HIPProgram:
-    low = analyze_subgraph(graph, inplace_inputs=inplace_inputs, fuse=fuse, exact_attention=exact_attention)
+                  fuse: bool = True, exact_attention: bool = False, fold_attention: bool | None = None) -> HIPProgram:
+    low = analyze_subgraph(graph, inplace_inputs=inplace_inputs, fuse=fuse, exact_attention=exact_attention,
+                           fold_attention=fold_attention)
     out_views: dict[str, TView] = {}
     for spec in graph.graph_outputs:
         v = low.view(spec.name)

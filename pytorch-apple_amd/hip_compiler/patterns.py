@@ -288,7 +288,11 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     vv_ = low.contiguous(v)
     if (kv_.offset * 2) % 16 or (vv_.offset * 2) % 16:
         raise NotImplementedError("attention caches must be 16-byte aligned")
-    spl = 64                     # FL_SPL of k_attn_flash
+    # 64 positions per split (4 waves); when the combine can fold into the next GEMV's
+    # prologue (at most ATTN_MAXT = 8 splits, 16 heads) 256 positions (16 waves), which
+    # leaves 4x fewer partials for every workgroup of that GEMV to read
+    wide = low.fold_attn_combine and (S + 255) // 256 <= 8 and H <= 16
+    spl = 256 if wide else 64
     nsplit = (S + spl - 1) // spl
     margs = dict(mask=None, mask_stride=0, mask_dtype=-1)
     if mask is not None:
@@ -302,10 +306,10 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     ins = [q, k, v] + ([mask] if mask else [])
     params = {"kv_heads": kvh, "q_per_kv": G, "seq_len": S, "head_dim": D, "nsplit": nsplit, "spl": spl,
               "nodes": names}
-    low.emit(LaunchStep(kind="attention", kernel="k_attn_flash" if dt == "bfloat16" else "k_attn_flash_f16",
-                        module="attention", arg_struct="FlashArgs",
-                        args=args, grid=(nsplit, kvh, G), inputs=ins, outputs=[out.name + ".partials"],
-                        params=params))
+    kname = ("k_attn_flash_w16" if wide else "k_attn_flash") + ("" if dt == "bfloat16" else "_f16")
+    low.emit(LaunchStep(kind="attention", kernel=kname, module="attention", arg_struct="FlashArgs",
+                        args=args, grid=(nsplit, kvh, G), block=(1024 if wide else 256, 1, 1), inputs=ins,
+                        outputs=[out.name + ".partials"], params=params))
 
     def combine():
         o = low.new_storage(out.name, out.shape, out.dtype)
@@ -629,6 +633,8 @@ def _emit_qkv(low, xname, q, k, v, names) -> None:
     cpos = low.contiguous(k["cpos"])
     if inv.dtype != "float32" or pos.numel != 1:
         raise NotImplementedError("fused RoPE needs fp32 inv_freq and one position")
+    if pos.dtype not in ("int64", "int32") or cpos.dtype not in ("int64", "int32"):
+        raise NotImplementedError("fused RoPE reads int64 or int32 positions")
     H, KVH, D = q["nh"], k["nh"], q["D"]
     K = x.shape[-1]
     if K % 8 or K > 3072:

@@ -84,13 +84,16 @@ class _Chain:
 class Lowering:
     """Lowers one IR graph; ``steps``, ``storages`` and ``views`` are the result."""
 
-    def __init__(self, graph: IRGraph, inplace_inputs: bool = True, exact_attention: bool = False):
+    def __init__(self, graph: IRGraph, inplace_inputs: bool = True, exact_attention: bool = False,
+                 fold_attention: bool | None = None):
         self.g = graph
         self.inplace_inputs = inplace_inputs
         self.exact_attention = exact_attention
-        # fold the split-attention combine into the following projection's prologue (1) or
-        # emit it as its own small kernel (0); HIPRT_FOLD_ATTN overrides for measurements
-        self.fold_attn_combine = os.environ.get("HIPRT_FOLD_ATTN", "0") == "1"
+        # fold the split-attention combine into the following projection's prologue (True) or
+        # emit it as its own small kernel (False); when not given, HIPRT_FOLD_ATTN decides
+        if fold_attention is None:
+            fold_attention = os.environ.get("HIPRT_FOLD_ATTN", "1") == "1"
+        self.fold_attn_combine = fold_attention
         self.steps: list[LaunchStep] = []
         self.storages: dict[str, Storage] = {}
         self.views: dict[str, TView] = {}
@@ -379,7 +382,7 @@ class Lowering:
                 norm = None
         if norm is None and self.fold_attn_combine:
             attn = self.foldable_attn(x_name, set(nodes))
-            if attn is not None and (K != attn["H"] * 128 or attn["H"] > 12 or attn["nsplit"] > 32
+            if attn is not None and (K != attn["H"] * 128 or attn["H"] > 16 or attn["nsplit"] > 8
                                      or epi not in ("bias", "resid")):
                 attn = None
         if attn is not None:
@@ -1060,10 +1063,11 @@ class Lowering:
 
 
 def analyze_subgraph(graph: IRGraph, inplace_inputs: bool = True, fuse: bool = True,
-                     exact_attention: bool = False) -> Lowering:
+                     exact_attention: bool = False, fold_attention: bool | None = None) -> Lowering:
     from hip_compiler.patterns import DEFAULT_PATTERNS
 
-    low = Lowering(graph, inplace_inputs=inplace_inputs, exact_attention=exact_attention)
+    low = Lowering(graph, inplace_inputs=inplace_inputs, exact_attention=exact_attention,
+                   fold_attention=fold_attention)
     low.run(DEFAULT_PATTERNS if fuse else [])
     return low
 

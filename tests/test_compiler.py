@@ -58,9 +58,20 @@ def test_rmsnorm_pattern_alone_is_one_kernel():
     assert abs(eps - 1e-6) < 1e-12
 
 
-def test_attention_block_is_four_launches_with_inplace_cache():
+def test_attention_block_is_three_launches_with_inplace_cache():
+    # default: 256-position splits, combined in the o_proj prologue
     p = compile_subgraph(build_attention_ir(1025))
-    assert kernels(p) == ["k_qkv_rope", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
+    assert kernels(p) == ["k_qkv_rope", "k_attn_flash_w16", "k_gemv_attn_bias_r4"]
+    flash = p.steps[1]
+    assert flash.args["nsplit"] == 5 and flash.block == (1024, 1, 1) and flash.grid == (5, 2, 6)
+    assert p.steps[2].args["attn_splits"] == 5 and p.steps[2].args["attn_heads"] == 12
+    # separate combine kernel: 64-position splits
+    sep = compile_subgraph(build_attention_ir(1025), fold_attention=False)
+    assert kernels(sep) == ["k_qkv_rope", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
+    assert sep.steps[1].args["nsplit"] == 17
+    # more than 8 splits of 256 do not fit the prologue: the separate combine is kept
+    long = compile_subgraph(build_attention_ir(4096))
+    assert kernels(long) == ["k_qkv_rope", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
     assert set(p.stats["mutated_inputs"]) == {"past_key_0", "past_value_0"}
     assert p.output_views["index_copy"].storage == "past_key_0"
     exact = compile_subgraph(build_attention_ir(1025), exact_attention=True)
@@ -72,7 +83,7 @@ def test_attention_block_is_four_launches_with_inplace_cache():
 def test_decode_step_launch_count_and_cache_aliasing():
     cfg = QwenConfig(layers=3)
     p = compile_subgraph(build_decode_ir(256, cfg, argmax=True))
-    assert len(p.steps) == 1 + 6 * cfg.layers + 2      # embedding, 6 per layer, lm_head+argmax, finalize
+    assert len(p.steps) == 1 + 5 * cfg.layers + 2      # embedding, 5 per layer, lm_head+argmax, finalize
     assert kernels(p)[0] == "k_embedding" and kernels(p)[-2:] == ["k_gemv_norm_argmax_r4", "k_argmax_finalize"]
     assert len(p.stats["mutated_inputs"]) == 2 * cfg.layers
     assert not any(s.kernel in ("k_rope_table", "k_rmsnorm", "k_copy") for s in p.steps)

@@ -32,14 +32,15 @@ def close(got, ref, rtol=RTOL):
     return err / scale
 
 
-def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True, exact=False):
+def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True, exact=False, fold=None):
     from hip_compiler import compile_subgraph, is_hip_op_supported
     from npu_compiler import partition
     from npu_runtime import DAGExecutor
 
     fn = supported or (lambda op, a=None: is_hip_op_supported(op, a) and op not in force_cpu)
     ex = DAGExecutor(partition(ir, fn), backend,
-                     compile_fn=lambda sub: compile_subgraph(sub, fuse=fuse, exact_attention=exact))
+                     compile_fn=lambda sub: compile_subgraph(sub, fuse=fuse, exact_attention=exact,
+                                                             fold_attention=fold))
     ex.load_weights(weights)
     out = ex.execute(inputs)
     return {k: (v if isinstance(v, np.ndarray) else v.to_numpy()) for k, v in out.items()}, ex
@@ -108,10 +109,14 @@ def test_attention_block_cfg2(backend, exact):
             assert np.array_equal(got[k][:, :, keep], src[:, :, keep])
 
 
-@pytest.mark.parametrize("exact", [False, True])
-@pytest.mark.parametrize("valid", [1, 10, 64, 65, 1000])
-def test_decode_attention_kernel_vs_closed_form(backend, valid, exact):
-    """The fused split-KV kernel against the closed form of tests/test_extended_kernels.py:621-640."""
+@pytest.mark.parametrize("mode", ["split", "fold", "exact"])
+@pytest.mark.parametrize("valid", [1, 10, 64, 65, 257, 1000])
+def test_decode_attention_kernel_vs_closed_form(backend, valid, mode):
+    """The fused split-KV kernel against the closed form of tests/test_extended_kernels.py:621-640.
+
+    ``split``: 64-position splits and a combine kernel; ``fold``: 256-position splits whose
+    combine runs in the o_proj prologue (valid=1 leaves 3 of the 4 splits fully masked);
+    ``exact``: the two-pass path that repeats every CPU rounding point."""
     from irgen.qwen import QwenConfig, build_attention_ir
     from irgen.workloads import attention_inputs, decode_mask, make_weights
     from oracle.numpy_ref import run_ir
@@ -125,7 +130,12 @@ def test_decode_attention_kernel_vs_closed_form(backend, valid, exact):
     x["position_ids"][:] = valid - 1
     x["cache_position"][:] = valid - 1
     x = host(x)
-    got, _ = run_hip(ir, x, w, backend, exact=exact)
+    got, ex = run_hip(ir, x, w, backend, exact=mode == "exact", fold=mode == "fold")
+    kernels = {st.kernel for p in ex.npu_programs.values() for st in p.steps}
+    if mode == "fold":
+        assert "k_attn_flash_w16" in kernels and "k_attn_combine" not in kernels
+    elif mode == "split":
+        assert "k_attn_flash" in kernels and "k_attn_combine" in kernels
     orc = run_ir(ir, x, w)
     for k in got:
         if not k.startswith("index_copy"):
@@ -305,7 +315,8 @@ def test_attention_block_unfused_generic_path(backend):
         close(got[k], ref[k])
 
 
-def test_full_decode_step_real_dims(backend):
+@pytest.mark.parametrize("fold", [False, True])
+def test_full_decode_step_real_dims(backend, fold):
     """cfg3 shapes (hidden 1536, vocab 151936, GQA 12/2, head 128) with 2 layers, vs the CPU fallback."""
     from irgen.qwen import QwenConfig, build_decode_ir
     from irgen.workloads import decode_inputs, make_weights
@@ -314,7 +325,7 @@ def test_full_decode_step_real_dims(backend):
     ir = build_decode_ir(2048, cfg, argmax=True)
     w = host(make_weights(ir, cfg))
     x = host(decode_inputs(2048, 1984, cfg))
-    got, ex = run_hip(ir, x, w, backend)
+    got, ex = run_hip(ir, x, w, backend, fold=fold)
     assert_all_npu(ex)
     ref = run_cpu(ir, x, w)
     logits = ir["graph_outputs"][0]["name"]
