@@ -462,21 +462,18 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   }
   const uint16_t* Bp = (a.flags & 2) ? (const uint16_t*)B : W;   // W: a valid dummy address
   const uint16_t b0r = Bp[r0], b1r = Bp[r1];
+  // rotary factors of angle inv_freq * position (fp32 product, as the reference forms it),
+  // computed for every task with no branch or table load, so that neither the frequency load
+  // nor a wait moves behind the weight loads; tasks without rotation ignore them
+  const long long pos_v = ld_i_decode(pos_r, a.pos_dtype);
+  float sf, cf;
+  sincos_rot(invf * (float)pos_v, &sf, &cf);
   rows_finish<1>(xp, 1, a.K, a.eps, a.n_dtype, norm, xs);
   if (!active) return;
-  const long long pos_v = ld_i_decode(pos_r, a.pos_dtype);
   const long long cpos_v = ld_i_decode(cpos_r, a.cpos_dtype);
   const float b0 = (a.flags & 2) ? bf16_to_f32(b0r) : 0.f, b1 = (a.flags & 2) ? bf16_to_f32(b1r) : 0.f;
-  // rotary factors now: they depend only on the position, so this runs while the weight
-  // loads are still in flight instead of after the dot products
   const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
-  float rc = 1.f, rs = 0.f;
-  if (rope) {
-    float sf, cf;
-    sincosf(invf * (float)pos_v, &sf, &cf);
-    rc = round_to(cf * a.rope_scaling, HS_BF16);
-    rs = round_to(sf * a.rope_scaling, HS_BF16);
-  }
+  const float rc = round_to(cf * a.rope_scaling, HS_BF16), rs = round_to(sf * a.rope_scaling, HS_BF16);
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
   for (int c = 0; c < 6; ++c) {
