@@ -269,7 +269,10 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) k_attn_flash(const FlashArgs a) { flash_body<HS_BF16, 4>(a); }
 extern "C" __global__ void __launch_bounds__(256) k_attn_flash_f16(const FlashArgs a) { flash_body<HS_F16, 4>(a); }
-// 16 waves, 256 positions per split: 4x fewer partials, for a combine folded into the next GEMV
+// 8 or 16 waves, 128 or 256 positions per split: 2x or 4x fewer partials, for a combine folded
+// into the next GEMV
+extern "C" __global__ void __launch_bounds__(512) k_attn_flash_w8(const FlashArgs a) { flash_body<HS_BF16, 8>(a); }
+extern "C" __global__ void __launch_bounds__(512) k_attn_flash_w8_f16(const FlashArgs a) { flash_body<HS_F16, 8>(a); }
 extern "C" __global__ void __launch_bounds__(1024) k_attn_flash_w16(const FlashArgs a) { flash_body<HS_BF16, 16>(a); }
 extern "C" __global__ void __launch_bounds__(1024) k_attn_flash_w16_f16(const FlashArgs a) { flash_body<HS_F16, 16>(a); }
 

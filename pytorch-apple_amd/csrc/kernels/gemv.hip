@@ -140,46 +140,48 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
 // Wave w combines heads w, w+4, w+8, w+12; lane d holds dims d and d+64 of each. attn_fetch
 // loads every partial the wave needs (its heads' o_t, and lane t's (m_t, l_t)) in one round,
 // issued before the weight loads; attn_finish combines them while the weights stream in.
-// At most ATTN_MAXT splits and 16 heads (checked on the host).
-#define ATTN_MAXT 8
+// At most T splits (8 or 16) and 16 heads (checked on the host).
+template <int T>
 struct AttnPre {
-  float o0[4][ATTN_MAXT], o1[4][ATTN_MAXT], m[4], l[4];
+  float o0[4][T], o1[4][T], m[4], l[4];
 };
 
-__device__ __forceinline__ void attn_fetch(const GemvArgs& a, AttnPre& p) {
-  const int H = a.attn_heads, T = a.attn_splits, G = a.attn_heads / a.attn_kvh;
+template <int T>
+__device__ __forceinline__ void attn_fetch(const GemvArgs& a, AttnPre<T>& p) {
+  const int H = a.attn_heads, NT = a.attn_splits, G = a.attn_heads / a.attn_kvh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (wave + 4 * j >= H) break;   // wave-uniform
     const int h = wave + 4 * j, kvh = h / G, g = h % G;
-    const float* po = a.attn_o + ((long long)kvh * T * G + g) * 128 + lane;
+    const float* po = a.attn_o + ((long long)kvh * NT * G + g) * 128 + lane;
 #pragma unroll
-    for (int t = 0; t < ATTN_MAXT; ++t) {   // splits past T repeat the last one (weight 0 below)
-      const long long off = (long long)min(t, T - 1) * G * 128;
+    for (int t = 0; t < T; ++t) {   // splits past NT repeat the last one (weight 0 below)
+      const long long off = (long long)min(t, NT - 1) * G * 128;
       p.o0[j][t] = po[off];
       p.o1[j][t] = po[off + 64];
     }
-    const float* ml = a.attn_ml + (((long long)kvh * T + min(lane, T - 1)) * G + g) * 2;
+    const float* ml = a.attn_ml + (((long long)kvh * NT + min(lane, NT - 1)) * G + g) * 2;
     p.m[j] = ml[0];
     p.l[j] = ml[1];
   }
 }
 
-__device__ __forceinline__ void attn_finish(const GemvArgs& a, const AttnPre& p, uint16_t* xs) {
-  const int H = a.attn_heads, T = a.attn_splits;
+template <int T>
+__device__ __forceinline__ void attn_finish(const GemvArgs& a, const AttnPre<T>& p, uint16_t* xs) {
+  const int H = a.attn_heads, NT = a.attn_splits;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int h = wave + 4 * j;
     if (h >= H) break;   // wave-uniform
-    const float mj = (lane < T && p.l[j] > 0.f) ? p.m[j] : -INFINITY;   // dead splits weigh 0
+    const float mj = (lane < NT && p.l[j] > 0.f) ? p.m[j] : -INFINITY;   // dead splits weigh 0
     const float M = wave_max(mj);
     const float f = (mj == -INFINITY) ? 0.f : __expf(mj - M);
     const float L = wave_sum(f * p.l[j]);
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int t = 0; t < ATTN_MAXT; ++t) {
+    for (int t = 0; t < T; ++t) {
       const float ft = HS_RL(f, t);
       s0 = fmaf(ft, p.o0[j][t], s0);
       s1 = fmaf(ft, p.o1[j][t], s1);
@@ -190,7 +192,7 @@ __device__ __forceinline__ void attn_finish(const GemvArgs& a, const AttnPre& p,
   __syncthreads();
 }
 
-enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ATTN = 2 };
+enum { PRO_NONE = 0, PRO_NORM = 1, PRO_ATTN = 2, PRO_ATTN16 = 3 };   // ATTN: <= 8 splits, ATTN16: <= 16
 
 // KS > 1: the 4 waves of a workgroup share the same RPW rows and split K (chunk c goes to
 // wave c % 4); the per-wave partial sums are added in LDS. Used for long rows (K = 8960),
@@ -243,14 +245,15 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   };
   // prologue loads first, then the first weight round; the prologue's math then runs while
   // the weights are in flight (loads complete in issue order)
+  constexpr int AT = PRO == PRO_ATTN16 ? 16 : 8;
   RowsPre<MB> rpre_x;
-  AttnPre apre;
+  AttnPre<AT> apre;
   if constexpr (PRO == PRO_NORM)
     rows_fetch<MB>(rpre_x, (const uint16_t*)a.x + m0 * a.ldx, a.ldx, mrows, (const uint16_t*)a.norm_w, a.K, true);
-  if constexpr (PRO == PRO_ATTN) attn_fetch(a, apre);
+  if constexpr (PRO >= PRO_ATTN) attn_fetch<AT>(a, apre);
   load_round(kstart);
   if constexpr (PRO == PRO_NORM) rows_finish<MB>(rpre_x, mrows, a.K, a.eps, a.n_dtype, true, xs);
-  if constexpr (PRO == PRO_ATTN) attn_finish(a, apre, xs);
+  if constexpr (PRO >= PRO_ATTN) attn_finish<AT>(a, apre, xs);
   // absent epilogue operands read a valid dummy address (the weights), so the loads carry no
   // branch and no wait; their flags are applied where the values are used
   const uint16_t* bias_p = (a.flags & 1) ? (const uint16_t*)a.bias : W[0];
@@ -387,8 +390,10 @@ GEMV_KERNEL(k_gemv_resid_m4, false, EPI_RESID, 2, 4)
 GEMV_KERNEL(k_gemv_norm_bias_m4, true, EPI_BIAS, 2, 4)
 GEMV_KERNEL(k_gemv_norm_silu_m4, true, EPI_SILU, 1, 4)
 GEMV_KERNEL(k_gemv_silu_m4, false, EPI_SILU, 1, 4)
-GEMV_KERNEL(k_gemv_attn_bias_r4, PRO_ATTN, EPI_BIAS, 4, 1)
-GEMV_KERNEL(k_gemv_attn_resid_r4, PRO_ATTN, EPI_RESID, 4, 1)
+GEMV_KERNEL(k_gemv_attn_bias_r2, PRO_ATTN, EPI_BIAS, 2, 1)
+GEMV_KERNEL(k_gemv_attn_resid_r2, PRO_ATTN, EPI_RESID, 2, 1)
+GEMV_KERNEL(k_gemv_attn16_bias_r2, PRO_ATTN16, EPI_BIAS, 2, 1)
+GEMV_KERNEL(k_gemv_attn16_resid_r2, PRO_ATTN16, EPI_RESID, 2, 1)
 
 // One workgroup per activation row: the largest of the row's per-workgroup keys is the
 // maximum logit with the smallest index among equal maxima (np.argmax's rule).

@@ -288,11 +288,15 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     vv_ = low.contiguous(v)
     if (kv_.offset * 2) % 16 or (vv_.offset * 2) % 16:
         raise NotImplementedError("attention caches must be 16-byte aligned")
-    # 64 positions per split (4 waves); when the combine can fold into the next GEMV's
-    # prologue (at most ATTN_MAXT = 8 splits, 16 heads) 256 positions (16 waves), which
-    # leaves 4x fewer partials for every workgroup of that GEMV to read
-    wide = low.fold_attn_combine and (S + 255) // 256 <= 8 and H <= 16
-    spl = 256 if wide else 64
+    # 64 positions per split (4 waves) with a combine kernel; when the combine can fold into
+    # the next GEMV's prologue (at most 16 splits and 16 heads) 128 positions (8 waves, up to
+    # S = 2048) or 256 (16 waves, up to S = 4096), which leaves 2x / 4x fewer partials for every
+    # workgroup of that GEMV to read (measured at S = 2048: 8 waves + 16-split fold 9.2 us,
+    # 16 waves + 8-split fold 9.6 us, 4 waves + combine + o_proj 12.5 us)
+    waves = 4
+    if low.fold_attn_combine and H <= 16:
+        waves = 8 if S <= 16 * 128 else (16 if S <= 16 * 256 else 4)
+    spl = 16 * waves
     nsplit = (S + spl - 1) // spl
     margs = dict(mask=None, mask_stride=0, mask_dtype=-1)
     if mask is not None:
@@ -306,9 +310,10 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     ins = [q, k, v] + ([mask] if mask else [])
     params = {"kv_heads": kvh, "q_per_kv": G, "seq_len": S, "head_dim": D, "nsplit": nsplit, "spl": spl,
               "nodes": names}
-    kname = ("k_attn_flash_w16" if wide else "k_attn_flash") + ("" if dt == "bfloat16" else "_f16")
+    kname = {4: "k_attn_flash", 8: "k_attn_flash_w8", 16: "k_attn_flash_w16"}[waves] + \
+        ("" if dt == "bfloat16" else "_f16")
     low.emit(LaunchStep(kind="attention", kernel=kname, module="attention", arg_struct="FlashArgs",
-                        args=args, grid=(nsplit, kvh, G), block=(1024 if wide else 256, 1, 1), inputs=ins,
+                        args=args, grid=(nsplit, kvh, G), block=(64 * waves, 1, 1), inputs=ins,
                         outputs=[out.name + ".partials"], params=params))
 
     def combine():

@@ -114,8 +114,8 @@ def test_attention_block_cfg2(backend, exact):
 def test_decode_attention_kernel_vs_closed_form(backend, valid, mode):
     """The fused split-KV kernel against the closed form of tests/test_extended_kernels.py:621-640.
 
-    ``split``: 64-position splits and a combine kernel; ``fold``: 256-position splits whose
-    combine runs in the o_proj prologue (valid=1 leaves 3 of the 4 splits fully masked);
+    ``split``: 64-position splits and a combine kernel; ``fold``: 128-position splits whose
+    combine runs in the o_proj prologue (valid=1 leaves 7 of the 8 splits fully masked);
     ``exact``: the two-pass path that repeats every CPU rounding point."""
     from irgen.qwen import QwenConfig, build_attention_ir
     from irgen.workloads import attention_inputs, decode_mask, make_weights
@@ -133,9 +133,33 @@ def test_decode_attention_kernel_vs_closed_form(backend, valid, mode):
     got, ex = run_hip(ir, x, w, backend, exact=mode == "exact", fold=mode == "fold")
     kernels = {st.kernel for p in ex.npu_programs.values() for st in p.steps}
     if mode == "fold":
-        assert "k_attn_flash_w16" in kernels and "k_attn_combine" not in kernels
+        assert "k_attn_flash_w8" in kernels and "k_attn_combine" not in kernels
     elif mode == "split":
         assert "k_attn_flash" in kernels and "k_attn_combine" in kernels
+    orc = run_ir(ir, x, w)
+    for k in got:
+        if not k.startswith("index_copy"):
+            close(got[k], orc[k])
+
+
+@pytest.mark.parametrize("valid", [5, 1500, 3000])
+def test_decode_attention_wide_splits_vs_closed_form(backend, valid):
+    """S = 3000: 256-position splits (16 waves), 12 of them, folded by the 16-split o_proj prologue."""
+    from irgen.qwen import QwenConfig, build_attention_ir
+    from irgen.workloads import attention_inputs, decode_mask, make_weights
+    from oracle.numpy_ref import run_ir
+
+    S = 3000
+    ir = build_attention_ir(S, QwenConfig())
+    w = host(make_weights(ir))
+    x = attention_inputs(S)
+    x["attention_mask"] = decode_mask(S, valid - 1)
+    x["position_ids"][:] = valid - 1
+    x["cache_position"][:] = valid - 1
+    x = host(x)
+    got, ex = run_hip(ir, x, w, backend)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert "k_attn_flash_w16" in kernels and "k_gemv_attn16_bias_r2" in kernels
     orc = run_ir(ir, x, w)
     for k in got:
         if not k.startswith("index_copy"):
