@@ -252,6 +252,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
     rows_fetch<MB>(rpre_x, (const uint16_t*)a.x + m0 * a.ldx, a.ldx, mrows, (const uint16_t*)a.norm_w, a.K, true);
   if constexpr (PRO >= PRO_ATTN) attn_fetch<AT>(a, apre);
   load_round(kstart);
+  if constexpr (PRO != PRO_NONE) __builtin_amdgcn_sched_barrier(0);   // loads issued before the prologue math
   if constexpr (PRO == PRO_NORM) rows_finish<MB>(rpre_x, mrows, a.K, a.eps, a.n_dtype, true, xs);
   if constexpr (PRO >= PRO_ATTN) attn_finish<AT>(a, apre, xs);
   // absent epilogue operands read a valid dummy address (the weights), so the loads carry no
@@ -467,12 +468,16 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   }
   const uint16_t* Bp = (a.flags & 2) ? (const uint16_t*)B : W;   // W: a valid dummy address
   const uint16_t b0r = Bp[r0], b1r = Bp[r1];
+  __builtin_amdgcn_sched_barrier(0);   // every load above is issued before the arithmetic below
   // rotary factors of angle inv_freq * position (fp32 product, as the reference forms it),
   // computed for every task with no branch or table load, so that neither the frequency load
   // nor a wait moves behind the weight loads; tasks without rotation ignore them
   const long long pos_v = ld_i_decode(pos_r, a.pos_dtype);
   float sf, cf;
   sincos_rot(invf * (float)pos_v, &sf, &cf);
+  // an empty use keeps the factors here: otherwise they are sunk into the lane-0 epilogue and
+  // computed after the dot products, on the kernel's critical path
+  asm volatile("" ::"v"(sf), "v"(cf));
   rows_finish<1>(xp, 1, a.K, a.eps, a.n_dtype, norm, xs);
   if (!active) return;
   const long long cpos_v = ld_i_decode(cpos_r, a.cpos_dtype);
