@@ -375,6 +375,47 @@ struct AttnOutArgs {          // second attention pass: global softmax and p.V p
   int pad;
 };
 
+// host and device (the rotary sincos below is also built into a host test helper)
+#ifdef __HIPCC__
+#define HS_HD __host__ __device__
+#else
+#define HS_HD
+#endif
+
+// sin and cos of an fp32 angle (|x| < 2^30), branch-free and table-free so that no load or
+// wait enters the caller's critical path: Cody-Waite reduction by pi/2 in double (k*pi/2 with
+// a two-part pi/2), Taylor polynomials in double on |r| <= pi/4 (truncation error < 1e-17),
+// quadrant by selects, then one rounding to fp32.
+HS_HD inline void sincos_rot(float xf, float* s_out, float* c_out) {
+  const double x = (double)xf;
+  const double q = __builtin_rint(x * 0.63661977236758134308);   // 2/pi
+  double r = __builtin_fma(-q, 1.57079632679489655800e+00, x);     // pi/2, high part
+  r = __builtin_fma(-q, 6.12323399573676603587e-17, r);             // pi/2, low part
+  const double r2 = r * r;
+  // sin r = r (1 - r2/3! + r2^2/5! - ... - r2^7/15!),  cos r = 1 - r2/2! + ... + r2^8/16!
+  double ps = -7.6471637318198164759e-13;                            // -1/15!
+  ps = __builtin_fma(ps, r2, 1.6059043836821614599e-10);             //  1/13!
+  ps = __builtin_fma(ps, r2, -2.5052108385441718775e-08);            // -1/11!
+  ps = __builtin_fma(ps, r2, 2.7557319223985890653e-06);             //  1/9!
+  ps = __builtin_fma(ps, r2, -1.9841269841269841270e-04);            // -1/7!
+  ps = __builtin_fma(ps, r2, 8.3333333333333333333e-03);             //  1/5!
+  ps = __builtin_fma(ps, r2, -1.6666666666666666667e-01);            // -1/3!
+  const double sn = __builtin_fma(ps * r2, r, r);
+  double pc = 4.7794773323873852974e-14;                             //  1/16!
+  pc = __builtin_fma(pc, r2, -1.1470745597729724714e-11);            // -1/14!
+  pc = __builtin_fma(pc, r2, 2.0876756987868098979e-09);             //  1/12!
+  pc = __builtin_fma(pc, r2, -2.7557319223985890653e-07);            // -1/10!
+  pc = __builtin_fma(pc, r2, 2.4801587301587301587e-05);             //  1/8!
+  pc = __builtin_fma(pc, r2, -1.3888888888888888889e-03);            // -1/6!
+  pc = __builtin_fma(pc, r2, 4.1666666666666666667e-02);             //  1/4!
+  pc = __builtin_fma(pc, r2, -0.5);                                  // -1/2!
+  const double cs = __builtin_fma(pc, r2, 1.0);
+  const int k = (int)((long long)q & 3);   // x = k*pi/2 + r (mod 2 pi)
+  const double sv = (k & 1) ? cs : sn, cv = (k & 1) ? sn : cs;
+  *s_out = (float)((k & 2) ? -sv : sv);
+  *c_out = (float)(((k + 1) & 2) ? -cv : cv);
+}
+
 #ifdef __HIPCC__
 // ---------------------------------------------------------------- device helpers
 
@@ -440,40 +481,6 @@ __device__ __forceinline__ FRaw ld_f_raw(const void* p, long long i, int dt) {
 __device__ __forceinline__ float ld_f_decode(FRaw r, int dt) {
   if (dt == HS_F32) return __uint_as_float(((uint32_t)r.hi << 16) | r.lo);
   return dt == HS_BF16 ? bf16_to_f32(r.lo) : f16_to_f32(r.lo);
-}
-
-// sin and cos of an fp32 angle (|x| < 2^30), branch-free and table-free so that no load or
-// wait enters the caller's critical path: Cody-Waite reduction by pi/2 in double (k*pi/2 with
-// a two-part pi/2), Taylor polynomials in double on |r| <= pi/4 (truncation error < 1e-17),
-// quadrant by selects, then one rounding to fp32.
-__host__ __device__ inline void sincos_rot(float xf, float* s_out, float* c_out) {
-  const double x = (double)xf;
-  const double q = __builtin_rint(x * 0.63661977236758134308);   // 2/pi
-  double r = __builtin_fma(-q, 1.57079632679489655800e+00, x);     // pi/2, high part
-  r = __builtin_fma(-q, 6.12323399573676603587e-17, r);             // pi/2, low part
-  const double r2 = r * r;
-  // sin r = r (1 - r2/3! + r2^2/5! - ... - r2^7/15!),  cos r = 1 - r2/2! + ... + r2^8/16!
-  double ps = -7.6471637318198164759e-13;                            // -1/15!
-  ps = __builtin_fma(ps, r2, 1.6059043836821614599e-10);             //  1/13!
-  ps = __builtin_fma(ps, r2, -2.5052108385441718775e-08);            // -1/11!
-  ps = __builtin_fma(ps, r2, 2.7557319223985890653e-06);             //  1/9!
-  ps = __builtin_fma(ps, r2, -1.9841269841269841270e-04);            // -1/7!
-  ps = __builtin_fma(ps, r2, 8.3333333333333333333e-03);             //  1/5!
-  ps = __builtin_fma(ps, r2, -1.6666666666666666667e-01);            // -1/3!
-  const double sn = __builtin_fma(ps * r2, r, r);
-  double pc = 4.7794773323873852974e-14;                             //  1/16!
-  pc = __builtin_fma(pc, r2, -1.1470745597729724714e-11);            // -1/14!
-  pc = __builtin_fma(pc, r2, 2.0876756987868098979e-09);             //  1/12!
-  pc = __builtin_fma(pc, r2, -2.7557319223985890653e-07);            // -1/10!
-  pc = __builtin_fma(pc, r2, 2.4801587301587301587e-05);             //  1/8!
-  pc = __builtin_fma(pc, r2, -1.3888888888888888889e-03);            // -1/6!
-  pc = __builtin_fma(pc, r2, 4.1666666666666666667e-02);             //  1/4!
-  pc = __builtin_fma(pc, r2, -0.5);                                  // -1/2!
-  const double cs = __builtin_fma(pc, r2, 1.0);
-  const int k = (int)((long long)q & 3);   // x = k*pi/2 + r (mod 2 pi)
-  const double sv = (k & 1) ? cs : sn, cv = (k & 1) ? sn : cs;
-  *s_out = (float)((k & 2) ? -sv : sv);
-  *c_out = (float)(((k + 1) & 2) ? -cv : cv);
 }
 
 // round a float to the storage precision of dt (identity for fp32); both roundings are single

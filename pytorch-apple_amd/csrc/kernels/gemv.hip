@@ -284,6 +284,17 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
       for (int u = 0; u < NW; ++u) acc[m][r][u] = 0.f;
   for (int kb = kstart; kb < a.K; kb += 512 * U * KS) {
     if (kb != kstart) load_round(kb);
+    // activations from global memory: the whole round's chunks are loaded before any is used
+    // (offsets clamped, no branch), so they take one round trip, not one per chunk
+    uint4 xr[NORM ? 1 : MB][NORM ? 1 : U];
+    if constexpr (!NORM) {
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int c = 0; c < U; ++c)
+          xr[m][c] = *(const uint4*)((const uint16_t*)a.x + (m0 + min(m, mrows - 1)) * a.ldx +
+                                     min(kb + c * 512 * KS, a.K - 8));
+    }
 #pragma unroll
     for (int c = 0; c < U; ++c) {
       const int k = kb + c * 512 * KS;
@@ -293,7 +304,7 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
         if (m < mrows) {
           uint4 xv;
           if constexpr (NORM) xv = *(const uint4*)(xs + m * a.K + k);
-          else xv = *(const uint4*)((const uint16_t*)a.x + (m0 + m) * a.ldx + k);
+          else xv = xr[m][c];
 #pragma unroll
           for (int r = 0; r < RPW; ++r)
 #pragma unroll
