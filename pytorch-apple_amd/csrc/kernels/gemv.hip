@@ -436,7 +436,9 @@ extern "C" __global__ void __launch_bounds__(256) k_argmax_finalize(const Argmax
 // One wave per task; a task is a pair of weight rows:
 //   q and k: rows (h*D + j, h*D + j + D/2) of one head, rotated together;
 //   v:       rows (2t, 2t+1), plain.
-extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
+// QC: 16-byte chunks of 512 elements per weight row and lane (K <= 512 * QC)
+template <int QC>
+__device__ __forceinline__ void qkv_body(const QKVArgs& a) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[3072];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -461,7 +463,7 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
     r0 = 2 * u; r1 = 2 * u + 1;
   }
   // Loads in issue order: the activation row and norm weight (the prologue) and the rotary
-  // operands, the weight rows (K <= 3072: at most 6 chunks of 512 per row), then the bias as
+  // operands, the weight rows (QC chunks of 512 per row), then the bias as
   // raw bits with no branch. Loads complete in order, so the norm and the rotary factors
   // wait only for their own loads and are computed while the weights stream in.
   const bool norm = (a.flags & 1) != 0;
@@ -470,9 +472,9 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   const IRaw pos_r = ld_i_raw(a.pos_ids, 0, a.pos_dtype);
   const IRaw cpos_r = ld_i_raw(a.cache_pos, 0, a.cpos_dtype);
   const float invf = a.inv_freq[(r0 % D) % half];
-  uint4 w0[6], w1[6];
+  uint4 w0[QC], w1[QC];
 #pragma unroll
-  for (int c = 0; c < 6; ++c) {   // no branch: chunks past K re-read the row's last 16 bytes
+  for (int c = 0; c < QC; ++c) {   // no branch: chunks past K re-read the row's last 16 bytes
     const int k = min(lane * 8 + c * 512, a.K - 8);
     w0[c] = ld_stream(W + (long long)r0 * a.K + k);
     w1[c] = ld_stream(W + (long long)r1 * a.K + k);
@@ -497,7 +499,7 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
   const float rc = round_to(cf * a.rope_scaling, HS_BF16), rs = round_to(sf * a.rope_scaling, HS_BF16);
   float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-  for (int c = 0; c < 6; ++c) {
+  for (int c = 0; c < QC; ++c) {
     const int k = lane * 8 + c * 512;
     if (k < a.K) {
       const uint4 xv = *(const uint4*)(xs + k);
@@ -536,3 +538,6 @@ extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) {
     ((uint16_t*)dst)[r1] = f32_to_bf16(v1);
   }
 }
+
+extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) { qkv_body<6>(a); }       // K <= 3072
+extern "C" __global__ void __launch_bounds__(256) k_qkv_rope_k1536(const QKVArgs a) { qkv_body<3>(a); } // K <= 1536

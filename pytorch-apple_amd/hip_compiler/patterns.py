@@ -661,7 +661,9 @@ def _emit_qkv(low, xname, q, k, v, names) -> None:
                 rope_scaling=float(rope.attrs.get("attention_scaling", 1.0)))
     tasks = (H * D + 2 * KVH * D) // 2
     ins = [norm["x"] if norm else xname, q["w"].name, k["w"].name, v["w"].name, k["cpos"], k["past"], v["past"]]
-    low.emit(LaunchStep(kind="gemv", kernel="k_qkv_rope", module="gemv", arg_struct="QKVArgs", args=args,
+    # three 512-element chunks per weight row and lane cover K <= 1536 (no chunk past K is issued)
+    low.emit(LaunchStep(kind="gemv", kernel="k_qkv_rope_k1536" if K <= 1536 else "k_qkv_rope", module="gemv",
+                        arg_struct="QKVArgs", args=args,
                         grid=((tasks + 3) // 4, 1, 1), inputs=ins,
                         outputs=[q["out"], k["ic"].outputs[0].name, v["ic"].outputs[0].name],
                         params={"M": 1, "N": H * D + 2 * KVH * D, "K": K, "epilogue": "qkv_rope",

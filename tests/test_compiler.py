@@ -61,28 +61,28 @@ def test_rmsnorm_pattern_alone_is_one_kernel():
 def test_attention_block_is_three_launches_with_inplace_cache():
     # default: 128-position splits (8 waves), combined in the o_proj prologue
     p = compile_subgraph(build_attention_ir(1025))
-    assert kernels(p) == ["k_qkv_rope", "k_attn_flash_w8", "k_gemv_attn16_bias_r2"]
+    assert kernels(p) == ["k_qkv_rope_k1536", "k_attn_flash_w8", "k_gemv_attn16_bias_r2"]
     flash = p.steps[1]
     assert flash.args["nsplit"] == 9 and flash.block == (512, 1, 1) and flash.grid == (9, 2, 6)
     assert p.steps[2].args["attn_splits"] == 9 and p.steps[2].args["attn_heads"] == 12
     # up to 8 splits: the 8-split prologue
     short = compile_subgraph(build_attention_ir(256))
-    assert kernels(short) == ["k_qkv_rope", "k_attn_flash_w8", "k_gemv_attn_bias_r2"]
+    assert kernels(short) == ["k_qkv_rope_k1536", "k_attn_flash_w8", "k_gemv_attn_bias_r2"]
     # 2048 < S <= 4096: 256-position splits (16 waves), at most 16 of them
     mid = compile_subgraph(build_attention_ir(4096))
-    assert kernels(mid) == ["k_qkv_rope", "k_attn_flash_w16", "k_gemv_attn16_bias_r2"]
+    assert kernels(mid) == ["k_qkv_rope_k1536", "k_attn_flash_w16", "k_gemv_attn16_bias_r2"]
     assert mid.steps[1].args["nsplit"] == 16 and mid.steps[1].block == (1024, 1, 1)
     # separate combine kernel: 64-position splits
     sep = compile_subgraph(build_attention_ir(1025), fold_attention=False)
-    assert kernels(sep) == ["k_qkv_rope", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
+    assert kernels(sep) == ["k_qkv_rope_k1536", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
     assert sep.steps[1].args["nsplit"] == 17
     # more than 16 splits of 256 do not fit the prologue: the separate combine is kept
     long = compile_subgraph(build_attention_ir(4097))
-    assert kernels(long) == ["k_qkv_rope", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
+    assert kernels(long) == ["k_qkv_rope_k1536", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
     assert set(p.stats["mutated_inputs"]) == {"past_key_0", "past_value_0"}
     assert p.output_views["index_copy"].storage == "past_key_0"
     exact = compile_subgraph(build_attention_ir(1025), exact_attention=True)
-    assert kernels(exact) == ["k_qkv_rope", "k_attn_scores", "k_attn_out", "k_gemv_bias_r1"]
+    assert kernels(exact) == ["k_qkv_rope_k1536", "k_attn_scores", "k_attn_out", "k_gemv_bias_r1"]
     gen = compile_subgraph(build_attention_ir(1025), fuse=False)
     assert "k_index_copy" in kernels(gen) and "k_bmm" in kernels(gen)
 

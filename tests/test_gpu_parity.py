@@ -166,6 +166,27 @@ def test_decode_attention_wide_splits_vs_closed_form(backend, valid):
             close(got[k], orc[k])
 
 
+def test_attention_block_hidden_2048(backend):
+    """A wider model (hidden 2048, 16 query heads, 2 KV heads): the 6-chunk q/k/v kernel (K <= 3072)
+    and the attention combine for 16 heads, against the CPU fallback and the oracle."""
+    from irgen.qwen import QwenConfig, build_attention_ir
+    from irgen.workloads import attention_inputs, make_weights
+    from oracle.numpy_ref import run_ir
+
+    cfg = QwenConfig(hidden=2048, heads=16, kv_heads=2)
+    ir = build_attention_ir(700, cfg)
+    w = host(make_weights(ir, cfg))
+    x = host(attention_inputs(700, cfg=cfg))
+    got, ex = run_hip(ir, x, w, backend)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert kernels[0] == "k_qkv_rope" and "k_gemv_attn_bias_r2" in kernels
+    ref = run_cpu(ir, x, w)
+    orc = run_ir(ir, x, w)
+    for k in got:
+        close(got[k], ref[k])
+        close(got[k], orc[k])
+
+
 def test_mixed_plan_forced_cpu_ops(backend):
     """Device/CPU/device plan with transfers (the reference's --force-cpu-ops path)."""
     from irgen.qwen import build_mlp_ir
