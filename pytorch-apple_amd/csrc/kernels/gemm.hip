@@ -25,8 +25,7 @@ typedef __attribute__((ext_vector_type(8))) _Float16 gm_f16x8;
 typedef __attribute__((ext_vector_type(16))) float gm_f32x16;
 
 enum { GE_BIAS = 0, GE_RESID = 1, GE_SILU = 2 };
-#define GM_BK 32
-#define GM_LDS_K 40   // padded row length in LDS (elements)
+#define GM_BK 32      // default K step
 
 template <int DT>
 __device__ __forceinline__ gm_f32x16 gm_mfma(const uint4 a, const uint4 b, gm_f32x16 c) {
@@ -54,20 +53,33 @@ __device__ __forceinline__ uint16_t gm_pack(float f) {
   return DT == HS_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
 }
 
-template <int DT, int EPI, int NW, int BM, int BN, bool KN = false>
+template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
+  constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
+  constexpr int CPR = BK / 8;             // 16-byte chunks per staged row
   constexpr int BNT = BN * NW;            // weight rows staged per step (BN columns per weight)
   constexpr int TI = BM / 64;             // 32-row MFMA tiles per wave
   constexpr int TJ = BN / 64;             // 32-column MFMA tiles per wave and weight
-  constexpr int A_LD = BM * GM_BK / 8 / 256;    // 16-byte A loads per thread per step
-  constexpr int B_LD = BNT * GM_BK / 8 / 256;   // 16-byte B loads per thread per step
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][GM_LDS_K];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BNT][GM_LDS_K];
+  constexpr int A_LD = BM * BK / 8 / 256;    // 16-byte A loads per thread per step
+  constexpr int B_LD = BNT * BK / 8 / 256;   // 16-byte B loads per thread per step
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BNT][LDK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
-  const long long m_base = (long long)blockIdx.y * BM;
-  const int n_base = blockIdx.x * BN;
-  const int bz = blockIdx.z / a.ksplit, kz = blockIdx.z % a.ksplit;   // batch, K split
+  // XCD-aware tile order: workgroup L (dispatch order) runs on XCD L % 8, so L is remapped
+  // to give each XCD a contiguous range of tiles, decoded M-tile fastest: the M tiles that
+  // read the same weight tile run back to back on one XCD and share its L2, instead of
+  // landing on different XCDs and fetching the weights once per XCD
+  const unsigned gx = gridDim.x, gy = gridDim.y;
+  const unsigned total = gx * gy * gridDim.z;
+  const unsigned lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const unsigned per = (total + 7) / 8, xcd = lin % 8, loc = lin / 8;
+  const unsigned tall = total % 8 == 0 ? 8 : total % 8;   // XCDs that get `per` tiles; the rest get per - 1
+  const unsigned tile = xcd < tall ? xcd * per + loc : tall * per + (xcd - tall) * (per - 1) + loc;
+  const unsigned tm = tile % gy, tn = (tile / gy) % gx, tz = tile / (gy * gx);
+  const long long m_base = (long long)tm * BM;
+  const int n_base = tn * BN;
+  const int bz = tz / a.ksplit, kz = tz % a.ksplit;   // batch, K split
   const uint16_t* X = (const uint16_t*)a.x + bz * a.sx;
   const long long wofs = (long long)(bz / a.bdiv) * a.sw;
   // two named pointers (a runtime-indexed pointer array would live in scratch memory)
@@ -78,10 +90,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   // global -> register staging of one K step, and register -> LDS. The staging lives in
   // named registers (A_LD, B_LD <= 2): a small per-thread array would be promoted to LDS by
   // the compiler, doubling the LDS traffic of the main loop.
-  static_assert(A_LD >= 1 && A_LD <= 2 && B_LD >= 1 && B_LD <= 2, "staging registers");
-  uint4 ra0, ra1, rb0, rb1;
+  static_assert(A_LD >= 1 && A_LD <= 4 && B_LD >= 1 && B_LD <= 4, "staging registers");
+  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
   auto a_ld = [&](int i, int k0) -> uint4 {
-    const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+    const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
     const long long m = min(m_base + row, a.M - 1);
     return *(const uint4*)(X + m * a.ldx + k0 + col);
   };
@@ -92,13 +104,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       const int n = min(n_base + nc, a.N - 8);
       return *(const uint4*)(W0 + (long long)(k0 + kr) * a.ldw + n);
     } else {
-      const int row = c >> 2, col = (c & 3) * 8;
+      const int row = c / CPR, col = (c % CPR) * 8;
       const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
       return *(const uint4*)((u == 0 ? W0 : W1) + (long long)n * a.ldw + k0 + col);
     }
   };
   auto a_st = [&](int buf, int i, uint4 v) {
-    const int c = tid + 256 * i, row = c >> 2, col = (c & 3) * 8;
+    const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
     *(uint4*)&As[buf][row][col] = v;
   };
   auto b_st = [&](int buf, int i, uint4 v) {
@@ -112,7 +124,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         Bs[buf][nc + 2 * j + 1][kr] = (uint16_t)(q[j] >> 16);
       }
     } else {
-      const int row = c >> 2, col = (c & 3) * 8;
+      const int row = c / CPR, col = (c % CPR) * 8;
       *(uint4*)&Bs[buf][row][col] = v;
     }
   };
@@ -120,15 +132,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   do {                                    \
     ra0 = a_ld(0, (k0));                  \
     if (A_LD > 1) ra1 = a_ld(1, (k0));    \
+    if (A_LD > 2) ra2 = a_ld(2, (k0));    \
+    if (A_LD > 3) ra3 = a_ld(3, (k0));    \
     rb0 = b_ld(0, (k0));                  \
     if (B_LD > 1) rb1 = b_ld(1, (k0));    \
+    if (B_LD > 2) rb2 = b_ld(2, (k0));    \
+    if (B_LD > 3) rb3 = b_ld(3, (k0));    \
   } while (0)
 #define GM_STORE_STEP(buf)                \
   do {                                    \
     a_st((buf), 0, ra0);                  \
     if (A_LD > 1) a_st((buf), 1, ra1);    \
+    if (A_LD > 2) a_st((buf), 2, ra2);    \
+    if (A_LD > 3) a_st((buf), 3, ra3);    \
     b_st((buf), 0, rb0);                  \
     if (B_LD > 1) b_st((buf), 1, rb1);    \
+    if (B_LD > 2) b_st((buf), 2, rb2);    \
+    if (B_LD > 3) b_st((buf), 3, rb3);    \
   } while (0)
 
   gm_f32x16 acc[NW][TI][TJ];
@@ -143,7 +163,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 
   // split K: workgroup z covers [z * kchunk, (z + 1) * kchunk)
   const int kbeg = kz * a.kchunk;
-  const int nsteps = min(a.kchunk, a.K - kbeg) / GM_BK;
+  const int nsteps = min(a.kchunk, a.K - kbeg) / BK;
   X += kbeg;
   if constexpr (KN) {
     W0 += (long long)kbeg * a.ldw;
@@ -157,9 +177,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // fragment row/column and k offset of this lane
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
-    if (s + 1 < nsteps) GM_LOAD_STEP((s + 1) * GM_BK);
+    if (s + 1 < nsteps) GM_LOAD_STEP((s + 1) * BK);
 #pragma unroll
-    for (int ks = 0; ks < GM_BK / 16; ++ks) {
+    for (int ks = 0; ks < BK / 16; ++ks) {
       uint4 af[TI], bfr[NW][TJ];
 #pragma unroll
       for (int i = 0; i < TI; ++i) af[i] = *(const uint4*)&As[buf][wr * (BM / 2) + i * 32 + fr][ks * 16 + fk];
@@ -253,10 +273,17 @@ __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
 // up to 2 waves per SIMD: the 64 accumulator registers plus staging and fragments need
 // more than the default register budget, which would otherwise spill the staging to scratch
 #define GM_ATTRS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
-#define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN) \
-  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); }
-#define GEMM_KERNEL_KN(NAME, DT, BM, BN) \
-  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, true>(a); }
+// Each kernel comes in two K steps: 32, and 64 (suffix _k64: twice the MFMA work per barrier and
+// per prefetch, which hides the operand latency better; 73.7 KB of LDS for 128 x 128 tiles, so two
+// workgroups still share a CU). Measured at M = 512, K = 1536: lm_head 381 -> 312 us, gate/up
+// 61 -> 51 us; K = 8960 down 39 -> 30 us. The host takes _k64 when K (and the split-K chunk) is a
+// multiple of 64.
+#define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN)                                                      \
+  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); } \
+  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN, false, 64>(a); }
+#define GEMM_KERNEL_KN(NAME, DT, BM, BN)                                                                  \
+  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, true>(a); } \
+  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, true, 64>(a); }
 #define GEMM_REDUCE(NAME, DT, EPI) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_reduce_body<DT, EPI>(a); }
 

@@ -42,6 +42,30 @@ GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 
 
+def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int]:
+    """(BM, BN, split-K) for an M x N x K MFMA GEMM (nw = 2: two weights, BN columns of each).
+
+    Rules fitted to a sweep on MI355X at M = 512 (bf16, K step 64, split-K reduce pass
+    included): the largest tile that still gives >= 256 workgroups, else the smallest tile.
+    Split K only where it pays for the reduce pass: long rows (K >= 4096) on 128 x 128 tiles
+    with up to 8 splits (~384 workgroups; down_proj 512 x 1536 x 8960: 35 us against 41+ us
+    without), or fewer than 128 tiles (k/v projections, 512 x 256 x 1536: 4 splits, 9.2 us
+    against 10.6). q/o projections (192 tiles of 64 x 64) run unsplit: 14-16 us against 17."""
+    tiles = [(128, 64), (64, 64)] if nw == 2 else [(128, 128), (64, 128), (64, 64)]
+    ntiles = lambda bm, bn: ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
+    for bm, bn in tiles:
+        if ntiles(bm, bn) >= GEMM_TARGET_WGS:
+            return bm, bn, 1
+    if nw == 1 and K >= 4096:
+        t = ntiles(128, 128)
+        return 128, 128, max(1, min(8, 384 // t, K // GEMM_MIN_KCHUNK))
+    bm, bn = tiles[-1]
+    t = ntiles(bm, bn)
+    if t >= 128:
+        return bm, bn, 1
+    return bm, bn, max(1, min((128 + t - 1) // t, K // GEMM_MIN_KCHUNK))
+
+
 def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
     return (max(1, min(cap, (int(n) + block - 1) // block)), 1, 1)
 
@@ -481,16 +505,11 @@ class Lowering:
         wv2 = self.aligned16(self.contiguous(w2), w2) if w2 else None
         bv2 = self.contiguous(b2) if b2 else None
         nw = 2 if epi == "silu" else 1
-        # the largest tile that still gives >= 256 workgroups; below that, split K as well
-        tiles = [(128, 64), (64, 64)] if nw == 2 else [(128, 128), (64, 128), (64, 64)]
-        for bm, bn in tiles:
-            ntiles = ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
-            if ntiles >= GEMM_TARGET_WGS:
-                break
-        ksplit, kchunk = 1, K
-        if ntiles < GEMM_TARGET_WGS:
-            ksplit = max(1, min((GEMM_TARGET_WGS + ntiles - 1) // ntiles, K // GEMM_MIN_KCHUNK))
-            kchunk = ((K // 32 + ksplit - 1) // ksplit) * 32
+        bm, bn, ksplit = gemm_tiling(M, N, K, nw)
+        bk = 64 if K % 64 == 0 else 32
+        kchunk = K
+        if ksplit > 1:
+            kchunk = ((K // bk + ksplit - 1) // ksplit) * bk
             ksplit = (K + kchunk - 1) // kchunk
         dt = "bf16" if dtype == "bfloat16" else "f16"
         part = self.scratch(out_name + ".kpart", ksplit * nw * M * N * 4) if ksplit > 1 else None
@@ -501,9 +520,10 @@ class Lowering:
                     N=N, K=K, flags=(1 if bias else 0) | (2 if bv2 else 0), ksplit=ksplit, kchunk=kchunk, nw=nw)
         ins = [x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t]
         params = {"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None, "weights": nw,
-                  "transpose_b": True, "nodes": nodes, "mfma": True, "tile": (bm, bn), "ksplit": ksplit}
+                  "transpose_b": True, "nodes": nodes, "mfma": True, "tile": (bm, bn), "ksplit": ksplit, "bk": bk}
         self.emit(LaunchStep(
-            kind="gemm", kernel=f"k_gemm_{dt}_{epi}_m{bm}n{bn}", module="gemm", arg_struct="GemmArgs", args=args,
+            kind="gemm", kernel=f"k_gemm_{dt}_{epi}_m{bm}n{bn}" + ("_k64" if bk == 64 else ""), module="gemm",
+            arg_struct="GemmArgs", args=args,
             grid=((N + bn - 1) // bn, (M + bm - 1) // bm, ksplit), inputs=ins,
             outputs=[out_name + ".kpart" if ksplit > 1 else out_name], params=params))
         if ksplit > 1:
@@ -660,7 +680,9 @@ class Lowering:
         for bm, bn in tiles:
             if ((M + bm - 1) // bm) * ((N + bn - 1) // bn) * nb >= GEMM_TARGET_WGS:
                 break
-        name = f"k_gemm_{'bf16' if dt == 'bfloat16' else 'f16'}_bias_m{bm}n{bn}" + ("_kn" if kn else "")
+        bk = 64 if K % 64 == 0 else 32
+        name = (f"k_gemm_{'bf16' if dt == 'bfloat16' else 'f16'}_bias_m{bm}n{bn}" + ("_kn" if kn else "") +
+                ("_k64" if bk == 64 else ""))
         args = dict(x=self.ref(a), w=self.ref(b), w2=None, bias=None, bias2=None, resid=None, out=self.ref(c),
                     part=None, M=M, ldx=a.strides[-2], ldw=ldw, ldo=N, ldr=N, sx=sx, sw=sw, so=M * N, batch=nb,
                     bdiv=1, N=N, K=K, flags=0, ksplit=1, kchunk=K, nw=1)
@@ -668,7 +690,7 @@ class Lowering:
             kind="gemm", kernel=name, module="gemm", arg_struct="GemmArgs", args=args,
             grid=((N + bn - 1) // bn, (M + bm - 1) // bm, nb), inputs=ins, outputs=outs,
             params={"M": M, "N": N, "K": K, "batch": nb, "epilogue": "bias", "weights": 1, "mfma": True,
-                    "tile": (bm, bn), "ksplit": 1, "b_layout": "kn" if kn else "nk"}))
+                    "tile": (bm, bn), "ksplit": 1, "bk": bk, "b_layout": "kn" if kn else "nk"}))
         return True
 
     def lower_addmm(self, node: OpNode) -> None:
