@@ -177,6 +177,8 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   const void* resid;          // [M, N] (row stride ldr) or null
   void* out;                  // [M, N] (row stride ldo)
   float* part;                // split-K: fp32 partial sums [ksplit, NW, M, N], reduced by k_gemm_reduce_*
+  const void* w3;             // grouped (_grp kernels): output columns [0, n1) use w / bias, [n1, n2) w2 / bias2,
+  const void* bias3;          //   [n2, N) w3 / bias3 (row n - group start); n1, n2 multiples of the tile width
   long long M;
   long long ldx;
   long long ldw;
@@ -193,6 +195,8 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   int ksplit;                 // 1: epilogue in the GEMM; > 1: grid.z splits K into chunks of kchunk
   int kchunk;                 // K elements per split (multiple of 32)
   int nw;                     // weights (1, or 2 for SiLU * mul); read by the reduce kernel
+  int n1;                     // grouped: first column of the second and third groups
+  int n2;
 };
 
 struct ConvArgs {             // implicit-GEMM conv2d (conv.hip), NCHW activations, OIHW weights, groups 1
@@ -296,6 +300,28 @@ struct QKVArgs {              // RMSNorm -> q/k/v projections -> RoPE -> K/V cac
   int flags;                  // 1 norm, 2 bias, 4 rope q, 8 rope k, 16 k to cache, 32 v to cache
   int pos_dtype;
   int cpos_dtype;
+  float rope_scaling;
+};
+
+struct RopeCacheArgs {        // prefill: RoPE of q and k from the q | k | v projection rows, K/V cache rows (gemv.hip)
+  const void* y;              // [T, ldy]: columns q (H*D) | k (KVH*D) | v (KVH*D)
+  const float* inv_freq;      // [D/2]
+  const void* pos_ids;        // [T] int64 / int32
+  const void* cache_pos;      // [T] int64 / int32
+  void* q_out;                // [H, T, D]
+  void* k_dst;                // K cache [KVH, S, D] (flag 16) or [KVH, T, D]
+  void* v_dst;                // V cache [KVH, S, D] (flag 32) or [KVH, T, D]
+  long long ldy;
+  long long kv_head_stride;   // elements between KV heads of the destination
+  long long cache_len;        // S (flag 16 / 32): rows at positions outside [0, S) are not written
+  int T;
+  int H;
+  int KVH;
+  int D;                      // even, <= 128
+  int flags;                  // 4 rope q, 8 rope k, 16 k to cache, 32 v to cache
+  int pos_dtype;
+  int cpos_dtype;
+  int dtype;                  // bf16 or fp16 storage
   float rope_scaling;
 };
 

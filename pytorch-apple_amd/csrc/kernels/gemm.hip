@@ -15,6 +15,8 @@
 //   RESID out = round(r + round(acc + b))
 //   SILU  out = round(round(silu(round(acc_g + b_g))) * round(acc_u + b_u))   (NW = 2)
 // Rows past M and columns past N are computed from clamped (valid) addresses and not stored.
+// Grouped use (_grp): output columns [0, n1), [n1, n2), [n2, N) are computed from three
+// weights (and biases), e.g. the q, k and v projections of one activation in one launch.
 // Batched use (grid.z = batch * ksplit): batch b reads x + b*sx and w + (b / bdiv)*sw (the
 // GQA head -> KV head map) and writes out + b*so. The _kn kernels take w as [K, N]
 // (N-contiguous, e.g. V in P.V) and transpose it while staging into LDS.
@@ -53,7 +55,7 @@ __device__ __forceinline__ uint16_t gm_pack(float f) {
   return DT == HS_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
 }
 
-template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK>
+template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
   constexpr int CPR = BK / 8;             // 16-byte chunks per staged row
@@ -85,6 +87,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   // two named pointers (a runtime-indexed pointer array would live in scratch memory)
   const uint16_t* W0 = (const uint16_t*)a.w + wofs;
   const uint16_t* W1 = (const uint16_t*)(NW == 2 ? a.w2 : a.w) + wofs;
+  // grouped: the tile's columns belong to one group (tile-aligned boundaries), whose weight
+  // rows and bias start at the group's first column
+  int g_lo = 0, g_hi = a.N;
+  const void* g_bias = a.bias;
+  if constexpr (GRP) {
+    const int g = (n_base >= a.n1) + (n_base >= a.n2);
+    g_lo = g == 0 ? 0 : (g == 1 ? a.n1 : a.n2);
+    g_hi = g == 0 ? a.n1 : (g == 1 ? a.n2 : a.N);
+    W0 = (const uint16_t*)(g == 0 ? a.w : (g == 1 ? a.w2 : a.w3)) + wofs;
+    g_bias = g == 0 ? a.bias : (g == 1 ? a.bias2 : a.bias3);
+  }
   uint16_t* OUT = (uint16_t*)a.out + bz * a.so;
 
   // global -> register staging of one K step, and register -> LDS. The staging lives in
@@ -105,6 +118,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       return *(const uint4*)(W0 + (long long)(k0 + kr) * a.ldw + n);
     } else {
       const int row = c / CPR, col = (c % CPR) * 8;
+      if constexpr (GRP) {   // NW == 1: row of the tile's group
+        const int n = min(n_base + row, g_hi - 1) - g_lo;
+        return *(const uint4*)(W0 + (long long)n * a.ldw + k0 + col);
+      }
       const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
       return *(const uint4*)((u == 0 ? W0 : W1) + (long long)n * a.ldw + k0 + col);
     }
@@ -221,7 +238,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   for (int j = 0; j < TJ; ++j) {
     const int n = n_base + wc * (BN / 2) + j * 32 + fr;
     if (n >= a.N) continue;
-    const float b0 = (a.flags & 1) ? gm_ld<DT>(a.bias, n) : 0.f;
+    const float b0 = (a.flags & 1) ? gm_ld<DT>(g_bias, n - g_lo) : 0.f;
     const float b1 = (EPI == GE_SILU && (a.flags & 2)) ? gm_ld<DT>(a.bias2, n) : 0.f;
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
@@ -302,6 +319,14 @@ GEMM_KERNEL(k_gemm_f16_bias_m64n64, HS_F16, GE_BIAS, 1, 64, 64)
 GEMM_KERNEL(k_gemm_f16_resid_m128n128, HS_F16, GE_RESID, 1, 128, 128)
 GEMM_KERNEL(k_gemm_f16_resid_m64n128, HS_F16, GE_RESID, 1, 64, 128)
 GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64)
+// grouped (q | k | v projections of one activation into one [M, N] output; no split K)
+#define GEMM_KERNEL_GRP(NAME, DT, BM, BN)                                                                      \
+  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, false, 32, true>(a); } \
+  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, false, 64, true>(a); }
+GEMM_KERNEL_GRP(k_gemm_bf16_grp_m64n64, HS_BF16, 64, 64)
+GEMM_KERNEL_GRP(k_gemm_bf16_grp_m128n128, HS_BF16, 128, 128)
+GEMM_KERNEL_GRP(k_gemm_f16_grp_m64n64, HS_F16, 64, 64)
+GEMM_KERNEL_GRP(k_gemm_f16_grp_m128n128, HS_F16, 128, 128)
 GEMM_REDUCE(k_gemm_reduce_bf16_bias, HS_BF16, GE_BIAS)
 GEMM_REDUCE(k_gemm_reduce_bf16_resid, HS_BF16, GE_RESID)
 GEMM_REDUCE(k_gemm_reduce_bf16_silu, HS_BF16, GE_SILU)

@@ -541,3 +541,54 @@ __device__ __forceinline__ void qkv_body(const QKVArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) k_qkv_rope(const QKVArgs a) { qkv_body<6>(a); }       // K <= 3072
 extern "C" __global__ void __launch_bounds__(256) k_qkv_rope_k1536(const QKVArgs a) { qkv_body<3>(a); } // K <= 1536
+
+// ------------------------------------------------------------------ prefill RoPE + K/V cache rows
+//
+// One wave per (token t, slot): slots 0..H-1 are q heads, H..H+KVH-1 k heads, then v heads.
+// Lane d takes the rotate-half pair (d, d + D/2) of the row:
+//   out[d] = r(r(x[d] c) + r(-x[d + D/2] s)),  out[d + D/2] = r(r(x[d + D/2] c) + r(x[d] s))
+// with c, s = r(cos / sin(inv_freq[d] * pos[t]) * scaling) and r() the model dtype's rounding:
+// q*cos + rotate_half(q)*sin as the reference's graph evaluates it, op by op. q goes to
+// [H, T, D]; k (rotated) and v to their caches at row cache_pos[t] (an in-place index_copy).
+extern "C" __global__ void __launch_bounds__(256) k_rope_cache(const RopeCacheArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int slots = a.H + 2 * a.KVH, half = a.D / 2;
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= (long long)a.T * slots) return;
+  const int t = (int)(row / slots), slot = (int)(row % slots);
+  const int seg = slot < a.H ? 0 : (slot < a.H + a.KVH ? 1 : 2);
+  const int hd = seg == 0 ? slot : (seg == 1 ? slot - a.H : slot - a.H - a.KVH);
+  if (lane >= half) return;
+  const long long col = (long long)slot * a.D;   // q | k | v heads are consecutive D-wide column blocks
+  const uint16_t* yr = (const uint16_t*)a.y + (long long)t * a.ldy + col;
+  const bool f16 = a.dtype == HS_F16;
+  auto ld = [&](int d) { return f16 ? f16_to_f32(yr[d]) : bf16_to_f32(yr[d]); };
+  auto rd = [&](float f) { return round_to(f, a.dtype); };
+  auto pk = [&](float f) { return f16 ? f32_to_f16(f) : f32_to_bf16(f); };
+  float v0 = ld(lane), v1 = ld(lane + half);
+  const bool rope = (seg == 0 && (a.flags & 4)) || (seg == 1 && (a.flags & 8));
+  if (rope) {
+    const long long pos = ld_i(a.pos_ids, t, a.pos_dtype);
+    float sf, cf;
+    sincos_rot(a.inv_freq[lane] * (float)pos, &sf, &cf);
+    const float c = rd(cf * a.rope_scaling), s = rd(sf * a.rope_scaling);
+    const float e0 = rd(rd(v0 * c) + rd(-v1 * s));
+    const float e1 = rd(rd(v1 * c) + rd(v0 * s));
+    v0 = e0;
+    v1 = e1;
+  }
+  uint16_t* dst;
+  if (seg == 0) {
+    dst = (uint16_t*)a.q_out + ((long long)hd * a.T + t) * a.D;
+  } else {
+    const bool to_cache = seg == 1 ? (a.flags & 16) : (a.flags & 32);
+    long long r = t;
+    if (to_cache) {
+      r = ld_i(a.cache_pos, t, a.cpos_dtype);
+      if (r < 0 || r >= a.cache_len) return;
+    }
+    dst = (uint16_t*)(seg == 1 ? a.k_dst : a.v_dst) + (long long)hd * a.kv_head_stride + r * a.D;
+  }
+  dst[lane] = pk(v0);
+  dst[lane + half] = pk(v1);
+}

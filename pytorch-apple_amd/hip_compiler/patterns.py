@@ -674,6 +674,152 @@ def _emit_qkv(low, xname, q, k, v, names) -> None:
     low.mutated_inputs.update({kc.storage, vc.storage})
 
 
+# ------------------------------------------------------------------ prefill q/k/v + RoPE + cache
+
+def _heads_t(cx: _Ctx, lin: OpNode):
+    """``linear → view [1, T, n, D] → transpose(1, 2)`` for any T: (view, transpose, T, n, D) or None."""
+    v = cx.only(lin.outputs[0].name, ("aten.view.default", "aten.reshape.default", "aten._unsafe_view.default"))
+    if v is None or len(v.outputs[0].shape) != 4 or v.outputs[0].shape[0] != 1:
+        return None
+    t = cx.only(v.outputs[0].name, "aten.transpose.int")
+    if t is None or sorted([int(t.attrs.get("dim0", 0)) % 4, int(t.attrs.get("dim1", 1)) % 4]) != [1, 2]:
+        return None
+    _, T, n, D = v.outputs[0].shape
+    return v, t, T, n, D
+
+
+def _inplace_target_t(low, cx: _Ctx, t_name: str, T: int):
+    """``index_copy(past, cpos, t, dim=2)`` with T positions, updatable in place: (node, past, cpos) or None."""
+    ic = cx.only(t_name, "aten.index_copy.default")
+    if ic is None or int(ic.attrs.get("dim", 0)) % 4 != 2 or ic.inputs[2].name != t_name:
+        return None
+    past, cpos = ic.inputs[0], ic.inputs[1]
+    st = low.storages.get(past.name)
+    if (st is None or st.kind != "input" or len(low.consumers.get(past.name, [])) != 1
+            or past.name in low.graph_output_names or not low.inplace_inputs or cpos.shape != [T]):
+        return None
+    return ic, past.name, cpos.name
+
+
+def qkv_rope_prefill(low) -> None:
+    """Prefill (T >= GEMM_MIN_M tokens): the q, k and v projections of one activation — q and k
+    rotated, k and v written into their caches in place — become one grouped MFMA GEMM (q | k | v
+    columns) and one ``k_rope_cache`` launch, instead of three GEMMs, the rotate-half chains and
+    two index_copy launches."""
+    from hip_compiler.subgraph_analyzer import GEMM_MIN_M
+    cx = _Ctx(low)
+    by_x: dict[str, dict] = {}
+    for lin in low.g.nodes:
+        p = _linear_parts(lin)
+        if p is None or lin.name in low.claimed:
+            continue
+        x, w, b = p
+        if x.dtype != "bfloat16" or w.dtype != "bfloat16" or (b is not None and b.dtype != "bfloat16"):
+            continue
+        hd = _heads_t(cx, lin)
+        if hd is None:
+            continue
+        vnode, tnode, T, nh, D = hd
+        if T < GEMM_MIN_M or D % 2 or D > 128 or x.shape[-1] != w.shape[1]:
+            continue
+        xname = tnode.outputs[0].name
+        rope = _rope_chain(cx, xname, D)
+        entry = {"lin": lin, "w": w, "b": b, "nh": nh, "D": D, "T": T, "nodes": [lin, vnode, tnode]}
+        if rope is not None:
+            rnodes, rout, rnode = rope
+            entry["nodes"] += rnodes
+            entry["rope"] = rnode
+            tgt = _inplace_target_t(low, cx, rout, T)
+            if tgt is None:
+                if rout in low.graph_output_names:
+                    continue
+                entry["role"], entry["out"] = "q", rout
+            else:
+                entry["role"], entry["ic"], entry["past"], entry["cpos"] = "k", *tgt
+                entry["nodes"].append(tgt[0])
+        else:
+            tgt = _inplace_target_t(low, cx, xname, T)
+            if tgt is None:
+                continue
+            entry["role"], entry["ic"], entry["past"], entry["cpos"] = "v", *tgt
+            entry["nodes"].append(tgt[0])
+        by_x.setdefault(x.name, {}).setdefault(entry["role"], []).append(entry)
+    for xname, roles in by_x.items():
+        if any(len(roles.get(r, [])) != 1 for r in ("q", "k", "v")):
+            continue
+        q, k, v = roles["q"][0], roles["k"][0], roles["v"][0]
+        if not (q["D"] == k["D"] == v["D"] and q["T"] == k["T"] == v["T"] and k["nh"] == v["nh"]
+                and q["rope"] is k["rope"] and k["cpos"] == v["cpos"] and q["nh"] % k["nh"] == 0):
+            continue
+        if len({q["b"] is None, k["b"] is None, v["b"] is None}) != 1:
+            continue
+        K = q["w"].shape[1]
+        if K % 32 or any(e["w"].shape != [e["nh"] * e["D"], K] for e in (q, k, v)):
+            continue
+        if (q["nh"] * q["D"]) % 64 or (k["nh"] * k["D"]) % 64:   # tile-aligned column groups
+            continue
+        past_k = low.views[k["past"]]
+        if list(past_k.shape[:2]) != [1, k["nh"]] or past_k.shape[3] != k["D"]:
+            continue
+        nodes = q["nodes"] + k["nodes"] + v["nodes"]
+        names = [n.name for n in nodes]
+
+        def emit(xname=xname, q=q, k=k, v=v, names=names):
+            _emit_qkv_prefill(low, xname, q, k, v, names)
+
+        cx.claim(nodes, emit)
+
+
+def _emit_qkv_prefill(low, xname, q, k, v, names) -> None:
+    from hip_compiler.subgraph_analyzer import gemm_tiling
+    x = low.aligned16(low.contiguous(xname), xname)   # a pending RMSNorm is materialised here
+    rope = q["rope"]
+    inv = low.contiguous(rope.inputs[0].name)
+    pos = low.contiguous(rope.inputs[1].name)
+    cpos = low.contiguous(k["cpos"])
+    H, KVH, D, T = q["nh"], k["nh"], q["D"], q["T"]
+    K = x.shape[-1]
+    if inv.dtype != "float32" or pos.numel != T or x.numel != T * K:
+        raise NotImplementedError("prefill RoPE needs fp32 inv_freq and one position per token")
+    if pos.dtype not in ("int64", "int32") or cpos.dtype not in ("int64", "int32"):
+        raise NotImplementedError("prefill RoPE reads int64 or int32 positions")
+    N = (H + 2 * KVH) * D
+    n1, n2 = H * D, (H + KVH) * D
+    bm, bn, _ = gemm_tiling(T, N, K)
+    if n1 % bn or n2 % bn:
+        bn = 64
+    bk = 64 if K % 64 == 0 else 32
+    ws = [low.aligned16(low.contiguous(e["w"].name), e["w"].name) for e in (q, k, v)]
+    bs = [low.contiguous(e["b"].name) if e["b"] is not None else None for e in (q, k, v)]
+    y = low.new_storage(q["out"] + ".qkv", [T, N], "bfloat16")
+    args = dict(x=low.ref(x), w=low.ref(ws[0]), w2=low.ref(ws[1]), w3=low.ref(ws[2]),
+                bias=low.ref(bs[0]) if bs[0] else None, bias2=low.ref(bs[1]) if bs[1] else None,
+                bias3=low.ref(bs[2]) if bs[2] else None, resid=None, out=low.ref(y), part=None,
+                M=T, ldx=K, ldw=K, ldo=N, ldr=N, sx=0, sw=0, so=0, batch=1, bdiv=1, N=N, K=K,
+                flags=1 if bs[0] else 0, ksplit=1, kchunk=K, nw=1, n1=n1, n2=n2)
+    ins = [xname] + [e["w"].name for e in (q, k, v)] + [e["b"].name for e in (q, k, v) if e["b"] is not None]
+    low.emit(LaunchStep(kind="gemm", kernel=f"k_gemm_bf16_grp_m{bm}n{bn}" + ("_k64" if bk == 64 else ""),
+                        module="gemm", arg_struct="GemmArgs", args=args,
+                        grid=((N + bn - 1) // bn, (T + bm - 1) // bm, 1), inputs=ins, outputs=[y.storage],
+                        params={"M": T, "N": N, "K": K, "epilogue": "bias", "groups": [n1, n2], "mfma": True,
+                                "tile": (bm, bn), "ksplit": 1, "bk": bk, "nodes": names}))
+    qo = low.new_storage(q["out"], [1, H, T, D], "bfloat16")
+    kc, vc = low.views[k["past"]], low.views[v["past"]]
+    rargs = dict(y=low.ref(y), inv_freq=low.ref(inv), pos_ids=low.ref(pos), cache_pos=low.ref(cpos), q_out=low.ref(qo),
+                 k_dst=low.ref(kc), v_dst=low.ref(vc), ldy=N, kv_head_stride=kc.strides[1], cache_len=kc.shape[2],
+                 T=T, H=H, KVH=KVH, D=D, flags=4 | 8 | 16 | 32, pos_dtype=DTYPE_CODE[pos.dtype],
+                 cpos_dtype=DTYPE_CODE[cpos.dtype], dtype=DTYPE_CODE["bfloat16"],
+                 rope_scaling=float(rope.attrs.get("attention_scaling", 1.0)))
+    low.emit(LaunchStep(kind="gemv", kernel="k_rope_cache", module="gemv", arg_struct="RopeCacheArgs", args=rargs,
+                        grid=((T * (H + 2 * KVH) + 3) // 4, 1, 1), inputs=[y.storage, k["cpos"], k["past"], v["past"]],
+                        outputs=[q["out"], k["ic"].outputs[0].name, v["ic"].outputs[0].name],
+                        params={"T": T, "heads": [H, KVH], "nodes": names}))
+    low.views[q["out"]] = qo
+    low.views[k["ic"].outputs[0].name] = kc
+    low.views[v["ic"].outputs[0].name] = vc
+    low.mutated_inputs.update({kc.storage, vc.storage})
+
+
 # ------------------------------------------------------------------ conv + BN (+ add) (+ ReLU)
 
 def conv_bn_act(low) -> None:
@@ -709,7 +855,8 @@ def conv_bn_act(low) -> None:
         cx.claim(nodes, emit)
 
 
-DEFAULT_PATTERNS = [decode_attention, rmsnorm, qkv_rope, gate_up_silu, linear_argmax, linear_resid, masked_softmax,
+DEFAULT_PATTERNS = [decode_attention, rmsnorm, qkv_rope, qkv_rope_prefill, gate_up_silu, linear_argmax, linear_resid,
+                    masked_softmax,
                     conv_bn_act]
 
 __all__ = ["DEFAULT_PATTERNS", "rmsnorm", "masked_softmax", "decode_attention", "V"]

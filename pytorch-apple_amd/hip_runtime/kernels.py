@@ -55,9 +55,9 @@ _struct("LinearArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P)
                        ("ldo", LL), ("ldr", LL), ("N", I), ("K", I), ("dtype", I), ("has_bias", I),
                        ("has_resid", I), ("pad", I)])
 _struct("GemmArgs", [("x", P), ("w", P), ("w2", P), ("bias", P), ("bias2", P), ("resid", P), ("out", P),
-                     ("part", P), ("M", LL), ("ldx", LL), ("ldw", LL), ("ldo", LL), ("ldr", LL), ("sx", LL),
-                     ("sw", LL), ("so", LL), ("batch", I), ("bdiv", I), ("N", I), ("K", I), ("flags", I),
-                     ("ksplit", I), ("kchunk", I), ("nw", I)])
+                     ("part", P), ("w3", P), ("bias3", P), ("M", LL), ("ldx", LL), ("ldw", LL), ("ldo", LL),
+                     ("ldr", LL), ("sx", LL), ("sw", LL), ("so", LL), ("batch", I), ("bdiv", I), ("N", I), ("K", I),
+                     ("flags", I), ("ksplit", I), ("kchunk", I), ("nw", I), ("n1", I), ("n2", I)])
 _struct("ConvArgs", [("x", P), ("w", P), ("bias", P), ("bn_w", P), ("bn_b", P), ("bn_mean", P), ("bn_var", P),
                      ("resid", P), ("out", P), ("M", LL), ("N", I), ("Cin", I), ("H", I), ("W", I), ("Cout", I),
                      ("Ho", I), ("Wo", I), ("KH", I), ("KW", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I),
@@ -66,6 +66,10 @@ _struct("PoolArgs", [("x", P), ("out", P), ("planes", LL), ("H", I), ("W", I), (
                      ("kw", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I), ("dtype", I), ("pad", I)])
 _struct("BatchNormArgs", [("x", P), ("w", P), ("b", P), ("mean", P), ("var", P), ("out", P), ("n", LL),
                           ("hw", LL), ("C", I), ("eps", F), ("dtype", I), ("relu", I)])
+_struct("RopeCacheArgs", [("y", P), ("inv_freq", P), ("pos_ids", P), ("cache_pos", P), ("q_out", P), ("k_dst", P),
+                          ("v_dst", P), ("ldy", LL), ("kv_head_stride", LL), ("cache_len", LL), ("T", I), ("H", I),
+                          ("KVH", I), ("D", I), ("flags", I), ("pos_dtype", I), ("cpos_dtype", I), ("dtype", I),
+                          ("rope_scaling", F)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])
 _struct("GemvArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P), ("w2", P), ("bias2", P),
                      ("norm_w", P), ("argmax_slot", P), ("attn_o", P), ("attn_ml", P), ("M", LL), ("ldx", LL),
