@@ -400,3 +400,255 @@ extern "C" __global__ void __launch_bounds__(256) k_attn_out(const AttnOutArgs a
     ((uint16_t*)a.out)[idx] = a.dtype == HS_BF16 ? f32_to_bf16(part) : f32_to_f16(part);
   }
 }
+
+// ------------------------------------------------------------------ prefill attention (MFMA)
+//
+// k_attn_prefill: grid (ceil(T / 32), H), 256 threads. Workgroup (qb, h) computes the outputs of
+// queries [32 qb, 32 qb + 32) of head h against all S keys of KV head h / (H / KVH), flash style;
+// wave w takes the 32-position KV blocks w, w + 4, ... and the four waves are merged at the end.
+// Per block, on v_mfma_f32_32x32x16 (D = 128, eight K steps):
+//   S^T = K Q^T (positions as rows, queries as columns), so each lane holds 16 scores of ONE
+//   query (lane l: query l % 32, positions 8i + 4(l / 32) + r): the online softmax and the
+//   rescaling of that query's outputs stay in the lane, with one exchange with lane l ^ 32;
+//   s = r(r(q.k) * scale) [+ mask, rounded to add_dtype] as the reference rounds them;
+//   O^T += V^T P^T with P in bf16 / fp16 (reordered into the operand layout by two exchanges
+//   with lane l ^ 32) and V^T staged through wave-private LDS (position pairs per dword).
+// Each block's mask values are loaded with its K and V; a block whose 32 x 32 mask entries are
+// all -inf (the causal upper triangle) is skipped. Scores of positions >= S are -inf; rows of
+// queries >= T are computed from a clamped query and not stored. The output is written as
+// [T, H, D], the layout the o_proj input needs after transpose(1, 2) + reshape.
+#define PA_BQ 32
+#define PA_BP 32
+#define PA_VLD 40   // V^T row length in LDS (positions, padded): 16-byte fragment reads spread over the banks
+
+typedef __attribute__((ext_vector_type(16))) float pa_f32x16;
+
+template <int DT>
+__device__ __forceinline__ pa_f32x16 pa_mfma(const uint4 a, const uint4 b, pa_f32x16 c) {
+  if constexpr (DT == HS_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(__attribute__((ext_vector_type(8))) __bf16, a),
+                                                   __builtin_bit_cast(__attribute__((ext_vector_type(8))) __bf16, b), c,
+                                                   0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(__attribute__((ext_vector_type(8))) _Float16, a),
+                                                  __builtin_bit_cast(__attribute__((ext_vector_type(8))) _Float16, b), c,
+                                                  0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pa_pack2(float lo, float hi) {
+  const uint16_t a = DT == HS_BF16 ? f32_to_bf16(lo) : f32_to_f16(lo);
+  const uint16_t b = DT == HS_BF16 ? f32_to_bf16(hi) : f32_to_f16(hi);
+  return (uint32_t)a | ((uint32_t)b << 16);
+}
+
+// MM: mask mode, 0 none, 1 16-bit mask of the model dtype (8-byte loads of 4 entries), 2 fp32 mask
+template <int DT, int MM>
+__device__ __forceinline__ void prefill_attn_body(const PrefillAttnArgs& a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vt[4][128][PA_VLD];
+  __shared__ float ml[4][2][PA_BQ];
+  __shared__ float ob[4][PA_BQ][128 + 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, hi = lane >> 5;
+  const int h = blockIdx.y, kvh = h / (a.H / a.KVH);
+  const long long q0 = (long long)blockIdx.x * PA_BQ;
+  const long long qrow = min(q0 + fr, a.T - 1);
+  const uint16_t* Qp = (const uint16_t*)a.q + (long long)h * a.q_head_stride + qrow * 128;
+  const uint16_t* Kb = (const uint16_t*)a.k + (long long)kvh * a.kv_head_stride;
+  const uint16_t* Vb = (const uint16_t*)a.v + (long long)kvh * a.kv_head_stride;
+  const void* mptr = MM == 0 ? a.q : a.mask;   // a.q: valid dummy address when there is no mask
+  const long long mrow = qrow * a.mask_row_stride;
+  auto rnd = [&](float f) { return round_to(f, DT); };
+
+  uint4 qf[8];   // B operand of S^T: query fr, dims 16 ks + 8 hi .. + 8
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const uint4*)(Qp + ks * 16 + hi * 8);
+  pa_f32x16 o[4];   // O^T: dims 32 t + 8i + 4 hi + r, query fr
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const int nblk = (int)((a.S + PA_BP - 1) / PA_BP);
+  const long long last = a.S - 1;
+  // V staging: lane -> positions pr, pr + 1 (pr = 2 (lane % 16)), 16-byte chunks cg + 4j of the dims
+  const int pr = 2 * (lane & 15), cg = lane >> 4;
+
+  // MM 1: 16-bit mask with unit column stride (S % 4 == 0, 8-byte aligned rows; the host
+  // checks): four positions per 8-byte load
+  struct Blk {
+    uint2 mq[4];   // mask bits, positions 8i + 4 hi + (0..3)
+    uint4 kf[8];   // A operand of S^T: position fr, dims 16 ks + 8 hi .. + 8
+    uint4 va[4], vb[4];
+  };
+  // issue every load of block `blk` (clamped to the last block: a spare load, never used)
+  auto load = [&](int blk, Blk& b) {
+    const long long p0 = (long long)min(blk, nblk - 1) * PA_BP;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (MM == 1) {
+        const long long p = min(p0 + 8 * i + 4 * hi, last & ~3ll);
+        b.mq[i] = *(const uint2*)((const uint16_t*)mptr + mrow + p);
+      } else if constexpr (MM == 2) {   // fp32: two entries per 8-byte load, the other pair below
+        const long long p = min(p0 + 8 * i + 4 * hi, last);
+        b.mq[i] = make_uint2(__float_as_uint(((const float*)mptr)[mrow + p * a.mask_col_stride]),
+                             __float_as_uint(((const float*)mptr)[mrow + min(p + 1, last) * a.mask_col_stride]));
+      } else {
+        b.mq[i] = make_uint2(0, 0);
+      }
+    }
+    const uint16_t* Kp = Kb + min(p0 + fr, last) * 128 + hi * 8;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) b.kf[ks] = *(const uint4*)(Kp + ks * 16);
+    const uint16_t* Va = Vb + min(p0 + pr, last) * 128;
+    const uint16_t* Vc = Vb + min(p0 + pr + 1, last) * 128;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      b.va[j] = *(const uint4*)(Va + (cg + 4 * j) * 8);
+      b.vb[j] = *(const uint4*)(Vc + (cg + 4 * j) * 8);
+    }
+  };
+  auto compute = [&](int blk, const Blk& b) {
+    const long long p0 = (long long)blk * PA_BP;
+    float mv[16];
+    bool any = false;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const long long p = p0 + 8 * (e >> 2) + 4 * hi + (e & 3);
+      float m = 0.f;
+      if constexpr (MM == 1) {
+        const uint32_t w = (e & 2) ? b.mq[e >> 2].y : b.mq[e >> 2].x;
+        const uint16_t bits = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+        m = DT == HS_BF16 ? bf16_to_f32(bits) : f16_to_f32(bits);
+      } else if constexpr (MM == 2) {
+        m = (e & 2) ? ((const float*)mptr)[mrow + min(p, last) * a.mask_col_stride]
+                    : __uint_as_float((e & 1) ? b.mq[e >> 2].y : b.mq[e >> 2].x);
+      }
+      mv[e] = p > last ? -INFINITY : m;
+      any = any || mv[e] != -INFINITY;
+    }
+    if (__ballot(any) == 0ull) return;   // wave-uniform: the whole 32 x 32 block is masked out
+
+    // V^T of the block into this wave's LDS rows (dims), position pairs per dword
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d0 = (cg + 4 * j) * 8;
+      const uint32_t x[4] = {b.va[j].x, b.va[j].y, b.va[j].z, b.va[j].w};
+      const uint32_t y[4] = {b.vb[j].x, b.vb[j].y, b.vb[j].z, b.vb[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *(uint32_t*)&vt[wave][d0 + 2 * i][pr] = (x[i] & 0xffffu) | (y[i] << 16);
+        *(uint32_t*)&vt[wave][d0 + 2 * i + 1][pr] = (x[i] >> 16) | (y[i] & 0xffff0000u);
+      }
+    }
+    // S^T = K Q^T
+    pa_f32x16 s;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) s = pa_mfma<DT>(b.kf[ks], qf[ks], s);
+    float sc[16], bm = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float v = rnd(rnd(s[e]) * a.scale);
+      if constexpr (MM != 0) v = round_to(v + mv[e], a.add_dtype);
+      if (mv[e] == -INFINITY) v = -INFINITY;
+      sc[e] = v;
+      bm = fmaxf(bm, v);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float m_new = fmaxf(m_run, bm);
+    const float alpha = (m_run == -INFINITY) ? 0.f : __expf(m_run - m_new);
+    float ps = 0.f;
+    float pv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      pv[e] = (sc[e] == -INFINITY) ? 0.f : __expf(sc[e] - m_new);
+      ps += pv[e];
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[t][e] *= alpha;
+    // P into the B-operand layout: lane half 0 needs positions 0-7 / 16-23, half 1 8-15 / 24-31;
+    // group i holds positions 8i + 4 hi + (0..3)
+    uint2 g[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) g[i] = make_uint2(pa_pack2<DT>(pv[4 * i], pv[4 * i + 1]), pa_pack2<DT>(pv[4 * i + 2], pv[4 * i + 3]));
+    const uint2 send0 = hi ? g[0] : g[1], send1 = hi ? g[2] : g[3];
+    const uint2 recv0 = make_uint2(__shfl_xor(send0.x, 32, 64), __shfl_xor(send0.y, 32, 64));
+    const uint2 recv1 = make_uint2(__shfl_xor(send1.x, 32, 64), __shfl_xor(send1.y, 32, 64));
+    const uint4 pf0 = hi ? make_uint4(recv0.x, recv0.y, g[1].x, g[1].y) : make_uint4(g[0].x, g[0].y, recv0.x, recv0.y);
+    const uint4 pf1 = hi ? make_uint4(recv1.x, recv1.y, g[3].x, g[3].y) : make_uint4(g[2].x, g[2].y, recv1.x, recv1.y);
+    // O^T += V^T P^T (the wave's own LDS writes above are complete before its reads: in-order LDS)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint4 v0 = *(const uint4*)&vt[wave][t * 32 + fr][hi * 8];
+      const uint4 v1 = *(const uint4*)&vt[wave][t * 32 + fr][16 + hi * 8];
+      o[t] = pa_mfma<DT>(v0, pf0, o[t]);
+      o[t] = pa_mfma<DT>(v1, pf1, o[t]);
+    }
+  };
+  // two blocks in flight: the loads of this wave's next block are issued before the current
+  // block is computed (named register sets; loads past the last block re-read it)
+  Blk ba, bb;
+  load(wave, ba);
+  for (int blk = wave; blk < nblk; blk += 8) {
+    load(blk + 4, bb);
+    compute(blk, ba);
+    if (blk + 4 >= nblk) break;
+    load(blk + 8, ba);
+    compute(blk + 4, bb);
+  }
+
+  // merge the four waves: o_final = sum_w e^(m_w - M) o_w / sum_w e^(m_w - M) l_w
+  if (hi == 0) {
+    ml[wave][0][fr] = m_run;
+    ml[wave][1][fr] = l_run;
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, ml[w][0][fr]);
+  const float f_own = (m_run == -INFINITY) ? 0.f : __expf(m_run - M);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ob[wave][fr][t * 32 + 8 * (e >> 2) + 4 * hi + (e & 3)] = o[t][e] * f_own;
+  __syncthreads();
+  // 256 threads x 16 outputs: query tid / 8, dims 16 (tid % 8) .. + 16
+  const int qq = tid >> 3, d0 = (tid & 7) * 16;
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float mw = ml[w][0][qq];
+    L += (mw == -INFINITY) ? 0.f : __expf(mw - fmaxf(fmaxf(ml[0][0][qq], ml[1][0][qq]), fmaxf(ml[2][0][qq], ml[3][0][qq]))) * ml[w][1][qq];
+  }
+  if (q0 + qq >= a.T) return;
+  uint32_t pk[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float x0 = 0.f, x1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      x0 += ob[w][qq][d0 + 2 * i];
+      x1 += ob[w][qq][d0 + 2 * i + 1];
+    }
+    pk[i] = pa_pack2<DT>(x0 / L, x1 / L);
+  }
+  uint4* dst = (uint4*)((uint16_t*)a.out + (q0 + qq) * (long long)a.H * 128 + (long long)h * 128 + d0);
+  dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+}
+
+#define PA_KERNEL(NAME, DT, MM) \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const PrefillAttnArgs a) { prefill_attn_body<DT, MM>(a); }
+PA_KERNEL(k_attn_prefill, HS_BF16, 1)              // 16-bit mask of the model dtype
+PA_KERNEL(k_attn_prefill_nomask, HS_BF16, 0)
+PA_KERNEL(k_attn_prefill_f32mask, HS_BF16, 2)
+PA_KERNEL(k_attn_prefill_f16, HS_F16, 1)
+PA_KERNEL(k_attn_prefill_f16_nomask, HS_F16, 0)
+PA_KERNEL(k_attn_prefill_f16_f32mask, HS_F16, 2)

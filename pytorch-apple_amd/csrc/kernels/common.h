@@ -374,6 +374,26 @@ struct FlashArgs {            // split-S decode attention: per-split (max, sum, 
   int dtype;
 };
 
+struct PrefillAttnArgs {      // causal / masked attention of T queries over S keys (attention.hip, MFMA)
+  const void* q;              // [H, T, D] (q_head_stride, row stride D)
+  const void* k;              // [KVH, S, D] (kv_head_stride, row stride D)
+  const void* v;              // [KVH, S, D]
+  const void* mask;           // additive mask element (t, s) at t*mask_row_stride + s*mask_col_stride, or null
+  void* out;                  // [T, H, D]: element (t, h, d) at t*H*D + h*D + d
+  long long T;
+  long long S;
+  long long q_head_stride;
+  long long kv_head_stride;
+  long long mask_row_stride;
+  long long mask_col_stride;
+  int H;
+  int KVH;
+  float scale;
+  int mask_dtype;             // -1: no mask
+  int add_dtype;              // rounding dtype of (scores + mask)
+  int dtype;                  // bf16 or fp16
+};
+
 struct CombineArgs {          // out[h, d] = round(sum_t e^(m_t - M) o_t[d] / sum_t e^(m_t - M) l_t)
   const float* part_o;
   const float* part_ml;

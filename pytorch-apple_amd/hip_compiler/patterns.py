@@ -199,7 +199,10 @@ def decode_attention(low) -> None:
         if mm1.op_type != "aten.matmul.default" or mm1.name in low.claimed:
             continue
         q_t, kt_t = mm1.inputs[0], mm1.inputs[1]
-        if len(q_t.shape) != 4 or q_t.shape[0] != 1 or q_t.shape[2] != 1:
+        if len(q_t.shape) != 4 or q_t.shape[0] != 1:
+            continue
+        T = q_t.shape[2]   # 1: decode; >= 16: prefill (the MFMA kernel)
+        if T != 1 and (T < 16 or low.exact_attention):
             continue
         H, D = q_t.shape[1], q_t.shape[3]
         if D != 128:
@@ -258,9 +261,13 @@ def decode_attention(low) -> None:
         if H % kvh or H // kvh > 8 or k_spec.shape[3] != D or S > 64 * 1024:
             continue
         add_dtype = add_n.outputs[0].dtype if mask_name is not None else dt
+        if mask_name is not None and T > 1:
+            mdt = next(t for t in add_n.inputs if t.name == mask_name).dtype
+            if mdt not in (dt, "float32"):
+                continue
         if mask_name is not None:
             ms = next(t for t in add_n.inputs if t.name == mask_name).shape
-            if len(ms) > 4 or ms[-1] != S or any(s != 1 for s in ms[:-1]):
+            if len(ms) > 4 or ms[-1] != S or any(s != 1 for s in ms[:-2]) or (len(ms) > 1 and ms[-2] not in (1, T)):
                 continue
         inside = {n.name for n in nodes}
         if not all(cx.private(n.outputs[0].name, inside) for n in nodes[:-1]):
@@ -268,13 +275,56 @@ def decode_attention(low) -> None:
         out = mm2.outputs[0]
 
         def emit(q=q_t.name, k=k_name, v=v_name, mask=mask_name, out=out, scale=scale, H=H, kvh=kvh, S=S,
-                 add_dtype=add_dtype, dt=dt, names=[n.name for n in nodes]):
-            if low.exact_attention:
+                 add_dtype=add_dtype, dt=dt, names=[n.name for n in nodes], T=T):
+            if T > 1:
+                _emit_prefill_attention(low, q, k, v, mask, out, scale, H, kvh, S, T, add_dtype, dt, names)
+            elif low.exact_attention:
                 _emit_decode_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names)
             else:
                 _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names)
 
         cx.claim(nodes, emit)
+
+
+def _emit_prefill_attention(low, q, k, v, mask, out, scale, H, kvh, S, T, add_dtype, dt, names) -> None:
+    """T queries (prefill) on MFMA, flash style (csrc/kernels/attention.hip, k_attn_prefill). The
+    output is stored [T, H, D] and exposed as the [1, H, T, D] view the graph expects, so the
+    transpose(1, 2) + reshape in front of o_proj is a view, not a copy."""
+    D = 128
+    qv = low.view(q)
+    if list(qv.strides[2:]) != [D, 1] or (qv.offset * 2) % 16:
+        qv = low.contiguous(q, qv)
+    kv_ = low.contiguous(k)
+    vv_ = low.contiguous(v)
+    if (kv_.offset * 2) % 16 or (vv_.offset * 2) % 16 or (qv.offset * 2) % 16:
+        raise NotImplementedError("attention operands must be 16-byte aligned")
+    margs = dict(mask=None, mask_row_stride=0, mask_col_stride=0, mask_dtype=-1)
+    if mask is not None:
+        mv = low.view(mask)
+        if mv.dtype not in (dt, "float32"):
+            raise NotImplementedError("prefill attention mask must have the model dtype or fp32")
+        if mv.dtype != "float32":
+            # the kernel reads four 16-bit mask entries per 8-byte load: unit column stride,
+            # rows and base 8-byte aligned
+            if S % 4:
+                raise NotImplementedError("prefill attention with a 16-bit mask needs S % 4 == 0")
+            rs = mv.strides[-2] if len(mv.shape) > 1 and mv.shape[-2] == T else 0
+            if mv.strides[-1] != 1 or rs % 4 or (mv.offset * 2) % 16:
+                mv = low.aligned16(low.contiguous(mask), mask)
+        row = mv.strides[-2] if len(mv.shape) > 1 and mv.shape[-2] == T else 0
+        margs = dict(mask=low.ref(mv), mask_row_stride=row, mask_col_stride=mv.strides[-1],
+                     mask_dtype=DTYPE_CODE[mv.dtype])
+    st = low.new_storage(out.name, [1, T, H, D], dt)
+    args = dict(q=low.ref(qv), k=low.ref(kv_), v=low.ref(vv_), out=low.ref(st), T=T, S=S, q_head_stride=qv.strides[1],
+                kv_head_stride=kv_.strides[1], H=H, KVH=kvh, scale=float(scale), add_dtype=DTYPE_CODE[add_dtype],
+                dtype=DTYPE_CODE[dt], **margs)
+    kname = "k_attn_prefill" + ("" if dt == "bfloat16" else "_f16") + \
+        ("_nomask" if mask is None else ("_f32mask" if margs["mask_dtype"] == DTYPE_CODE["float32"] else ""))
+    low.emit(LaunchStep(kind="attention", kernel=kname,
+                        module="attention", arg_struct="PrefillAttnArgs", args=args, grid=((T + 31) // 32, H, 1),
+                        inputs=[q, k, v] + ([mask] if mask else []), outputs=[out.name],
+                        params={"T": T, "S": S, "heads": H, "kv_heads": kvh, "nodes": names}))
+    low.views[out.name] = st.with_(shape=(1, H, T, D), strides=(T * H * D, D, H * D, 1))
 
 
 def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names) -> None:

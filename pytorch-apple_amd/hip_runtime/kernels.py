@@ -70,6 +70,10 @@ _struct("RopeCacheArgs", [("y", P), ("inv_freq", P), ("pos_ids", P), ("cache_pos
                           ("v_dst", P), ("ldy", LL), ("kv_head_stride", LL), ("cache_len", LL), ("T", I), ("H", I),
                           ("KVH", I), ("D", I), ("flags", I), ("pos_dtype", I), ("cpos_dtype", I), ("dtype", I),
                           ("rope_scaling", F)])
+_struct("PrefillAttnArgs", [("q", P), ("k", P), ("v", P), ("mask", P), ("out", P), ("T", LL), ("S", LL),
+                            ("q_head_stride", LL), ("kv_head_stride", LL), ("mask_row_stride", LL),
+                            ("mask_col_stride", LL), ("H", I), ("KVH", I), ("scale", F), ("mask_dtype", I),
+                            ("add_dtype", I), ("dtype", I)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])
 _struct("GemvArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P), ("w2", P), ("bias2", P),
                      ("norm_w", P), ("argmax_slot", P), ("attn_o", P), ("attn_ml", P), ("M", LL), ("ldx", LL),

@@ -488,6 +488,9 @@ def test_prefill_two_layers_real_dims(backend):
     x = host(prefill_inputs(T, T, cfg))
     got, ex = run_hip(ir, x, w, backend)
     assert_all_npu(ex)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert {"k_gemm_bf16_grp_m64n64_k64", "k_rope_cache", "k_attn_prefill"} <= set(kernels)
+    assert "k_copy" not in kernels and "k_softmax" not in kernels
     ref = run_cpu(ir, x, w)
     logits = ir["graph_outputs"][0]["name"]
     close(got[logits], ref[logits])
@@ -496,6 +499,99 @@ def test_prefill_two_layers_real_dims(backend):
     assert (tok_g == tok_c).mean() >= 0.95
     for o in ir["graph_outputs"][1:-1]:
         close(got[o["name"]], ref[o["name"]])
+
+
+def _prefill_attention_ir(T, S, H=12, KVH=2, D=128, mask_dtype=None):
+    """Standalone GQA attention of T queries over S keys, the op sequence of the Qwen2 eager
+    graph (repeat_kv as unsqueeze/expand/reshape, transpose, matmul, scale, [+ mask], softmax in
+    fp32, cast, matmul)."""
+    from irgen.builder import IRBuilder
+    from irgen.qwen import repeat_kv
+
+    b = IRBuilder("PrefillAttention")
+    q = b.input("q", [1, H, T, D], "bfloat16")
+    k = b.input("k", [1, KVH, S, D], "bfloat16")
+    v = b.input("v", [1, KVH, S, D], "bfloat16")
+    kt = b.op("aten.transpose.int", [repeat_kv(b, k, H // KVH)], {"dim0": 2, "dim1": 3})
+    sc = b.op("aten.mul.Tensor", [b.op("aten.matmul.default", [q, kt])], {"other": D ** -0.5})
+    if mask_dtype is not None:
+        sc = b.op("aten.add.Tensor", [sc, b.input("mask", [1, 1, T, S], mask_dtype)])
+    p = b.op("aten.softmax.int", [sc], {"dim": -1, "dtype": "float32"})
+    p = b.op("aten.to.dtype", [p], {"dtype": "bfloat16"}, base="to")
+    b.output(b.op("aten.matmul.default", [p, repeat_kv(b, v, H // KVH)]))
+    return b.to_dict()
+
+
+@pytest.mark.parametrize("mask", [None, "float32", "bfloat16"])
+def test_prefill_attention_kernel_mask_modes(backend, mask):
+    """k_attn_prefill without a mask, with an fp32 mask and with a bf16 mask (T = 70 queries over
+    S = 96 keys, a banded causal mask), against the numpy oracle and the CPU fallback."""
+    from oracle.numpy_ref import run_ir
+
+    T, S = 70, 96
+    ir = _prefill_attention_ir(T, S, mask_dtype=mask)
+    g = torch.Generator().manual_seed(11)
+    x = {"q": torch.randn(1, 12, T, 128, generator=g).bfloat16(),
+         "k": torch.randn(1, 2, S, 128, generator=g).bfloat16(),
+         "v": torch.randn(1, 2, S, 128, generator=g).bfloat16()}
+    if mask is not None:
+        m = torch.zeros(T, S)
+        for t in range(T):
+            m[t, t + S - T + 1:] = float("-inf")   # causal over the last T positions
+            m[t, :max(0, t - 40)] = float("-inf")  # and a sliding window of 40
+        x["mask"] = m.to(torch.float32 if mask == "float32" else torch.bfloat16).reshape(1, 1, T, S)
+    x = host(x)
+    got, ex = run_hip(ir, x, {}, backend)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    want = {None: "k_attn_prefill_nomask", "float32": "k_attn_prefill_f32mask", "bfloat16": "k_attn_prefill"}[mask]
+    assert kernels[0] == want and "k_softmax" not in kernels   # (+ one copy: the graph output is [1, H, T, D])
+    ref = run_cpu(ir, x, {})
+    orc = run_ir(ir, x, {})
+    for k in got:
+        close(got[k], ref[k])
+        close(got[k], orc[k])
+
+
+def test_prefill_chunk_ragged_vs_cpu_and_oracle(backend):
+    """A 100-token chunk (not a multiple of the 32-query tile) at positions 40..139 of a 160-entry
+    cache whose first 40 rows hold earlier keys and values: the grouped q/k/v GEMM, the RoPE and
+    cache-row kernel and the MFMA prefill attention (causal over the cached prefix, the rows past
+    the chunk masked), against the CPU fallback and the numpy oracle."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import make_weights
+    from oracle.numpy_ref import run_ir
+
+    cfg = QwenConfig(layers=1, vocab=4096)
+    T, S, P0 = 100, 160, 40
+    ir = build_decode_ir(S, cfg, argmax=True, tokens=T)
+    w = host(make_weights(ir, cfg))
+    g = torch.Generator().manual_seed(7)
+    mask = torch.full((T, S), float("-inf"))
+    for t in range(T):
+        mask[t, :P0 + t + 1] = 0.0
+    x = {"input_ids": torch.randint(0, cfg.vocab, (1, T), generator=g),
+         "attention_mask": mask.bfloat16().reshape(1, 1, T, S),
+         "position_ids": torch.arange(P0, P0 + T, dtype=torch.int64).reshape(1, T),
+         "cache_position": torch.arange(P0, P0 + T, dtype=torch.int64)}
+    for kind in ("key", "value"):
+        c = torch.zeros((1, cfg.kv_heads, S, cfg.head_dim))
+        c[:, :, :P0] = torch.randn((1, cfg.kv_heads, P0, cfg.head_dim), generator=g)
+        x[f"past_{kind}_0"] = c.bfloat16()
+    x = host(x)
+    got, ex = run_hip(ir, x, w, backend)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert "k_attn_prefill" in kernels and "k_rope_cache" in kernels
+    ref = run_cpu(ir, x, w)
+    orc = run_ir(ir, x, w)
+    for o in ir["graph_outputs"][:-1]:
+        close(got[o["name"]], ref[o["name"]])
+        close(got[o["name"]], orc[o["name"]])
+    for kind in ("key", "value"):   # rows outside the chunk are untouched copies of the input
+        name = next(o["name"] for o in ir["graph_outputs"] if f"past_{kind}" in o["name"] or
+                    o["name"] == ("index_copy" if kind == "key" else "index_copy_1"))
+        keep = np.ones(S, bool)
+        keep[P0:P0 + T] = False
+        assert np.array_equal(np.asarray(got[name])[:, :, keep], np.asarray(x[f"past_{kind}_0"])[:, :, keep])
 
 
 @pytest.mark.parametrize("transposed_b", [False, True])
