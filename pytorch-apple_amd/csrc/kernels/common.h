@@ -133,6 +133,16 @@ struct ReduceLastArgs {       // mean / argmax over the last dim of a [rows, col
   int out_dtype;
 };
 
+struct ArgmaxPartArgs {       // per (row, column segment) argmax key of a [rows, cols] 16-bit view (gemv.hip)
+  const void* x;              // rows of `cols` elements, 16-byte aligned, cols % 8 == 0
+  unsigned long long* slot;   // [rows, parts] keys, reduced by k_argmax_finalize
+  long long rows;
+  long long cols;
+  long long seg;              // columns per segment (multiple of 8); grid = (parts, rows)
+  int x_dtype;                // bf16 or fp16
+  int parts;
+};
+
 struct BmmArgs {              // c[b, m, n] = sum_k a[b, m, k] * b[b, k, n] (strided, broadcast batch)
   const void* a;
   const void* b;

@@ -592,3 +592,60 @@ extern "C" __global__ void __launch_bounds__(256) k_rope_cache(const RopeCacheAr
   dst[lane] = pk(v0);
   dst[lane + half] = pk(v1);
 }
+
+// ------------------------------------------------------------------ argmax over long rows
+//
+// k_argmax_part: grid (parts, rows), 256 threads; workgroup (p, r) scans columns
+// [p * seg, (p + 1) * seg) of row r with 16-byte loads (all of a thread's loads in flight
+// together) and writes one key to slot[r * parts + p]; k_argmax_finalize reduces the keys of
+// a row. The key orders like torch.argmax / np.argmax: larger value first, NaN above every
+// number, -0.0 equal to +0.0, then the smaller index.
+__device__ __forceinline__ unsigned long long argmax_key_nan(float v, unsigned idx) {
+  uint32_t b = __float_as_uint(v);
+  b = (v == 0.f) ? 0u : b;
+  const uint32_t o = (v != v) ? 0xFFFFFFFFu : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+  return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+extern "C" __global__ void __launch_bounds__(256) k_argmax_part(const ArgmaxPartArgs a) {
+  __shared__ unsigned long long red[4];
+  const long long row = blockIdx.y;
+  const long long c0 = (long long)blockIdx.x * a.seg, c1 = min(c0 + a.seg, a.cols);
+  const uint16_t* xr = (const uint16_t*)a.x + row * a.cols;
+  const bool f16 = a.x_dtype == HS_F16;
+  unsigned long long best = 0ull;
+  constexpr int U = 4;
+  for (long long c = c0 + threadIdx.x * 8; c < c1; c += 256 * 8 * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long cc = c + (long long)u * 256 * 8;
+      v[u] = cc < c1 ? *(const uint4*)(xr + cc) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long cc = c + (long long)u * 256 * 8;
+      if (cc >= c1) break;
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint16_t hbits = (j & 1) ? (uint16_t)(w[j >> 1] >> 16) : (uint16_t)(w[j >> 1] & 0xffffu);
+        const float f = f16 ? f16_to_f32(hbits) : bf16_to_f32(hbits);
+        const unsigned long long k = argmax_key_nan(f, (unsigned)(cc + j));
+        best = k > best ? k : best;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long other = __shfl_xor(best, o, 64);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = red[0];
+    for (int w = 1; w < 4; ++w) k = red[w] > k ? red[w] : k;
+    a.slot[row * a.parts + blockIdx.x] = k;
+  }
+}

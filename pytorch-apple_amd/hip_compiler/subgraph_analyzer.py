@@ -898,6 +898,26 @@ class Lowering:
         cols = pv.shape[-1]
         rows = pv.numel // cols
         o = self.new_storage(out.name, out.shape, out.dtype)
+        if (pv.dtype in ("bfloat16", "float16") and cols % 8 == 0 and cols >= 4096 and (pv.offset * 2) % 16 == 0
+                and out.dtype in ("int64", "int32") and cols < 2 ** 32):
+            # long rows: split across workgroups (16-byte loads), then one key per row segment
+            # is reduced by k_argmax_finalize (same tie and NaN rules as k_argmax)
+            parts = (cols + 8191) // 8192
+            seg = ((cols + parts - 1) // parts + 7) // 8 * 8
+            slot = self.scratch(out.name + ".argmax", 8 * rows * parts)
+            self.emit(LaunchStep(
+                kind="reduction", kernel="k_argmax_part", module="gemv", arg_struct="ArgmaxPartArgs",
+                args=dict(x=self.ref(pv), slot=slot, rows=rows, cols=cols, seg=seg, x_dtype=DTYPE_CODE[pv.dtype],
+                          parts=parts),
+                grid=(parts, max(rows, 1), 1), inputs=[x.name], outputs=[out.name + ".argmax"],
+                params={"rows": rows, "cols": cols, "parts": parts}))
+            self.emit(LaunchStep(
+                kind="reduction", kernel="k_argmax_finalize", module="gemv", arg_struct="ArgmaxFinalizeArgs",
+                args=dict(slot=slot, out=self.ref(o), rows=rows, parts=parts, out_dtype=DTYPE_CODE[out.dtype]),
+                grid=(max(rows, 1), 1, 1), inputs=[out.name + ".argmax"], outputs=[out.name],
+                params={"rows": rows, "parts": parts}))
+            self.views[out.name] = o
+            return
         self.emit(LaunchStep(
             kind="reduction", kernel="k_argmax", module="basic", arg_struct="ReduceLastArgs",
             args=dict(x=self.ref(pv), out=self.ref(o), rows=rows, cols=cols, x_dtype=DTYPE_CODE[pv.dtype],

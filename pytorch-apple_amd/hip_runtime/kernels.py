@@ -74,6 +74,8 @@ _struct("PrefillAttnArgs", [("q", P), ("k", P), ("v", P), ("mask", P), ("out", P
                             ("q_head_stride", LL), ("kv_head_stride", LL), ("mask_row_stride", LL),
                             ("mask_col_stride", LL), ("H", I), ("KVH", I), ("scale", F), ("mask_dtype", I),
                             ("add_dtype", I), ("dtype", I)])
+_struct("ArgmaxPartArgs", [("x", P), ("slot", P), ("rows", LL), ("cols", LL), ("seg", LL), ("x_dtype", I),
+                           ("parts", I)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])
 _struct("GemvArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P), ("w2", P), ("bias2", P),
                      ("norm_w", P), ("argmax_slot", P), ("attn_o", P), ("attn_ml", P), ("M", LL), ("ldx", LL),

@@ -144,7 +144,7 @@ def test_arena_live_ranges_never_share_bytes(build, fuse):
 def test_steps_read_only_already_written_arena_storage(fuse):
     p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True), fuse=fuse)
     out_fields = {"dst", "out", "c", "cos_out", "sin_out", "q_out", "k_dst", "v_dst", "part_o", "part_ml",
-                  "scores", "stats", "argmax_slot", "part"}
+                  "scores", "stats", "argmax_slot", "part", "slot"}
     written = set()
     for s in p.steps:
         outs = {v.storage for k, v in s.args.items() if k in out_fields and isinstance(v, Ref)}

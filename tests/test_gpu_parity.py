@@ -227,6 +227,39 @@ def test_embedding_and_argmax_bitexact(backend):
     assert np.array_equal(got["argmax"], np.argmax(f32(got["linear"]), axis=-1))
 
 
+def test_argmax_long_rows_ties_nan_zero(backend):
+    """The split argmax (k_argmax_part + k_argmax_finalize) over 151936-wide bf16 rows is bit-exact
+    with np.argmax: equal maxima resolve to the first index (also across segment boundaries),
+    NaN (either sign) counts as the maximum, -0.0 equals +0.0, +inf beats every finite value."""
+    from irgen.builder import IRBuilder
+
+    R, V = 6, 151936
+    b = IRBuilder("am")
+    x = b.input("x", [R, V], "bfloat16")
+    b.output(b.op("aten.argmax.default", [x], {"dim": -1}))
+    ir = b.to_dict()
+    g = torch.Generator().manual_seed(3)
+    v = torch.randn(R, V, generator=g)
+    v[0, [9000, 70000, 151935]] = 50.0                       # tie across segments: first wins
+    v[1, [123456, 5]] = float("nan")                         # NaN anywhere is the maximum
+    v[1, 3] = 1e30
+    v[2] = -torch.rand(V, generator=g) - 1.0                 # all negative but two zeros
+    v[2, 77777] = -0.0
+    v[2, 88888] = 0.0
+    v[3, 100000] = float("inf")
+    v[4] = float("-inf")                                     # all -inf: index 0
+    v[5, 7999:8001] = 40.0                                   # tie across a segment edge (8000)
+    xb = v.bfloat16()
+    xb[1, 5] = -xb[1, 5]                                     # a negative-signed NaN as well
+    x_h = host({"x": xb})
+    got, ex = run_hip(ir, x_h, {}, backend)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert kernels == ["k_argmax_part", "k_argmax_finalize"]
+    want = np.argmax(f32(x_h["x"]), axis=-1)
+    assert list(want) == [9000, 5, 77777, 100000, 0, 7999]
+    assert np.array_equal(np.asarray(got["argmax"]).reshape(-1), want)
+
+
 def mini_cfg(layers=2):
     from irgen.qwen import QwenConfig
 
