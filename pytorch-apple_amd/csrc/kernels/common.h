@@ -219,11 +219,14 @@ struct ConvArgs {             // implicit-GEMM conv2d (conv.hip), NCHW activatio
   const void* bn_var;
   const void* resid;          // [N, Cout, Ho, Wo] added after the batch norm, or null
   void* out;                  // [N, Cout, Ho, Wo]
+  float* part;                // split K: fp32 partial sums [ksplit, Cout, M], reduced by k_conv_reduce_*
   long long M;                // N * Ho * Wo
   int N, Cin, H, W, Cout, Ho, Wo, KH, KW, sh, sw, ph, pw;
   int K;                      // Cin * KH * KW
   float eps;
   int flags;                  // 1 bias, 2 batch norm, 4 residual add, 8 ReLU
+  int ksplit;                 // 1: epilogue in the conv; > 1: grid.z splits K into chunks of kchunk
+  int kchunk;                 // multiple of the K step (32)
 };
 
 struct PoolArgs {             // NCHW max pooling (pool.hip)

@@ -159,17 +159,20 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nsteps = (a.K + CV_BK - 1) / CV_BK;
-  load_a(0, ra);
-  load_b(0);
+  // split K: workgroup z covers k in [z * kchunk, min(K, (z + 1) * kchunk))
+  const int kz = blockIdx.z;
+  const int kbeg = kz * a.kchunk;
+  const int nsteps = (min(a.K - kbeg, a.kchunk) + CV_BK - 1) / CV_BK;
+  load_a(kbeg, ra);
+  load_b(kbeg);
   store(0);
   __syncthreads();
   const int fr = lane & 31, fk = (lane >> 5) * 8;
   for (int s = 0; s < nsteps; ++s) {
     const int buf = s & 1;
     if (s + 1 < nsteps) {
-      load_a((s + 1) * CV_BK, ra);
-      load_b((s + 1) * CV_BK);
+      load_a(kbeg + (s + 1) * CV_BK, ra);
+      load_b(kbeg + (s + 1) * CV_BK);
     }
 #pragma unroll
     for (int ks = 0; ks < CV_BK / 16; ++ks) {
@@ -187,6 +190,21 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
     __syncthreads();
   }
 
+  if (a.ksplit > 1) {   // raw fp32 partials [z][channel][pixel]; k_conv_reduce_* applies the epilogue
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int m = (int)m_base + wr * 64 + i * 32 + fr;
+      if (m >= M32) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int co = n_base + wc * 64 + j * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+          if (co < a.Cout) a.part[((long long)kz * a.Cout + co) * a.M + m] = acc[i][j][e];
+        }
+    }
+    return;
+  }
   // epilogue. The MFMA operands are swapped (weights as the row operand), so each
   // accumulator register holds one channel for 32 consecutive pixels across the lanes:
   // stores (and residual loads) of a register are 64 contiguous bytes in NCHW.
@@ -232,7 +250,35 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   }
 }
 
+// Split-K reduction with the conv epilogue: one thread per output element (channel-major, pixels
+// contiguous), partials summed in a fixed order.
+template <int DT>
+__device__ __forceinline__ void conv_reduce_body(const ConvArgs& a) {
+  const long long total = (long long)a.Cout * a.M;
+  const int HoWo = a.Ho * a.Wo;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+    const int co = (int)(i / a.M);
+    const long long m = i - (long long)co * a.M;
+    float acc = 0.f;
+    for (int z = 0; z < a.ksplit; ++z) acc += a.part[(long long)z * total + i];
+    float v = cv_round<DT>(acc + ((a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[co]) : 0.f));
+    if (a.flags & 2) {
+      const float g = cv_f<DT>(((const uint16_t*)a.bn_w)[co]), bb = cv_f<DT>(((const uint16_t*)a.bn_b)[co]);
+      const float mu = cv_f<DT>(((const uint16_t*)a.bn_mean)[co]), var = cv_f<DT>(((const uint16_t*)a.bn_var)[co]);
+      const float al = g / sqrtf(var + a.eps);
+      v = cv_round<DT>(v * al + (bb - mu * al));
+    }
+    const long long n = m / HoWo, p = m - n * HoWo;
+    const long long o = (n * a.Cout + co) * HoWo + p;
+    if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
+    if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
+    ((uint16_t*)a.out)[o] = cv_h<DT>(v);
+  }
+}
+
 #define CV_ATTRS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+extern "C" __global__ void __launch_bounds__(256) k_conv_reduce_f16(const ConvArgs a) { conv_reduce_body<HS_F16>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_conv_reduce_bf16(const ConvArgs a) { conv_reduce_body<HS_BF16>(a); }
 extern "C" __global__ void CV_ATTRS k_conv_f16(const ConvArgs a) { conv_body<HS_F16, true>(a); }
 extern "C" __global__ void CV_ATTRS k_conv_f16_g(const ConvArgs a) { conv_body<HS_F16, false>(a); }
 extern "C" __global__ void CV_ATTRS k_conv_f16_1x1(const ConvArgs a) { conv_body<HS_F16, true, 1>(a); }

@@ -815,20 +815,37 @@ class Lowering:
             raise NotImplementedError("conv2d with 2^31 or more input elements or output pixels")
         ins = [conv.inputs[0].name, conv.inputs[1].name] + ([conv.inputs[2].name] if has_bias else []) + \
             ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
+        # few 128 x 128 tiles (small images deep in the network) and long K: split K across
+        # workgroups (fp32 partials, then k_conv_reduce_* applies the epilogue). Measured at batch 32:
+        # 3x3 512 -> 512 on 7 x 7 (52 tiles, K = 4608) and 1x1 2048 -> 512 run latency-bound unsplit
+        tiles = ((Cout + 127) // 128) * ((M + 127) // 128)
+        ksplit, kchunk = 1, K
+        if tiles < 256 and K >= 512:
+            ksplit = max(1, min(8, (384 + tiles - 1) // tiles, K // 256))
+            kchunk = ((K + 31) // 32 + ksplit - 1) // ksplit * 32
+            ksplit = (K + kchunk - 1) // kchunk
+        part = self.scratch(out_name + ".kpart", ksplit * Cout * M * 4) if ksplit > 1 else None
+        args = dict(x=self.ref(x), w=self.ref(w), bias=self.ref(self.contiguous(conv.inputs[2].name)) if has_bias
+                    else None, bn_w=self.ref(bnv[0]) if bn is not None else None,
+                    bn_b=self.ref(bnv[1]) if bn is not None else None,
+                    bn_mean=self.ref(bnv[2]) if bn is not None else None,
+                    bn_var=self.ref(bnv[3]) if bn is not None else None,
+                    resid=self.ref(rv) if rv is not None else None, out=self.ref(o), part=part, M=M, N=N, Cin=Cin,
+                    H=H, W=W, Cout=Cout, Ho=Ho, Wo=Wo, KH=KH, KW=KW, sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], K=K,
+                    eps=float(bn.attrs.get("eps", 1e-5)) if bn is not None else 0.0, flags=flags, ksplit=ksplit,
+                    kchunk=kchunk)
+        params = {"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
+                  "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
+                  "ksplit": ksplit, "nodes": nodes or [conv.name]}
         self.emit(LaunchStep(
-            kind="conv", kernel=kname, module="conv", arg_struct="ConvArgs",
-            args=dict(x=self.ref(x), w=self.ref(w), bias=self.ref(self.contiguous(conv.inputs[2].name)) if has_bias
-                      else None, bn_w=self.ref(bnv[0]) if bn is not None else None,
-                      bn_b=self.ref(bnv[1]) if bn is not None else None,
-                      bn_mean=self.ref(bnv[2]) if bn is not None else None,
-                      bn_var=self.ref(bnv[3]) if bn is not None else None,
-                      resid=self.ref(rv) if rv is not None else None, out=self.ref(o), M=M, N=N, Cin=Cin, H=H, W=W,
-                      Cout=Cout, Ho=Ho, Wo=Wo, KH=KH, KW=KW, sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], K=K,
-                      eps=float(bn.attrs.get("eps", 1e-5)) if bn is not None else 0.0, flags=flags),
-            grid=((Cout + 127) // 128, (M + 127) // 128, 1), inputs=ins, outputs=[out_name],
-            params={"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
-                    "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
-                    "nodes": nodes or [conv.name]}))
+            kind="conv", kernel=kname, module="conv", arg_struct="ConvArgs", args=args,
+            grid=((Cout + 127) // 128, (M + 127) // 128, ksplit), inputs=ins,
+            outputs=[out_name + ".kpart" if ksplit > 1 else out_name], params=params))
+        if ksplit > 1:
+            self.emit(LaunchStep(
+                kind="conv", kernel=f"k_conv_reduce_{'bf16' if dt == 'bfloat16' else 'f16'}", module="conv",
+                arg_struct="ConvArgs", args=dict(args), grid=grid1d(Cout * M),
+                inputs=[out_name + ".kpart"] + ins[2:], outputs=[out_name], params=dict(params, reduce=True)))
         self.views[out_name] = o
 
     def lower_conv2d(self, node: OpNode) -> None:

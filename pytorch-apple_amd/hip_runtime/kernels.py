@@ -59,9 +59,9 @@ _struct("GemmArgs", [("x", P), ("w", P), ("w2", P), ("bias", P), ("bias2", P), (
                      ("ldr", LL), ("sx", LL), ("sw", LL), ("so", LL), ("batch", I), ("bdiv", I), ("N", I), ("K", I),
                      ("flags", I), ("ksplit", I), ("kchunk", I), ("nw", I), ("n1", I), ("n2", I)])
 _struct("ConvArgs", [("x", P), ("w", P), ("bias", P), ("bn_w", P), ("bn_b", P), ("bn_mean", P), ("bn_var", P),
-                     ("resid", P), ("out", P), ("M", LL), ("N", I), ("Cin", I), ("H", I), ("W", I), ("Cout", I),
-                     ("Ho", I), ("Wo", I), ("KH", I), ("KW", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I),
-                     ("K", I), ("eps", F), ("flags", I)])
+                     ("resid", P), ("out", P), ("part", P), ("M", LL), ("N", I), ("Cin", I), ("H", I), ("W", I),
+                     ("Cout", I), ("Ho", I), ("Wo", I), ("KH", I), ("KW", I), ("sh", I), ("sw", I), ("ph", I),
+                     ("pw", I), ("K", I), ("eps", F), ("flags", I), ("ksplit", I), ("kchunk", I)])
 _struct("PoolArgs", [("x", P), ("out", P), ("planes", LL), ("H", I), ("W", I), ("Ho", I), ("Wo", I), ("kh", I),
                      ("kw", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I), ("dtype", I), ("pad", I)])
 _struct("BatchNormArgs", [("x", P), ("w", P), ("b", P), ("mean", P), ("var", P), ("out", P), ("n", LL),

@@ -200,7 +200,11 @@ def test_resnet50_compiles_to_fused_convs():
     plan = partition(ir, is_hip_op_supported)
     assert len(plan.steps) == 1 and plan.steps[0].target == "npu"
     p = compile_subgraph(ir)
-    convs = [s for s in p.steps if s.kind == "conv"]
-    assert len(convs) == 53 and len(p.steps) <= 57          # every BN / add / ReLU folded into a conv
+    convs = [s for s in p.steps if s.kind == "conv" and not s.params.get("reduce")]
+    reduces = [s for s in p.steps if s.kind == "conv" and s.params.get("reduce")]
+    # every BN / add / ReLU folded into a conv (or into the split-K reduce that finishes it)
+    assert len(convs) == 53 and len(p.steps) <= 57 + len(reduces)
+    assert all(s.kernel.startswith("k_conv_reduce_") for s in reduces)
+    assert len(reduces) == sum(1 for s in convs if s.params["ksplit"] > 1)
     assert sum(1 for s in convs if s.args["flags"] & 4) == 16 and all(s.args["flags"] & 2 for s in convs)
     assert convs[0].kernel.endswith("_g") and convs[0].args["K"] == 147   # 3-channel stem: gathered weights
