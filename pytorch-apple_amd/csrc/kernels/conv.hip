@@ -53,8 +53,18 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][CV_BN][CV_LDS_K];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
-  const long long m_base = (long long)blockIdx.y * CV_BM;
-  const int n_base = blockIdx.x * CV_BN;
+  // XCD-aware tile order (workgroup L runs on XCD L % 8): each XCD gets a contiguous range of
+  // tiles, output-channel tiles fastest, so the channel tiles that share one gathered pixel
+  // tile run back to back on the same XCD and find it in its L2
+  const unsigned gx = gridDim.x, gy = gridDim.y;
+  const unsigned total = gx * gy * gridDim.z;
+  const unsigned lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const unsigned per = (total + 7) / 8, xcd = lin % 8, loc = lin / 8;
+  const unsigned tall = total % 8 == 0 ? 8 : total % 8;
+  const unsigned tile = xcd < tall ? xcd * per + loc : tall * per + (xcd - tall) * (per - 1) + loc;
+  const unsigned tn = tile % gx, tm = (tile / gx) % gy, tkz = tile / (gx * gy);
+  const long long m_base = (long long)tm * CV_BM;
+  const int n_base = tn * CV_BN;
   const uint16_t* X = (const uint16_t*)a.x;
   const uint16_t* Wt = (const uint16_t*)a.w;
   const int HW = a.H * a.W;
@@ -160,7 +170,7 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   // split K: workgroup z covers k in [z * kchunk, min(K, (z + 1) * kchunk))
-  const int kz = blockIdx.z;
+  const int kz = (int)tkz;
   const int kbeg = kz * a.kchunk;
   const int nsteps = (min(a.K - kbeg, a.kchunk) + CV_BK - 1) / CV_BK;
   load_a(kbeg, ra);

@@ -817,10 +817,12 @@ class Lowering:
             ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
         # few 128 x 128 tiles (small images deep in the network) and long K: split K across
         # workgroups (fp32 partials, then k_conv_reduce_* applies the epilogue). Measured at batch 32:
-        # 3x3 512 -> 512 on 7 x 7 (52 tiles, K = 4608) and 1x1 2048 -> 512 run latency-bound unsplit
+        # 3x3 512 -> 512 on 7 x 7 (52 tiles, K = 4608) 257 -> 65 us, 1x1 2048 -> 512 73 -> 33 us,
+        # 3x3 128 -> 128 on 28 x 28 (196 tiles, K = 1152) 74 -> 67 us; at K = 512 the reduce pass
+        # costs more than the split gains (1x1 512 -> 128 on 28 x 28: 26 -> 29 us), hence K >= 1024
         tiles = ((Cout + 127) // 128) * ((M + 127) // 128)
         ksplit, kchunk = 1, K
-        if tiles < 256 and K >= 512:
+        if tiles < 256 and K >= 1024:
             ksplit = max(1, min(8, (384 + tiles - 1) // tiles, K // 256))
             kchunk = ((K + 31) // 32 + ksplit - 1) // ksplit * 32
             ksplit = (K + kchunk - 1) // kchunk
