@@ -260,29 +260,41 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   }
 }
 
-// Split-K reduction with the conv epilogue: one thread per output element (channel-major, pixels
-// contiguous), partials summed in a fixed order.
+// Split-K reduction with the conv epilogue: one thread per 4 consecutive pixels of one channel
+// (16-byte partial loads, M % 4 == 0: the host checks), partials summed in a fixed order.
 template <int DT>
 __device__ __forceinline__ void conv_reduce_body(const ConvArgs& a) {
-  const long long total = (long long)a.Cout * a.M;
+  const long long total = (long long)a.Cout * a.M, quads = total / 4;
   const int HoWo = a.Ho * a.Wo;
-  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+  for (long long iq = (long long)blockIdx.x * 256 + threadIdx.x; iq < quads; iq += (long long)gridDim.x * 256) {
+    const long long i = iq * 4;
     const int co = (int)(i / a.M);
-    const long long m = i - (long long)co * a.M;
-    float acc = 0.f;
-    for (int z = 0; z < a.ksplit; ++z) acc += a.part[(long long)z * total + i];
-    float v = cv_round<DT>(acc + ((a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[co]) : 0.f));
+    const long long m0 = i - (long long)co * a.M;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int z = 0; z < a.ksplit; ++z) {
+      const float4 p = *(const float4*)(a.part + (long long)z * total + i);
+      acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+    }
+    const float bias = (a.flags & 1) ? cv_f<DT>(((const uint16_t*)a.bias)[co]) : 0.f;
+    float al = 1.f, be = 0.f;
     if (a.flags & 2) {
       const float g = cv_f<DT>(((const uint16_t*)a.bn_w)[co]), bb = cv_f<DT>(((const uint16_t*)a.bn_b)[co]);
       const float mu = cv_f<DT>(((const uint16_t*)a.bn_mean)[co]), var = cv_f<DT>(((const uint16_t*)a.bn_var)[co]);
-      const float al = g / sqrtf(var + a.eps);
-      v = cv_round<DT>(v * al + (bb - mu * al));
+      al = g / sqrtf(var + a.eps);
+      be = bb - mu * al;
     }
-    const long long n = m / HoWo, p = m - n * HoWo;
-    const long long o = (n * a.Cout + co) * HoWo + p;
-    if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
-    if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
-    ((uint16_t*)a.out)[o] = cv_h<DT>(v);
+    const float vs[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long long m = m0 + j;
+      float v = cv_round<DT>(vs[j] + bias);
+      if (a.flags & 2) v = cv_round<DT>(v * al + be);
+      const long long n = m / HoWo, p = m - n * HoWo;
+      const long long o = (n * a.Cout + co) * HoWo + p;
+      if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
+      if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
+      ((uint16_t*)a.out)[o] = cv_h<DT>(v);
+    }
   }
 }
 

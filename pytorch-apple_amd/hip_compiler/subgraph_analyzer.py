@@ -822,7 +822,7 @@ class Lowering:
         # costs more than the split gains (1x1 512 -> 128 on 28 x 28: 26 -> 29 us), hence K >= 1024
         tiles = ((Cout + 127) // 128) * ((M + 127) // 128)
         ksplit, kchunk = 1, K
-        if tiles < 256 and K >= 1024:
+        if tiles < 256 and K >= 1024 and M % 4 == 0:   # the reduce reads 4 pixels per load
             ksplit = max(1, min(8, (384 + tiles - 1) // tiles, K // 256))
             kchunk = ((K + 31) // 32 + ksplit - 1) // ksplit * 32
             ksplit = (K + kchunk - 1) // kchunk
@@ -846,7 +846,7 @@ class Lowering:
         if ksplit > 1:
             self.emit(LaunchStep(
                 kind="conv", kernel=f"k_conv_reduce_{'bf16' if dt == 'bfloat16' else 'f16'}", module="conv",
-                arg_struct="ConvArgs", args=dict(args), grid=grid1d(Cout * M),
+                arg_struct="ConvArgs", args=dict(args), grid=grid1d(Cout * M // 4),
                 inputs=[out_name + ".kpart"] + ins[2:], outputs=[out_name], params=dict(params, reduce=True)))
         self.views[out_name] = o
 
