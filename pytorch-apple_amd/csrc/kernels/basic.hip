@@ -148,6 +148,16 @@ extern "C" __global__ void __launch_bounds__(256) k_softmax(const SoftmaxArgs a)
 
 // ---------------------------------------------------------------- last-dim mean / argmax
 
+// rows of at most 64 elements (e.g. a 7 x 7 global average pool): one wave per row
+extern "C" __global__ void __launch_bounds__(256) k_mean_short(const ReduceLastArgs a) {
+  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= a.rows) return;   // wave-uniform
+  const float v = lane < a.cols ? ld_f(a.x, row * a.cols + lane, a.x_dtype) : 0.f;
+  const float s = wave_sum(v);
+  if (lane == 0) st_f(a.out, row, a.out_dtype, s / (float)a.cols);
+}
+
 extern "C" __global__ void __launch_bounds__(256) k_mean_last(const ReduceLastArgs a) {
   __shared__ float red[4];
   const long long row = blockIdx.x;

@@ -315,13 +315,44 @@ extern "C" __global__ void CV_ATTRS k_conv_bf16_3x3(const ConvArgs a) { conv_bod
 // max over the window; positions outside the image are skipped (ATen's -inf padding)
 extern "C" __global__ void __launch_bounds__(256) k_maxpool2d(const PoolArgs a) {
   const long long total = a.planes * a.Ho * a.Wo;
+  const bool small = total < (1ll << 31) && a.planes * a.H * a.W < (1ll << 31);   // 32-bit index math
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
-    const int wo = (int)(i % a.Wo);
-    const int ho = (int)((i / a.Wo) % a.Ho);
-    const long long pl = i / ((long long)a.Wo * a.Ho);
+    int wo, ho;
+    long long pl;
+    if (small) {
+      const unsigned u = (unsigned)i, q = u / (unsigned)a.Wo;
+      wo = (int)(u - q * (unsigned)a.Wo);
+      const unsigned q2 = q / (unsigned)a.Ho;
+      ho = (int)(q - q2 * (unsigned)a.Ho);
+      pl = q2;
+    } else {
+      wo = (int)(i % a.Wo);
+      ho = (int)((i / a.Wo) % a.Ho);
+      pl = i / ((long long)a.Wo * a.Ho);
+    }
     const uint16_t* x = (const uint16_t*)a.x + pl * a.H * a.W;
     float best = -INFINITY;
     bool nan = false;
+    if (a.kh == 3 && a.kw == 3) {   // all nine loads in flight together (clamped addresses, masked values)
+      uint16_t v[9];
+      bool ok[9];
+#pragma unroll
+      for (int t = 0; t < 9; ++t) {
+        const int hi = ho * a.sh - a.ph + t / 3, wi = wo * a.sw - a.pw + t % 3;
+        ok[t] = (unsigned)hi < (unsigned)a.H && (unsigned)wi < (unsigned)a.W;
+        v[t] = x[ok[t] ? hi * a.W + wi : 0];
+      }
+#pragma unroll
+      for (int t = 0; t < 9; ++t) {
+        if (!ok[t]) continue;
+        const float f = a.dtype == HS_BF16 ? bf16_to_f32(v[t]) : f16_to_f32(v[t]);
+        nan |= f != f;
+        best = fmaxf(best, f);
+      }
+      if (nan) best = NAN;
+      ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(best) : f32_to_f16(best);
+      continue;
+    }
     for (int kh = 0; kh < a.kh; ++kh) {
       const int hi = ho * a.sh - a.ph + kh;
       if (hi < 0 || hi >= a.H) continue;

@@ -70,6 +70,18 @@ def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
     return (max(1, min(cap, (int(n) + block - 1) // block)), 1, 1)
 
 
+def mean_rows_step(x, out, rows: int, cols: int, x_dtype: str, out_dtype: str, ins, outs) -> LaunchStep:
+    """Mean over the last dimension of a [rows, cols] contiguous view: one wave per row when the
+    rows are short (k_mean_short, e.g. a 7 x 7 global pool), else one workgroup per row."""
+    short = cols <= 64
+    return LaunchStep(
+        kind="reduction", kernel="k_mean_short" if short else "k_mean_last", module="basic",
+        arg_struct="ReduceLastArgs",
+        args=dict(x=x, out=out, rows=rows, cols=cols, x_dtype=DTYPE_CODE[x_dtype], out_dtype=DTYPE_CODE[out_dtype]),
+        grid=((max(rows, 1) + 3) // 4 if short else max(rows, 1), 1, 1), inputs=ins, outputs=outs,
+        params={"rows": rows, "cols": cols})
+
+
 def apply_alias(node: OpNode, v: TView) -> TView | None:
     """The view a shape op produces from ``v`` (getitem excluded), or None when it needs a copy."""
     op = node.op_type
@@ -775,11 +787,7 @@ class Lowering:
         cols = numel([x.shape[d] for d in dims])
         rows = pv.numel // cols
         o = self.new_storage(out.name, out.shape, out.dtype)
-        self.emit(LaunchStep(
-            kind="reduction", kernel="k_mean_last", module="basic", arg_struct="ReduceLastArgs",
-            args=dict(x=self.ref(pv), out=self.ref(o), rows=rows, cols=cols, x_dtype=DTYPE_CODE[pv.dtype],
-                      out_dtype=DTYPE_CODE[out.dtype]),
-            grid=(max(rows, 1), 1, 1), inputs=[x.name], outputs=[out.name], params={"rows": rows, "cols": cols}))
+        self.emit(mean_rows_step(self.ref(pv), self.ref(o), rows, cols, pv.dtype, out.dtype, [x.name], [out.name]))
         self.views[out.name] = o
 
     # ------------------------------------------------------------------ convolution network ops
@@ -892,12 +900,8 @@ class Lowering:
         out = node.outputs[0]
         N, C, H, W = x.shape
         o = self.new_storage(out.name, out.shape, out.dtype)
-        self.emit(LaunchStep(
-            kind="reduction", kernel="k_mean_last", module="basic", arg_struct="ReduceLastArgs",
-            args=dict(x=self.ref(x), out=self.ref(o), rows=N * C, cols=H * W, x_dtype=DTYPE_CODE[x.dtype],
-                      out_dtype=DTYPE_CODE[out.dtype]),
-            grid=(max(N * C, 1), 1, 1), inputs=[node.inputs[0].name], outputs=[out.name],
-            params={"rows": N * C, "cols": H * W}))
+        self.emit(mean_rows_step(self.ref(x), self.ref(o), N * C, H * W, x.dtype, out.dtype, [node.inputs[0].name],
+                                 [out.name]))
         self.views[out.name] = o
 
     def lower_argmax(self, node: OpNode) -> None:
