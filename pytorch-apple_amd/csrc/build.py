@@ -11,6 +11,7 @@ Every HIP compile carries ``-Xclang -target-feature -Xclang -packed-fp32-ops``
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import subprocess
 import sys
@@ -21,6 +22,25 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 NO_PK_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 KDIR = os.path.join(HERE, "kernels")
+
+
+SHIM_SOURCES = [os.path.join(HERE, "shim.cpp"), os.path.join(KDIR, "common.h"), os.path.join(ROOT, "include", "hipshim.h")]
+
+
+def source_hash(paths: list[str]) -> str:
+    """sha1 over the files' bytes in order; stored beside each built file as ``<out>.srchash``
+    so the loader (``hip_runtime/_shim.py``) refuses a build older than its sources."""
+    h = hashlib.sha1()
+    for p in paths:
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def _stamp(out: str, sources: list[str]) -> None:
+    with open(out + ".srchash.tmp", "w") as f:
+        f.write(source_hash(sources) + "\n")
+    os.replace(out + ".srchash.tmp", out + ".srchash")
 
 
 def _run(cmd: list[str]) -> None:
@@ -35,6 +55,7 @@ def build_shim() -> str:
           "-I", os.path.join(ROOT, "include"), os.path.join(HERE, "shim.cpp"), "-o", out + ".tmp",
           "-L/opt/rocm/lib", "-lhiprtc", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(out + ".tmp", out)
+    _stamp(out, SHIM_SOURCES)
     return out
 
 
@@ -43,6 +64,7 @@ def build_kernel(src: str) -> str:
     _run([HIPCC, "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17", *NO_PK_FP32, "-I", KDIR, src,
           "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
+    _stamp(out, [src, os.path.join(KDIR, "common.h")])
     return out
 
 

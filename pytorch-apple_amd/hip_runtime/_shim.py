@@ -8,11 +8,15 @@ code paths can run), but the first call raises ``HIPShimError``.
 from __future__ import annotations
 
 import ctypes as C
+import hashlib
 import os
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG, "csrc", "libhipshim.so")
 KERNEL_DIR = os.path.join(PKG, "csrc", "kernels")
+# what libhipshim.so is built from (csrc/build.py SHIM_SOURCES)
+SHIM_SOURCES = [os.path.join(PKG, "csrc", "shim.cpp"), os.path.join(KERNEL_DIR, "common.h"),
+                os.path.join(os.path.dirname(PKG), "include", "hipshim.h")]
 
 
 class HIPShimError(RuntimeError):
@@ -58,12 +62,36 @@ EXPORTED = tuple(_SIGS)
 _lib = None
 
 
+def _source_hash(paths: list[str]) -> str:
+    h = hashlib.sha1()
+    for p in paths:
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def check_built_from(out: str, sources: list[str]) -> None:
+    """Raise ``HIPShimError`` unless ``out`` was built from the current bytes of ``sources``
+    (the ``<out>.srchash`` stamp written by ``csrc/build.py``). A code object or shim older
+    than ``common.h`` disagrees with the argument structs the host packs, and a kernel that
+    reads fields past the packed struct would take them from unrelated memory."""
+    try:
+        with open(out + ".srchash") as f:
+            stamp = f.read().strip()
+    except OSError:
+        raise HIPShimError(f"{out} has no build stamp; rebuild (`python -c 'import __graft_entry__ as g; g.build()'`)")
+    if stamp != _source_hash(sources):
+        raise HIPShimError(f"{out} is older than its sources; rebuild (`python -c 'import __graft_entry__ as g; "
+                           f"g.build()'`)")
+
+
 def lib():
     """Load ``libhipshim.so`` once; raise ``HIPShimError`` when it is missing."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise HIPShimError(f"{LIB_PATH} not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+        check_built_from(LIB_PATH, SHIM_SOURCES)
         L = C.CDLL(LIB_PATH)
         for name, (args, res) in _SIGS.items():
             f = getattr(L, name)

@@ -137,6 +137,11 @@ class ModuleCache:
         path = os.path.join(_shim.KERNEL_DIR, module + ".hsaco")
         if not os.path.exists(path):
             raise _shim.HIPShimError(f"code object {path} not built (run csrc/build.py)")
+        _shim.check_built_from(path, [path[:-6] + ".hip", os.path.join(_shim.KERNEL_DIR, "common.h")])
+        if not self.modules:   # first code object: the packed structs must match the built ones
+            bad = check_layouts()
+            if bad:
+                raise _shim.HIPShimError(f"argument struct sizes differ from the built code (ctypes, C): {bad}")
         with open(path, "rb") as f:
             self._load(module, f.read())
 

@@ -35,6 +35,33 @@ def test_kernel_argument_layouts_match():
     assert C.sizeof(STRUCTS["GemvArgs"]) % 8 == 0
 
 
+def test_built_code_matches_its_sources():
+    """Every code object and the shim carry the hash of the sources they were built from, and
+    the tree's built files are current (a stale code object reads argument fields the host no
+    longer packs)."""
+    kdir = _shim.KERNEL_DIR
+    _shim.check_built_from(_shim.LIB_PATH, _shim.SHIM_SOURCES)
+    built = [f for f in os.listdir(kdir) if f.endswith(".hsaco")]
+    assert len(built) >= 6
+    for f in built:
+        _shim.check_built_from(os.path.join(kdir, f), [os.path.join(kdir, f[:-6] + ".hip"),
+                                                      os.path.join(kdir, "common.h")])
+
+
+def test_stale_build_is_refused(tmp_path):
+    src, hdr, out = tmp_path / "k.hip", tmp_path / "common.h", tmp_path / "k.hsaco"
+    src.write_text("kernel v1")
+    hdr.write_text("struct A { int x; };")
+    out.write_bytes(b"code")
+    with pytest.raises(_shim.HIPShimError, match="no build stamp"):
+        _shim.check_built_from(str(out), [str(src), str(hdr)])
+    (tmp_path / "k.hsaco.srchash").write_text(_shim._source_hash([str(src), str(hdr)]) + "\n")
+    _shim.check_built_from(str(out), [str(src), str(hdr)])
+    hdr.write_text("struct A { int x; void* pf; };")
+    with pytest.raises(_shim.HIPShimError, match="older than its sources"):
+        _shim.check_built_from(str(out), [str(src), str(hdr)])
+
+
 def test_init_reports_errors_without_aborting():
     lib = _shim.lib()
     rc = lib.hs_init(12345)
