@@ -55,8 +55,51 @@ __device__ __forceinline__ uint16_t gm_pack(float f) {
   return DT == HS_BF16 ? f32_to_bf16(f) : f32_to_f16(f);
 }
 
-template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false>
+// slot permutation of the direct-to-LDS rows (GM_SWZ_PAIR: rows 2j and 2j + 1 share one,
+// for an LDS that serves 16 lanes of a 16-byte read per cycle)
+#ifndef GM_SWZ_PAIR
+#define GM_SWZ_PAIR 0
+#endif
+__device__ __forceinline__ int gm_swz(int r) { return GM_SWZ_PAIR ? (r >> 1) & 7 : r & 7; }
+
+// 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane (gfx950). Issued
+// from inline assembly so that the compiler does not wait for every one of them before each
+// LDS read (it cannot tell the stages apart); the waits are explicit (gm_vmcnt) instead, and
+// the loop issues no other vector-memory loads.
+__device__ __forceinline__ void gm_dma16(const void* g, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+// s_waitcnt vmcnt(N), the other counters untouched
+template <int N>
+__device__ __forceinline__ void gm_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+// wait until at most `after` stages of NI loads each are outstanding (after <= MAXA, uniform)
+template <int NI, int MAXA>
+__device__ __forceinline__ void gm_vmcnt_after(int after) {
+  if constexpr (MAXA > 0) {
+    if (after >= MAXA) {
+      gm_vmcnt<MAXA * NI>();
+      return;
+    }
+    gm_vmcnt_after<NI, MAXA - 1>(after);
+  } else {
+    gm_vmcnt<0>();
+  }
+}
+
+// STAGES 0: LDS double buffer filled through registers (the loads of step s + 1 are in flight
+// while step s is multiplied). STAGES >= 3 (BK 64, not KN): the operands go from global memory
+// straight into LDS (gfx950 global_load_lds_dwordx4), STAGES buffers deep, so the loads of
+// steps s + 1 .. s + STAGES - 1 are in flight while step s is multiplied and no registers hold
+// them. Those rows are unpadded 128-byte rows; 16-byte chunk c of row r sits in slot
+// c ^ gm_swz(r), so the fragment reads of 8 consecutive rows hit 8 different bank groups.
+template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false,
+          int STAGES = 0>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
+  constexpr bool DMA = STAGES >= 3;
+  static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
   constexpr int CPR = BK / 8;             // 16-byte chunks per staged row
   constexpr int BNT = BN * NW;            // weight rows staged per step (BN columns per weight)
@@ -64,8 +107,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr int TJ = BN / 64;             // 32-column MFMA tiles per wave and weight
   constexpr int A_LD = BM * BK / 8 / 256;    // 16-byte A loads per thread per step
   constexpr int B_LD = BNT * BK / 8 / 256;   // 16-byte B loads per thread per step
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BNT][LDK];
+  constexpr int SROW = 64;                   // DMA: elements per LDS row
+  constexpr int SSTAGE = (BM + BNT) * SROW;  // DMA: elements per stage (A rows, then B rows)
+  __shared__ __attribute__((aligned(16))) uint16_t As[DMA ? 1 : 2][DMA ? 1 : BM][LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[DMA ? 1 : 2][DMA ? 1 : BNT][LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Ls[DMA ? STAGES * SSTAGE : 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
   // XCD-aware tile order: workgroup L (dispatch order) runs on XCD L % 8, so L is remapped
@@ -145,28 +191,30 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       *(uint4*)&Bs[buf][row][col] = v;
     }
   };
-#define GM_LOAD_STEP(k0)                  \
+#define GM_LOAD_INTO(k0, A, B)            \
   do {                                    \
-    ra0 = a_ld(0, (k0));                  \
-    if (A_LD > 1) ra1 = a_ld(1, (k0));    \
-    if (A_LD > 2) ra2 = a_ld(2, (k0));    \
-    if (A_LD > 3) ra3 = a_ld(3, (k0));    \
-    rb0 = b_ld(0, (k0));                  \
-    if (B_LD > 1) rb1 = b_ld(1, (k0));    \
-    if (B_LD > 2) rb2 = b_ld(2, (k0));    \
-    if (B_LD > 3) rb3 = b_ld(3, (k0));    \
+    A##0 = a_ld(0, (k0));                 \
+    if (A_LD > 1) A##1 = a_ld(1, (k0));   \
+    if (A_LD > 2) A##2 = a_ld(2, (k0));   \
+    if (A_LD > 3) A##3 = a_ld(3, (k0));   \
+    B##0 = b_ld(0, (k0));                 \
+    if (B_LD > 1) B##1 = b_ld(1, (k0));   \
+    if (B_LD > 2) B##2 = b_ld(2, (k0));   \
+    if (B_LD > 3) B##3 = b_ld(3, (k0));   \
   } while (0)
-#define GM_STORE_STEP(buf)                \
+#define GM_STORE_FROM(buf, A, B)          \
   do {                                    \
-    a_st((buf), 0, ra0);                  \
-    if (A_LD > 1) a_st((buf), 1, ra1);    \
-    if (A_LD > 2) a_st((buf), 2, ra2);    \
-    if (A_LD > 3) a_st((buf), 3, ra3);    \
-    b_st((buf), 0, rb0);                  \
-    if (B_LD > 1) b_st((buf), 1, rb1);    \
-    if (B_LD > 2) b_st((buf), 2, rb2);    \
-    if (B_LD > 3) b_st((buf), 3, rb3);    \
+    a_st((buf), 0, A##0);                 \
+    if (A_LD > 1) a_st((buf), 1, A##1);   \
+    if (A_LD > 2) a_st((buf), 2, A##2);   \
+    if (A_LD > 3) a_st((buf), 3, A##3);   \
+    b_st((buf), 0, B##0);                 \
+    if (B_LD > 1) b_st((buf), 1, B##1);   \
+    if (B_LD > 2) b_st((buf), 2, B##2);   \
+    if (B_LD > 3) b_st((buf), 3, B##3);   \
   } while (0)
+#define GM_LOAD_STEP(k0) GM_LOAD_INTO(k0, ra, rb)
+#define GM_STORE_STEP(buf) GM_STORE_FROM(buf, ra, rb)
 
   gm_f32x16 acc[NW][TI][TJ];
 #pragma unroll
@@ -188,32 +236,113 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     W0 += kbeg;
     W1 += kbeg;
   }
-  GM_LOAD_STEP(0);
-  GM_STORE_STEP(0);
-  __syncthreads();
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // fragment row/column and k offset of this lane
-  for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nsteps) GM_LOAD_STEP((s + 1) * BK);
+  if constexpr (!DMA) {
+    auto compute = [&](const int buf) {
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      uint4 af[TI], bfr[NW][TJ];
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        uint4 af[TI], bfr[NW][TJ];
 #pragma unroll
-      for (int i = 0; i < TI; ++i) af[i] = *(const uint4*)&As[buf][wr * (BM / 2) + i * 32 + fr][ks * 16 + fk];
+        for (int i = 0; i < TI; ++i) af[i] = *(const uint4*)&As[buf][wr * (BM / 2) + i * 32 + fr][ks * 16 + fk];
 #pragma unroll
-      for (int u = 0; u < NW; ++u)
+        for (int u = 0; u < NW; ++u)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          bfr[u][j] = *(const uint4*)&Bs[buf][u * BN + wc * (BN / 2) + j * 32 + fr][ks * 16 + fk];
+          for (int j = 0; j < TJ; ++j)
+            bfr[u][j] = *(const uint4*)&Bs[buf][u * BN + wc * (BN / 2) + j * 32 + fr][ks * 16 + fk];
 #pragma unroll
-      for (int u = 0; u < NW; ++u)
+        for (int u = 0; u < NW; ++u)
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
+          for (int i = 0; i < TI; ++i)
 #pragma unroll
-          for (int j = 0; j < TJ; ++j) acc[u][i][j] = gm_mfma<DT>(af[i], bfr[u][j], acc[u][i][j]);
-    }
-    if (s + 1 < nsteps) GM_STORE_STEP(buf ^ 1);
+            for (int j = 0; j < TJ; ++j) acc[u][i][j] = gm_mfma<DT>(af[i], bfr[u][j], acc[u][i][j]);
+      }
+    };
+    GM_LOAD_STEP(0);
+    GM_STORE_STEP(0);
     __syncthreads();
+    for (int s = 0; s < nsteps; ++s) {
+      const int buf = s & 1;
+      if (s + 1 < nsteps) GM_LOAD_STEP((s + 1) * BK);
+      compute(buf);
+      if (s + 1 < nsteps) GM_STORE_STEP(buf ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // wave w fills rows [w * 8 * NA, (w + 1) * 8 * NA) of A and [w * 8 * NB, ...) of B; one
+    // instruction writes 8 rows (1 KB): lane l -> row 8 * blk + l / 8, slot l % 8, which holds
+    // chunk (l % 8) ^ gm_swz(row), so the lane fetches that chunk
+    constexpr int NA = BM / 32, NB = BNT / 32;   // DMA instructions per wave and step
+    const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&Ls[0];
+    const int lr = lane >> 3, ls = lane & 7;
+    const char* asrc[NA];
+    const char* bsrc[NB];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      const int row = (wave * NA + q) * 8 + lr;
+      const long long m = min(m_base + row, a.M - 1);
+      asrc[q] = (const char*)(X + m * a.ldx) + ((ls ^ gm_swz(row)) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int row = (wave * NB + q) * 8 + lr;
+      const uint16_t* wrow;
+      if constexpr (GRP) {
+        wrow = W0 + (long long)(min(n_base + row, g_hi - 1) - g_lo) * a.ldw;
+      } else {
+        const int u = row / BN, n = min(n_base + row % BN, a.N - 1);
+        wrow = (u == 0 ? W0 : W1) + (long long)n * a.ldw;
+      }
+      bsrc[q] = (const char*)wrow + ((ls ^ gm_swz(row)) * 16);
+    }
+    auto issue = [&](int st) {   // stage st of the K loop into LDS buffer st % STAGES
+      const unsigned base = lds0 + (unsigned)((st % STAGES) * SSTAGE) * 2u;
+      const long long kb = (long long)st * BK * 2;
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+        gm_dma16(asrc[q] + kb, __builtin_amdgcn_readfirstlane(base + (unsigned)((wave * NA + q) * 8 * SROW * 2)));
+#pragma unroll
+      for (int q = 0; q < NB; ++q)
+        gm_dma16(bsrc[q] + kb, __builtin_amdgcn_readfirstlane(base + (unsigned)((BM + (wave * NB + q) * 8) * SROW * 2)));
+    };
+    auto compute = [&](const int buf) {
+      const uint16_t* LA = Ls + buf * SSTAGE;
+      const uint16_t* LB = LA + BM * SROW;
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        const int c = ks * 2 + (lane >> 5);   // this lane's 16-byte chunk of the 64-element row
+        uint4 af[TI], bfr[NW][TJ];
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+          const int r = wr * (BM / 2) + i * 32 + fr;
+          af[i] = *(const uint4*)&LA[r * SROW + ((c ^ gm_swz(r)) * 8)];
+        }
+#pragma unroll
+        for (int u = 0; u < NW; ++u)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) {
+            const int r = u * BN + wc * (BN / 2) + j * 32 + fr;
+            bfr[u][j] = *(const uint4*)&LB[r * SROW + ((c ^ gm_swz(r)) * 8)];
+          }
+#pragma unroll
+        for (int u = 0; u < NW; ++u)
+#pragma unroll
+          for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[u][i][j] = gm_mfma<DT>(af[i], bfr[u][j], acc[u][i][j]);
+      }
+    };
+    constexpr int NI = NA + NB;   // vmcnt per stage
+#pragma unroll
+    for (int st = 0; st < STAGES - 1; ++st)
+      if (st < nsteps) issue(st);
+    for (int s = 0; s < nsteps; ++s) {
+      // stage s has landed when at most the stages issued after it are outstanding
+      gm_vmcnt_after<NI, STAGES - 2>(min(nsteps - 1 - s, STAGES - 2));
+      __syncthreads();   // every wave's part of stage s is in LDS; every wave is done with step s - 1
+      if (s + STAGES - 1 < nsteps) issue(s + STAGES - 1);   // into the buffer step s - 1 used
+      compute(s % STAGES);
+    }
+    gm_vmcnt<0>();
   }
 
   if (a.ksplit > 1) {   // raw fp32 partial sums; k_gemm_reduce_* applies the epilogue
@@ -261,6 +390,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 
 #undef GM_LOAD_STEP
 #undef GM_STORE_STEP
+#undef GM_LOAD_INTO
+#undef GM_STORE_FROM
 
 // Split-K reduction and epilogue: one thread per output element (fixed summation order).
 template <int DT, int EPI>
@@ -294,39 +425,49 @@ __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
 // per prefetch, which hides the operand latency better; 73.7 KB of LDS for 128 x 128 tiles, so two
 // workgroups still share a CU). Measured at M = 512, K = 1536: lm_head 381 -> 312 us, gate/up
 // 61 -> 51 us; K = 8960 down 39 -> 30 us. The host takes _k64 when K (and the split-K chunk) is a
-// multiple of 64.
-#define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN)                                                      \
-  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); } \
-  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN, false, 64>(a); }
+// multiple of 64. Suffix _k64d: K step 64 with direct-to-LDS staging, ST buffers deep (the stage
+// count fits two workgroups per CU where the tile allows). Measured at M = 512 (same launch,
+// bit-identical results): gate/up 64 x 64 57 -> 52 us, down 128 x 128 with 4 K splits 31 -> 26 us,
+// o_proj 64 x 64 with 2 K splits 15.8 -> 9.5 us, q | k | v 14.6 -> 11.4 us; the lm_head's 4,748
+// tiles of 128 x 128 keep enough workgroups in flight without it (324 us against 367).
+#define GEMM_KERNEL(NAME, DT, EPI, NW, BM, BN, ST)                                                      \
+  extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN>(a); }     \
+  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, EPI, NW, BM, BN, false, 64>(a); } \
+  extern "C" __global__ void GM_ATTRS NAME##_k64d(const GemmArgs a) {                                  \
+    gemm_body<DT, EPI, NW, BM, BN, false, 64, false, ST>(a);                                           \
+  }
 #define GEMM_KERNEL_KN(NAME, DT, BM, BN)                                                                  \
   extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, true>(a); } \
   extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, true, 64>(a); }
 #define GEMM_REDUCE(NAME, DT, EPI) \
   extern "C" __global__ void __launch_bounds__(256) NAME(const GemmArgs a) { gemm_reduce_body<DT, EPI>(a); }
 
-// k_gemm_<dtype>_<epilogue>_m<BM>n<BN>: BN columns per weight
-GEMM_KERNEL(k_gemm_bf16_bias_m128n128, HS_BF16, GE_BIAS, 1, 128, 128)
-GEMM_KERNEL(k_gemm_bf16_bias_m64n128, HS_BF16, GE_BIAS, 1, 64, 128)
-GEMM_KERNEL(k_gemm_bf16_bias_m64n64, HS_BF16, GE_BIAS, 1, 64, 64)
-GEMM_KERNEL(k_gemm_bf16_resid_m128n128, HS_BF16, GE_RESID, 1, 128, 128)
-GEMM_KERNEL(k_gemm_bf16_resid_m64n128, HS_BF16, GE_RESID, 1, 64, 128)
-GEMM_KERNEL(k_gemm_bf16_resid_m64n64, HS_BF16, GE_RESID, 1, 64, 64)
-GEMM_KERNEL(k_gemm_bf16_silu_m128n64, HS_BF16, GE_SILU, 2, 128, 64)
-GEMM_KERNEL(k_gemm_bf16_silu_m64n64, HS_BF16, GE_SILU, 2, 64, 64)
-GEMM_KERNEL(k_gemm_f16_bias_m128n128, HS_F16, GE_BIAS, 1, 128, 128)
-GEMM_KERNEL(k_gemm_f16_bias_m64n128, HS_F16, GE_BIAS, 1, 64, 128)
-GEMM_KERNEL(k_gemm_f16_bias_m64n64, HS_F16, GE_BIAS, 1, 64, 64)
-GEMM_KERNEL(k_gemm_f16_resid_m128n128, HS_F16, GE_RESID, 1, 128, 128)
-GEMM_KERNEL(k_gemm_f16_resid_m64n128, HS_F16, GE_RESID, 1, 64, 128)
-GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64)
+// k_gemm_<dtype>_<epilogue>_m<BM>n<BN>: BN columns per weight; last argument: direct-to-LDS stages
+GEMM_KERNEL(k_gemm_bf16_bias_m128n128, HS_BF16, GE_BIAS, 1, 128, 128, 4)
+GEMM_KERNEL(k_gemm_bf16_bias_m64n128, HS_BF16, GE_BIAS, 1, 64, 128, 3)
+GEMM_KERNEL(k_gemm_bf16_bias_m64n64, HS_BF16, GE_BIAS, 1, 64, 64, 4)
+GEMM_KERNEL(k_gemm_bf16_resid_m128n128, HS_BF16, GE_RESID, 1, 128, 128, 4)
+GEMM_KERNEL(k_gemm_bf16_resid_m64n128, HS_BF16, GE_RESID, 1, 64, 128, 3)
+GEMM_KERNEL(k_gemm_bf16_resid_m64n64, HS_BF16, GE_RESID, 1, 64, 64, 4)
+GEMM_KERNEL(k_gemm_bf16_silu_m128n64, HS_BF16, GE_SILU, 2, 128, 64, 3)
+GEMM_KERNEL(k_gemm_bf16_silu_m64n64, HS_BF16, GE_SILU, 2, 64, 64, 3)
+GEMM_KERNEL(k_gemm_f16_bias_m128n128, HS_F16, GE_BIAS, 1, 128, 128, 4)
+GEMM_KERNEL(k_gemm_f16_bias_m64n128, HS_F16, GE_BIAS, 1, 64, 128, 3)
+GEMM_KERNEL(k_gemm_f16_bias_m64n64, HS_F16, GE_BIAS, 1, 64, 64, 4)
+GEMM_KERNEL(k_gemm_f16_resid_m128n128, HS_F16, GE_RESID, 1, 128, 128, 4)
+GEMM_KERNEL(k_gemm_f16_resid_m64n128, HS_F16, GE_RESID, 1, 64, 128, 3)
+GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
 // grouped (q | k | v projections of one activation into one [M, N] output; no split K)
-#define GEMM_KERNEL_GRP(NAME, DT, BM, BN)                                                                      \
+#define GEMM_KERNEL_GRP(NAME, DT, BM, BN, ST)                                                                  \
   extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, false, 32, true>(a); } \
-  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, false, 64, true>(a); }
-GEMM_KERNEL_GRP(k_gemm_bf16_grp_m64n64, HS_BF16, 64, 64)
-GEMM_KERNEL_GRP(k_gemm_bf16_grp_m128n128, HS_BF16, 128, 128)
-GEMM_KERNEL_GRP(k_gemm_f16_grp_m64n64, HS_F16, 64, 64)
-GEMM_KERNEL_GRP(k_gemm_f16_grp_m128n128, HS_F16, 128, 128)
+  extern "C" __global__ void GM_ATTRS NAME##_k64(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, false, 64, true>(a); } \
+  extern "C" __global__ void GM_ATTRS NAME##_k64d(const GemmArgs a) {                                              \
+    gemm_body<DT, GE_BIAS, 1, BM, BN, false, 64, true, ST>(a);                                                     \
+  }
+GEMM_KERNEL_GRP(k_gemm_bf16_grp_m64n64, HS_BF16, 64, 64, 4)
+GEMM_KERNEL_GRP(k_gemm_bf16_grp_m128n128, HS_BF16, 128, 128, 4)
+GEMM_KERNEL_GRP(k_gemm_f16_grp_m64n64, HS_F16, 64, 64, 4)
+GEMM_KERNEL_GRP(k_gemm_f16_grp_m128n128, HS_F16, 128, 128, 4)
 GEMM_REDUCE(k_gemm_reduce_bf16_bias, HS_BF16, GE_BIAS)
 GEMM_REDUCE(k_gemm_reduce_bf16_resid, HS_BF16, GE_RESID)
 GEMM_REDUCE(k_gemm_reduce_bf16_silu, HS_BF16, GE_SILU)

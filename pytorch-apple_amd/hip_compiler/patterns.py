@@ -835,10 +835,12 @@ def _emit_qkv_prefill(low, xname, q, k, v, names) -> None:
         raise NotImplementedError("prefill RoPE reads int64 or int32 positions")
     N = (H + 2 * KVH) * D
     n1, n2 = H * D, (H + KVH) * D
-    bm, bn, _ = gemm_tiling(T, N, K)
+    bm, bn, _, dma = gemm_tiling(T, N, K)
     if n1 % bn or n2 % bn:
         bn = 64
     bk = 64 if K % 64 == 0 else 32
+    if bm == 64 and bn == 128:   # grouped kernels come in 64 x 64 and 128 x 128
+        bn = 64
     ws = [low.aligned16(low.contiguous(e["w"].name), e["w"].name) for e in (q, k, v)]
     bs = [low.contiguous(e["b"].name) if e["b"] is not None else None for e in (q, k, v)]
     y = low.new_storage(q["out"] + ".qkv", [T, N], "bfloat16")
@@ -848,11 +850,12 @@ def _emit_qkv_prefill(low, xname, q, k, v, names) -> None:
                 M=T, ldx=K, ldw=K, ldo=N, ldr=N, sx=0, sw=0, so=0, batch=1, bdiv=1, N=N, K=K,
                 flags=1 if bs[0] else 0, ksplit=1, kchunk=K, nw=1, n1=n1, n2=n2)
     ins = [xname] + [e["w"].name for e in (q, k, v)] + [e["b"].name for e in (q, k, v) if e["b"] is not None]
-    low.emit(LaunchStep(kind="gemm", kernel=f"k_gemm_bf16_grp_m{bm}n{bn}" + ("_k64" if bk == 64 else ""),
+    low.emit(LaunchStep(kind="gemm", kernel=f"k_gemm_bf16_grp_m{bm}n{bn}" + ("_k64d" if dma else "_k64" if bk == 64
+                                                                               else ""),
                         module="gemm", arg_struct="GemmArgs", args=args,
                         grid=((N + bn - 1) // bn, (T + bm - 1) // bm, 1), inputs=ins, outputs=[y.storage],
                         params={"M": T, "N": N, "K": K, "epilogue": "bias", "groups": [n1, n2], "mfma": True,
-                                "tile": (bm, bn), "ksplit": 1, "bk": bk, "nodes": names}))
+                                "tile": (bm, bn), "ksplit": 1, "bk": bk, "lds_direct": dma, "nodes": names}))
     qo = low.new_storage(q["out"], [1, H, T, D], "bfloat16")
     kc, vc = low.views[k["past"]], low.views[v["past"]]
     rargs = dict(y=low.ref(y), inv_freq=low.ref(inv), pos_ids=low.ref(pos), cache_pos=low.ref(cpos), q_out=low.ref(qo),

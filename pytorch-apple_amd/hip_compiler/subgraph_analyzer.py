@@ -40,30 +40,42 @@ HS_BF16, HS_F16 = DTYPE_CODE["bfloat16"], DTYPE_CODE["float16"]
 GEMM_MIN_M = 16
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
+GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
 
 
-def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int]:
-    """(BM, BN, split-K) for an M x N x K MFMA GEMM (nw = 2: two weights, BN columns of each).
+def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, bool]:
+    """(BM, BN, split-K, direct-to-LDS) for an M x N x K MFMA GEMM (nw = 2: two weights, BN
+    columns of each).
 
-    Rules fitted to a sweep on MI355X at M = 512 (bf16, K step 64, split-K reduce pass
-    included): the largest tile that still gives >= 256 workgroups, else the smallest tile.
-    Split K only where it pays for the reduce pass: long rows (K >= 4096) on 128 x 128 tiles
-    with up to 8 splits (~384 workgroups; down_proj 512 x 1536 x 8960: 35 us against 41+ us
-    without), or fewer than 128 tiles (k/v projections, 512 x 256 x 1536: 4 splits, 9.2 us
-    against 10.6). q/o projections (192 tiles of 64 x 64) run unsplit: 14-16 us against 17."""
-    tiles = [(128, 64), (64, 64)] if nw == 2 else [(128, 128), (64, 128), (64, 64)]
+    Rules fitted to sweeps on MI355X at M = 512 (bf16, K step 64, split-K reduce pass
+    included). Direct-to-LDS staging (the ``_k64d`` kernels: operands land in LDS several
+    K steps ahead without passing through registers) needs K % 64 == 0; it pays wherever the
+    tile grid is not large enough to hide the operand latency by itself, i.e. below
+    GEMM_DMA_MAX_TILES tiles. Two weights (gate/up with the SiLU-mul epilogue): 64 x 64
+    tiles, 52 us against 57 for 128 x 64 without. One weight: the largest tile that still
+    gives >= 256 workgroups; long rows (K >= 4096) take 128 x 128 with up to 4 K splits
+    (down_proj 512 x 1536 x 8960: 26 us with 4 splits, 32 with 8); other grids under 256
+    tiles split K toward ~384 workgroups (o_proj 512 x 1536 x 1536 on 64 x 64: 9.5 us with
+    2 splits, 12.9 unsplit). The lm_head (4,748 tiles of 128 x 128) keeps register staging:
+    324 us against 367."""
+    dma = K % 64 == 0
     ntiles = lambda bm, bn: ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
-    for bm, bn in tiles:
-        if ntiles(bm, bn) >= GEMM_TARGET_WGS:
-            return bm, bn, 1
-    if nw == 1 and K >= 4096:
+    if nw == 2:
+        if dma:
+            return 64, 64, 1, True
+        for bm, bn in ((128, 64), (64, 64)):
+            if ntiles(bm, bn) >= GEMM_TARGET_WGS:
+                return bm, bn, 1, False
+        return 64, 64, 1, False
+    for bm, bn in ((128, 128), (64, 128), (64, 64)):
+        t = ntiles(bm, bn)
+        if t >= GEMM_TARGET_WGS:
+            return bm, bn, 1, dma and t < GEMM_DMA_MAX_TILES
+    if K >= 4096:
         t = ntiles(128, 128)
-        return 128, 128, max(1, min(8, 384 // t, K // GEMM_MIN_KCHUNK))
-    bm, bn = tiles[-1]
-    t = ntiles(bm, bn)
-    if t >= 128:
-        return bm, bn, 1
-    return bm, bn, max(1, min((128 + t - 1) // t, K // GEMM_MIN_KCHUNK))
+        return 128, 128, max(1, min(4, 384 // t, K // GEMM_MIN_KCHUNK)), dma
+    t = ntiles(64, 64)
+    return 64, 64, max(1, min((384 + t - 1) // t, K // GEMM_MIN_KCHUNK)), dma
 
 
 def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
@@ -517,7 +529,7 @@ class Lowering:
         wv2 = self.aligned16(self.contiguous(w2), w2) if w2 else None
         bv2 = self.contiguous(b2) if b2 else None
         nw = 2 if epi == "silu" else 1
-        bm, bn, ksplit = gemm_tiling(M, N, K, nw)
+        bm, bn, ksplit, dma = gemm_tiling(M, N, K, nw)
         bk = 64 if K % 64 == 0 else 32
         kchunk = K
         if ksplit > 1:
@@ -532,9 +544,11 @@ class Lowering:
                     N=N, K=K, flags=(1 if bias else 0) | (2 if bv2 else 0), ksplit=ksplit, kchunk=kchunk, nw=nw)
         ins = [x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t]
         params = {"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None, "weights": nw,
-                  "transpose_b": True, "nodes": nodes, "mfma": True, "tile": (bm, bn), "ksplit": ksplit, "bk": bk}
+                  "transpose_b": True, "nodes": nodes, "mfma": True, "tile": (bm, bn), "ksplit": ksplit, "bk": bk,
+                  "lds_direct": dma}
         self.emit(LaunchStep(
-            kind="gemm", kernel=f"k_gemm_{dt}_{epi}_m{bm}n{bn}" + ("_k64" if bk == 64 else ""), module="gemm",
+            kind="gemm", kernel=f"k_gemm_{dt}_{epi}_m{bm}n{bn}" + ("_k64d" if dma else "_k64" if bk == 64 else ""),
+            module="gemm",
             arg_struct="GemmArgs", args=args,
             grid=((N + bn - 1) // bn, (M + bm - 1) // bm, ksplit), inputs=ins,
             outputs=[out_name + ".kpart" if ksplit > 1 else out_name], params=params))

@@ -38,6 +38,12 @@ def test_prefill_mlp_is_norm_plus_two_mfma_gemms():
     assert kernels(p)[0] == "k_rmsnorm" and abs(p.steps[0].args["eps"] - 1e-6) < 1e-12
     assert [s.params["epilogue"] for s in main] == ["silu", "resid"]
     assert main[0].params["weights"] == 2 and main[0].args["w2"] is not None
+    # K % 64 == 0 and a tile grid below 1024: operands staged straight into LDS (the _k64d kernels)
+    assert all(s.params["lds_direct"] and s.kernel.endswith("_k64d") for s in main)
+    from irgen.qwen import QwenConfig
+    odd = [s for s in compile_subgraph(build_mlp_ir(512, QwenConfig(hidden=96, intermediate=160))).steps
+           if s.kind == "gemm" and not s.params.get("reduce")]
+    assert odd and not any(s.params["lds_direct"] for s in odd)   # K = 96 or 160: not a multiple of 64
     for s in main:   # every workgroup covers a whole K range; splits tile K exactly
         g = s.grid
         assert g[2] == s.args["ksplit"] and s.args["kchunk"] % 32 == 0

@@ -522,7 +522,7 @@ def test_prefill_two_layers_real_dims(backend):
     got, ex = run_hip(ir, x, w, backend)
     assert_all_npu(ex)
     kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
-    assert {"k_gemm_bf16_grp_m64n64_k64", "k_rope_cache", "k_attn_prefill"} <= set(kernels)
+    assert {"k_gemm_bf16_grp_m64n64_k64d", "k_rope_cache", "k_attn_prefill"} <= set(kernels)
     assert "k_copy" not in kernels and "k_softmax" not in kernels
     ref = run_cpu(ir, x, w)
     logits = ir["graph_outputs"][0]["name"]
