@@ -207,6 +207,23 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   int nw;                     // weights (1, or 2 for SiLU * mul); read by the reduce kernel
   int n1;                     // grouped: first column of the second and third groups
   int n2;
+  // conv epilogue (_conv kernels; flags 1 bias, 2 batch norm, 4 residual, 8 ReLU, as ConvArgs)
+  const void* bn_w;           // [N] batch norm weight, bias, running mean, running var
+  const void* bn_b;
+  const void* bn_mean;
+  const void* bn_var;
+  const void* zero;           // conv gather (_convg kernels): >= 16 zero bytes, read for padded taps
+  float eps;
+  int cH;                     // conv gather: x is NHWC [*, cH, cW, cCin], row m = output pixel (n, ho, wo),
+  int cW;                     //   k = (kh * cKW + kw) * cCin + ci, cCin % 64 == 0; w is [N, KH * KW * Cin] (OHWI)
+  int cCin;
+  int cHo;
+  int cWo;
+  int cKW;
+  int csh;
+  int csw;
+  int cph;
+  int cpw;
 };
 
 struct ConvArgs {             // implicit-GEMM conv2d (conv.hip), NCHW activations, OIHW weights, groups 1
@@ -229,13 +246,21 @@ struct ConvArgs {             // implicit-GEMM conv2d (conv.hip), NCHW activatio
   int kchunk;                 // multiple of the K step (32)
 };
 
-struct PoolArgs {             // NCHW max pooling (pool.hip)
+struct PoolArgs {             // max pooling (conv.hip): NCHW, or NHWC for the _nhwc kernel
   const void* x;
   void* out;
   long long planes;           // N * C
   int H, W, Ho, Wo, kh, kw, sh, sw, ph, pw;
   int dtype;
-  int pad;
+  int C;                      // channels-last kernels (_nhwc): C (multiple of 8); unused otherwise
+};
+
+struct MeanNHWCArgs {         // [n, hw, c] -> [n, c] mean over hw (conv.hip, global average pool of NHWC)
+  const void* x;
+  void* out;
+  long long n;
+  int hw;
+  int c;                      // multiple of 8, 16-byte aligned rows
 };
 
 struct BatchNormArgs {        // inference batch norm over NCHW (channel = dim 1), optional ReLU
@@ -431,7 +456,7 @@ struct AttnOutArgs {          // second attention pass: global softmax and p.V p
   int ntiles;
   int mask_dtype;
   int dtype;
-  int pad;
+  int C;                      // channels-last kernels (_nhwc): C (multiple of 8); unused otherwise
 };
 
 // host and device (the rotary sincos below is also built into a host test helper)

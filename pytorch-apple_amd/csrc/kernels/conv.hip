@@ -236,6 +236,32 @@ __device__ __forceinline__ void conv_body(const ConvArgs& a) {
   }
   __syncthreads();
   const float* s_bias = (const float*)&Bs[0][0][0];
+  if (a.flags & 16) {   // channels-last output [pixels, Cout] (Cout % 4 == 0): 4 channels per 8-byte store
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int m = (int)m_base + wr * 64 + i * 32 + fr;
+      if (m >= M32) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cl0 = wc * 64 + j * 32 + q * 8 + (lane >> 5) * 4;
+          if (n_base + cl0 >= a.Cout) continue;
+          const long long o = (long long)m * a.Cout + n_base + cl0;
+          uint16_t h[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v = cv_round<DT>(acc[i][j][q * 4 + r] + s_bias[cl0 + r]);
+            if (a.flags & 2) v = cv_round<DT>(v * s_al[cl0 + r] + s_be[cl0 + r]);
+            if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o + r]));
+            if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
+            h[r] = cv_h<DT>(v);
+          }
+          *(uint2*)((uint16_t*)a.out + o) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int m = (int)m_base + wr * 64 + i * 32 + fr;
@@ -290,7 +316,7 @@ __device__ __forceinline__ void conv_reduce_body(const ConvArgs& a) {
       float v = cv_round<DT>(vs[j] + bias);
       if (a.flags & 2) v = cv_round<DT>(v * al + be);
       const long long n = m / HoWo, p = m - n * HoWo;
-      const long long o = (n * a.Cout + co) * HoWo + p;
+      const long long o = (a.flags & 16) ? m * a.Cout + co : (n * a.Cout + co) * HoWo + p;
       if (a.flags & 4) v = cv_round<DT>(v + cv_f<DT>(((const uint16_t*)a.resid)[o]));
       if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
       ((uint16_t*)a.out)[o] = cv_h<DT>(v);
@@ -384,3 +410,93 @@ extern "C" __global__ void __launch_bounds__(256) k_batchnorm(const BatchNormArg
     ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(v) : f32_to_f16(v);
   }
 }
+
+// ---------------------------------------------------------------- channels-last pooling
+
+// max pooling of an NHWC image [planes = N, H, W, C] into [N, Ho, Wo, C]: one thread per output
+// pixel and 8 channels (16-byte loads and store); a 3 x 3 window issues its nine loads together
+// (clamped addresses, masked values). NaN in a window gives NaN, as the NCHW kernel.
+template <int DT>
+__device__ __forceinline__ void maxpool_nhwc_body(const PoolArgs& a) {
+  const int CG = a.C / 8;
+  const long long total = a.planes * a.Ho * a.Wo * CG;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+    const int cg = (int)(i % CG);
+    long long t = i / CG;
+    const int wo = (int)(t % a.Wo);
+    t /= a.Wo;
+    const int ho = (int)(t % a.Ho);
+    const long long n = t / a.Ho;
+    const uint16_t* x = (const uint16_t*)a.x + n * a.H * a.W * a.C + cg * 8;
+    float best[8];
+    bool nan[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) { best[c] = -INFINITY; nan[c] = false; }
+    auto take = [&](const uint4 v) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint16_t hb = (uint16_t)(w[c >> 1] >> ((c & 1) * 16));
+        const float f = cv_f<DT>(hb);
+        nan[c] |= f != f;
+        best[c] = fmaxf(best[c], f);
+      }
+    };
+    if (a.kh == 3 && a.kw == 3) {
+      uint4 v[9];
+      bool ok[9];
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp) {
+        const int hi = ho * a.sh - a.ph + tp / 3, wi = wo * a.sw - a.pw + tp % 3;
+        ok[tp] = (unsigned)hi < (unsigned)a.H && (unsigned)wi < (unsigned)a.W;
+        v[tp] = *(const uint4*)(x + (ok[tp] ? ((long long)hi * a.W + wi) * a.C : 0));
+      }
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp)
+        if (ok[tp]) take(v[tp]);
+    } else {
+      for (int kh = 0; kh < a.kh; ++kh)
+        for (int kw = 0; kw < a.kw; ++kw) {
+          const int hi = ho * a.sh - a.ph + kh, wi = wo * a.sw - a.pw + kw;
+          if ((unsigned)hi < (unsigned)a.H && (unsigned)wi < (unsigned)a.W)
+            take(*(const uint4*)(x + ((long long)hi * a.W + wi) * a.C));
+        }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float f0 = nan[2 * c] ? NAN : best[2 * c], f1 = nan[2 * c + 1] ? NAN : best[2 * c + 1];
+      o[c] = cv_h<DT>(f0) | ((uint32_t)cv_h<DT>(f1) << 16);
+    }
+    *(uint4*)((uint16_t*)a.out + ((n * a.Ho + ho) * a.Wo + wo) * a.C + cg * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+extern "C" __global__ void __launch_bounds__(256) k_maxpool2d_nhwc_f16(const PoolArgs a) { maxpool_nhwc_body<HS_F16>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_maxpool2d_nhwc_bf16(const PoolArgs a) { maxpool_nhwc_body<HS_BF16>(a); }
+
+// mean over the pixels of an NHWC image [n, hw, c] into [n, c] (a global average pool): one
+// thread per image and 8 channels, 16-byte loads, fp32 sum divided by hw, rounded once
+template <int DT>
+__device__ __forceinline__ void mean_nhwc_body(const MeanNHWCArgs& a) {
+  const int CG = a.c / 8;
+  const long long total = a.n * CG;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long long)gridDim.x * 256) {
+    const long long img = i / CG;
+    const int cg = (int)(i - img * CG);
+    const uint16_t* x = (const uint16_t*)a.x + img * a.hw * a.c + cg * 8;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < a.hw; ++p) {
+      const uint4 v = *(const uint4*)(x + (long long)p * a.c);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c) s[c] += cv_f<DT>((uint16_t)(w[c >> 1] >> ((c & 1) * 16)));
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      o[c] = cv_h<DT>(s[2 * c] / (float)a.hw) | ((uint32_t)cv_h<DT>(s[2 * c + 1] / (float)a.hw) << 16);
+    *(uint4*)((uint16_t*)a.out + img * a.c + cg * 8) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+extern "C" __global__ void __launch_bounds__(256) k_mean_nhwc_f16(const MeanNHWCArgs a) { mean_nhwc_body<HS_F16>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_mean_nhwc_bf16(const MeanNHWCArgs a) { mean_nhwc_body<HS_BF16>(a); }

@@ -26,7 +26,7 @@ typedef __attribute__((ext_vector_type(8))) __bf16 gm_bf16x8;
 typedef __attribute__((ext_vector_type(8))) _Float16 gm_f16x8;
 typedef __attribute__((ext_vector_type(16))) float gm_f32x16;
 
-enum { GE_BIAS = 0, GE_RESID = 1, GE_SILU = 2 };
+enum { GE_BIAS = 0, GE_RESID = 1, GE_SILU = 2, GE_CONV = 3 };
 #define GM_BK 32      // default K step
 
 template <int DT>
@@ -89,17 +89,38 @@ __device__ __forceinline__ void gm_vmcnt_after(int after) {
   }
 }
 
+// conv epilogue (conv.hip's rounding points): after v = round(acc + bias),
+//   batch norm: v = round(v * al + be), al = w / sqrt(var + eps), be = bias - mean * al;
+//   residual: v = round(v + r);  ReLU: v = max(v, 0) (NaN kept)
+template <int DT>
+__device__ __forceinline__ void gm_bn_factors(const GemmArgs& a, int n, float& al, float& be) {
+  const float g = gm_ld<DT>(a.bn_w, n), bb = gm_ld<DT>(a.bn_b, n);
+  const float mu = gm_ld<DT>(a.bn_mean, n), var = gm_ld<DT>(a.bn_var, n);
+  al = g / sqrtf(var + a.eps);
+  be = bb - mu * al;
+}
+template <int DT>
+__device__ __forceinline__ float gm_conv_tail(const GemmArgs& a, float v, float al, float be, uint16_t r) {
+  if (a.flags & 2) v = gm_round<DT>(v * al + be);
+  if (a.flags & 4) v = gm_round<DT>(v + (DT == HS_BF16 ? bf16_to_f32(r) : f16_to_f32(r)));
+  if (a.flags & 8) v = v != v ? v : fmaxf(v, 0.f);
+  return v;
+}
+
 // STAGES 0: LDS double buffer filled through registers (the loads of step s + 1 are in flight
 // while step s is multiplied). STAGES >= 3 (BK 64, not KN): the operands go from global memory
 // straight into LDS (gfx950 global_load_lds_dwordx4), STAGES buffers deep, so the loads of
 // steps s + 1 .. s + STAGES - 1 are in flight while step s is multiplied and no registers hold
 // them. Those rows are unpadded 128-byte rows; 16-byte chunk c of row r sits in slot
 // c ^ gm_swz(r), so the fragment reads of 8 consecutive rows hit 8 different bank groups.
+// CV (direct-to-LDS only): A is gathered from an NHWC image, row m = output pixel, k = (kh, kw, ci)
+// with a whole 64-channel block per K step; padded taps read a.zero (see GemmArgs).
 template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false,
-          int STAGES = 0>
+          int STAGES = 0, bool CV = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr bool DMA = STAGES >= 3;
   static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
+  static_assert(!CV || (DMA && NW == 1 && !GRP), "conv gather: direct-to-LDS, one weight");
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
   constexpr int CPR = BK / 8;             // 16-byte chunks per staged row
   constexpr int BNT = BN * NW;            // weight rows staged per step (BN columns per weight)
@@ -276,11 +297,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     const int lr = lane >> 3, ls = lane & 7;
     const char* asrc[NA];
     const char* bsrc[NB];
+    int ghi[CV ? NA : 1], gwi[CV ? NA : 1];   // CV: top-left input tap of the row's pixel
+    long long gpb[CV ? NA : 1];               // CV: element offset of (n, ghi, gwi, lane's chunk)
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       const int row = (wave * NA + q) * 8 + lr;
       const long long m = min(m_base + row, a.M - 1);
       asrc[q] = (const char*)(X + m * a.ldx) + ((ls ^ gm_swz(row)) * 16);
+      if constexpr (CV) {
+        const int HoWo = a.cHo * a.cWo, mi = (int)m;
+        const int n = mi / HoWo, p = mi - n * HoWo, ho = p / a.cWo, wo = p - ho * a.cWo;
+        ghi[q] = ho * a.csh - a.cph;
+        gwi[q] = wo * a.csw - a.cpw;
+        gpb[q] = (((long long)n * a.cH + ghi[q]) * a.cW + gwi[q]) * a.cCin + (ls ^ gm_swz(row)) * 8;
+      }
     }
 #pragma unroll
     for (int q = 0; q < NB; ++q) {
@@ -297,9 +327,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     auto issue = [&](int st) {   // stage st of the K loop into LDS buffer st % STAGES
       const unsigned base = lds0 + (unsigned)((st % STAGES) * SSTAGE) * 2u;
       const long long kb = (long long)st * BK * 2;
+      if constexpr (CV) {   // one tap and one 64-channel block per step (uniform)
+        const int k = kbeg + st * BK;
+        const int tap = k / a.cCin, c0 = k - tap * a.cCin;
+        const int kh = tap / a.cKW, kw = tap - kh * a.cKW;
+        const long long toff = ((long long)kh * a.cW + kw) * a.cCin + c0;
 #pragma unroll
-      for (int q = 0; q < NA; ++q)
-        gm_dma16(asrc[q] + kb, __builtin_amdgcn_readfirstlane(base + (unsigned)((wave * NA + q) * 8 * SROW * 2)));
+        for (int q = 0; q < NA; ++q) {
+          const int hi = ghi[q] + kh, wi = gwi[q] + kw;
+          const bool ok = (unsigned)hi < (unsigned)a.cH && (unsigned)wi < (unsigned)a.cW;
+          const char* src = ok ? (const char*)((const uint16_t*)a.x + gpb[q] + toff) : (const char*)a.zero;
+          gm_dma16(src, __builtin_amdgcn_readfirstlane(base + (unsigned)((wave * NA + q) * 8 * SROW * 2)));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < NA; ++q)
+          gm_dma16(asrc[q] + kb, __builtin_amdgcn_readfirstlane(base + (unsigned)((wave * NA + q) * 8 * SROW * 2)));
+      }
 #pragma unroll
       for (int q = 0; q < NB; ++q)
         gm_dma16(bsrc[q] + kb, __builtin_amdgcn_readfirstlane(base + (unsigned)((BM + (wave * NB + q) * 8) * SROW * 2)));
@@ -369,6 +413,20 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     if (n >= a.N) continue;
     const float b0 = (a.flags & 1) ? gm_ld<DT>(g_bias, n - g_lo) : 0.f;
     const float b1 = (EPI == GE_SILU && (a.flags & 2)) ? gm_ld<DT>(a.bias2, n) : 0.f;
+    float al = 1.f, be = 0.f;   // conv: inference batch norm v * al + be (the conv.hip factors)
+    if (EPI == GE_CONV && (a.flags & 2)) gm_bn_factors<DT>(a, n, al, be);
+    // the column's residual operands are loaded before any store: as far as the compiler knows a
+    // store may alias them, so loads interleaved with the stores would each wait a memory latency
+    uint16_t rr[(EPI == GE_RESID || EPI == GE_CONV) ? TI : 1][16] = {};
+    if (EPI == GE_RESID || (EPI == GE_CONV && (a.flags & 4))) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const long long m = min(m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), a.M - 1);
+          rr[i][e] = ((const uint16_t*)a.resid)[m * a.ldr + n];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
 #pragma unroll
@@ -376,7 +434,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (m >= a.M) continue;
         float v = gm_round<DT>(acc[0][i][j][e] + b0);
-        if constexpr (EPI == GE_RESID) v = gm_round<DT>(gm_ld<DT>(a.resid, m * a.ldr + n) + v);
+        if constexpr (EPI == GE_RESID)
+          v = gm_round<DT>((DT == HS_BF16 ? bf16_to_f32(rr[i][e]) : f16_to_f32(rr[i][e])) + v);
+        if constexpr (EPI == GE_CONV) v = gm_conv_tail<DT>(a, v, al, be, rr[i][e]);
         if constexpr (EPI == GE_SILU) {
           const float up = gm_round<DT>(acc[NW - 1][i][j][e] + b1);
           const float sg = gm_round<DT>(v / (1.f + expf(-v)));
@@ -409,6 +469,11 @@ __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
     }
     float v = gm_round<DT>(g + ((a.flags & 1) ? gm_ld<DT>(a.bias, n) : 0.f));
     if constexpr (EPI == GE_RESID) v = gm_round<DT>(gm_ld<DT>(a.resid, m * a.ldr + n) + v);
+    if constexpr (EPI == GE_CONV) {
+      float al = 1.f, be = 0.f;
+      if (a.flags & 2) gm_bn_factors<DT>(a, n, al, be);
+      v = gm_conv_tail<DT>(a, v, al, be, (a.flags & 4) ? ((const uint16_t*)a.resid)[m * a.ldr + n] : (uint16_t)0);
+    }
     if constexpr (EPI == GE_SILU) {
       const float u = gm_round<DT>(up + ((a.flags & 2) ? gm_ld<DT>(a.bias2, n) : 0.f));
       const float sg = gm_round<DT>(v / (1.f + expf(-v)));
@@ -464,6 +529,29 @@ GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
   extern "C" __global__ void GM_ATTRS NAME##_k64d(const GemmArgs a) {                                              \
     gemm_body<DT, GE_BIAS, 1, BM, BN, false, 64, true, ST>(a);                                                     \
   }
+// conv2d on channels-last activations (conv epilogue): _conv takes x as the [pixels, Cin] rows of
+// an NHWC image (1 x 1, stride 1, no padding); _convg gathers the taps of any kernel / stride /
+// padding (Cin % 64 == 0) with direct-to-LDS staging
+#define GEMM_CONV(DTN, DT, BM, BN, ST)                                                                           \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64(const GemmArgs a) {                 \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64>(a);                                                             \
+  }                                                                                                             \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64d(const GemmArgs a) {                \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST>(a);                                                  \
+  }                                                                                                             \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d(const GemmArgs a) {               \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST, true>(a);                                            \
+  }
+GEMM_CONV(f16, HS_F16, 128, 128, 4)
+GEMM_CONV(f16, HS_F16, 128, 64, 3)
+GEMM_CONV(f16, HS_F16, 64, 128, 3)
+GEMM_CONV(f16, HS_F16, 64, 64, 4)
+GEMM_CONV(bf16, HS_BF16, 128, 128, 4)
+GEMM_CONV(bf16, HS_BF16, 128, 64, 3)
+GEMM_CONV(bf16, HS_BF16, 64, 128, 3)
+GEMM_CONV(bf16, HS_BF16, 64, 64, 4)
+GEMM_REDUCE(k_gemm_reduce_f16_conv, HS_F16, GE_CONV)
+GEMM_REDUCE(k_gemm_reduce_bf16_conv, HS_BF16, GE_CONV)
 GEMM_KERNEL_GRP(k_gemm_bf16_grp_m64n64, HS_BF16, 64, 64, 4)
 GEMM_KERNEL_GRP(k_gemm_bf16_grp_m128n128, HS_BF16, 128, 128, 4)
 GEMM_KERNEL_GRP(k_gemm_f16_grp_m64n64, HS_F16, 64, 64, 4)

@@ -251,6 +251,7 @@ size_t hs_argsize(const char* s) {
   HS_SZ(GemmArgs)
   HS_SZ(ConvArgs)
   HS_SZ(PoolArgs)
+  HS_SZ(MeanNHWCArgs)
   HS_SZ(BatchNormArgs)
   HS_SZ(DecodeAttnArgs)
   HS_SZ(FusedArgs)

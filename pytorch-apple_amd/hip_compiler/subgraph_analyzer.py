@@ -78,6 +78,30 @@ def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, boo
     return 64, 64, max(1, min((384 + t - 1) // t, K // GEMM_MIN_KCHUNK)), dma
 
 
+def _is_nhwc(v: TView) -> bool:
+    """A 4-d [N, C, H, W] view whose memory is channels-last ([N, H, W, C] contiguous)."""
+    if len(v.shape) != 4:
+        return False
+    _, C, H, W = v.shape
+    return tuple(v.strides) == (H * W * C, 1, W * C, C) and C > 1
+
+
+def conv_gemm_tiling(M: int, N: int, K: int) -> tuple[int, int, int]:
+    """(BM, BN, split-K) for a conv as a GEMM over M pixels, N output channels, K = KH*KW*Cin:
+    the largest tile no wider than the channels that still gives >= 256 workgroups; smaller
+    grids take 64 x 64 tiles and, for K >= 1024, split K toward ~384 workgroups (fp32
+    partials, then the reduce applies the epilogue)."""
+    ntiles = lambda bm, bn: ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
+    cands = [(bm, bn) for bm, bn in ((128, 128), (128, 64), (64, 128), (64, 64)) if bn <= max(N, 64)]
+    for bm, bn in cands:
+        if ntiles(bm, bn) >= GEMM_TARGET_WGS:
+            return bm, bn, 1
+    t = ntiles(64, 64)
+    if K >= 1024:
+        return 64, 64, max(1, min(8, (384 + t - 1) // t, K // GEMM_MIN_KCHUNK))
+    return 64, 64, 1
+
+
 def grid1d(n: int, block: int = 256, cap: int = 65536) -> tuple[int, int, int]:
     return (max(1, min(cap, (int(n) + block - 1) // block)), 1, 1)
 
@@ -142,6 +166,9 @@ class Lowering:
         if fold_attention is None:
             fold_attention = os.environ.get("HIPRT_FOLD_ATTN", "1") == "1"
         self.fold_attn_combine = fold_attention
+        # convolutions on channels-last activations through the MFMA GEMM (HIPRT_CONV_NHWC=0: NCHW kernels only)
+        self.conv_nhwc = os.environ.get("HIPRT_CONV_NHWC", "1") == "1"
+        self._conv_zero: Ref | None = None
         self.steps: list[LaunchStep] = []
         self.storages: dict[str, Storage] = {}
         self.views: dict[str, TView] = {}
@@ -808,7 +835,16 @@ class Lowering:
 
     def emit_conv(self, conv: OpNode, out_name: str, *, bn: OpNode | None = None, resid: str | None = None,
                   relu: bool = False, nodes: list[str] | None = None) -> None:
-        """conv2d (+ batch norm) (+ residual add) (+ ReLU) as one implicit-GEMM launch (conv.hip)."""
+        """conv2d (+ batch norm) (+ residual add) (+ ReLU) as one implicit-GEMM launch.
+
+        Channels-last (NHWC) activations with Cin % 64 == 0 go to the MFMA GEMM (gemm.hip, conv
+        epilogue): 16-byte channel loads and direct-to-LDS staging instead of 2-byte gathers.
+        Otherwise conv.hip's NCHW kernel runs (e.g. the 3-channel stem), writing its output
+        channels-last when the channels suit the GEMM path downstream."""
+        xv = self.view(conv.inputs[0].name)
+        if self.conv_nhwc and _is_nhwc(xv) and xv.shape[1] % 64 == 0 and xv.dtype in ("float16", "bfloat16") \
+                and (xv.offset * 2) % 16 == 0:
+            return self.emit_conv_nhwc(conv, out_name, xv, bn=bn, resid=resid, relu=relu, nodes=nodes)
         x = self.contiguous(conv.inputs[0].name)
         w = self.contiguous(conv.inputs[1].name)
         has_bias = len(conv.inputs) > 2
@@ -822,17 +858,27 @@ class Lowering:
         pd = [pd, pd] if isinstance(pd, int) else list(pd)
         K = Cin * KH * KW
         dt = x.dtype
-        o = self.new_storage(out_name, [N, Cout, Ho, Wo], dt)
         bnv = [self.contiguous(t.name) for t in bn.inputs[1:5]] if bn is not None else [None] * 4
-        rv = self.contiguous(resid) if resid else None
-        flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
+        M = N * Ho * Wo
+        tiles = ((Cout + 127) // 128) * ((M + 127) // 128)
+        # channels-last output (flag 16) when the next convolutions can take the GEMM path
+        nhwc_out = (self.conv_nhwc and Cout % 64 == 0 and dt in ("float16", "bfloat16")
+                    and not (tiles < 256 and K >= 1024) and (resid is None or _is_nhwc(self.view(resid))))
+        if nhwc_out:
+            ob = self.new_storage(out_name, [N, Ho, Wo, Cout], dt)
+            o = ob.with_(shape=(N, Cout, Ho, Wo), strides=(Ho * Wo * Cout, 1, Wo * Cout, Cout))
+            rv = self.view(resid) if resid else None
+        else:
+            o = ob = self.new_storage(out_name, [N, Cout, Ho, Wo], dt)
+            rv = self.contiguous(resid) if resid else None
+        flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0) \
+            | (16 if nhwc_out else 0)
         vec = K % 8 == 0 and (w.offset * 2) % 16 == 0
         kname = f"k_conv_{'bf16' if dt == 'bfloat16' else 'f16'}" + ("" if vec else "_g")
         if vec and KH == KW == 1 and pd == [0, 0] and K % 32 == 0:
             kname += "_1x1"
         elif vec and KH == KW == 3:
             kname += "_3x3"
-        M = N * Ho * Wo
         if M + 256 >= 2 ** 31 or x.numel * 2 >= 2 ** 32:
             raise NotImplementedError("conv2d with 2^31 or more input elements or output pixels")
         ins = [conv.inputs[0].name, conv.inputs[1].name] + ([conv.inputs[2].name] if has_bias else []) + \
@@ -842,7 +888,6 @@ class Lowering:
         # 3x3 512 -> 512 on 7 x 7 (52 tiles, K = 4608) 257 -> 65 us, 1x1 2048 -> 512 73 -> 33 us,
         # 3x3 128 -> 128 on 28 x 28 (196 tiles, K = 1152) 74 -> 67 us; at K = 512 the reduce pass
         # costs more than the split gains (1x1 512 -> 128 on 28 x 28: 26 -> 29 us), hence K >= 1024
-        tiles = ((Cout + 127) // 128) * ((M + 127) // 128)
         ksplit, kchunk = 1, K
         if tiles < 256 and K >= 1024 and M % 4 == 0:   # the reduce reads 4 pixels per load
             ksplit = max(1, min(8, (384 + tiles - 1) // tiles, K // 256))
@@ -854,13 +899,13 @@ class Lowering:
                     bn_b=self.ref(bnv[1]) if bn is not None else None,
                     bn_mean=self.ref(bnv[2]) if bn is not None else None,
                     bn_var=self.ref(bnv[3]) if bn is not None else None,
-                    resid=self.ref(rv) if rv is not None else None, out=self.ref(o), part=part, M=M, N=N, Cin=Cin,
+                    resid=self.ref(rv) if rv is not None else None, out=self.ref(ob), part=part, M=M, N=N, Cin=Cin,
                     H=H, W=W, Cout=Cout, Ho=Ho, Wo=Wo, KH=KH, KW=KW, sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], K=K,
                     eps=float(bn.attrs.get("eps", 1e-5)) if bn is not None else 0.0, flags=flags, ksplit=ksplit,
                     kchunk=kchunk)
         params = {"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
                   "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
-                  "ksplit": ksplit, "nodes": nodes or [conv.name]}
+                  "ksplit": ksplit, "nhwc_out": nhwc_out, "nodes": nodes or [conv.name]}
         self.emit(LaunchStep(
             kind="conv", kernel=kname, module="conv", arg_struct="ConvArgs", args=args,
             grid=((Cout + 127) // 128, (M + 127) // 128, ksplit), inputs=ins,
@@ -870,6 +915,88 @@ class Lowering:
                 kind="conv", kernel=f"k_conv_reduce_{'bf16' if dt == 'bfloat16' else 'f16'}", module="conv",
                 arg_struct="ConvArgs", args=dict(args), grid=grid1d(Cout * M // 4),
                 inputs=[out_name + ".kpart"] + ins[2:], outputs=[out_name], params=dict(params, reduce=True)))
+        self.views[out_name] = o
+
+    def emit_conv_nhwc(self, conv: OpNode, out_name: str, xv: TView, *, bn: OpNode | None, resid: str | None,
+                       relu: bool, nodes: list[str] | None) -> None:
+        """conv2d on an NHWC image as an MFMA GEMM over [pixels, KH*KW*Cin] x [Cout, KH*KW*Cin]^T with
+        the conv epilogue; writes NHWC. 1 x 1 / stride 1 / no padding reads the image rows as they
+        are (_conv); other shapes gather one tap and 64 channels per K step (_convg, padded taps
+        read a zeroed buffer). Weights [Cout, Cin, KH, KW] are read as [Cout, KH, KW, Cin]: a
+        strided copy for KH*KW > 1 at the start of each run (bound weights can change between runs)."""
+        wname = conv.inputs[1].name
+        wv = self.view(wname)
+        has_bias = len(conv.inputs) > 2
+        N, Cin, H, W = xv.shape
+        Cout, _, KH, KW = wv.shape
+        out_t = conv.outputs[0]
+        Ho, Wo = out_t.shape[2], out_t.shape[3]
+        st = conv.attrs.get("stride", [1, 1])
+        pd = conv.attrs.get("padding", [0, 0])
+        st = [st, st] if isinstance(st, int) else list(st)
+        pd = [pd, pd] if isinstance(pd, int) else list(pd)
+        dt = xv.dtype
+        K = KH * KW * Cin
+        M = N * Ho * Wo
+        if M + 256 >= 2 ** 31 or xv.numel >= 2 ** 31:
+            raise NotImplementedError("conv2d with 2^31 or more input elements or output pixels")
+        if KH * KW > 1:
+            key = wname + ".ohwi"
+            w = self.views.get(key)
+            if w is None:
+                w = self.new_storage(key, [Cout, KH, KW, Cin], dt)
+                self.emit_copy(V.permute(wv, [0, 2, 3, 1]), w, [wname], [key])
+                self.views[key] = w
+        else:
+            w = self.aligned16(self.contiguous(wname), wname)
+        plain = KH == KW == 1 and st == [1, 1] and pd == [0, 0]
+        ob = self.new_storage(out_name, [N, Ho, Wo, Cout], dt)
+        o = ob.with_(shape=(N, Cout, Ho, Wo), strides=(Ho * Wo * Cout, 1, Wo * Cout, Cout))
+        rv = None
+        if resid is not None:
+            rv = self.view(resid)
+            if not _is_nhwc(rv) or (rv.offset * 2) % 16:
+                rb = self.new_storage(resid + ".nhwc", [rv.shape[0], rv.shape[2], rv.shape[3], rv.shape[1]], dt)
+                rn = rb.with_(shape=rv.shape, strides=(rb.strides[0], 1, rb.strides[1], rb.strides[2]))
+                self.emit_copy(rv, rn, [resid], [resid + ".nhwc"])
+                rv = rb
+        bnv = [self.contiguous(t.name) for t in bn.inputs[1:5]] if bn is not None else [None] * 4
+        flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
+        bm, bn_, ksplit = conv_gemm_tiling(M, Cout, K)
+        dma = (not plain) or ((M + bm - 1) // bm) * ((Cout + bn_ - 1) // bn_) < GEMM_DMA_MAX_TILES
+        kchunk = K
+        if ksplit > 1:
+            kchunk = ((K // 64 + ksplit - 1) // ksplit) * 64
+            ksplit = (K + kchunk - 1) // kchunk
+        if self._conv_zero is None:
+            self._conv_zero = self.scratch("conv.zero", 256, persistent=True)
+        dts = "bf16" if dt == "bfloat16" else "f16"
+        kname = f"k_gemm_{dts}_{'conv' if plain else 'convg'}_m{bm}n{bn_}" + ("_k64d" if dma else "_k64")
+        part = self.scratch(out_name + ".kpart", ksplit * M * Cout * 4) if ksplit > 1 else None
+        args = dict(x=self.ref(xv), w=self.ref(w), w2=None, bias=self.ref(self.contiguous(conv.inputs[2].name))
+                    if has_bias else None, bias2=None, resid=self.ref(rv) if rv is not None else None,
+                    out=self.ref(ob), part=part, M=M, ldx=Cin, ldw=K, ldo=Cout, ldr=Cout, sx=0, sw=0, so=0, batch=1,
+                    bdiv=1, N=Cout, K=K, flags=flags, ksplit=ksplit, kchunk=kchunk, nw=1,
+                    bn_w=self.ref(bnv[0]) if bn is not None else None,
+                    bn_b=self.ref(bnv[1]) if bn is not None else None,
+                    bn_mean=self.ref(bnv[2]) if bn is not None else None,
+                    bn_var=self.ref(bnv[3]) if bn is not None else None,
+                    zero=self._conv_zero, eps=float(bn.attrs.get("eps", 1e-5)) if bn is not None else 0.0,
+                    cH=H, cW=W, cCin=Cin, cHo=Ho, cWo=Wo, cKW=KW, csh=st[0], csw=st[1], cph=pd[0], cpw=pd[1])
+        ins = [conv.inputs[0].name, wname] + ([conv.inputs[2].name] if has_bias else []) + \
+            ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
+        params = {"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
+                  "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
+                  "ksplit": ksplit, "nhwc": True, "tile": (bm, bn_), "lds_direct": dma, "nodes": nodes or [conv.name]}
+        self.emit(LaunchStep(
+            kind="conv", kernel=kname, module="gemm", arg_struct="GemmArgs", args=args,
+            grid=((Cout + bn_ - 1) // bn_, (M + bm - 1) // bm, ksplit), inputs=ins,
+            outputs=[out_name + ".kpart" if ksplit > 1 else out_name], params=params))
+        if ksplit > 1:
+            self.emit(LaunchStep(
+                kind="conv", kernel=f"k_gemm_reduce_{dts}_conv", module="gemm", arg_struct="GemmArgs",
+                args=dict(args), grid=grid1d(M * Cout), inputs=[out_name + ".kpart"] + ins[2:],
+                outputs=[out_name], params=dict(params, reduce=True)))
         self.views[out_name] = o
 
     def lower_conv2d(self, node: OpNode) -> None:
@@ -890,6 +1017,10 @@ class Lowering:
         self.views[out.name] = o
 
     def lower_max_pool2d(self, node: OpNode) -> None:
+        xv = self.view(node.inputs[0].name)
+        if _is_nhwc(xv) and xv.shape[1] % 8 == 0 and (xv.offset * 2) % 16 == 0 and \
+                xv.dtype in ("float16", "bfloat16"):
+            return self._max_pool2d_nhwc(node, xv)
         x = self.contiguous(node.inputs[0].name)
         out = node.outputs[0]
         ks = node.attrs.get("kernel_size", [2, 2])
@@ -904,14 +1035,46 @@ class Lowering:
         self.emit(LaunchStep(
             kind="reduction", kernel="k_maxpool2d", module="conv", arg_struct="PoolArgs",
             args=dict(x=self.ref(x), out=self.ref(o), planes=N * C, H=H, W=W, Ho=Ho, Wo=Wo, kh=ks[0], kw=ks[1],
-                      sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], dtype=DTYPE_CODE[x.dtype], pad=0),
+                      sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], dtype=DTYPE_CODE[x.dtype], C=0),
             grid=grid1d(N * C * Ho * Wo), inputs=[node.inputs[0].name], outputs=[out.name], params={}))
         self.views[out.name] = o
 
+    def _max_pool2d_nhwc(self, node: OpNode, xv: TView) -> None:
+        """Max pooling of a channels-last image into a channels-last result (8 channels per thread)."""
+        out = node.outputs[0]
+        ks = node.attrs.get("kernel_size", [2, 2])
+        ks = [ks, ks] if isinstance(ks, int) else list(ks)
+        st = node.attrs.get("stride", None) or ks
+        st = [st, st] if isinstance(st, int) else list(st)
+        pd = node.attrs.get("padding", [0, 0])
+        pd = [pd, pd] if isinstance(pd, int) else list(pd)
+        N, C, H, W = xv.shape
+        Ho, Wo = out.shape[2], out.shape[3]
+        ob = self.new_storage(out.name, [N, Ho, Wo, C], out.dtype)
+        self.emit(LaunchStep(
+            kind="reduction", kernel=f"k_maxpool2d_nhwc_{'bf16' if xv.dtype == 'bfloat16' else 'f16'}",
+            module="conv", arg_struct="PoolArgs",
+            args=dict(x=self.ref(xv), out=self.ref(ob), planes=N, H=H, W=W, Ho=Ho, Wo=Wo, kh=ks[0], kw=ks[1],
+                      sh=st[0], sw=st[1], ph=pd[0], pw=pd[1], dtype=DTYPE_CODE[xv.dtype], C=C),
+            grid=grid1d(N * Ho * Wo * C // 8), inputs=[node.inputs[0].name], outputs=[out.name],
+            params={"nhwc": True}))
+        self.views[out.name] = ob.with_(shape=(N, C, Ho, Wo), strides=(Ho * Wo * C, 1, Wo * C, C))
+
     def lower_adaptive_avg_pool2d(self, node: OpNode) -> None:
         """Global average pooling (output 1 x 1): the mean over H*W of each (n, c) plane."""
-        x = self.contiguous(node.inputs[0].name)
+        xv = self.view(node.inputs[0].name)
         out = node.outputs[0]
+        if _is_nhwc(xv) and xv.shape[1] % 8 == 0 and (xv.offset * 2) % 16 == 0 and \
+                xv.dtype in ("float16", "bfloat16") and out.dtype == xv.dtype:
+            N, C, H, W = xv.shape
+            o = self.new_storage(out.name, out.shape, out.dtype)   # [N, C, 1, 1]: the same bytes in either layout
+            self.emit(LaunchStep(
+                kind="reduction", kernel=f"k_mean_nhwc_{'bf16' if xv.dtype == 'bfloat16' else 'f16'}", module="conv",
+                arg_struct="MeanNHWCArgs", args=dict(x=self.ref(xv), out=self.ref(o), n=N, hw=H * W, c=C),
+                grid=grid1d(N * C // 8), inputs=[node.inputs[0].name], outputs=[out.name], params={"nhwc": True}))
+            self.views[out.name] = o
+            return
+        x = self.contiguous(node.inputs[0].name)
         N, C, H, W = x.shape
         o = self.new_storage(out.name, out.shape, out.dtype)
         self.emit(mean_rows_step(self.ref(x), self.ref(o), N * C, H * W, x.dtype, out.dtype, [node.inputs[0].name],

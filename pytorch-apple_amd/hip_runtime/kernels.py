@@ -57,13 +57,16 @@ _struct("LinearArgs", [("x", P), ("w", P), ("bias", P), ("out", P), ("resid", P)
 _struct("GemmArgs", [("x", P), ("w", P), ("w2", P), ("bias", P), ("bias2", P), ("resid", P), ("out", P),
                      ("part", P), ("w3", P), ("bias3", P), ("M", LL), ("ldx", LL), ("ldw", LL), ("ldo", LL),
                      ("ldr", LL), ("sx", LL), ("sw", LL), ("so", LL), ("batch", I), ("bdiv", I), ("N", I), ("K", I),
-                     ("flags", I), ("ksplit", I), ("kchunk", I), ("nw", I), ("n1", I), ("n2", I)])
+                     ("flags", I), ("ksplit", I), ("kchunk", I), ("nw", I), ("n1", I), ("n2", I), ("bn_w", P),
+                     ("bn_b", P), ("bn_mean", P), ("bn_var", P), ("zero", P), ("eps", F), ("cH", I), ("cW", I),
+                     ("cCin", I), ("cHo", I), ("cWo", I), ("cKW", I), ("csh", I), ("csw", I), ("cph", I), ("cpw", I)])
 _struct("ConvArgs", [("x", P), ("w", P), ("bias", P), ("bn_w", P), ("bn_b", P), ("bn_mean", P), ("bn_var", P),
                      ("resid", P), ("out", P), ("part", P), ("M", LL), ("N", I), ("Cin", I), ("H", I), ("W", I),
                      ("Cout", I), ("Ho", I), ("Wo", I), ("KH", I), ("KW", I), ("sh", I), ("sw", I), ("ph", I),
                      ("pw", I), ("K", I), ("eps", F), ("flags", I), ("ksplit", I), ("kchunk", I)])
 _struct("PoolArgs", [("x", P), ("out", P), ("planes", LL), ("H", I), ("W", I), ("Ho", I), ("Wo", I), ("kh", I),
-                     ("kw", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I), ("dtype", I), ("pad", I)])
+                     ("kw", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I), ("dtype", I), ("C", I)])
+_struct("MeanNHWCArgs", [("x", P), ("out", P), ("n", LL), ("hw", I), ("c", I)])
 _struct("BatchNormArgs", [("x", P), ("w", P), ("b", P), ("mean", P), ("var", P), ("out", P), ("n", LL),
                           ("hw", LL), ("C", I), ("eps", F), ("dtype", I), ("relu", I)])
 _struct("RopeCacheArgs", [("y", P), ("inv_freq", P), ("pos_ids", P), ("cache_pos", P), ("q_out", P), ("k_dst", P),

@@ -208,9 +208,26 @@ def test_resnet50_compiles_to_fused_convs():
     p = compile_subgraph(ir)
     convs = [s for s in p.steps if s.kind == "conv" and not s.params.get("reduce")]
     reduces = [s for s in p.steps if s.kind == "conv" and s.params.get("reduce")]
-    # every BN / add / ReLU folded into a conv (or into the split-K reduce that finishes it)
-    assert len(convs) == 53 and len(p.steps) <= 57 + len(reduces)
-    assert all(s.kernel.startswith("k_conv_reduce_") for s in reduces)
+    # every BN / add / ReLU folded into a conv (or into the split-K reduce that finishes it); the 16
+    # convs with a kernel wider than 1 x 1 read their weights through a per-run OHWI copy
+    copies = [s for s in p.steps if s.kernel == "k_copy"]
+    assert len(convs) == 53 and len(copies) == 16 and len(p.steps) <= 57 + len(reduces) + len(copies)
+    assert all(s.kernel.startswith(("k_conv_reduce_", "k_gemm_reduce_f16_conv")) for s in reduces)
     assert len(reduces) == sum(1 for s in convs if s.params["ksplit"] > 1)
     assert sum(1 for s in convs if s.args["flags"] & 4) == 16 and all(s.args["flags"] & 2 for s in convs)
     assert convs[0].kernel.endswith("_g") and convs[0].args["K"] == 147   # 3-channel stem: gathered weights
+    # channels-last from the stem on: the stem writes NHWC (flag 16), the other 52 convs are MFMA GEMMs
+    # over NHWC (1 x 1 stride 1: the image rows as they are; else tap gathers), pools read NHWC
+    assert convs[0].args["flags"] & 16 and all(s.params.get("nhwc") for s in convs[1:])
+    assert all(s.kernel.startswith(("k_gemm_f16_conv_", "k_gemm_f16_convg_")) for s in convs[1:])
+    assert sum(1 for s in convs[1:] if "_convg_" in s.kernel) == 16 + 3   # 3 x 3 and the stride-2 1 x 1
+    ks = [s.kernel for s in p.steps]
+    assert "k_maxpool2d_nhwc_f16" in ks and "k_mean_nhwc_f16" in ks
+    # HIPRT_CONV_NHWC=0 keeps every conv on the NCHW kernels
+    import os
+    os.environ["HIPRT_CONV_NHWC"] = "0"
+    try:
+        q = compile_subgraph(ir)
+    finally:
+        del os.environ["HIPRT_CONV_NHWC"]
+    assert all(s.kernel.startswith("k_conv_") for s in q.steps if s.kind == "conv")

@@ -699,10 +699,14 @@ def test_conv_bn_act_vs_fp32_conv(backend, N, Cin, H, W, Cout, k, stride, pad, a
         ins["r"] = torch.randn(yshape, generator=g).half()
     got, ex = run_hip(ir, host(ins), host(w), backend)
     (prog,) = ex.npu_programs.values()
-    kernels = [s.kernel for s in prog.steps]
-    assert [s.kind for s in prog.steps] == ["conv"] * len(kernels) and kernels[0].startswith("k_conv_")
+    # an NCHW graph input takes conv.hip's kernel; a channels-last result (64-multiple channels) is
+    # copied to the NCHW graph output at the end
+    kernels = [s.kernel for s in prog.steps if s.kernel != "k_copy"]
+    assert [s.kind for s in prog.steps if s.kernel != "k_copy"] == ["conv"] * len(kernels)
+    assert kernels[0].startswith("k_conv_")
     split = prog.steps[0].params["ksplit"] > 1   # split K: the reduce kernel applies the epilogue
     assert kernels[1:] == (["k_conv_reduce_f16"] if split else [])
+    assert bool(prog.steps[0].args["flags"] & 16) == (Cout % 64 == 0 and not add and not split)
     if Cin >= 128 and k == 3 or Cin >= 1024:
         assert split
     (name,) = got
@@ -714,6 +718,72 @@ def test_conv_bn_act_vs_fp32_conv(backend, N, Cin, H, W, Cout, k, stride, pad, a
     if add:
         y = (y + ins["r"].float()).half().float()
     close(got[name], torch.relu(y).numpy())
+
+
+def _conv_chain_ir(N, Cin, H, W, C1, C2, k, stride, pad, add, dtype="float16"):
+    """x -> 1x1 conv (C1) + BN + ReLU -> y1 (written channels-last) -> k x k conv (C2) + BN (+ y1) + ReLU:
+    the second conv reads an NHWC image, i.e. the MFMA GEMM path of the convolutions."""
+    from irgen.builder import IRBuilder
+
+    b = IRBuilder("conv_chain")
+    x = b.input("x", [N, Cin, H, W], dtype)
+    y = x
+    for i, (co, ci, kk, st, pd) in enumerate(((C1, Cin, 1, 1, 0), (C2, C1, k, stride, pad))):
+        w = b.weight(f"w{i}", [co, ci, kk, kk], dtype)
+        z = b.op("aten.conv2d.default", [y, w], {"stride": [st, st], "padding": [pd, pd], "dilation": [1, 1],
+                                                 "groups": 1})
+        ps = [b.weight(f"{n}{i}", [co], dtype) for n in ("g", "beta", "mu", "var")]
+        z = b.op("aten.batch_norm.default", [z] + ps, {"training": False, "momentum": 0.1, "eps": 1e-5,
+                                                       "cudnn_enabled": True})
+        if i == 1 and add:
+            z = b.op("aten.add.Tensor", [z, y])
+        y = b.op("aten.relu.default", [z])
+    b.output(y)
+    return b.to_dict()
+
+
+@pytest.mark.parametrize("N,Cin,H,W,C1,C2,k,stride,pad,add,kernel", [
+    (2, 64, 14, 14, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m"),     # 1x1 on the image rows, direct-to-LDS
+    (2, 32, 15, 15, 64, 64, 3, 1, 1, True, "k_gemm_f16_convg_m"),      # 3x3 pad 1, NHWC residual
+    (2, 64, 15, 17, 128, 96, 3, 2, 1, False, "k_gemm_f16_convg_m"),    # 3x3 stride 2, odd sizes, 96 channels
+    (1, 64, 9, 9, 256, 128, 1, 2, 0, False, "k_gemm_f16_convg_m"),     # strided 1x1 (downsample)
+    (2, 64, 8, 8, 1024, 256, 1, 1, 0, False, "k_gemm_f16_conv_m"),     # K = 1024, 32 tiles: split K + reduce
+    (16, 64, 64, 64, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m128n128_k64"),   # 1,024 tiles: register staging
+])
+def test_conv_chain_nhwc_gemm_vs_fp32(backend, N, Cin, H, W, C1, C2, k, stride, pad, add, kernel):
+    """A conv reading the channels-last output of the previous one runs as an MFMA GEMM (gemm.hip):
+    vs the same chain in float32 with every fp16 rounding point mirrored, and vs the CPU fallback."""
+    ir = _conv_chain_ir(N, Cin, H, W, C1, C2, k, stride, pad, add)
+    g = torch.Generator().manual_seed(C1 * 3 + C2 + k)
+    x = torch.randn(N, Cin, H, W, generator=g).half()
+    w = {}
+    for i, (co, ci, kk) in enumerate(((C1, Cin, 1), (C2, C1, k))):
+        w[f"w{i}"] = ((2.0 / (ci * kk * kk)) ** 0.5 * torch.randn(co, ci, kk, kk, generator=g)).half()
+        w[f"g{i}"] = (1 + 0.1 * torch.randn(co, generator=g)).half()
+        w[f"beta{i}"] = (0.1 * torch.randn(co, generator=g)).half()
+        w[f"mu{i}"] = (0.1 * torch.randn(co, generator=g)).half()
+        w[f"var{i}"] = (0.5 + torch.rand(co, generator=g)).half()
+    got, ex = run_hip(ir, host({"x": x}), host(w), backend)
+    (prog,) = ex.npu_programs.values()
+    convs = [s for s in prog.steps if s.kind == "conv" and not s.params.get("reduce")]
+    assert len(convs) == 2 and convs[0].args["flags"] & 16 and convs[1].kernel.startswith(kernel)
+    split = convs[1].params["ksplit"] > 1
+    assert convs[1].params["nhwc"] and split == any(s.params.get("reduce") for s in prog.steps)
+    assert split or C1 != 1024
+    (name,) = got
+    y = x.float()
+    for i, (st, pd) in enumerate(((1, 0), (stride, pad))):
+        z = torch.nn.functional.conv2d(y, w[f"w{i}"].float(), stride=st, padding=pd).half().float()
+        a = w[f"g{i}"].float() / torch.sqrt(w[f"var{i}"].float() + 1e-5)
+        z = (z * a[None, :, None, None] + (w[f"beta{i}"].float() - w[f"mu{i}"].float() * a)[None, :, None, None])
+        z = z.half().float()
+        if i == 1 and add:
+            z = (z + y).half().float()
+        y = torch.relu(z)
+    close(got[name], y.numpy())
+    if N * H * W <= 4096:   # the CPU fallback's fp16 conv is slow on big images
+        ref = run_cpu(ir, host({"x": x}), host(w))
+        close(got[name], ref[name])
 
 
 def test_resnet50_small_images_top5(backend):
