@@ -255,6 +255,17 @@ struct PoolArgs {             // max pooling (conv.hip): NCHW, or NHWC for the _
   int C;                      // channels-last kernels (_nhwc): C (multiple of 8); unused otherwise
 };
 
+#define HS_OHWI_MAX 24
+struct PermuteOHWIArgs {      // OIHW -> OHWI copies of up to HS_OHWI_MAX 2-byte weights in one launch (conv.hip)
+  const void* src[HS_OHWI_MAX];   // [Cout, Cin, KH, KW]
+  void* dst[HS_OHWI_MAX];         // [Cout, KH, KW, Cin]
+  long long start[HS_OHWI_MAX + 1];   // first element of tensor i in the joint index space; start[n] = total
+  int cin[HS_OHWI_MAX];           // multiple of 8
+  int kk[HS_OHWI_MAX];            // KH * KW
+  int n;
+  int pad;
+};
+
 struct MeanNHWCArgs {         // [n, hw, c] -> [n, c] mean over hw (conv.hip, global average pool of NHWC)
   const void* x;
   void* out;

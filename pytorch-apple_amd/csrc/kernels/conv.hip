@@ -500,3 +500,25 @@ __device__ __forceinline__ void mean_nhwc_body(const MeanNHWCArgs& a) {
 }
 extern "C" __global__ void __launch_bounds__(256) k_mean_nhwc_f16(const MeanNHWCArgs a) { mean_nhwc_body<HS_F16>(a); }
 extern "C" __global__ void __launch_bounds__(256) k_mean_nhwc_bf16(const MeanNHWCArgs a) { mean_nhwc_body<HS_BF16>(a); }
+
+// OIHW -> OHWI weight copies (the channels-last convs read k = (kh, kw, ci)): one thread per 8
+// destination elements (16-byte store), gathered from 8 source rows; tensor found by a scan of
+// the start offsets (at most HS_OHWI_MAX)
+extern "C" __global__ void __launch_bounds__(256) k_permute_ohwi(const PermuteOHWIArgs a) {
+  const long long total8 = a.start[a.n] / 8;
+  for (long long g = (long long)blockIdx.x * 256 + threadIdx.x; g < total8; g += (long long)gridDim.x * 256) {
+    const long long e0 = g * 8;
+    int i = 0;
+    while (i + 1 < a.n && a.start[i + 1] <= e0) ++i;
+    const long long e = e0 - a.start[i];
+    const int cin = a.cin[i], kk = a.kk[i];
+    const long long per = (long long)cin * kk;
+    const long long co = e / per;
+    const int rem = (int)(e - co * per), t = rem / cin, ci = rem - t * cin;
+    const uint16_t* src = (const uint16_t*)a.src[i] + (co * cin + ci) * kk + t;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = src[(2 * j) * kk] | ((uint32_t)src[(2 * j + 1) * kk] << 16);
+    *(uint4*)((uint16_t*)a.dst[i] + e) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}

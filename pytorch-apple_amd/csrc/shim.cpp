@@ -252,6 +252,7 @@ size_t hs_argsize(const char* s) {
   HS_SZ(ConvArgs)
   HS_SZ(PoolArgs)
   HS_SZ(MeanNHWCArgs)
+  HS_SZ(PermuteOHWIArgs)
   HS_SZ(BatchNormArgs)
   HS_SZ(DecodeAttnArgs)
   HS_SZ(FusedArgs)

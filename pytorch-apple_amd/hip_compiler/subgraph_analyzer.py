@@ -169,6 +169,7 @@ class Lowering:
         # convolutions on channels-last activations through the MFMA GEMM (HIPRT_CONV_NHWC=0: NCHW kernels only)
         self.conv_nhwc = os.environ.get("HIPRT_CONV_NHWC", "1") == "1"
         self._conv_zero: Ref | None = None
+        self._ohwi: list = []   # bound conv weights read as OHWI: (name, OIHW view, OHWI view, Cin, KH*KW)
         self.steps: list[LaunchStep] = []
         self.storages: dict[str, Storage] = {}
         self.views: dict[str, TView] = {}
@@ -945,7 +946,10 @@ class Lowering:
             w = self.views.get(key)
             if w is None:
                 w = self.new_storage(key, [Cout, KH, KW, Cin], dt)
-                self.emit_copy(V.permute(wv, [0, 2, 3, 1]), w, [wname], [key])
+                if self.is_constant(wv) and wv.is_contiguous() and (wv.offset * 2) % 16 == 0:
+                    self._ohwi.append((wname, wv, w, Cin, KH * KW))   # one launch at the program start
+                else:
+                    self.emit_copy(V.permute(wv, [0, 2, 3, 1]), w, [wname], [key])
                 self.views[key] = w
         else:
             w = self.aligned16(self.contiguous(wname), wname)
@@ -1272,6 +1276,36 @@ class Lowering:
             self.lower_node(node)
         for o in self.g.graph_outputs:
             self.view(o.name)
+        self.emit_weight_permutes()
+
+    def emit_weight_permutes(self) -> None:
+        """The OIHW -> OHWI copies of bound conv weights, in launches of up to OHWI_MAX tensors placed
+        first in the program (they depend on nothing else), re-run every execution like any step."""
+        from hip_runtime.kernels import OHWI_MAX
+
+        pre = []
+        for c in range(0, len(self._ohwi), OHWI_MAX):
+            chunk = self._ohwi[c:c + OHWI_MAX]
+            start, tot = [], 0
+            for _, wv, _, _, _ in chunk:
+                start.append(tot)
+                tot += wv.numel
+            pad = OHWI_MAX - len(chunk)
+            pre.append(LaunchStep(
+                kind="copy", kernel="k_permute_ohwi", module="conv", arg_struct="PermuteOHWIArgs",
+                args=dict(src=[self.ref(e[1]) for e in chunk] + [None] * pad,
+                          dst=[self.ref(e[2]) for e in chunk] + [None] * pad,
+                          start=start + [tot] * (pad + 1), cin=[e[3] for e in chunk] + [0] * pad,
+                          kk=[e[4] for e in chunk] + [0] * pad, n=len(chunk), pad=0),
+                grid=grid1d(tot // 8), inputs=[e[0] for e in chunk], outputs=[e[0] + ".ohwi" for e in chunk],
+                params={"tensors": len(chunk), "elements": tot}))
+        self.steps[:0] = pre
+        self._ohwi = []
+
+    def is_constant(self, v: TView) -> bool:
+        """True for a view of a bound weight: memory that no launch of the program writes."""
+        st = self.storages.get(v.storage)
+        return st is not None and st.kind == "weight" and v.storage not in self.mutated_inputs
 
     def lower_node(self, node: OpNode) -> None:
         op = node.op_type

@@ -66,6 +66,9 @@ _struct("ConvArgs", [("x", P), ("w", P), ("bias", P), ("bn_w", P), ("bn_b", P), 
                      ("pw", I), ("K", I), ("eps", F), ("flags", I), ("ksplit", I), ("kchunk", I)])
 _struct("PoolArgs", [("x", P), ("out", P), ("planes", LL), ("H", I), ("W", I), ("Ho", I), ("Wo", I), ("kh", I),
                      ("kw", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I), ("dtype", I), ("C", I)])
+OHWI_MAX = 24   # HS_OHWI_MAX
+_struct("PermuteOHWIArgs", [("src", P * OHWI_MAX), ("dst", P * OHWI_MAX), ("start", LL * (OHWI_MAX + 1)),
+                            ("cin", I * OHWI_MAX), ("kk", I * OHWI_MAX), ("n", I), ("pad", I)])
 _struct("MeanNHWCArgs", [("x", P), ("out", P), ("n", LL), ("hw", I), ("c", I)])
 _struct("BatchNormArgs", [("x", P), ("w", P), ("b", P), ("mean", P), ("var", P), ("out", P), ("n", LL),
                           ("hw", LL), ("C", I), ("eps", F), ("dtype", I), ("relu", I)])

@@ -209,9 +209,11 @@ def test_resnet50_compiles_to_fused_convs():
     convs = [s for s in p.steps if s.kind == "conv" and not s.params.get("reduce")]
     reduces = [s for s in p.steps if s.kind == "conv" and s.params.get("reduce")]
     # every BN / add / ReLU folded into a conv (or into the split-K reduce that finishes it); the 16
-    # convs with a kernel wider than 1 x 1 read their weights through a per-run OHWI copy
-    copies = [s for s in p.steps if s.kernel == "k_copy"]
-    assert len(convs) == 53 and len(copies) == 16 and len(p.steps) <= 57 + len(reduces) + len(copies)
+    # convs with a kernel wider than 1 x 1 read their weights as OHWI, copied by one launch that
+    # opens every run
+    perm = [s for s in p.steps if s.kernel == "k_permute_ohwi"]
+    assert len(convs) == 53 and len(perm) == 1 and perm[0].params["tensors"] == 16 and p.steps[0] is perm[0]
+    assert len(p.steps) <= 57 + len(reduces) + 1 and not any(s.kernel == "k_copy" for s in p.steps)
     assert all(s.kernel.startswith(("k_conv_reduce_", "k_gemm_reduce_f16_conv")) for s in reduces)
     assert len(reduces) == sum(1 for s in convs if s.params["ksplit"] > 1)
     assert sum(1 for s in convs if s.args["flags"] & 4) == 16 and all(s.args["flags"] & 2 for s in convs)
