@@ -108,7 +108,7 @@ __device__ __forceinline__ float gm_conv_tail(const GemmArgs& a, float v, float 
 }
 
 // STAGES 0: LDS double buffer filled through registers (the loads of step s + 1 are in flight
-// while step s is multiplied). STAGES >= 3 (BK 64, not KN): the operands go from global memory
+// while step s is multiplied). STAGES >= 2 (BK 64, not KN): the operands go from global memory
 // straight into LDS (gfx950 global_load_lds_dwordx4), STAGES buffers deep, so the loads of
 // steps s + 1 .. s + STAGES - 1 are in flight while step s is multiplied and no registers hold
 // them. Those rows are unpadded 128-byte rows; 16-byte chunk c of row r sits in slot
@@ -118,7 +118,7 @@ __device__ __forceinline__ float gm_conv_tail(const GemmArgs& a, float v, float 
 template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false,
           int STAGES = 0, bool CV = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
-  constexpr bool DMA = STAGES >= 3;
+  constexpr bool DMA = STAGES >= 2;
   static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
   static_assert(!CV || (DMA && NW == 1 && !GRP), "conv gather: direct-to-LDS, one weight");
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
@@ -258,6 +258,32 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     W1 += kbeg;
   }
   const int fr = lane & 31, fk = (lane >> 5) * 8;   // fragment row/column and k offset of this lane
+  // residual operands of this lane's outputs, two rows per register: loaded before any store (as far
+  // as the compiler knows a store may alias them, so loads interleaved with the stores would each
+  // wait a memory latency), and on the direct-to-LDS path before the main loop, so that their
+  // latency overlaps the operand loads instead of following the last MFMA
+  constexpr bool HAS_R = EPI == GE_RESID || EPI == GE_CONV;
+  const bool want_r = EPI == GE_RESID || (EPI == GE_CONV && (a.flags & 4));
+  uint32_t rr[HAS_R ? TJ : 1][HAS_R ? TI : 1][8];
+  auto load_resid = [&](const int j0, const int j1) {   // column groups [j0, j1)
+#pragma unroll
+    for (int j = j0; j < j1; ++j) {
+      const int n = min(n_base + wc * (BN / 2) + j * 32 + fr, a.N - 1);
+#pragma unroll
+      for (int i = 0; i < (HAS_R ? TI : 1); ++i)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          uint32_t w = 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int e = 2 * e2 + h;
+            const long long m = min(m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), a.M - 1);
+            w |= (uint32_t)((const uint16_t*)a.resid)[m * a.ldr + n] << (16 * h);
+          }
+          rr[j][i][e2] = w;
+        }
+    }
+  };
   if constexpr (!DMA) {
     auto compute = [&](const int buf) {
 #pragma unroll
@@ -376,6 +402,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       }
     };
     constexpr int NI = NA + NB;   // vmcnt per stage
+    if (HAS_R && want_r && a.ksplit == 1) load_resid(0, TJ);   // issued first: the first stage's wait covers them
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
       if (st < nsteps) issue(st);
@@ -406,27 +433,28 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       }
     return;
   }
-  // epilogue
+  // epilogue (register staging: one column group's residuals at a time, which keeps the epilogue
+  // under the main loop's register count)
+  if constexpr (HAS_R) {
+    if (!want_r) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int e2 = 0; e2 < 8; ++e2) rr[j][i][e2] = 0;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
+    if constexpr (HAS_R && !DMA)
+      if (want_r) load_resid(j, j + 1);
     const int n = n_base + wc * (BN / 2) + j * 32 + fr;
     if (n >= a.N) continue;
     const float b0 = (a.flags & 1) ? gm_ld<DT>(g_bias, n - g_lo) : 0.f;
     const float b1 = (EPI == GE_SILU && (a.flags & 2)) ? gm_ld<DT>(a.bias2, n) : 0.f;
     float al = 1.f, be = 0.f;   // conv: inference batch norm v * al + be (the conv.hip factors)
     if (EPI == GE_CONV && (a.flags & 2)) gm_bn_factors<DT>(a, n, al, be);
-    // the column's residual operands are loaded before any store: as far as the compiler knows a
-    // store may alias them, so loads interleaved with the stores would each wait a memory latency
-    uint16_t rr[(EPI == GE_RESID || EPI == GE_CONV) ? TI : 1][16] = {};
-    if (EPI == GE_RESID || (EPI == GE_CONV && (a.flags & 4))) {
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const long long m = min(m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), a.M - 1);
-          rr[i][e] = ((const uint16_t*)a.resid)[m * a.ldr + n];
-        }
-    }
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
 #pragma unroll
@@ -434,9 +462,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (m >= a.M) continue;
         float v = gm_round<DT>(acc[0][i][j][e] + b0);
-        if constexpr (EPI == GE_RESID)
-          v = gm_round<DT>((DT == HS_BF16 ? bf16_to_f32(rr[i][e]) : f16_to_f32(rr[i][e])) + v);
-        if constexpr (EPI == GE_CONV) v = gm_conv_tail<DT>(a, v, al, be, rr[i][e]);
+        const uint16_t r16 = HAS_R ? (uint16_t)(rr[HAS_R ? j : 0][HAS_R ? i : 0][e >> 1] >> (16 * (e & 1))) : 0;
+        if constexpr (EPI == GE_RESID) v = gm_round<DT>((DT == HS_BF16 ? bf16_to_f32(r16) : f16_to_f32(r16)) + v);
+        if constexpr (EPI == GE_CONV) v = gm_conv_tail<DT>(a, v, al, be, r16);
         if constexpr (EPI == GE_SILU) {
           const float up = gm_round<DT>(acc[NW - 1][i][j][e] + b1);
           const float sg = gm_round<DT>(v / (1.f + expf(-v)));
@@ -541,6 +569,12 @@ GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
   }                                                                                                             \
   extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d(const GemmArgs a) {               \
     gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST, true>(a);                                            \
+  }                                                                                                             \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64d2(const GemmArgs a) {               \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2>(a);                                                   \
+  }                                                                                                             \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d2(const GemmArgs a) {              \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, true>(a);                                             \
   }
 GEMM_CONV(f16, HS_F16, 128, 128, 4)
 GEMM_CONV(f16, HS_F16, 128, 64, 3)

@@ -41,6 +41,7 @@ GEMM_MIN_M = 16
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
+CONV_D2_MAX_K = int(os.environ.get("HIPRT_CONV_D2_MAX_K", "512"))   # convs up to this K: 2-stage staging
 
 
 def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, bool]:
@@ -967,7 +968,9 @@ class Lowering:
         bnv = [self.contiguous(t.name) for t in bn.inputs[1:5]] if bn is not None else [None] * 4
         flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
         bm, bn_, ksplit = conv_gemm_tiling(M, Cout, K)
-        dma = (not plain) or ((M + bm - 1) // bm) * ((Cout + bn_ - 1) // bn_) < GEMM_DMA_MAX_TILES
+        # always direct-to-LDS; short K (few steps: the pipeline depth buys nothing) takes the 2-stage
+        # variant, whose smaller LDS footprint lets two workgroups share a CU
+        stages = "d2" if K <= CONV_D2_MAX_K else "d"
         kchunk = K
         if ksplit > 1:
             kchunk = ((K // 64 + ksplit - 1) // ksplit) * 64
@@ -975,7 +978,7 @@ class Lowering:
         if self._conv_zero is None:
             self._conv_zero = self.scratch("conv.zero", 256, persistent=True)
         dts = "bf16" if dt == "bfloat16" else "f16"
-        kname = f"k_gemm_{dts}_{'conv' if plain else 'convg'}_m{bm}n{bn_}" + ("_k64d" if dma else "_k64")
+        kname = f"k_gemm_{dts}_{'conv' if plain else 'convg'}_m{bm}n{bn_}_k64{stages}"
         part = self.scratch(out_name + ".kpart", ksplit * M * Cout * 4) if ksplit > 1 else None
         args = dict(x=self.ref(xv), w=self.ref(w), w2=None, bias=self.ref(self.contiguous(conv.inputs[2].name))
                     if has_bias else None, bias2=None, resid=self.ref(rv) if rv is not None else None,
@@ -991,7 +994,8 @@ class Lowering:
             ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
         params = {"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
                   "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
-                  "ksplit": ksplit, "nhwc": True, "tile": (bm, bn_), "lds_direct": dma, "nodes": nodes or [conv.name]}
+                  "ksplit": ksplit, "nhwc": True, "tile": (bm, bn_), "lds_direct": True, "stages": stages,
+                  "nodes": nodes or [conv.name]}
         self.emit(LaunchStep(
             kind="conv", kernel=kname, module="gemm", arg_struct="GemmArgs", args=args,
             grid=((Cout + bn_ - 1) // bn_, (M + bm - 1) // bm, ksplit), inputs=ins,
