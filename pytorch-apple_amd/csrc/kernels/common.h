@@ -214,6 +214,9 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   const void* bn_var;
   const void* zero;           // conv gather (_convg kernels): >= 16 zero bytes, read for padded taps
   float eps;
+  // _convg: x is NHWC [*, cH, cW, cCin], row m = output pixel (n, ho, wo), padded taps read `zero`;
+  // _convp: x is an already zero-bordered NHWC image [*, cH, cW, cCin = 4], k = (kh * cKW + kw) * 4 + c
+  // with cKW even, so a 16-byte chunk is two neighbouring taps of one kernel row (always in bounds)
   int cH;                     // conv gather: x is NHWC [*, cH, cW, cCin], row m = output pixel (n, ho, wo),
   int cW;                     //   k = (kh * cKW + kw) * cCin + ci, cCin % 64 == 0; w is [N, KH * KW * Cin] (OHWI)
   int cCin;
@@ -256,13 +259,31 @@ struct PoolArgs {             // max pooling (conv.hip): NCHW, or NHWC for the _
 };
 
 #define HS_OHWI_MAX 24
-struct PermuteOHWIArgs {      // OIHW -> OHWI copies of up to HS_OHWI_MAX 2-byte weights in one launch (conv.hip)
-  const void* src[HS_OHWI_MAX];   // [Cout, Cin, KH, KW]
-  void* dst[HS_OHWI_MAX];         // [Cout, KH, KW, Cin]
+struct PermuteOHWIArgs {      // OIHW -> (zero-padded) OHWI copies of up to HS_OHWI_MAX 2-byte weights, one launch (conv.hip)
+  const void* src[HS_OHWI_MAX];   // [Cout, cin, kh, kw]
+  void* dst[HS_OHWI_MAX];         // [Cout, khp, kwp, cp]: zero where kh <= y, kw <= x or cin <= c
   long long start[HS_OHWI_MAX + 1];   // first element of tensor i in the joint index space; start[n] = total
-  int cin[HS_OHWI_MAX];           // multiple of 8
-  int kk[HS_OHWI_MAX];            // KH * KW
+  int cin[HS_OHWI_MAX];
+  int kh[HS_OHWI_MAX];
+  int kw[HS_OHWI_MAX];
+  int cp[HS_OHWI_MAX];
+  int khp[HS_OHWI_MAX];
+  int kwp[HS_OHWI_MAX];           // Cout * khp * kwp * cp is a multiple of 8
   int n;
+  int pad;
+};
+
+struct PadNHWCArgs {          // NCHW [N, C, H, W] -> zero-bordered NHWC [N, Hp, Wp, 4] (C <= 4) (conv.hip)
+  const void* x;
+  void* out;
+  long long n;
+  int C;
+  int H;
+  int W;
+  int Hp;
+  int Wp;
+  int top;                    // rows / columns of zeros before the image
+  int left;
   int pad;
 };
 

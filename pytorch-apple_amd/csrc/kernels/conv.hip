@@ -501,9 +501,9 @@ __device__ __forceinline__ void mean_nhwc_body(const MeanNHWCArgs& a) {
 extern "C" __global__ void __launch_bounds__(256) k_mean_nhwc_f16(const MeanNHWCArgs a) { mean_nhwc_body<HS_F16>(a); }
 extern "C" __global__ void __launch_bounds__(256) k_mean_nhwc_bf16(const MeanNHWCArgs a) { mean_nhwc_body<HS_BF16>(a); }
 
-// OIHW -> OHWI weight copies (the channels-last convs read k = (kh, kw, ci)): one thread per 8
-// destination elements (16-byte store), gathered from 8 source rows; tensor found by a scan of
-// the start offsets (at most HS_OHWI_MAX)
+// OIHW -> OHWI weight copies (the channels-last convs read k = (kh, kw, ci)), zero-padded to
+// [Cout, khp, kwp, cp] where asked: one thread per 8 destination elements (one 16-byte store), each
+// element decoded on its own; the tensor is found by a scan of the start offsets
 extern "C" __global__ void __launch_bounds__(256) k_permute_ohwi(const PermuteOHWIArgs a) {
   const long long total8 = a.start[a.n] / 8;
   for (long long g = (long long)blockIdx.x * 256 + threadIdx.x; g < total8; g += (long long)gridDim.x * 256) {
@@ -511,14 +511,50 @@ extern "C" __global__ void __launch_bounds__(256) k_permute_ohwi(const PermuteOH
     int i = 0;
     while (i + 1 < a.n && a.start[i + 1] <= e0) ++i;
     const long long e = e0 - a.start[i];
-    const int cin = a.cin[i], kk = a.kk[i];
-    const long long per = (long long)cin * kk;
-    const long long co = e / per;
-    const int rem = (int)(e - co * per), t = rem / cin, ci = rem - t * cin;
-    const uint16_t* src = (const uint16_t*)a.src[i] + (co * cin + ci) * kk + t;
+    const int cin = a.cin[i], kh = a.kh[i], kw = a.kw[i], cp = a.cp[i], kwp = a.kwp[i];
+    const long long per = (long long)a.khp[i] * kwp * cp;
+    const uint16_t* src = (const uint16_t*)a.src[i];
     uint32_t w[4];
+    if (cp == cin && a.khp[i] == kh && kwp == kw && (cin & 7) == 0) {   // unpadded: 8 channels of one tap
+      const int kk = kh * kw;
+      const long long co = e / per;
+      const int rem = (int)(e - co * per), t = rem / cin, ci = rem - t * cin;
+      const uint16_t* s0 = src + (co * cin + ci) * kk + t;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = src[(2 * j) * kk] | ((uint32_t)src[(2 * j + 1) * kk] << 16);
+      for (int j = 0; j < 4; ++j) w[j] = s0[(2 * j) * kk] | ((uint32_t)s0[(2 * j + 1) * kk] << 16);
+      *(uint4*)((uint16_t*)a.dst[i] + e) = make_uint4(w[0], w[1], w[2], w[3]);
+      continue;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const long long ej = e + j;
+      const long long co = ej / per;
+      const int r = (int)(ej - co * per), y = r / (kwp * cp), xc = r - y * (kwp * cp), x = xc / cp, c = xc - x * cp;
+      const uint16_t v = (y < kh && x < kw && c < cin) ? src[((co * cin + c) * kh + y) * kw + x] : (uint16_t)0;
+      if (j & 1) w[j >> 1] |= (uint32_t)v << 16;
+      else w[j >> 1] = v;
+    }
     *(uint4*)((uint16_t*)a.dst[i] + e) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// NCHW image with C <= 4 channels -> zero-bordered channels-last [N, Hp, Wp, 4] (channels past C
+// are 0): the input of the _convp GEMM, whose taps then never leave the buffer. One thread per
+// output pixel (one 8-byte store).
+extern "C" __global__ void __launch_bounds__(256) k_pad_nhwc4(const PadNHWCArgs a) {
+  const long long total = a.n * a.Hp * a.Wp;
+  const long long plane = (long long)a.H * a.W;
+  for (long long p = (long long)blockIdx.x * 256 + threadIdx.x; p < total; p += (long long)gridDim.x * 256) {
+    const int xo = (int)(p % a.Wp);
+    const long long t = p / a.Wp;
+    const int yo = (int)(t % a.Hp);
+    const long long img = t / a.Hp;
+    const int y = yo - a.top, x = xo - a.left;
+    uint16_t v[4] = {0, 0, 0, 0};
+    if ((unsigned)y < (unsigned)a.H && (unsigned)x < (unsigned)a.W) {
+      const uint16_t* src = (const uint16_t*)a.x + img * a.C * plane + (long long)y * a.W + x;
+      for (int c = 0; c < a.C; ++c) v[c] = src[c * plane];
+    }
+    *(uint2*)((uint16_t*)a.out + p * 4) = make_uint2(v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16));
   }
 }

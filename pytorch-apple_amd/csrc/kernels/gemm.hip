@@ -113,10 +113,11 @@ __device__ __forceinline__ float gm_conv_tail(const GemmArgs& a, float v, float 
 // steps s + 1 .. s + STAGES - 1 are in flight while step s is multiplied and no registers hold
 // them. Those rows are unpadded 128-byte rows; 16-byte chunk c of row r sits in slot
 // c ^ gm_swz(r), so the fragment reads of 8 consecutive rows hit 8 different bank groups.
-// CV (direct-to-LDS only): A is gathered from an NHWC image, row m = output pixel, k = (kh, kw, ci)
-// with a whole 64-channel block per K step; padded taps read a.zero (see GemmArgs).
+// CV (direct-to-LDS only), A gathered from an NHWC image with row m = output pixel (see GemmArgs):
+// 1: k = (kh, kw, ci), a whole 64-channel block per K step, padded taps read a.zero;
+// 2: a zero-bordered 4-channel image, each 16-byte chunk two neighbouring taps of one kernel row.
 template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false,
-          int STAGES = 0, bool CV = false>
+          int STAGES = 0, int CV = 0>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr bool DMA = STAGES >= 2;
   static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
@@ -324,7 +325,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     const char* asrc[NA];
     const char* bsrc[NB];
     int ghi[CV ? NA : 1], gwi[CV ? NA : 1];   // CV: top-left input tap of the row's pixel
-    long long gpb[CV ? NA : 1];               // CV: element offset of (n, ghi, gwi, lane's chunk)
+    long long gpb[CV ? NA : 1];               // CV: element offset of (n, ghi, gwi) (+ the lane's chunk for CV 1)
+    int lcs[CV ? NA : 1];                     // CV: the 16-byte chunk of the step this lane fetches
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
       const int row = (wave * NA + q) * 8 + lr;
@@ -335,7 +337,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         const int n = mi / HoWo, p = mi - n * HoWo, ho = p / a.cWo, wo = p - ho * a.cWo;
         ghi[q] = ho * a.csh - a.cph;
         gwi[q] = wo * a.csw - a.cpw;
-        gpb[q] = (((long long)n * a.cH + ghi[q]) * a.cW + gwi[q]) * a.cCin + (ls ^ gm_swz(row)) * 8;
+        lcs[q] = ls ^ gm_swz(row);
+        gpb[q] = (((long long)n * a.cH + ghi[q]) * a.cW + gwi[q]) * a.cCin + (CV == 1 ? lcs[q] * 8 : 0);
       }
     }
 #pragma unroll
@@ -353,7 +356,15 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     auto issue = [&](int st) {   // stage st of the K loop into LDS buffer st % STAGES
       const unsigned base = lds0 + (unsigned)((st % STAGES) * SSTAGE) * 2u;
       const long long kb = (long long)st * BK * 2;
-      if constexpr (CV) {   // one tap and one 64-channel block per step (uniform)
+      if constexpr (CV == 2) {   // chunk t of the K range: kernel row t / cpr, taps 2 (t % cpr), + 1
+        const int cpr = a.cKW * a.cCin / 8;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) {
+          const int kt = kbeg / 8 + st * 8 + lcs[q], kh = kt / cpr, kwc = kt - kh * cpr;
+          const uint16_t* src = (const uint16_t*)a.x + gpb[q] + (long long)kh * a.cW * a.cCin + kwc * 8;
+          gm_dma16(src, __builtin_amdgcn_readfirstlane(base + (unsigned)((wave * NA + q) * 8 * SROW * 2)));
+        }
+      } else if constexpr (CV == 1) {   // one tap and one 64-channel block per step (uniform)
         const int k = kbeg + st * BK;
         const int tap = k / a.cCin, c0 = k - tap * a.cCin;
         const int kh = tap / a.cKW, kw = tap - kh * a.cKW;
@@ -559,7 +570,8 @@ GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
   }
 // conv2d on channels-last activations (conv epilogue): _conv takes x as the [pixels, Cin] rows of
 // an NHWC image (1 x 1, stride 1, no padding); _convg gathers the taps of any kernel / stride /
-// padding (Cin % 64 == 0) with direct-to-LDS staging
+// padding (Cin % 64 == 0) with direct-to-LDS staging; _convp reads a zero-bordered 4-channel image
+// (a network's first conv on a 3-channel input, after k_pad_nhwc4)
 #define GEMM_CONV(DTN, DT, BM, BN, ST)                                                                           \
   extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64(const GemmArgs a) {                 \
     gemm_body<DT, GE_CONV, 1, BM, BN, false, 64>(a);                                                             \
@@ -568,13 +580,16 @@ GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
     gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST>(a);                                                  \
   }                                                                                                             \
   extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d(const GemmArgs a) {               \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST, true>(a);                                            \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST, 1>(a);                                               \
   }                                                                                                             \
   extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64d2(const GemmArgs a) {               \
     gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2>(a);                                                   \
   }                                                                                                             \
   extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d2(const GemmArgs a) {              \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, true>(a);                                             \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 1>(a);                                                \
+  }                                                                                                             \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convp_m##BM##n##BN##_k64d2(const GemmArgs a) {              \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 2>(a);                                                \
   }
 GEMM_CONV(f16, HS_F16, 128, 128, 4)
 GEMM_CONV(f16, HS_F16, 128, 64, 3)

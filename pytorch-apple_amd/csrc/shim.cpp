@@ -253,6 +253,7 @@ size_t hs_argsize(const char* s) {
   HS_SZ(PoolArgs)
   HS_SZ(MeanNHWCArgs)
   HS_SZ(PermuteOHWIArgs)
+  HS_SZ(PadNHWCArgs)
   HS_SZ(BatchNormArgs)
   HS_SZ(DecodeAttnArgs)
   HS_SZ(FusedArgs)

@@ -170,7 +170,9 @@ class Lowering:
         # convolutions on channels-last activations through the MFMA GEMM (HIPRT_CONV_NHWC=0: NCHW kernels only)
         self.conv_nhwc = os.environ.get("HIPRT_CONV_NHWC", "1") == "1"
         self._conv_zero: Ref | None = None
-        self._ohwi: list = []   # bound conv weights read as OHWI: (name, OIHW view, OHWI view, Cin, KH*KW)
+        # bound conv weights read as (zero-padded) OHWI: (name, OIHW view, destination view,
+        # (cin, kh, kw) of the source, (cp, khp, kwp) of the destination)
+        self._ohwi: list = []
         self.steps: list[LaunchStep] = []
         self.storages: dict[str, Storage] = {}
         self.views: dict[str, TView] = {}
@@ -847,6 +849,10 @@ class Lowering:
         if self.conv_nhwc and _is_nhwc(xv) and xv.shape[1] % 64 == 0 and xv.dtype in ("float16", "bfloat16") \
                 and (xv.offset * 2) % 16 == 0:
             return self.emit_conv_nhwc(conv, out_name, xv, bn=bn, resid=resid, relu=relu, nodes=nodes)
+        wv0 = self.view(conv.inputs[1].name)
+        if self.conv_nhwc and len(xv.shape) == 4 and xv.shape[1] <= 4 and xv.dtype in ("float16", "bfloat16") \
+                and wv0.dtype == xv.dtype and wv0.shape[0] % 8 == 0 and wv0.shape[2] <= 16 and wv0.shape[3] <= 16:
+            return self.emit_conv_stem(conv, out_name, bn=bn, resid=resid, relu=relu, nodes=nodes)
         x = self.contiguous(conv.inputs[0].name)
         w = self.contiguous(conv.inputs[1].name)
         has_bias = len(conv.inputs) > 2
@@ -947,10 +953,11 @@ class Lowering:
             w = self.views.get(key)
             if w is None:
                 w = self.new_storage(key, [Cout, KH, KW, Cin], dt)
-                if self.is_constant(wv) and wv.is_contiguous() and (wv.offset * 2) % 16 == 0:
-                    self._ohwi.append((wname, wv, w, Cin, KH * KW))   # one launch at the program start
+                ent = (wname, wv, w, (Cin, KH, KW), (Cin, KH, KW))
+                if self.is_constant(wv) and wv.is_contiguous():
+                    self._ohwi.append(ent)   # one launch at the program start
                 else:
-                    self.emit_copy(V.permute(wv, [0, 2, 3, 1]), w, [wname], [key])
+                    self.emit(self._permute_step([ent]))
                 self.views[key] = w
         else:
             w = self.aligned16(self.contiguous(wname), wname)
@@ -1005,6 +1012,87 @@ class Lowering:
                 kind="conv", kernel=f"k_gemm_reduce_{dts}_conv", module="gemm", arg_struct="GemmArgs",
                 args=dict(args), grid=grid1d(M * Cout), inputs=[out_name + ".kpart"] + ins[2:],
                 outputs=[out_name], params=dict(params, reduce=True)))
+        self.views[out_name] = o
+
+    def emit_conv_stem(self, conv: OpNode, out_name: str, *, bn: OpNode | None, resid: str | None, relu: bool,
+                       nodes: list[str] | None) -> None:
+        """A conv on an image of at most 4 channels (a network's first layer, e.g. ResNet's 7 x 7 / 2 on
+        RGB): the image is written once per run as a zero-bordered channels-last [N, Hp, Wp, 4] buffer
+        (k_pad_nhwc4), the weights as [Cout, KHp, KWp, 4] with zeros past the kernel (KWp even, so a
+        16-byte chunk is two neighbouring taps), and the _convp GEMM reads every tap in bounds with
+        no checks. K = KHp * KWp * 4 (256 for 7 x 7) instead of 2-byte gathers over K = 147."""
+        x = self.contiguous(conv.inputs[0].name)
+        wname = conv.inputs[1].name
+        wv = self.view(wname)
+        has_bias = len(conv.inputs) > 2
+        N, C, H, W = x.shape
+        Cout, _, KH, KW = wv.shape
+        Ho, Wo = conv.outputs[0].shape[2], conv.outputs[0].shape[3]
+        st = conv.attrs.get("stride", [1, 1])
+        pd = conv.attrs.get("padding", [0, 0])
+        st = [st, st] if isinstance(st, int) else list(st)
+        pd = [pd, pd] if isinstance(pd, int) else list(pd)
+        dt = x.dtype
+        kwp = KW + (KW & 1)
+        khp = KH
+        while (khp * kwp * 4) % 64:
+            khp += 1
+        K = khp * kwp * 4
+        Hp = max(H + 2 * pd[0], (Ho - 1) * st[0] + khp)
+        Wp = max(W + 2 * pd[1], (Wo - 1) * st[1] + kwp)
+        M = N * Ho * Wo
+        if M + 256 >= 2 ** 31 or N * Hp * Wp * 4 >= 2 ** 31:
+            raise NotImplementedError("conv2d with 2^31 or more padded input elements or output pixels")
+        xp = self.new_storage(conv.inputs[0].name + ".pad4", [N, Hp, Wp, 4], dt)
+        self.emit(LaunchStep(
+            kind="copy", kernel="k_pad_nhwc4", module="conv", arg_struct="PadNHWCArgs",
+            args=dict(x=self.ref(x), out=self.ref(xp), n=N, C=C, H=H, W=W, Hp=Hp, Wp=Wp, top=pd[0], left=pd[1], pad=0),
+            grid=grid1d(N * Hp * Wp), inputs=[conv.inputs[0].name], outputs=[xp.storage],
+            params={"padded": [Hp, Wp]}))
+        key = wname + ".pad4"
+        w = self.views.get(key)
+        if w is None:
+            w = self.new_storage(key, [Cout, khp, kwp, 4], dt)
+            ent = (wname, wv, w, (C, KH, KW), (4, khp, kwp))
+            if self.is_constant(wv) and wv.is_contiguous():
+                self._ohwi.append(ent)
+            else:
+                self.emit(self._permute_step([ent] if wv.is_contiguous() else [(wname, self.contiguous(wname), w,
+                                                                                 (C, KH, KW), (4, khp, kwp))]))
+            self.views[key] = w
+        ob = self.new_storage(out_name, [N, Ho, Wo, Cout], dt)
+        o = ob.with_(shape=(N, Cout, Ho, Wo), strides=(Ho * Wo * Cout, 1, Wo * Cout, Cout))
+        rv = None
+        if resid is not None:
+            rv = self.view(resid)
+            if not _is_nhwc(rv):
+                rb = self.new_storage(resid + ".nhwc", [rv.shape[0], rv.shape[2], rv.shape[3], rv.shape[1]], dt)
+                self.emit_copy(rv, rb.with_(shape=rv.shape, strides=(rb.strides[0], 1, rb.strides[1], rb.strides[2])),
+                               [resid], [resid + ".nhwc"])
+                rv = rb
+        bnv = [self.contiguous(t.name) for t in bn.inputs[1:5]] if bn is not None else [None] * 4
+        flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
+        bm, bn_, _ = conv_gemm_tiling(M, Cout, K)
+        dts = "bf16" if dt == "bfloat16" else "f16"
+        args = dict(x=self.ref(xp), w=self.ref(w), w2=None, bias=self.ref(self.contiguous(conv.inputs[2].name))
+                    if has_bias else None, bias2=None, resid=self.ref(rv) if rv is not None else None,
+                    out=self.ref(ob), part=None, M=M, ldx=0, ldw=K, ldo=Cout, ldr=Cout, sx=0, sw=0, so=0, batch=1,
+                    bdiv=1, N=Cout, K=K, flags=flags, ksplit=1, kchunk=K, nw=1,
+                    bn_w=self.ref(bnv[0]) if bn is not None else None,
+                    bn_b=self.ref(bnv[1]) if bn is not None else None,
+                    bn_mean=self.ref(bnv[2]) if bn is not None else None,
+                    bn_var=self.ref(bnv[3]) if bn is not None else None,
+                    zero=None, eps=float(bn.attrs.get("eps", 1e-5)) if bn is not None else 0.0,
+                    cH=Hp, cW=Wp, cCin=4, cHo=Ho, cWo=Wo, cKW=kwp, csh=st[0], csw=st[1], cph=0, cpw=0)
+        ins = [conv.inputs[0].name, wname] + ([conv.inputs[2].name] if has_bias else []) + \
+            ([t.name for t in bn.inputs[1:5]] if bn is not None else []) + ([resid] if resid else [])
+        self.emit(LaunchStep(
+            kind="conv", kernel=f"k_gemm_{dts}_convp_m{bm}n{bn_}_k64d2", module="gemm", arg_struct="GemmArgs",
+            args=args, grid=((Cout + bn_ - 1) // bn_, (M + bm - 1) // bm, 1), inputs=ins, outputs=[out_name],
+            params={"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
+                    "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
+                    "ksplit": 1, "nhwc": True, "tile": (bm, bn_), "lds_direct": True, "stages": "d2",
+                    "padded_taps": [khp, kwp, 4], "nodes": nodes or [conv.name]}))
         self.views[out_name] = o
 
     def lower_conv2d(self, node: OpNode) -> None:
@@ -1282,28 +1370,32 @@ class Lowering:
             self.view(o.name)
         self.emit_weight_permutes()
 
-    def emit_weight_permutes(self) -> None:
-        """The OIHW -> OHWI copies of bound conv weights, in launches of up to OHWI_MAX tensors placed
-        first in the program (they depend on nothing else), re-run every execution like any step."""
+    def _permute_step(self, chunk: list) -> LaunchStep:
+        """One k_permute_ohwi launch over up to OHWI_MAX (name, src, dst, (cin, kh, kw), (cp, khp, kwp))."""
         from hip_runtime.kernels import OHWI_MAX
 
-        pre = []
-        for c in range(0, len(self._ohwi), OHWI_MAX):
-            chunk = self._ohwi[c:c + OHWI_MAX]
-            start, tot = [], 0
-            for _, wv, _, _, _ in chunk:
-                start.append(tot)
-                tot += wv.numel
-            pad = OHWI_MAX - len(chunk)
-            pre.append(LaunchStep(
-                kind="copy", kernel="k_permute_ohwi", module="conv", arg_struct="PermuteOHWIArgs",
-                args=dict(src=[self.ref(e[1]) for e in chunk] + [None] * pad,
-                          dst=[self.ref(e[2]) for e in chunk] + [None] * pad,
-                          start=start + [tot] * (pad + 1), cin=[e[3] for e in chunk] + [0] * pad,
-                          kk=[e[4] for e in chunk] + [0] * pad, n=len(chunk), pad=0),
-                grid=grid1d(tot // 8), inputs=[e[0] for e in chunk], outputs=[e[0] + ".ohwi" for e in chunk],
-                params={"tensors": len(chunk), "elements": tot}))
-        self.steps[:0] = pre
+        start, tot = [], 0
+        for e in chunk:
+            start.append(tot)
+            tot += e[2].numel
+        pad = OHWI_MAX - len(chunk)
+        col = lambda f: [f(e) for e in chunk] + [1] * pad
+        return LaunchStep(
+            kind="copy", kernel="k_permute_ohwi", module="conv", arg_struct="PermuteOHWIArgs",
+            args=dict(src=[self.ref(e[1]) for e in chunk] + [None] * pad,
+                      dst=[self.ref(e[2]) for e in chunk] + [None] * pad,
+                      start=start + [tot] * (pad + 1), cin=col(lambda e: e[3][0]), kh=col(lambda e: e[3][1]),
+                      kw=col(lambda e: e[3][2]), cp=col(lambda e: e[4][0]), khp=col(lambda e: e[4][1]),
+                      kwp=col(lambda e: e[4][2]), n=len(chunk), pad=0),
+            grid=grid1d(tot // 8), inputs=[e[0] for e in chunk], outputs=[e[2].storage for e in chunk],
+            params={"tensors": len(chunk), "elements": tot})
+
+    def emit_weight_permutes(self) -> None:
+        """The OHWI copies of bound conv weights, in launches of up to OHWI_MAX tensors placed first in
+        the program (they depend on nothing else), re-run every execution like any step."""
+        from hip_runtime.kernels import OHWI_MAX
+
+        self.steps[:0] = [self._permute_step(self._ohwi[c:c + OHWI_MAX]) for c in range(0, len(self._ohwi), OHWI_MAX)]
         self._ohwi = []
 
     def is_constant(self, v: TView) -> bool:

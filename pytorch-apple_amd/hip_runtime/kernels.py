@@ -68,7 +68,10 @@ _struct("PoolArgs", [("x", P), ("out", P), ("planes", LL), ("H", I), ("W", I), (
                      ("kw", I), ("sh", I), ("sw", I), ("ph", I), ("pw", I), ("dtype", I), ("C", I)])
 OHWI_MAX = 24   # HS_OHWI_MAX
 _struct("PermuteOHWIArgs", [("src", P * OHWI_MAX), ("dst", P * OHWI_MAX), ("start", LL * (OHWI_MAX + 1)),
-                            ("cin", I * OHWI_MAX), ("kk", I * OHWI_MAX), ("n", I), ("pad", I)])
+                            ("cin", I * OHWI_MAX), ("kh", I * OHWI_MAX), ("kw", I * OHWI_MAX), ("cp", I * OHWI_MAX),
+                            ("khp", I * OHWI_MAX), ("kwp", I * OHWI_MAX), ("n", I), ("pad", I)])
+_struct("PadNHWCArgs", [("x", P), ("out", P), ("n", LL), ("C", I), ("H", I), ("W", I), ("Hp", I), ("Wp", I),
+                        ("top", I), ("left", I), ("pad", I)])
 _struct("MeanNHWCArgs", [("x", P), ("out", P), ("n", LL), ("hw", I), ("c", I)])
 _struct("BatchNormArgs", [("x", P), ("w", P), ("b", P), ("mean", P), ("var", P), ("out", P), ("n", LL),
                           ("hw", LL), ("C", I), ("eps", F), ("dtype", I), ("relu", I)])

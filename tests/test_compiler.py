@@ -212,15 +212,17 @@ def test_resnet50_compiles_to_fused_convs():
     # convs with a kernel wider than 1 x 1 read their weights as OHWI, copied by one launch that
     # opens every run
     perm = [s for s in p.steps if s.kernel == "k_permute_ohwi"]
-    assert len(convs) == 53 and len(perm) == 1 and perm[0].params["tensors"] == 16 and p.steps[0] is perm[0]
-    assert len(p.steps) <= 57 + len(reduces) + 1 and not any(s.kernel == "k_copy" for s in p.steps)
-    assert all(s.kernel.startswith(("k_conv_reduce_", "k_gemm_reduce_f16_conv")) for s in reduces)
+    assert len(convs) == 53 and len(perm) == 1 and perm[0].params["tensors"] == 17 and p.steps[0] is perm[0]
+    assert len(p.steps) <= 57 + len(reduces) + 2 and not any(s.kernel == "k_copy" for s in p.steps)
+    assert all(s.kernel.startswith("k_gemm_reduce_f16_conv") for s in reduces)
     assert len(reduces) == sum(1 for s in convs if s.params["ksplit"] > 1)
     assert sum(1 for s in convs if s.args["flags"] & 4) == 16 and all(s.args["flags"] & 2 for s in convs)
-    assert convs[0].kernel.endswith("_g") and convs[0].args["K"] == 147   # 3-channel stem: gathered weights
-    # channels-last from the stem on: the stem writes NHWC (flag 16), the other 52 convs are MFMA GEMMs
-    # over NHWC (1 x 1 stride 1: the image rows as they are; else tap gathers), pools read NHWC
-    assert convs[0].args["flags"] & 16 and all(s.params.get("nhwc") for s in convs[1:])
+    # the 3-channel stem reads a zero-bordered 4-channel NHWC copy of the image: 8 x 8 x 4 taps, K = 256
+    assert p.steps[1].kernel == "k_pad_nhwc4" and p.steps[1].params["padded"] == [230, 230]
+    assert convs[0].kernel.startswith("k_gemm_f16_convp_") and convs[0].args["K"] == 256
+    # channels-last from the stem on: all 53 convs are MFMA GEMMs over NHWC (1 x 1 stride 1: the image
+    # rows as they are; else tap gathers), pools read NHWC
+    assert all(s.params.get("nhwc") for s in convs)
     assert all(s.kernel.startswith(("k_gemm_f16_conv_", "k_gemm_f16_convg_")) for s in convs[1:])
     assert sum(1 for s in convs[1:] if "_convg_" in s.kernel) == 16 + 3   # 3 x 3 and the stride-2 1 x 1
     ks = [s.kernel for s in p.steps]

@@ -678,7 +678,8 @@ def _conv_ir(N, Cin, H, W, Cout, k, stride, pad, bn=True, add=False, relu=True, 
 
 
 @pytest.mark.parametrize("N,Cin,H,W,Cout,k,stride,pad,add", [
-    (2, 3, 33, 40, 64, 7, 2, 3, False),      # stem shape: K = 147 (gathered weights), odd sizes
+    (2, 3, 33, 40, 64, 7, 2, 3, False),      # stem shape: padded 8 x 8 x 4 taps, odd sizes
+    (3, 3, 30, 31, 64, 3, 1, 1, True),       # 3-channel 3 x 3 (4 x 4 x 4 taps), NCHW residual
     (3, 64, 14, 14, 256, 1, 1, 0, True),     # 1x1 expand + residual add + ReLU
     (2, 128, 15, 15, 128, 3, 2, 1, False),   # 3x3 stride 2
     (1, 256, 7, 9, 200, 1, 2, 0, False),     # strided 1x1 (downsample), Cout not a tile multiple
@@ -699,16 +700,20 @@ def test_conv_bn_act_vs_fp32_conv(backend, N, Cin, H, W, Cout, k, stride, pad, a
         ins["r"] = torch.randn(yshape, generator=g).half()
     got, ex = run_hip(ir, host(ins), host(w), backend)
     (prog,) = ex.npu_programs.values()
-    # an NCHW graph input takes conv.hip's kernel; a channels-last result (64-multiple channels) is
-    # copied to the NCHW graph output at the end
-    kernels = [s.kernel for s in prog.steps if s.kernel != "k_copy"]
-    assert [s.kind for s in prog.steps if s.kernel != "k_copy"] == ["conv"] * len(kernels)
-    assert kernels[0].startswith("k_conv_")
-    split = prog.steps[0].params["ksplit"] > 1   # split K: the reduce kernel applies the epilogue
-    assert kernels[1:] == (["k_conv_reduce_f16"] if split else [])
-    assert bool(prog.steps[0].args["flags"] & 16) == (Cout % 64 == 0 and not add and not split)
-    if Cin >= 128 and k == 3 or Cin >= 1024:
-        assert split
+    # an NCHW graph input takes conv.hip's kernel, or for at most 4 channels the MFMA GEMM over a
+    # zero-bordered NHWC copy; a channels-last result is copied to the NCHW graph output at the end
+    convs = [s for s in prog.steps if s.kind == "conv"]
+    kernels = [s.kernel for s in convs]
+    if Cin <= 4:
+        assert len(kernels) == 1 and kernels[0].startswith("k_gemm_f16_convp_m") and kernels[0].endswith("_k64d2")
+        assert [s.kernel for s in prog.steps[:2]] == ["k_permute_ohwi", "k_pad_nhwc4"]
+    else:
+        assert kernels[0].startswith("k_conv_")
+        split = convs[0].params["ksplit"] > 1   # split K: the reduce kernel applies the epilogue
+        assert kernels[1:] == (["k_conv_reduce_f16"] if split else [])
+        assert bool(convs[0].args["flags"] & 16) == (Cout % 64 == 0 and not add and not split)
+        if Cin >= 128 and k == 3 or Cin >= 1024:
+            assert split
     (name,) = got
     ref = run_cpu(ir, host(ins), host(w))
     close(got[name], ref[name])
