@@ -1092,7 +1092,7 @@ class Lowering:
             params={"M": M, "N": Cout, "K": K, "kernel": [KH, KW], "stride": st, "padding": pd,
                     "batch_norm": bn is not None, "residual": rv is not None, "relu": relu, "mfma": True,
                     "ksplit": 1, "nhwc": True, "tile": (bm, bn_), "lds_direct": True, "stages": "d2",
-                    "padded_taps": [khp, kwp, 4], "nodes": nodes or [conv.name]}))
+                    "padded_taps": [khp, kwp, 4], "K_alg": C * KH * KW, "nodes": nodes or [conv.name]}))
         self.views[out_name] = o
 
     def lower_conv2d(self, node: OpNode) -> None:
