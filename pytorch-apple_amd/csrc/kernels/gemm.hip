@@ -265,13 +265,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   // latency overlaps the operand loads instead of following the last MFMA
   constexpr bool HAS_R = EPI == GE_RESID || EPI == GE_CONV;
   const bool want_r = EPI == GE_RESID || (EPI == GE_CONV && (a.flags & 4));
-  uint32_t rr[HAS_R ? TJ : 1][HAS_R ? TI : 1][8];
+  // row-chunk epilogue through LDS (see below): 8 columns per 16-byte residual load and store
+  constexpr bool CAN_STAGE = NW == 1 && !GRP && BM * (BN + 8) + 4 * BN <= (DMA ? STAGES * SSTAGE : 2 * BM * LDK);
+  const bool staged = CAN_STAGE && a.ksplit == 1 && (a.N & 7) == 0 && (a.ldo & 7) == 0 &&
+                      (((size_t)a.out) & 15) == 0 && (!want_r || ((a.ldr & 7) == 0 && (((size_t)a.resid) & 15) == 0));
+  uint32_t rr[HAS_R && !CAN_STAGE ? TJ : 1][HAS_R && !CAN_STAGE ? TI : 1][8];
   auto load_resid = [&](const int j0, const int j1) {   // column groups [j0, j1)
 #pragma unroll
     for (int j = j0; j < j1; ++j) {
       const int n = min(n_base + wc * (BN / 2) + j * 32 + fr, a.N - 1);
 #pragma unroll
-      for (int i = 0; i < (HAS_R ? TI : 1); ++i)
+      for (int i = 0; i < (HAS_R && !CAN_STAGE ? TI : 1); ++i)
 #pragma unroll
         for (int e2 = 0; e2 < 8; ++e2) {
           uint32_t w = 0;
@@ -413,7 +417,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       }
     };
     constexpr int NI = NA + NB;   // vmcnt per stage
-    if (HAS_R && want_r && a.ksplit == 1) load_resid(0, TJ);   // issued first: the first stage's wait covers them
+    // (kernels with the row-chunk epilogue load their residuals there instead)
+    if constexpr (HAS_R && !CAN_STAGE)
+      if (want_r && a.ksplit == 1) load_resid(0, TJ);   // issued first: the first stage's wait covers them
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
       if (st < nsteps) issue(st);
@@ -444,9 +450,81 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       }
     return;
   }
+  // Row-chunk epilogue: the accumulators leave the MFMA layout (one column per lane, rows across
+  // registers) through LDS, so that residual loads and output stores are 16 bytes of 8 columns of
+  // one row each instead of 2-byte accesses spread over rows. round(acc + bias) is the first rounding
+  // point, so holding it as a 16-bit value in LDS changes nothing; batch norm factors are computed
+  // once per column. Residual chunks are loaded first, so their latency overlaps the LDS work.
+  if constexpr (CAN_STAGE) {
+    if (staged) {
+      constexpr int TLD = BN + 8;               // padded row: the two half-waves' writes miss each other's banks
+      constexpr int CH = BM * BN / 8 / 256;     // chunks per thread
+      uint16_t* T = DMA ? Ls : &As[0][0][0];
+      float* F = (float*)(T + BM * TLD);
+      uint4 rv[CH];
+      if (want_r) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const int idx = tid + 256 * k, r = idx / (BN / 8), q = idx - r * (BN / 8);
+          const long long m = min(m_base + r, a.M - 1);
+          const int n0 = min(n_base + q * 8, a.N - 8);
+          rv[k] = *(const uint4*)((const uint16_t*)a.resid + m * a.ldr + n0);
+        }
+      }
+      __syncthreads();   // every wave is done with the operand buffers
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int col = wc * (BN / 2) + j * 32 + fr, n = n_base + col;
+        const float b0 = ((a.flags & 1) && n < a.N) ? gm_ld<DT>(a.bias, n) : 0.f;
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            T[(wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3)) * TLD + col] =
+                gm_pack<DT>(acc[0][i][j][e] + b0);
+      }
+      if (EPI == GE_CONV && tid < BN && (a.flags & 2)) {
+        float al, be;
+        gm_bn_factors<DT>(a, min(n_base + tid, a.N - 1), al, be);
+        F[tid] = al;
+        F[BN + tid] = be;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const int idx = tid + 256 * k, r = idx / (BN / 8), q = idx - r * (BN / 8);
+        const long long m = m_base + r;
+        const int n0 = n_base + q * 8;
+        if (m >= a.M || n0 >= a.N) continue;
+        const uint4 tv = *(const uint4*)&T[r * TLD + q * 8];
+        const uint32_t tw[4] = {tv.x, tv.y, tv.z, tv.w}, rw[4] = {rv[k].x, rv[k].y, rv[k].z, rv[k].w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int c2 = 0; c2 < 4; ++c2) {
+          uint32_t o = 0;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int c = 2 * c2 + h;
+            const uint16_t tb = (uint16_t)(tw[c2] >> (16 * h));
+            float v = DT == HS_BF16 ? bf16_to_f32(tb) : f16_to_f32(tb);
+            const uint16_t rb = want_r ? (uint16_t)(rw[c2] >> (16 * h)) : (uint16_t)0;
+            if constexpr (EPI == GE_RESID) v = gm_round<DT>((DT == HS_BF16 ? bf16_to_f32(rb) : f16_to_f32(rb)) + v);
+            if constexpr (EPI == GE_CONV) {
+              const float al = (a.flags & 2) ? F[q * 8 + c] : 1.f, be = (a.flags & 2) ? F[BN + q * 8 + c] : 0.f;
+              v = gm_conv_tail<DT>(a, v, al, be, rb);
+            }
+            o |= (uint32_t)gm_pack<DT>(v) << (16 * h);
+          }
+          ow[c2] = o;
+        }
+        *(uint4*)(OUT + m * a.ldo + n0) = make_uint4(ow[0], ow[1], ow[2], ow[3]);
+      }
+      return;
+    }
+  }
   // epilogue (register staging: one column group's residuals at a time, which keeps the epilogue
   // under the main loop's register count)
-  if constexpr (HAS_R) {
+  if constexpr (HAS_R && !CAN_STAGE) {
     if (!want_r) {
 #pragma unroll
       for (int j = 0; j < TJ; ++j)
@@ -458,7 +536,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   }
 #pragma unroll
   for (int j = 0; j < TJ; ++j) {
-    if constexpr (HAS_R && !DMA)
+    if constexpr (HAS_R && !CAN_STAGE)
       if (want_r) load_resid(j, j + 1);
     const int n = n_base + wc * (BN / 2) + j * 32 + fr;
     if (n >= a.N) continue;
@@ -473,7 +551,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (m >= a.M) continue;
         float v = gm_round<DT>(acc[0][i][j][e] + b0);
-        const uint16_t r16 = HAS_R ? (uint16_t)(rr[HAS_R ? j : 0][HAS_R ? i : 0][e >> 1] >> (16 * (e & 1))) : 0;
+        // (kernels with the row-chunk epilogue come here only for odd shapes: plain loads, fewer registers)
+        uint16_t r16 = 0;
+        if constexpr (HAS_R && CAN_STAGE) {
+          if (want_r) r16 = ((const uint16_t*)a.resid)[m * a.ldr + n];
+        } else if constexpr (HAS_R) {
+          r16 = (uint16_t)(rr[j][i][e >> 1] >> (16 * (e & 1)));
+        }
         if constexpr (EPI == GE_RESID) v = gm_round<DT>((DT == HS_BF16 ? bf16_to_f32(r16) : f16_to_f32(r16)) + v);
         if constexpr (EPI == GE_CONV) v = gm_conv_tail<DT>(a, v, al, be, r16);
         if constexpr (EPI == GE_SILU) {
