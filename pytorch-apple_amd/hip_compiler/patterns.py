@@ -121,12 +121,16 @@ def rmsnorm(low) -> None:
             cols = xv.shape[-1]
             rows = xv.numel // cols
             o = low.new_storage(out.name, out.shape, out.dtype)
+            # one wave per row with 16-byte accesses for 16-bit rows that fit (k_rmsnorm_w)
+            half = ("bfloat16", "float16")
+            wave = (xv.dtype in half and wv.dtype == xv.dtype and out.dtype in half and cols % 8 == 0
+                    and cols <= 4096 and (xv.offset * 2) % 16 == 0 and (wv.offset * 2) % 16 == 0)
             low.emit(LaunchStep(
-                kind="rmsnorm", kernel="k_rmsnorm", module="basic", arg_struct="RMSNormArgs",
+                kind="rmsnorm", kernel="k_rmsnorm_w" if wave else "k_rmsnorm", module="basic", arg_struct="RMSNormArgs",
                 args=dict(x=low.ref(xv), w=low.ref(wv), out=low.ref(o), rows=rows, ldx=cols, ldo=cols, cols=cols,
                           eps=eps, x_dtype=DTYPE_CODE[xv.dtype], w_dtype=DTYPE_CODE[wv.dtype],
                           n_dtype=DTYPE_CODE[n_dtype], out_dtype=DTYPE_CODE[out.dtype]),
-                grid=(max(rows, 1), 1, 1), inputs=[x.name, w.name], outputs=[out.name],
+                grid=(max((rows + 3) // 4 if wave else rows, 1), 1, 1), inputs=[x.name, w.name], outputs=[out.name],
                 params={"rows": rows, "cols": cols, "eps": eps, "nodes": names}))
             low.views[out.name] = o
 

@@ -35,7 +35,7 @@ def test_mlp_block_fused_and_generic_step_lists():
 def test_prefill_mlp_is_norm_plus_two_mfma_gemms():
     p = compile_subgraph(build_mlp_ir(512))
     main = [s for s in p.steps if s.kind == "gemm" and not s.params.get("reduce")]
-    assert kernels(p)[0] == "k_rmsnorm" and abs(p.steps[0].args["eps"] - 1e-6) < 1e-12
+    assert kernels(p)[0] == "k_rmsnorm_w" and abs(p.steps[0].args["eps"] - 1e-6) < 1e-12   # wave per row
     assert [s.params["epilogue"] for s in main] == ["silu", "resid"]
     assert main[0].params["weights"] == 2 and main[0].args["w2"] is not None
     # K % 64 == 0 and a tile grid below 1024: operands staged straight into LDS (the _k64d kernels)
@@ -99,7 +99,7 @@ def test_decode_step_launch_count_and_cache_aliasing():
     assert len(p.steps) == 1 + 5 * cfg.layers + 2      # embedding, 5 per layer, lm_head+argmax, finalize
     assert kernels(p)[0] == "k_embedding" and kernels(p)[-2:] == ["k_gemv_norm_argmax_r4", "k_argmax_finalize"]
     assert len(p.stats["mutated_inputs"]) == 2 * cfg.layers
-    assert not any(s.kernel in ("k_rope_table", "k_rmsnorm", "k_copy") for s in p.steps)
+    assert not any(s.kernel in ("k_rope_table", "k_rmsnorm", "k_rmsnorm_w", "k_copy") for s in p.steps)
 
 
 def test_not_inplace_when_cache_input_has_another_reader():
