@@ -259,7 +259,9 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
       L = fmaf(f, lsh[w], L);
     }
     const long long part = (long long)(kvh * a.nsplit + split) * G + g;
-    a.part_o[part * AT_D + dd] = o;
+    // the split's own normalised output in bf16 (half the bytes for the combine to read; its
+    // weight e^(m - M) l is applied there): 2^-9 relative, below the output's own bf16 rounding
+    a.part_o[part * AT_D + dd] = f32_to_bf16(L > 0.f ? o / L : 0.f);
     if (dd == 0) {
       a.part_ml[part * 2] = M;
       a.part_ml[part * 2 + 1] = L;
@@ -276,7 +278,8 @@ extern "C" __global__ void __launch_bounds__(512) k_attn_flash_w8_f16(const Flas
 extern "C" __global__ void __launch_bounds__(1024) k_attn_flash_w16(const FlashArgs a) { flash_body<HS_BF16, 16>(a); }
 extern "C" __global__ void __launch_bounds__(1024) k_attn_flash_w16_f16(const FlashArgs a) { flash_body<HS_F16, 16>(a); }
 
-// out[h, d] = round(sum_t e^(m_t - M) o_t[d] / sum_t e^(m_t - M) l_t); one workgroup of 128
+// out[h, d] = round(sum_t e^(m_t - M) l_t o_t[d] / sum_t e^(m_t - M) l_t) over the splits' normalised
+// outputs o_t (bf16); one workgroup of 128
 // threads per head. Splits are folded in chunks of 64: lane t of every wave loads split t's
 // (m, l), so each wave forms the chunk's weights itself (no LDS, no barrier) and thread d
 // takes them with readlane while its 64 partial loads are already in flight.
@@ -286,13 +289,13 @@ extern "C" __global__ void __launch_bounds__(128) k_attn_combine(const CombineAr
   const int G = a.H / a.KVH, kvh = h / G, g = h % G;
   const int d = threadIdx.x, lane = threadIdx.x & 63;
   const float* ml = a.part_ml + ((long long)kvh * a.nsplit * G + g) * 2;
-  const float* po = a.part_o + ((long long)kvh * a.nsplit * G + g) * AT_D + d;
+  const uint16_t* po = a.part_o + ((long long)kvh * a.nsplit * G + g) * AT_D + d;
   float M = -INFINITY, L = 0.f, acc = 0.f;
   for (int c0 = 0; c0 < a.nsplit; c0 += CB_CHUNK) {
     const int n = min(CB_CHUNK, a.nsplit - c0);
     float ot[CB_CHUNK];
 #pragma unroll
-    for (int i = 0; i < CB_CHUNK; ++i) ot[i] = po[(long long)(c0 + min(i, n - 1)) * G * AT_D];
+    for (int i = 0; i < CB_CHUNK; ++i) ot[i] = bf16_to_f32(po[(long long)(c0 + min(i, n - 1)) * G * AT_D]);
     float m = -INFINITY, l = 0.f;
     if (lane < n) {
       m = ml[(long long)(c0 + lane) * G * 2];
@@ -303,13 +306,14 @@ extern "C" __global__ void __launch_bounds__(128) k_attn_combine(const CombineAr
     const float r = (M == -INFINITY) ? 0.f : __expf(M - Mn);
     const float f = (m == -INFINITY) ? 0.f : __expf(m - Mn);
     L = L * r + wave_sum(f * l);
+    const float fl = f * l;   // the weight of split lane's normalised output
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
     for (int i = 0; i < CB_CHUNK; i += 4) {
-      if (i < n) s0 = fmaf(HS_RL(f, i), ot[i], s0);
-      if (i + 1 < n) s1 = fmaf(HS_RL(f, i + 1), ot[i + 1], s1);
-      if (i + 2 < n) s2 = fmaf(HS_RL(f, i + 2), ot[i + 2], s2);
-      if (i + 3 < n) s3 = fmaf(HS_RL(f, i + 3), ot[i + 3], s3);
+      if (i < n) s0 = fmaf(HS_RL(fl, i), ot[i], s0);
+      if (i + 1 < n) s1 = fmaf(HS_RL(fl, i + 1), ot[i + 1], s1);
+      if (i + 2 < n) s2 = fmaf(HS_RL(fl, i + 2), ot[i + 2], s2);
+      if (i + 3 < n) s3 = fmaf(HS_RL(fl, i + 3), ot[i + 3], s3);
     }
     acc = acc * r + ((s0 + s1) + (s2 + s3));
     M = Mn;

@@ -320,7 +320,7 @@ struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm,
   const void* bias2;          // [N] or null
   const void* norm_w;         // [K] RMSNorm weight (NORM)
   unsigned long long* argmax_slot;  // [M, grid.x] packed (value, ~index) keys per workgroup (ARGMAX)
-  const float* attn_o;        // ATTN prologue: split partials of the decode attention feeding x
+  const uint16_t* attn_o;     // ATTN prologue: split partials (bf16, normalised) of the decode attention feeding x
   const float* attn_ml;
   long long M;
   long long ldx;
@@ -428,7 +428,7 @@ struct FlashArgs {            // split-S decode attention: per-split (max, sum, 
   const void* k;              // [KVH, S, D]
   const void* v;              // [KVH, S, D]
   const void* mask;           // [S] (stride mask_stride), broadcast over heads
-  float* part_o;              // [KVH, nsplit, G, D] sum_s exp(s - m) v_s over the split
+  uint16_t* part_o;           // [KVH, nsplit, G, D] bf16 of the split's own softmax . V: sum_s e^(s - m) v_s / l
   float* part_ml;             // [KVH, nsplit, G, 2] (m, l) of the split; l = 0 when fully masked
   long long S;
   long long q_head_stride;
@@ -464,8 +464,8 @@ struct PrefillAttnArgs {      // causal / masked attention of T queries over S k
   int dtype;                  // bf16 or fp16
 };
 
-struct CombineArgs {          // out[h, d] = round(sum_t e^(m_t - M) o_t[d] / sum_t e^(m_t - M) l_t)
-  const float* part_o;
+struct CombineArgs {          // out[h, d] = round(sum_t e^(m_t - M) l_t o_t[d] / sum_t e^(m_t - M) l_t), o_t normalised
+  const uint16_t* part_o;     // bf16 [KVH, nsplit, G, D]
   const float* part_ml;
   void* out;                  // [H, D]
   int H;

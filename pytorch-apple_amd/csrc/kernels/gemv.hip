@@ -143,7 +143,8 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int n) {
 // At most T splits (8 or 16) and 16 heads (checked on the host).
 template <int T>
 struct AttnPre {
-  float o0[4][T], o1[4][T], m[4], l[4];
+  uint32_t o[4][T];   // dims 2 lane, 2 lane + 1 of head j, split t (bf16 pair)
+  float m[4], l[4];
 };
 
 template <int T>
@@ -154,13 +155,10 @@ __device__ __forceinline__ void attn_fetch(const GemvArgs& a, AttnPre<T>& p) {
   for (int j = 0; j < 4; ++j) {
     if (wave + 4 * j >= H) break;   // wave-uniform
     const int h = wave + 4 * j, kvh = h / G, g = h % G;
-    const float* po = a.attn_o + ((long long)kvh * NT * G + g) * 128 + lane;
+    const uint32_t* po = (const uint32_t*)(a.attn_o + ((long long)kvh * NT * G + g) * 128) + lane;
 #pragma unroll
-    for (int t = 0; t < T; ++t) {   // splits past NT repeat the last one (weight 0 below)
-      const long long off = (long long)min(t, NT - 1) * G * 128;
-      p.o0[j][t] = po[off];
-      p.o1[j][t] = po[off + 64];
-    }
+    for (int t = 0; t < T; ++t)   // splits past NT repeat the last one (weight 0 below)
+      p.o[j][t] = po[(long long)min(t, NT - 1) * G * 64];
     const float* ml = a.attn_ml + (((long long)kvh * NT + min(lane, NT - 1)) * G + g) * 2;
     p.m[j] = ml[0];
     p.l[j] = ml[1];
@@ -178,16 +176,16 @@ __device__ __forceinline__ void attn_finish(const GemvArgs& a, const AttnPre<T>&
     const float mj = (lane < NT && p.l[j] > 0.f) ? p.m[j] : -INFINITY;   // dead splits weigh 0
     const float M = wave_max(mj);
     const float f = (mj == -INFINITY) ? 0.f : __expf(mj - M);
-    const float L = wave_sum(f * p.l[j]);
+    const float fl = f * p.l[j];   // weight of split lane's normalised output
+    const float L = wave_sum(fl);
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const float ft = HS_RL(f, t);
-      s0 = fmaf(ft, p.o0[j][t], s0);
-      s1 = fmaf(ft, p.o1[j][t], s1);
+      const float ft = HS_RL(fl, t);
+      s0 = fmaf(ft, bf16_to_f32((uint16_t)(p.o[j][t] & 0xffffu)), s0);
+      s1 = fmaf(ft, bf16_to_f32((uint16_t)(p.o[j][t] >> 16)), s1);
     }
-    xs[h * 128 + lane] = f32_to_bf16(s0 / L);
-    xs[h * 128 + 64 + lane] = f32_to_bf16(s1 / L);
+    *(uint32_t*)&xs[h * 128 + 2 * lane] = f32_to_bf16(s0 / L) | ((uint32_t)f32_to_bf16(s1 / L) << 16);
   }
   __syncthreads();
 }

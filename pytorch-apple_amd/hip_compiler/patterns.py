@@ -356,7 +356,7 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     if mask is not None:
         mv = low.view(mask)
         margs = dict(mask=low.ref(mv), mask_stride=mv.strides[-1], mask_dtype=DTYPE_CODE[mv.dtype])
-    part_o = low.scratch(out.name + ".part_o", kvh * nsplit * G * D * 4)
+    part_o = low.scratch(out.name + ".part_o", kvh * nsplit * G * D * 2)   # bf16, normalised per split
     part_ml = low.scratch(out.name + ".part_ml", kvh * nsplit * G * 2 * 4)
     args = dict(q=low.ref(qv), k=low.ref(kv_), v=low.ref(vv_), part_o=part_o, part_ml=part_ml, S=S,
                 q_head_stride=qv.strides[1], kv_head_stride=kv_.strides[1], H=H, KVH=kvh, nsplit=nsplit, spl=spl,
