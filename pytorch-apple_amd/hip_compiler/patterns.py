@@ -666,7 +666,7 @@ def qkv_rope(low) -> None:
         if not (q["D"] == k["D"] == v["D"] and k["nh"] == v["nh"] and q["rope"] is k["rope"]
                 and k["cpos"] == v["cpos"] and q["nh"] % k["nh"] == 0):
             continue
-        if len({q["b"] is None, k["b"] is None, v["b"] is None}) != 1:
+        if len({q["b"] is None, k["b"] is None, v["b"] is None}) != 1 or not _rope_inputs_ok(q["rope"], 1):
             continue
         K = q["w"].shape[1]
         if K > 3072 or any(e["w"].shape != [e["nh"] * e["D"], K] for e in (q, k, v)):
@@ -681,6 +681,16 @@ def qkv_rope(low) -> None:
             _emit_qkv(low, xname, q, k, v, names)
 
         cx.claim(nodes, emit)
+
+
+def _rope_inputs_ok(rnode, n_pos: int) -> bool:
+    """The fused RoPE kernels compute cos / sin from an fp32 ``inv_freq`` and one
+    position per token; anything else stays on the unfused lowering."""
+    inv, pos = rnode.inputs[0], rnode.inputs[1]
+    n = 1
+    for d in pos.shape:
+        n *= int(d)
+    return inv.dtype == "float32" and n == n_pos
 
 
 def _emit_qkv(low, xname, q, k, v, names) -> None:
@@ -805,7 +815,7 @@ def qkv_rope_prefill(low) -> None:
         if not (q["D"] == k["D"] == v["D"] and q["T"] == k["T"] == v["T"] and k["nh"] == v["nh"]
                 and q["rope"] is k["rope"] and k["cpos"] == v["cpos"] and q["nh"] % k["nh"] == 0):
             continue
-        if len({q["b"] is None, k["b"] is None, v["b"] is None}) != 1:
+        if len({q["b"] is None, k["b"] is None, v["b"] is None}) != 1 or not _rope_inputs_ok(q["rope"], q["T"]):
             continue
         K = q["w"].shape[1]
         if K % 32 or any(e["w"].shape != [e["nh"] * e["D"], K] for e in (q, k, v)):

@@ -21,6 +21,8 @@ grows elementwise chains — with MI355X-specific choices:
 
 from __future__ import annotations
 
+import dataclasses
+
 import math
 import os
 from dataclasses import dataclass, field
@@ -154,11 +156,32 @@ class _Chain:
     dtype: str = "float32"
 
 
+_RENAMES = ("aten.alias.default", "aten.detach.default")
+
+
+def drop_renames(graph: IRGraph) -> IRGraph:
+    """``graph`` without ``alias`` / ``detach`` nodes: their readers read the source tensor
+    itself. They only rename a value, but a rename between two ops hides one from a
+    fusion pattern (transformers 5 places an ``alias`` between the final RMSNorm and the
+    lm_head). A node whose output is a graph output stays."""
+    outs = {o.name for o in graph.graph_outputs}
+    src: dict[str, object] = {}
+    nodes = []
+    for n in graph.nodes:
+        ins = [src.get(t.name, t) for t in n.inputs]
+        if n.op_type in _RENAMES and ins and n.outputs[0].name not in outs:
+            src[n.outputs[0].name] = ins[0]
+            continue
+        nodes.append(n if not src else dataclasses.replace(n, inputs=ins))
+    return dataclasses.replace(graph, nodes=nodes) if src else graph
+
+
 class Lowering:
     """Lowers one IR graph; ``steps``, ``storages`` and ``views`` are the result."""
 
     def __init__(self, graph: IRGraph, inplace_inputs: bool = True, exact_attention: bool = False,
                  fold_attention: bool | None = None):
+        graph = drop_renames(graph)
         self.g = graph
         self.inplace_inputs = inplace_inputs
         self.exact_attention = exact_attention
@@ -1255,8 +1278,10 @@ class Lowering:
         cos_s, sin_s = node.outputs[0], node.outputs[1]
         inv = self.contiguous(inv_t.name)
         pos = self.contiguous(pos_t.name)
-        if inv.dtype != "float32":
-            raise NotImplementedError("rotary inv_freq must be float32")
+        if inv.dtype != "float32":   # HF upcasts: inv_freq[None, :, None].float()
+            f32 = self.new_storage(inv_t.name + ".f32", inv.shape, "float32")
+            self.emit_copy(inv, f32, [inv_t.name], [inv_t.name + ".f32"])
+            inv = f32
         half = inv.numel
         S = pos.numel
         c = self.new_storage(cos_s.name, cos_s.shape, cos_s.dtype)

@@ -1,0 +1,165 @@
+"""HF Qwen2 → exported IR → HIP path, on the GPU.
+
+The model is this image's transformers ``Qwen2ForCausalLM`` (random init, eager
+attention), exported with ``irgen.hf_qwen.export_qwen``, saved as safetensors and
+loaded straight into device memory by ``npu_runtime.hf_weights``. The reference for
+every comparison is HF's own eager forward on the CPU (ATen bf16). Tolerances:
+rtol 2e-2 of the output's largest magnitude for floating point, bit-exact for cache
+rows the step does not write, and the next token equal to HF's argmax unless HF's
+top two logits are within that tolerance (a near tie).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import gpu_available
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+transformers = pytest.importorskip("transformers")
+
+RTOL = 2e-2
+S = 256
+
+
+def tiny_model(layers=2, seed=0):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from irgen.hf_qwen import to_dtype_keep_rotary
+
+    cfg = Qwen2Config(hidden_size=1536, intermediate_size=8960, num_hidden_layers=layers, num_attention_heads=12,
+                      num_key_value_heads=2, head_dim=128, vocab_size=8192, rope_theta=1e6,
+                      tie_word_embeddings=True, rms_norm_eps=1e-6, max_position_embeddings=4096)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(seed)
+    m = Qwen2ForCausalLM(cfg).eval()
+    with torch.no_grad():   # HF's init gives near-constant logits at this size; widen them
+        m.model.embed_tokens.weight.normal_(0, 0.5)
+    return to_dtype_keep_rotary(m)
+
+
+@pytest.fixture(scope="module")
+def hf(tmp_path_factory):
+    m = tiny_model()
+    d = tmp_path_factory.mktemp("qwen2")
+    m.save_pretrained(str(d), safe_serialization=True)
+    return m, str(d)
+
+
+def hip_executor(ir, model_dir, backend):
+    from hip_compiler import compile_subgraph, is_hip_op_supported
+    from npu_compiler import partition
+    from npu_runtime import DAGExecutor
+    from npu_runtime.hf_weights import load_safetensors_weights
+
+    plan = partition(ir, is_hip_op_supported)
+    assert [p.target for p in plan.steps] == ["npu"], "the exported graph must run as one device partition"
+    ex = DAGExecutor(plan, backend, compile_fn=compile_subgraph)
+    ex.load_weights(load_safetensors_weights(model_dir, ir, device="cuda"))
+    return ex
+
+
+def f32(t):
+    return t.float().cpu()
+
+
+def close(got, ref, rtol=RTOL):
+    g, r = f32(got), f32(ref)
+    assert g.shape == r.shape
+    err = (g - r).abs().max().item()
+    scale = max(r.abs().max().item(), 1e-6)
+    assert err <= rtol * scale, f"max abs err {err} vs scale {scale}"
+    return err / scale
+
+
+def token_ok(tok, logits_row):
+    r = logits_row.float()
+    best = r.max().item()
+    return int(tok) == int(r.argmax()) or r[int(tok)].item() >= best - RTOL * r.abs().max().item()
+
+
+def test_exported_decode_step_on_hip_matches_hf(hf, backend):
+    from irgen.hf_qwen import QwenStaticWrapper, export_qwen
+
+    m, d = hf
+    ir = export_qwen(m, S, tokens=1, argmax=True)
+    ex = hip_executor(ir, d, backend)
+    pos = 200
+    g = torch.Generator().manual_seed(1)
+    kv = [torch.randn(1, 2, S, 128, generator=g).to(torch.bfloat16) for _ in range(4)]
+    mask = torch.zeros(1, 1, 1, S, dtype=torch.bfloat16)
+    mask[..., pos + 1:] = float("-inf")
+    args = (torch.tensor([[4321]]), mask, torch.tensor([[pos]]), torch.tensor([pos]), *kv)
+    with torch.no_grad():
+        ref = QwenStaticWrapper(m, 2, argmax=True)(*args)
+    print(f"[case] exported decode, S={S}, pos={pos}", flush=True)
+    out = ex.execute({s["name"]: backend.allocate_buffer(a.clone()) for s, a in zip(ir["graph_inputs"], args)})
+    names = [o["name"] for o in ir["graph_outputs"]]
+    logits = out[names[0]].to_torch()
+    close(logits, ref[0])
+    assert token_ok(out[names[-1]].to_torch().reshape(-1)[0].item(), ref[0].reshape(-1))
+    for name, r in zip(names[1:-1], ref[1:-1]):
+        got = f32(out[name].to_torch())
+        rr = f32(r)
+        keep = torch.ones(S, dtype=torch.bool)
+        keep[pos] = False
+        assert torch.equal(got[:, :, keep], rr[:, :, keep]), name
+        close(got[:, :, pos], rr[:, :, pos])
+
+
+def test_exported_prefill_on_hip_matches_hf(hf, backend):
+    from irgen.hf_qwen import QwenStaticWrapper, export_qwen
+
+    m, d = hf
+    T = 64
+    ir = export_qwen(m, S, tokens=T, argmax=True)
+    ex = hip_executor(ir, d, backend)
+    g = torch.Generator().manual_seed(2)
+    mask = torch.full((T, S), float("-inf"))
+    mask[:, :T] = torch.triu(torch.full((T, T), float("-inf")), diagonal=1)
+    ar = torch.arange(T)
+    kv = [torch.zeros(1, 2, S, 128, dtype=torch.bfloat16) for _ in range(4)]
+    args = (torch.randint(0, 8192, (1, T), generator=g), mask.to(torch.bfloat16).reshape(1, 1, T, S),
+            ar.reshape(1, T), ar, *kv)
+    with torch.no_grad():
+        ref = QwenStaticWrapper(m, 2, argmax=True)(*args)
+    print(f"[case] exported prefill, T={T}, S={S}", flush=True)
+    out = ex.execute({s["name"]: backend.allocate_buffer(a.clone()) for s, a in zip(ir["graph_inputs"], args)})
+    names = [o["name"] for o in ir["graph_outputs"]]
+    close(out[names[0]].to_torch(), ref[0])
+    toks = out[names[-1]].to_torch().reshape(-1).cpu()
+    rl = ref[0].reshape(T, -1)
+    assert all(token_ok(toks[i], rl[i]) for i in range(T))
+    for name, r in zip(names[1:-1], ref[1:-1]):
+        got = f32(out[name].to_torch())
+        close(got[:, :, :T], f32(r)[:, :, :T])
+        assert got[:, :, T:].eq(0).all()
+
+
+def test_generation_on_hip_follows_hf_teacher_forced(hf, backend):
+    """Padded 32-token prefill graph, a 23-token prompt, then 12 device-resident decode
+    steps. Every generated token must be HF's argmax (or a near tie) given the tokens
+    before it, from one uncached HF forward over the whole sequence."""
+    from irgen.hf_qwen import export_qwen, kv_mapping
+    from npu_runtime.generation import GreedyGenerator
+
+    m, d = hf
+    T = 32
+    pre = export_qwen(m, S, tokens=T, argmax=True)
+    dec = export_qwen(m, S, tokens=1, argmax=True)
+    gen = GreedyGenerator(hip_executor(pre, d, backend), hip_executor(dec, d, backend),
+                          kv_mapping(pre, dec, 2, T, S), pre, dec, backend=backend)
+    prompt = [int(t) for t in torch.randint(0, 8192, (23,), generator=torch.Generator().manual_seed(7))]
+    print("[case] generation, prompt 23 / prefill 32 / 13 tokens", flush=True)
+    res = gen.generate(prompt, 13)
+    assert len(res.tokens) == 13
+    seq = torch.tensor([prompt + res.tokens[:-1]])
+    with torch.no_grad():
+        logits = m(seq).logits[0]
+    for i, tok in enumerate(res.tokens):
+        assert token_ok(tok, logits[len(prompt) - 1 + i]), f"step {i}: token {tok}"
+    again = gen.generate(prompt, 13)        # caches are fresh per call: same tokens
+    assert again.tokens == res.tokens
+    eos = res.tokens[5]
+    cut = gen.generate(prompt, 13, eos_token_id=eos)
+    assert cut.tokens == res.tokens[:res.tokens.index(eos)]
