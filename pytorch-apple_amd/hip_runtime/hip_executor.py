@@ -5,9 +5,13 @@ Init-time work: load code objects (AOT ``.hsaco`` and hiprtc-compiled chains),
 allocate the arena (zero-filled once), pack every step's argument struct with
 concrete arena pointers, and record where external buffers (graph inputs and
 weights) must be patched in. ``run()`` resolves the external pointers; when they
-are the same as in the previous call the captured HIP graph is relaunched as-is
+match a set seen before, the HIP graph captured for that set is relaunched as-is
 (one host call per step, instead of the reference's one Python dispatch per IR
-step), otherwise the affected kernargs are re-packed and the graph re-captured.
+step); a new set re-packs the affected kernargs and captures one more graph. Up to
+``MAX_GRAPHS`` graphs are kept, least recently used first out, so a loop whose
+first step reads one buffer and whose later steps read another (a decode loop
+feeding its own argmax back as ``input_ids``) captures twice in total, not twice
+per run. A captured graph holds its own copy of the kernel arguments.
 
 Returned outputs alias executor-owned storage and stay valid until the next
 ``run()``, as in the reference (`cuda_executor.py:153-176`); outputs that are
@@ -18,6 +22,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+from collections import OrderedDict
 
 import torch
 
@@ -27,6 +32,7 @@ from hip_runtime.hip_backend import _TORCH_OF_IR, HIPBuffer
 from hip_runtime.kernels import STRUCTS, ModuleCache
 
 _MODULES: dict[int, ModuleCache] = {}
+MAX_GRAPHS = 8
 
 
 def module_cache(device_index: int) -> ModuleCache:
@@ -77,8 +83,8 @@ class HIPExecutor:
             r.kernarg_size = C.sizeof(s)
             r.kernarg = C.addressof(s)
         self._n = n
-        self._ext_key: tuple | None = None
-        self._graph = None
+        self._ext_key: tuple | None = None        # external pointers packed into the kernargs now
+        self._graphs: OrderedDict[tuple, int] = OrderedDict()   # pointer set -> captured graph
         self._capture_stream = None
         self._out_cache: dict[str, HIPBuffer] = {}
         for spec in program.output_specs:
@@ -143,29 +149,32 @@ class HIPExecutor:
         """Enqueue the whole program on ``stream`` (default: torch's current stream)."""
         ptrs = self._resolve(inputs, weights)
         key = tuple(ptrs[n] for n in self._ext_names)
-        if key != self._ext_key:
-            self._patch(ptrs)
-            self._ext_key = key
-            if self._graph is not None:
-                _shim.check(_shim.lib().hs_graph_destroy(self._graph), "graph destroy")
-                self._graph = None
         if stream is None:
             stream = torch.cuda.current_stream(self.device).cuda_stream
         if self._n == 0:
             return
-        if self.use_graph:
-            if self._graph is None:
-                if self._capture_stream is None:
-                    cs = C.c_void_p()
-                    _shim.check(_shim.lib().hs_stream_create(C.byref(cs)), "stream create")
-                    self._capture_stream = cs.value
-                g = C.c_void_p()
-                _shim.check(_shim.lib().hs_graph_capture(self._recs, self._n, self._capture_stream, C.byref(g)),
-                            "graph capture")
-                self._graph = g.value
-            _shim.check(_shim.lib().hs_graph_launch(self._graph, stream), "graph launch")
+        lib = _shim.lib()
+        graph = self._graphs.get(key) if self.use_graph else None
+        if graph is not None:
+            self._graphs.move_to_end(key)
         else:
-            _shim.check(_shim.lib().hs_replay(self._recs, self._n, stream), "replay")
+            if key != self._ext_key:
+                self._patch(ptrs)
+                self._ext_key = key
+            if not self.use_graph:
+                _shim.check(lib.hs_replay(self._recs, self._n, stream), "replay")
+                return
+            if self._capture_stream is None:
+                cs = C.c_void_p()
+                _shim.check(lib.hs_stream_create(C.byref(cs)), "stream create")
+                self._capture_stream = cs.value
+            g = C.c_void_p()
+            _shim.check(lib.hs_graph_capture(self._recs, self._n, self._capture_stream, C.byref(g)), "graph capture")
+            graph = self._graphs[key] = g.value
+            while len(self._graphs) > MAX_GRAPHS:
+                _, old = self._graphs.popitem(last=False)
+                _shim.check(lib.hs_graph_destroy(old), "graph destroy")
+        _shim.check(lib.hs_graph_launch(graph, stream), "graph launch")
 
     def run(self, inputs: dict, weights: dict) -> dict[str, HIPBuffer]:
         self.launch(inputs, weights)
@@ -186,8 +195,9 @@ class HIPExecutor:
     def __del__(self):
         try:
             lib = _shim.lib()
-            if self._graph is not None:
-                lib.hs_graph_destroy(self._graph)
+            for g in self._graphs.values():
+                lib.hs_graph_destroy(g)
+            self._graphs.clear()
             if self._capture_stream is not None:
                 lib.hs_stream_destroy(self._capture_stream)
         except Exception:

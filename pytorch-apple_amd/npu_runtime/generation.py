@@ -23,6 +23,9 @@ What differs:
   whose buffers are torch tensors, the mask and positions are advanced in place on
   the device, so a decode step needs no host round trip unless ``eos_token_id`` is
   given (then each token is read back to test it, as the reference does);
+* on such a backend the caches and the per-step inputs are allocated once per
+  generator and rewritten in place by each call (caches zeroed), so every call
+  hands the executors the same buffers and their captured HIP graphs are reused;
 * masked entries hold the dtype's lowest finite value (the reference's fp16 -65504):
   a padding row closed on every column then has a finite softmax, and no NaN can
   reach a cache row that a later step opens.
@@ -110,6 +113,7 @@ class GreedyGenerator:
         self.p_cache_of = {d["name"]: p for d, p in zip(self.cache_specs, p_caches)}
         if any(_spec(prefill_ir, p)["shape"][-2] != self.S for p in p_caches):
             raise ValueError("prefill caches must be the decode graph's static caches")
+        self._bufs: dict | None = None
 
     # -- buffers ---------------------------------------------------------------------------
 
@@ -123,6 +127,18 @@ class GreedyGenerator:
 
     def _put(self, arr: np.ndarray):
         return self.backend.allocate_buffer(arr) if self._on_device() else arr
+
+    def _device_buffers(self) -> dict:
+        """Caches and step inputs, allocated on the first call and reused by every later one."""
+        if self._bufs is None:
+            T, S, dt = self.T, self.S, self.mask_dtype
+            b = {d["name"]: self._zeros(d) for d in self.cache_specs}
+            b.update(p_ids=self._put(np.zeros((1, T), np.int64)), p_mask=self._put(prefill_mask(T, S, T, dt)),
+                     p_pos=self._put(np.zeros((1, T), np.int64)), p_cpos=self._put(np.zeros(T, np.int64)),
+                     d_ids=self._put(np.zeros((1, 1), np.int64)), d_mask=self._put(decode_mask(S, 0, dt)),
+                     d_pos=self._put(np.zeros((1, 1), np.int64)), d_cpos=self._put(np.zeros(1, np.int64)))
+            self._bufs = b
+        return self._bufs
 
     def _token_host(self, val, index: int) -> int:
         if hasattr(val, "to_numpy"):
@@ -145,12 +161,26 @@ class GreedyGenerator:
             raise ValueError(f"prompt length {n} must be in 1..{self.T}")
         if max_tokens < 1 or n + max_tokens - 1 > self.S:
             raise ValueError(f"{n} prompt tokens + {max_tokens - 1} decode steps exceed the cache ({self.S})")
-        ids = np.zeros((1, self.T), np.int64)
+        T, S, dt = self.T, self.S, self.mask_dtype
+        ids = np.zeros((1, T), np.int64)
         ids[0, :n] = np.asarray(prompt_ids, np.int64)
-        ar = np.arange(self.T, dtype=np.int64)
-        caches = {d["name"]: self._zeros(d) for d in self.cache_specs}
-        pin = {"input_ids": self._put(ids), "attention_mask": self._put(prefill_mask(self.T, self.S, n, self.mask_dtype)),
-               "position_ids": self._put(ar.reshape(1, -1)), "cache_position": self._put(ar)}
+        ar = np.arange(T, dtype=np.int64)
+        dev = self._on_device()
+        if dev:
+            b = self._device_buffers()
+            for d in self.cache_specs:
+                b[d["name"]].native_handle.zero_()
+            for key, arr in (("p_ids", ids), ("p_mask", prefill_mask(T, S, n, dt)), ("p_pos", ar.reshape(1, -1)),
+                             ("p_cpos", ar), ("d_mask", decode_mask(S, n, dt)), ("d_pos", np.array([[n]], np.int64)),
+                             ("d_cpos", np.array([n], np.int64))):
+                b[key].write_from_numpy(arr)
+            pin = {"input_ids": b["p_ids"], "attention_mask": b["p_mask"], "position_ids": b["p_pos"],
+                   "cache_position": b["p_cpos"]}
+            caches = {d["name"]: b[d["name"]] for d in self.cache_specs}
+        else:
+            pin = {"input_ids": ids, "attention_mask": prefill_mask(T, S, n, dt), "position_ids": ar.reshape(1, -1),
+                   "cache_position": ar}
+            caches = {d["name"]: self._zeros(d) for d in self.cache_specs}
         for d, buf in caches.items():
             pin[self.p_cache_of[d]] = buf
 
@@ -169,35 +199,33 @@ class GreedyGenerator:
         if max_tokens == 1 or (eos_token_id is not None and first == eos_token_id):
             return GenerationResult(tokens if first != eos_token_id else [], n, ttft, 0.0)
 
-        dev = self._on_device() and self.tok_d is not None
+        fast = dev and self.tok_d is not None
         t1 = time.perf_counter()
-        if dev:
-            ids_b = self._put(np.array([[first]], np.int64))
-            mask_b = self._put(decode_mask(self.S, n, self.mask_dtype))
-            pos_b = self._put(np.array([[n]], np.int64))
-            cpos_b = self._put(np.array([n], np.int64))
-            mask_t, pos_t, cpos_t = (b.native_handle for b in (mask_b, pos_b, cpos_b))
+        if fast:
+            mask_t, pos_t, cpos_t = (b[k].native_handle for k in ("d_mask", "d_pos", "d_cpos"))
+            b["d_ids"].native_handle.fill_(first)
             hist = torch.zeros(max_tokens - 1, dtype=torch.int64, device=pos_t.device)
-            cur = ids_b
+            cur = b["d_ids"]
         else:
             cur = np.array([[first]], np.int64)
         steps = 0
         for step in range(max_tokens - 1):
             pos = n + step
-            if dev:
+            if fast:
                 if step:
                     mask_t[..., pos] = 0.0
                     pos_t.fill_(pos)
                     cpos_t.fill_(pos)
-                din = {"input_ids": cur, "attention_mask": mask_b, "position_ids": pos_b, "cache_position": cpos_b}
+                din = {"input_ids": cur, "attention_mask": b["d_mask"], "position_ids": b["d_pos"],
+                       "cache_position": b["d_cpos"]}
             else:
-                din = {"input_ids": cur, "attention_mask": self._put(decode_mask(self.S, pos, self.mask_dtype)),
+                din = {"input_ids": self._put(cur), "attention_mask": self._put(decode_mask(S, pos, dt)),
                        "position_ids": self._put(np.array([[pos]], np.int64)),
                        "cache_position": self._put(np.array([pos], np.int64))}
             din.update(kv)
             out = self.decode.execute(din)
             steps += 1
-            if dev:
+            if fast:
                 cur = out[self.tok_d]
                 hist[step].copy_(cur.native_handle.reshape(-1)[0])
                 if eos_token_id is not None and int(hist[step].item()) == eos_token_id:
@@ -212,7 +240,7 @@ class GreedyGenerator:
             for layer in self.kv_map["layers"]:
                 kv[layer["decode_key_input"]] = out[layer["decode_key_output"]]
                 kv[layer["decode_value_input"]] = out[layer["decode_value_output"]]
-        if dev:
+        if fast:
             self.backend.synchronize()
             got = hist[:steps].cpu().tolist()
             if eos_token_id is not None and eos_token_id in got:
