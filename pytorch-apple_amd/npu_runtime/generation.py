@@ -2,8 +2,8 @@
 
 Restates the reference's generation loop (`examples/run_qwen.py:84-200`):
 
-* the prompt is padded to the prefill graph's length T, under a causal mask that
-  also closes every padding row and column (`:90-99`);
+* the prompt is padded to the prefill graph's length T under a causal mask
+  (`:90-99`), so no real row sees a padding column;
 * the first token is the argmax of the prefill logits at the last real position
   (`:121-125`);
 * each decode step feeds the previous token at position ``prompt_len + step``, with
@@ -26,9 +26,13 @@ What differs:
 * on such a backend the caches and the per-step inputs are allocated once per
   generator and rewritten in place by each call (caches zeroed), so every call
   hands the executors the same buffers and their captured HIP graphs are reused;
-* masked entries hold the dtype's lowest finite value (the reference's fp16 -65504):
-  a padding row closed on every column then has a finite softmax, and no NaN can
-  reach a cache row that a later step opens.
+* closed entries are ``-inf`` and padding rows stay causal (open on ``0 .. i``),
+  where the reference closes them completely with fp16 -65504: every row keeps an
+  open entry, so no softmax is taken over a fully closed row (NaN with ``-inf``), and
+  the attention kernels skip every closed block exactly (a 128-token prefill over a
+  2048-position cache reads the first 128 positions, not 2048). Padding rows only
+  produce logits nobody reads and cache rows that decode steps overwrite before
+  opening them.
 """
 
 from __future__ import annotations
@@ -49,18 +53,19 @@ def _host(t: torch.Tensor) -> np.ndarray:
 
 
 def prefill_mask(T: int, S: int, prompt_len: int, dtype: str = "bfloat16") -> np.ndarray:
-    """[1, 1, T, S]: row i < prompt_len is open on 0..i; padding rows and columns are closed."""
-    low = torch.finfo(_TORCH[dtype]).min
-    m = torch.full((T, S), low, dtype=torch.float32)
+    """[1, 1, T, S]: row i open on 0..i, ``-inf`` elsewhere. A real row (i < prompt_len)
+    therefore sees no padding column; padding rows stay causal (see the module docstring)."""
+    if not 0 < prompt_len <= T <= S:
+        raise ValueError("need 0 < prompt_len <= T <= S")
     i = torch.arange(T).unsqueeze(1)
     j = torch.arange(S).unsqueeze(0)
-    m[(j <= i) & (i < prompt_len) & (j < prompt_len)] = 0.0
+    m = torch.where(j <= i, 0.0, float("-inf"))
     return _host(m.to(_TORCH[dtype]).reshape(1, 1, T, S))
 
 
 def decode_mask(S: int, pos: int, dtype: str = "bfloat16") -> np.ndarray:
-    """[1, 1, 1, S]: open on 0..pos."""
-    m = torch.full((1, 1, 1, S), torch.finfo(_TORCH[dtype]).min, dtype=torch.float32)
+    """[1, 1, 1, S]: open on 0..pos, ``-inf`` after."""
+    m = torch.full((1, 1, 1, S), float("-inf"), dtype=torch.float32)
     m[..., :pos + 1] = 0.0
     return _host(m.to(_TORCH[dtype]))
 

@@ -328,16 +328,20 @@ def test_generator_rejects_prompts_that_do_not_fit(model, graphs):
         gen.generate(list(range(16)), S)
 
 
-def test_prefill_mask_closes_padding_rows_and_columns():
+def test_prefill_mask_is_causal_and_keeps_padding_rows_open():
+    """Real rows see no padding column; padding rows stay causal, so no row is fully
+    closed (a softmax over an all ``-inf`` row is NaN in ATen)."""
     from npu_runtime.generation import decode_mask, prefill_mask
 
     m = torch.from_numpy(prefill_mask(6, 10, 4)).view(torch.bfloat16).float()[0, 0]
-    low = torch.finfo(torch.bfloat16).min
     for i in range(6):
         for j in range(10):
-            assert m[i, j] == (0.0 if (i < 4 and j <= i) else low)
+            assert m[i, j] == (0.0 if j <= i else float("-inf"))
+    assert bool(torch.isfinite(m).any(dim=1).all())
     d = torch.from_numpy(decode_mask(10, 6)).view(torch.bfloat16).float().reshape(-1)
-    assert d[:7].eq(0).all() and d[7:].eq(low).all()
+    assert d[:7].eq(0).all() and d[7:].eq(float("-inf")).all()
+    with pytest.raises(ValueError):
+        prefill_mask(6, 5, 4)
 
 
 def test_full_size_qwen2_5_export_lowers_to_the_bench_launch_list():
