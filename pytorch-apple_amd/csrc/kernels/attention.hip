@@ -474,6 +474,9 @@ __device__ __forceinline__ void prefill_attn_body(const PrefillAttnArgs& a) {
     for (int e = 0; e < 16; ++e) o[t][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
   const int nblk = (int)((a.S + PA_BP - 1) / PA_BP);
+  // position blocks past the last open mask column of this workgroup's rows are closed for all
+  // of them: not visited at all (no K/V loads), which is what a long static cache needs
+  const int nb = a.blk_limit != nullptr ? min(nblk, a.blk_limit[blockIdx.x]) : nblk;
   const long long last = a.S - 1;
   // V staging: lane -> positions pr, pr + 1 (pr = 2 (lane % 16)), 16-byte chunks cg + 4j of the dims
   const int pr = 2 * (lane & 15), cg = lane >> 4;
@@ -487,7 +490,7 @@ __device__ __forceinline__ void prefill_attn_body(const PrefillAttnArgs& a) {
   };
   // issue every load of block `blk` (clamped to the last block: a spare load, never used)
   auto load = [&](int blk, Blk& b) {
-    const long long p0 = (long long)min(blk, nblk - 1) * PA_BP;
+    const long long p0 = (long long)min(blk, max(nb, 1) - 1) * PA_BP;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (MM == 1) {
@@ -600,10 +603,10 @@ __device__ __forceinline__ void prefill_attn_body(const PrefillAttnArgs& a) {
   // block is computed (named register sets; loads past the last block re-read it)
   Blk ba, bb;
   load(wave, ba);
-  for (int blk = wave; blk < nblk; blk += 8) {
+  for (int blk = wave; blk < nb; blk += 8) {
     load(blk + 4, bb);
     compute(blk, ba);
-    if (blk + 4 >= nblk) break;
+    if (blk + 4 >= nb) break;
     load(blk + 8, ba);
     compute(blk + 4, bb);
   }
@@ -656,3 +659,44 @@ PA_KERNEL(k_attn_prefill_f32mask, HS_BF16, 2)
 PA_KERNEL(k_attn_prefill_f16, HS_F16, 1)
 PA_KERNEL(k_attn_prefill_f16_nomask, HS_F16, 0)
 PA_KERNEL(k_attn_prefill_f16_f32mask, HS_F16, 2)
+
+// k_mask_extent: grid (ceil(T / 32)), 256 threads. nblk_out[qb] = 1 + c / 32 for the largest
+// column c < S whose mask entry is not -inf in any of rows 32 qb .. 32 qb + 31 (rows past T are
+// not read), 0 when there is none. Every block past it is closed for all of those rows, so
+// k_attn_prefill leaves it out: its terms would be e^-inf = 0 exactly. NaN entries count as
+// open. 16-bit masks are read four entries per 8-byte load (unit column stride, 8-byte aligned
+// rows, S % 4 == 0: the host checks); wave w scans rows w, w + 4, ..., lanes along the row.
+extern "C" __global__ void __launch_bounds__(256) k_mask_extent(const MaskExtentArgs a) {
+  __shared__ int best[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const long long q0 = (long long)blockIdx.x * 32;
+  int mx = -1;
+  for (int r = wave; r < 32; r += 4) {
+    const long long t = q0 + r;
+    if (t >= a.T) break;   // wave-uniform
+    if (a.mask_dtype == HS_F32) {
+      const float* row = (const float*)a.mask + t * a.row_stride;
+      for (long long c = lane; c < a.S; c += 64)
+        if (row[c * a.col_stride] != -INFINITY) mx = max(mx, (int)c);
+    } else {
+      const uint16_t ninf = a.mask_dtype == HS_BF16 ? 0xFF80u : 0xFC00u;
+      const uint16_t* row = (const uint16_t*)a.mask + t * a.row_stride;
+      for (long long c = 4 * lane; c < a.S; c += 256) {
+        const uint2 w = *(const uint2*)(row + c);
+        const uint16_t e[4] = {(uint16_t)(w.x & 0xffffu), (uint16_t)(w.x >> 16), (uint16_t)(w.y & 0xffffu),
+                               (uint16_t)(w.y >> 16)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (e[j] != ninf) mx = max(mx, (int)c + j);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) best[wave] = mx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int m = max(max(best[0], best[1]), max(best[2], best[3]));
+    a.nblk_out[blockIdx.x] = m < 0 ? 0 : m / PA_BP + 1;
+  }
+}

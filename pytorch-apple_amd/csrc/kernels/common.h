@@ -462,6 +462,17 @@ struct PrefillAttnArgs {      // causal / masked attention of T queries over S k
   int mask_dtype;             // -1: no mask
   int add_dtype;              // rounding dtype of (scores + mask)
   int dtype;                  // bf16 or fp16
+  const int* blk_limit;       // per 32-query block: position blocks to visit (k_mask_extent), or null: all
+};
+
+struct MaskExtentArgs {       // k_mask_extent: last open mask column of each block of 32 query rows
+  const void* mask;           // element (t, s) at t*row_stride + s*col_stride
+  int* nblk_out;              // [ceil(T / 32)]: 1 + (last column != -inf) / 32, 0 when none
+  long long T;
+  long long S;
+  long long row_stride;
+  long long col_stride;       // 1 for 16-bit masks (8-byte aligned rows, S % 4 == 0); any for fp32
+  int mask_dtype;             // HS_BF16 / HS_F16 / HS_F32
 };
 
 struct CombineArgs {          // out[h, d] = round(sum_t e^(m_t - M) l_t o_t[d] / sum_t e^(m_t - M) l_t), o_t normalised

@@ -302,7 +302,7 @@ def _emit_prefill_attention(low, q, k, v, mask, out, scale, H, kvh, S, T, add_dt
     vv_ = low.contiguous(v)
     if (kv_.offset * 2) % 16 or (vv_.offset * 2) % 16 or (qv.offset * 2) % 16:
         raise NotImplementedError("attention operands must be 16-byte aligned")
-    margs = dict(mask=None, mask_row_stride=0, mask_col_stride=0, mask_dtype=-1)
+    margs = dict(mask=None, mask_row_stride=0, mask_col_stride=0, mask_dtype=-1, blk_limit=None)
     if mask is not None:
         mv = low.view(mask)
         if mv.dtype not in (dt, "float32"):
@@ -317,7 +317,7 @@ def _emit_prefill_attention(low, q, k, v, mask, out, scale, H, kvh, S, T, add_dt
                 mv = low.aligned16(low.contiguous(mask), mask)
         row = mv.strides[-2] if len(mv.shape) > 1 and mv.shape[-2] == T else 0
         margs = dict(mask=low.ref(mv), mask_row_stride=row, mask_col_stride=mv.strides[-1],
-                     mask_dtype=DTYPE_CODE[mv.dtype])
+                     mask_dtype=DTYPE_CODE[mv.dtype], blk_limit=_mask_extent(low, mask, mv, row, T, S))
     st = low.new_storage(out.name, [1, T, H, D], dt)
     args = dict(q=low.ref(qv), k=low.ref(kv_), v=low.ref(vv_), out=low.ref(st), T=T, S=S, q_head_stride=qv.strides[1],
                 kv_head_stride=kv_.strides[1], H=H, KVH=kvh, scale=float(scale), add_dtype=DTYPE_CODE[add_dtype],
@@ -329,6 +329,24 @@ def _emit_prefill_attention(low, q, k, v, mask, out, scale, H, kvh, S, T, add_dt
                         inputs=[q, k, v] + ([mask] if mask else []), outputs=[out.name],
                         params={"T": T, "S": S, "heads": H, "kv_heads": kvh, "nodes": names}))
     low.views[out.name] = st.with_(shape=(1, H, T, D), strides=(T * H * D, D, H * D, 1))
+
+
+def _mask_extent(low, name: str, mv, row: int, T: int, S: int):
+    """Per block of 32 query rows, how many 32-position blocks the mask leaves open at most
+    (``k_mask_extent``), computed once per distinct mask view and shared by every layer's
+    prefill attention."""
+    key = (mv.storage, mv.offset, tuple(mv.shape), tuple(mv.strides), row, T, S)
+    ref = low.mask_extents.get(key)
+    if ref is None:
+        nqb = (T + 31) // 32
+        ref = low.scratch(name + ".extent", 4 * nqb)
+        low.emit(LaunchStep(kind="special", kernel="k_mask_extent", module="attention", arg_struct="MaskExtentArgs",
+                            args=dict(mask=low.ref(mv), nblk_out=ref, T=T, S=S, row_stride=row,
+                                      col_stride=mv.strides[-1], mask_dtype=DTYPE_CODE[mv.dtype]),
+                            grid=(nqb, 1, 1), inputs=[name], outputs=[ref.storage],
+                            params={"T": T, "S": S}))
+        low.mask_extents[key] = ref
+    return ref
 
 
 def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, dt, names) -> None:

@@ -212,6 +212,7 @@ class Lowering:
         self.lazy: dict[str, object] = {}        # tensor name -> emitter run when the value is first needed
         self.rms_info: dict[str, dict] = {}      # RMSNorm output -> {x, w, eps, n_dtype} (foldable prologue)
         self.attn_info: dict[str, dict] = {}     # split decode attention output -> partials (foldable prologue)
+        self.mask_extents: dict[tuple, Ref] = {}  # prefill mask view -> per-query-block open extent
         self.graph_output_names = {o.name for o in graph.graph_outputs}
         self.mutated_inputs: set[str] = set()
         self._uid = 0

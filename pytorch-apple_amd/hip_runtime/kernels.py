@@ -82,7 +82,9 @@ _struct("RopeCacheArgs", [("y", P), ("inv_freq", P), ("pos_ids", P), ("cache_pos
 _struct("PrefillAttnArgs", [("q", P), ("k", P), ("v", P), ("mask", P), ("out", P), ("T", LL), ("S", LL),
                             ("q_head_stride", LL), ("kv_head_stride", LL), ("mask_row_stride", LL),
                             ("mask_col_stride", LL), ("H", I), ("KVH", I), ("scale", F), ("mask_dtype", I),
-                            ("add_dtype", I), ("dtype", I)])
+                            ("add_dtype", I), ("dtype", I), ("blk_limit", P)])
+_struct("MaskExtentArgs", [("mask", P), ("nblk_out", P), ("T", LL), ("S", LL), ("row_stride", LL),
+                           ("col_stride", LL), ("mask_dtype", I)])
 _struct("ArgmaxPartArgs", [("x", P), ("slot", P), ("rows", LL), ("cols", LL), ("seg", LL), ("x_dtype", I),
                            ("parts", I)])
 _struct("FusedArgs", [("out", P), ("in", P * 8), ("n", LL)])

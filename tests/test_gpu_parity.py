@@ -577,7 +577,42 @@ def test_prefill_attention_kernel_mask_modes(backend, mask):
     got, ex = run_hip(ir, x, {}, backend)
     kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
     want = {None: "k_attn_prefill_nomask", "float32": "k_attn_prefill_f32mask", "bfloat16": "k_attn_prefill"}[mask]
-    assert kernels[0] == want and "k_softmax" not in kernels   # (+ one copy: the graph output is [1, H, T, D])
+    assert want in kernels and "k_softmax" not in kernels   # (+ one copy: the graph output is [1, H, T, D])
+    assert ("k_mask_extent" in kernels) == (mask is not None)
+    ref = run_cpu(ir, x, {})
+    orc = run_ir(ir, x, {})
+    for k in got:
+        close(got[k], ref[k])
+        close(got[k], orc[k])
+
+
+@pytest.mark.parametrize("mask", ["float32", "bfloat16"])
+@pytest.mark.parametrize("pattern", ["static_cache", "far_column"])
+def test_prefill_attention_bounded_by_mask_extent(backend, mask, pattern):
+    """T = 70 queries over a 1000-position cache: k_mask_extent bounds each 32-query block's
+    position loop by the last open column of its rows. static_cache: causal over the first T
+    positions (the generator's padded prefill); far_column: as static_cache, plus row 40 open
+    on column 997 (the second query block must reach the last position block, the others not)."""
+    from oracle.numpy_ref import run_ir
+
+    T, S = 70, 1000
+    ir = _prefill_attention_ir(T, S, mask_dtype=mask)
+    g = torch.Generator().manual_seed(13)
+    x = {"q": torch.randn(1, 12, T, 128, generator=g).bfloat16(),
+         "k": torch.randn(1, 2, S, 128, generator=g).bfloat16(),
+         "v": torch.randn(1, 2, S, 128, generator=g).bfloat16()}
+    m = torch.full((T, S), float("-inf"))
+    for t in range(T):
+        m[t, :t + 1] = 0.0
+    if pattern == "far_column":
+        m[40, 997] = -2.0
+    dt = torch.float32 if mask == "float32" else torch.bfloat16
+    x["mask"] = m.to(dt).reshape(1, 1, T, S)
+    x = host(x)
+    print(f"[case] prefill attention extent {pattern} {mask}", flush=True)
+    got, ex = run_hip(ir, x, {}, backend)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert "k_mask_extent" in kernels
     ref = run_cpu(ir, x, {})
     orc = run_ir(ir, x, {})
     for k in got:
