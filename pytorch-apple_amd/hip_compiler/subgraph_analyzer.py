@@ -57,7 +57,9 @@ def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, boo
     GEMM_DMA_MAX_TILES tiles. Two weights (gate/up with the SiLU-mul epilogue): 64 x 64
     tiles, 52 us against 57 for 128 x 64 without. One weight: the largest tile that still
     gives >= 256 workgroups; long rows (K >= 4096) take 128 x 128 with up to 4 K splits
-    (down_proj 512 x 1536 x 8960: 26 us with 4 splits, 32 with 8); other grids under 256
+    (down_proj 512 x 1536 x 8960: 26 us with 4 splits, 32 with 8), or, with fewer than 48 such
+    tiles, 64 x 64 with up to 8 (down_proj at M = 128, a 128-token prefill: 17.0 us on 64 x 64
+    with 8 splits, 18.2 on 64 x 128 with 8, 19.6 on 128 x 128 with 16, 29.0 with 4); other grids under 256
     tiles split K toward ~384 workgroups (o_proj 512 x 1536 x 1536 on 64 x 64: 9.5 us with
     2 splits, 12.9 unsplit). The lm_head (4,748 tiles of 128 x 128) keeps register staging:
     324 us against 367."""
@@ -76,7 +78,10 @@ def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, boo
             return bm, bn, 1, dma and t < GEMM_DMA_MAX_TILES
     if K >= 4096:
         t = ntiles(128, 128)
-        return 128, 128, max(1, min(4, 384 // t, K // GEMM_MIN_KCHUNK)), dma
+        if t >= 48:
+            return 128, 128, max(1, min(4, 384 // t, K // GEMM_MIN_KCHUNK)), dma
+        t = ntiles(64, 64)
+        return 64, 64, max(1, min(8, (384 + t - 1) // t, K // GEMM_MIN_KCHUNK)), dma
     t = ntiles(64, 64)
     return 64, 64, max(1, min((384 + t - 1) // t, K // GEMM_MIN_KCHUNK)), dma
 
