@@ -660,34 +660,54 @@ PA_KERNEL(k_attn_prefill_f16, HS_F16, 1)
 PA_KERNEL(k_attn_prefill_f16_nomask, HS_F16, 0)
 PA_KERNEL(k_attn_prefill_f16_f32mask, HS_F16, 2)
 
-// k_mask_extent: grid (ceil(T / 32)), 256 threads. nblk_out[qb] = 1 + c / 32 for the largest
+// k_mask_extent: grid (ceil(T / 32)), 1024 threads. nblk_out[qb] = 1 + c / 32 for the largest
 // column c < S whose mask entry is not -inf in any of rows 32 qb .. 32 qb + 31 (rows past T are
 // not read), 0 when there is none. Every block past it is closed for all of those rows, so
 // k_attn_prefill leaves it out: its terms would be e^-inf = 0 exactly. NaN entries count as
-// open. 16-bit masks are read four entries per 8-byte load (unit column stride, 8-byte aligned
-// rows, S % 4 == 0: the host checks); wave w scans rows w, w + 4, ..., lanes along the row.
-extern "C" __global__ void __launch_bounds__(256) k_mask_extent(const MaskExtentArgs a) {
-  __shared__ int best[4];
+// open. Wave w scans rows w and w + 16, lanes along the row, all loads of a 2048-column chunk
+// (eight per lane) issued before the first is tested, so a scan of S <= 2048 is one memory
+// latency. 16-bit masks are read four entries per 8-byte load (unit column stride, 8-byte aligned
+// rows, S % 4 == 0: the host checks).
+extern "C" __global__ void __launch_bounds__(1024) k_mask_extent(const MaskExtentArgs a) {
+  __shared__ int best[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const long long q0 = (long long)blockIdx.x * 32;
   int mx = -1;
-  for (int r = wave; r < 32; r += 4) {
+  for (int r = wave; r < 32; r += 16) {
     const long long t = q0 + r;
     if (t >= a.T) break;   // wave-uniform
     if (a.mask_dtype == HS_F32) {
       const float* row = (const float*)a.mask + t * a.row_stride;
-      for (long long c = lane; c < a.S; c += 64)
-        if (row[c * a.col_stride] != -INFINITY) mx = max(mx, (int)c);
-    } else {
-      const uint16_t ninf = a.mask_dtype == HS_BF16 ? 0xFF80u : 0xFC00u;
-      const uint16_t* row = (const uint16_t*)a.mask + t * a.row_stride;
-      for (long long c = 4 * lane; c < a.S; c += 256) {
-        const uint2 w = *(const uint2*)(row + c);
-        const uint16_t e[4] = {(uint16_t)(w.x & 0xffffu), (uint16_t)(w.x >> 16), (uint16_t)(w.y & 0xffffu),
-                               (uint16_t)(w.y >> 16)};
+      for (long long c0 = 0; c0 < a.S; c0 += 512) {
+        float v[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (e[j] != ninf) mx = max(mx, (int)c + j);
+        for (int j = 0; j < 8; ++j) {
+          const long long c = c0 + lane + 64 * j;
+          v[j] = c < a.S ? row[c * a.col_stride] : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (v[j] != -INFINITY) mx = max(mx, (int)(c0 + lane + 64 * j));
+      }
+    } else {
+      const uint32_t ninf = a.mask_dtype == HS_BF16 ? 0xFF80u : 0xFC00u;
+      const uint32_t ninf2 = ninf | (ninf << 16);
+      const uint16_t* row = (const uint16_t*)a.mask + t * a.row_stride;
+      for (long long c0 = 0; c0 < a.S; c0 += 2048) {
+        uint2 w[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const long long c = c0 + 4 * lane + 256 * j;
+          w[j] = c < a.S ? *(const uint2*)(row + c) : make_uint2(ninf2, ninf2);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int c = (int)(c0 + 4 * lane + 256 * j);
+          if ((w[j].y >> 16) != ninf) mx = max(mx, c + 3);
+          else if ((w[j].y & 0xffffu) != ninf) mx = max(mx, c + 2);
+          else if ((w[j].x >> 16) != ninf) mx = max(mx, c + 1);
+          else if ((w[j].x & 0xffffu) != ninf) mx = max(mx, c);
+        }
       }
     }
   }
@@ -696,7 +716,9 @@ extern "C" __global__ void __launch_bounds__(256) k_mask_extent(const MaskExtent
   if (lane == 0) best[wave] = mx;
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int m = max(max(best[0], best[1]), max(best[2], best[3]));
+    int m = best[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) m = max(m, best[w]);
     a.nblk_out[blockIdx.x] = m < 0 ? 0 : m / PA_BP + 1;
   }
 }

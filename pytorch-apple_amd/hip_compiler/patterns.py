@@ -343,7 +343,7 @@ def _mask_extent(low, name: str, mv, row: int, T: int, S: int):
         low.emit(LaunchStep(kind="special", kernel="k_mask_extent", module="attention", arg_struct="MaskExtentArgs",
                             args=dict(mask=low.ref(mv), nblk_out=ref, T=T, S=S, row_stride=row,
                                       col_stride=mv.strides[-1], mask_dtype=DTYPE_CODE[mv.dtype]),
-                            grid=(nqb, 1, 1), inputs=[name], outputs=[ref.storage],
+                            grid=(nqb, 1, 1), block=(1024, 1, 1), inputs=[name], outputs=[ref.storage],
                             params={"T": T, "S": S}))
         low.mask_extents[key] = ref
     return ref
