@@ -465,6 +465,24 @@ struct PrefillAttnArgs {      // causal / masked attention of T queries over S k
   const int* blk_limit;       // per 32-query block: position blocks to visit (k_mask_extent), or null: all
 };
 
+struct ReduceNormArgs {       // split-K reduce + residual, then RMSNorm of the result (gemm.hip)
+  const float* part;          // fp32 partial sums [ksplit, M, N]
+  const void* bias;           // [N] or null (flags & 1)
+  const void* resid;          // [M, N] (row stride ldr)
+  void* out;                  // [M, N] (row stride ldo): round(resid + round(sum_z part + bias))
+  const void* norm_w;         // [N], the dtype of out
+  void* norm_out;             // [M, N] (row stride ldn): norm_w * round_n(out * rsqrt(mean(out^2) + eps))
+  long long M;
+  long long ldr;
+  long long ldo;
+  long long ldn;
+  int N;                      // N % 8 == 0, N <= 2048, 16-byte aligned rows; grid = M workgroups
+  int ksplit;
+  float eps;
+  int n_dtype;                // rounding dtype of the normalised value
+  int flags;
+};
+
 struct MaskExtentArgs {       // k_mask_extent: last open mask column of each block of 32 query rows
   const void* mask;           // element (t, s) at t*row_stride + s*col_stride
   int* nblk_out;              // [ceil(T / 32)]: 1 + (last column != -inf) / 32, 0 when none

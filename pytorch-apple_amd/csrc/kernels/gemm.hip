@@ -606,6 +606,98 @@ __device__ __forceinline__ void gemm_reduce_body(const GemmArgs& a) {
   }
 }
 
+// Split-K reduce with the residual epilogue, fused with the RMSNorm that reads its result (the
+// next norm of a transformer layer): one workgroup per row, thread t owns the 16-byte column
+// chunk t (N <= 2048). Its residual, norm weight and the partials of up to 8 splits are loaded
+// in one round. Each element sums its partials in split order and is rounded as GE_RESID rounds
+// it (as gemm_reduce_body); the row is stored and staged in LDS, and wave 0 takes the sum of
+// squares over it in k_rmsnorm_w's lane and chunk order, so both outputs equal those of the
+// reduce kernel followed by k_rmsnorm_w bit for bit, with one launch and one pass less.
+template <int DT>
+__device__ __forceinline__ void reduce_norm_body(const ReduceNormArgs& a) {
+  __shared__ float xs[2048];
+  __shared__ float rsh;
+  const long long row = blockIdx.x;
+  const int t = threadIdx.x;
+  const int nch = a.N / 8;
+  const bool own = t < nch;
+  const int c = own ? t : 0;   // idle threads re-read chunk 0 and store nothing
+  const long long plane = a.M * (long long)a.N;
+  const float* p = a.part + row * a.N + 8 * c;
+  const uint4 r = *(const uint4*)((const uint16_t*)a.resid + row * a.ldr + 8 * c);
+  const uint4 g = *(const uint4*)((const uint16_t*)a.norm_w + 8 * c);
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  for (int z0 = 0; z0 < a.ksplit; z0 += 8) {
+    float4 u[8], v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {   // past the last split: re-read it (not added)
+      const long long z = min(z0 + j, a.ksplit - 1);
+      u[j] = *(const float4*)(p + z * plane);
+      v[j] = *(const float4*)(p + z * plane + 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (z0 + j >= a.ksplit) break;   // workgroup-uniform
+      acc[0] += u[j].x; acc[1] += u[j].y; acc[2] += u[j].z; acc[3] += u[j].w;
+      acc[4] += v[j].x; acc[5] += v[j].y; acc[6] += v[j].z; acc[7] += v[j].w;
+    }
+  }
+  const uint32_t rq[4] = {r.x, r.y, r.z, r.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float b = (a.flags & 1) ? gm_ld<DT>(a.bias, 8 * c + e) : 0.f;
+    const float v = gm_round<DT>(acc[e] + b);
+    const uint16_t rb = (uint16_t)(rq[e >> 1] >> (16 * (e & 1)));
+    acc[e] = gm_round<DT>((DT == HS_BF16 ? bf16_to_f32(rb) : f16_to_f32(rb)) + v);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = (uint32_t)gm_pack<DT>(acc[2 * k]) | ((uint32_t)gm_pack<DT>(acc[2 * k + 1]) << 16);
+  if (own) {
+    *(uint4*)((uint16_t*)a.out + row * a.ldo + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xs[8 * c + e] = acc[e];
+  }
+  __syncthreads();
+  if (t < 64) {   // k_rmsnorm_w's order: lane l sums chunks l, l + 64, ... element by element
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int cc = t + 64 * k;
+      if (cc >= nch) continue;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += xs[8 * cc + e] * xs[8 * cc + e];
+    }
+    ss = wave_sum(ss);
+    if (t == 0) rsh = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+  }
+  __syncthreads();
+  if (!own) return;
+  const float rs = rsh;
+  const uint32_t gq[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t w2 = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float n = round_to(acc[2 * k + h] * rs, a.n_dtype);
+      const uint16_t gb = (uint16_t)(gq[k] >> (16 * h));
+      w2 |= (uint32_t)gm_pack<DT>((DT == HS_BF16 ? bf16_to_f32(gb) : f16_to_f32(gb)) * n) << (16 * h);
+    }
+    o[k] = w2;
+  }
+  *(uint4*)((uint16_t*)a.norm_out + row * a.ldn + 8 * c) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+extern "C" __global__ void __launch_bounds__(256) k_gemm_reduce_bf16_resid_norm(const ReduceNormArgs a) {
+  reduce_norm_body<HS_BF16>(a);
+}
+extern "C" __global__ void __launch_bounds__(256) k_gemm_reduce_f16_resid_norm(const ReduceNormArgs a) {
+  reduce_norm_body<HS_F16>(a);
+}
+
 // up to 2 waves per SIMD: the 64 accumulator registers plus staging and fragments need
 // more than the default register budget, which would otherwise spill the staging to scratch
 #define GM_ATTRS __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))

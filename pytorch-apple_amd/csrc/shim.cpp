@@ -248,6 +248,7 @@ size_t hs_argsize(const char* s) {
   HS_SZ(RopeCacheArgs)
   HS_SZ(PrefillAttnArgs)
   HS_SZ(MaskExtentArgs)
+  HS_SZ(ReduceNormArgs)
   HS_SZ(ArgmaxPartArgs)
   HS_SZ(GemmArgs)
   HS_SZ(ConvArgs)

@@ -24,6 +24,10 @@ from hip_compiler import views as V
 from hip_compiler.program import DTYPE_CODE, LaunchStep
 from npu_compiler.ir_reader import OpNode
 
+# a split-K reduce with the residual epilogue and the RMSNorm reading its result run as one
+# kernel (k_gemm_reduce_*_resid_norm); off = two launches with the same results
+FUSE_REDUCE_NORM = True
+
 _PASS = ("aten._assert_tensor_metadata.default",)
 
 
@@ -125,6 +129,25 @@ def rmsnorm(low) -> None:
             half = ("bfloat16", "float16")
             wave = (xv.dtype in half and wv.dtype == xv.dtype and out.dtype in half and cols % 8 == 0
                     and cols <= 4096 and (xv.offset * 2) % 16 == 0 and (wv.offset * 2) % 16 == 0)
+            # x was just produced by a split-K reduce with the residual epilogue (o_proj or down_proj
+            # + residual of a prefill-sized GEMM): that launch becomes reduce + residual + RMSNorm
+            prev = low.steps[-1] if low.steps else None
+            if (FUSE_REDUCE_NORM and wave and out.dtype == xv.dtype and prev is not None and prev.params.get("reduce")
+                    and prev.params.get("epilogue") == "resid" and prev.outputs == [x.name]
+                    and prev.args.get("nw", 1) == 1 and prev.args["N"] == cols <= 2048 and prev.args["M"] == rows
+                    and prev.args["ldo"] == cols and prev.args["out"] == low.ref(xv)):
+                pa = prev.args
+                low.steps[-1] = LaunchStep(
+                    kind="gemm", kernel=f"k_gemm_reduce_{'bf16' if xv.dtype == 'bfloat16' else 'f16'}_resid_norm",
+                    module="gemm", arg_struct="ReduceNormArgs",
+                    args=dict(part=pa["part"], bias=pa["bias"] if pa["flags"] & 1 else None, resid=pa["resid"],
+                              out=pa["out"], norm_w=low.ref(wv), norm_out=low.ref(o), M=rows, ldr=pa["ldr"],
+                              ldo=cols, ldn=cols, N=cols, ksplit=pa["ksplit"], eps=eps,
+                              n_dtype=DTYPE_CODE[n_dtype], flags=pa["flags"] & 1),
+                    grid=(rows, 1, 1), inputs=prev.inputs + [w.name], outputs=prev.outputs + [out.name],
+                    params=dict(prev.params, norm=True, norm_nodes=names))
+                low.views[out.name] = o
+                return
             low.emit(LaunchStep(
                 kind="rmsnorm", kernel="k_rmsnorm_w" if wave else "k_rmsnorm", module="basic", arg_struct="RMSNormArgs",
                 args=dict(x=low.ref(xv), w=low.ref(wv), out=low.ref(o), rows=rows, ldx=cols, ldo=cols, cols=cols,

@@ -83,6 +83,9 @@ _struct("PrefillAttnArgs", [("q", P), ("k", P), ("v", P), ("mask", P), ("out", P
                             ("q_head_stride", LL), ("kv_head_stride", LL), ("mask_row_stride", LL),
                             ("mask_col_stride", LL), ("H", I), ("KVH", I), ("scale", F), ("mask_dtype", I),
                             ("add_dtype", I), ("dtype", I), ("blk_limit", P)])
+_struct("ReduceNormArgs", [("part", P), ("bias", P), ("resid", P), ("out", P), ("norm_w", P), ("norm_out", P),
+                           ("M", LL), ("ldr", LL), ("ldo", LL), ("ldn", LL), ("N", I), ("ksplit", I), ("eps", F),
+                           ("n_dtype", I), ("flags", I)])
 _struct("MaskExtentArgs", [("mask", P), ("nblk_out", P), ("T", LL), ("S", LL), ("row_stride", LL),
                            ("col_stride", LL), ("mask_dtype", I)])
 _struct("ArgmaxPartArgs", [("x", P), ("slot", P), ("rows", LL), ("cols", LL), ("seg", LL), ("x_dtype", I),

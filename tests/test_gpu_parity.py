@@ -620,6 +620,30 @@ def test_prefill_attention_bounded_by_mask_extent(backend, mask, pattern):
         close(got[k], orc[k])
 
 
+@pytest.mark.parametrize("T", [128, 512])
+def test_reduce_norm_fusion_is_bit_identical(backend, T, monkeypatch):
+    """A 2-layer full-width prefill with the split-K reduce + residual + RMSNorm fused into one
+    kernel and without (the reduce kernel, then k_rmsnorm_w): every output bit-identical."""
+    import hip_compiler.patterns as P
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import make_weights, prefill_inputs
+
+    cfg = QwenConfig(layers=2, vocab=4096)
+    ir = build_decode_ir(512, cfg, argmax=True, tokens=T)
+    w = host(make_weights(ir, cfg, norm_std=0.02))
+    x = host(prefill_inputs(T, 512, cfg))
+    outs = []
+    for fuse in (True, False):
+        monkeypatch.setattr(P, "FUSE_REDUCE_NORM", fuse)
+        print(f"[case] reduce+norm fusion={fuse} T={T}", flush=True)
+        got, ex = run_hip(ir, x, w, backend)
+        kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+        assert ("k_gemm_reduce_bf16_resid_norm" in kernels) == fuse
+        outs.append(got)
+    for k in outs[0]:
+        assert np.array_equal(outs[0][k], outs[1][k]), k
+
+
 def test_prefill_chunk_ragged_vs_cpu_and_oracle(backend):
     """A 100-token chunk (not a multiple of the 32-query tile) at positions 40..139 of a 160-entry
     cache whose first 40 rows hold earlier keys and values: the grouped q/k/v GEMM, the RoPE and
