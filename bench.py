@@ -84,6 +84,34 @@ def time_kernel_subset(ex, indices, repeats, stream) -> float:
     return ms.value / (repeats * len(indices))
 
 
+def time_graph_reps(ex, reps: int, stream) -> float:
+    """Device ms per step: ``reps`` copies of the step's launch list captured into one HIP
+    graph and launched once between two HIP events, so no host work sits between steps."""
+    from hip_runtime import _shim
+
+    lib = _shim.lib()
+    n = len(ex._recs)
+    recs = (_shim.LaunchRec * (n * reps))(*[ex._recs[i] for _ in range(reps) for i in range(n)])
+    cs, g = C.c_void_p(), C.c_void_p()
+    _shim.check(lib.hs_stream_create(C.byref(cs)))
+    _shim.check(lib.hs_graph_capture(recs, n * reps, cs, C.byref(g)))
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    _shim.check(lib.hs_event_create(C.byref(e0)))
+    _shim.check(lib.hs_event_create(C.byref(e1)))
+    _shim.check(lib.hs_graph_launch(g, stream))      # warm
+    _shim.check(lib.hs_event_record(e0, stream))
+    _shim.check(lib.hs_graph_launch(g, stream))
+    _shim.check(lib.hs_event_record(e1, stream))
+    _shim.check(lib.hs_event_sync(e1))
+    ms = C.c_float()
+    _shim.check(lib.hs_event_elapsed_ms(e0, e1, C.byref(ms)))
+    for e in (e0, e1):
+        lib.hs_event_destroy(e)
+    lib.hs_graph_destroy(g)
+    lib.hs_stream_destroy(cs)
+    return ms.value / reps
+
+
 def time_in_step(ex, indices, replays, stream) -> float:
     """Average ms of the launches ``indices`` inside full replays of the step's launch list:
     every launch of the step runs in order, and HIP events on ``stream`` bracket each selected
@@ -252,12 +280,16 @@ def main() -> int:
                     help="size of the k_copy calibration launches run after timing (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=28)
-    ap.add_argument("--workload", choices=("decode", "prefill", "resnet50", "generate"), default="decode",
+    ap.add_argument("--workload", choices=("decode", "prefill", "resnet50", "generate", "mlp", "attention"),
+                    default="decode",
                     help="decode: the headline (cfg3); prefill: 512-token prefill (cfg4); resnet50: batch-32 "
                          "ResNet-50 inference (cfg5); the last two report MFMA utilisation; generate: HF "
-                         "Qwen2 exported to IR, padded prefill then greedy decode (TTFT and tok/s)")
+                         "Qwen2 exported to IR, padded prefill then greedy decode (TTFT and tok/s); mlp: the "
+                         "RMSNorm + gated MLP + residual subgraph (cfg1) at --tokens; attention: one decode "
+                         "attention block over a 1025-entry cache (cfg2); the last two report HBM GB/s")
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--tokens", type=int, default=1, help="cfg1 rows (1, 16 or 128)")
     args = ap.parse_args()
     if args.workload == "prefill" and args.gpus == 1:
         return main_prefill(args)
@@ -265,6 +297,8 @@ def main() -> int:
         return main_resnet(args)
     if args.workload == "generate" and args.gpus == 1:
         return main_generate(args)
+    if args.workload in ("mlp", "attention") and args.gpus == 1:
+        return main_block(args)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (sharding across "
                                    "GPUs is a design note, not implemented)"}))
@@ -556,6 +590,107 @@ def main_prefill(args) -> int:
         "step_roofline": {"achieved": round(step_tf, 1), "unit": "TFLOP/s",
                           "frac": round(step_tf / MFMA_PEAK_TFLOPS, 4)},
         "kernels": per_kernel,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def main_block(args) -> int:
+    """cfg1 / cfg2: one subgraph, HBM-bound. A step is one run of the graph on inputs resident
+    in HBM; ``value`` is its achieved algorithmic GB/s over the device time of one step (50
+    steps captured back to back into one HIP graph, timed with HIP events; the wall time of
+    one ``execute()`` call, host-bound at these sizes, is reported beside it), with the
+    per-step bytes of the survey's formulas: cfg1 82,578,432 B of weights (gate, up, down
+    and the norm weight) + 3 T 1536 2 B of activations (x, residual, output); cfg2
+    11,014,144 B of weights and biases + 1,024 S B of K/V read (S = 1025) + 1,024 B of K/V
+    written. The CPU baseline is the same graph through the all-CPU plan (median of 5 runs
+    after 3 warmups, all host threads)."""
+    import statistics
+
+    import torch
+
+    from hip_compiler import compile_subgraph, is_hip_op_supported
+    from hip_runtime import HIPBackend
+    from irgen.qwen import build_attention_ir, build_mlp_ir
+    from irgen.workloads import attention_inputs, make_weights, mlp_inputs, to_host
+    from npu_compiler import partition
+    from npu_runtime import DAGExecutor
+
+    if args.workload == "mlp":
+        T = args.tokens
+        ir = build_mlp_ir(T)
+        x0 = mlp_inputs(T)
+        weights = make_weights(ir, norm_std=0.02, device="cuda")
+        nbytes = 82_578_432 + 3 * T * 1536 * 2
+        name, unit_note = f"cfg1: RMSNorm -> gate/up -> SiLU*up -> down -> +residual, T={T}", f"T={T}"
+    else:
+        S = 1025
+        ir = build_attention_ir(S)
+        x0 = attention_inputs(S)
+        weights = make_weights(ir, device="cuda")
+        nbytes = 11_014_144 + 1_024 * S + 1_024
+        name, unit_note = "cfg2: decode attention block (q/k/v + RoPE + index_copy + GQA attention + o_proj), S=1025", "S=1025"
+    steps = args.steps if args.steps != 64 else 200
+    warm = args.warmup if args.warmup != 8 else 20
+    backend = HIPBackend(0)
+    ex = DAGExecutor(partition(ir, is_hip_op_supported), backend, compile_fn=compile_subgraph)
+    ex.load_weights(weights)
+    state = {k: backend.allocate_buffer(v) for k, v in x0.items()}
+    (program,) = ex.npu_programs.values()
+    for _ in range(warm):
+        ex.execute(state)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ex.execute(state)
+    torch.cuda.synchronize()
+    host_ms = (time.perf_counter() - t0) * 1e3 / steps
+    # device time of one step: 50 steps back to back in one HIP graph between two HIP events (a
+    # step of a few tens of microseconds of kernels is shorter than the host's own cost of one
+    # execute() call, so the wall time above measures the host, not the kernels); per-launch
+    # times from events around each launch inside full replays, for the breakdown only
+    (hexec,) = ex._npu_executors.values()
+    stream = torch.cuda.current_stream().cuda_stream
+    ms = time_graph_reps(hexec, 50, stream)
+    per = {}
+    for i, st in enumerate(program.steps):
+        per.setdefault(st.kernel, []).append(i)
+    ktimes = {k: time_in_step(hexec, idx, 20, stream) for k, idx in per.items()}
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"{args.workload} {unit_note}: device {ms * 1e3:.2f} us/step ({gbs:.0f} GB/s), host-inclusive "
+        f"{host_ms * 1e3:.2f} us per execute() ({len(program.steps)} launches)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        n = len(os.sched_getaffinity(0))
+        torch.set_num_threads(n)
+        cex = DAGExecutor(partition(ir, lambda *_: False), None)
+        cex.load_weights({k: v.detach().cpu() for k, v in weights.items()})
+        ins = {k: to_host(v) for k, v in x0.items()}
+        for _ in range(3):
+            cex.execute(ins)
+        ts = []
+        for _ in range(5):
+            t1 = time.perf_counter()
+            cex.execute(ins)
+            ts.append(time.perf_counter() - t1)
+        med = statistics.median(ts)
+        cpu = {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": n, "kind": "port",
+               "sample": f"the same graph through DAGExecutor's all-CPU plan (ATen bf16, {n} threads), median of 5 "
+                         f"runs after 3 warmups: {med * 1e3:.2f} ms per run"}
+        log(f"cpu: {cpu}")
+    line = {
+        "metric": f"Qwen2.5-1.5B-shaped {args.workload} block bf16: achieved HBM GB/s vs peak ({unit_note})",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": name, "launches_per_step": len(program.steps), "bytes_per_step": nbytes,
+                   "host_inclusive_us_per_step": round(host_ms * 1e3, 2),
+                   "host_inclusive_GBs": round(nbytes / (host_ms * 1e-3) / 1e9, 1),
+                   "kernels_in_step_event_us": {k: {"launches_per_step": len(per[k]),
+                                                    "avg_us": round(ktimes[k] * 1e3, 3)} for k in per}},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
