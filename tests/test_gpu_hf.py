@@ -219,3 +219,28 @@ def test_executor_keeps_one_graph_per_pointer_set(backend):
     assert len(hexec._graphs) == 2
     assert torch.equal(runs[0], runs[2])
     assert not torch.equal(runs[0], runs[1])
+
+
+def test_long_generation_across_attention_splits(hf, backend):
+    """A 32-token prompt filling the prefill graph (no padding), then 120 device-resident
+    decode steps at positions 32..151: the in-place mask / position updates and the split-S
+    attention cross several 64- and 128-position split boundaries. Every token must be HF's
+    argmax (or a near tie) given the tokens before it."""
+    from irgen.hf_qwen import export_qwen, kv_mapping
+    from npu_runtime.generation import GreedyGenerator
+
+    m, d = hf
+    T = 32
+    pre = export_qwen(m, S, tokens=T, argmax=True)
+    dec = export_qwen(m, S, tokens=1, argmax=True)
+    gen = GreedyGenerator(hip_executor(pre, d, backend), hip_executor(dec, d, backend),
+                          kv_mapping(pre, dec, 2, T, S), pre, dec, backend=backend)
+    prompt = [int(t) for t in torch.randint(0, 8192, (T,), generator=torch.Generator().manual_seed(9))]
+    print("[case] generation, prompt 32 / prefill 32 / 121 tokens", flush=True)
+    res = gen.generate(prompt, 121)
+    assert len(res.tokens) == 121 and res.decode_tok_s > 0
+    seq = torch.tensor([prompt + res.tokens[:-1]])
+    with torch.no_grad():
+        logits = m(seq).logits[0]
+    bad = [i for i, tok in enumerate(res.tokens) if not token_ok(tok, logits[T - 1 + i])]
+    assert not bad, f"steps {bad[:5]} differ from HF beyond a near tie"
