@@ -342,6 +342,7 @@ def main() -> int:
     state = {k: backend.allocate_buffer(v) for k, v in x0.items()}
     first_token = state["input_ids"]
     mask_t, pos_t, cpos_t = (state[k].native_handle for k in ("attention_mask", "position_ids", "cache_position"))
+    advance = backend.decode_advance(state["attention_mask"], state["position_ids"], state["cache_position"])
 
     host_steps = None
 
@@ -353,19 +354,22 @@ def main() -> int:
         # feed: per-step host input_ids (teacher forcing); record: list that gets (token, logits)
         st = dict(state)
         st["input_ids"] = first_token
+        if not host:
+            # the first step's inputs in place; every later step's come from k_decode_advance, one
+            # launch on the same stream after each step, so the executor's pointers stay fixed
+            # and its captured graph is relaunched as-is
+            mask_t.copy_(masks[0])
+            pos_t.copy_(pos_ids[0])
+            cpos_t.copy_(cpos[0])
         for s in range(n_steps):
             if feed is not None and s > 0:
                 st["input_ids"] = feed[s]
             if host:
                 # host-side per-step inputs (numpy), uploaded by DAGExecutor every step
                 st.update(host_steps[s])
-            else:
-                # per-step inputs are refreshed in place (device copies on the launch stream), so
-                # the executor's pointers stay fixed and its captured graph is relaunched as-is
-                mask_t.copy_(masks[s])
-                pos_t.copy_(pos_ids[s])
-                cpos_t.copy_(cpos[s])
             out = ex.execute(st)
+            if not host:
+                advance()
             st["input_ids"] = out["next_token"]
             if record is not None:
                 record.append((int(out["next_token"].native_handle.reshape(-1)[0].item()),

@@ -288,3 +288,16 @@ extern "C" __global__ void __launch_bounds__(256) k_bmm(const BmmArgs a) {
     st_f(a.c, t, a.c_dtype, acc);
   }
 }
+
+// k_decode_advance: one thread. Moves a greedy decode loop's position inputs to the next step
+// in place: p = cache_position + 1; cache_position = position_ids = p; mask[p] = 0 (the row
+// was open on 0 .. p - 1 and -inf after). One launch instead of three host-issued copies.
+extern "C" __global__ void __launch_bounds__(64) k_decode_advance(const AdvanceArgs a) {
+  if (threadIdx.x != 0) return;
+  const long long p = a.cpos[0] + 1;
+  if (p < 0 || p >= a.S) return;
+  a.cpos[0] = p;
+  a.pos[0] = p;
+  if (a.mask_bytes == 4) ((float*)a.mask)[p] = 0.f;
+  else ((uint16_t*)a.mask)[p] = 0;
+}

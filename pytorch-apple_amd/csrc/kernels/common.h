@@ -53,6 +53,15 @@ struct FillArgs {
   int pad;
 };
 
+struct AdvanceArgs {          // k_decode_advance: the next decode step's position inputs, on the device
+  void* mask;                 // [S] additive mask row, element size mask_bytes (2 or 4): entry p set to 0
+  long long* pos;             // position_ids [1, 1]
+  long long* cpos;            // cache_position [1]
+  long long S;
+  int mask_bytes;
+  int pad;
+};
+
 struct RMSNormArgs {          // out = w * round_n(x * rsqrt(mean(x^2) + eps)), one row per workgroup
   const void* x;
   const void* w;

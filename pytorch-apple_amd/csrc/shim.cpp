@@ -237,6 +237,7 @@ size_t hs_argsize(const char* s) {
   if (!strcmp(s, #T)) return sizeof(T);
   HS_SZ(CopyArgs)
   HS_SZ(FillArgs)
+  HS_SZ(AdvanceArgs)
   HS_SZ(RMSNormArgs)
   HS_SZ(EmbeddingArgs)
   HS_SZ(RopeTableArgs)

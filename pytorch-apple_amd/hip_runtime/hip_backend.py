@@ -192,5 +192,13 @@ class HIPBackend(Backend):
 
         return HIPExecutor(program, self)
 
+    def decode_advance(self, mask: HIPBuffer, pos: HIPBuffer, cpos: HIPBuffer):
+        """A callable that moves a decode loop's mask / position inputs to the next step on the
+        device (one launch of ``k_decode_advance`` on the current stream)."""
+        self._ensure()
+        from hip_runtime.hip_executor import DecodeAdvance
+
+        return DecodeAdvance(mask, pos, cpos)
+
     def synchronize(self):
         torch.cuda.synchronize(self._device)

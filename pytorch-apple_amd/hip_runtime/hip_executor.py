@@ -246,3 +246,26 @@ def _refs(args: dict):
             for x in v:
                 if isinstance(x, Ref):
                     yield x
+
+
+class DecodeAdvance:
+    """Advances a decode loop's ``attention_mask`` / ``position_ids`` / ``cache_position``
+    buffers to the next step on the device (``k_decode_advance``), ordered after the step on
+    the same stream: the loop needs no host-side input preparation between steps."""
+
+    def __init__(self, mask: HIPBuffer, pos: HIPBuffer, cpos: HIPBuffer):
+        m, p, c = mask.native_handle, pos.native_handle, cpos.native_handle
+        if m.element_size() not in (2, 4) or p.dtype != torch.int64 or c.dtype != torch.int64:
+            raise TypeError("DecodeAdvance needs a 16- or 32-bit mask and int64 positions")
+        self.device = m.device
+        mods = module_cache(self.device.index or 0)
+        mods.ensure_builtin("basic")
+        self._fn = mods.function("basic", "k_decode_advance")
+        self._args = STRUCTS["AdvanceArgs"](mask=m.data_ptr(), pos=p.data_ptr(), cpos=c.data_ptr(), S=m.numel(),
+                                            mask_bytes=m.element_size(), pad=0)
+        self._keep = (m, p, c)
+
+    def __call__(self, stream: int | None = None) -> None:
+        s = stream if stream is not None else _current_stream(self.device)
+        _shim.check(_shim.lib().hs_launch(self._fn, 1, 1, 1, 64, 1, 1, 0, s, C.byref(self._args),
+                                          C.sizeof(self._args)), "k_decode_advance")

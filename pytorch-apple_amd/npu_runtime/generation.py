@@ -21,8 +21,9 @@ What differs:
 * when a graph has an argmax output (``aten.argmax`` of the logits, int64), the
   token stays on the device and is fed back as the next ``input_ids``; on a backend
   whose buffers are torch tensors, the mask and positions are advanced in place on
-  the device, so a decode step needs no host round trip unless ``eos_token_id`` is
-  given (then each token is read back to test it, as the reference does);
+  the device (one ``decode_advance`` launch per step when the backend offers one), so a
+  decode step needs no host round trip unless ``eos_token_id`` is given (then each token
+  is read back to test it, as the reference does);
 * on such a backend the caches and the per-step inputs are allocated once per
   generator and rewritten in place by each call (caches zeroed), so every call
   hands the executors the same buffers and their captured HIP graphs are reused;
@@ -208,6 +209,9 @@ class GreedyGenerator:
         t1 = time.perf_counter()
         if fast:
             mask_t, pos_t, cpos_t = (b[k].native_handle for k in ("d_mask", "d_pos", "d_cpos"))
+            if "advance" not in b:   # one device launch per step when the backend has one
+                make = getattr(self.backend, "decode_advance", None)
+                b["advance"] = make(b["d_mask"], b["d_pos"], b["d_cpos"]) if make is not None else None
             b["d_ids"].native_handle.fill_(first)
             hist = torch.zeros(max_tokens - 1, dtype=torch.int64, device=pos_t.device)
             cur = b["d_ids"]
@@ -217,7 +221,9 @@ class GreedyGenerator:
         for step in range(max_tokens - 1):
             pos = n + step
             if fast:
-                if step:
+                if step and b["advance"] is not None:
+                    b["advance"]()
+                elif step:
                     mask_t[..., pos] = 0.0
                     pos_t.fill_(pos)
                     cpos_t.fill_(pos)
