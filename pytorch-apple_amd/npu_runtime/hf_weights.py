@@ -11,8 +11,8 @@ Restates the reference's loader (`examples/run_qwen_graph.py:30-100`,
 * a missing ``lm_head.weight`` takes the embedding matrix (tied embeddings);
 * a missing rotary ``inv_freq`` is synthesised as ``1 / theta^(2i/d)`` in fp32
   with ``theta`` = ``rope_theta`` from the directory's ``config.json`` (1e6 for
-  Qwen2.5; the reference hard-codes 10000 and writes it in bf16 — both differ
-  from what HF computes);
+  Qwen2.5; 10000, Qwen2Config's default, when the file has none), as HF builds it
+  (the reference hard-codes 10000 and writes it in bf16);
 * an empty ``lifted_tensor`` placeholder becomes an empty tensor;
 * floating tensors are converted to the IR's declared dtype (bf16 for Qwen2.5).
 
@@ -88,7 +88,8 @@ def load_safetensors_weights(model_dir: str, ir: dict, device: str | torch.devic
                 t = f.get_tensor(plan[key])
                 want = _TORCH.get(specs[key].get("dtype", "float32"), t.dtype)
                 out[key] = t.to(want) if t.dtype != want else t
-    theta = rope_theta if rope_theta is not None else _rope_theta(model_dir, 1e6)
+    # without rope_theta in config.json HF builds inv_freq with Qwen2Config's default, 10000
+    theta = rope_theta if rope_theta is not None else _rope_theta(model_dir, 10000.0)
     for key, w in specs.items():
         if key in out:
             continue

@@ -363,3 +363,25 @@ def test_full_size_qwen2_5_export_lowers_to_the_bench_launch_list():
     b = compile_subgraph(build_decode_ir(2048, argmax=True))
     assert len(a.steps) == 143
     assert [(s.kernel, s.grid, s.lds) for s in a.steps] == [(s.kernel, s.grid, s.lds) for s in b.steps]
+
+
+def test_safetensors_loader_theta_default_is_hfs(tmp_path, model):
+    """No rope_theta in config.json: inv_freq is built with Qwen2Config's default (10000),
+    as HF itself would build it."""
+    import json as _json
+
+    from npu_runtime.hf_weights import load_safetensors_weights
+    from transformers import Qwen2Config
+
+    model.save_pretrained(str(tmp_path), safe_serialization=True)
+    cfgp = tmp_path / "config.json"
+    c = _json.loads(cfgp.read_text())
+    c.pop("rope_theta", None)
+    c.pop("rope_parameters", None)
+    cfgp.write_text(_json.dumps(c))
+    ir = {"weights": [{"name": "model.rotary_emb.inv_freq", "shape": [64], "dtype": "float32"}]}
+    got = load_safetensors_weights(str(tmp_path), ir)["model.rotary_emb.inv_freq"]
+    theta = Qwen2Config().rope_parameters["rope_theta"] if hasattr(Qwen2Config(), "rope_parameters") \
+        else Qwen2Config().rope_theta
+    want = 1.0 / (theta ** (torch.arange(0, 128, 2, dtype=torch.int64).float() / 128))
+    assert theta == 10000.0 and torch.equal(got, want)
