@@ -174,7 +174,8 @@ class HIPExecutor:
         very objects of the previous call: a ``HIPBuffer`` never rebinds its tensor, so the
         same objects mean the same pointers (the loop of a decode step passes the same ones)."""
         bufs = self._buffers(inputs, weights)
-        if self._last_bufs is not None and bufs == self._last_bufs:
+        last = self._last_bufs
+        if last is not None and len(bufs) == len(last) and all(b is c for b, c in zip(bufs, last)):
             key = self._last_key
         else:
             ptrs = self._resolve(inputs, weights)
@@ -261,8 +262,8 @@ class DecodeAdvance:
         mods = module_cache(self.device.index or 0)
         mods.ensure_builtin("basic")
         self._fn = mods.function("basic", "k_decode_advance")
-        self._args = STRUCTS["AdvanceArgs"](mask=m.data_ptr(), pos=p.data_ptr(), cpos=c.data_ptr(), S=m.numel(),
-                                            mask_bytes=m.element_size(), pad=0)
+        self._args = STRUCTS["AdvanceArgs"](mask=m.data_ptr(), pos=p.data_ptr(), cpos=c.data_ptr(),
+                                            S=int(mask.shape[-1]), mask_bytes=m.element_size(), pad=0)
         self._keep = (m, p, c)
 
     def __call__(self, stream: int | None = None) -> None:
