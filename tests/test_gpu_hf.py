@@ -244,3 +244,26 @@ def test_long_generation_across_attention_splits(hf, backend):
         logits = m(seq).logits[0]
     bad = [i for i, tok in enumerate(res.tokens) if not token_ok(tok, logits[T - 1 + i])]
     assert not bad, f"steps {bad[:5]} differ from HF beyond a near tie"
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_decode_advance_moves_positions_and_opens_one_mask_entry(backend, dt):
+    """k_decode_advance: p = cache_position + 1 written to both position inputs, mask[p] = 0,
+    every other mask entry untouched; at the last cache position it changes nothing."""
+    S = 16
+    mask = torch.full((1, 1, 1, S), float("-inf"))
+    mask[..., :4] = 0.0
+    mb = backend.allocate_buffer(mask.to(dt))
+    pb = backend.allocate_buffer(torch.tensor([[3]]))
+    cb = backend.allocate_buffer(torch.tensor([3]))
+    adv = backend.decode_advance(mb, pb, cb)
+    for p in range(4, S):
+        print(f"[case] decode advance to {p} ({dt})", flush=True)
+        adv()
+        torch.cuda.synchronize()
+        m = mb.to_torch().float().reshape(-1).cpu()
+        assert int(pb.to_torch().item()) == p and int(cb.to_torch().item()) == p
+        assert m[:p + 1].eq(0).all() and m[p + 1:].eq(float("-inf")).all()
+    adv()   # at S - 1: no position past the cache
+    torch.cuda.synchronize()
+    assert int(cb.to_torch().item()) == S - 1 and int(pb.to_torch().item()) == S - 1
