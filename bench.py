@@ -152,14 +152,52 @@ def time_in_step(ex, indices, replays, stream) -> float:
     return total / (replays * len(indices))
 
 
-def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int, warmup: int = 3):
-    """CPU fallback (all-CPU plan through DAGExecutor, ATen bf16): ``warmup`` untimed steps, then
-    ``steps`` timed greedy decode steps from the same starting state. Returns the baseline record,
-    the greedy tokens and the logits (float32) of the timed steps."""
+def _cpu_decode_loop(ex, ir, x, n_steps, times=None, tokens=None, logits=None, feed=None):
+    """Greedy decode steps on a CPU-plan DAGExecutor from the state ``x`` (host arrays) at its
+    ``cache_position``. ``feed``: the input token of each step after the first (teacher forcing);
+    without it each step reads the previous step's argmax. Every step writes its cache row before
+    reading it, so re-running positions from the same first token reproduces a cold run exactly."""
     import numpy as np
     import torch
 
     from irgen.workloads import decode_mask, to_host
+
+    kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
+    kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
+    start = int(np.asarray(x["cache_position"]).reshape(-1)[0])
+    S = x["attention_mask"].shape[-1]
+    lname = ir["graph_outputs"][0]["name"]
+    mdt = torch.float32 if np.asarray(x["attention_mask"]).dtype == np.float32 else torch.bfloat16
+    ins = dict(x)
+    for s in range(n_steps):
+        pos = start + s
+        ins["attention_mask"] = to_host(decode_mask(S, pos).to(mdt))
+        ins["position_ids"] = np.array([[pos]], np.int64)
+        ins["cache_position"] = np.array([pos], np.int64)
+        if feed is not None and s > 0:
+            ins["input_ids"] = np.array([[feed[s - 1]]], np.int64)
+        t0 = time.perf_counter()
+        out = ex.execute(ins)
+        if times is not None:
+            times.append(time.perf_counter() - t0)
+        ins["input_ids"] = out["next_token"]
+        if tokens is not None:
+            tokens.append(int(np.asarray(out["next_token"]).reshape(-1)[0]))
+        if logits is not None:
+            lg = np.asarray(out[lname])
+            logits.append(torch.from_numpy(lg.view(np.int16)).view(torch.bfloat16).float().reshape(-1).numpy()
+                          if lg.dtype == np.uint16 else lg.astype(np.float32).reshape(-1))
+        for i, o in zip(kv_in, kv_out):
+            ins[i] = out[o]
+
+
+def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int, warmup: int = 3):
+    """CPU fallback (all-CPU plan through DAGExecutor, ATen bf16): ``warmup`` untimed steps, then
+    ``steps`` timed greedy decode steps from the same starting state. Returns the baseline record,
+    the greedy tokens and the logits (float32) of the timed steps."""
+    import torch
+
+    from irgen.workloads import to_host
     from npu_compiler import partition
     from npu_runtime import DAGExecutor
 
@@ -169,37 +207,10 @@ def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int, warmup: int = 3):
     x = {k: to_host(v.detach().cpu()) for k, v in inputs_dev.items()}
     ex = DAGExecutor(partition(ir, lambda *_: False), None)
     ex.load_weights(w)
-    kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
-    kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
     start = int(x["cache_position"][0])
-    S = x["attention_mask"].shape[-1]
-
-    lname = ir["graph_outputs"][0]["name"]
-
-    def loop(n_steps, times=None, tokens=None, logits=None):
-        # every step writes its cache row before reading it, so re-running positions from the same
-        # first token reproduces a cold run exactly
-        ins = dict(x)
-        for s in range(n_steps):
-            pos = start + s
-            ins["attention_mask"] = to_host(decode_mask(S, pos))
-            ins["position_ids"] = np.array([[pos]], np.int64)
-            ins["cache_position"] = np.array([pos], np.int64)
-            t0 = time.perf_counter()
-            out = ex.execute(ins)
-            if times is not None:
-                times.append(time.perf_counter() - t0)
-            ins["input_ids"] = out["next_token"]
-            if tokens is not None:
-                tokens.append(int(np.asarray(out["next_token"]).reshape(-1)[0]))
-                logits.append(torch.from_numpy(np.asarray(out[lname]).view(np.int16)).view(torch.bfloat16)
-                              .float().reshape(-1).numpy())
-            for i, o in zip(kv_in, kv_out):
-                ins[i] = out[o]
-
-    loop(warmup)
+    _cpu_decode_loop(ex, ir, x, warmup)
     times, tokens, logits = [], [], []
-    loop(steps, times, tokens, logits)
+    _cpu_decode_loop(ex, ir, x, steps, times, tokens, logits)
     med = statistics.median(times)
     total = sum(times)
     rec = {"value": round(steps / total, 4), "unit": "tok/s", "cores": n, "kind": "port",
@@ -210,8 +221,72 @@ def cpu_baseline(ir, weights_dev, inputs_dev, cfg, steps: int, warmup: int = 3):
     return rec, tokens, logits
 
 
+def fp32_teacher_forced(cfg, weights_dev, inputs_dev, feed, steps: int):
+    """The same decode graph evaluated in float32 on the CPU (plain ATen fp32: weights, caches and
+    mask upcast from the bf16 values), teacher-forced with ``feed``. Returns the logits of each
+    step: the reference point both bf16 paths are graded against."""
+    import dataclasses
+
+    import torch
+
+    from irgen.qwen import build_decode_ir
+    from irgen.workloads import to_host
+    from npu_compiler import partition
+    from npu_runtime import DAGExecutor
+
+    S = inputs_dev["attention_mask"].shape[-1]
+    ir32 = build_decode_ir(S, dataclasses.replace(cfg, dtype="float32"), argmax=True)
+    w = {k: (v.detach().cpu().float() if v.dtype == torch.bfloat16 else v.detach().cpu())
+         for k, v in weights_dev.items()}
+    x = {k: to_host(v.detach().cpu().float() if v.dtype == torch.bfloat16 else v.detach().cpu())
+         for k, v in inputs_dev.items()}
+    ex = DAGExecutor(partition(ir32, lambda *_: False), None)
+    ex.load_weights(w)
+    logits: list = []
+    _cpu_decode_loop(ex, ir32, x, steps, logits=logits, feed=feed)
+    return logits
+
+
+def bf16_ulp(v: float) -> float:
+    """Spacing of bf16 values (8 significant bits) at magnitude ``v``."""
+    import math
+
+    return 2.0 ** (math.floor(math.log2(max(abs(v), 1e-30))) - 7)
+
+
+def parity_vs_fp32(hip_rec, cpu_tokens, cpu_logits, f32_logits, tie_ulps: int = 4) -> dict:
+    """Grades both bf16 paths against the float32 evaluation of the same teacher-forced steps.
+
+    Per step: each path's largest logit difference from fp32 (relative to fp32's largest
+    |logit|) and whether its top-1 token is fp32's. A step is a near tie when fp32's own two
+    best logits are within ``tie_ulps`` bf16 ulps of the largest logit: a fixed window set by
+    the storage precision, not by either path's error. Raw agreement counts are reported
+    beside the near-tie counts."""
+    import numpy as np
+
+    n = len(f32_logits)
+    rec = {"steps": n, "tie_window": f"fp32 top-2 gap <= {tie_ulps} bf16 ulps of the largest logit"}
+    ties = []
+    for t in f32_logits:
+        top2 = np.partition(t, -2)[-2:]
+        ties.append(float(top2[1] - top2[0]) <= tie_ulps * bf16_ulp(float(np.abs(t).max())))
+    for name, toks, lgs in (("hip", [g for g, _ in hip_rec], [gl for _, gl in hip_rec]),
+                            ("cpu", cpu_tokens, cpu_logits)):
+        agree = [int(tk == int(np.argmax(t))) for tk, t in zip(toks, f32_logits)]
+        err = [float(np.abs(lg - t).max() / np.abs(t).max()) for lg, t in zip(lgs, f32_logits)]
+        rec[f"{name}_vs_fp32"] = {
+            "top1_agree": sum(agree),
+            "misses": n - sum(agree),
+            "misses_at_near_ties": sum(1 for a, tie in zip(agree, ties) if not a and tie),
+            "logits_max_rel_err": round(max(err), 4),
+            "logits_mean_rel_err": round(float(np.mean(err)), 4)}
+    rec["near_tie_steps"] = sum(ties)
+    return rec
+
+
 def run_copy_probe(device_index: int, stream, mib: int = 512, repeats: int = 3) -> float:
-    """Launch the library's plain copy kernel (``k_copy``) over ``mib`` MiB of bf16, ``repeats`` times.
+    """Launch the library's plain copy kernel (``k_copy16``, the contiguous form of the copy
+    lowering) over ``mib`` MiB of bf16, ``repeats`` times.
 
     Its known traffic (``mib`` MiB read, ``mib`` MiB written per launch) calibrates the
     FETCH_SIZE / WRITE_SIZE counters that give the ``traffic`` figure. Returns the average
@@ -226,26 +301,25 @@ def run_copy_probe(device_index: int, stream, mib: int = 512, repeats: int = 3) 
     src = torch.ones(n, dtype=torch.bfloat16, device=f"cuda:{device_index}")
     dst = torch.empty_like(src)
     a = STRUCTS["CopyArgs"]()
-    a.dst, a.src, a.n, a.ndim = dst.data_ptr(), src.data_ptr(), n, 1
-    a.shape[0], a.sstride[0], a.dstride[0] = n, 1, 1
+    a.dst, a.src, a.n, a.ndim = dst.data_ptr(), src.data_ptr(), n * 2 // 16, 1   # n: 16-byte chunks
     a.sdtype = a.ddtype = 2
     mods = module_cache(device_index)
     mods.ensure_builtin("basic")
-    fn = mods.function("basic", "k_copy")
+    fn = mods.function("basic", "k_copy16")
     lib = _shim.lib()
     e0, e1 = C.c_void_p(), C.c_void_p()
     _shim.check(lib.hs_event_create(C.byref(e0)))
     _shim.check(lib.hs_event_create(C.byref(e1)))
     _shim.check(lib.hs_event_record(e0, stream))
     for _ in range(repeats):
-        _shim.check(lib.hs_launch(fn, 4096, 1, 1, 256, 1, 1, 0, stream, C.byref(a), C.sizeof(a)), "k_copy")
+        _shim.check(lib.hs_launch(fn, 8192, 1, 1, 256, 1, 1, 0, stream, C.byref(a), C.sizeof(a)), "k_copy16")
     _shim.check(lib.hs_event_record(e1, stream))
     _shim.check(lib.hs_event_sync(e1))
     ms = C.c_float()
     _shim.check(lib.hs_event_elapsed_ms(e0, e1, C.byref(ms)))
     lib.hs_event_destroy(e0)
     lib.hs_event_destroy(e1)
-    if not torch.equal(dst[:4096], src[:4096]):
+    if not torch.equal(dst, src):
         raise RuntimeError("copy probe produced wrong data")
     return ms.value / repeats
 
@@ -279,6 +353,8 @@ def main() -> int:
     ap.add_argument("--copy-probe-mib", type=int, default=512,
                     help="size of the k_copy calibration launches run after timing (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-fp32-parity", action="store_true",
+                    help="skip grading the parity pass against a float32 evaluation of the same steps")
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--workload", choices=("decode", "prefill", "resnet50", "generate", "mlp", "attention"),
                     default="decode",
@@ -386,6 +462,7 @@ def main() -> int:
     run(args.steps)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    advance.check()   # no step moved past the cache end
     ms = elapsed * 1e3 / args.steps
     toks = args.steps / elapsed
     valid_avg = start + (args.steps + 1) / 2.0
@@ -437,7 +514,7 @@ def main() -> int:
     probe = None
     if args.copy_probe_mib > 0:
         pm = run_copy_probe(0, stream, args.copy_probe_mib)
-        probe = {"kernel": "k_copy", "mib": args.copy_probe_mib, "avg_ms": round(pm, 4),
+        probe = {"kernel": "k_copy16", "mib": args.copy_probe_mib, "avg_ms": round(pm, 4),
                  "GBs": round(2 * args.copy_probe_mib * (1 << 20) / (pm * 1e-3) / 1e9, 1)}
         log(f"copy probe: {probe}")
 
@@ -457,13 +534,13 @@ def main() -> int:
         run(n_check, feed=feed, record=rec)
         agree = sum(int(g == c) for (g, _), c in zip(rec, cpu_tokens))
         rel = max(float(np.abs(gl - cl).max() / np.abs(cl).max()) for (_, gl), cl in zip(rec, cpu_logits))
-        # a disagreement is a near tie when the CPU logits of the two tokens differ by less than the
-        # step's largest GPU-vs-CPU logit difference
-        ties = sum(1 for (g, gl), c, cl in zip(rec, cpu_tokens, cpu_logits)
-                   if g != c and cl[c] - cl[g] <= np.abs(gl - cl).max())
-        cpu["parity"] = {"steps": n_check, "top1_agree": agree, "disagree_near_ties": ties,
-                         "logits_max_rel_err": round(rel, 4),
-                         "mode": "device loop teacher-forced with the CPU greedy tokens"}
+        cpu["parity"] = {"steps": n_check, "hip_cpu_top1_agree": agree, "hip_cpu_logits_max_rel_err": round(rel, 4),
+                         "mode": "device loop teacher-forced with the CPU greedy tokens; both graded against "
+                                 "the same steps evaluated in float32 on the CPU"}
+        if not args.no_fp32_parity:
+            log("fp32 reference of the same teacher-forced steps")
+            f32 = fp32_teacher_forced(cfg, weights, x_cpu, cpu_tokens[:n_check - 1], n_check)
+            cpu["parity"].update(parity_vs_fp32(rec, cpu_tokens[:n_check], cpu_logits[:n_check], f32))
         log(f"parity: {cpu['parity']}")
 
     line = {

@@ -74,6 +74,18 @@ int hs_memcpy_htod(void* dst, const void* src, size_t n, void* stream);
 int hs_memcpy_dtoh(void* dst, const void* src, size_t n, void* stream);
 int hs_memcpy_dtod(void* dst, const void* src, size_t n, void* stream);
 
+/* Device argmax of every row of a row-major [rows, cols] bf16 (dtype 2) or fp16 (dtype 1)
+ * matrix, written as int64 to out[rows]: the largest value's first index (np.argmax's tie
+ * rule), NaN above every number, -0.0 equal to +0.0. Replaces the host-side
+ * np.argmax(logits[0, -1, :]) of the reference's generation loops (examples/run_qwen.py:125,180;
+ * examples/run_qwen_graph.py:227) for callers that hold logits on the device.
+ * x: 16-byte aligned; cols: a positive multiple of 8; rows <= 65535. workspace: device memory of
+ * at least hs_argmax_workspace_bytes(rows, cols) bytes (8-byte aligned) for the per-segment keys;
+ * its contents need no initialisation. Two launches on `stream`, nothing allocated. */
+size_t hs_argmax_workspace_bytes(int64_t rows, int64_t cols);
+int hs_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 /* sizeof() of the kernel argument struct with the given name (e.g. "LinearArgs"),
  * or 0 when unknown; lets the host check its ctypes mirrors. */
 size_t hs_argsize(const char* struct_name);

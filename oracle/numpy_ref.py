@@ -171,6 +171,8 @@ def _bin(op, a, b, out_dtype, alpha=1.0):
         r = a * b
     elif op == "div":
         r = np.asarray(a, np.float32) / np.asarray(b, np.float32)
+    elif op in ("maximum", "minimum"):   # NaN in either operand gives NaN (torch.maximum / minimum)
+        r = np.maximum(a, b) if op == "maximum" else np.minimum(a, b)
     else:
         raise ValueError(op)
     return round_to(r, out_dtype)
@@ -199,6 +201,10 @@ def _unary(op, a, out_dtype):
             r = np.tanh(x)
         elif op == "sqrt":
             r = np.sqrt(x)
+        elif op == "abs":
+            r = np.abs(x)
+        elif op == "reciprocal":
+            r = np.float32(1.0) / x
         else:
             raise ValueError(op)
     return round_to(r, out_dtype)
@@ -233,11 +239,12 @@ def run_node(node: dict, env: dict) -> None:
         put(c.reshape(oshape), 0)
         put(s.reshape(oshape), 1)
         return
-    if short in ("add", "sub", "mul", "div", "add_", "mul_"):
+    if short in ("add", "sub", "mul", "div", "add_", "mul_", "maximum", "minimum"):
         other = ins[1] if len(ins) > 1 else np.float32(a["other"]) if od in FLOAT else a["other"]
         put(_bin(short.rstrip("_"), ins[0], other, od, float(a.get("alpha", 1.0))))
         return
-    if short in ("neg", "rsqrt", "silu", "relu", "relu_", "cos", "sin", "exp", "sigmoid", "tanh", "sqrt"):
+    if short in ("neg", "rsqrt", "silu", "relu", "relu_", "cos", "sin", "exp", "sigmoid", "tanh", "sqrt", "abs",
+                 "reciprocal"):
         put(_unary(short.rstrip("_"), ins[0], od))
         return
     if op == "aten.pow.Tensor_Scalar":

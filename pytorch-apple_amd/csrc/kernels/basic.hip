@@ -31,6 +31,24 @@ extern "C" __global__ void __launch_bounds__(256) k_copy(const CopyArgs a) {
   }
 }
 
+// Contiguous copy of a.n 16-byte chunks (src and dst 16-byte aligned, same dtype): the generic
+// kernel above spends its time on per-element index arithmetic; here each thread keeps four
+// 16-byte loads in flight per pass of a grid-stride loop.
+extern "C" __global__ void __launch_bounds__(256) k_copy16(const CopyArgs a) {
+  const uint4* s = (const uint4*)a.src;
+  uint4* d = (uint4*)a.dst;
+  const long long n = a.n, T = (long long)gridDim.x * blockDim.x;
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i + 3 * T < n; i += 4 * T) {
+    const uint4 v0 = s[i], v1 = s[i + T], v2 = s[i + 2 * T], v3 = s[i + 3 * T];
+    d[i] = v0;
+    d[i + T] = v1;
+    d[i + 2 * T] = v2;
+    d[i + 3 * T] = v3;
+  }
+  for (; i < n; i += T) d[i] = s[i];
+}
+
 extern "C" __global__ void __launch_bounds__(256) k_fill(const FillArgs a) {
   const long long stride = (long long)gridDim.x * blockDim.x;
   for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += stride) {
@@ -292,10 +310,14 @@ extern "C" __global__ void __launch_bounds__(256) k_bmm(const BmmArgs a) {
 // k_decode_advance: one thread. Moves a greedy decode loop's position inputs to the next step
 // in place: p = cache_position + 1; cache_position = position_ids = p; mask[p] = 0 (the row
 // was open on 0 .. p - 1 and -inf after). One launch instead of three host-issued copies.
+// A step past the cache end (p >= S) changes nothing and sets *overflow, which the host checks.
 extern "C" __global__ void __launch_bounds__(64) k_decode_advance(const AdvanceArgs a) {
   if (threadIdx.x != 0) return;
   const long long p = a.cpos[0] + 1;
-  if (p < 0 || p >= a.S) return;
+  if (p < 0 || p >= a.S) {
+    a.overflow[0] = 1;
+    return;
+  }
   a.cpos[0] = p;
   a.pos[0] = p;
   if (a.mask_bytes == 4) ((float*)a.mask)[p] = 0.f;

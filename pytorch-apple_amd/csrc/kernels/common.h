@@ -57,6 +57,7 @@ struct AdvanceArgs {          // k_decode_advance: the next decode step's positi
   void* mask;                 // [S] additive mask row, element size mask_bytes (2 or 4): entry p set to 0
   long long* pos;             // position_ids [1, 1]
   long long* cpos;            // cache_position [1]
+  int* overflow;              // set to 1 when a step would move past the cache end (nothing else written)
   long long S;
   int mask_bytes;
   int pad;
@@ -657,6 +658,45 @@ __device__ __forceinline__ void st_f(void* p, long long i, int dt, float f) {
   }
 }
 
+// Eight consecutive float-typed elements from element i (16-byte aligned for 16-bit dtypes, 32-byte
+// for fp32): one or two 16-byte loads. ld1x8_f repeats element i eight times (an operand broadcast
+// along the last dimension). st8_f writes eight values from element i with 16-byte stores.
+__device__ __forceinline__ void ld8_f(const void* p, long long i, int dt, float* v) {
+  if (dt == HS_F32) {
+    const float4 a = ((const float4*)p)[i >> 2], b = ((const float4*)p)[(i >> 2) + 1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    return;
+  }
+  const uint4 q = ((const uint4*)p)[i >> 3];
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t lo = (uint16_t)(w[j] & 0xffffu), hi = (uint16_t)(w[j] >> 16);
+    v[2 * j] = dt == HS_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+    v[2 * j + 1] = dt == HS_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+  }
+}
+__device__ __forceinline__ void ld1x8_f(const void* p, long long i, int dt, float* v) {
+  const float x = ld_f(p, i, dt);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = x;
+}
+__device__ __forceinline__ void st8_f(void* p, long long i, int dt, const float* v) {
+  if (dt == HS_F32) {
+    ((float4*)p)[i >> 2] = make_float4(v[0], v[1], v[2], v[3]);
+    ((float4*)p)[(i >> 2) + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    return;
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t lo = dt == HS_BF16 ? f32_to_bf16(v[2 * j]) : f32_to_f16(v[2 * j]);
+    const uint16_t hi = dt == HS_BF16 ? f32_to_bf16(v[2 * j + 1]) : f32_to_f16(v[2 * j + 1]);
+    w[j] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  ((uint4*)p)[i >> 3] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // Cross-lane moves without LDS: DPP (quad permutes, rotations within a row of 16 lanes)
 // and readlane. They need every lane of the wave active, which holds at every call site.
 #define HS_DPP(v, ctrl) \
@@ -682,6 +722,83 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, HS_DPP(v, HS_ROW_ROR4));
   v = fmaxf(v, HS_DPP(v, HS_ROW_ROR8));
   return fmaxf(fmaxf(HS_RL(v, 0), HS_RL(v, 16)), fmaxf(HS_RL(v, 32), HS_RL(v, 48)));
+}
+
+// ---------------------------------------------------------------- argmax over long rows
+//
+// argmax_part_body: workgroup (part, row) of 256 threads scans columns [part * seg, (part + 1) * seg)
+// of row `row` with 16-byte loads (all of a thread's loads of a pass in flight together) and
+// writes one key to slot[row * parts + part]; argmax_finalize_body: one workgroup per row takes
+// the largest of its `parts` keys. The key orders like torch.argmax / np.argmax: larger value
+// first, NaN above every number, -0.0 equal to +0.0, then the smaller index.
+__device__ __forceinline__ unsigned long long argmax_key_nan(float v, unsigned idx) {
+  uint32_t b = __float_as_uint(v);
+  b = (v == 0.f) ? 0u : b;
+  const uint32_t o = (v != v) ? 0xFFFFFFFFu : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
+  return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+__device__ __forceinline__ void argmax_part_body(const ArgmaxPartArgs& a, long long part, long long row) {
+  __shared__ unsigned long long red[4];
+  const long long c0 = part * a.seg, c1 = min(c0 + a.seg, a.cols);
+  const uint16_t* xr = (const uint16_t*)a.x + row * a.cols;
+  const bool f16 = a.x_dtype == HS_F16;
+  unsigned long long best = 0ull;
+  constexpr int U = 4;
+  for (long long c = c0 + threadIdx.x * 8; c < c1; c += 256 * 8 * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long cc = c + (long long)u * 256 * 8;
+      v[u] = cc < c1 ? *(const uint4*)(xr + cc) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long cc = c + (long long)u * 256 * 8;
+      if (cc >= c1) break;
+      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint16_t hbits = (j & 1) ? (uint16_t)(w[j >> 1] >> 16) : (uint16_t)(w[j >> 1] & 0xffffu);
+        const float f = f16 ? f16_to_f32(hbits) : bf16_to_f32(hbits);
+        const unsigned long long k = argmax_key_nan(f, (unsigned)(cc + j));
+        best = k > best ? k : best;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long other = __shfl_xor(best, o, 64);
+    best = other > best ? other : best;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = red[0];
+    for (int w = 1; w < 4; ++w) k = red[w] > k ? red[w] : k;
+    a.slot[row * a.parts + part] = k;
+  }
+}
+
+__device__ __forceinline__ void argmax_finalize_body(const ArgmaxFinalizeArgs& a, long long m) {
+  __shared__ unsigned long long red[256];
+  if (m >= a.rows) return;
+  unsigned long long k = 0ull;
+  for (int i = threadIdx.x; i < a.parts; i += 256) {
+    const unsigned long long v = a.slot[m * a.parts + i];
+    k = v > k ? v : k;
+  }
+  red[threadIdx.x] = k;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o && red[threadIdx.x + o] > red[threadIdx.x]) red[threadIdx.x] = red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const long long idx = (long long)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFull));
+    if (a.out_dtype == HS_I64) ((long long*)a.out)[m] = idx;
+    else ((int*)a.out)[m] = (int)idx;
+  }
 }
 
 // sum over a 256-thread workgroup; every thread gets the result

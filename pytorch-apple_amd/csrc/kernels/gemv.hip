@@ -8,7 +8,9 @@
 //   epilogue  BIAS   out = round(acc + b)
 //             RESID  out = round(r + round(acc + b))                     (linear then residual add)
 //             SILU   out = round(round(silu(round(acc_g))) * round(acc_u)) (gate/up pair, SiLU*mul)
-//             ARGMAX out = round(acc); atomicMax of (ordered value, ~index) per activation row
+//             ARGMAX out = round(acc); each workgroup writes the largest (ordered value, ~index) key
+//                    of its rows to its own slot per activation row (no atomics); k_argmax_finalize
+//                    reduces the slots
 // k_qkv_rope additionally applies rotary embedding to q/k row pairs (d, d+D/2) and
 // writes k/v straight into the static caches at cache_position (index_copy in place).
 #include "common.h"
@@ -408,25 +410,7 @@ GEMV_KERNEL(k_gemv_attn16_resid_r2, PRO_ATTN16, EPI_RESID, 2, 1)
 // One workgroup per activation row: the largest of the row's per-workgroup keys is the
 // maximum logit with the smallest index among equal maxima (np.argmax's rule).
 extern "C" __global__ void __launch_bounds__(256) k_argmax_finalize(const ArgmaxFinalizeArgs a) {
-  __shared__ unsigned long long red[256];
-  const long long m = blockIdx.x;
-  if (m >= a.rows) return;
-  unsigned long long k = 0ull;
-  for (int i = threadIdx.x; i < a.parts; i += 256) {
-    const unsigned long long v = a.slot[m * a.parts + i];
-    k = v > k ? v : k;
-  }
-  red[threadIdx.x] = k;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (threadIdx.x < o && red[threadIdx.x + o] > red[threadIdx.x]) red[threadIdx.x] = red[threadIdx.x + o];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    const long long idx = (long long)(0xFFFFFFFFu - (uint32_t)(red[0] & 0xFFFFFFFFull));
-    if (a.out_dtype == HS_I64) ((long long*)a.out)[m] = idx;
-    else ((int*)a.out)[m] = (int)idx;
-  }
+  argmax_finalize_body(a, blockIdx.x);
 }
 
 // ------------------------------------------------------------------------ q/k/v + RoPE + cache
@@ -593,57 +577,9 @@ extern "C" __global__ void __launch_bounds__(256) k_rope_cache(const RopeCacheAr
 
 // ------------------------------------------------------------------ argmax over long rows
 //
-// k_argmax_part: grid (parts, rows), 256 threads; workgroup (p, r) scans columns
-// [p * seg, (p + 1) * seg) of row r with 16-byte loads (all of a thread's loads in flight
-// together) and writes one key to slot[r * parts + p]; k_argmax_finalize reduces the keys of
-// a row. The key orders like torch.argmax / np.argmax: larger value first, NaN above every
-// number, -0.0 equal to +0.0, then the smaller index.
-__device__ __forceinline__ unsigned long long argmax_key_nan(float v, unsigned idx) {
-  uint32_t b = __float_as_uint(v);
-  b = (v == 0.f) ? 0u : b;
-  const uint32_t o = (v != v) ? 0xFFFFFFFFu : ((b & 0x80000000u) ? ~b : (b | 0x80000000u));
-  return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
-}
-
+// k_argmax_part: grid (parts, rows), 256 threads; k_argmax_finalize: one workgroup per row.
+// The bodies (argmax_part_body / argmax_finalize_body in common.h) are shared with the shim's
+// hs_argmax_rows entry points.
 extern "C" __global__ void __launch_bounds__(256) k_argmax_part(const ArgmaxPartArgs a) {
-  __shared__ unsigned long long red[4];
-  const long long row = blockIdx.y;
-  const long long c0 = (long long)blockIdx.x * a.seg, c1 = min(c0 + a.seg, a.cols);
-  const uint16_t* xr = (const uint16_t*)a.x + row * a.cols;
-  const bool f16 = a.x_dtype == HS_F16;
-  unsigned long long best = 0ull;
-  constexpr int U = 4;
-  for (long long c = c0 + threadIdx.x * 8; c < c1; c += 256 * 8 * U) {
-    uint4 v[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long long cc = c + (long long)u * 256 * 8;
-      v[u] = cc < c1 ? *(const uint4*)(xr + cc) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long long cc = c + (long long)u * 256 * 8;
-      if (cc >= c1) break;
-      const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint16_t hbits = (j & 1) ? (uint16_t)(w[j >> 1] >> 16) : (uint16_t)(w[j >> 1] & 0xffffu);
-        const float f = f16 ? f16_to_f32(hbits) : bf16_to_f32(hbits);
-        const unsigned long long k = argmax_key_nan(f, (unsigned)(cc + j));
-        best = k > best ? k : best;
-      }
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long other = __shfl_xor(best, o, 64);
-    best = other > best ? other : best;
-  }
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned long long k = red[0];
-    for (int w = 1; w < 4; ++w) k = red[w] > k ? red[w] : k;
-    a.slot[row * a.parts + blockIdx.x] = k;
-  }
+  argmax_part_body(a, blockIdx.x, blockIdx.y);
 }

@@ -27,6 +27,51 @@ int fail_hip(hipError_t e, const char* what) {
     if (e_ != hipSuccess) return fail_hip(e_, #call);   \
   } while (0)
 
+// ---- device argmax over rows (hs_argmax_rows): the bodies are the code objects' k_argmax_part /
+// k_argmax_finalize, compiled into this library so the entry point needs no module load
+__global__ void __launch_bounds__(256) shim_argmax_part(const ArgmaxPartArgs a) {
+  argmax_part_body(a, blockIdx.x, blockIdx.y);
+}
+__global__ void __launch_bounds__(256) shim_argmax_finalize(const ArgmaxFinalizeArgs a) {
+  argmax_finalize_body(a, blockIdx.x);
+}
+
+constexpr int64_t kArgmaxSeg = 8192;    // columns per part (one workgroup)
+constexpr int64_t kArgmaxMaxRows = 65535;
+
+int64_t argmax_parts(int64_t cols) { return (cols + kArgmaxSeg - 1) / kArgmaxSeg; }
+
+int fail_arg(const std::string& what) {
+  g_err = what;
+  return (int)hipErrorInvalidValue;
+}
+
+// Checks the operands of a row argmax; 0 when the call may launch.
+int argmax_check(const void* x, int dtype, int64_t rows, int64_t cols, const int64_t* out) {
+  if (rows < 0 || rows > kArgmaxMaxRows) return fail_arg("hs_argmax_rows: rows must be in [0, 65535]");
+  if (rows == 0) return 0;
+  if (!x || !out) return fail_arg("hs_argmax_rows: null x or out");
+  if (dtype != HS_BF16 && dtype != HS_F16) return fail_arg("hs_argmax_rows: dtype must be bf16 (2) or fp16 (1)");
+  if (cols < 8 || cols % 8 != 0 || cols > 0xFFFFFFFFll)
+    return fail_arg("hs_argmax_rows: cols must be a positive multiple of 8 below 2^32");
+  if (((uintptr_t)x) % 16 != 0) return fail_arg("hs_argmax_rows: x must be 16-byte aligned");
+  return 0;
+}
+
+// Two launches on `s`: per-part keys into `slot` ([rows, parts] 64-bit keys), then one index per row.
+int argmax_launch(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, unsigned long long* slot,
+                  hipStream_t s) {
+  const int64_t parts = argmax_parts(cols);
+  const int64_t seg = (cols + parts - 1) / parts + 7 & ~(int64_t)7;
+  const ArgmaxPartArgs pa{x, slot, rows, cols, seg, dtype, (int)parts};
+  hipLaunchKernelGGL(shim_argmax_part, dim3((unsigned)parts, (unsigned)rows), dim3(256), 0, s, pa);
+  HS_CHECK(hipGetLastError());
+  const ArgmaxFinalizeArgs fa{slot, out, rows, (int)parts, HS_I64};
+  hipLaunchKernelGGL(shim_argmax_finalize, dim3((unsigned)rows), dim3(256), 0, s, fa);
+  HS_CHECK(hipGetLastError());
+  return 0;
+}
+
 int launch_one(const hs_launch_rec& r, hipStream_t s) {
   size_t sz = r.kernarg_size;
   void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(r.kernarg), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
@@ -230,6 +275,23 @@ int hs_memcpy_dtoh(void* dst, const void* src, size_t n, void* stream) {
 int hs_memcpy_dtod(void* dst, const void* src, size_t n, void* stream) {
   HS_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, (hipStream_t)stream));
   return 0;
+}
+
+size_t hs_argmax_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)rows * (size_t)argmax_parts(cols) * sizeof(unsigned long long);
+}
+
+int hs_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  if (int rc = argmax_check(x, dtype, rows, cols, out)) return rc;
+  if (rows == 0) return 0;
+  const size_t need = hs_argmax_workspace_bytes(rows, cols);
+  if (!workspace || workspace_bytes < need)
+    return fail_arg("hs_argmax_rows: workspace smaller than hs_argmax_workspace_bytes(rows, cols) = " +
+                    std::to_string(need));
+  if (((uintptr_t)workspace) % 8 != 0) return fail_arg("hs_argmax_rows: workspace must be 8-byte aligned");
+  return argmax_launch(x, dtype, rows, cols, out, (unsigned long long*)workspace, (hipStream_t)stream);
 }
 
 size_t hs_argsize(const char* s) {

@@ -6,7 +6,8 @@ each separately at executor init (`cuda_compiler/buffer_planner.py:25-77`,
 flattening fused outputs (D11). Here aliases own no storage at all, and every
 real intermediate gets an offset in one device arena: storages whose live ranges
 (first writing step .. last reading step) overlap never share bytes, graph
-outputs stay live to the end of the program, and "persistent" storages (tickets
+outputs are live for the whole program (no other storage ever shares their bytes,
+so an output can be fed back as the next run's input), and "persistent" storages (tickets
 of the split attention, which must read zero at every launch) are never shared.
 """
 
@@ -36,8 +37,12 @@ def plan_arena(steps: list[LaunchStep], storages: dict[str, Storage], live_to_en
                 s.first = i
             s.last = i
     end = len(steps)
+    # graph outputs hold their bytes for the whole program: a caller may feed an output back as
+    # the next run's input (the greedy loop's next token, KV caches), and no step of that run may
+    # write those bytes before its last read of the input
     for name in live_to_end:
         if name in storages and storages[name].first >= 0:
+            storages[name].first = 0
             storages[name].last = end
     off = 0
     for s in storages.values():

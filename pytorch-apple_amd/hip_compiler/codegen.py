@@ -49,8 +49,9 @@ _BINARY = {
     "aten.mul.Tensor": "(({a}) * ({b}))",
     "aten.mul_.Tensor": "(({a}) * ({b}))",
     "aten.div.Tensor": "(({a}) / ({b}))",
-    "aten.maximum.default": "fmaxf(({a}), ({b}))",
-    "aten.minimum.default": "fminf(({a}), ({b}))",
+    # NaN in either operand gives NaN, as torch.maximum / minimum (fmaxf alone would drop it)
+    "aten.maximum.default": "(({a}) != ({a}) ? ({a}) : (({b}) != ({b}) ? ({b}) : fmaxf(({a}), ({b}))))",
+    "aten.minimum.default": "(({a}) != ({a}) ? ({a}) : (({b}) != ({b}) ? ({b}) : fminf(({a}), ({b}))))",
 }
 EW_OPS = set(_UNARY_F) | set(_BINARY) | {"aten.pow.Tensor_Scalar"}
 
@@ -71,15 +72,46 @@ def _lit(x: float) -> str:
     return f"(float)({float(x)!r})"
 
 
+VEC = 8   # elements per thread on the vector path (16 bytes of a 16-bit dtype)
+
+
+def vector_ok(ext: list[TView], out_shape: tuple[int, ...], out_dtype: str) -> bool:
+    """Whether a chain can run 8 consecutive output elements per thread with 16-byte accesses:
+    float operands and result, the last dimension a multiple of 8, and every operand either
+    contiguous along it (stride 1, its 8-element groups 16-byte aligned for 16-bit dtypes and
+    32-byte aligned for fp32: offset and outer strides multiples of 8) or broadcast along it
+    (stride 0: one load serves the 8 elements)."""
+    if not out_shape or out_dtype not in FLOAT_DTYPES or out_shape[-1] % VEC:
+        return False
+    for v in ext:
+        if v.dtype not in FLOAT_DTYPES:
+            return False
+        if not v.shape:
+            continue
+        st = list(v.strides)
+        if st[-1] == 0:
+            continue
+        if st[-1] != 1 or v.offset % VEC or any(s % VEC for s in st[:-1]):
+            return False
+    return True
+
+
 def generate_chain(ops: list[ChainOp], ext: list[TView], out_shape: tuple[int, ...], out_dtype: str) -> tuple[str, str]:
-    """Return ``(kernel_name, source)`` computing ``ops`` over ``out_shape``."""
+    """Return ``(kernel_name, source)`` computing ``ops`` over ``out_shape``.
+
+    Where ``vector_ok`` holds, thread g computes output elements 8g..8g+7 (one row of the last
+    dimension, so they share every outer coordinate): 16-byte loads of each contiguous operand,
+    one load of each operand broadcast along the last dimension, the chain evaluated per
+    element at the same rounding points, and 16-byte stores (``n`` is then the number of
+    8-element groups). Otherwise one element per thread."""
     if len(ext) > MAX_CHAIN_INPUTS:
         raise ValueError("too many chain inputs")
+    vec = vector_ok(ext, out_shape, out_dtype)
     nd = max(len(out_shape), 1)
     shape = list(out_shape) if out_shape else [1]
     body: list[str] = []
     # coordinates of element i of the contiguous output
-    body.append("    long long r_ = i;")
+    body.append(f"    long long r_ = i{' * 8' if vec else ''};")
     for d in range(nd - 1, -1, -1):
         if shape[d] == 1:
             body.append(f"    const long long c{d} = 0;")
@@ -94,10 +126,20 @@ def generate_chain(ops: list[ChainOp], ext: list[TView], out_shape: tuple[int, .
         terms = [f"c{d} * {strides[d]}LL" for d in range(nd) if strides[d] != 0 and shape[d] != 1]
         off = " + ".join(terms) if terms else "0LL"
         dt = v.dtype
-        if dt in FLOAT_DTYPES:
+        if vec:
+            wide = v.shape and strides[-1] == 1
+            fn = "ld8_f" if wide else "ld1x8_f"
+            body.append(f"    float e{k}v[8]; {fn}(a.in[{k}], {off}, {DTYPE_CODE[dt]}, e{k}v);")
+        elif dt in FLOAT_DTYPES:
             body.append(f"    const float e{k} = ld_f(a.in[{k}], {off}, {DTYPE_CODE[dt]});")
         else:
             body.append(f"    const long long e{k} = ld_i(a.in[{k}], {off}, {DTYPE_CODE[dt]});")
+    if vec:
+        body.append("    float res_[8];")
+        body.append("#pragma unroll")
+        body.append("    for (int j_ = 0; j_ < 8; ++j_) {")
+        for k in range(len(ext)):
+            body.append(f"    const float e{k} = e{k}v[j_];")
     vals: list[tuple[str, str]] = []     # (expr var, dtype)
 
     def operand(o, want_float: bool) -> str:
@@ -145,7 +187,11 @@ def generate_chain(ops: list[ChainOp], ext: list[TView], out_shape: tuple[int, .
         body.append(f"    const {ctype} t{j} = {expr};")
         vals.append((f"t{j}", op.out_dtype))
     last, ldt = vals[-1]
-    if out_dtype in FLOAT_DTYPES:
+    if vec:
+        body.append(f"    res_[j_] = {last if ldt in FLOAT_DTYPES else f'(float){last}'};")
+        body.append("    }")
+        body.append(f"    st8_f(a.out, i * 8, {DTYPE_CODE[out_dtype]}, res_);")
+    elif out_dtype in FLOAT_DTYPES:
         src_last = last if ldt in FLOAT_DTYPES else f"(float){last}"
         body.append(f"    st_f(a.out, i, {DTYPE_CODE[out_dtype]}, {src_last});")
     elif out_dtype == "int64":

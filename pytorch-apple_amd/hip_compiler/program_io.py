@@ -102,21 +102,43 @@ def load_program(path: str) -> HIPProgram:
 
 
 def compiler_fingerprint() -> str:
-    """Hash of the compiler's own sources: a cached program is reused only with the
+    """Hash of every source the lowering depends on: the compiler itself, the IR reader and
+    partitioner it imports (``npu_compiler``) and the kernel-argument layouts the launch records
+    are packed against (``hip_runtime/kernels.py``). A cached program is reused only with the
     lowering that produced it."""
     h = hashlib.sha256()
     here = os.path.dirname(os.path.abspath(__file__))
-    for name in sorted(os.listdir(here)):
-        if name.endswith(".py"):
-            with open(os.path.join(here, name), "rb") as f:
-                h.update(name.encode() + b"\0" + f.read())
+    pkg = os.path.dirname(here)
+    files = [os.path.join(here, n) for n in sorted(os.listdir(here)) if n.endswith(".py")]
+    npu = os.path.join(pkg, "npu_compiler")
+    files += [os.path.join(npu, n) for n in sorted(os.listdir(npu)) if n.endswith(".py")]
+    files.append(os.path.join(pkg, "hip_runtime", "kernels.py"))
+    for path in files:
+        with open(path, "rb") as f:
+            h.update(os.path.relpath(path, pkg).encode() + b"\0" + f.read())
     return h.hexdigest()
+
+
+def lowering_settings(options: dict) -> dict:
+    """The resolved values of every setting that changes the lowering besides the call's own
+    options: environment switches read at compile time and module-level switches."""
+    from hip_compiler import patterns, subgraph_analyzer
+
+    fold = options.get("fold_attention")
+    return {
+        "fold_attention": (os.environ.get("HIPRT_FOLD_ATTN", "1") == "1") if fold is None else bool(fold),
+        "conv_nhwc": os.environ.get("HIPRT_CONV_NHWC", "1") == "1",
+        "conv_d2_max_k": subgraph_analyzer.CONV_D2_MAX_K,
+        "fuse_reduce_norm": bool(patterns.FUSE_REDUCE_NORM),
+        "persistent_decode": os.environ.get("HIPRT_PERSISTENT", "1") == "1",
+    }
 
 
 def cache_key(ir_dict: dict, options: dict) -> str:
     h = hashlib.sha256()
     h.update(json.dumps(ir_dict, sort_keys=True, separators=(",", ":")).encode())
     h.update(json.dumps(options, sort_keys=True).encode())
+    h.update(json.dumps(lowering_settings(options), sort_keys=True).encode())
     h.update(compiler_fingerprint().encode())
     return h.hexdigest()[:32]
 

@@ -28,7 +28,7 @@ import os
 from dataclasses import dataclass, field
 
 from hip_compiler import views as V
-from hip_compiler.codegen import MAX_CHAIN_INPUTS, ChainOp, generate_chain
+from hip_compiler.codegen import MAX_CHAIN_INPUTS, VEC, ChainOp, generate_chain, vector_ok
 from hip_compiler.op_classify import OpCategory, classify_op
 from hip_compiler.program import (DTYPE_CODE, ELEM_SIZE, FLOAT_DTYPES, LaunchStep, Ref, Storage, TView,
                                   contiguous_strides, numel)
@@ -300,6 +300,17 @@ class Lowering:
         ss = list(src.strides) + [0] * (6 - nd)
         ds = list(dst.strides) + [0] * (6 - nd)
         n = src.numel
+        nbytes = n * ELEM_SIZE[src.dtype]
+        if src.dtype == dst.dtype and src.is_contiguous() and dst.is_contiguous() and nbytes % 16 == 0 and \
+                (src.offset * ELEM_SIZE[src.dtype]) % 16 == 0 and (dst.offset * ELEM_SIZE[dst.dtype]) % 16 == 0:
+            # a plain byte copy: 16-byte chunks, four in flight per thread
+            chunks = nbytes // 16
+            self.emit(LaunchStep(
+                kind="copy", kernel="k_copy16", module="basic", arg_struct="CopyArgs",
+                args=dict(dst=self.ref(dst), src=self.ref(src), n=chunks, shape=[1] * 6, sstride=[0] * 6,
+                          dstride=[0] * 6, ndim=1, sdtype=DTYPE_CODE[src.dtype], ddtype=DTYPE_CODE[dst.dtype]),
+                grid=grid1d(chunks, cap=8192), inputs=ins, outputs=outs, params={"total": n}))
+            return
         self.emit(LaunchStep(
             kind="copy", kernel="k_copy", module="basic", arg_struct="CopyArgs",
             args=dict(dst=self.ref(dst), src=self.ref(src), n=n, shape=shape, sstride=ss, dstride=ds,
@@ -314,10 +325,12 @@ class Lowering:
         name, src = generate_chain(ch.ops, ch.ext, ch.shape, ch.dtype)
         self.kernel_sources[name] = src
         n = numel(ch.shape)
+        # the vector form takes 8 elements per thread (its `n` counts 8-element groups)
+        nt = n // VEC if vector_ok(ch.ext, ch.shape, ch.dtype) else n
         ptrs = [self.ref(v) for v in ch.ext] + [None] * (MAX_CHAIN_INPUTS - len(ch.ext))
         self.emit(LaunchStep(
             kind="fused", kernel=name, module=name, arg_struct="FusedArgs",
-            args=dict(out=self.ref(out), **{"in": ptrs}, n=n), grid=grid1d(n),
+            args=dict(out=self.ref(out), **{"in": ptrs}, n=nt), grid=grid1d(nt),
             inputs=list(ch.ext_names), outputs=[tail],
             params={"total": n, "ops": [o.op_type for o in ch.ops], "nodes": list(ch.node_names)}))
         self.views[tail] = out

@@ -55,6 +55,9 @@ _SIGS = {
     "hs_memcpy_htod": ([C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "hs_memcpy_dtoh": ([C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "hs_memcpy_dtod": ([C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "hs_argmax_workspace_bytes": ([C.c_int64, C.c_int64], C.c_size_t),
+    "hs_argmax_rows": ([C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p],
+                       C.c_int),
     "hs_argsize": ([C.c_char_p], C.c_size_t),
 }
 EXPORTED = tuple(_SIGS)

@@ -252,7 +252,11 @@ def _refs(args: dict):
 class DecodeAdvance:
     """Advances a decode loop's ``attention_mask`` / ``position_ids`` / ``cache_position``
     buffers to the next step on the device (``k_decode_advance``), ordered after the step on
-    the same stream: the loop needs no host-side input preparation between steps."""
+    the same stream: the loop needs no host-side input preparation between steps.
+
+    A call that would move past the cache end (position S) writes nothing and raises a flag on
+    the device instead; ``check()`` (a synchronising read) raises ``RuntimeError`` once it is
+    set, so a loop that ran too long is reported instead of re-running position S - 1."""
 
     def __init__(self, mask: HIPBuffer, pos: HIPBuffer, cpos: HIPBuffer):
         m, p, c = mask.native_handle, pos.native_handle, cpos.native_handle
@@ -262,11 +266,23 @@ class DecodeAdvance:
         mods = module_cache(self.device.index or 0)
         mods.ensure_builtin("basic")
         self._fn = mods.function("basic", "k_decode_advance")
+        self._flag = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.S = int(mask.shape[-1])
         self._args = STRUCTS["AdvanceArgs"](mask=m.data_ptr(), pos=p.data_ptr(), cpos=c.data_ptr(),
-                                            S=int(mask.shape[-1]), mask_bytes=m.element_size(), pad=0)
+                                            overflow=self._flag.data_ptr(), S=self.S,
+                                            mask_bytes=m.element_size(), pad=0)
         self._keep = (m, p, c)
 
     def __call__(self, stream: int | None = None) -> None:
         s = stream if stream is not None else _current_stream(self.device)
         _shim.check(_shim.lib().hs_launch(self._fn, 1, 1, 1, 64, 1, 1, 0, s, C.byref(self._args),
                                           C.sizeof(self._args)), "k_decode_advance")
+
+    def check(self) -> None:
+        """Raise if any call since construction (or ``clear()``) tried to step past the cache end."""
+        if int(self._flag.item()):
+            raise RuntimeError(f"decode loop stepped past the end of the {self.S}-position cache "
+                               "(k_decode_advance left the inputs at the last position)")
+
+    def clear(self) -> None:
+        self._flag.zero_()

@@ -34,7 +34,8 @@ def _struct(name: str, fields: list):
 _struct("CopyArgs", [("dst", P), ("src", P), ("n", LL), ("shape", LL * 6), ("sstride", LL * 6),
                      ("dstride", LL * 6), ("ndim", I), ("sdtype", I), ("ddtype", I), ("pad", I)])
 _struct("FillArgs", [("out", P), ("n", LL), ("value", C.c_double), ("dtype", I), ("pad", I)])
-_struct("AdvanceArgs", [("mask", P), ("pos", P), ("cpos", P), ("S", LL), ("mask_bytes", I), ("pad", I)])
+_struct("AdvanceArgs", [("mask", P), ("pos", P), ("cpos", P), ("overflow", P), ("S", LL), ("mask_bytes", I),
+                        ("pad", I)])
 _struct("RMSNormArgs", [("x", P), ("w", P), ("out", P), ("rows", LL), ("ldx", LL), ("ldo", LL), ("cols", I),
                         ("eps", F), ("x_dtype", I), ("w_dtype", I), ("n_dtype", I), ("out_dtype", I)])
 _struct("EmbeddingArgs", [("w", P), ("ids", P), ("out", P), ("n_ids", LL), ("vocab", LL), ("row_bytes", LL),

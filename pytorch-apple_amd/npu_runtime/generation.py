@@ -253,6 +253,8 @@ class GreedyGenerator:
                 kv[layer["decode_value_input"]] = out[layer["decode_value_output"]]
         if fast:
             self.backend.synchronize()
+            if b.get("advance") is not None:
+                b["advance"].check()
             got = hist[:steps].cpu().tolist()
             if eos_token_id is not None and eos_token_id in got:
                 got = got[:got.index(eos_token_id)]

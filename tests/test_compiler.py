@@ -188,8 +188,23 @@ def test_generated_chain_reads_broadcast_operands_with_zero_stride():
     name, src = generate_chain([ChainOp("aten.mul.Tensor", [("ext", 0), ("ext", 1)], "bfloat16")], [x, c], out,
                                "bfloat16")
     assert "c1 * 128LL" in src                     # x walks heads
-    assert "ld_f(a.in[1], c3 * 1LL, 2)" in src       # cos broadcast over heads: only the dim term
+    # 8 outputs per thread (last dim 128): 16-byte loads; cos broadcast over heads: only the dim term
+    assert "ld8_f(a.in[1], c3 * 1LL, 2" in src and "st8_f(a.out, i * 8, 2" in src
     assert name.startswith("fused_ew_")
+    # a last dimension that is not a multiple of 8 keeps one element per thread
+    out = (1, 12, 1, 100)
+    x = TView("x", 0, out, contiguous_strides(out), "bfloat16")
+    c = V.broadcast_to(TView("c", 0, (1, 1, 1, 100), contiguous_strides((1, 1, 1, 100)), "bfloat16"), out)
+    _, src = generate_chain([ChainOp("aten.mul.Tensor", [("ext", 0), ("ext", 1)], "bfloat16")], [x, c], out,
+                            "bfloat16")
+    assert "ld_f(a.in[1], c3 * 1LL, 2)" in src and "st8_f" not in src
+    # an operand broadcast along the last dimension is one load per 8 outputs
+    out = (4, 64)
+    x = TView("x", 0, out, contiguous_strides(out), "float32")
+    s_ = V.broadcast_to(TView("s", 0, (4, 1), contiguous_strides((4, 1)), "float32"), out)
+    _, src = generate_chain([ChainOp("aten.mul.Tensor", [("ext", 0), ("ext", 1)], "float32")], [x, s_], out,
+                            "float32")
+    assert "ld1x8_f(a.in[1], c0 * 1LL, 0" in src and "ld8_f(a.in[0]" in src
 
 
 def test_output_views_are_whole_contiguous_storages():
@@ -235,3 +250,24 @@ def test_resnet50_compiles_to_fused_convs():
     finally:
         del os.environ["HIPRT_CONV_NHWC"]
     assert all(s.kernel.startswith("k_conv_") for s in q.steps if s.kind == "conv")
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_graph_outputs_share_no_arena_bytes(fuse):
+    """A greedy loop feeds ``next_token`` (an arena output) back as the next run's ``input_ids``;
+    no step of a run may write bytes of an output storage other than the output itself, so the
+    embedding that reads input_ids first never races with a write into the same bytes."""
+    p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True), fuse=fuse)
+    out_storages = {p.output_views[spec.name].storage for spec in p.output_specs if spec.name in p.output_views}
+    assert {"next_token"} <= {spec.name for spec in p.output_specs} and out_storages
+    placed = [s for s in p.storages.values() if s.kind in ("arena", "persistent") and s.offset >= 0]
+    for o in placed:
+        if o.name not in out_storages:
+            continue
+        lo, hi = o.offset, o.offset + (o.nbytes + 255) // 256 * 256
+        assert o.first == 0 and o.last >= len(p.steps) - 1
+        for s in placed:
+            if s is o:
+                continue
+            s_hi = s.offset + (s.nbytes + 255) // 256 * 256
+            assert s_hi <= lo or hi <= s.offset, (o.name, s.name)

@@ -1,0 +1,132 @@
+"""cfg4 and cfg5 at their full configurations, HIP path vs the CPU fallback (ATen).
+
+cfg4 — Qwen2.5-1.5B-architecture prefill, 28 layers, 512 prompt tokens, vocab 151936 — is
+judged as the reference judges a full-depth Qwen prefill (tests/test_e2e_qwen.py:127-137 and
+291-298): at every position the top-5 tokens of the two paths share at least 3, and the top-1
+token at the last position is the same. Over 28 layers two bf16 evaluations that sum in
+different orders drift apart by about the distance each has from the float32 result, so the
+logits are also compared with the same graph evaluated in float32 (plain ATen fp32): the HIP
+path must be as close to it as the CPU fallback is (within 1.25x + 5e-3 of the largest logit).
+
+cfg5 — ResNet-50, fp16, batch 32, 3 x 224 x 224 — is the reference's convnet check
+(tests/test_dag_executor.py:345-412: allclose plus argmax) at the benchmark size: logits within
+2e-2 of the largest magnitude and the same top-5 classes for every image. At this size the
+1x1 convolutions take the large-tile and split-K kernel variants the 96 x 96 test never reaches.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from conftest import gpu_available
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a ROCm GPU")]
+
+
+def _f32(a):
+    from oracle.numpy_ref import bf16_bits_to_f32
+
+    a = np.asarray(a)
+    return bf16_bits_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+
+
+def _host(d):
+    from irgen.workloads import to_host
+
+    return {k: to_host(v) for k, v in d.items()}
+
+
+def _executors(ir, backend):
+    from hip_compiler import compile_subgraph, is_hip_op_supported
+    from npu_compiler import partition
+    from npu_compiler.partitioner import Partition
+    from npu_runtime import DAGExecutor
+
+    hip = DAGExecutor(partition(ir, is_hip_op_supported), backend, compile_fn=compile_subgraph)
+    assert all(s.target == "npu" for s in hip.plan.steps if isinstance(s, Partition))
+    cpu = DAGExecutor(partition(ir, lambda *_: False), None)
+    return hip, cpu
+
+
+def _top5(x):
+    return np.argpartition(-x, 5, axis=-1)[..., :5]
+
+
+def test_prefill_512_full_depth_vs_cpu_fallback(backend):
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import make_weights, prefill_inputs
+
+    cfg = QwenConfig(layers=28)
+    T = 512
+    print("[case] cfg4 prefill T=512, 28 layers: HIP", flush=True)
+    ir = build_decode_ir(T, cfg, argmax=True, tokens=T)
+    w = _host(make_weights(ir, cfg, device="cuda"))
+    x = _host(prefill_inputs(T, T, cfg))
+    hip, cpu = _executors(ir, backend)
+    hip.load_weights(w)
+    got = {k: v.to_numpy() for k, v in hip.execute(x).items()}
+    kernels = [st.kernel for p in hip.npu_programs.values() for st in p.steps]
+    assert "k_attn_prefill" in kernels and any(k.startswith("k_gemm_") for k in kernels)
+    print("[case] cfg4: CPU fallback bf16", flush=True)
+    cpu.load_weights(w)
+    ref = cpu.execute(x)
+    print("[case] cfg4: CPU float32", flush=True)
+    ir32 = build_decode_ir(T, dataclasses.replace(cfg, dtype="float32"), argmax=True, tokens=T)
+    from npu_compiler import partition
+    from npu_runtime import DAGExecutor
+
+    cpu32 = DAGExecutor(partition(ir32, lambda *_: False), None)
+    cpu32.load_weights({k: _f32(v) if np.asarray(v).dtype == np.uint16 else v for k, v in w.items()})
+    truth = cpu32.execute({k: _f32(v) if np.asarray(v).dtype == np.uint16 else v for k, v in x.items()})
+
+    lg = ir["graph_outputs"][0]["name"]
+    g = _f32(got[lg]).reshape(T, -1)
+    c = _f32(ref[lg]).reshape(T, -1)
+    t = np.asarray(truth[lg], np.float32).reshape(T, -1)
+    tg, tc, tt = _top5(g), _top5(c), _top5(t)
+    ov_hc = np.array([len(set(tg[p]) & set(tc[p])) for p in range(T)])
+    ov_hf = np.array([len(set(tg[p]) & set(tt[p])) for p in range(T)])
+    ov_cf = np.array([len(set(tc[p]) & set(tt[p])) for p in range(T)])
+    err_hip = float(np.abs(g - t).max() / np.abs(t).max())
+    err_cpu = float(np.abs(c - t).max() / np.abs(t).max())
+    print(f"top-5 overlap HIP/CPU min {ov_hc.min()} mean {ov_hc.mean():.2f}; vs fp32: HIP min {ov_hf.min()} "
+          f"mean {ov_hf.mean():.2f}, CPU min {ov_cf.min()} mean {ov_cf.mean():.2f}; logits vs fp32: "
+          f"HIP {err_hip:.4f}, CPU {err_cpu:.4f}", flush=True)
+    # the reference's rule (tests/test_e2e_qwen.py:127-137)
+    assert ov_hc.min() >= 3, f"positions with top-5 overlap < 3: {np.nonzero(ov_hc < 3)[0].tolist()}"
+    assert int(np.argmax(g[-1])) == int(np.argmax(c[-1]))
+    # the greedy tokens of the graph (device argmax) are the argmax of the logits it returns
+    assert np.array_equal(np.asarray(got["next_token"]).reshape(-1), np.argmax(g, axis=-1))
+    # full-depth floating-point bar: as close to the fp32 evaluation as the CPU fallback
+    assert err_hip <= 1.25 * err_cpu + 5e-3
+    # the caches written by the prefill: the first layer's within 2e-2 of the CPU path
+    for o in ir["graph_outputs"][1:3]:
+        a, b = _f32(got[o["name"]]), _f32(ref[o["name"]])
+        assert np.abs(a - b).max() <= 2e-2 * np.abs(b).max()
+
+
+def test_resnet50_batch32_224_vs_cpu_fallback(backend):
+    from irgen.resnet import build_resnet50_ir, resnet_inputs, resnet_weights
+
+    print("[case] cfg5 ResNet-50 fp16 batch 32 224x224: HIP", flush=True)
+    ir = build_resnet50_ir(32, 224)
+    w = _host(resnet_weights(ir))
+    x = _host(resnet_inputs(32, 224))
+    hip, cpu = _executors(ir, backend)
+    hip.load_weights(w)
+    got = {k: v.to_numpy() for k, v in hip.execute(x).items()}
+    kernels = [st.kernel for p in hip.npu_programs.values() for st in p.steps]
+    assert any("_conv" in k for k in kernels)
+    print("[case] cfg5: CPU fallback fp16", flush=True)
+    cpu.load_weights(w)
+    ref = cpu.execute(x)
+    (name,) = got
+    g, r = np.asarray(got[name], np.float32), np.asarray(ref[name], np.float32)
+    assert g.shape == r.shape == (32, 1000)
+    err = float(np.abs(g - r).max() / np.abs(r).max())
+    same = [set(np.argsort(-g[i])[:5]) == set(np.argsort(-r[i])[:5]) for i in range(32)]
+    print(f"logits max rel err {err:.4f}; images with the same top-5: {sum(same)}/32; "
+          f"top-1 equal: {int((g.argmax(1) == r.argmax(1)).sum())}/32", flush=True)
+    assert err <= 2e-2
+    assert all(same), f"images whose top-5 differ: {[i for i, s in enumerate(same) if not s]}"

@@ -264,6 +264,11 @@ def test_decode_advance_moves_positions_and_opens_one_mask_entry(backend, dt):
         m = mb.to_torch().float().reshape(-1).cpu()
         assert int(pb.to_torch().item()) == p and int(cb.to_torch().item()) == p
         assert m[:p + 1].eq(0).all() and m[p + 1:].eq(float("-inf")).all()
-    adv()   # at S - 1: no position past the cache
+    adv.check()   # every step so far stayed inside the cache
+    adv()   # at S - 1: no position past the cache; the overflow flag is raised instead
     torch.cuda.synchronize()
     assert int(cb.to_torch().item()) == S - 1 and int(pb.to_torch().item()) == S - 1
+    with pytest.raises(RuntimeError, match="past the end"):
+        adv.check()
+    adv.clear()
+    adv.check()

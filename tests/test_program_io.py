@@ -85,3 +85,26 @@ def test_program_cache_serves_dag_executor_as_compile_fn(tmp_path):
     DAGExecutor(plan, rec, compile_fn=lambda sub: compile_cached(sub, str(tmp_path)))
     assert len(rec.programs) == 1 and len(os.listdir(tmp_path)) == 1
     assert rec.programs[0] == compile_subgraph(_build_sub_ir_dict(plan.steps[0], ir))
+
+
+def test_cache_key_covers_lowering_switches(monkeypatch):
+    """Environment and module switches that change the lowering change the key, so a cached
+    program built under other settings is never returned."""
+    from hip_compiler import patterns, subgraph_analyzer
+
+    ir = graphs()["decode"]
+    base = cache_key(ir, {})
+    monkeypatch.setenv("HIPRT_FOLD_ATTN", "0")
+    assert cache_key(ir, {}) != base
+    assert cache_key(ir, {"fold_attention": True}) == cache_key(ir, {"fold_attention": True}) != base
+    monkeypatch.delenv("HIPRT_FOLD_ATTN")
+    monkeypatch.setenv("HIPRT_CONV_NHWC", "0")
+    assert cache_key(ir, {}) != base
+    monkeypatch.delenv("HIPRT_CONV_NHWC")
+    monkeypatch.setattr(patterns, "FUSE_REDUCE_NORM", False)
+    assert cache_key(ir, {}) != base
+    monkeypatch.setattr(patterns, "FUSE_REDUCE_NORM", True)
+    monkeypatch.setattr(subgraph_analyzer, "CONV_D2_MAX_K", 256)
+    assert cache_key(ir, {}) != base
+    monkeypatch.setattr(subgraph_analyzer, "CONV_D2_MAX_K", 512)
+    assert cache_key(ir, {}) == base

@@ -90,3 +90,29 @@ def test_backend_fails_loudly_without_a_gpu():
 
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         HIPBackend().allocate_zeros((2, 2))
+
+
+def test_argmax_entry_point_sizes_and_rejects_bad_operands_without_launching():
+    """hs_argmax_rows validates before any HIP call, so these run without a device."""
+    lib = _shim.lib()
+    assert lib.hs_argmax_workspace_bytes(1, 151936) == 19 * 8          # 8192-column parts
+    assert lib.hs_argmax_workspace_bytes(512, 151936) == 512 * 19 * 8
+    assert lib.hs_argmax_workspace_bytes(3, 8) == 3 * 8
+    assert lib.hs_argmax_workspace_bytes(0, 100) == 0
+    buf = (C.c_uint16 * 64)()
+    out = (C.c_int64 * 4)()
+    ws = (C.c_uint64 * 8)()
+    base = C.addressof(buf)
+    aligned = base + (-base) % 16
+    cases = [
+        (aligned, 2, 1, 12, "multiple of 8"),       # cols % 8 != 0
+        (aligned, 0, 1, 16, "dtype"),               # fp32 not supported
+        (aligned + 2, 2, 1, 16, "16-byte aligned"),
+        (aligned, 2, 70000, 16, "rows"),
+    ]
+    for x, dt, rows, cols, msg in cases:
+        rc = lib.hs_argmax_rows(x, dt, rows, cols, C.addressof(out), C.addressof(ws), C.sizeof(ws), None)
+        assert rc != 0 and msg.encode() in lib.hs_last_error(), (msg, lib.hs_last_error())
+    rc = lib.hs_argmax_rows(aligned, 2, 1, 16, C.addressof(out), C.addressof(ws), 4, None)
+    assert rc != 0 and b"workspace" in lib.hs_last_error()
+    assert lib.hs_argmax_rows(aligned, 2, 0, 16, C.addressof(out), None, 0, None) == 0   # no rows: nothing to do
