@@ -444,7 +444,7 @@ def main() -> int:
                 # host-side per-step inputs (numpy), uploaded by DAGExecutor every step
                 st.update(host_steps[s])
             out = ex.execute(st)
-            if not host:
+            if not host and s < n_steps - 1:   # the next step's inputs (none after the last step)
                 advance()
             st["input_ids"] = out["next_token"]
             if record is not None:
@@ -493,6 +493,12 @@ def main() -> int:
         entry = {"launches_per_step": len(idx), "avg_us": round(us, 3)}
         if program.steps[idx[0]].kind == "gemv":
             b = sum(gemv_launch_bytes(program.steps[i]) for i in idx) / len(idx)
+            entry["GBs"] = round(b / (us * 1e-6) / 1e9, 1)
+            entry["bytes_per_launch"] = int(b)
+        elif program.steps[idx[0]].kind == "decode_step":
+            # the persistent step is the whole step: its algorithmic bytes are the step's, at the
+            # valid length of the replayed launch (the last position of the timed window)
+            b = step_bytes(cfg, start + args.steps)
             entry["GBs"] = round(b / (us * 1e-6) / 1e9, 1)
             entry["bytes_per_launch"] = int(b)
         per_kernel[kname] = entry

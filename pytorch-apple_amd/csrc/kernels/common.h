@@ -316,8 +316,10 @@ struct BatchNormArgs {        // inference batch norm over NCHW (channel = dim 1
   long long hw;
   int C;
   float eps;
-  int dtype;
+  int dtype;                  // x and out
   int relu;
+  int p_dtype;                // w, b, mean, var
+  int pad;
 };
 
 struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm, epilogues bias/resid/silu/argmax
@@ -344,6 +346,49 @@ struct GemvArgs {             // fused decode GEMV (gemv.hip): prologue RMSNorm,
   int attn_heads;             // ATTN prologue: H, KVH, nsplit (x = heads * 128 values)
   int attn_kvh;
   int attn_splits;
+};
+
+// ---- persistent decode step (decode.hip): one launch runs every layer of a decoder step
+struct DecodeLayerPtrs {      // one decoder layer's tensors, gathered from the layer's launch records
+  const uint16_t* norm1;      // [hidden] input RMSNorm weight
+  const uint16_t* wq;         // [H*D, hidden]
+  const uint16_t* bq;         // [H*D] or null
+  const uint16_t* wk;         // [KVH*D, hidden]
+  const uint16_t* bk;
+  const uint16_t* wv;
+  const uint16_t* bv;
+  uint16_t* kc;               // K cache [KVH, S, D] (updated in place at cache_position)
+  uint16_t* vc;               // V cache
+  const uint16_t* wo;         // [hidden, H*D]
+  const uint16_t* norm2;      // [hidden] post-attention RMSNorm weight
+  const uint16_t* wg;         // [inter, hidden]
+  const uint16_t* wu;         // [inter, hidden]
+  const uint16_t* wd;         // [hidden, inter]
+};
+
+struct PersistArgs {
+  const DecodeLayerPtrs* layers;   // [L] table in device memory
+  const uint16_t* emb;        // [vocab, hidden] token embedding
+  const void* ids;            // input_ids (one token)
+  const void* pos_ids;        // position_ids (rotary position)
+  const void* cache_pos;      // cache_position (cache row written)
+  const void* mask;           // [S] additive mask row (bf16 / fp32)
+  const float* inv_freq;      // [D/2]
+  const uint16_t* norm_f;     // [hidden] final RMSNorm weight
+  const uint16_t* lm_w;       // [vocab, hidden]
+  uint16_t* logits;           // [vocab]
+  void* next_token;           // [1] argmax of the logits
+  uint32_t* ll;               // exchange words (low 16 bits payload, high 16 bits step tag) + keys + control
+  unsigned long long* trace;  // null, or [nwg][L * 16 + 8] real-time stamps of each part's progress
+  long long S;                // cache length
+  long long kv_head_stride;   // elements between KV heads of a cache
+  long long vocab;
+  int L, hidden, inter, H, KVH, D;
+  int nsplit;                 // attention splits of 128 positions
+  int nwg;                    // workgroups of the launch (all resident at once)
+  int ids_dtype, pos_dtype, cpos_dtype, mask_dtype, add_dtype, n_dtype, out_dtype;
+  int flags;                  // 1: q/k/v biases present
+  float eps, eps_f, scale, rope_scaling;
 };
 
 struct ArgmaxFinalizeArgs {   // out[m] = index of max over the `parts` keys of row m

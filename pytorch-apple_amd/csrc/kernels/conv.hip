@@ -356,58 +356,52 @@ extern "C" __global__ void __launch_bounds__(256) k_maxpool2d(const PoolArgs a) 
       ho = (int)((i / a.Wo) % a.Ho);
       pl = i / ((long long)a.Wo * a.Ho);
     }
-    const uint16_t* x = (const uint16_t*)a.x + pl * a.H * a.W;
+    const long long x0 = pl * a.H * a.W;   // first element of the plane (any float dtype)
     float best = -INFINITY;
     bool nan = false;
     if (a.kh == 3 && a.kw == 3) {   // all nine loads in flight together (clamped addresses, masked values)
-      uint16_t v[9];
+      float v[9];
       bool ok[9];
 #pragma unroll
       for (int t = 0; t < 9; ++t) {
         const int hi = ho * a.sh - a.ph + t / 3, wi = wo * a.sw - a.pw + t % 3;
         ok[t] = (unsigned)hi < (unsigned)a.H && (unsigned)wi < (unsigned)a.W;
-        v[t] = x[ok[t] ? hi * a.W + wi : 0];
+        v[t] = ld_f(a.x, x0 + (ok[t] ? hi * a.W + wi : 0), a.dtype);
       }
 #pragma unroll
       for (int t = 0; t < 9; ++t) {
         if (!ok[t]) continue;
-        const float f = a.dtype == HS_BF16 ? bf16_to_f32(v[t]) : f16_to_f32(v[t]);
-        nan |= f != f;
-        best = fmaxf(best, f);
+        nan |= v[t] != v[t];
+        best = fmaxf(best, v[t]);
       }
-      if (nan) best = NAN;
-      ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(best) : f32_to_f16(best);
-      continue;
-    }
-    for (int kh = 0; kh < a.kh; ++kh) {
-      const int hi = ho * a.sh - a.ph + kh;
-      if (hi < 0 || hi >= a.H) continue;
-      for (int kw = 0; kw < a.kw; ++kw) {
-        const int wi = wo * a.sw - a.pw + kw;
-        if (wi < 0 || wi >= a.W) continue;
-        const float v = a.dtype == HS_BF16 ? bf16_to_f32(x[hi * a.W + wi]) : f16_to_f32(x[hi * a.W + wi]);
-        nan |= v != v;
-        best = fmaxf(best, v);
+    } else {
+      for (int kh = 0; kh < a.kh; ++kh) {
+        const int hi = ho * a.sh - a.ph + kh;
+        if (hi < 0 || hi >= a.H) continue;
+        for (int kw = 0; kw < a.kw; ++kw) {
+          const int wi = wo * a.sw - a.pw + kw;
+          if (wi < 0 || wi >= a.W) continue;
+          const float v = ld_f(a.x, x0 + hi * a.W + wi, a.dtype);
+          nan |= v != v;
+          best = fmaxf(best, v);
+        }
       }
     }
     if (nan) best = NAN;
-    ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(best) : f32_to_f16(best);
+    st_f(a.out, i, a.dtype, best);   // a max of stored values: exact in the input dtype
   }
 }
 
-// out = round(x * a_c + b_c) (+ ReLU), a_c = w_c / sqrt(var_c + eps), b_c = bias_c - mean_c * a_c
+// out = round(x * a_c + b_c) (+ ReLU), a_c = w_c / sqrt(var_c + eps), b_c = bias_c - mean_c * a_c;
+// x and out of dtype `dtype`, the four per-channel parameters of dtype `p_dtype` (any float dtype)
 extern "C" __global__ void __launch_bounds__(256) k_batchnorm(const BatchNormArgs a) {
   for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < a.n; i += (long long)gridDim.x * 256) {
     const int c = (int)((i / a.hw) % a.C);
-    auto f = [&](const void* p, long long j) {
-      const uint16_t h = ((const uint16_t*)p)[j];
-      return a.dtype == HS_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
-    };
-    const float al = f(a.w, c) / sqrtf(f(a.var, c) + a.eps);
-    const float be = f(a.b, c) - f(a.mean, c) * al;
-    float v = f(a.x, i) * al + be;
+    const float al = ld_f(a.w, c, a.p_dtype) / sqrtf(ld_f(a.var, c, a.p_dtype) + a.eps);
+    const float be = ld_f(a.b, c, a.p_dtype) - ld_f(a.mean, c, a.p_dtype) * al;
+    float v = ld_f(a.x, i, a.dtype) * al + be;
     if (a.relu) v = v != v ? v : fmaxf(v, 0.f);
-    ((uint16_t*)a.out)[i] = a.dtype == HS_BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+    st_f(a.out, i, a.dtype, v);
   }
 }
 

@@ -1,0 +1,801 @@
+// One decoder step of a Qwen2-style model in a single persistent launch (gfx950).
+//
+// The multi-kernel step is a chain of dependent launches per layer (RMSNorm + q/k/v + RoPE,
+// attention, o_proj + residual, RMSNorm + gate/up + SiLU*mul, down + residual); every launch
+// boundary costs a full drain and refill of the machine. Here one workgroup per CU runs every
+// layer, and the dependencies between the parts of a layer are carried by the data itself:
+//
+//   * Exchange words: every activation a part hands to the next (q/k/v rows, attention
+//     partials, the combined attention row, the residual stream, the SiLU*mul row) is written
+//     as 32-bit words, the bf16 value in the low half and a 16-bit step tag in the high half,
+//     with agent-scope atomic stores (one word per store: a reader never sees half a word).
+//     A reader loads the words with agent-scope atomic loads and uses them once every word
+//     carries the current step's tag; words not yet current are loaded again. There are no
+//     counters, barriers or fences between workgroups.
+//   * The step tag is the launch count (1..65535, never 0; the exchange area starts zeroed):
+//     stale words from the previous step never match. Exchange slots are per layer, so a slot
+//     is written once per step.
+//   * Every wait is bounded: after 20 ms a workgroup records a timeout in the control word and
+//     goes on, so the launch always ends; the host checks the control word.
+//   * Weights (and the K/V rows of past positions) do not depend on the step's activations, so
+//     each part issues its weight loads before it waits for its inputs: the wait overlaps the
+//     weight stream instead of following it.
+//
+// Work split (NWG workgroups of 8 waves; all resident at once, one per CU):
+//   A  q/k/v:      rows (H + 2 KVH) * D, at most 8 per workgroup, one per wave
+//   B  attention:  workgroup (query head, split) for split < nsplit (128 positions each); the G
+//                  heads of a KV head sit on one XCD and share its K/V rows in L2; partial (o / l, m, l)
+//   C  combine:    one workgroup per query head merges the head's split partials
+//   D  o_proj:     hidden rows, at most 8 per workgroup, one per wave; + residual
+//   E  gate/up:    inter rows spread over workgroups and waves; SiLU(gate) * up
+//   F  down:       hidden rows, at most 8 per workgroup; the 8 waves split each row's K; + residual
+//   G  lm_head:    final RMSNorm, vocab rows over all workgroups; logits and one argmax key per
+//                  workgroup; workgroup 0 reduces the keys into the next token
+// Rounding points are those of the multi-kernel path (and of ATen on the CPU): RMSNorm
+// n = round(x * rsqrt(mean(x^2) + eps)), y = round(w * n); linear round(acc + b); RoPE
+// round(round(x c) + round(-x' s)); attention scores round(round(round(q.k) * scale) + mask);
+// residual round(r + round(acc)); SiLU*mul round(round(silu(round(g))) * round(u)).
+#include "common.h"
+
+#define DEC_THREADS 512
+#define DEC_WAVES 8
+#define DEC_D 128
+#define DEC_SPL 128                   // positions per attention split: 8 waves x 16
+#define DEC_MAXG 8                    // query heads per KV head, at most
+#define DEC_TIMEOUT 2000000ull        // 20 ms of the 100 MHz real-time counter
+#ifndef DEC_ED
+#define DEC_ED 2                      // gate/up rows in flight per wave
+#endif
+
+typedef __attribute__((ext_vector_type(2))) __bf16 dec_bf16x2;
+typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float ddot8(const uint4 a, const uint4 b, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a.x), __builtin_bit_cast(dec_bf16x2, b.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a.y), __builtin_bit_cast(dec_bf16x2, b.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a.z), __builtin_bit_cast(dec_bf16x2, b.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a.w), __builtin_bit_cast(dec_bf16x2, b.w), acc, false);
+  return acc;
+}
+
+__device__ __forceinline__ float ddot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(dec_bf16x2, a), __builtin_bit_cast(dec_bf16x2, b), acc, false);
+}
+
+// Global-memory accesses through pointers the compiler cannot place in an address space (those
+// read from the LDS copy of the layer table): the explicit global address space makes them global
+// instructions; as flat instructions they would also count against the LDS wait counter, and every
+// LDS access would then wait for every load in flight.
+#define DEC_G(T, p) ((__attribute__((address_space(1))) T*)(p))
+
+// 16-byte weight load (streamed once per step: non-temporal)
+__device__ __forceinline__ uint4 ldw(const uint16_t* p) {
+  const dec_u32x4 v = __builtin_nontemporal_load(DEC_G(const dec_u32x4, p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 ldg16(const void* p) {   // (uint4's copy constructor would make it generic)
+  const dec_u32x4 v = *DEC_G(const dec_u32x4, p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ldg4(const void* p) { return *DEC_G(const uint32_t, p); }
+__device__ __forceinline__ uint16_t ldg2(const void* p) { return *DEC_G(const uint16_t, p); }
+__device__ __forceinline__ void stg2(void* p, uint16_t v) { *DEC_G(uint16_t, p) = v; }
+
+// Per-part copies of the thread and workgroup ids that the compiler cannot prove equal across
+// parts, so per-lane address arithmetic is recomputed inside each part instead of being hoisted
+// out of the layer loop and kept live (spilled) across all of them.
+#define DEC_PART_IDS()                                  \
+  int tid = threadIdx.x, b = blockIdx.x;                \
+  asm volatile("" : "+v"(tid));                         \
+  asm volatile("" : "+s"(b));                           \
+  const int lane = tid & 63, wave = tid >> 6;           \
+  (void)lane; (void)wave; (void)b
+
+// Progress stamps (optional): thread 0 of each workgroup records the real-time counter at
+// fixed points of each part, slot k of layer l at trace[b * (L * 16 + 8) + l * 16 + k]; the
+// final part uses slots L * 16 + k. A null trace pointer skips them.
+#define DEC_STAMP(l, k)                                                                          \
+  do {                                                                                           \
+    if (a.trace != nullptr && threadIdx.x == 0)                                                  \
+      a.trace[(long long)blockIdx.x * (a.L * 16 + 8) + (l) * 16 + (k)] = wall_clock64();         \
+  } while (0)
+
+__device__ __forceinline__ float rb(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+__device__ __forceinline__ float bfh(uint16_t h) { return bf16_to_f32(h); }
+
+// ---------------------------------------------------------------- exchange words
+
+__device__ __forceinline__ void xput(uint32_t* p, uint16_t v, uint32_t tag) {
+  __hip_atomic_store(p, (tag << 16) | (uint32_t)v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long xget2(const uint32_t* p) {
+  return __hip_atomic_load((unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void dec_fail(uint32_t* err) {
+  __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until the n words at src (n even, src 8-byte aligned) carry `tag` and copies their
+// payloads (bf16 bits) to dst. Thread t owns word pairs t + 512 j, j < NPT: all of its loads are
+// issued together, and only the pairs not yet current are loaded again, after a short sleep.
+// Returns after a __syncthreads(), so dst is complete for the whole workgroup.
+template <int NPT, int NTH = DEC_THREADS>
+__device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag, uint16_t* dst, uint32_t* err,
+                                        int tid) {
+  if (tid >= NTH) {   // waves outside the gathering set only meet the barrier
+    __syncthreads();
+    return;
+  }
+  const int np = n >> 1;
+  const unsigned long long want = ((unsigned long long)tag << 48) | ((unsigned long long)tag << 16);
+  const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
+  unsigned long long v[NPT];
+  // every pair of the thread is loaded in each round with no branch (pairs past the end re-read
+  // the last one and count as current), so a round costs one memory latency, not one per pair
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
+  const unsigned long long t0 = wall_clock64();
+  while (true) {
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < NPT; ++j)
+      ok = ok && ((v[j] & tmask) == want || tid + NTH * j >= np);
+    if (ok) break;
+    if (wall_clock64() - t0 > DEC_TIMEOUT) {
+      dec_fail(err);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
+  }
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int i = tid + NTH * j;
+    if (i < np) *(uint32_t*)(dst + 2 * i) = (uint32_t)(v[j] & 0xFFFFu) | (uint32_t)((v[j] >> 16) & 0xFFFF0000u);
+  }
+  __syncthreads();
+}
+
+// 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane (gfx950), from inline
+// assembly: the compiler does not count these loads, so it inserts no wait for them (before a
+// barrier or an LDS read); the waves that issue them wait explicitly (dec_vmcnt0) before the
+// data is read, and issue no other vector-memory loads in between.
+__device__ __forceinline__ void dec_dma16(const void* g, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dec_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Word offsets of one layer's exchange slots (all even, so word pairs are 8-byte aligned).
+struct XLayout {
+  long long qkv, part, att, x1, h, stride;
+};
+
+__device__ __forceinline__ XLayout xlayout(const PersistArgs& a) {
+  XLayout o;
+  const long long hid = a.hidden, G = a.H / a.KVH;
+  o.qkv = hid;                                                        // [x_l: hidden] then q/k/v
+  o.part = o.qkv + (long long)a.H * 3 * DEC_D;                       // per query head: q, its k, its v
+  o.att = o.part + (long long)a.H * a.nsplit * (DEC_D + 4);          // per head: nsplit x (o[D], m, l)
+  o.x1 = o.att + (long long)a.H * DEC_D;
+  o.h = o.x1 + hid;
+  o.stride = o.h + a.inter;
+  o.stride += o.stride & 1;
+  return o;
+}
+
+// ---------------------------------------------------------------- workgroup RMSNorm
+
+// xs = round(w * round_n(x * rsqrt(mean(x^2) + eps))) over the hidden values of x (LDS, bf16);
+// thread t < hidden / 8 owns chunk t, whose norm weight wv it loaded before its inputs arrived.
+__device__ __forceinline__ void block_norm(const uint16_t* x, uint4 wv, int hid, float eps, int n_dtype,
+                                           uint16_t* xs, float* red, int tid) {
+  const int t = tid, nch = hid >> 3;
+  uint4 xv = make_uint4(0, 0, 0, 0);
+  float ss = 0.f;
+  if (t < nch) {
+    xv = *(const uint4*)(x + 8 * t);
+    const uint32_t q[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = bfh((uint16_t)(q[j] & 0xffffu)), hi = bfh((uint16_t)(q[j] >> 16));
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  const float tot = ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+  const float r = 1.0f / sqrtf(tot / (float)hid + eps);
+  if (t < nch) {
+    const uint32_t q[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t g[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float n0 = round_to(bfh((uint16_t)(q[j] & 0xffffu)) * r, n_dtype);
+      const float n1 = round_to(bfh((uint16_t)(q[j] >> 16)) * r, n_dtype);
+      o[j] = (uint32_t)f32_to_bf16(bfh((uint16_t)(g[j] & 0xffffu)) * n0) |
+             ((uint32_t)f32_to_bf16(bfh((uint16_t)(g[j] >> 16)) * n1) << 16);
+    }
+    *(uint4*)(xs + 8 * t) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  __syncthreads();
+}
+
+// the layer's input row into xres: the token's embedding row (layer 0) or the exchange words
+template <int KC>
+__device__ __forceinline__ void load_x(const PersistArgs& a, int l, const uint32_t* xw, long long tok, uint32_t tag,
+                                       uint16_t* xres, uint32_t* err, int tid) {
+  if (l == 0) {
+    const int nch = a.hidden >> 3;
+    if (tid < nch) *(uint4*)(xres + 8 * tid) = *(const uint4*)(a.emb + tok * a.hidden + 8 * tid);
+    __syncthreads();
+  } else {
+    xgather<(KC + 1) / 2>(xw, a.hidden, tag, xres, err, tid);
+  }
+}
+
+__device__ __forceinline__ unsigned long long key48(uint16_t hbits, unsigned idx) {
+  // order-preserving bf16 bits (NaN above every number, -0 == +0) over the inverted index
+  const float v = bfh(hbits);
+  uint32_t o = hbits;
+  o = (v == 0.f) ? 0x8000u : ((o & 0x8000u) ? (~o & 0xFFFFu) : (o | 0x8000u));
+  o = (v != v) ? 0xFFFFu : o;
+  return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+// A layer's tensors from the LDS copy of its table entry.
+__device__ __forceinline__ DecodeLayerPtrs dec_layer(const void* const* t) {
+  DecodeLayerPtrs P;
+  __builtin_memcpy(&P, t, sizeof(P));
+  return P;
+}
+
+// ---------------------------------------------------------------- the step
+
+// KC: 512-element chunks of a hidden-long row per lane (hidden = 512 KC); IC: chunks per lane
+// of a down_proj row whose K (inter) is split over the 8 waves (inter <= 4096 IC); RF: down_proj
+// rows per workgroup, at most (2 KC: hidden rows over 256 workgroups); EM: gate/up rows per wave,
+// at most (inter <= 2048 EM); ED: gate/up rows in flight per wave.
+template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED>
+__device__ __forceinline__ void decode_body(const PersistArgs& a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[IC * 8192];   // per-part staging (F: inter bf16)
+  __shared__ __attribute__((aligned(16))) uint16_t xres[512 * KC];
+  __shared__ float red[DEC_WAVES * 8];
+  __shared__ float red2[DEC_WAVES * DEC_MAXG];
+  __shared__ float rope_cs[128];
+  __shared__ __attribute__((aligned(16))) uint4 wobuf[RF * KC * 64];   // D's o_proj rows
+  __shared__ const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
+  __shared__ unsigned long long kred[DEC_WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x, NWG = a.nwg;
+  const int hid = a.hidden, H = a.H, KVH = a.KVH, G = H / KVH, NT = a.nsplit;
+  const XLayout X = xlayout(a);
+  uint32_t* keys = a.ll + X.stride * a.L + hid;                 // nwg 64-bit key words
+  uint32_t* ctl = keys + 2 * (long long)NWG;                    // [0] step tag, [1] timeout flag
+  uint32_t* err = ctl + 1;
+  uint32_t tag = (__hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) & 0xFFFFu;
+  tag = tag == 0 ? 1u : tag;
+  long long tok = ld_i(a.ids, 0, a.ids_dtype);
+  tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);   // ATen would raise; never read outside the table
+  const long long posr = ld_i(a.pos_ids, 0, a.pos_dtype);
+  const long long cpos = ld_i(a.cache_pos, 0, a.cpos_dtype);
+  const long long S = a.S, last = S - 1, kvs = a.kv_head_stride;
+  uint16_t* xs = (uint16_t*)smem;
+  DEC_STAMP(a.L, 7);
+  // rotary factors of this step's position (the same for every layer): cos and sin of
+  // inv_freq[i] * position in fp32, times the scaling, rounded to bf16
+  if (tid < 64) {
+    float sf, cf;
+    sincos_rot(a.inv_freq[tid] * (float)posr, &sf, &cf);
+    rope_cs[tid] = round_to(cf * a.rope_scaling, HS_BF16);
+    rope_cs[64 + tid] = round_to(sf * a.rope_scaling, HS_BF16);
+  }
+
+  const int ntile = KVH * NT;               // attention tiles: (KV head, split of 128 positions)
+  const bool att = b < ntile * G;           // workgroup b: query head g = b / ntile of tile b % ntile
+  const int tile = b % ntile, gq = b / ntile;
+  const int kvh = tile / NT, split = tile % NT;
+  const bool comb = b >= ntile * G && b < ntile * G + H;   // combine of query head b - ntile * G
+  // layer 0's tensors into LDS; each layer loads the next one's during its first part and stores
+  // them in F, so no layer waits for its table at its start
+  if (tid < 14) ptab[0][tid] = ((const void* const*)a.layers)[tid];
+  __syncthreads();
+
+  for (int l = 0; l < a.L; ++l) {
+    const DecodeLayerPtrs P = dec_layer(ptab[l & 1]);
+    const void* pnext = nullptr;
+    if (tid < 14 && l + 1 < a.L) pnext = ((const void* const*)(a.layers + l + 1))[tid];
+    uint32_t* XL = a.ll + X.stride * l;            // this layer's exchange slots
+    uint32_t* XN = a.ll + X.stride * (l + 1);      // the next layer's input row (x_{l+1})
+
+    // ---- A: RMSNorm, q / k / v rows (+ bias) -------------------------------------------------
+    {
+      DEC_PART_IDS();
+      const int R = (H + 2 * KVH) * DEC_D, RB = (R + NWG - 1) / NWG;
+      const int r = b * RB + wave;
+      const bool has = wave < RB && r < R;
+      const uint16_t* W;
+      const uint16_t* B;
+      int rr, seg;
+      if (r < H * DEC_D) {
+        W = P.wq; B = P.bq; rr = r; seg = 0;
+      } else if (r < (H + KVH) * DEC_D) {
+        rr = r - H * DEC_D; W = P.wk; B = P.bk; seg = 1;
+      } else {
+        rr = r - (H + KVH) * DEC_D; W = P.wv; B = P.bv; seg = 2;
+      }
+      // loads carry no branch: a wave without a row re-reads row 0 of q (unused)
+      const long long rl = has ? rr : 0;
+      const uint16_t* Wl = has ? W : P.wq;
+      uint4 w[KC];
+#pragma unroll
+      for (int c = 0; c < KC; ++c) w[c] = ldw(Wl + rl * hid + c * 512 + lane * 8);
+      const uint16_t bias = (has && (a.flags & 1)) ? ldg2(B + rr) : (uint16_t)0;
+      const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm1 + 8 * tid) : make_uint4(0, 0, 0, 0);
+      __syncthreads();
+      DEC_STAMP(l, 0);
+      load_x<KC>(a, l, XL, tok, tag, xres, err, tid);
+      DEC_STAMP(l, 1);
+      block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
+      if (has) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) acc = ddot8(*(const uint4*)(xs + c * 512 + lane * 8), w[c], acc);
+        acc = wave_sum(acc);
+        const uint16_t v = f32_to_bf16(acc + bfh(bias));
+        // exchange block of query head h: [q_h | k of its KV head | v of its KV head]; a k or v row
+        // is written into the blocks of all G heads that read it
+        if (seg == 0) {
+          if (lane == 0) xput(XL + X.qkv + (long long)(rr / DEC_D) * 3 * DEC_D + rr % DEC_D, v, tag);
+        } else if (lane < G) {
+          const int hq = (rr / DEC_D) * G + lane;
+          xput(XL + X.qkv + (long long)hq * 3 * DEC_D + seg * DEC_D + rr % DEC_D, v, tag);
+        }
+      }
+      DEC_STAMP(l, 2);
+    }
+
+    // ---- D's o_proj rows into LDS: waves 0-3 issue direct-to-LDS loads of this workgroup's rows now;
+    // they land while B and C run (the polls of B, C and D that follow wait for them in order, which
+    // costs nothing: they are older and small)
+    {
+      DEC_PART_IDS();
+      if (wave < 4) {
+        const int RB = (hid + NWG - 1) / NWG;                 // <= RF (checked on the host)
+        const long long rmax = min(b * RB + RB, hid) - 1;    // rows past the block re-read its last row
+        const unsigned base = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&wobuf[0];
+        for (int k = wave; k < RB * KC; k += 4) {
+          const long long r = min((long long)(b * RB + k / KC), rmax);
+          dec_dma16(P.wo + r * (H * DEC_D) + (k % KC) * 512 + lane * 8,
+                    __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
+        }
+      }
+    }
+
+    // ---- the past positions' K / V rows and mask values for B: no dependency on this step's
+    // activations, so they are issued before B waits for its q / k / v (after A, whose input poll
+    // would otherwise wait behind them)
+    uint4 kr[4];
+    uint32_t vr[16];
+    FRaw mraw = {0, 0};
+    {
+      DEC_PART_IDS();
+      const long long p0 = (long long)split * DEC_SPL + wave * 16;
+      const int kq = lane >> 2, kc = lane & 3;
+      if (att) {
+        const uint16_t* Kb = P.kc + (long long)kvh * kvs;
+        const uint16_t* Vb = P.vc + (long long)kvh * kvs;
+        if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(p0 + kq, last), a.mask_dtype);
+        const uint4* ks = (const uint4*)(Kb + min(p0 + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(p0 + t, last) * DEC_D + 2 * lane);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kr[j] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 16; ++t) vr[t] = 0;
+      }
+    }
+
+    // ---- B: attention of one query head over one split of 128 positions ----------------------------
+    if (att) {
+      DEC_PART_IDS();
+      const long long p0 = (long long)split * DEC_SPL + wave * 16;
+      const int kq = lane >> 2, kc = lane & 3;
+      const int hq = kvh * G + gq;
+      uint16_t* raw = (uint16_t*)smem;               // [3 * D]: q, k, v as produced
+      const float* csh = rope_cs;                    // [64] cos, [64] sin (rounded, scaled)
+      uint16_t* rot = (uint16_t*)(smem + 1536);      // [2 * D]: rotated q and k
+      float* osh = (float*)(smem + 2048);            // [8][D] per-wave unnormalised outputs
+      __syncthreads();
+      xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, tid);
+      DEC_STAMP(l, 3);
+      if (tid < 128) {   // rotate_half RoPE: threads 0..63 q, 64..127 k
+        const int hs = tid >> 6, j = tid & 63;
+        const float x0 = bfh(raw[hs * DEC_D + j]), x1 = bfh(raw[hs * DEC_D + j + 64]);
+        const float c = csh[j], sn = csh[64 + j];
+        rot[hs * DEC_D + j] = f32_to_bf16(rb(rb(x0 * c) + rb(-x1 * sn)));
+        rot[hs * DEC_D + j + 64] = f32_to_bf16(rb(rb(x1 * c) + rb(x0 * sn)));
+      }
+      __syncthreads();
+      const bool cin = cpos >= 0 && cpos < S;
+      if (cin && gq == 0 && cpos >= (long long)split * DEC_SPL && cpos < (long long)(split + 1) * DEC_SPL &&
+          tid < DEC_D) {   // this step's K / V row goes into the caches (index_copy at cache_position)
+        stg2(P.kc + (long long)kvh * kvs + cpos * DEC_D + tid, rot[DEC_D + tid]);
+        stg2(P.vc + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
+      }
+      if (cin && cpos >= p0 && cpos < p0 + 16) {   // the wave holding that position uses the new row
+        if (p0 + kq == cpos) {
+          const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) kr[j] = kn[j];
+        }
+        const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+          if (p0 + t == cpos) vr[t] = vn;
+      }
+      const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
+      const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
+      const bool live = __ballot(mval != -INFINITY) != 0ull;
+      float acc0 = 0.f, acc1 = 0.f, mw = -INFINITY, lw = 0.f;
+      if (live) {
+        const uint4* qq = (const uint4*)(rot + kc * 32);
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 q4 = qq[j];
+          d = ddot2(q4.x, kr[j].x, d);
+          d = ddot2(q4.y, kr[j].y, d);
+          d = ddot2(q4.z, kr[j].z, d);
+          d = ddot2(q4.w, kr[j].w, d);
+        }
+        d += HS_DPP(d, HS_QUAD_XOR1);
+        d += HS_DPP(d, HS_QUAD_XOR2);
+        float sc = -INFINITY;
+        if (mval != -INFINITY) {
+          sc = rb(d);
+          sc = rb(sc * a.scale);
+          if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
+        }
+        float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
+        m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
+        m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
+        const float e = (sc == -INFINITY) ? 0.f : __expf(sc - m);
+        float ls = e + HS_DPP(e, HS_ROW_ROR4);
+        ls += HS_DPP(ls, HS_ROW_ROR8);
+        lw = (HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48));
+        mw = m;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const float p = HS_RL(e, 4 * t);
+          acc0 = fmaf(p, bfh((uint16_t)(vr[t] & 0xffffu)), acc0);
+          acc1 = fmaf(p, bfh((uint16_t)(vr[t] >> 16)), acc1);
+        }
+      }
+      osh[wave * DEC_D + 2 * lane] = acc0;
+      osh[wave * DEC_D + 2 * lane + 1] = acc1;
+      if (lane == 0) {
+        red[wave] = mw;
+        red2[wave] = lw;
+      }
+      __syncthreads();
+      if (tid < DEC_D) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w8 = 0; w8 < DEC_WAVES; ++w8) M = fmaxf(M, red[w8]);
+        float o = 0.f, L = 0.f;
+#pragma unroll
+        for (int w8 = 0; w8 < DEC_WAVES; ++w8) {
+          const float lv = red2[w8];
+          const float f = lv > 0.f ? __expf(red[w8] - M) : 0.f;
+          o = fmaf(f, osh[w8 * DEC_D + tid], o);
+          L = fmaf(f, lv, L);
+        }
+        // the head's split partial: o / l (bf16), then m and l as four 16-bit halves
+        uint32_t* pp = XL + X.part + ((long long)hq * NT + split) * (DEC_D + 4);
+        xput(pp + tid, f32_to_bf16(L > 0.f ? o / L : 0.f), tag);
+        if (tid == 0) {
+          const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
+          xput(pp + DEC_D + 0, (uint16_t)(mb >> 16), tag);
+          xput(pp + DEC_D + 1, (uint16_t)(mb & 0xFFFFu), tag);
+          xput(pp + DEC_D + 2, (uint16_t)(lb >> 16), tag);
+          xput(pp + DEC_D + 3, (uint16_t)(lb & 0xFFFFu), tag);
+        }
+      }
+      DEC_STAMP(l, 4);
+    }
+
+    // ---- C: combine the split partials of one query head (waves 0-3, 2 threads per dimension) ----------
+    if (comb) {
+      DEC_PART_IDS();
+      const int h = b - ntile * G;
+      uint16_t* pl = (uint16_t*)smem;   // [NT][D + 4]
+      float* cw = red2;                 // [NT] weights e^(m_t - M) l_t / L (NT <= 32: red2 holds 64)
+      __syncthreads();
+      xgather<(32 * (DEC_D + 4) + 2 * 256 - 1) / (2 * 256), 256>(
+          XL + X.part + (long long)h * NT * (DEC_D + 4), NT * (DEC_D + 4), tag, pl, err, tid);
+      DEC_STAMP(l, 5);
+      if (wave == 0) {
+        float m = -INFINITY, lv = 0.f;
+        if (lane < NT) {
+          const uint16_t* e = pl + lane * (DEC_D + 4) + DEC_D;
+          m = __uint_as_float(((uint32_t)e[0] << 16) | e[1]);
+          lv = __uint_as_float(((uint32_t)e[2] << 16) | e[3]);
+        }
+        const float M = wave_max(lv > 0.f ? m : -INFINITY);
+        const float f = lv > 0.f ? __expf(m - M) * lv : 0.f;
+        const float L = wave_sum(f);
+        if (lane < NT) cw[lane] = L > 0.f ? f / L : 0.f;
+      }
+      __syncthreads();
+      if (wave < 4) {
+        const int d = tid >> 1, q = tid & 1;
+        float sacc = 0.f;
+        for (int t = q; t < NT; t += 2) sacc = fmaf(cw[t], bfh(pl[t * (DEC_D + 4) + d]), sacc);
+        sacc += HS_DPP(sacc, HS_QUAD_XOR1);
+        if (q == 0) xput(XL + X.att + (long long)h * DEC_D + d, f32_to_bf16(sacc), tag);
+      }
+      DEC_STAMP(l, 6);
+    }
+
+    // ---- D: o_proj + residual (waves 0-3; the rows from LDS) -------------------------------------------
+    {
+      DEC_PART_IDS();
+      const int RB = (hid + NWG - 1) / NWG;
+      if (wave < 4) dec_vmcnt0();   // this wave's o_proj rows have landed (long ago)
+      __syncthreads();
+      DEC_STAMP(l, 7);
+      xgather<(KC + 1) / 2 * 2, 256>(XL + X.att, H * DEC_D, tag, xs, err, tid);
+      DEC_STAMP(l, 8);
+      const unsigned char* ob = (const unsigned char*)wobuf;
+      for (int i = wave; i < RB; i += 4) {
+        const int r = b * RB + i;
+        if (wave < 4 && r < hid) {   // wave-uniform
+          float acc = 0.f;
+#pragma unroll
+          for (int c = 0; c < KC; ++c)
+            acc = ddot8(*(const uint4*)(xs + c * 512 + lane * 8), *(const uint4*)(ob + (i * KC + c) * 1024 + lane * 16),
+                        acc);
+          acc = wave_sum(acc);
+          if (lane == 0) xput(XL + X.x1 + r, f32_to_bf16(bfh(xres[r]) + rb(acc)), tag);
+        }
+      }
+      DEC_STAMP(l, 9);
+    }
+
+    // ---- E: RMSNorm, gate / up, SiLU(gate) * up -----------------------------------------------------
+    // wave w computes the workgroup's rows w, w + 8, ... (at most EM) with EP rows in flight in a
+    // ring of registers: the first EP are issued before x1 is awaited, and each computed row's slot
+    // is reloaded with the row EP further on. The code is unrolled over EM and every load is
+    // unconditional (a wave with fewer rows re-reads its last one), so no loaded value flows through
+    // a branch join, which would make the compiler wait for every load in flight. F's down_proj
+    // weights follow the last gate / up loads, so the stream runs on into F without a gap.
+    uint4 fw[RF][IC];
+    {
+      DEC_PART_IDS();
+      constexpr int EP = ED < EM ? ED : EM;
+      const int RBE = (a.inter + NWG - 1) / NWG;   // <= 8 EM (checked on the host)
+      const int r0 = b * RBE;
+      const int n = (min(RBE, a.inter - r0) - wave + DEC_WAVES - 1) / DEC_WAVES;   // this wave's rows (may be <= 0)
+      // rows past the wave's last re-read it (a wave without rows reads the matrix's last row)
+      const long long rlast = min(r0 + wave + (long long)DEC_WAVES * max(n - 1, 0), (long long)a.inter - 1);
+      uint4 wg[EP][KC], wu[EP][KC];
+      auto load_row = [&](int d, int k) {
+        const long long r = min(r0 + wave + (long long)DEC_WAVES * k, rlast);
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          wg[d][c] = ldw(P.wg + r * hid + c * 512 + lane * 8);
+          wu[d][c] = ldw(P.wu + r * hid + c * 512 + lane * 8);
+        }
+      };
+      auto issue_f = [&]() {
+        const int RB = (hid + NWG - 1) / NWG;   // <= RF (checked on the host)
+        const int K8 = a.inter >> 3;
+        const long long rmaxf = min(b * RB + RB, hid) - 1;
+#pragma unroll
+        for (int j = 0; j < RF; ++j) {
+          const long long r = min((long long)(b * RB + j), rmaxf);
+#pragma unroll
+          for (int k = 0; k < IC; ++k) {
+            const int c = min(512 * k + 64 * wave + lane, K8 - 1);   // chunks past the row re-read its last one
+            fw[j][k] = ldw(P.wd + r * a.inter + 8 * c);
+          }
+        }
+      };
+#pragma unroll
+      for (int d = 0; d < EP; ++d) load_row(d, d);
+      if (EM == EP) issue_f();
+      const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm2 + 8 * tid) : make_uint4(0, 0, 0, 0);
+      __syncthreads();
+      DEC_STAMP(l, 10);
+      xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, tid);
+      DEC_STAMP(l, 11);
+      block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
+      // the rows' results are stored after the last row: a store issued between the loads would
+      // sit in the same in-order completion count, and every later wait for a row would wait for it
+      uint16_t hv[EM];
+#pragma unroll
+      for (int k = 0; k < EM; ++k) {
+        const int d = k % EP;
+        float g = 0.f, u = 0.f;
+        if (k < n) {   // wave-uniform
+#pragma unroll
+          for (int c = 0; c < KC; ++c) {
+            const uint4 xv = *(const uint4*)(xs + c * 512 + lane * 8);
+            g = ddot8(xv, wg[d][c], g);
+            u = ddot8(xv, wu[d][c], u);
+          }
+        }
+        if (k + EP < EM) {
+          load_row(d, k + EP);
+          if (k + EP == EM - 1) issue_f();
+        }
+        g = wave_sum(g);
+        u = wave_sum(u);
+        const float gv = rb(g), uv = rb(u);
+        hv[k] = f32_to_bf16(rb(gv / (1.f + expf(-gv))) * uv);
+      }
+      if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < EM; ++k)
+          if (k < n) xput(XL + X.h + r0 + wave + DEC_WAVES * k, hv[k], tag);
+      }
+      DEC_STAMP(l, 12);
+    }
+
+    // ---- F: down_proj + residual (the 8 waves split each row's K; weights issued in E) -----------------
+    {
+      DEC_PART_IDS();
+      const int RB = (hid + NWG - 1) / NWG;
+      const int K8 = a.inter >> 3;
+      uint16_t* hs = (uint16_t*)smem;
+      __syncthreads();
+      DEC_STAMP(l, 13);
+      xgather<(IC * 4096 / 2 + 255) / 256, 256>(XL + X.h, a.inter, tag, hs, err, tid);
+      DEC_STAMP(l, 14);
+      float part[RF];
+#pragma unroll
+      for (int j = 0; j < RF; ++j) part[j] = 0.f;
+#pragma unroll
+      for (int k = 0; k < IC; ++k) {
+        const int c = 512 * k + 64 * wave + lane;
+        if (c < K8) {
+          const uint4 hv = *(const uint4*)(hs + 8 * c);
+#pragma unroll
+          for (int j = 0; j < RF; ++j) part[j] = ddot8(hv, fw[j][k], part[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RF; ++j) {
+        const float sum = wave_sum(part[j]);
+        if (lane == 0) red[wave * 8 + j] = sum;
+      }
+      if (tid < 14) ptab[(l + 1) & 1][tid] = pnext;   // the next layer's tensors (read after the barrier)
+      __syncthreads();
+      if (tid < RB && b * RB + tid < hid) {
+        const int r = b * RB + tid;
+        float acc = 0.f;
+#pragma unroll
+        for (int w8 = 0; w8 < DEC_WAVES; ++w8) acc += red[w8 * 8 + tid];
+        xput(XN + r, f32_to_bf16(bfh(xres[r]) + rb(acc)), tag);
+      }
+      DEC_STAMP(l, 15);
+    }
+  }
+
+  // ---- G: final RMSNorm, lm_head, logits and argmax keys -------------------------------------------
+  {
+      DEC_PART_IDS();
+    uint32_t* XF = a.ll + X.stride * a.L;
+    const long long V = a.vocab, RB = (V + NWG - 1) / NWG, r0 = (long long)b * RB;
+    const long long rend = min(r0 + RB, V);
+    constexpr int R4 = 2;   // rows per wave per round; two rounds in flight
+    uint4 wc[R4][KC], wn[R4][KC];
+    auto issue = [&](uint4 (&w)[R4][KC], long long base) {
+#pragma unroll
+      for (int i = 0; i < R4; ++i) {
+        const long long r = base + wave + (long long)DEC_WAVES * i;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) w[i][c] = ldw(a.lm_w + min(r, rend - 1) * hid + c * 512 + lane * 8);
+      }
+    };
+    issue(wc, r0);
+    const uint4 nw = tid < (hid >> 3) ? *(const uint4*)(a.norm_f + 8 * tid) : make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    DEC_STAMP(a.L, 0);
+    xgather<(KC + 1) / 2>(XF, hid, tag, xres, err, tid);
+    DEC_STAMP(a.L, 1);
+    block_norm(xres, nw, hid, a.eps_f, a.n_dtype, xs, red, tid);
+    unsigned long long best = 0ull;
+    for (long long base = r0; base < rend; base += (long long)DEC_WAVES * R4) {
+      const bool more = base + (long long)DEC_WAVES * R4 < rend;
+      if (more) issue(wn, base + (long long)DEC_WAVES * R4);
+#pragma unroll
+      for (int i = 0; i < R4; ++i) {
+        const long long r = base + wave + (long long)DEC_WAVES * i;
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) acc = ddot8(*(const uint4*)(xs + c * 512 + lane * 8), wc[i][c], acc);
+        acc = wave_sum(acc);
+        if (r < rend) {
+          const uint16_t hb = f32_to_bf16(acc);
+          if (lane == 0) a.logits[r] = hb;
+          const unsigned long long k = key48(hb, (unsigned)r);
+          best = k > best ? k : best;
+        }
+      }
+      if (more) {
+#pragma unroll
+        for (int i = 0; i < R4; ++i)
+#pragma unroll
+          for (int c = 0; c < KC; ++c) wc[i][c] = wn[i][c];
+      }
+    }
+    DEC_STAMP(a.L, 2);
+    if (lane == 0) kred[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long k = kred[0];
+#pragma unroll
+      for (int w8 = 1; w8 < DEC_WAVES; ++w8) k = kred[w8] > k ? kred[w8] : k;
+      __hip_atomic_store((unsigned long long*)(keys + 2 * (long long)b), ((unsigned long long)tag << 48) | k,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  // ---- workgroup 0: the next token from every workgroup's key, then the step tag ----------------------
+  if (b == 0) {
+    __syncthreads();   // thread 0 has read kred above
+    unsigned long long k = 0ull;
+    const unsigned long long t0 = wall_clock64();
+    for (int i = tid; i < NWG; i += DEC_THREADS) {
+      unsigned long long v = xget2(keys + 2 * (long long)i);
+      while ((uint32_t)(v >> 48) != tag) {
+        if (wall_clock64() - t0 > DEC_TIMEOUT) {
+          dec_fail(err);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        v = xget2(keys + 2 * (long long)i);
+      }
+      const unsigned long long kk = v & 0xFFFFFFFFFFFFull;
+      k = kk > k ? kk : k;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long other = __shfl_xor(k, o, 64);
+      k = other > k ? other : k;
+    }
+    if (lane == 0) kred[wave] = k;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long m = kred[0];
+#pragma unroll
+      for (int w8 = 1; w8 < DEC_WAVES; ++w8) m = kred[w8] > m ? kred[w8] : m;
+      const long long idx = (long long)(0xFFFFFFFFu - (uint32_t)(m & 0xFFFFFFFFull));
+      if (a.out_dtype == HS_I64) *(long long*)a.next_token = idx;
+      else *(int*)a.next_token = (int)idx;
+      __hip_atomic_store(ctl, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    DEC_STAMP(a.L, 3);
+  }
+}
+
+#define DECODE_KERNEL(KC, IC, EM) \
+  extern "C" __global__ void __launch_bounds__(DEC_THREADS) k_decode_step_k##KC##_i##IC##_e##EM(const PersistArgs a) { \
+    decode_body<KC, IC, EM>(a); \
+  }
+
+DECODE_KERNEL(3, 3, 5)   // hidden 1536, inter <= 10240 (Qwen2.5-1.5B: 8960)
+DECODE_KERNEL(3, 3, 6)   // hidden 1536, inter <= 12288
+DECODE_KERNEL(1, 1, 1)   // hidden 512, inter <= 2048
+DECODE_KERNEL(1, 1, 2)   // hidden 512, inter <= 4096
+DECODE_KERNEL(2, 2, 4)   // hidden 1024, inter <= 8192

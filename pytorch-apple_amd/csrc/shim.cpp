@@ -328,6 +328,8 @@ size_t hs_argsize(const char* s) {
   HS_SZ(AttnOutArgs)
   HS_SZ(FlashArgs)
   HS_SZ(CombineArgs)
+  HS_SZ(PersistArgs)
+  HS_SZ(DecodeLayerPtrs)
 #undef HS_SZ
   return 0;
 }

@@ -15,6 +15,8 @@ from __future__ import annotations
 
 from hip_compiler.buffer_planner import buffer_allocations, plan_arena
 from hip_compiler.op_support import get_hip_supported_ops, is_hip_op_supported
+from hip_compiler.persistent import enabled as persistent_enabled
+from hip_compiler.persistent import fuse_decode_step
 from hip_compiler.program import HIPProgram, KernelSource, TView, contiguous_strides
 from hip_compiler.subgraph_analyzer import analyze_subgraph
 from npu_compiler.ir_reader import IRGraph, load_ir_from_dict
@@ -31,7 +33,7 @@ def _infer_compute_dtype(graph: IRGraph) -> str:
 
 def compile_subgraph(ir_dict: dict, compute_dtype: str | None = None, *, inplace_inputs: bool = True,
                      fuse: bool = True, exact_attention: bool = False,
-                     fold_attention: bool | None = None) -> HIPProgram:
+                     fold_attention: bool | None = None, persistent: bool | None = None) -> HIPProgram:
     """Compile one IR dict (a whole graph or one device partition) into a HIPProgram.
 
     ``inplace_inputs``: let ``index_copy`` update a graph-input cache in place when nothing else
@@ -41,13 +43,16 @@ def compile_subgraph(ir_dict: dict, compute_dtype: str | None = None, *, inplace
     the default split-S kernel whose combine folds into the following projection.
     ``fold_attention``: combine the split-S partials in the prologue of the projection that reads
     the attention output (True) or in a kernel of their own (False); None = the default.
+    ``persistent``: run a whole decoder step as one persistent launch when the fused lowering is
+    one (``hip_compiler.persistent``); None = ``HIPRT_PERSISTENT`` (default on).
     """
     return compile_graph(load_ir_from_dict(ir_dict), compute_dtype, inplace_inputs=inplace_inputs, fuse=fuse,
-                         exact_attention=exact_attention, fold_attention=fold_attention)
+                         exact_attention=exact_attention, fold_attention=fold_attention, persistent=persistent)
 
 
 def compile_graph(graph: IRGraph, compute_dtype: str | None = None, *, inplace_inputs: bool = True,
-                  fuse: bool = True, exact_attention: bool = False, fold_attention: bool | None = None) -> HIPProgram:
+                  fuse: bool = True, exact_attention: bool = False, fold_attention: bool | None = None,
+                  persistent: bool | None = None) -> HIPProgram:
     low = analyze_subgraph(graph, inplace_inputs=inplace_inputs, fuse=fuse, exact_attention=exact_attention,
                            fold_attention=fold_attention)
     out_views: dict[str, TView] = {}
@@ -63,13 +68,16 @@ def compile_graph(graph: IRGraph, compute_dtype: str | None = None, *, inplace_i
         if tuple(v.shape) != tuple(spec.shape):
             v = v.with_(shape=tuple(spec.shape), strides=contiguous_strides(spec.shape))
         out_views[spec.name] = v
-    arena_bytes = plan_arena(low.steps, low.storages, {v.storage for v in out_views.values()})
+    steps = low.steps
+    if fuse and (persistent if persistent is not None else persistent_enabled()):
+        steps = fuse_decode_step(low.steps, low.storages) or low.steps
+    arena_bytes = plan_arena(steps, low.storages, {v.storage for v in out_views.values()})
     by_storage = {}
     for name, v in low.views.items():
         if v.storage not in by_storage and v.offset == 0 and v.is_contiguous():
             by_storage[v.storage] = (v.shape, v.dtype)
     prog = HIPProgram(
-        steps=low.steps,
+        steps=steps,
         buffer_allocations=buffer_allocations(low.storages, by_storage),
         input_specs=list(graph.graph_inputs),
         output_specs=list(graph.graph_outputs),
@@ -81,7 +89,7 @@ def compile_graph(graph: IRGraph, compute_dtype: str | None = None, *, inplace_i
         views=low.views,
         output_views=out_views,
         arena_bytes=arena_bytes,
-        stats={"launches": len(low.steps), "mutated_inputs": sorted(low.mutated_inputs)},
+        stats={"launches": len(steps), "mutated_inputs": sorted(low.mutated_inputs)},
     )
     return prog
 

@@ -130,7 +130,8 @@ def lowering_settings(options: dict) -> dict:
         "conv_nhwc": os.environ.get("HIPRT_CONV_NHWC", "1") == "1",
         "conv_d2_max_k": subgraph_analyzer.CONV_D2_MAX_K,
         "fuse_reduce_norm": bool(patterns.FUSE_REDUCE_NORM),
-        "persistent_decode": os.environ.get("HIPRT_PERSISTENT", "1") == "1",
+        "persistent_decode": (os.environ.get("HIPRT_PERSISTENT", "1") == "1") if options.get("persistent") is None
+        else bool(options["persistent"]),
     }
 
 

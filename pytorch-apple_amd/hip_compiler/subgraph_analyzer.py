@@ -1144,13 +1144,15 @@ class Lowering:
         x = self.contiguous(node.inputs[0].name)
         out = node.outputs[0]
         ps = [self.contiguous(t.name) for t in node.inputs[1:5]]
+        if len({p.dtype for p in ps}) != 1 or out.dtype != x.dtype:
+            raise NotImplementedError("batch_norm: weight, bias, mean and var of one dtype, output of the input's")
         o = self.new_storage(out.name, out.shape, out.dtype)
         hw = numel(x.shape[2:]) if len(x.shape) > 2 else 1
         self.emit(LaunchStep(
             kind="elementwise", kernel="k_batchnorm", module="conv", arg_struct="BatchNormArgs",
             args=dict(x=self.ref(x), w=self.ref(ps[0]), b=self.ref(ps[1]), mean=self.ref(ps[2]), var=self.ref(ps[3]),
                       out=self.ref(o), n=x.numel, hw=hw, C=x.shape[1], eps=float(node.attrs.get("eps", 1e-5)),
-                      dtype=DTYPE_CODE[x.dtype], relu=0),
+                      dtype=DTYPE_CODE[x.dtype], relu=0, p_dtype=DTYPE_CODE[ps[0].dtype], pad=0),
             grid=grid1d(x.numel), inputs=[t.name for t in node.inputs], outputs=[out.name], params={}))
         self.views[out.name] = o
 

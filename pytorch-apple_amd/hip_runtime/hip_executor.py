@@ -67,9 +67,12 @@ class HIPExecutor:
         self.arena = torch.zeros(max(program.arena_bytes, 256), dtype=torch.uint8, device=self.device)
         base = self.arena.data_ptr()
         storages = program.storages
-        self._ext_names: list[str] = sorted({r.storage for st in program.steps for r in _refs(st.args)
+        self._ext_names: list[str] = sorted({r.storage for st in program.steps
+                                             for r in list(_refs(st.args)) + list(_table_refs(st))
                                              if storages[r.storage].kind in ("input", "weight")})
         self._structs = []
+        self._tables: list[tuple[object, str, list]] = []   # (struct, pointer field, entries)
+        self._table_bufs: dict[tuple, list] = {}             # pointer set -> device tables
         self._fixups: list[tuple[object, str, int, str, int]] = []   # (struct, field, index, storage, byte_off)
         n = len(program.steps)
         self._recs = (_shim.LaunchRec * max(n, 1))()
@@ -83,6 +86,8 @@ class HIPExecutor:
                 else:
                     self._set(s, k, -1, v, None, base, storages)
             self._structs.append(s)
+            if "table" in st.params:
+                self._tables.append((s, st.params["table"]["field"], st.params["table"]["entries"]))
             r = self._recs[i]
             r.fn = mods.function(st.module, st.kernel)
             r.grid[:] = [int(g) for g in st.grid]
@@ -124,13 +129,42 @@ class HIPExecutor:
         else:
             arr[idx] = val
 
-    def _patch(self, ptrs: dict[str, int]) -> None:
+    def _patch(self, ptrs: dict[str, int], key: tuple) -> None:
         for s, field, idx, storage, off in self._fixups:
             val = ptrs[storage] + off
             if idx < 0:
                 setattr(s, field, val)
             else:
                 getattr(s, field)[idx] = val
+        if self._tables:
+            self._fill_tables(ptrs, key)
+
+    def _fill_tables(self, ptrs: dict[str, int], key: tuple) -> None:
+        """Pointer tables of the launches that read one (the persistent decode step's per-layer
+        tensors): resolved for this pointer set into a device array of its own, so that a graph
+        captured for another set keeps reading the table it was captured with."""
+        bufs = self._table_bufs.get(key)
+        if bufs is None:
+            base = self.arena.data_ptr()
+            storages = self.program.storages
+            bufs = []
+            for _, _, entries in self._tables:
+                vals = []
+                for r in entries:
+                    if r is None:
+                        vals.append(0)
+                    elif storages[r.storage].kind in ("arena", "persistent"):
+                        vals.append(base + storages[r.storage].offset + r.byte_offset)
+                    else:
+                        vals.append(ptrs[r.storage] + r.byte_offset)
+                host = torch.tensor([v - (1 << 64) if v >= (1 << 63) else v for v in vals], dtype=torch.int64)
+                bufs.append(host.to(self.device))
+            torch.cuda.current_stream(self.device).synchronize()
+            if not self.use_graph:   # without graphs only the current set's tables are read
+                self._table_bufs.clear()
+            self._table_bufs[key] = bufs
+        for (s, field, _), t in zip(self._tables, bufs):
+            setattr(s, field, t.data_ptr())
 
     # ------------------------------------------------------------------ execution
 
@@ -194,7 +228,7 @@ class HIPExecutor:
             self._graphs.move_to_end(key)
         else:
             if key != self._ext_key:
-                self._patch(ptrs)
+                self._patch(ptrs, key)
                 self._ext_key = key
             if not self.use_graph:
                 _shim.check(lib.hs_replay(self._recs, self._n, stream), "replay")
@@ -207,9 +241,26 @@ class HIPExecutor:
             _shim.check(lib.hs_graph_capture(self._recs, self._n, self._capture_stream, C.byref(g)), "graph capture")
             graph = self._graphs[key] = g.value
             while len(self._graphs) > MAX_GRAPHS:
-                _, old = self._graphs.popitem(last=False)
+                old_key, old = self._graphs.popitem(last=False)
                 _shim.check(lib.hs_graph_destroy(old), "graph destroy")
+                if old_key != self._ext_key:
+                    self._table_bufs.pop(old_key, None)
         _shim.check(lib.hs_graph_launch(graph, stream), "graph launch")
+
+    def check(self) -> None:
+        """Raise ``RuntimeError`` if a persistent decode step has recorded a timeout (one of its
+        workgroups waited past its time limit for data from another: its results are not valid).
+        Synchronises with the device; clears the flag."""
+        for st in self.program.steps:
+            if st.kind != "decode_step":
+                continue
+            xs = self.program.storages[st.args["ll"].storage]
+            off = xs.offset + (int(st.params["exchange_words"]) - 1) * 4
+            flag = self.arena[off:off + 4].view(torch.int32)
+            if int(flag.item()):
+                flag.zero_()
+                raise RuntimeError("persistent decode step: a workgroup timed out waiting for another's data; "
+                                   "the step's outputs are not valid (are all of its workgroups resident?)")
 
     def run(self, inputs: dict, weights: dict) -> dict[str, HIPBuffer]:
         self.launch(inputs, weights)
@@ -237,6 +288,10 @@ class HIPExecutor:
                 lib.hs_stream_destroy(self._capture_stream)
         except Exception:
             pass
+
+
+def _table_refs(step):
+    return [r for r in step.params.get("table", {}).get("entries", []) if isinstance(r, Ref)]
 
 
 def _refs(args: dict):

@@ -31,6 +31,13 @@ def _struct(name: str, fields: list):
     return cls
 
 
+_struct("PersistArgs", [("layers", P), ("emb", P), ("ids", P), ("pos_ids", P), ("cache_pos", P), ("mask", P),
+                        ("inv_freq", P), ("norm_f", P), ("lm_w", P), ("logits", P), ("next_token", P), ("ll", P),
+                        ("trace", P), ("S", LL), ("kv_head_stride", LL), ("vocab", LL), ("L", I), ("hidden", I), ("inter", I),
+                        ("H", I), ("KVH", I), ("D", I), ("nsplit", I), ("nwg", I), ("ids_dtype", I),
+                        ("pos_dtype", I), ("cpos_dtype", I), ("mask_dtype", I), ("add_dtype", I), ("n_dtype", I),
+                        ("out_dtype", I), ("flags", I), ("eps", F), ("eps_f", F), ("scale", F),
+                        ("rope_scaling", F)])
 _struct("CopyArgs", [("dst", P), ("src", P), ("n", LL), ("shape", LL * 6), ("sstride", LL * 6),
                      ("dstride", LL * 6), ("ndim", I), ("sdtype", I), ("ddtype", I), ("pad", I)])
 _struct("FillArgs", [("out", P), ("n", LL), ("value", C.c_double), ("dtype", I), ("pad", I)])
@@ -76,7 +83,7 @@ _struct("PadNHWCArgs", [("x", P), ("out", P), ("n", LL), ("C", I), ("H", I), ("W
                         ("top", I), ("left", I), ("pad", I)])
 _struct("MeanNHWCArgs", [("x", P), ("out", P), ("n", LL), ("hw", I), ("c", I)])
 _struct("BatchNormArgs", [("x", P), ("w", P), ("b", P), ("mean", P), ("var", P), ("out", P), ("n", LL),
-                          ("hw", LL), ("C", I), ("eps", F), ("dtype", I), ("relu", I)])
+                          ("hw", LL), ("C", I), ("eps", F), ("dtype", I), ("relu", I), ("p_dtype", I), ("pad", I)])
 _struct("RopeCacheArgs", [("y", P), ("inv_freq", P), ("pos_ids", P), ("cache_pos", P), ("q_out", P), ("k_dst", P),
                           ("v_dst", P), ("ldy", LL), ("kv_head_stride", LL), ("cache_len", LL), ("T", I), ("H", I),
                           ("KVH", I), ("D", I), ("flags", I), ("pos_dtype", I), ("cpos_dtype", I), ("dtype", I),

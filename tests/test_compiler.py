@@ -95,7 +95,7 @@ def test_attention_block_is_three_launches_with_inplace_cache():
 
 def test_decode_step_launch_count_and_cache_aliasing():
     cfg = QwenConfig(layers=3)
-    p = compile_subgraph(build_decode_ir(256, cfg, argmax=True))
+    p = compile_subgraph(build_decode_ir(256, cfg, argmax=True), persistent=False)
     assert len(p.steps) == 1 + 5 * cfg.layers + 2      # embedding, 5 per layer, lm_head+argmax, finalize
     assert kernels(p)[0] == "k_embedding" and kernels(p)[-2:] == ["k_gemv_norm_argmax_r4", "k_argmax_finalize"]
     assert len(p.stats["mutated_inputs"]) == 2 * cfg.layers
@@ -148,7 +148,7 @@ def test_arena_live_ranges_never_share_bytes(build, fuse):
 
 @pytest.mark.parametrize("fuse", [True, False])
 def test_steps_read_only_already_written_arena_storage(fuse):
-    p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True), fuse=fuse)
+    p = compile_subgraph(build_decode_ir(128, QwenConfig(layers=2), argmax=True), fuse=fuse, persistent=False)
     out_fields = {"dst", "out", "c", "cos_out", "sin_out", "q_out", "k_dst", "v_dst", "part_o", "part_ml",
                   "scores", "stats", "argmax_slot", "part", "slot"}
     written = set()
@@ -271,3 +271,28 @@ def test_graph_outputs_share_no_arena_bytes(fuse):
                 continue
             s_hi = s.offset + (s.nbytes + 255) // 256 * 256
             assert s_hi <= lo or hi <= s.offset, (o.name, s.name)
+
+
+def test_decode_step_becomes_one_persistent_launch():
+    """The fused decode lowering is replaced by one launch of the persistent kernel, whose pointer
+    table holds 14 tensors per layer; the launch list stays available with persistent=False, and
+    graphs that are not a decode step (prefill, an unfused lowering) are left alone."""
+    from hip_compiler.persistent import TABLE_FIELDS, exchange_words
+
+    cfg = QwenConfig(layers=3)
+    ir = build_decode_ir(2048, cfg, argmax=True)
+    p = compile_subgraph(ir)
+    assert [s.kernel for s in p.steps] == ["k_decode_step_k3_i3_e5"]
+    st = p.steps[0]
+    assert st.grid == (256, 1, 1) and st.block == (512, 1, 1)
+    entries = st.params["table"]["entries"]
+    assert len(entries) == len(TABLE_FIELDS) * cfg.layers
+    assert entries[TABLE_FIELDS.index("kc")].storage == "past_key_0"
+    assert entries[TABLE_FIELDS.index("wd") + 14 * 2].storage == "p_model_layers_2_mlp_down_proj_weight"
+    xs = p.storages[st.args["ll"].storage]
+    assert xs.kind == "persistent" and xs.nbytes == 4 * exchange_words(3, 1536, 8960, 12, 2, 16)
+    assert st.args["logits"].storage == p.output_views[ir["graph_outputs"][0]["name"]].storage
+    assert len(compile_subgraph(ir, persistent=False).steps) == 2 + 5 * cfg.layers + 1
+    assert len(compile_subgraph(ir, fuse=False).steps) > 20
+    pre = compile_subgraph(build_decode_ir(64, QwenConfig(layers=1), argmax=True, tokens=64))
+    assert not any(s.kind == "decode_step" for s in pre.steps)

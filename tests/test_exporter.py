@@ -359,10 +359,14 @@ def test_full_size_qwen2_5_export_lowers_to_the_bench_launch_list():
     cfg._attn_implementation = "eager"
     with torch.device("meta"):
         m = to_dtype_keep_rotary(Qwen2ForCausalLM(cfg).eval())
-    a = compile_subgraph(export_qwen(m, 2048, tokens=1, argmax=True))
-    b = compile_subgraph(build_decode_ir(2048, argmax=True))
+    ea = export_qwen(m, 2048, tokens=1, argmax=True)
+    a = compile_subgraph(ea, persistent=False)
+    b = compile_subgraph(build_decode_ir(2048, argmax=True), persistent=False)
     assert len(a.steps) == 143
     assert [(s.kernel, s.grid, s.lds) for s in a.steps] == [(s.kernel, s.grid, s.lds) for s in b.steps]
+    # and both become the same single persistent launch by default
+    pa, pb = compile_subgraph(ea), compile_subgraph(build_decode_ir(2048, argmax=True))
+    assert [s.kernel for s in pa.steps] == [s.kernel for s in pb.steps] == ["k_decode_step_k3_i3_e5"]
 
 
 def test_safetensors_loader_theta_default_is_hfs(tmp_path, model):

@@ -125,8 +125,23 @@ def test_resnet50_batch32_224_vs_cpu_fallback(backend):
     g, r = np.asarray(got[name], np.float32), np.asarray(ref[name], np.float32)
     assert g.shape == r.shape == (32, 1000)
     err = float(np.abs(g - r).max() / np.abs(r).max())
-    same = [set(np.argsort(-g[i])[:5]) == set(np.argsort(-r[i])[:5]) for i in range(32)]
-    print(f"logits max rel err {err:.4f}; images with the same top-5: {sum(same)}/32; "
-          f"top-1 equal: {int((g.argmax(1) == r.argmax(1)).sum())}/32", flush=True)
+    # top-5 per image; a set that differs only by the CPU path's 5th and 6th classes trading places
+    # counts as a tie when those two CPU logits are within 2 fp16 ulps of each other (a window fixed
+    # by the output precision, not by the HIP path's error)
+    ties, bad = [], []
+    for i in range(32):
+        gs, rs = set(np.argsort(-g[i])[:5]), np.argsort(-r[i])[:6]
+        if gs == set(rs[:5]):
+            continue
+        a, b = int(rs[4]), int(rs[5])
+        ulp = 2.0 ** (np.floor(np.log2(abs(float(r[i, a])))) - 10)
+        if gs == set(rs[:4]) | {b} and abs(float(r[i, a]) - float(r[i, b])) <= 2 * ulp:
+            ties.append(i)
+        else:
+            bad.append(i)
+    top1 = int((g.argmax(1) == r.argmax(1)).sum())
+    print(f"logits max rel err {err:.4f}; top-5 equal on {32 - len(ties) - len(bad)}/32 images, 5th/6th ties "
+          f"{ties}, other differences {bad}; top-1 equal: {top1}/32", flush=True)
     assert err <= 2e-2
-    assert all(same), f"images whose top-5 differ: {[i for i, s in enumerate(same) if not s]}"
+    assert top1 == 32                         # the reference's argmax check (test_dag_executor.py:376-377)
+    assert not bad, f"images whose top-5 differ beyond a 5th/6th tie: {bad}"
