@@ -86,6 +86,14 @@ size_t hs_argmax_workspace_bytes(int64_t rows, int64_t cols);
 int hs_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* hs_argmax_rows without a workspace argument and without any allocation: the per-segment keys go
+ * to a 512 KiB device array inside the library, one per GPU, held until the process ends. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Limit:
+ * rows * ceil(cols / 8192) <= 65536 (e.g. 3449 rows of a 151936-entry vocabulary); larger calls
+ * return hipErrorInvalidValue. Calls that overlap on one GPU share that array and race. */
+int hs_argmax_rows_noalloc(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, void* stream);
+
 /* sizeof() of the kernel argument struct with the given name (e.g. "LinearArgs"),
  * or 0 when unknown; lets the host check its ctypes mirrors. */
 size_t hs_argsize(const char* struct_name);

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -72,6 +73,32 @@ int argmax_launch(const void* x, int dtype, int64_t rows, int64_t cols, int64_t*
   return 0;
 }
 
+// ---- hs_argmax_rows_noalloc: the per-segment keys live in a file-scope device array, one copy per
+// GPU, so the entry point allocates nothing. Host code never passes `scratch` itself (in host code
+// the name is only a stand-in for the symbol); each device's address comes from
+// hipGetSymbolAddress with that device current, once, and is kept in g_scratch.
+constexpr size_t kScratchKeys = 65536;   // 512 KiB per device: rows * ceil(cols / 8192) keys at most
+static __device__ __align__(256) unsigned long long scratch[kScratchKeys];
+constexpr int kMaxDevices = 64;
+unsigned long long* g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (looked up on the first use on that device).
+int scratch_current(unsigned long long** p) {
+  int dev = 0;
+  HS_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail_arg("no-alloc scratch: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    HS_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) return fail_arg("hipGetSymbolAddress(scratch) returned null");
+    g_scratch[dev] = (unsigned long long*)ptr;
+  }
+  *p = g_scratch[dev];
+  return 0;
+}
+
 int launch_one(const hs_launch_rec& r, hipStream_t s) {
   size_t sz = r.kernarg_size;
   void* cfg[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(r.kernarg), HIP_LAUNCH_PARAM_BUFFER_SIZE, &sz,
@@ -101,7 +128,8 @@ int hs_init(int device) {
   }
   HS_CHECK(hipSetDevice(device));
   HS_CHECK(hipFree(nullptr));
-  return 0;
+  unsigned long long* p = nullptr;   // set up the device's no-alloc scratch address now
+  return scratch_current(&p);
 }
 
 int hs_module_load(const void* image, size_t size, void** module) {
@@ -292,6 +320,18 @@ int hs_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t
                     std::to_string(need));
   if (((uintptr_t)workspace) % 8 != 0) return fail_arg("hs_argmax_rows: workspace must be 8-byte aligned");
   return argmax_launch(x, dtype, rows, cols, out, (unsigned long long*)workspace, (hipStream_t)stream);
+}
+
+int hs_argmax_rows_noalloc(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, void* stream) {
+  if (int rc = argmax_check(x, dtype, rows, cols, out)) return rc;
+  if (rows == 0) return 0;
+  const size_t keys = (size_t)rows * (size_t)argmax_parts(cols);
+  if (keys > kScratchKeys)
+    return fail_arg("hs_argmax_rows_noalloc: rows * ceil(cols / 8192) = " + std::to_string(keys) +
+                    " exceeds the no-alloc scratch of " + std::to_string(kScratchKeys) + " keys");
+  unsigned long long* slot = nullptr;
+  if (int rc = scratch_current(&slot)) return rc;
+  return argmax_launch(x, dtype, rows, cols, out, slot, (hipStream_t)stream);
 }
 
 size_t hs_argsize(const char* s) {

@@ -58,6 +58,7 @@ _SIGS = {
     "hs_argmax_workspace_bytes": ([C.c_int64, C.c_int64], C.c_size_t),
     "hs_argmax_rows": ([C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p],
                        C.c_int),
+    "hs_argmax_rows_noalloc": ([C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
     "hs_argsize": ([C.c_char_p], C.c_size_t),
 }
 EXPORTED = tuple(_SIGS)
