@@ -43,9 +43,12 @@
 #define DEC_SPL 128                   // positions per attention split: 8 waves x 16
 #define DEC_MAXG 8                    // query heads per KV head, at most
 #define DEC_TIMEOUT 2000000ull        // 20 ms of the 100 MHz real-time counter
+#define DEC_NWG_MAX 256               // workgroups of the launch, at most
+#define DEC_OSTAGE 128                // o_proj or gate / up rows of one workgroup, at most
 #ifndef DEC_ED
 #define DEC_ED 2                      // gate/up rows in flight per wave
 #endif
+#define DEC_NE(KC) ((KC) == 3 ? 21 : ((KC) == 2 ? 32 : 48))   // gate/up rows in LDS per attention workgroup
 
 typedef __attribute__((ext_vector_type(2))) __bf16 dec_bf16x2;
 typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
@@ -159,6 +162,37 @@ __device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag
   __syncthreads();
 }
 
+// Waits until the n words at src (n even, src 8-byte aligned) carry `tag`, like xgather without
+// the copy: for the per-workgroup "done" words polled before a large gather, so the repeated
+// rounds of a wait read a few hundred words instead of the whole row.
+template <int NPT, int NTH>
+__device__ __forceinline__ void xwait(const uint32_t* src, int n, uint32_t tag, uint32_t* err, int tid) {
+  if (tid < NTH) {
+    const int np = n >> 1;
+    const unsigned long long want = ((unsigned long long)tag << 48) | ((unsigned long long)tag << 16);
+    const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
+    unsigned long long v[NPT];
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
+    const unsigned long long t0 = wall_clock64();
+    while (true) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < NPT; ++j)
+        ok = ok && ((v[j] & tmask) == want || tid + NTH * j >= np);
+      if (ok) break;
+      if (wall_clock64() - t0 > DEC_TIMEOUT) {
+        dec_fail(err);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
+    }
+  }
+  __syncthreads();
+}
+
 // 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane (gfx950), from inline
 // assembly: the compiler does not count these loads, so it inserts no wait for them (before a
 // barrier or an LDS read); the waves that issue them wait explicitly (dec_vmcnt0) before the
@@ -170,7 +204,7 @@ __device__ __forceinline__ void dec_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)"
 
 // Word offsets of one layer's exchange slots (all even, so word pairs are 8-byte aligned).
 struct XLayout {
-  long long qkv, part, att, x1, h, stride;
+  long long qkv, part, att, x1, h, hdone, stride;
 };
 
 __device__ __forceinline__ XLayout xlayout(const PersistArgs& a) {
@@ -181,9 +215,32 @@ __device__ __forceinline__ XLayout xlayout(const PersistArgs& a) {
   o.att = o.part + (long long)a.H * a.nsplit * (DEC_D + 4);          // per head: nsplit x (o[D], m, l)
   o.x1 = o.att + (long long)a.H * DEC_D;
   o.h = o.x1 + hid;
-  o.stride = o.h + a.inter;
+  o.hdone = o.h + a.inter;                                            // one word per workgroup: its h rows are out
+  o.hdone += o.hdone & 1;
+  o.stride = o.hdone + a.nwg;
   o.stride += o.stride & 1;
   return o;
+}
+
+// ---------------------------------------------------------------- E's register ring
+
+// Row of the k-th gate / up row a wave streams through registers: rows rs + wave + 8 k for
+// k < n; rows past the wave's last re-read it, and a wave without rows reads the matrix's last
+// row, so every load of the ring is unconditional.
+__device__ __forceinline__ long long ering_row(int k, int rs, int nr, int wave, int inter) {
+  const int n = (nr - wave + DEC_WAVES - 1) / DEC_WAVES;
+  const long long rlast = min(rs + wave + (long long)DEC_WAVES * max(n - 1, 0), (long long)inter - 1);
+  return min(rs + wave + (long long)DEC_WAVES * k, rlast);
+}
+
+template <int KC>
+__device__ __forceinline__ void ering_load(uint4 (&g)[KC], uint4 (&u)[KC], const uint16_t* wg, const uint16_t* wu,
+                                           long long r, int hid, int lane) {
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    g[c] = ldw(wg + r * hid + c * 512 + lane * 8);
+    u[c] = ldw(wu + r * hid + c * 512 + lane * 8);
+  }
 }
 
 // ---------------------------------------------------------------- workgroup RMSNorm
@@ -259,18 +316,25 @@ __device__ __forceinline__ DecodeLayerPtrs dec_layer(const void* const* t) {
 
 // KC: 512-element chunks of a hidden-long row per lane (hidden = 512 KC); IC: chunks per lane
 // of a down_proj row whose K (inter) is split over the 8 waves (inter <= 4096 IC); RF: down_proj
-// rows per workgroup, at most (2 KC: hidden rows over 256 workgroups); EM: gate/up rows per wave,
-// at most (inter <= 2048 EM); ED: gate/up rows in flight per wave.
-template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED>
+// rows per workgroup, at most (2 KC: hidden rows over 256 workgroups); EM: gate/up rows per wave
+// streamed through registers, at most; ED: those rows in flight per wave; NE: gate/up rows an
+// attention workgroup loads into LDS once its attention part is done.
+template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC)>
 __device__ __forceinline__ void decode_body(const PersistArgs& a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[IC * 8192];   // per-part staging (F: inter bf16)
   __shared__ __attribute__((aligned(16))) uint16_t xres[512 * KC];
   __shared__ float red[DEC_WAVES * 8];
   __shared__ float red2[DEC_WAVES * DEC_MAXG];
   __shared__ float rope_cs[128];
-  __shared__ __attribute__((aligned(16))) uint4 wobuf[RF * KC * 64];   // D's o_proj rows
+  // an attention workgroup's first NE gate / up rows (row i: gate chunks, then up chunks, 1 KB
+  // each); in the other workgroups, their o_proj rows (at most 2 NE)
+  __shared__ __attribute__((aligned(16))) uint4 ebuf[NE * 2 * KC * 64];
   __shared__ const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
   __shared__ unsigned long long kred[DEC_WAVES];
+  // a part's results (o_proj rows, gate / up rows) staged here, then published with one store
+  // instruction per 64 words: many single-word stores spread over the waves are acknowledged far
+  // more slowly while the memory system is busy with the weight stream
+  __shared__ uint16_t ostage[DEC_OSTAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.x, NWG = a.nwg;
   const int hid = a.hidden, H = a.H, KVH = a.KVH, G = H / KVH, NT = a.nsplit;
@@ -296,11 +360,24 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     rope_cs[64 + tid] = round_to(sf * a.rope_scaling, HS_BF16);
   }
 
-  const int ntile = KVH * NT;               // attention tiles: (KV head, split of 128 positions)
-  const bool att = b < ntile * G;           // workgroup b: query head g = b / ntile of tile b % ntile
+  // Roles. Workgroups b < NB (= H * nsplit) run attention: query head g = b / ntile of tile
+  // b % ntile (KV head, split of 128 positions). The other ND run o_proj (RD rows each), and the
+  // first H of them the combine of query head b - NB. An attention workgroup is done with its
+  // latency-bound parts well before x1 exists, so it spends that time loading NE gate / up rows
+  // into LDS, and takes NE more gate / up rows than the others; the rest are spread so that every
+  // workgroup has about the same left to stream once x1 has arrived.
+  const int ntile = KVH * NT;
+  const int NB = ntile * G, ND = NWG - NB;
+  const bool att = b < NB;
   const int tile = b % ntile, gq = b / ntile;
   const int kvh = tile / NT, split = tile % NT;
-  const bool comb = b >= ntile * G && b < ntile * G + H;   // combine of query head b - ntile * G
+  const bool comb = b >= NB && b < NB + H;
+  const int RD = (hid + ND - 1) / ND;                                   // <= 2 NE (checked on the host)
+  const int RBD = max(a.inter - NB * NE + NWG - 1, 0) / NWG;            // gate / up rows streamed per workgroup
+  const int RBB = NE + RBD;                                             // an attention workgroup's rows
+  const int e0 = att ? b * RBB : NB * RBB + (b - NB) * RBD;             // first gate / up row
+  const int ecnt = max(min(att ? RBB : RBD, a.inter - e0), 0);          // its rows
+  const int NL = att ? min(NE, ecnt) : 0;                               // of which in LDS
   // layer 0's tensors into LDS; each layer loads the next one's during its first part and stores
   // them in F, so no layer waits for its table at its start
   if (tid < 14) ptab[0][tid] = ((const void* const*)a.layers)[tid];
@@ -347,33 +424,33 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
 #pragma unroll
         for (int c = 0; c < KC; ++c) acc = ddot8(*(const uint4*)(xs + c * 512 + lane * 8), w[c], acc);
         acc = wave_sum(acc);
-        const uint16_t v = f32_to_bf16(acc + bfh(bias));
-        // exchange block of query head h: [q_h | k of its KV head | v of its KV head]; a k or v row
-        // is written into the blocks of all G heads that read it
-        if (seg == 0) {
-          if (lane == 0) xput(XL + X.qkv + (long long)(rr / DEC_D) * 3 * DEC_D + rr % DEC_D, v, tag);
-        } else if (lane < G) {
-          const int hq = (rr / DEC_D) * G + lane;
-          xput(XL + X.qkv + (long long)hq * 3 * DEC_D + seg * DEC_D + rr % DEC_D, v, tag);
+        if (lane == 0) ostage[wave] = f32_to_bf16(acc + bfh(bias));
+      }
+      __syncthreads();
+      // published by wave 0 in one store: exchange block of query head h is [q_h | k of its KV
+      // head | v of its KV head], and a k or v row goes into the blocks of all G heads that read it
+      if (wave == 0 && lane < RB * G) {
+        const int j = lane / G, g = lane % G, rj = b * RB + j;
+        if (rj < R) {
+          const int sj = rj < H * DEC_D ? 0 : (rj < (H + KVH) * DEC_D ? 1 : 2);
+          const int rrj = rj - (sj == 0 ? 0 : (sj == 1 ? H * DEC_D : (H + KVH) * DEC_D));
+          const int hq = sj == 0 ? rrj / DEC_D : (rrj / DEC_D) * G + g;
+          if (sj != 0 || g == 0) xput(XL + X.qkv + (long long)hq * 3 * DEC_D + sj * DEC_D + rrj % DEC_D, ostage[j], tag);
         }
       }
       DEC_STAMP(l, 2);
     }
 
-    // ---- D's o_proj rows into LDS: waves 0-3 issue direct-to-LDS loads of this workgroup's rows now;
-    // they land while B and C run (the polls of B, C and D that follow wait for them in order, which
-    // costs nothing: they are older and small)
-    {
+    // ---- D's o_proj rows into LDS (o_proj workgroups): issued now, they land while B and C run ----
+    if (!att) {
       DEC_PART_IDS();
-      if (wave < 4) {
-        const int RB = (hid + NWG - 1) / NWG;                 // <= RF (checked on the host)
-        const long long rmax = min(b * RB + RB, hid) - 1;    // rows past the block re-read its last row
-        const unsigned base = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&wobuf[0];
-        for (int k = wave; k < RB * KC; k += 4) {
-          const long long r = min((long long)(b * RB + k / KC), rmax);
-          dec_dma16(P.wo + r * (H * DEC_D) + (k % KC) * 512 + lane * 8,
-                    __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
-        }
+      const long long d0 = (long long)(b - NB) * RD;
+      const long long rmax = min(d0 + RD, (long long)hid) - 1;   // rows past the block re-read its last row
+      const unsigned base = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&ebuf[0];
+      for (int k = wave; k < RD * KC; k += DEC_WAVES) {
+        const long long r = max(min(d0 + k / KC, rmax), 0ll);
+        dec_dma16(P.wo + r * (H * DEC_D) + (k % KC) * 512 + lane * 8,
+                  __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
       }
     }
 
@@ -487,7 +564,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         red2[wave] = lw;
       }
       __syncthreads();
-      if (tid < DEC_D) {
+      if (tid < DEC_D + 4) {
         float M = -INFINITY;
 #pragma unroll
         for (int w8 = 0; w8 < DEC_WAVES; ++w8) M = fmaxf(M, red[w8]);
@@ -496,21 +573,26 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         for (int w8 = 0; w8 < DEC_WAVES; ++w8) {
           const float lv = red2[w8];
           const float f = lv > 0.f ? __expf(red[w8] - M) : 0.f;
-          o = fmaf(f, osh[w8 * DEC_D + tid], o);
+          o = fmaf(f, osh[w8 * DEC_D + min(tid, DEC_D - 1)], o);
           L = fmaf(f, lv, L);
         }
-        // the head's split partial: o / l (bf16), then m and l as four 16-bit halves
-        uint32_t* pp = XL + X.part + ((long long)hq * NT + split) * (DEC_D + 4);
-        xput(pp + tid, f32_to_bf16(L > 0.f ? o / L : 0.f), tag);
-        if (tid == 0) {
-          const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
-          xput(pp + DEC_D + 0, (uint16_t)(mb >> 16), tag);
-          xput(pp + DEC_D + 1, (uint16_t)(mb & 0xFFFFu), tag);
-          xput(pp + DEC_D + 2, (uint16_t)(lb >> 16), tag);
-          xput(pp + DEC_D + 3, (uint16_t)(lb & 0xFFFFu), tag);
-        }
+        // the head's split partial, one contiguous block: o / l (bf16), then m and l as four
+        // 16-bit halves
+        const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
+        const int e = tid - DEC_D;
+        const uint16_t v = tid < DEC_D ? f32_to_bf16(L > 0.f ? o / L : 0.f)
+                                       : (uint16_t)(((e < 2 ? mb : lb) >> ((e & 1) ? 0 : 16)) & 0xFFFFu);
+        xput(XL + X.part + ((long long)hq * NT + split) * (DEC_D + 4) + tid, v, tag);
       }
       DEC_STAMP(l, 4);
+      // this workgroup's first NL gate / up rows into LDS: its next wait (x1, in E) is some
+      // microseconds away, and these land by then
+      const unsigned base = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&ebuf[0];
+      for (int k = wave; k < NL * 2 * KC; k += DEC_WAVES) {
+        const int i = k / (2 * KC), u = (k / KC) & 1, c = k % KC;
+        dec_dma16((u ? P.wu : P.wg) + (long long)(e0 + i) * hid + c * 512 + lane * 8,
+                  __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
+      }
     }
 
     // ---- C: combine the split partials of one query head (waves 0-3, 2 threads per dimension) ----------
@@ -546,81 +628,78 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       DEC_STAMP(l, 6);
     }
 
-    // ---- D: o_proj + residual (waves 0-3; the rows from LDS) -------------------------------------------
-    {
+    // ---- D: o_proj + residual (o_proj workgroups; the rows from LDS) ------------------------------------
+    if (!att) {
       DEC_PART_IDS();
-      const int RB = (hid + NWG - 1) / NWG;
-      if (wave < 4) dec_vmcnt0();   // this wave's o_proj rows have landed (long ago)
+      dec_vmcnt0();   // this wave's o_proj rows have landed (long ago)
       __syncthreads();
       DEC_STAMP(l, 7);
       xgather<(KC + 1) / 2 * 2, 256>(XL + X.att, H * DEC_D, tag, xs, err, tid);
       DEC_STAMP(l, 8);
-      const unsigned char* ob = (const unsigned char*)wobuf;
-      for (int i = wave; i < RB; i += 4) {
-        const int r = b * RB + i;
-        if (wave < 4 && r < hid) {   // wave-uniform
+      const unsigned char* ob = (const unsigned char*)ebuf;
+      const int d0 = (b - NB) * RD;
+      for (int i = wave; i < RD; i += DEC_WAVES) {
+        const int r = d0 + i;
+        if (r < hid) {   // wave-uniform
           float acc = 0.f;
 #pragma unroll
           for (int c = 0; c < KC; ++c)
             acc = ddot8(*(const uint4*)(xs + c * 512 + lane * 8), *(const uint4*)(ob + (i * KC + c) * 1024 + lane * 16),
                         acc);
           acc = wave_sum(acc);
-          if (lane == 0) xput(XL + X.x1 + r, f32_to_bf16(bfh(xres[r]) + rb(acc)), tag);
+          if (lane == 0) ostage[i] = f32_to_bf16(bfh(xres[r]) + rb(acc));
         }
       }
+      __syncthreads();
+      if (tid < min(RD, hid - d0)) xput(XL + X.x1 + d0 + tid, ostage[tid], tag);
       DEC_STAMP(l, 9);
     }
 
     // ---- E: RMSNorm, gate / up, SiLU(gate) * up -----------------------------------------------------
-    // wave w computes the workgroup's rows w, w + 8, ... (at most EM) with EP rows in flight in a
-    // ring of registers: the first EP are issued before x1 is awaited, and each computed row's slot
-    // is reloaded with the row EP further on. The code is unrolled over EM and every load is
-    // unconditional (a wave with fewer rows re-reads its last one), so no loaded value flows through
-    // a branch join, which would make the compiler wait for every load in flight. F's down_proj
-    // weights follow the last gate / up loads, so the stream runs on into F without a gap.
-    uint4 fw[RF][IC];
+    // Rows e0 .. e0 + NL - 1 are in LDS (attention workgroups). The others, e0 + NL + w + 8 k for wave
+    // w (at most EM), stream through a ring of registers with EP rows in flight: the first EP are
+    // issued before x1 is awaited (they land during the hop), and each computed row's slot is
+    // reloaded with the row EP further on. The code is unrolled over EM and every load is unconditional (a wave with fewer rows
+    // re-reads its last one), so no loaded value flows through a branch join, which would make the
+    // compiler wait for every load in flight. Results are published after the last row: a store
+    // between the loads would sit in the same in-order completion count.
     {
       DEC_PART_IDS();
       constexpr int EP = ED < EM ? ED : EM;
-      const int RBE = (a.inter + NWG - 1) / NWG;   // <= 8 EM (checked on the host)
-      const int r0 = b * RBE;
-      const int n = (min(RBE, a.inter - r0) - wave + DEC_WAVES - 1) / DEC_WAVES;   // this wave's rows (may be <= 0)
-      // rows past the wave's last re-read it (a wave without rows reads the matrix's last row)
-      const long long rlast = min(r0 + wave + (long long)DEC_WAVES * max(n - 1, 0), (long long)a.inter - 1);
+      const int rs = e0 + NL, nr = ecnt - NL;   // ring rows: rs .. rs + nr - 1 (nr <= 8 EM, checked on the host)
+      const int n = (nr - wave + DEC_WAVES - 1) / DEC_WAVES;   // this wave's (may be <= 0)
       uint4 wg[EP][KC], wu[EP][KC];
       auto load_row = [&](int d, int k) {
-        const long long r = min(r0 + wave + (long long)DEC_WAVES * k, rlast);
-#pragma unroll
-        for (int c = 0; c < KC; ++c) {
-          wg[d][c] = ldw(P.wg + r * hid + c * 512 + lane * 8);
-          wu[d][c] = ldw(P.wu + r * hid + c * 512 + lane * 8);
-        }
-      };
-      auto issue_f = [&]() {
-        const int RB = (hid + NWG - 1) / NWG;   // <= RF (checked on the host)
-        const int K8 = a.inter >> 3;
-        const long long rmaxf = min(b * RB + RB, hid) - 1;
-#pragma unroll
-        for (int j = 0; j < RF; ++j) {
-          const long long r = min((long long)(b * RB + j), rmaxf);
-#pragma unroll
-          for (int k = 0; k < IC; ++k) {
-            const int c = min(512 * k + 64 * wave + lane, K8 - 1);   // chunks past the row re-read its last one
-            fw[j][k] = ldw(P.wd + r * a.inter + 8 * c);
-          }
-        }
+        ering_load<KC>(wg[d], wu[d], P.wg, P.wu, ering_row(k, rs, nr, wave, a.inter), hid, lane);
       };
 #pragma unroll
       for (int d = 0; d < EP; ++d) load_row(d, d);
-      if (EM == EP) issue_f();
       const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm2 + 8 * tid) : make_uint4(0, 0, 0, 0);
+      if (att && wave >= 4) dec_vmcnt0();   // waves outside the x1 gather: their LDS loads have landed
       __syncthreads();
       DEC_STAMP(l, 10);
       xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, tid);
       DEC_STAMP(l, 11);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
-      // the rows' results are stored after the last row: a store issued between the loads would
-      // sit in the same in-order completion count, and every later wait for a row would wait for it
+      auto silu_mul = [&](float g, float u) {
+        g = wave_sum(g);
+        u = wave_sum(u);
+        const float gv = rb(g), uv = rb(u);
+        return f32_to_bf16(rb(gv / (1.f + expf(-gv))) * uv);
+      };
+      // the LDS rows first: their results go out while the ring's rows are still arriving
+      const unsigned char* eb = (const unsigned char*)ebuf;
+      for (int i = wave; i < NL; i += DEC_WAVES) {
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          const uint4 xv = *(const uint4*)(xs + c * 512 + lane * 8);
+          g = ddot8(xv, *(const uint4*)(eb + ((i * 2 + 0) * KC + c) * 1024 + lane * 16), g);
+          u = ddot8(xv, *(const uint4*)(eb + ((i * 2 + 1) * KC + c) * 1024 + lane * 16), u);
+        }
+        const uint16_t h = silu_mul(g, u);
+        if (lane == 0) ostage[i] = h;
+      }
       uint16_t hv[EM];
 #pragma unroll
       for (int k = 0; k < EM; ++k) {
@@ -634,31 +713,45 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
             u = ddot8(xv, wu[d][c], u);
           }
         }
-        if (k + EP < EM) {
-          load_row(d, k + EP);
-          if (k + EP == EM - 1) issue_f();
-        }
-        g = wave_sum(g);
-        u = wave_sum(u);
-        const float gv = rb(g), uv = rb(u);
-        hv[k] = f32_to_bf16(rb(gv / (1.f + expf(-gv))) * uv);
+        if (k + EP < EM) load_row(d, k + EP);
+        hv[k] = silu_mul(g, u);
       }
       if (lane == 0) {
 #pragma unroll
         for (int k = 0; k < EM; ++k)
-          if (k < n) xput(XL + X.h + r0 + wave + DEC_WAVES * k, hv[k], tag);
+          if (k < n) ostage[NL + wave + DEC_WAVES * k] = hv[k];
       }
+      __syncthreads();
+      if (tid < ecnt) xput(XL + X.h + e0 + tid, ostage[tid], tag);
       DEC_STAMP(l, 12);
     }
 
-    // ---- F: down_proj + residual (the 8 waves split each row's K; weights issued in E) -----------------
+    // ---- F: down_proj + residual (the 8 waves split each row's K) ---------------------------------------
     {
       DEC_PART_IDS();
       const int RB = (hid + NWG - 1) / NWG;
       const int K8 = a.inter >> 3;
       uint16_t* hs = (uint16_t*)smem;
       __syncthreads();
+      if (tid == 0) xput(XL + X.hdone + b, 0, tag);   // every wave's h rows were stored before the barrier
+      // the weights are issued only now: a CU's memory requests complete in order, so loads issued
+      // before the h stores would hold those stores back, and with them every workgroup's F
+      uint4 fw[RF][IC];
+      {
+        const int K8 = a.inter >> 3;
+        const long long rmaxf = min(b * RB + RB, hid) - 1;
+#pragma unroll
+        for (int j = 0; j < RF; ++j) {
+          const long long r = min((long long)(b * RB + j), rmaxf);
+#pragma unroll
+          for (int k = 0; k < IC; ++k) {
+            const int c = min(512 * k + 64 * wave + lane, K8 - 1);   // chunks past the row re-read its last one
+            fw[j][k] = ldw(P.wd + r * a.inter + 8 * c);
+          }
+        }
+      }
       DEC_STAMP(l, 13);
+      xwait<(DEC_NWG_MAX / 2 + 255) / 256, 256>(XL + X.hdone, NWG, tag, err, tid);
       xgather<(IC * 4096 / 2 + 255) / 256, 256>(XL + X.h, a.inter, tag, hs, err, tid);
       DEC_STAMP(l, 14);
       float part[RF];
@@ -794,8 +887,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     decode_body<KC, IC, EM>(a); \
   }
 
-DECODE_KERNEL(3, 3, 5)   // hidden 1536, inter <= 10240 (Qwen2.5-1.5B: 8960)
-DECODE_KERNEL(3, 3, 6)   // hidden 1536, inter <= 12288
-DECODE_KERNEL(1, 1, 1)   // hidden 512, inter <= 2048
-DECODE_KERNEL(1, 1, 2)   // hidden 512, inter <= 4096
-DECODE_KERNEL(2, 2, 4)   // hidden 1024, inter <= 8192
+DECODE_KERNEL(3, 3, 3)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 splits: 20 streamed rows)
+DECODE_KERNEL(3, 3, 4)   // hidden 1536, up to 32 streamed gate/up rows per workgroup
+DECODE_KERNEL(3, 3, 6)   // hidden 1536, up to 48
+DECODE_KERNEL(1, 1, 1)   // hidden 512, up to 8
+DECODE_KERNEL(1, 1, 2)   // hidden 512, up to 16
+DECODE_KERNEL(2, 2, 4)   // hidden 1024, up to 32

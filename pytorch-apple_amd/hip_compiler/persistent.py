@@ -32,7 +32,8 @@ SPL = 128            # positions per attention split
 MAX_G = 8            # query heads per KV head
 MAX_SPLITS = 32
 VARIANTS = {1, 2, 3}     # hidden / 512 with a kernel instance (inter <= 4096 * that)
-ROWS_PER_WAVE = {1: (1, 2), 2: (4,), 3: (5, 6)}   # gate/up rows per wave of each instance (inter <= 2048 * that)
+E_LDS_ROWS = {1: 48, 2: 32, 3: 21}   # gate/up rows an attention workgroup holds in LDS (decode.hip DEC_NE)
+RING_ROWS = {1: (1, 2), 2: (4,), 3: (3, 4, 6)}   # instances: gate/up rows per wave streamed through registers
 
 TABLE_FIELDS = ("norm1", "wq", "bq", "wk", "bk", "wv", "bv", "kc", "vc", "wo", "norm2", "wg", "wu", "wd")
 
@@ -49,9 +50,12 @@ def enabled() -> bool:
 def exchange_words(L: int, hidden: int, inter: int, H: int, KVH: int, nsplit: int) -> int:
     """32-bit words of the exchange area (decode.hip ``xlayout``): per layer the input row, each
     query head's q row with its KV head's k and v rows, the attention partials (o[D] plus m and l as four half-words per split and
-    head), the combined attention row, the o_proj output and the SiLU * up row; then the final
-    row, one 64-bit argmax key per workgroup and two control words (step tag, timeout flag)."""
-    stride = hidden + H * 3 * D + H * nsplit * (D + 4) + H * D + hidden + inter
+    head), the combined attention row, the o_proj output, the SiLU * up row and one "done" word
+    per workgroup for it; then the final row, one 64-bit argmax key per workgroup and two control
+    words (step tag, timeout flag)."""
+    hdone = hidden + H * 3 * D + H * nsplit * (D + 4) + H * D + hidden + inter
+    hdone += hdone & 1
+    stride = hdone + NWG
     stride += stride & 1
     return stride * L + hidden + 2 * NWG + 2
 
@@ -83,13 +87,21 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     if int(q0["D"]) != D or H * D != hidden or hidden % 512 or hidden // 512 not in VARIANTS:
         return None
     KC = hidden // 512
-    em = [e for e in ROWS_PER_WAVE[KC] if inter <= 2048 * e]
-    if H % KVH or H // KVH > MAX_G or inter % 8 or inter > 4096 * KC or not em or (H + 2 * KVH) * D > 8 * NWG:
+    if H % KVH or H // KVH > MAX_G or inter % 8 or inter > 4096 * KC or (H + 2 * KVH) * D > 8 * NWG:
         return None
     # attention runs one workgroup per (query head, split), the combine one per query head
     if S % SPL or S // SPL > MAX_SPLITS or H * (S // SPL) + H > NWG or vocab >= 2 ** 32:
         return None
     nsplit = S // SPL
+    # the work split of decode.hip: NB attention workgroups (each also holds NE gate/up rows in
+    # LDS), ND o_proj workgroups of RD rows; every workgroup streams at most RBD gate/up rows
+    NB, NE = H * nsplit, E_LDS_ROWS[KC]
+    ND = NWG - NB
+    RD = -(-hidden // ND)
+    RBD = max(inter - NB * NE + NWG - 1, 0) // NWG
+    em = [e for e in RING_ROWS[KC] if 8 * e >= RBD]
+    if RD > 2 * NE or not em or NE + RBD > 128:   # decode.hip DEC_OSTAGE: a workgroup's rows, staged
+        return None
     if nsplit * (D + 4) * 2 > 8192 * KC:   # the combine stages a head's partials in LDS
         return None
     shared = ("pos_ids", "cache_pos", "inv_freq")
