@@ -43,7 +43,6 @@
 #define DEC_SPL 128                   // positions per attention split: 8 waves x 16
 #define DEC_MAXG 8                    // query heads per KV head, at most
 #define DEC_TIMEOUT 2000000ull        // 20 ms of the 100 MHz real-time counter
-#define DEC_NWG_MAX 256               // workgroups of the launch, at most
 #define DEC_OSTAGE 128                // o_proj or gate / up rows of one workgroup, at most
 #ifndef DEC_ED
 #define DEC_ED 2                      // gate/up rows in flight per wave
@@ -162,37 +161,6 @@ __device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag
   __syncthreads();
 }
 
-// Waits until the n words at src (n even, src 8-byte aligned) carry `tag`, like xgather without
-// the copy: for the per-workgroup "done" words polled before a large gather, so the repeated
-// rounds of a wait read a few hundred words instead of the whole row.
-template <int NPT, int NTH>
-__device__ __forceinline__ void xwait(const uint32_t* src, int n, uint32_t tag, uint32_t* err, int tid) {
-  if (tid < NTH) {
-    const int np = n >> 1;
-    const unsigned long long want = ((unsigned long long)tag << 48) | ((unsigned long long)tag << 16);
-    const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
-    unsigned long long v[NPT];
-#pragma unroll
-    for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
-    const unsigned long long t0 = wall_clock64();
-    while (true) {
-      bool ok = true;
-#pragma unroll
-      for (int j = 0; j < NPT; ++j)
-        ok = ok && ((v[j] & tmask) == want || tid + NTH * j >= np);
-      if (ok) break;
-      if (wall_clock64() - t0 > DEC_TIMEOUT) {
-        dec_fail(err);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-      for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
-    }
-  }
-  __syncthreads();
-}
-
 // 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane (gfx950), from inline
 // assembly: the compiler does not count these loads, so it inserts no wait for them (before a
 // barrier or an LDS read); the waves that issue them wait explicitly (dec_vmcnt0) before the
@@ -204,7 +172,7 @@ __device__ __forceinline__ void dec_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)"
 
 // Word offsets of one layer's exchange slots (all even, so word pairs are 8-byte aligned).
 struct XLayout {
-  long long qkv, part, att, x1, h, hdone, stride;
+  long long qkv, part, att, x1, h, stride;
 };
 
 __device__ __forceinline__ XLayout xlayout(const PersistArgs& a) {
@@ -215,9 +183,7 @@ __device__ __forceinline__ XLayout xlayout(const PersistArgs& a) {
   o.att = o.part + (long long)a.H * a.nsplit * (DEC_D + 4);          // per head: nsplit x (o[D], m, l)
   o.x1 = o.att + (long long)a.H * DEC_D;
   o.h = o.x1 + hid;
-  o.hdone = o.h + a.inter;                                            // one word per workgroup: its h rows are out
-  o.hdone += o.hdone & 1;
-  o.stride = o.hdone + a.nwg;
+  o.stride = o.h + a.inter;
   o.stride += o.stride & 1;
   return o;
 }
@@ -733,7 +699,6 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       const int K8 = a.inter >> 3;
       uint16_t* hs = (uint16_t*)smem;
       __syncthreads();
-      if (tid == 0) xput(XL + X.hdone + b, 0, tag);   // every wave's h rows were stored before the barrier
       // the weights are issued only now: a CU's memory requests complete in order, so loads issued
       // before the h stores would hold those stores back, and with them every workgroup's F
       uint4 fw[RF][IC];
@@ -751,7 +716,6 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         }
       }
       DEC_STAMP(l, 13);
-      xwait<(DEC_NWG_MAX / 2 + 255) / 256, 256>(XL + X.hdone, NWG, tag, err, tid);
       xgather<(IC * 4096 / 2 + 255) / 256, 256>(XL + X.h, a.inter, tag, hs, err, tid);
       DEC_STAMP(l, 14);
       float part[RF];

@@ -50,12 +50,9 @@ def enabled() -> bool:
 def exchange_words(L: int, hidden: int, inter: int, H: int, KVH: int, nsplit: int) -> int:
     """32-bit words of the exchange area (decode.hip ``xlayout``): per layer the input row, each
     query head's q row with its KV head's k and v rows, the attention partials (o[D] plus m and l as four half-words per split and
-    head), the combined attention row, the o_proj output, the SiLU * up row and one "done" word
-    per workgroup for it; then the final row, one 64-bit argmax key per workgroup and two control
-    words (step tag, timeout flag)."""
-    hdone = hidden + H * 3 * D + H * nsplit * (D + 4) + H * D + hidden + inter
-    hdone += hdone & 1
-    stride = hdone + NWG
+    head), the combined attention row, the o_proj output and the SiLU * up row; then the final
+    row, one 64-bit argmax key per workgroup and two control words (step tag, timeout flag)."""
+    stride = hidden + H * 3 * D + H * nsplit * (D + 4) + H * D + hidden + inter
     stride += stride & 1
     return stride * L + hidden + 2 * NWG + 2
 
