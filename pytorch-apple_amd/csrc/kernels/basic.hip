@@ -32,21 +32,24 @@ extern "C" __global__ void __launch_bounds__(256) k_copy(const CopyArgs a) {
 }
 
 // Contiguous copy of a.n 16-byte chunks (src and dst 16-byte aligned, same dtype): the generic
-// kernel above spends its time on per-element index arithmetic; here each thread keeps four
-// 16-byte loads in flight per pass of a grid-stride loop.
+// kernel above spends its time on per-element index arithmetic. Here workgroup b copies one
+// contiguous range of ceil(n / grid) chunks, each thread with eight non-temporal 16-byte loads in
+// flight (measured on 512 MiB: 5.7 TB/s of read + write, against 4.6 for a grid-stride loop with
+// four cached loads and 4.7 for hipMemcpy device to device).
+typedef unsigned int copy_u32x4 __attribute__((ext_vector_type(4)));
 extern "C" __global__ void __launch_bounds__(256) k_copy16(const CopyArgs a) {
-  const uint4* s = (const uint4*)a.src;
-  uint4* d = (uint4*)a.dst;
-  const long long n = a.n, T = (long long)gridDim.x * blockDim.x;
-  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  for (; i + 3 * T < n; i += 4 * T) {
-    const uint4 v0 = s[i], v1 = s[i + T], v2 = s[i + 2 * T], v3 = s[i + 3 * T];
-    d[i] = v0;
-    d[i + T] = v1;
-    d[i + 2 * T] = v2;
-    d[i + 3 * T] = v3;
+  const copy_u32x4* s = (const copy_u32x4*)a.src;
+  copy_u32x4* d = (copy_u32x4*)a.dst;
+  const long long n = a.n, C = (n + gridDim.x - 1) / gridDim.x;
+  const long long b0 = (long long)blockIdx.x * C, e = min(b0 + C, n);
+  for (long long i = b0 + threadIdx.x; i < e; i += 8 * 256) {
+    copy_u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(s + min(i + u * 256, e - 1));   // past the range: re-read its last chunk
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i + u * 256 < e) __builtin_nontemporal_store(v[u], d + i + u * 256);
   }
-  for (; i < n; i += T) d[i] = s[i];
 }
 
 extern "C" __global__ void __launch_bounds__(256) k_fill(const FillArgs a) {

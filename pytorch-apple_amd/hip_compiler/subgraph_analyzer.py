@@ -303,13 +303,14 @@ class Lowering:
         nbytes = n * ELEM_SIZE[src.dtype]
         if src.dtype == dst.dtype and src.is_contiguous() and dst.is_contiguous() and nbytes % 16 == 0 and \
                 (src.offset * ELEM_SIZE[src.dtype]) % 16 == 0 and (dst.offset * ELEM_SIZE[dst.dtype]) % 16 == 0:
-            # a plain byte copy: 16-byte chunks, four in flight per thread
+            # a plain byte copy: 16-byte chunks, one contiguous range per workgroup, eight chunks
+            # in flight per thread
             chunks = nbytes // 16
             self.emit(LaunchStep(
                 kind="copy", kernel="k_copy16", module="basic", arg_struct="CopyArgs",
                 args=dict(dst=self.ref(dst), src=self.ref(src), n=chunks, shape=[1] * 6, sstride=[0] * 6,
                           dstride=[0] * 6, ndim=1, sdtype=DTYPE_CODE[src.dtype], ddtype=DTYPE_CODE[dst.dtype]),
-                grid=grid1d(chunks, cap=8192), inputs=ins, outputs=outs, params={"total": n}))
+                grid=grid1d(-(-chunks // 8), cap=8192), inputs=ins, outputs=outs, params={"total": n}))
             return
         self.emit(LaunchStep(
             kind="copy", kernel="k_copy", module="basic", arg_struct="CopyArgs",
