@@ -421,10 +421,10 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     }
 
     // ---- the past positions' K / V rows and mask values for B: no dependency on this step's
-    // activations, so they are issued before B waits for its q / k / v (after A, whose input poll
-    // would otherwise wait behind them)
+    // activations, so the K rows are issued before B waits for its q / k / v (after A, whose input
+    // poll would otherwise wait behind them); the V rows, needed last, are issued once q / k / v
+    // are in, so the poll does not wait behind them either and their latency overlaps the scores
     uint4 kr[4];
-    uint32_t vr[16];
     FRaw mraw = {0, 0};
     {
       DEC_PART_IDS();
@@ -432,18 +432,13 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       const int kq = lane >> 2, kc = lane & 3;
       if (att) {
         const uint16_t* Kb = P.kc + (long long)kvh * kvs;
-        const uint16_t* Vb = P.vc + (long long)kvh * kvs;
         if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(p0 + kq, last), a.mask_dtype);
         const uint4* ks = (const uint4*)(Kb + min(p0 + kq, last) * DEC_D + kc * 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
-#pragma unroll
-        for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(p0 + t, last) * DEC_D + 2 * lane);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) kr[j] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < 16; ++t) vr[t] = 0;
       }
     }
 
@@ -460,6 +455,12 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       __syncthreads();
       xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, tid);
       DEC_STAMP(l, 3);
+      uint32_t vr[16];
+      {
+        const uint16_t* Vb = P.vc + (long long)kvh * kvs;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(p0 + t, last) * DEC_D + 2 * lane);
+      }
       if (tid < 128) {   // rotate_half RoPE: threads 0..63 q, 64..127 k
         const int hs = tid >> 6, j = tid & 63;
         const float x0 = bfh(raw[hs * DEC_D + j]), x1 = bfh(raw[hs * DEC_D + j + 64]);
@@ -474,16 +475,14 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         stg2(P.kc + (long long)kvh * kvs + cpos * DEC_D + tid, rot[DEC_D + tid]);
         stg2(P.vc + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
       }
-      if (cin && cpos >= p0 && cpos < p0 + 16) {   // the wave holding that position uses the new row
-        if (p0 + kq == cpos) {
-          const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
+      // the wave holding that position uses the new K / V row (V chosen at its use below, so no
+      // branch joins the loaded V values, which would make the compiler wait for them here)
+      const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
+      const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
+      if (vnew && p0 + kq == cpos) {
+        const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) kr[j] = kn[j];
-        }
-        const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
-#pragma unroll
-        for (int t = 0; t < 16; ++t)
-          if (p0 + t == cpos) vr[t] = vn;
+        for (int j = 0; j < 4; ++j) kr[j] = kn[j];
       }
       const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
       const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
@@ -519,8 +518,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
           const float p = HS_RL(e, 4 * t);
-          acc0 = fmaf(p, bfh((uint16_t)(vr[t] & 0xffffu)), acc0);
-          acc1 = fmaf(p, bfh((uint16_t)(vr[t] >> 16)), acc1);
+          const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
+          acc0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), acc0);
+          acc1 = fmaf(p, bfh((uint16_t)(vt >> 16)), acc1);
         }
       }
       osh[wave * DEC_D + 2 * lane] = acc0;
