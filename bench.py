@@ -926,6 +926,34 @@ def main_resnet(args) -> int:
             conv_flops += f
         per_kernel[kname] = e
         log(f"  {kname}: {e}")
+    # per conv: its floor max(FLOPs / MFMA peak, algorithmic bytes / HBM peak) next to its own measured
+    # time (the conv launch plus its split-K reduce, if any, each timed alone on the launch stream)
+    conv_rows = []
+    for i, st in enumerate(program.steps):
+        if st.kind != "conv" or st.params.get("reduce"):
+            continue
+        a, pm = st.args, st.params
+        kh, kw = pm["kernel"]
+        cout, m = a.get("Cout", a.get("N")), a["M"]
+        kalg = pm.get("K_alg", a["K"])
+        cin = kalg // (kh * kw)
+        hw_o = a["cHo"] * a["cWo"]
+        nimg = m // hw_o
+        # the stem reads a pre-padded buffer: its algorithmic input is the unpadded image
+        hin = a["cH"] - (2 * pm["padding"][0] if a.get("cph", 0) == 0 else 0)
+        win = a["cW"] - (2 * pm["padding"][1] if a.get("cpw", 0) == 0 else 0)
+        nbytes = 2 * (nimg * hin * win * cin + cout * kalg + m * cout * (2 if pm.get("residual") else 1))
+        f = 2.0 * m * cout * kalg
+        t_f, t_b = f / (MFMA_PEAK_TFLOPS * 1e12) * 1e6, nbytes / (HBM_PEAK_GBS * 1e9) * 1e6
+        idx = [i] + ([i + 1] if i + 1 < len(program.steps) and program.steps[i + 1].params.get("reduce") else [])
+        meas = time_kernel_subset(hexec, idx, max(1, args.kernel_repeats // 5), stream) * 1e3
+        conv_rows.append({"conv": pm["nodes"][0], "kernel": st.kernel,
+                          "shape": f"{nimg}x{hin}x{win}x{cin} -> {cout} k{kh}x{kw} s{pm['stride'][0]}",
+                          "floor_us": round(max(t_f, t_b), 2), "bound": "mfma" if t_f >= t_b else "hbm",
+                          "measured_us": round(meas, 2), "launches": len(idx)})
+    floor_sum = sum(r["floor_us"] for r in conv_rows)
+    meas_sum = sum(r["measured_us"] for r in conv_rows)
+    log(f"conv roofline: floor {floor_sum:.1f} us vs measured {meas_sum:.1f} us over {len(conv_rows)} convs")
     # per conv launch (every conv has its own shape): time each inside the family replay
     n_red = sum(1 for s in program.steps if s.kind == "conv" and s.params.get("reduce"))
     n_conv = sum(1 for s in program.steps if s.kind == "conv") - n_red
@@ -966,6 +994,10 @@ def main_resnet(args) -> int:
                      "traffic": None},
         "step_roofline": {"flops_per_step": flops, "achieved": round(step_tf, 1), "unit": "TFLOP/s",
                           "frac": round(step_tf / MFMA_PEAK_TFLOPS, 4)},
+        "conv_roofline": {"floor_us_sum": round(floor_sum, 1), "measured_us_sum": round(meas_sum, 1),
+                          "floor_frac": round(floor_sum / meas_sum, 4) if meas_sum else None,
+                          "floor": "max(FLOPs / 2.5 PFLOP/s, algorithmic bytes / 8 TB/s) per conv",
+                          "per_conv": conv_rows},
         "kernels": per_kernel,
         "cpu_baseline": cpu,
     }
