@@ -751,6 +751,7 @@ __device__ __forceinline__ void st8_f(void* p, long long i, int dt, const float*
 #define HS_QUAD_XOR2 0x4E
 #define HS_ROW_ROR4 0x124
 #define HS_ROW_ROR8 0x128
+#define HS_ROW_ROR12 0x12C   // row_ror:n moves lane j's value to lane j + n (mod 16)
 
 // sum / max over the 64 lanes of a wave; every lane gets the result
 __device__ __forceinline__ float wave_sum(float v) {
@@ -767,6 +768,60 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, HS_DPP(v, HS_ROW_ROR4));
   v = fmaxf(v, HS_DPP(v, HS_ROW_ROR8));
   return fmaxf(fmaxf(HS_RL(v, 0), HS_RL(v, 16)), fmaxf(HS_RL(v, 32), HS_RL(v, 48)));
+}
+
+#define HS_ROW_MIRROR 0x140        // lane j of a row of 16 reads lane 15 - j
+#define HS_ROW_HALF_MIRROR 0x141   // lane j of a half-row of 8 reads lane 7 - j
+
+// Sums of several values over the 64 lanes at once, halving the values each step (each lane
+// keeps one value of every exchanged pair and receives its partner's other one): 8 or 16
+// values cost about as much as two or three single wave_sum calls. gfx950's permlane32 / 16
+// swaps exchange the upper 32 lanes of one value with the lower 32 of another (odd rows of 16
+// with even rows, for the 16-lane form), so one swap and one add halve two values.
+__device__ __forceinline__ void hs_swap_add(float a, float b, bool rows16, float& out) {
+  const unsigned ua = __builtin_bit_cast(unsigned, a), ub = __builtin_bit_cast(unsigned, b);
+  if (rows16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+    out = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+    out = __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+  }
+}
+
+// v[0..15] per lane -> in lane l, the total over the wave of value
+// ((l >> 5) & 1) * 8 + ((l >> 4) & 1) * 4 + ((l >> 3) & 1) * 2 + ((l >> 2) & 1)
+// (lane 8 s + 4 holds value 2 s + 1, lane 8 s value 2 s; the 4 lanes of a quad agree)
+__device__ __forceinline__ float wave_sum16(const float (&v)[16], int lane) {
+  float w[8], x[4], y[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) hs_swap_add(v[i], v[i + 8], false, w[i]);   // value bit 3 = lane bit 5
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hs_swap_add(w[i], w[i + 4], true, x[i]);    // value bit 2 = lane bit 4
+  const bool b3 = (lane & 8) != 0, b2 = (lane & 4) != 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)   // value bit 1 = lane bit 3 (lane j pairs with 15 - j)
+    y[i] = (b3 ? x[i + 2] : x[i]) + HS_DPP(b3 ? x[i] : x[i + 2], HS_ROW_MIRROR);
+  float z = (b2 ? y[1] : y[0]) + HS_DPP(b2 ? y[0] : y[1], HS_ROW_HALF_MIRROR);   // value bit 0 = lane bit 2
+  z += HS_DPP(z, HS_QUAD_XOR2);
+  z += HS_DPP(z, HS_QUAD_XOR1);
+  return z;
+}
+
+// v[0..7] per lane -> in lane l, the total over the wave of value
+// ((l >> 5) & 1) * 4 + ((l >> 4) & 1) * 2 + ((l >> 3) & 1) (every lane of an 8-lane group agrees)
+__device__ __forceinline__ float wave_sum8(const float (&v)[8], int lane) {
+  float w[4], x[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) hs_swap_add(v[i], v[i + 4], false, w[i]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) hs_swap_add(w[i], w[i + 2], true, x[i]);
+  const bool b3 = (lane & 8) != 0;
+  float z = (b3 ? x[1] : x[0]) + HS_DPP(b3 ? x[0] : x[1], HS_ROW_MIRROR);
+  z += HS_DPP(z, HS_ROW_HALF_MIRROR);
+  z += HS_DPP(z, HS_QUAD_XOR2);
+  z += HS_DPP(z, HS_QUAD_XOR1);
+  return z;
 }
 
 // ---------------------------------------------------------------- argmax over long rows

@@ -650,26 +650,37 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, tid);
       DEC_STAMP(l, 11);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
-      auto silu_mul = [&](float g, float u) {
-        g = wave_sum(g);
-        u = wave_sum(u);
-        const float gv = rb(g), uv = rb(u);
-        return f32_to_bf16(rb(gv / (1.f + expf(-gv))) * uv);
-      };
-      // the LDS rows first: their results go out while the ring's rows are still arriving
-      const unsigned char* eb = (const unsigned char*)ebuf;
-      for (int i = wave; i < NL; i += DEC_WAVES) {
-        float g = 0.f, u = 0.f;
+      uint4 xv[KC];
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-          const uint4 xv = *(const uint4*)(xs + c * 512 + lane * 8);
-          g = ddot8(xv, *(const uint4*)(eb + ((i * 2 + 0) * KC + c) * 1024 + lane * 16), g);
-          u = ddot8(xv, *(const uint4*)(eb + ((i * 2 + 1) * KC + c) * 1024 + lane * 16), u);
+      for (int c = 0; c < KC; ++c) xv[c] = *(const uint4*)(xs + c * 512 + lane * 8);
+      // per-lane partial sums of this wave's rows: slot k < MLW is LDS row wave + 8 k, slot
+      // MLW + k ring row k; summed over the wave 8 slots (16 values) at a time afterwards
+      constexpr int MLW = (NE + DEC_WAVES - 1) / DEC_WAVES, NS = MLW + EM, NG = (NS + 7) / 8;
+      float gs[8 * NG], us[8 * NG];
+#pragma unroll
+      for (int s = 0; s < 8 * NG; ++s) gs[s] = us[s] = 0.f;
+      // the LDS rows first (a row's 2 KC reads issued together)
+      if (NL > 0) {   // workgroup-uniform
+        const unsigned char* eb = (const unsigned char*)ebuf;
+#pragma unroll
+        for (int k = 0; k < MLW; ++k) {
+          const int i = wave + DEC_WAVES * k, ii = min(i, NL - 1);
+          uint4 eg[KC], eu[KC];
+#pragma unroll
+          for (int c = 0; c < KC; ++c) {
+            eg[c] = *(const uint4*)(eb + ((ii * 2 + 0) * KC + c) * 1024 + lane * 16);
+            eu[c] = *(const uint4*)(eb + ((ii * 2 + 1) * KC + c) * 1024 + lane * 16);
+          }
+          float g = 0.f, u = 0.f;
+#pragma unroll
+          for (int c = 0; c < KC; ++c) {
+            g = ddot8(xv[c], eg[c], g);
+            u = ddot8(xv[c], eu[c], u);
+          }
+          gs[k] = i < NL ? g : 0.f;
+          us[k] = i < NL ? u : 0.f;
         }
-        const uint16_t h = silu_mul(g, u);
-        if (lane == 0) ostage[i] = h;
       }
-      uint16_t hv[EM];
 #pragma unroll
       for (int k = 0; k < EM; ++k) {
         const int d = k % EP;
@@ -677,18 +688,34 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         if (k < n) {   // wave-uniform
 #pragma unroll
           for (int c = 0; c < KC; ++c) {
-            const uint4 xv = *(const uint4*)(xs + c * 512 + lane * 8);
-            g = ddot8(xv, wg[d][c], g);
-            u = ddot8(xv, wu[d][c], u);
+            g = ddot8(xv[c], wg[d][c], g);
+            u = ddot8(xv[c], wu[d][c], u);
           }
         }
         if (k + EP < EM) load_row(d, k + EP);
-        hv[k] = silu_mul(g, u);
+        gs[MLW + k] = g;
+        us[MLW + k] = u;
       }
-      if (lane == 0) {
+      // lane 8 s + 4 j of group q ends with slot 8 q + s's gate (j = 0) or up (j = 1) total; lane
+      // 8 s computes SiLU(gate) * up and stages it under the slot's row
 #pragma unroll
-        for (int k = 0; k < EM; ++k)
-          if (k < n) ostage[NL + wave + DEC_WAVES * k] = hv[k];
+      for (int q = 0; q < NG; ++q) {
+        float v[16];
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          v[2 * s] = gs[8 * q + s];
+          v[2 * s + 1] = us[8 * q + s];
+        }
+        const float t = wave_sum16(v, lane);
+        // row_ror:12 moves lane j + 4's value (mod 16) to lane j: lane 8 s receives the up total
+        const float gv = rb(t), uv = rb(HS_DPP(t, HS_ROW_ROR12));
+        const uint16_t h = f32_to_bf16(rb(gv / (1.f + expf(-gv))) * uv);
+        const int s = 8 * q + (lane >> 3);
+        if ((lane & 7) == 0 && s < NS) {
+          const int k = s < MLW ? s : s - MLW;
+          const bool ok = s < MLW ? wave + DEC_WAVES * k < NL : k < n;
+          if (ok) ostage[(s < MLW ? 0 : NL) + wave + DEC_WAVES * k] = h;
+        }
       }
       __syncthreads();
       if (tid < ecnt) xput(XL + X.h + e0 + tid, ostage[tid], tag);
@@ -733,10 +760,13 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
           for (int j = 0; j < RF; ++j) part[j] = ddot8(hv, fw[j][k], part[j]);
         }
       }
+      {   // the RF (<= 8) row sums of this wave at once: lane 8 j ends with row j's
+        static_assert(RF <= 8, "down_proj rows per workgroup");
+        float v[8];
 #pragma unroll
-      for (int j = 0; j < RF; ++j) {
-        const float sum = wave_sum(part[j]);
-        if (lane == 0) red[wave * 8 + j] = sum;
+        for (int j = 0; j < 8; ++j) v[j] = j < RF ? part[j] : 0.f;
+        const float sum = wave_sum8(v, lane);
+        if ((lane & 7) == 0 && (lane >> 3) < RF) red[wave * 8 + (lane >> 3)] = sum;
       }
       if (tid < 14) ptab[(l + 1) & 1][tid] = pnext;   // the next layer's tensors (read after the barrier)
       __syncthreads();
