@@ -50,7 +50,8 @@
 #ifndef DEC_R4
 #define DEC_R4 2                      // lm_head rows per wave in each of its two rounds in flight
 #endif
-#define DEC_NE(KC) ((KC) == 3 ? 21 : ((KC) == 2 ? 32 : 48))   // gate/up rows in LDS per attention workgroup
+#define DEC_NE(KC) ((KC) == 3 ? 24 : ((KC) == 2 ? 32 : 48))   // gate/up rows in LDS per attention workgroup
+#define DEC_SMEM (32 * (DEC_D + 4) * 2)   // per-part staging: the combine's partials of up to 32 splits
 
 typedef __attribute__((ext_vector_type(2))) __bf16 dec_bf16x2;
 typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
@@ -290,13 +291,14 @@ __device__ __forceinline__ DecodeLayerPtrs dec_layer(const void* const* t) {
 // attention workgroup loads into LDS once its attention part is done.
 template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC)>
 __device__ __forceinline__ void decode_body(const PersistArgs& a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[IC * 8192];   // per-part staging (F: inter bf16)
+  __shared__ __attribute__((aligned(16))) unsigned char smem[DEC_SMEM];   // per-part staging (B, C; xs)
   __shared__ __attribute__((aligned(16))) uint16_t xres[512 * KC];
   __shared__ float red[DEC_WAVES * 8];
   __shared__ float red2[DEC_WAVES * DEC_MAXG];
   __shared__ float rope_cs[128];
   // an attention workgroup's first NE gate / up rows (row i: gate chunks, then up chunks, 1 KB
-  // each); in the other workgroups, their o_proj rows (at most 2 NE)
+  // each); in the other workgroups, their o_proj rows (at most 2 NE), then (except the combine
+  // workgroups) their first NEO gate / up rows. F stages the SiLU * up row here.
   __shared__ __attribute__((aligned(16))) uint4 ebuf[NE * 2 * KC * 64];
   __shared__ const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
   __shared__ unsigned long long kred[DEC_WAVES];
@@ -342,11 +344,17 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
   const int kvh = tile / NT, split = tile % NT;
   const bool comb = b >= NB && b < NB + H;
   const int RD = (hid + ND - 1) / ND;                                   // <= 2 NE (checked on the host)
-  const int RBD = max(a.inter - NB * NE + NWG - 1, 0) / NWG;            // gate / up rows streamed per workgroup
-  const int RBB = NE + RBD;                                             // an attention workgroup's rows
-  const int e0 = att ? b * RBB : NB * RBB + (b - NB) * RBD;             // first gate / up row
-  const int ecnt = max(min(att ? RBB : RBD, a.inter - e0), 0);          // its rows
-  const int NL = att ? min(NE, ecnt) : 0;                               // of which in LDS
+  // gate / up rows in LDS: NE on an attention workgroup; NEO behind the o_proj rows of an o_proj
+  // workgroup that runs no combine (issued with its o_proj rows, they land while it waits for
+  // the attention row); none on a combine workgroup, whose partials poll comes sooner
+  const int NEO = max(2 * NE - RD, 0) / 2;
+  const int NLC = att ? NE : (comb ? 0 : NEO);
+  const int RBD = max(a.inter - NB * NE - (ND - H) * NEO + NWG - 1, 0) / NWG;   // gate / up rows streamed per workgroup
+  const int e0 = att ? b * (NE + RBD)                                   // first gate / up row
+                     : NB * (NE + RBD) + (b - NB) * RBD + max(b - NB - H, 0) * NEO;
+  const int ecnt = max(min(NLC + RBD, a.inter - e0), 0);                // its rows
+  const int NL = min(NLC, ecnt);                                        // of which in LDS
+  const unsigned EOFF = att ? 0u : (unsigned)(RD * KC * 1024);          // where they sit in ebuf
   // layer 0's tensors into LDS; each layer loads the next one's during its first part and stores
   // them in F, so no layer waits for its table at its start
   if (tid < 14) ptab[0][tid] = ((const void* const*)a.layers)[tid];
@@ -420,6 +428,11 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         const long long r = max(min(d0 + k / KC, rmax), 0ll);
         dec_dma16(P.wo + r * (H * DEC_D) + (k % KC) * 512 + lane * 8,
                   __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
+      }
+      for (int k = wave; k < NL * 2 * KC; k += DEC_WAVES) {   // and the first NL gate / up rows
+        const int i = k / (2 * KC), u = (k / KC) & 1, c = k % KC;
+        dec_dma16((u ? P.wu : P.wg) + (long long)(e0 + i) * hid + c * 512 + lane * 8,
+                  __builtin_amdgcn_readfirstlane(base + EOFF + (unsigned)k * 1024u));
       }
     }
 
@@ -607,17 +620,32 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       DEC_STAMP(l, 8);
       const unsigned char* ob = (const unsigned char*)ebuf;
       const int d0 = (b - NB) * RD;
-      for (int i = wave; i < RD; i += DEC_WAVES) {
-        const int r = d0 + i;
-        if (r < hid) {   // wave-uniform
-          float acc = 0.f;
+      uint4 xv[KC];
 #pragma unroll
-          for (int c = 0; c < KC; ++c)
-            acc = ddot8(*(const uint4*)(xs + c * 512 + lane * 8), *(const uint4*)(ob + (i * KC + c) * 1024 + lane * 16),
-                        acc);
-          acc = wave_sum(acc);
-          if (lane == 0) ostage[i] = f32_to_bf16(bfh(xres[r]) + rb(acc));
+      for (int c = 0; c < KC; ++c) xv[c] = *(const uint4*)(xs + c * 512 + lane * 8);
+      // rows wave + 8 k (RD <= 2 NE); the row sums of 8 of them at a time: lane 8 k ends with row k's
+      constexpr int MD = (2 * NE + DEC_WAVES - 1) / DEC_WAVES;
+#pragma unroll
+      for (int q = 0; q < (MD + 7) / 8; ++q) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int i = wave + DEC_WAVES * (8 * q + k);
+          v[k] = 0.f;
+          if (8 * q + k < MD && i < RD && d0 + i < hid) {   // wave-uniform
+            uint4 w[KC];
+#pragma unroll
+            for (int c = 0; c < KC; ++c) w[c] = *(const uint4*)(ob + (i * KC + c) * 1024 + lane * 16);
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) acc = ddot8(xv[c], w[c], acc);
+            v[k] = acc;
+          }
         }
+        const float sum = wave_sum8(v, lane);
+        const int i = wave + DEC_WAVES * (8 * q + (lane >> 3));
+        if ((lane & 7) == 0 && 8 * q + (lane >> 3) < MD && i < RD && d0 + i < hid)
+          ostage[i] = f32_to_bf16(bfh(xres[d0 + i]) + rb(sum));
       }
       __syncthreads();
       if (tid < min(RD, hid - d0)) xput(XL + X.x1 + d0 + tid, ostage[tid], tag);
@@ -625,7 +653,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     }
 
     // ---- E: RMSNorm, gate / up, SiLU(gate) * up -----------------------------------------------------
-    // Rows e0 .. e0 + NL - 1 are in LDS (attention workgroups). The others, e0 + NL + w + 8 k for wave
+    // Rows e0 .. e0 + NL - 1 are in LDS. The others, e0 + NL + w + 8 k for wave
     // w (at most EM), stream through a ring of registers with EP rows in flight: the first EP are
     // issued before x1 is awaited (they land during the hop), and each computed row's slot is
     // reloaded with the row EP further on. The code is unrolled over EM and every load is unconditional (a wave with fewer rows
@@ -661,7 +689,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       for (int s = 0; s < 8 * NG; ++s) gs[s] = us[s] = 0.f;
       // the LDS rows first (a row's 2 KC reads issued together)
       if (NL > 0) {   // workgroup-uniform
-        const unsigned char* eb = (const unsigned char*)ebuf;
+        const unsigned char* eb = (const unsigned char*)ebuf + EOFF;
 #pragma unroll
         for (int k = 0; k < MLW; ++k) {
           const int i = wave + DEC_WAVES * k, ii = min(i, NL - 1);
@@ -727,7 +755,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       DEC_PART_IDS();
       const int RB = (hid + NWG - 1) / NWG;
       const int K8 = a.inter >> 3;
-      uint16_t* hs = (uint16_t*)smem;
+      uint16_t* hs = (uint16_t*)ebuf;   // (this layer's gate / up and o_proj rows are consumed)
       __syncthreads();
       // the weights are issued only now: a CU's memory requests complete in order, so loads issued
       // before the h stores would hold those stores back, and with them every workgroup's F
@@ -884,8 +912,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     decode_body<KC, IC, EM>(a); \
   }
 
-DECODE_KERNEL(3, 3, 3)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 splits: 20 streamed rows)
-DECODE_KERNEL(3, 3, 4)   // hidden 1536, up to 32 streamed gate/up rows per workgroup
+DECODE_KERNEL(3, 3, 2)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 splits: 15 streamed rows)
+DECODE_KERNEL(3, 3, 3)   // hidden 1536, up to 24 streamed gate/up rows per workgroup
+DECODE_KERNEL(3, 3, 4)   // hidden 1536, up to 32
 DECODE_KERNEL(3, 3, 6)   // hidden 1536, up to 48
 DECODE_KERNEL(1, 1, 1)   // hidden 512, up to 8
 DECODE_KERNEL(1, 1, 2)   // hidden 512, up to 16

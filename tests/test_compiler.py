@@ -282,7 +282,7 @@ def test_decode_step_becomes_one_persistent_launch():
     cfg = QwenConfig(layers=3)
     ir = build_decode_ir(2048, cfg, argmax=True)
     p = compile_subgraph(ir)
-    assert [s.kernel for s in p.steps] == ["k_decode_step_k3_i3_e3"]
+    assert [s.kernel for s in p.steps] == ["k_decode_step_k3_i3_e2"]
     st = p.steps[0]
     assert st.grid == (256, 1, 1) and st.block == (512, 1, 1)
     entries = st.params["table"]["entries"]

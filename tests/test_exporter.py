@@ -366,7 +366,7 @@ def test_full_size_qwen2_5_export_lowers_to_the_bench_launch_list():
     assert [(s.kernel, s.grid, s.lds) for s in a.steps] == [(s.kernel, s.grid, s.lds) for s in b.steps]
     # and both become the same single persistent launch by default
     pa, pb = compile_subgraph(ea), compile_subgraph(build_decode_ir(2048, argmax=True))
-    assert [s.kernel for s in pa.steps] == [s.kernel for s in pb.steps] == ["k_decode_step_k3_i3_e3"]
+    assert [s.kernel for s in pa.steps] == [s.kernel for s in pb.steps] == ["k_decode_step_k3_i3_e2"]
 
 
 def test_safetensors_loader_theta_default_is_hfs(tmp_path, model):
