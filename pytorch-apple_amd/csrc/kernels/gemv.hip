@@ -407,6 +407,236 @@ GEMV_KERNEL(k_gemv_attn_resid_r2, PRO_ATTN, EPI_RESID, 2, 1)
 GEMV_KERNEL(k_gemv_attn16_bias_r2, PRO_ATTN16, EPI_BIAS, 2, 1)
 GEMV_KERNEL(k_gemv_attn16_resid_r2, PRO_ATTN16, EPI_RESID, 2, 1)
 
+// ---------------------------------------------------------------- skinny MFMA GEMM (M <= 16 MT)
+//
+// out = epi(x . W^T) for a handful of activation rows: the weights are the HBM stream, read
+// once, and each weight element meets all M rows in one v_mfma_f32_16x16x32_bf16 (A: 16 weight
+// rows x 32 k, B: 32 k x 16 activation rows). Operand layout (gfx950 16x16x32): lane l holds 8
+// consecutive k, at offset 8 (l / 16) of the step, of A row l % 16 and of B column l % 16; D
+// element (4 (l / 16) + i, l % 16) is the lane's register i. Activation rows past M read row
+// M - 1 and are not stored.
+// Each wave streams its K steps through a ring of R stages in LDS: a stage is one 16-byte
+// global-to-LDS load per lane for A and per 16-row activation tile, landing at the lane's own
+// 16 bytes, so the lane reads its fragment back as it was loaded. The loads are issued from
+// inline assembly and waited for explicitly (the compiler neither counts nor serialises them),
+// R - 1 stages ahead of the step being multiplied.
+//   SILU (k_skinny_silu_*): one wave per workgroup and per tile of 8 gate rows over the same 8
+//   up rows, the whole of K; the up half of each output pair is swapped across the wave halves
+//   and the SiLU * up row leaves from registers.
+//   BIAS / RESID: 8 waves split K into 8 ranges over one tile of 16 output rows (or 8, RW == 8,
+//   rows 8..15 repeating 0..7: twice the workgroups for a short N at no extra HBM bytes); the
+//   wave tiles are added in LDS in wave order.
+// Epilogues at the GEMV kernels' rounding points.
+typedef __attribute__((ext_vector_type(8))) __bf16 sk_bf16x8;
+typedef __attribute__((ext_vector_type(4))) float sk_f32x4;
+typedef __attribute__((address_space(3))) uint4 sk_lds16;   // LDS reads as ds_read, not flat loads
+
+__device__ __forceinline__ void sk_dma16(const void* g, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void sk_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+__device__ __forceinline__ void sk_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Stages [s0, s0 + ns) of 64 k each, of one wave, into acc. A stage is NA KB of weight rows
+// (NA = 2: 16 rows; 1: 8 rows that stand for rows 8..15 too) and 2 KB per 16-row activation
+// tile, each KB one global-to-LDS load of 8 rows x 128 contiguous bytes: lane l carries
+// 16-byte chunk (l & 7) ^ (l >> 3) of row l >> 3, so chunk c of row r sits in slot
+// c ^ (r & 7) of the row's 8 and the fragment reads of 8 consecutive rows hit 8 bank groups.
+// The weights (HBM) run RA stages ahead in their ring, the activations RB <= RA in theirs.
+// Issue order, oldest first: A 0 .. RA - RB - 1, then (B p, A RA - RB + p) for p < RB, then at
+// step s (B s + RB, A s + RA); so when B s has landed, at most NA + (RB - 1) (NA + 2 MT) later
+// loads are outstanding, and A s (older) has landed too. With RB == RA each step issues
+// (A, B) and waits until at most (RA - 1) (NA + 2 MT) are outstanding.
+// wr[j] / xr[t][j]: this lane's row of load j (element 0 of the row).
+template <int MT, int NA, int RA, int RB>
+__device__ __forceinline__ void sk_stream(const uint16_t* const (&wr)[2], const uint16_t* const (&xr)[MT][2], int s0,
+                                          int ns, int rot, sk_lds16* ring, sk_f32x4 (&acc)[MT]) {
+  static_assert(RB >= 1 && RB <= RA, "ring depths");
+  constexpr int WAITN = RB == RA ? (RA - 1) * (NA + 2 * MT) : NA + (RB - 1) * (NA + 2 * MT);
+  const int lane = threadIdx.x & 63, q = lane >> 4, r16 = lane & 15;
+  const int cl = 8 * ((lane & 7) ^ (lane >> 3));   // this lane's source chunk (elements)
+  const unsigned abase = __builtin_amdgcn_readfirstlane((unsigned)(size_t)ring);
+  const unsigned bbase = abase + RA * NA * 1024u;   // B ring behind the A ring
+  // the wave's stages are visited from rot on (mod ns): workgroups that run side by side then
+  // read different column ranges of their rows, which spreads them over the memory channels
+  auto col = [&](int s) {
+    const int j = min(s, ns - 1) + rot;
+    return ((s0 + (j >= ns ? j - ns : j)) << 6) + cl;
+  };
+  auto issue_a = [&](int s, int slot) {   // stage s (clamped to the last) into A slot
+    const int k = col(s);
+#pragma unroll
+    for (int j = 0; j < NA; ++j) sk_dma16(wr[j] + k, abase + (unsigned)(slot * NA + j) * 1024u);
+  };
+  auto issue_b = [&](int s, int slot) {
+    const int k = col(s);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) sk_dma16(xr[t][j] + k, bbase + (unsigned)(slot * 2 * MT + 2 * t + j) * 1024u);
+  };
+  // fragment slots (16-byte units) of MFMA step u: A row ra, B row r16, chunk 4 u + q
+  const int ra = NA == 1 ? (r16 & 7) : r16;
+  int fa[2], fb[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    fa[u] = (ra >> 3) * 64 + (ra & 7) * 8 + ((4 * u + q) ^ (ra & 7));
+    fb[u] = RA * NA * 64 + (r16 >> 3) * 64 + (r16 & 7) * 8 + ((4 * u + q) ^ (r16 & 7));
+  }
+#pragma unroll
+  for (int p = 0; p < RA - RB; ++p) issue_a(p, p);
+#pragma unroll
+  for (int p = 0; p < RB; ++p) {
+    if (RB == RA) issue_a(p, p);
+    issue_b(p, p);
+    if (RB != RA) issue_a(RA - RB + p, RA - RB + p);
+  }
+  // A slots cycle with period RA, B slots with period RB: unroll over their common multiple
+  constexpr int U = RA % RB == 0 ? RA : RA * RB;
+  for (int j0 = 0; j0 < ns; j0 += U) {
+#pragma unroll
+    for (int p = 0; p < U; ++p) {
+      sk_vmcnt<WAITN>();   // stage j0 + p has landed
+      const int sa = p % RA, sb = p % RB;
+      // a stage past the wave's last (its slots re-read the last one) is multiplied as zeros
+      const unsigned ok = j0 + p < ns ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint4 av = ring[sa * NA * 64 + fa[u]];
+        av = make_uint4(av.x & ok, av.y & ok, av.z & ok, av.w & ok);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const uint4 bv = ring[sb * 2 * MT * 64 + fb[u] + 128 * t];
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sk_bf16x8, av),
+                                                           __builtin_bit_cast(sk_bf16x8, bv), acc[t], 0, 0, 0);
+        }
+      }
+      sk_lgkm0();   // these slots' reads are done before they are refilled
+      if (RB == RA) issue_a(j0 + p + RA, sa);
+      issue_b(j0 + p + RB, sb);
+      if (RB != RA) issue_a(j0 + p + RA, sa);
+    }
+  }
+  sk_vmcnt<0>();
+}
+
+template <int MT, int RA, int RB>
+__device__ __forceinline__ void skinny_silu_body(const GemvArgs& a) {
+  __shared__ uint4 ring[(RA * 2 + RB * 2 * MT) * 64];
+  const int lane = threadIdx.x & 63, q = lane >> 4, r16 = lane & 15, lr = lane >> 3;
+  const int K = a.K, n0 = blockIdx.x * 8;
+  // loads: j = 0 the 8 gate rows, j = 1 the 8 up rows; lane l carries row l >> 3 of each
+  const long long wrow = (long long)min(n0 + lr, a.N - 1) * K;
+  const uint16_t* wr[2] = {(const uint16_t*)a.w + wrow, (const uint16_t*)a.w2 + wrow};
+  const uint16_t* xr[MT][2];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xr[t][j] = (const uint16_t*)a.x + min((long long)(t * 16 + 8 * j + lr), a.M - 1) * a.ldx;
+  sk_f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = sk_f32x4{0.f, 0.f, 0.f, 0.f};
+  sk_stream<MT, 2, RA, RB>(wr, xr, 0, K >> 6, (int)(blockIdx.x % (unsigned)(K >> 6)), (sk_lds16*)ring, acc);
+  // lanes 0..31 hold gate rows 4 q + i, lanes 32..63 the up rows 8 + 4 (q - 2) + i of the same
+  // columns: lane l takes lane l + 32's
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    float g[4], u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g[i] = acc[t][i];
+      u[i] = __shfl_xor(acc[t][i], 32, 64);
+    }
+    const int m = t * 16 + r16;
+    if (lane < 32 && m < a.M) {
+      uint16_t h[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = min(n0 + 4 * q + i, a.N - 1);
+        float v = g[i], uu = u[i];
+        if (a.flags & 1) v += bf(a.bias, n);
+        if (a.flags & 4) uu += bf(a.bias2, n);
+        v = rbf(v);
+        uu = rbf(uu);
+        h[i] = f32_to_bf16(rbf(v / (1.f + expf(-v))) * uu);
+      }
+      uint16_t* o = (uint16_t*)a.out + (long long)m * a.ldo + n0 + 4 * q;
+      if (n0 + 4 * q + 3 < a.N && (((a.ldo | n0) & 3) == 0)) {
+        *(uint2*)o = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n0 + 4 * q + i < a.N) o[i] = h[i];
+      }
+    }
+  }
+}
+
+// BIAS / RESID: 8 waves split K into 8 ranges of one output tile; their fp32 tiles are added in
+// LDS in wave order.
+template <int EPI, int MT, int RW, int RA, int RB>
+__device__ __forceinline__ void skinny_body(const GemvArgs& a) {
+  constexpr int NA = RW == 8 ? 1 : 2;
+  constexpr int RING = (RA * NA + RB * 2 * MT) * 64;   // uint4 per wave
+  __shared__ uint4 ring[8 * RING];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15, lr = lane >> 3;
+  const int K = a.K, stages = K >> 6;
+  const int per = (stages + 7) >> 3, s0 = wave * per, ns = max(min(per, stages - s0), 0);
+  const uint16_t* wr[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) wr[j] = (const uint16_t*)a.w + (long long)min(blockIdx.x * RW + 8 * j + lr, a.N - 1) * K;
+  const uint16_t* xr[MT][2];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xr[t][j] = (const uint16_t*)a.x + min((long long)(t * 16 + 8 * j + lr), a.M - 1) * a.ldx;
+  sk_f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = sk_f32x4{0.f, 0.f, 0.f, 0.f};
+  if (ns > 0)   // wave-uniform
+    sk_stream<MT, NA, RA, RB>(wr, xr, s0, ns, (int)(blockIdx.x % (unsigned)ns), (sk_lds16*)ring + wave * RING, acc);
+  __syncthreads();   // every wave is done with its ring: its tiles go there
+  float* red = (float*)ring;   // [8][MT][256]
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * MT + t) * 256 + (4 * q + i) * 16 + r16] = acc[t][i];
+  __syncthreads();
+  constexpr int NO = RW == 8 ? 8 : 16;
+  for (int e = tid; e < MT * NO * 16; e += 512) {
+    const int t = e / (NO * 16), i = (e / 16) % NO, mc = e % 16, m = t * 16 + mc;
+    const int nn = blockIdx.x * RW + i;
+    if (m >= a.M || nn >= a.N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) v += red[(w * MT + t) * 256 + i * 16 + mc];
+    if (a.flags & 1) v += bf(a.bias, nn);
+    v = rbf(v);
+    if constexpr (EPI == EPI_RESID) v = bf(a.resid, (long long)m * a.ldr + nn) + v;
+    ((uint16_t*)a.out)[(long long)m * a.ldo + nn] = f32_to_bf16(v);
+  }
+}
+
+#define SKINNY_SILU(NAME, MT, RA, RB) \
+  extern "C" __global__ void __launch_bounds__(64) NAME(const GemvArgs a) { skinny_silu_body<MT, RA, RB>(a); }
+#define SKINNY_KERNEL(NAME, EPI, MT, RW, RA, RB) \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const GemvArgs a) { skinny_body<EPI, MT, RW, RA, RB>(a); }
+// ring depths (stages of weights, stages of activations) measured at M = 16 on MI355X: deeper
+// rings were slower (gate/up 12.6 us with 6 stages, 12.9 with 7, 14.5 with 8; down 8.5 us with
+// 4..6 and 10.2..13.8 with 12 weight stages ahead of 3 activation stages)
+SKINNY_SILU(k_skinny_silu_mt1, 1, 6, 6)
+SKINNY_SILU(k_skinny_silu_mt2, 2, 4, 4)
+SKINNY_KERNEL(k_skinny_bias_mt1, EPI_BIAS, 1, 16, 4, 4)
+SKINNY_KERNEL(k_skinny_bias_mt2, EPI_BIAS, 2, 16, 3, 3)
+SKINNY_KERNEL(k_skinny_resid_mt1, EPI_RESID, 1, 16, 4, 4)
+SKINNY_KERNEL(k_skinny_resid_mt2, EPI_RESID, 2, 16, 3, 3)
+SKINNY_KERNEL(k_skinny_bias_mt1_r8, EPI_BIAS, 1, 8, 5, 5)
+SKINNY_KERNEL(k_skinny_bias_mt2_r8, EPI_BIAS, 2, 8, 3, 3)
+SKINNY_KERNEL(k_skinny_resid_mt1_r8, EPI_RESID, 1, 8, 5, 5)
+SKINNY_KERNEL(k_skinny_resid_mt2_r8, EPI_RESID, 2, 8, 3, 3)
+
 // One workgroup per activation row: the largest of the row's per-workgroup keys is the
 // maximum logit with the smallest index among equal maxima (np.argmax's rule).
 extern "C" __global__ void __launch_bounds__(256) k_argmax_finalize(const ArgmaxFinalizeArgs a) {

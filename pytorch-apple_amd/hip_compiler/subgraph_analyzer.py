@@ -40,6 +40,9 @@ HS_BF16, HS_F16 = DTYPE_CODE["bfloat16"], DTYPE_CODE["float16"]
 # linears with at least this many activation rows use the MFMA GEMM (weights read once per
 # column tile) instead of the streaming GEMV (weights re-read per block of 4 rows)
 GEMM_MIN_M = 16
+# up to this many activation rows, bf16 linears take the skinny MFMA kernels (gemv.hip
+# k_skinny_*: every weight element read once and multiplied with all rows in one 16x16x32 MFMA)
+SKINNY_MAX_M = 32
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
@@ -592,7 +595,8 @@ class Lowering:
                   epi: str, nodes: list[str], resid: str | None = None, w2: str | None = None,
                   b2: str | None = None) -> None:
         """MFMA GEMM (csrc/kernels/gemm.hip) for M >= GEMM_MIN_M: out = epi(x . W^T); a pending
-        RMSNorm of ``x`` is materialised first (it is cheap next to the GEMM)."""
+        RMSNorm of ``x`` is materialised first (it is cheap next to the GEMM). Up to SKINNY_MAX_M
+        bf16 rows take the skinny kernels instead."""
         w = self.aligned16(self.contiguous(w_name), w_name)
         N, K = w.shape
         x = self.aligned16(self.contiguous(x_name), x_name)
@@ -602,6 +606,29 @@ class Lowering:
         r = self.contiguous(resid) if resid else None
         wv2 = self.aligned16(self.contiguous(w2), w2) if w2 else None
         bv2 = self.contiguous(b2) if b2 else None
+        if M <= SKINNY_MAX_M and dtype == "bfloat16" and K % 64 == 0 and K >= 512 and epi in ("bias", "resid", "silu"):
+            # SiLU: one wave per tile of 8 gate + 8 up rows. Bias / residual: 8 waves per tile of
+            # 16 output rows (8 when that gives fewer than 256 tiles), splitting K.
+            mt = 1 if M <= 16 else 2
+            if epi == "silu":
+                per, kname, block = 8, f"k_skinny_silu_mt{mt}", 64
+            else:
+                per = 8 if -(-N // 16) < GEMM_TARGET_WGS else 16
+                kname, block = f"k_skinny_{epi}_mt{mt}" + ("_r8" if per == 8 else ""), 512
+            args = dict(x=self.ref(x), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
+                        resid=self.ref(r) if r else None, w2=self.ref(wv2) if wv2 else None,
+                        bias2=self.ref(bv2) if bv2 else None, norm_w=None, argmax_slot=None, attn_o=None,
+                        attn_ml=None, M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=0.0, n_dtype=0,
+                        flags=(1 if bias else 0) | (4 if bv2 else 0), attn_heads=0, attn_kvh=0, attn_splits=0)
+            self.emit(LaunchStep(
+                kind="gemm", kernel=kname, module="gemv", arg_struct="GemvArgs", args=args,
+                grid=(-(-N // per), 1, 1), block=(block, 1, 1),
+                inputs=[x_name, w_name] + [t for t in (b_name, resid, w2, b2) if t], outputs=[out_name],
+                params={"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None,
+                        "weights": 2 if epi == "silu" else 1, "transpose_b": True, "nodes": nodes, "mfma": True,
+                        "skinny": True}))
+            self.views[out_name] = o
+            return
         nw = 2 if epi == "silu" else 1
         bm, bn, ksplit, dma = gemm_tiling(M, N, K, nw)
         bk = 64 if K % 64 == 0 else 32

@@ -242,3 +242,50 @@ def test_views_materialised_bit_exact(backend, view):
     got, ref, _ = _run(ir, xin, backend)
     (name,) = got
     assert np.array_equal(np.ascontiguousarray(got[name]), np.ascontiguousarray(ref[name]))
+
+
+@pytest.mark.parametrize("case", ["bias_r8", "resid_r8", "bias_r16", "silu", "silu_bias", "resid_m24", "silu_m24"])
+def test_skinny_linear_vs_cpu_fallback(backend, case):
+    """The skinny MFMA kernels (16-32 activation rows, gemv.hip k_skinny_*): a linear with bias,
+    a linear + residual add, and SiLU(gate) * up over two weights, against the CPU fallback;
+    the output tile widths (8 / 16 rows, the short-N variant), one and two 16-row tiles, a
+    long K and an N that is not a multiple of the tile."""
+    from irgen.builder import IRBuilder
+    from irgen.qwen import linear
+
+    M, N, K, kind = {"bias_r8": (16, 1000, 768, "bias"), "resid_r8": (16, 1536, 8960, "resid"),
+                     "bias_r16": (16, 4104, 512, "bias"), "silu": (16, 2056, 1536, "silu"),
+                     "silu_bias": (16, 1032, 512, "silu_bias"), "resid_m24": (24, 1536, 2048, "resid"),
+                     "silu_m24": (24, 2048, 1536, "silu")}[case]
+    dt = "bfloat16"
+    b = IRBuilder(f"skinny_{case}")
+    x = b.input("x0", [M, K], dt)
+    w = b.input("x1", [N, K], dt)
+    shapes = [(M, K), (N, K)]
+    if kind == "bias":
+        bias = b.input("x2", [N], dt)
+        shapes.append((N,))
+        y = linear(b, x, w, bias)
+    elif kind == "resid":
+        r = b.input("x2", [M, N], dt)
+        shapes.append((M, N))
+        y = b.op("aten.add.Tensor", [r, linear(b, x, w)])
+    else:
+        w2 = b.input("x2", [N, K], dt)
+        shapes.append((N, K))
+        bias = bias2 = None
+        if kind == "silu_bias":
+            bias, bias2 = b.input("x3", [N], dt), b.input("x4", [N], dt)
+            shapes += [(N,), (N,)]
+        y = b.op("aten.mul.Tensor", [b.op("aten.silu.default", [linear(b, x, w, bias)]), linear(b, x, w2, bias2)])
+    b.output(y)
+    ir = b.to_dict()
+    xin = _inputs(shapes, dt, seed=21)
+    for k in ("x1", "x2", "x3", "x4"):   # weights of a trained scale: sums over K stay O(1)
+        if k in xin and xin[k].ndim == 2 and xin[k].shape[1] == K:
+            xin[k] = (torch.from_numpy(_f(xin[k]) / np.sqrt(K)).to(torch.bfloat16).view(torch.int16).numpy()
+                      .view(np.uint16))
+    got, ref, kernels = _run(ir, xin, backend)
+    assert any(k.startswith("k_skinny_") for k in kernels), kernels
+    (name,) = got
+    _close(got[name], ref[name])

@@ -67,7 +67,7 @@ def assert_all_npu(ex):
     assert all(s.target == "npu" for s in ex.plan.steps if isinstance(s, Partition))
 
 
-@pytest.mark.parametrize("tokens", [1, 16, 128])
+@pytest.mark.parametrize("tokens", [1, 16, 24, 128])
 def test_mlp_block_cfg1(backend, tokens):
     from irgen.qwen import build_mlp_ir
     from irgen.workloads import make_weights, mlp_inputs
