@@ -33,7 +33,8 @@ MAX_G = 8            # query heads per KV head
 MAX_SPLITS = 32
 VARIANTS = {1, 2, 3}     # hidden / 512 with a kernel instance (inter <= 4096 * that)
 E_LDS_ROWS = {1: 48, 2: 32, 3: 24}   # gate/up rows an attention workgroup holds in LDS (decode.hip DEC_NE)
-RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}   # instances: gate/up rows per wave streamed through registers
+RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}
+O_RING_MAX = 11     # gate/up rows an o_proj workgroup streams, at most (decode.hip DEC_RBO)   # instances: gate/up rows per wave streamed through registers
 
 TABLE_FIELDS = ("norm1", "wq", "bq", "wk", "bk", "wv", "bv", "kc", "vc", "wo", "norm2", "wg", "wu", "wd")
 
@@ -92,14 +93,17 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     nsplit = S // SPL
     # the work split of decode.hip: NB attention workgroups (each also holds NE gate/up rows in
     # LDS), ND o_proj workgroups of RD rows (those that run no combine also hold NEO gate/up rows
-    # in LDS); every workgroup streams at most RBD gate/up rows
+    # in LDS); an o_proj workgroup streams RBO gate/up rows, an attention workgroup RBA
     NB, NE = H * nsplit, E_LDS_ROWS[KC]
     ND = NWG - NB
     RD = -(-hidden // ND)
     NEO = max(2 * NE - RD, 0) // 2
-    RBD = max(inter - NB * NE - (ND - H) * NEO + NWG - 1, 0) // NWG
-    em = [e for e in RING_ROWS[KC] if 8 * e >= RBD]
-    if RD > 2 * NE or not em or NE + RBD > 128:   # decode.hip DEC_OSTAGE: a workgroup's rows, staged
+    ring = max(inter - NB * NE - (ND - H) * NEO, 0)
+    RBO = min(-(-ring // NWG), O_RING_MAX)
+    RBA = -(-max(ring - ND * RBO, 0) // NB)
+    RB = max(RBA, RBO)
+    em = [e for e in RING_ROWS[KC] if 8 * e >= RB]
+    if RD > 2 * NE or not em or NE + RB > 128:   # decode.hip DEC_OSTAGE: a workgroup's rows, staged
         return None
     if nsplit * (D + 4) * 2 > 8192 * KC:   # the combine stages a head's partials in LDS
         return None
