@@ -389,6 +389,14 @@ struct PersistArgs {
   int ids_dtype, pos_dtype, cpos_dtype, mask_dtype, add_dtype, n_dtype, out_dtype;
   int flags;                  // 1: q/k/v biases present
   float eps, eps_f, scale, rope_scaling;
+  // optional in-kernel decode advance (adv_flag null: none). After the step, the next step's
+  // inputs: p = adv_cpos + 1; adv_cpos = adv_pos = p; adv_mask[p] = 0 when p < S. A step that
+  // starts with cache_position outside [0, S) sets adv_flag[0] (it re-runs no position silently).
+  void* adv_mask;             // [S] additive mask row, element size adv_mask_bytes (2 or 4)
+  long long* adv_pos;         // position_ids [1, 1]
+  long long* adv_cpos;        // cache_position [1]
+  int* adv_flag;              // [0]: a step ran past the cache end
+  int adv_mask_bytes, adv_pad;
 };
 
 struct ArgmaxFinalizeArgs {   // out[m] = index of max over the `parts` keys of row m

@@ -47,6 +47,9 @@
 #ifndef DEC_ED
 #define DEC_ED 3                      // gate/up rows in flight per wave (2: 0.780 ms, 3: 0.766 ms per step)
 #endif
+#ifndef DEC_RFE
+#define DEC_RFE 2                     // down_proj rows per workgroup issued before the gate / up arithmetic
+#endif
 #ifndef DEC_R4
 #define DEC_R4 2                      // lm_head rows per wave in each of its two rounds in flight
 #endif
@@ -292,7 +295,7 @@ __device__ __forceinline__ DecodeLayerPtrs dec_layer(const void* const* t) {
 // rows per workgroup, at most (2 KC: hidden rows over 256 workgroups); EM: gate/up rows per wave
 // streamed through registers, at most; ED: those rows in flight per wave; NE: gate/up rows an
 // attention workgroup loads into LDS once its attention part is done.
-template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC)>
+template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC), int RFE = DEC_RFE>
 __device__ __forceinline__ void decode_body(const PersistArgs& a) {
   __shared__ __attribute__((aligned(16))) unsigned char smem[DEC_SMEM];   // per-part staging (B, C; xs)
   __shared__ __attribute__((aligned(16))) uint16_t xres[512 * KC];
@@ -325,6 +328,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
   const long long S = a.S, last = S - 1, kvs = a.kv_head_stride;
   uint16_t* xs = (uint16_t*)smem;
   DEC_STAMP(a.L, 7);
+  // a decode loop advanced in the kernel has moved past the cache end: this step is reported
+  if (a.adv_flag != nullptr && b == 0 && tid == 0 && (cpos < 0 || cpos >= S)) a.adv_flag[0] = 1;
   // rotary factors of this step's position (the same for every layer): cos and sin of
   // inv_freq[i] * position in fp32, times the scaling, rounded to bf16
   if (tid < 64) {
@@ -667,6 +672,20 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     // re-reads its last one), so no loaded value flows through a branch join, which would make the
     // compiler wait for every load in flight. Results are published after the last row: a store
     // between the loads would sit in the same in-order completion count.
+    // down_proj rows of F (rows b * RB + j): the first RFE are issued as soon as x1 is in, when
+    // every load this workgroup issued before has landed, so they arrive during the gate / up
+    // arithmetic; the rest follow the h stores
+    uint4 fw[RF][IC];
+    auto load_down = [&](int j) {
+      const int RB = (hid + NWG - 1) / NWG, K8 = a.inter >> 3, wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+      const long long rmaxf = min(b * RB + RB, hid) - 1;
+      const long long r = min((long long)(b * RB + j), rmaxf);
+#pragma unroll
+      for (int k = 0; k < IC; ++k) {
+        const int c = min(512 * k + 64 * wv + ln, K8 - 1);   // chunks past the row re-read its last one
+        fw[j][k] = ldw(P.wd + r * a.inter + 8 * c);
+      }
+    };
     {
       DEC_PART_IDS();
       constexpr int EP = ED < EM ? ED : EM;
@@ -684,6 +703,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       DEC_STAMP(l, 10);
       xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, tid);
       DEC_STAMP(l, 11);
+#pragma unroll
+      for (int j = 0; j < RFE; ++j) load_down(j);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
       uint4 xv[KC];
 #pragma unroll
@@ -766,20 +787,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       __syncthreads();
       // the weights are issued only now: a CU's memory requests complete in order, so loads issued
       // before the h stores would hold those stores back, and with them every workgroup's F
-      uint4 fw[RF][IC];
-      {
-        const int K8 = a.inter >> 3;
-        const long long rmaxf = min(b * RB + RB, hid) - 1;
 #pragma unroll
-        for (int j = 0; j < RF; ++j) {
-          const long long r = min((long long)(b * RB + j), rmaxf);
-#pragma unroll
-          for (int k = 0; k < IC; ++k) {
-            const int c = min(512 * k + 64 * wave + lane, K8 - 1);   // chunks past the row re-read its last one
-            fw[j][k] = ldw(P.wd + r * a.inter + 8 * c);
-          }
-        }
-      }
+      for (int j = RFE; j < RF; ++j) load_down(j);
       DEC_STAMP(l, 13);
       xgather<(IC * 4096 / 2 + 255) / 256, 256>(XL + X.h, a.inter, tag, hs, err, tid);
       DEC_STAMP(l, 14);
@@ -909,6 +918,17 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       if (a.out_dtype == HS_I64) *(long long*)a.next_token = idx;
       else *(int*)a.next_token = (int)idx;
       __hip_atomic_store(ctl, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the next step's position inputs (every workgroup read its inputs before its argmax key,
+      // and every key is in): one more position, its mask entry opened
+      if (a.adv_flag != nullptr) {
+        const long long p = a.adv_cpos[0] + 1;
+        a.adv_cpos[0] = p;
+        a.adv_pos[0] = p;
+        if (p >= 0 && p < S) {
+          if (a.adv_mask_bytes == 4) ((float*)a.adv_mask)[p] = 0.f;
+          else ((uint16_t*)a.adv_mask)[p] = 0;
+        }
+      }
     }
     DEC_STAMP(a.L, 3);
   }

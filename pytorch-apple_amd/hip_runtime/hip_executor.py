@@ -97,9 +97,17 @@ class HIPExecutor:
             r.kernarg = C.addressof(s)
         self._n = n
         self._ext_key: tuple | None = None        # external pointers packed into the kernargs now
-        self._last_bufs: tuple | None = None      # external buffer objects of the previous launch
-        self._last_key: tuple | None = None
-        self._graphs: OrderedDict[tuple, int] = OrderedDict()   # pointer set -> captured graph
+        # external storages bound to weights (checked once per weights dict) and to graph inputs
+        # (checked once per set of buffer objects)
+        self._w_names = [n for n in self._ext_names if storages[n].kind == "weight"]
+        self._in_names = [n for n in self._ext_names if storages[n].kind != "weight"]
+        self._w_names_set = frozenset(self._w_names)
+        self._w_src, self._w_len, self._w_key = None, -1, ()
+        self._last_bufs: tuple | None = None      # input buffer objects of the previous launch
+        self._last_in_key: tuple = ()
+        self._in_cache: OrderedDict[tuple, tuple] = OrderedDict()
+        self._graphs: OrderedDict[tuple, int] = OrderedDict()   # (pointer set, advance) -> captured graph
+        self._adv_ptr = 0                         # flag word of a decode advance folded into the launch
         self._capture_stream = None
         self._out_cache: dict[str, HIPBuffer] = {}
         for spec in program.output_specs:
@@ -168,67 +176,81 @@ class HIPExecutor:
 
     # ------------------------------------------------------------------ execution
 
-    def _resolve(self, inputs: dict, weights: dict) -> dict[str, int]:
-        ptrs: dict[str, int] = {}
-        wmap = self.program.weight_name_mapping
-        for name in self._ext_names:
-            buf = inputs.get(name)
-            if buf is None:
-                buf = weights.get(name)
-            if buf is None and name in wmap:
-                buf = weights.get(wmap[name])
-            if buf is None:
-                raise KeyError(f"HIPExecutor: no buffer for '{name}' (graph input or weight)")
-            t = buf.native_handle if isinstance(buf, HIPBuffer) else buf
-            if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
-                raise TypeError(f"HIPExecutor: '{name}' must be a device buffer, got {type(buf).__name__}")
-            spec_st = self.program.storages[name]
-            if t.numel() * t.element_size() < spec_st.nbytes:
-                raise ValueError(f"HIPExecutor: '{name}' holds {t.numel() * t.element_size()} bytes, "
-                                 f"program needs {spec_st.nbytes}")
-            ptrs[name] = t.data_ptr()
-        return ptrs
+    def _check(self, name: str, buf) -> int:
+        """The device pointer of ``buf`` after checking that it can back storage ``name``."""
+        if buf is None:
+            raise KeyError(f"HIPExecutor: no buffer for '{name}' (graph input or weight)")
+        t = buf.native_handle if isinstance(buf, HIPBuffer) else buf
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise TypeError(f"HIPExecutor: '{name}' must be a device buffer, got {type(buf).__name__}")
+        spec_st = self.program.storages[name]
+        if t.numel() * t.element_size() < spec_st.nbytes:
+            raise ValueError(f"HIPExecutor: '{name}' holds {t.numel() * t.element_size()} bytes, "
+                             f"program needs {spec_st.nbytes}")
+        return t.data_ptr()
 
-    def _buffers(self, inputs: dict, weights: dict) -> tuple:
-        wmap = self.program.weight_name_mapping
-        out = []
-        for name in self._ext_names:
-            buf = inputs.get(name)
-            if buf is None:
-                buf = weights.get(name)
-            if buf is None and name in wmap:
-                buf = weights.get(wmap[name])
-            out.append(buf)
-        return tuple(out)
+    def _lookup(self, name: str, inputs: dict, weights: dict):
+        buf = inputs.get(name)
+        if buf is None:
+            buf = weights.get(name)
+        if buf is None and name in self.program.weight_name_mapping:
+            buf = weights.get(self.program.weight_name_mapping[name])
+        return buf
+
+    def _pointer_key(self, inputs: dict, weights: dict) -> tuple:
+        """The external pointer set of this call, as (weight pointers, input pointers).
+
+        Weights are checked once per weights dict (the DAGExecutor hands the same dict to every
+        call; a new one, or one whose size changed, is checked again). Inputs are checked once per
+        set of buffer objects (a ``HIPBuffer`` never rebinds its tensor, so the same objects mean
+        the same pointers); the last few sets are remembered, so a loop that alternates between two
+        sets (the prompt's token buffer, then the previous step's argmax) checks each once."""
+        if weights is not self._w_src or len(weights) != self._w_len or self._w_names_set & inputs.keys():
+            self._w_src, self._w_len = None, -1
+            wk = tuple(self._check(n, self._lookup(n, inputs, weights)) for n in self._w_names)
+            if not (self._w_names_set & inputs.keys()):   # an input shadowing a weight is not cached
+                self._w_src, self._w_len, self._w_key = weights, len(weights), wk
+        else:
+            wk = self._w_key
+        bufs = tuple(self._lookup(n, inputs, weights) for n in self._in_names)
+        last = self._last_bufs
+        if last is not None and all(b is c for b, c in zip(bufs, last)):
+            return (wk, self._last_in_key)
+        ids = tuple(map(id, bufs))
+        hit = self._in_cache.get(ids)
+        if hit is not None and all(b is c for b, c in zip(bufs, hit[0])):
+            self._in_cache.move_to_end(ids)
+            ik = hit[1]
+        else:
+            ik = tuple(self._check(n, b) for n, b in zip(self._in_names, bufs))
+            if all(isinstance(b, HIPBuffer) for b in bufs):
+                self._in_cache[ids] = (bufs, ik)
+                while len(self._in_cache) > MAX_GRAPHS:
+                    self._in_cache.popitem(last=False)
+        if all(isinstance(b, HIPBuffer) for b in bufs):
+            self._last_bufs, self._last_in_key = bufs, ik
+        else:
+            self._last_bufs = None
+        return (wk, ik)
+
+    def _ptrs_of(self, key: tuple) -> dict[str, int]:
+        return dict(zip(self._w_names, key[0])) | dict(zip(self._in_names, key[1]))
 
     def launch(self, inputs: dict, weights: dict, stream: int | None = None) -> None:
-        """Enqueue the whole program on ``stream`` (default: torch's current stream).
-
-        The external buffers are checked and their pointers taken only when they are not the
-        very objects of the previous call: a ``HIPBuffer`` never rebinds its tensor, so the
-        same objects mean the same pointers (the loop of a decode step passes the same ones)."""
-        bufs = self._buffers(inputs, weights)
-        last = self._last_bufs
-        if last is not None and len(bufs) == len(last) and all(b is c for b, c in zip(bufs, last)):
-            key = self._last_key
-        else:
-            ptrs = self._resolve(inputs, weights)
-            key = tuple(ptrs[n] for n in self._ext_names)
-            if all(isinstance(b, HIPBuffer) for b in bufs):
-                self._last_bufs, self._last_key = bufs, key
-            else:
-                self._last_bufs = None
+        """Enqueue the whole program on ``stream`` (default: torch's current stream)."""
+        key = self._pointer_key(inputs, weights)
         if stream is None:
             stream = _current_stream(self.device)
         if self._n == 0:
             return
         lib = _shim.lib()
-        graph = self._graphs.get(key) if self.use_graph else None
+        gkey = (key, self._adv_ptr)
+        graph = self._graphs.get(gkey) if self.use_graph else None
         if graph is not None:
-            self._graphs.move_to_end(key)
+            self._graphs.move_to_end(gkey)
         else:
             if key != self._ext_key:
-                self._patch(ptrs, key)
+                self._patch(self._ptrs_of(key), key)
                 self._ext_key = key
             if not self.use_graph:
                 _shim.check(lib.hs_replay(self._recs, self._n, stream), "replay")
@@ -239,13 +261,36 @@ class HIPExecutor:
                 self._capture_stream = cs.value
             g = C.c_void_p()
             _shim.check(lib.hs_graph_capture(self._recs, self._n, self._capture_stream, C.byref(g)), "graph capture")
-            graph = self._graphs[key] = g.value
+            graph = self._graphs[gkey] = g.value
             while len(self._graphs) > MAX_GRAPHS:
-                old_key, old = self._graphs.popitem(last=False)
+                (old_key, _), old = self._graphs.popitem(last=False)
                 _shim.check(lib.hs_graph_destroy(old), "graph destroy")
-                if old_key != self._ext_key:
+                if old_key != self._ext_key and all(k[0] != old_key for k in self._graphs):
                     self._table_bufs.pop(old_key, None)
         _shim.check(lib.hs_graph_launch(graph, stream), "graph launch")
+
+    def fold_advance(self, advance: "DecodeAdvance | None") -> bool:
+        """Fold ``advance`` into this program's launch: a persistent decode step then moves its
+        loop's position inputs to the next step itself, after its argmax (no second launch, and
+        also after a loop's last step). The step launched after the inputs have moved past the
+        cache end sets ``advance``'s flag (``advance.check()`` raises) instead of re-running the
+        last position. Returns False and changes nothing when the program is not a single
+        persistent decode step (call ``advance()`` after each step then). ``None`` unfolds."""
+        if len(self.program.steps) != 1 or self.program.steps[0].kind != "decode_step":
+            return False
+        s = self._structs[0]
+        if advance is None:
+            s.adv_mask = s.adv_pos = s.adv_cpos = s.adv_flag = None
+            s.adv_mask_bytes = 0
+            self._adv_ptr = 0
+        else:
+            a = advance._args
+            s.adv_mask, s.adv_pos, s.adv_cpos, s.adv_flag = a.mask, a.pos, a.cpos, a.overflow
+            s.adv_mask_bytes = a.mask_bytes
+            if int(a.S) != int(self.program.steps[0].args["S"]):
+                raise ValueError("the advance's mask length differs from the step's cache length")
+            self._adv_ptr = int(a.overflow)
+        return True
 
     def check(self) -> None:
         """Raise ``RuntimeError`` if a persistent decode step has recorded a timeout (one of its

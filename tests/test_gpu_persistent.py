@@ -162,3 +162,59 @@ def test_persistent_greedy_loop_follows_launch_list_and_wraps_step_tags(backend)
     for s in range(n):
         _close(runs[True]["logits"][s], runs[False]["logits"][s])
     assert runs[True]["toks"] == runs[False]["toks"]
+
+
+def test_folded_advance_matches_separate_launches_and_reports_the_cache_end(backend):
+    """``HIPExecutor.fold_advance``: the persistent step moves its own position inputs after each
+    step. A greedy loop run that way gives the same tokens and bit-identical logits as the same
+    loop with a ``k_decode_advance`` launch after each step; after the step at the last cache
+    position the inputs stand at S (mask untouched past the cache), ``check()`` stays quiet, and
+    the step launched there sets the flag."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(hidden=512, intermediate=1024, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=4096)
+    S, start = 256, 244
+    n = S - start
+    ir = build_decode_ir(S, cfg, argmax=True)
+    w = make_weights(ir, cfg, device="cuda")
+    kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
+    kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
+    lg = ir["graph_outputs"][0]["name"]
+    ex = _executor(ir, backend, True)
+    ex.load_weights(w)
+    h = _hexec(ex)
+    runs = {}
+    for fold in (False, True):
+        state = {k: backend.allocate_buffer(v) for k, v in decode_inputs(S, start, cfg, device="cuda").items()}
+        adv = backend.decode_advance(state["attention_mask"], state["position_ids"], state["cache_position"])
+        assert h.fold_advance(adv if fold else None)
+        toks, logits = [], []
+        for s in range(n):
+            print(f"[case] folded advance={fold} step {s}", flush=True)
+            out = ex.execute(state)
+            toks.append(int(out["next_token"].native_handle.reshape(-1)[0].item()))
+            logits.append(out[lg].native_handle.view(torch.int16).cpu().numpy().reshape(-1).copy())
+            state["input_ids"] = out["next_token"]
+            for i, o in zip(kv_in, kv_out):
+                state[i] = out[o]
+            if not fold and s < n - 1:
+                adv()
+        torch.cuda.synchronize()
+        adv.check()
+        h.check()
+        mask = state["attention_mask"].native_handle.float().cpu().numpy().reshape(-1)
+        assert np.all(mask[:S] == 0.0)                     # every position of the cache opened
+        runs[fold] = (toks, logits)
+        if fold:
+            assert int(state["cache_position"].native_handle.item()) == S
+            assert int(state["position_ids"].native_handle.item()) == S
+            print("[case] folded advance: one step past the cache end", flush=True)
+            ex.execute(state)
+            torch.cuda.synchronize()
+            with pytest.raises(RuntimeError):
+                adv.check()
+            h.fold_advance(None)
+    assert runs[True][0] == runs[False][0]
+    for a, b in zip(runs[True][1], runs[False][1]):
+        assert np.array_equal(a, b)
