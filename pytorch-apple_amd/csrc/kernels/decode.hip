@@ -48,14 +48,19 @@
 #define DEC_ED 3                      // gate/up rows in flight per wave (2: 0.780 ms, 3: 0.766 ms per step)
 #endif
 #ifndef DEC_RFE
-#define DEC_RFE 2                     // down_proj rows per workgroup issued before the gate / up arithmetic
+#define DEC_RFE 0                     // down_proj rows per workgroup issued before the gate / up arithmetic (1-4: no faster)
 #endif
 #ifndef DEC_R4
 #define DEC_R4 2                      // lm_head rows per wave in each of its two rounds in flight
 #endif
 // gate/up rows an o_proj workgroup streams, at most (Qwen2.5-1.5B: 11 and 16 per attention
 // workgroup, 0.724 ms per step; the even split, 15 and 15: 0.733; 12: 0.725; 13-14: 0.734)
+#ifndef DEC_RBO
 #define DEC_RBO 11
+#endif
+#ifndef DEC_EARLY
+#define DEC_EARLY 1   // o_proj workgroups issue E's first ring rows with their o_proj rows (0: 0.730 ms, 1: 0.717)
+#endif
 #define DEC_NE(KC) ((KC) == 3 ? 24 : ((KC) == 2 ? 32 : 48))   // gate/up rows in LDS per attention workgroup
 #define DEC_SMEM (32 * (DEC_D + 4) * 2)   // per-part staging: the combine's partials of up to 32 splits
 
@@ -290,28 +295,42 @@ __device__ __forceinline__ DecodeLayerPtrs dec_layer(const void* const* t) {
 
 // ---------------------------------------------------------------- the step
 
+// The step's LDS, declared once per kernel (both role instances of decode_body use it).
+template <int KC, int NE>
+struct DecShared {
+  __attribute__((aligned(16))) unsigned char smem[DEC_SMEM];   // per-part staging (B, C; xs)
+  __attribute__((aligned(16))) uint16_t xres[512 * KC];
+  float red[DEC_WAVES * 8];
+  float red2[DEC_WAVES * DEC_MAXG];
+  float rope_cs[128];
+  // an attention workgroup's first NE gate / up rows (row i: gate chunks, then up chunks, 1 KB
+  // each); in the other workgroups, their o_proj rows (at most 2 NE), then (except the combine
+  // workgroups) their first NEO gate / up rows. F stages the SiLU * up row here.
+  __attribute__((aligned(16))) uint4 ebuf[NE * 2 * KC * 64];
+  const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
+  unsigned long long kred[DEC_WAVES];
+  // a part's results (o_proj rows, gate / up rows) staged here, then published with one store
+  // instruction per 64 words: many single-word stores spread over the waves are acknowledged far
+  // more slowly while the memory system is busy with the weight stream
+  uint16_t ostage[DEC_OSTAGE];
+};
+
 // KC: 512-element chunks of a hidden-long row per lane (hidden = 512 KC); IC: chunks per lane
 // of a down_proj row whose K (inter) is split over the 8 waves (inter <= 4096 IC); RF: down_proj
 // rows per workgroup, at most (2 KC: hidden rows over 256 workgroups); EM: gate/up rows per wave
 // streamed through registers, at most; ED: those rows in flight per wave; NE: gate/up rows an
 // attention workgroup loads into LDS once its attention part is done.
-template <int KC, int IC, int EM, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC), int RFE = DEC_RFE>
-__device__ __forceinline__ void decode_body(const PersistArgs& a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[DEC_SMEM];   // per-part staging (B, C; xs)
-  __shared__ __attribute__((aligned(16))) uint16_t xres[512 * KC];
-  __shared__ float red[DEC_WAVES * 8];
-  __shared__ float red2[DEC_WAVES * DEC_MAXG];
-  __shared__ float rope_cs[128];
-  // an attention workgroup's first NE gate / up rows (row i: gate chunks, then up chunks, 1 KB
-  // each); in the other workgroups, their o_proj rows (at most 2 NE), then (except the combine
-  // workgroups) their first NEO gate / up rows. F stages the SiLU * up row here.
-  __shared__ __attribute__((aligned(16))) uint4 ebuf[NE * 2 * KC * 64];
-  __shared__ const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
-  __shared__ unsigned long long kred[DEC_WAVES];
-  // a part's results (o_proj rows, gate / up rows) staged here, then published with one store
-  // instruction per 64 words: many single-word stores spread over the waves are acknowledged far
-  // more slowly while the memory system is busy with the weight stream
-  __shared__ uint16_t ostage[DEC_OSTAGE];
+template <int KC, int IC, int EM, int ROLE, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC), int RFE = DEC_RFE>
+__device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, NE>& sh) {
+  auto& smem = sh.smem;
+  auto& xres = sh.xres;
+  auto& red = sh.red;
+  auto& red2 = sh.red2;
+  auto& rope_cs = sh.rope_cs;
+  auto& ebuf = sh.ebuf;
+  auto& ptab = sh.ptab;
+  auto& kred = sh.kred;
+  auto& ostage = sh.ostage;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.x, NWG = a.nwg;
   const int hid = a.hidden, H = a.H, KVH = a.KVH, G = H / KVH, NT = a.nsplit;
@@ -347,10 +366,10 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
   // workgroup has about the same left to stream once x1 has arrived.
   const int ntile = KVH * NT;
   const int NB = ntile * G, ND = NWG - NB;
-  const bool att = b < NB;
+  constexpr bool att = ROLE == 0;   // (the kernel entry picks the role instance from b)
   const int tile = b % ntile, gq = b / ntile;
   const int kvh = tile / NT, split = tile % NT;
-  const bool comb = b >= NB && b < NB + H;
+  constexpr bool comb = ROLE == 2;   // o_proj workgroups b in [NB, NB + H) also run the combine
   const int RD = (hid + ND - 1) / ND;                                   // <= 2 NE (checked on the host)
   // gate / up rows in LDS: NE on an attention workgroup; NEO behind the o_proj rows of an o_proj
   // workgroup that runs no combine (issued with its o_proj rows, they land while it waits for
@@ -430,6 +449,16 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
       DEC_STAMP(l, 2);
     }
 
+    // E's ring of gate / up rows in registers (see E); an o_proj workgroup issues its first EP
+    // rows with its o_proj rows when DEC_EARLY is set
+    constexpr int EP = ED < EM ? ED : EM;
+    uint4 wg[EP][KC], wu[EP][KC];
+    const int rs = e0 + NL, nr = ecnt - NL;   // ring rows: rs .. rs + nr - 1 (nr <= 8 EM, checked on the host)
+    auto load_row = [&](int d, int k) {
+      ering_load<KC>(wg[d], wu[d], P.wg, P.wu, ering_row(k, rs, nr, threadIdx.x >> 6, a.inter), hid,
+                     threadIdx.x & 63);
+    };
+
     // ---- D's o_proj rows into LDS (o_proj workgroups): issued now, they land while B and C run ----
     if (!att) {
       DEC_PART_IDS();
@@ -445,6 +474,10 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
         const int i = k / (2 * KC), u = (k / KC) & 1, c = k % KC;
         dec_dma16((u ? P.wu : P.wg) + (long long)(e0 + i) * hid + c * 512 + lane * 8,
                   __builtin_amdgcn_readfirstlane(base + EOFF + (unsigned)k * 1024u));
+      }
+      if constexpr (DEC_EARLY && !comb) {
+#pragma unroll
+        for (int d = 0; d < EP; ++d) load_row(d, d);
       }
     }
 
@@ -688,15 +721,11 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
     };
     {
       DEC_PART_IDS();
-      constexpr int EP = ED < EM ? ED : EM;
-      const int rs = e0 + NL, nr = ecnt - NL;   // ring rows: rs .. rs + nr - 1 (nr <= 8 EM, checked on the host)
       const int n = (nr - wave + DEC_WAVES - 1) / DEC_WAVES;   // this wave's (may be <= 0)
-      uint4 wg[EP][KC], wu[EP][KC];
-      auto load_row = [&](int d, int k) {
-        ering_load<KC>(wg[d], wu[d], P.wg, P.wu, ering_row(k, rs, nr, wave, a.inter), hid, lane);
-      };
+      if constexpr (att || comb || !DEC_EARLY) {
 #pragma unroll
-      for (int d = 0; d < EP; ++d) load_row(d, d);
+        for (int d = 0; d < EP; ++d) load_row(d, d);
+      }
       const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm2 + 8 * tid) : make_uint4(0, 0, 0, 0);
       if (att && wave >= 4) dec_vmcnt0();   // waves outside the x1 gather: their LDS loads have landed
       __syncthreads();
@@ -936,7 +965,11 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a) {
 
 #define DECODE_KERNEL(KC, IC, EM) \
   extern "C" __global__ void __launch_bounds__(DEC_THREADS) k_decode_step_k##KC##_i##IC##_e##EM(const PersistArgs a) { \
-    decode_body<KC, IC, EM>(a); \
+    __shared__ DecShared<KC, DEC_NE(KC)> sh; \
+    const int nb_ = a.H * a.nsplit; \
+    if ((int)blockIdx.x < nb_) decode_body<KC, IC, EM, 0>(a, sh); \
+    else if ((int)blockIdx.x < nb_ + a.H) decode_body<KC, IC, EM, 2>(a, sh); \
+    else decode_body<KC, IC, EM, 1>(a, sh); \
   }
 
 DECODE_KERNEL(3, 3, 2)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 splits: 15 streamed rows)
