@@ -58,7 +58,7 @@ __device__ __forceinline__ uint16_t gm_pack(float f) {
 // slot permutation of the direct-to-LDS rows (GM_SWZ_PAIR: rows 2j and 2j + 1 share one,
 // for an LDS that serves 16 lanes of a 16-byte read per cycle)
 #ifndef GM_SWZ_PAIR
-#define GM_SWZ_PAIR 0
+#define GM_SWZ_PAIR 1
 #endif
 __device__ __forceinline__ int gm_swz(int r) { return GM_SWZ_PAIR ? (r >> 1) & 7 : r & 7; }
 
