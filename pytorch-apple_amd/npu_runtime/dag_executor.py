@@ -103,6 +103,11 @@ class DAGExecutor:
             out[ph] = self.backend.allocate_buffer(arr, spec=spec)
         return out
 
+    @property
+    def npu_executors(self) -> dict:
+        """The backend executor of each device partition (partition id -> executor), read-only."""
+        return dict(self._npu_executors)
+
     def load_weights(self, weights: dict) -> None:
         self._cpu_weights = weights
         self._npu_weight_cache.clear()

@@ -215,13 +215,20 @@ class GreedyGenerator:
             b["d_ids"].native_handle.fill_(first)
             hist = torch.zeros(max_tokens - 1, dtype=torch.int64, device=pos_t.device)
             cur = b["d_ids"]
+            # a decode program that is one persistent step moves its own inputs after each step (one
+            # launch per step); folded for this loop only, so other runs of the program see no advance
+            folded = [ex for ex in getattr(self.decode, "npu_executors", {}).values()
+                      if b["advance"] is not None and getattr(ex, "fold_advance", None) is not None
+                      and ex.fold_advance(b["advance"])]
         else:
             cur = np.array([[first]], np.int64)
         steps = 0
         for step in range(max_tokens - 1):
             pos = n + step
             if fast:
-                if step and b["advance"] is not None:
+                if step and folded:
+                    pass   # the previous step moved the inputs itself
+                elif step and b["advance"] is not None:
                     b["advance"]()
                 elif step:
                     mask_t[..., pos] = 0.0
@@ -252,6 +259,8 @@ class GreedyGenerator:
                 kv[layer["decode_key_input"]] = out[layer["decode_key_output"]]
                 kv[layer["decode_value_input"]] = out[layer["decode_value_output"]]
         if fast:
+            for ex in folded:
+                ex.fold_advance(None)
             self.backend.synchronize()
             if b.get("advance") is not None:
                 b["advance"].check()
