@@ -6,7 +6,7 @@
 // at k offset 8 * (l / 32), and the 32x32 fp32 result sits in 16 registers per lane,
 // element 4q + r at row 8q + 4(l / 32) + r, column l % 32.
 // Workgroup tile BM x BN (BN columns per weight), K step 32, 256 threads as 2 x 2
-// waves of (BM / 2) x (BN / 2). Tiles are double-buffered in LDS through registers: the
+// waves of (BM / 2) x (BN / 2) (or 4 x 1 waves: GEMM_KERNEL_W4). Tiles are double-buffered in LDS through registers: the
 // global loads of step k+1 are in flight while step k is multiplied, then stored to the
 // other buffer, one barrier per step. LDS rows are padded (40 elements) so the 16-byte
 // fragment reads of 32 consecutive rows spread over the banks.
@@ -117,7 +117,7 @@ __device__ __forceinline__ float gm_conv_tail(const GemmArgs& a, float v, float 
 // 1: k = (kh, kw, ci), a whole 64-channel block per K step, padded taps read a.zero;
 // 2: a zero-bordered 4-channel image, each 16-byte chunk two neighbouring taps of one kernel row.
 template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false,
-          int STAGES = 0, int CV = 0>
+          int STAGES = 0, int CV = 0, int WR = 2>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr bool DMA = STAGES >= 2;
   static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
@@ -125,17 +125,25 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
   constexpr int CPR = BK / 8;             // 16-byte chunks per staged row
   constexpr int BNT = BN * NW;            // weight rows staged per step (BN columns per weight)
-  constexpr int TI = BM / 64;             // 32-row MFMA tiles per wave
-  constexpr int TJ = BN / 64;             // 32-column MFMA tiles per wave and weight
+  // the 4 waves as WR rows x WC columns of (BM / WR) x (BN / WC) each (per weight)
+  static_assert(WR == 1 || WR == 2 || WR == 4, "wave rows");
+  constexpr int WC = 4 / WR, WM = BM / WR, WN = BN / WC;
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile");
+  constexpr int TI = WM / 32;             // 32-row MFMA tiles per wave
+  constexpr int TJ = WN / 32;             // 32-column MFMA tiles per wave and weight
   constexpr int A_LD = BM * BK / 8 / 256;    // 16-byte A loads per thread per step
   constexpr int B_LD = BNT * BK / 8 / 256;   // 16-byte B loads per thread per step
   constexpr int SROW = 64;                   // DMA: elements per LDS row
   constexpr int SSTAGE = (BM + BNT) * SROW;  // DMA: elements per stage (A rows, then B rows)
-  __shared__ __attribute__((aligned(16))) uint16_t As[DMA ? 1 : 2][DMA ? 1 : BM][LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[DMA ? 1 : 2][DMA ? 1 : BNT][LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Ls[DMA ? STAGES * SSTAGE : 8];
+  // one LDS buffer: the direct-to-LDS stages, or the register path's double-buffered A and B tiles
+  // (so a direct-to-LDS kernel holds no unused arrays: 80 KB stages fit two workgroups per CU)
+  __shared__ __attribute__((aligned(16))) uint16_t Ls[DMA ? STAGES * SSTAGE : 2 * (BM + BNT) * LDK];
+  typedef uint16_t AsT[2][DMA ? 1 : BM][LDK];
+  typedef uint16_t BsT[2][DMA ? 1 : BNT][LDK];
+  AsT& As = *reinterpret_cast<AsT*>(&Ls[0]);
+  BsT& Bs = *reinterpret_cast<BsT*>(&Ls[DMA ? 0 : 2 * BM * LDK]);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
+  const int wr = wave / WC, wc = wave % WC;
   // XCD-aware tile order: workgroup L (dispatch order) runs on XCD L % 8, so L is remapped
   // to give each XCD a contiguous range of tiles, decoded M-tile fastest: the M tiles that
   // read the same weight tile run back to back on one XCD and share its L2, instead of
@@ -171,7 +179,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   // global -> register staging of one K step, and register -> LDS. The staging lives in
   // named registers (A_LD, B_LD <= 2): a small per-thread array would be promoted to LDS by
   // the compiler, doubling the LDS traffic of the main loop.
-  static_assert(A_LD >= 1 && A_LD <= 4 && B_LD >= 1 && B_LD <= 4, "staging registers");
+  static_assert(DMA || (A_LD >= 1 && A_LD <= 4 && B_LD >= 1 && B_LD <= 4), "staging registers");
   uint4 ra0, ra1, ra2, ra3, rb0, rb1, rb2, rb3;
   auto a_ld = [&](int i, int k0) -> uint4 {
     const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
@@ -273,7 +281,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   auto load_resid = [&](const int j0, const int j1) {   // column groups [j0, j1)
 #pragma unroll
     for (int j = j0; j < j1; ++j) {
-      const int n = min(n_base + wc * (BN / 2) + j * 32 + fr, a.N - 1);
+      const int n = min(n_base + wc * WN + j * 32 + fr, a.N - 1);
 #pragma unroll
       for (int i = 0; i < (HAS_R && !CAN_STAGE ? TI : 1); ++i)
 #pragma unroll
@@ -282,7 +290,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int e = 2 * e2 + h;
-            const long long m = min(m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), a.M - 1);
+            const long long m = min(m_base + wr * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3), a.M - 1);
             w |= (uint32_t)((const uint16_t*)a.resid)[m * a.ldr + n] << (16 * h);
           }
           rr[j][i][e2] = w;
@@ -295,12 +303,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       for (int ks = 0; ks < BK / 16; ++ks) {
         uint4 af[TI], bfr[NW][TJ];
 #pragma unroll
-        for (int i = 0; i < TI; ++i) af[i] = *(const uint4*)&As[buf][wr * (BM / 2) + i * 32 + fr][ks * 16 + fk];
+        for (int i = 0; i < TI; ++i) af[i] = *(const uint4*)&As[buf][wr * WM + i * 32 + fr][ks * 16 + fk];
 #pragma unroll
         for (int u = 0; u < NW; ++u)
 #pragma unroll
           for (int j = 0; j < TJ; ++j)
-            bfr[u][j] = *(const uint4*)&Bs[buf][u * BN + wc * (BN / 2) + j * 32 + fr][ks * 16 + fk];
+            bfr[u][j] = *(const uint4*)&Bs[buf][u * BN + wc * WN + j * 32 + fr][ks * 16 + fk];
 #pragma unroll
         for (int u = 0; u < NW; ++u)
 #pragma unroll
@@ -398,14 +406,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         uint4 af[TI], bfr[NW][TJ];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
-          const int r = wr * (BM / 2) + i * 32 + fr;
+          const int r = wr * WM + i * 32 + fr;
           af[i] = *(const uint4*)&LA[r * SROW + ((c ^ gm_swz(r)) * 8)];
         }
 #pragma unroll
         for (int u = 0; u < NW; ++u)
 #pragma unroll
           for (int j = 0; j < TJ; ++j) {
-            const int r = u * BN + wc * (BN / 2) + j * 32 + fr;
+            const int r = u * BN + wc * WN + j * 32 + fr;
             bfr[u][j] = *(const uint4*)&LB[r * SROW + ((c ^ gm_swz(r)) * 8)];
           }
 #pragma unroll
@@ -438,13 +446,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     for (int u = 0; u < NW; ++u)
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
-        const int n = n_base + wc * (BN / 2) + j * 32 + fr;
+        const int n = n_base + wc * WN + j * 32 + fr;
         if (n >= a.N) continue;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+            const long long m = m_base + wr * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
             if (m < a.M) a.part[(((long long)kz * NW + u) * a.M + m) * a.N + n] = acc[u][i][j][e];
           }
       }
@@ -459,7 +467,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     if (staged) {
       constexpr int TLD = BN + 8;               // padded row: the two half-waves' writes miss each other's banks
       constexpr int CH = BM * BN / 8 / 256;     // chunks per thread
-      uint16_t* T = DMA ? Ls : &As[0][0][0];
+      uint16_t* T;
+      if constexpr (DMA) T = Ls;
+      else T = &As[0][0][0];
       float* F = (float*)(T + BM * TLD);
       uint4 rv[CH];
       if (want_r) {
@@ -474,13 +484,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       __syncthreads();   // every wave is done with the operand buffers
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
-        const int col = wc * (BN / 2) + j * 32 + fr, n = n_base + col;
+        const int col = wc * WN + j * 32 + fr, n = n_base + col;
         const float b0 = ((a.flags & 1) && n < a.N) ? gm_ld<DT>(a.bias, n) : 0.f;
 #pragma unroll
         for (int i = 0; i < TI; ++i)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
-            T[(wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3)) * TLD + col] =
+            T[(wr * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3)) * TLD + col] =
                 gm_pack<DT>(acc[0][i][j][e] + b0);
       }
       if (EPI == GE_CONV && tid < BN && (a.flags & 2)) {
@@ -538,7 +548,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   for (int j = 0; j < TJ; ++j) {
     if constexpr (HAS_R && !CAN_STAGE)
       if (want_r) load_resid(j, j + 1);
-    const int n = n_base + wc * (BN / 2) + j * 32 + fr;
+    const int n = n_base + wc * WN + j * 32 + fr;
     if (n >= a.N) continue;
     const float b0 = (a.flags & 1) ? gm_ld<DT>(g_bias, n - g_lo) : 0.f;
     const float b1 = (EPI == GE_SILU && (a.flags & 2)) ? gm_ld<DT>(a.bias2, n) : 0.f;
@@ -548,7 +558,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     for (int i = 0; i < TI; ++i) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const long long m = m_base + wr * (BM / 2) + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
+        const long long m = m_base + wr * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3);
         if (m >= a.M) continue;
         float v = gm_round<DT>(acc[0][i][j][e] + b0);
         // (kernels with the row-chunk epilogue come here only for odd shapes: plain loads, fewer registers)
@@ -737,6 +747,16 @@ GEMM_KERNEL(k_gemm_f16_bias_m64n64, HS_F16, GE_BIAS, 1, 64, 64, 4)
 GEMM_KERNEL(k_gemm_f16_resid_m128n128, HS_F16, GE_RESID, 1, 128, 128, 4)
 GEMM_KERNEL(k_gemm_f16_resid_m64n128, HS_F16, GE_RESID, 1, 64, 128, 3)
 GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
+// direct-to-LDS only, the 4 waves as 4 rows x 1 column (wave tile BM / 4 x BN per weight): for tile
+// widths that are an odd multiple of 32 (BN = 96: 94 column tiles of a 8960-row weight pair, so
+// M = 512 takes 376 workgroups, one round at two per CU)
+#define GEMM_KERNEL_W4(NAME, DT, EPI, NW, BM, BN, ST)                                                   \
+  extern "C" __global__ void GM_ATTRS NAME##_k64d(const GemmArgs a) {                                  \
+    gemm_body<DT, EPI, NW, BM, BN, false, 64, false, ST, 0, 4>(a);                                     \
+  }
+GEMM_KERNEL_W4(k_gemm_bf16_silu_m128n96, HS_BF16, GE_SILU, 2, 128, 96, 2)
+GEMM_KERNEL_W4(k_gemm_f16_silu_m128n96, HS_F16, GE_SILU, 2, 128, 96, 2)
+
 // grouped (q | k | v projections of one activation into one [M, N] output; no split K)
 #define GEMM_KERNEL_GRP(NAME, DT, BM, BN, ST)                                                                  \
   extern "C" __global__ void GM_ATTRS NAME(const GemmArgs a) { gemm_body<DT, GE_BIAS, 1, BM, BN, false, 32, true>(a); } \

@@ -70,7 +70,10 @@ def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, boo
     ntiles = lambda bm, bn: ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
     if nw == 2:
         if dma:
-            return 64, 64, 1, True
+            # 128 x 96 tiles (4 x 1 waves) where they still give a full round of workgroups: more
+            # MFMA work per operand byte than 64 x 64 (77 against 44 FLOP per staged byte), and a
+            # grid that fits one round at two per CU (M = 512, N = 8960: 376)
+            return (128, 96, 1, True) if ntiles(128, 96) >= GEMM_TARGET_WGS else (64, 64, 1, True)
         for bm, bn in ((128, 64), (64, 64)):
             if ntiles(bm, bn) >= GEMM_TARGET_WGS:
                 return bm, bn, 1, False
