@@ -218,3 +218,45 @@ def test_folded_advance_matches_separate_launches_and_reports_the_cache_end(back
     assert runs[True][0] == runs[False][0]
     for a, b in zip(runs[True][1], runs[False][1]):
         assert np.array_equal(a, b)
+
+
+def test_executor_sees_a_weight_replaced_in_its_dict_and_alternating_inputs(backend):
+    """The executor checks a weights dict once, but a buffer replaced inside the same dict (same
+    key, new object) is picked up on the next call; two alternating input-buffer sets each keep
+    their own pointers. Checked against a fresh executor built with the replaced weight."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(hidden=512, intermediate=1024, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=4096)
+    S, pos = 128, 40
+    ir = build_decode_ir(S, cfg, argmax=True)
+    w = make_weights(ir, cfg, device="cuda")
+    lg = ir["graph_outputs"][0]["name"]
+    ex = _executor(ir, backend, True)
+    ex.load_weights(w)
+    xa = {k: backend.allocate_buffer(v) for k, v in decode_inputs(S, pos, cfg, device="cuda").items()}
+    xb = {k: backend.allocate_buffer(v) for k, v in decode_inputs(S, pos, cfg, device="cuda").items()}
+    xb["input_ids"] = backend.allocate_buffer(torch.tensor([[7]], device="cuda"))
+
+    def logits(e, x):
+        return e.execute(x)[lg].native_handle.view(torch.int16).cpu().numpy().copy()
+
+    print("[case] alternating input sets", flush=True)
+    la, lb = logits(ex, xa), logits(ex, xb)
+    assert np.array_equal(logits(ex, xa), la) and np.array_equal(logits(ex, xb), lb)
+    assert not np.array_equal(la, lb)
+    print("[case] weight replaced in place", flush=True)
+    ((pid, prog),) = ex.npu_programs.items()
+    wd = ex._npu_weight_cache[pid]
+    wmap = getattr(prog, "weight_name_mapping", {})
+    name = next(k for k in wd if wmap.get(k, k) == "model.norm.weight")
+    old = wd[name].native_handle
+    wd[name] = backend.allocate_buffer(old * 2)
+    got = logits(ex, xa)
+    w2 = dict(w)
+    w2["model.norm.weight"] = old * 2
+    fresh = _executor(ir, backend, True)
+    fresh.load_weights(w2)
+    ref = logits(fresh, xa)
+    assert np.array_equal(got, ref)
+    assert not np.array_equal(got, la)
