@@ -749,13 +749,18 @@ GEMM_KERNEL(k_gemm_f16_resid_m64n128, HS_F16, GE_RESID, 1, 64, 128, 3)
 GEMM_KERNEL(k_gemm_f16_resid_m64n64, HS_F16, GE_RESID, 1, 64, 64, 4)
 // direct-to-LDS only, the 4 waves as 4 rows x 1 column (wave tile BM / 4 x BN per weight): for tile
 // widths that are an odd multiple of 32 (BN = 96: 94 column tiles of a 8960-row weight pair, so
-// M = 512 takes 376 workgroups, one round at two per CU)
+// M = 512 takes 376 workgroups, one round at two per CU; a 1536-row weight over K = 8960, 64
+// tiles x 8 K splits, one round of 512)
 #define GEMM_KERNEL_W4(NAME, DT, EPI, NW, BM, BN, ST)                                                   \
   extern "C" __global__ void GM_ATTRS NAME##_k64d(const GemmArgs a) {                                  \
     gemm_body<DT, EPI, NW, BM, BN, false, 64, false, ST, 0, 4>(a);                                     \
   }
 GEMM_KERNEL_W4(k_gemm_bf16_silu_m128n96, HS_BF16, GE_SILU, 2, 128, 96, 2)
 GEMM_KERNEL_W4(k_gemm_f16_silu_m128n96, HS_F16, GE_SILU, 2, 128, 96, 2)
+GEMM_KERNEL_W4(k_gemm_bf16_resid_m128n96, HS_BF16, GE_RESID, 1, 128, 96, 2)
+GEMM_KERNEL_W4(k_gemm_f16_resid_m128n96, HS_F16, GE_RESID, 1, 128, 96, 2)
+GEMM_KERNEL_W4(k_gemm_bf16_bias_m128n96, HS_BF16, GE_BIAS, 1, 128, 96, 2)
+GEMM_KERNEL_W4(k_gemm_f16_bias_m128n96, HS_F16, GE_BIAS, 1, 128, 96, 2)
 
 // grouped (q | k | v projections of one activation into one [M, N] output; no split K)
 #define GEMM_KERNEL_GRP(NAME, DT, BM, BN, ST)                                                                  \

@@ -487,7 +487,9 @@ def _linear_ir(M, N, K, epi, dtype="bfloat16"):
 @pytest.mark.parametrize("M,N,K,epi", [(16, 200, 96, "bias"), (77, 1000, 1536, "resid"), (300, 136, 8960, "resid"),
                                        (512, 1536, 1536, "bias"), (128, 640, 1536, "silu"), (33, 96, 64, "silu"),
                                        # 128 x 96 tiles over 4 x 1 waves (>= 256 tiles), ragged in M, N and K steps
-                                       (700, 4200, 192, "silu"), (520, 8960, 1536, "silu")])
+                                       (700, 4200, 192, "silu"), (520, 8960, 1536, "silu"),
+                                       # long K on 128 x 96 tiles with 6 and 8 K splits
+                                       (520, 1536, 8960, "resid"), (600, 1000, 4096, "bias")])
 def test_mfma_gemm_vs_fp32_matmul(backend, M, N, K, epi):
     """The MFMA GEMM (tiles, split-K, epilogues) against x @ W.T in float32 (test_cuda_executor.py:209-243's
     closed form), within bf16 rounding of the output, and against the CPU fallback."""
