@@ -217,7 +217,8 @@ struct GemmArgs {             // MFMA GEMM (gemm.hip): out = epi(x . w^T), x [M,
   int nw;                     // weights (1, or 2 for SiLU * mul); read by the reduce kernel
   int n1;                     // grouped: first column of the second and third groups
   int n2;
-  // conv epilogue (_conv kernels; flags 1 bias, 2 batch norm, 4 residual, 8 ReLU, as ConvArgs)
+  // conv epilogue (_conv kernels; flags 1 bias, 2 batch norm, 4 residual, 8 ReLU, as ConvArgs;
+  // 16: tiles ordered N tile fastest)
   const void* bn_w;           // [N] batch norm weight, bias, running mean, running var
   const void* bn_b;
   const void* bn_mean;

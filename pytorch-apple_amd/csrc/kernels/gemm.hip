@@ -154,7 +154,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const unsigned per = (total + 7) / 8, xcd = lin % 8, loc = lin / 8;
   const unsigned tall = total % 8 == 0 ? 8 : total % 8;   // XCDs that get `per` tiles; the rest get per - 1
   const unsigned tile = xcd < tall ? xcd * per + loc : tall * per + (xcd - tall) * (per - 1) + loc;
-  const unsigned tm = tile % gy, tn = (tile / gy) % gx, tz = tile / (gy * gx);
+  // conv with flags & 16 (an input larger than its weights): N tile fastest instead, so the N tiles
+  // of one block of output pixels run back to back on one XCD and read its input rows once from
+  // HBM, while the (smaller) weights stay in every XCD's L2
+  const bool nfast = EPI == GE_CONV && (a.flags & 16);
+  const unsigned tm = nfast ? (tile / gx) % gy : tile % gy, tn = nfast ? tile % gx : (tile / gy) % gx;
+  const unsigned tz = tile / (gy * gx);
   const long long m_base = (long long)tm * BM;
   const int n_base = tn * BN;
   const int bz = tz / a.ksplit, kz = tz % a.ksplit;   // batch, K split
@@ -278,6 +283,36 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   const bool staged = CAN_STAGE && a.ksplit == 1 && (a.N & 7) == 0 && (a.ldo & 7) == 0 &&
                       (((size_t)a.out) & 15) == 0 && (!want_r || ((a.ldr & 7) == 0 && (((size_t)a.resid) & 15) == 0));
   uint32_t rr[HAS_R && !CAN_STAGE ? TJ : 1][HAS_R && !CAN_STAGE ? TI : 1][8];
+  // row-chunk epilogue operands: the residual chunks (CH per thread) and the raw batch norm
+  // parameters of column tid (tid < BN). On the direct-to-LDS path they are loaded before the
+  // first stage is issued, so the first stage's wait covers their latency instead of the epilogue
+  // waiting a memory latency of its own after the last MFMA
+  constexpr int CH = BM * BN / 8 / 256;   // 16-byte chunks per thread (row-chunk epilogue)
+  uint4 rv[CAN_STAGE && HAS_R ? CH : 1];
+  float bnr[EPI == GE_CONV && CAN_STAGE ? 4 : 1];
+  auto load_stage_operands = [&]() {
+    if constexpr (CAN_STAGE && HAS_R) {
+      if (want_r) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const int idx = tid + 256 * k, r = idx / (BN / 8), q = idx - r * (BN / 8);
+          const long long m = min(m_base + r, a.M - 1);
+          const int n0 = min(n_base + q * 8, a.N - 8);
+          rv[k] = *(const uint4*)((const uint16_t*)a.resid + m * a.ldr + n0);
+        }
+      }
+    }
+    if constexpr (EPI == GE_CONV && CAN_STAGE) {
+      if (tid < BN && (a.flags & 2)) {
+        const int n = min(n_base + tid, a.N - 1);
+        bnr[0] = gm_ld<DT>(a.bn_w, n);
+        bnr[1] = gm_ld<DT>(a.bn_b, n);
+        bnr[2] = gm_ld<DT>(a.bn_mean, n);
+        bnr[3] = gm_ld<DT>(a.bn_var, n);
+      }
+    }
+  };
+  bool stage_ops_loaded = false;
   auto load_resid = [&](const int j0, const int j1) {   // column groups [j0, j1)
 #pragma unroll
     for (int j = j0; j < j1; ++j) {
@@ -428,6 +463,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     // (kernels with the row-chunk epilogue load their residuals there instead)
     if constexpr (HAS_R && !CAN_STAGE)
       if (want_r && a.ksplit == 1) load_resid(0, TJ);   // issued first: the first stage's wait covers them
+    if constexpr (CAN_STAGE)
+      if (staged) {
+        load_stage_operands();
+        stage_ops_loaded = true;
+      }
 #pragma unroll
     for (int st = 0; st < STAGES - 1; ++st)
       if (st < nsteps) issue(st);
@@ -466,21 +506,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   if constexpr (CAN_STAGE) {
     if (staged) {
       constexpr int TLD = BN + 8;               // padded row: the two half-waves' writes miss each other's banks
-      constexpr int CH = BM * BN / 8 / 256;     // chunks per thread
       uint16_t* T;
       if constexpr (DMA) T = Ls;
       else T = &As[0][0][0];
       float* F = (float*)(T + BM * TLD);
-      uint4 rv[CH];
-      if (want_r) {
-#pragma unroll
-        for (int k = 0; k < CH; ++k) {
-          const int idx = tid + 256 * k, r = idx / (BN / 8), q = idx - r * (BN / 8);
-          const long long m = min(m_base + r, a.M - 1);
-          const int n0 = min(n_base + q * 8, a.N - 8);
-          rv[k] = *(const uint4*)((const uint16_t*)a.resid + m * a.ldr + n0);
-        }
-      }
+      if (!stage_ops_loaded) load_stage_operands();
       __syncthreads();   // every wave is done with the operand buffers
 #pragma unroll
       for (int j = 0; j < TJ; ++j) {
@@ -493,11 +523,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
             T[(wr * WM + i * 32 + (e >> 2) * 8 + (lane >> 5) * 4 + (e & 3)) * TLD + col] =
                 gm_pack<DT>(acc[0][i][j][e] + b0);
       }
-      if (EPI == GE_CONV && tid < BN && (a.flags & 2)) {
-        float al, be;
-        gm_bn_factors<DT>(a, min(n_base + tid, a.N - 1), al, be);
-        F[tid] = al;
-        F[BN + tid] = be;
+      if constexpr (EPI == GE_CONV) {
+        if (tid < BN && (a.flags & 2)) {   // inference batch norm v * al + be (gm_bn_factors)
+          const float al = bnr[0] / sqrtf(bnr[3] + a.eps);
+          F[tid] = al;
+          F[BN + tid] = bnr[1] - bnr[2] * al;
+        }
       }
       __syncthreads();
 #pragma unroll
@@ -773,24 +804,32 @@ GEMM_KERNEL_W4(k_gemm_f16_bias_m128n96, HS_F16, GE_BIAS, 1, 128, 96, 2)
 // an NHWC image (1 x 1, stride 1, no padding); _convg gathers the taps of any kernel / stride /
 // padding (Cin % 64 == 0) with direct-to-LDS staging; _convp reads a zero-bordered 4-channel image
 // (a network's first conv on a 3-channel input, after k_pad_nhwc4)
-#define GEMM_CONV(DTN, DT, BM, BN, ST)                                                                           \
-  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64(const GemmArgs a) {                 \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64>(a);                                                             \
-  }                                                                                                             \
-  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64d(const GemmArgs a) {                \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST>(a);                                                  \
-  }                                                                                                             \
-  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d(const GemmArgs a) {               \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST, 1>(a);                                               \
-  }                                                                                                             \
-  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64d2(const GemmArgs a) {               \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2>(a);                                                   \
-  }                                                                                                             \
-  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convg_m##BM##n##BN##_k64d2(const GemmArgs a) {              \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 1>(a);                                                \
-  }                                                                                                             \
-  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_convp_m##BM##n##BN##_k64d2(const GemmArgs a) {              \
-    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 2>(a);                                                \
+// direct-to-LDS convs: no cap on waves per SIMD (their registers fit 8), so the workgroups a CU's
+// LDS holds all run (five 64 x 64 tiles at two stages, three 128 x 64): short-K convs spend most
+// of a tile waiting on its loads and its stores, which other resident workgroups overlap
+// (ResNet-50 b32: 64 x 64 tiles on 56 x 56 1 x 1 convs 44 -> 34 us; the 7 x 7 stem 55 -> 45 us)
+#ifndef GM_CONV_WPE
+#define GM_CONV_WPE 8
+#endif
+#define GM_ATTRS_CONV __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, GM_CONV_WPE)))
+#define GEMM_CONV(DTN, DT, BM, BN, ST)                                                                              \
+  extern "C" __global__ void GM_ATTRS k_gemm_##DTN##_conv_m##BM##n##BN##_k64(const GemmArgs a) {                    \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64>(a);                                                                \
+  }                                                                                                                 \
+  extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_conv_m##BM##n##BN##_k64d(const GemmArgs a) {              \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST>(a);                                                     \
+  }                                                                                                                 \
+  extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_convg_m##BM##n##BN##_k64d(const GemmArgs a) {             \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, ST, 1>(a);                                                  \
+  }                                                                                                                 \
+  extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_conv_m##BM##n##BN##_k64d2(const GemmArgs a) {             \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2>(a);                                                      \
+  }                                                                                                                 \
+  extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_convg_m##BM##n##BN##_k64d2(const GemmArgs a) {            \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 1>(a);                                                   \
+  }                                                                                                                 \
+  extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_convp_m##BM##n##BN##_k64d2(const GemmArgs a) {            \
+    gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 2>(a);                                                   \
   }
 GEMM_CONV(f16, HS_F16, 128, 128, 4)
 GEMM_CONV(f16, HS_F16, 128, 64, 3)

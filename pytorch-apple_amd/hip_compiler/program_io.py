@@ -129,6 +129,8 @@ def lowering_settings(options: dict) -> dict:
         "fold_attention": (os.environ.get("HIPRT_FOLD_ATTN", "1") == "1") if fold is None else bool(fold),
         "conv_nhwc": os.environ.get("HIPRT_CONV_NHWC", "1") == "1",
         "conv_d2_max_k": subgraph_analyzer.CONV_D2_MAX_K,
+        "conv_small_tile_max_k": subgraph_analyzer.CONV_SMALL_TILE_MAX_K,
+        "conv_nfast": bool(subgraph_analyzer.CONV_NFAST),
         "fuse_reduce_norm": bool(patterns.FUSE_REDUCE_NORM),
         "persistent_decode": (os.environ.get("HIPRT_PERSISTENT", "1") == "1") if options.get("persistent") is None
         else bool(options["persistent"]),

@@ -46,7 +46,9 @@ SKINNY_MAX_M = 32
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
-CONV_D2_MAX_K = int(os.environ.get("HIPRT_CONV_D2_MAX_K", "512"))   # convs up to this K: 2-stage staging
+CONV_D2_MAX_K = int(os.environ.get("HIPRT_CONV_D2_MAX_K", "1024"))   # convs up to this K: 2-stage staging
+CONV_SMALL_TILE_MAX_K = 512   # conv_gemm_tiling: 64 x 64 tiles for K up to this over many tiles
+CONV_NFAST = os.environ.get("HIPRT_CONV_NFAST", "1") == "1"   # conv tile order by operand sizes (emit_conv_nhwc)
 
 
 def gemm_tiling(M: int, N: int, K: int, nw: int = 1) -> tuple[int, int, int, bool]:
@@ -108,10 +110,16 @@ def _is_nhwc(v: TView) -> bool:
 
 def conv_gemm_tiling(M: int, N: int, K: int) -> tuple[int, int, int]:
     """(BM, BN, split-K) for a conv as a GEMM over M pixels, N output channels, K = KH*KW*Cin:
-    the largest tile no wider than the channels that still gives >= 256 workgroups; smaller
+    64 x 64 for short K over many tiles (K <= 512, >= 1024 tiles); otherwise the largest tile no
+    wider than the channels that still gives >= 256 workgroups; smaller
     grids take 64 x 64 tiles and, for K >= 1024, split K toward ~384 workgroups (fp32
     partials, then the reduce applies the epilogue)."""
     ntiles = lambda bm, bn: ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
+    if K <= CONV_SMALL_TILE_MAX_K and ntiles(64, 64) >= 4 * GEMM_TARGET_WGS:
+        # short K, many tiles: the time goes to each tile's load latency and store drain, not to
+        # MFMA work; 64 x 64 tiles (32 KB of LDS at two stages) let five workgroups share a CU,
+        # so one workgroup's loads overlap another's stores
+        return 64, 64, 1
     cands = [(bm, bn) for bm, bn in ((128, 128), (128, 64), (64, 128), (64, 64)) if bn <= max(N, 64)]
     for bm, bn in cands:
         if ntiles(bm, bn) >= GEMM_TARGET_WGS:
@@ -1053,9 +1061,12 @@ class Lowering:
                 rv = rb
         bnv = [self.contiguous(t.name) for t in bn.inputs[1:5]] if bn is not None else [None] * 4
         flags = (1 if has_bias else 0) | (2 if bn is not None else 0) | (4 if rv is not None else 0) | (8 if relu else 0)
+        if CONV_NFAST and xv.numel > Cout * K:   # input larger than the weights: N tiles fastest
+            flags |= 16
         bm, bn_, ksplit = conv_gemm_tiling(M, Cout, K)
-        # always direct-to-LDS; short K (few steps: the pipeline depth buys nothing) takes the 2-stage
-        # variant, whose smaller LDS footprint lets two workgroups share a CU
+        # always direct-to-LDS; K up to 1024 (at most 16 steps, where the pipeline depth buys little)
+        # takes the 2-stage variant, whose smaller LDS footprint lets more workgroups share a CU
+        # (the 56 x 56 3 x 3 convs, K = 576: 28 -> 25.5 us)
         stages = "d2" if K <= CONV_D2_MAX_K else "d"
         kchunk = K
         if ksplit > 1:

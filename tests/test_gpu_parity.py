@@ -817,11 +817,11 @@ def _conv_chain_ir(N, Cin, H, W, C1, C2, k, stride, pad, add, dtype="float16"):
 
 @pytest.mark.parametrize("N,Cin,H,W,C1,C2,k,stride,pad,add,kernel", [
     (2, 64, 14, 14, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m"),     # 1x1 on the image rows, direct-to-LDS
-    (2, 32, 15, 15, 64, 64, 3, 1, 1, True, "k_gemm_f16_convg_m"),      # 3x3 pad 1, NHWC residual
+    (2, 32, 15, 15, 64, 64, 3, 1, 1, True, "k_gemm_f16_convg_m64n64_k64d2"),   # 3x3 pad 1, NHWC residual, K 576: 2 stages
     (2, 64, 15, 17, 128, 96, 3, 2, 1, False, "k_gemm_f16_convg_m"),    # 3x3 stride 2, odd sizes, 96 channels
     (1, 64, 9, 9, 256, 128, 1, 2, 0, False, "k_gemm_f16_convg_m"),     # strided 1x1 (downsample)
     (2, 64, 8, 8, 1024, 256, 1, 1, 0, False, "k_gemm_f16_conv_m"),     # K = 1024, 32 tiles: split K + reduce
-    (16, 64, 64, 64, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m128n128_k64d2"),   # 1,024 tiles, short K: 2 stages
+    (16, 64, 64, 64, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m64n64_k64d2"),   # 4,096 short-K tiles: 64 x 64, 2 stages
 ])
 def test_conv_chain_nhwc_gemm_vs_fp32(backend, N, Cin, H, W, C1, C2, k, stride, pad, add, kernel):
     """A conv reading the channels-last output of the previous one runs as an MFMA GEMM (gemm.hip):
@@ -840,6 +840,8 @@ def test_conv_chain_nhwc_gemm_vs_fp32(backend, N, Cin, H, W, C1, C2, k, stride, 
     (prog,) = ex.npu_programs.values()
     convs = [s for s in prog.steps if s.kind == "conv" and not s.params.get("reduce")]
     assert len(convs) == 2 and convs[0].args["flags"] & 16 and convs[1].kernel.startswith(kernel)
+    # GEMM flag 16: tiles ordered N tile fastest when the input is larger than the weights
+    assert bool(convs[1].args["flags"] & 16) == (N * C1 * H * W > C2 * convs[1].args["K"])
     split = convs[1].params["ksplit"] > 1
     assert convs[1].params["nhwc"] and split == any(s.params.get("reduce") for s in prog.steps)
     assert split or C1 != 1024

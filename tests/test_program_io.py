@@ -104,7 +104,10 @@ def test_cache_key_covers_lowering_switches(monkeypatch):
     monkeypatch.setattr(patterns, "FUSE_REDUCE_NORM", False)
     assert cache_key(ir, {}) != base
     monkeypatch.setattr(patterns, "FUSE_REDUCE_NORM", True)
+    d2 = subgraph_analyzer.CONV_D2_MAX_K
     monkeypatch.setattr(subgraph_analyzer, "CONV_D2_MAX_K", 256)
     assert cache_key(ir, {}) != base
-    monkeypatch.setattr(subgraph_analyzer, "CONV_D2_MAX_K", 512)
+    monkeypatch.setattr(subgraph_analyzer, "CONV_D2_MAX_K", d2)
     assert cache_key(ir, {}) == base
+    monkeypatch.setattr(subgraph_analyzer, "CONV_NFAST", not subgraph_analyzer.CONV_NFAST)
+    assert cache_key(ir, {}) != base
