@@ -805,8 +805,9 @@ GEMM_KERNEL_W4(k_gemm_f16_bias_m128n96, HS_F16, GE_BIAS, 1, 128, 96, 2)
 // padding (Cin % 64 == 0) with direct-to-LDS staging; _convp reads a zero-bordered 4-channel image
 // (a network's first conv on a 3-channel input, after k_pad_nhwc4)
 // direct-to-LDS convs: no cap on waves per SIMD (their registers fit 8), so the workgroups a CU's
-// LDS holds all run (five 64 x 64 tiles at two stages, three 128 x 64): short-K convs spend most
-// of a tile waiting on its loads and its stores, which other resident workgroups overlap
+// LDS holds all run (four 64 x 64 tiles at two stages were seen resident, three 128 x 64):
+// short-K convs spend most of a tile waiting on its loads and its stores, which other resident
+// workgroups overlap
 // (ResNet-50 b32: 64 x 64 tiles on 56 x 56 1 x 1 convs 44 -> 34 us; the 7 x 7 stem 55 -> 45 us)
 #ifndef GM_CONV_WPE
 #define GM_CONV_WPE 8

@@ -117,7 +117,7 @@ def conv_gemm_tiling(M: int, N: int, K: int) -> tuple[int, int, int]:
     ntiles = lambda bm, bn: ((M + bm - 1) // bm) * ((N + bn - 1) // bn)
     if K <= CONV_SMALL_TILE_MAX_K and ntiles(64, 64) >= 4 * GEMM_TARGET_WGS:
         # short K, many tiles: the time goes to each tile's load latency and store drain, not to
-        # MFMA work; 64 x 64 tiles (32 KB of LDS at two stages) let five workgroups share a CU,
+        # MFMA work; 64 x 64 tiles (32 KB of LDS at two stages) let four workgroups share a CU,
         # so one workgroup's loads overlap another's stores
         return 64, 64, 1
     cands = [(bm, bn) for bm, bn in ((128, 128), (128, 64), (64, 128), (64, 64)) if bn <= max(N, 64)]
