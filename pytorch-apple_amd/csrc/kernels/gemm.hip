@@ -117,9 +117,13 @@ __device__ __forceinline__ float gm_conv_tail(const GemmArgs& a, float v, float 
 // 1: k = (kh, kw, ci), a whole 64-channel block per K step, padded taps read a.zero;
 // 2: a zero-bordered 4-channel image, each 16-byte chunk two neighbouring taps of one kernel row.
 template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_BK, bool GRP = false,
-          int STAGES = 0, int CV = 0, int WR = 2>
+          int STAGES = 0, int CV = 0, int WR = 2, int LDSST = 0>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr bool DMA = STAGES >= 2;
+  // LDSST (direct-to-LDS, > 0): LDS for only that many stages, for K ranges of at most LDSST steps
+  // (the host guarantees it; longer ranges are cut there rather than written past the buffer)
+  constexpr int LST = LDSST > 0 ? LDSST : STAGES;
+  static_assert(LDSST == 0 || (DMA && LDSST < STAGES), "LDS stages");
   static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
   static_assert(!CV || (DMA && NW == 1 && !GRP), "conv gather: direct-to-LDS, one weight");
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
@@ -137,7 +141,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr int SSTAGE = (BM + BNT) * SROW;  // DMA: elements per stage (A rows, then B rows)
   // one LDS buffer: the direct-to-LDS stages, or the register path's double-buffered A and B tiles
   // (so a direct-to-LDS kernel holds no unused arrays: 80 KB stages fit two workgroups per CU)
-  __shared__ __attribute__((aligned(16))) uint16_t Ls[DMA ? STAGES * SSTAGE : 2 * (BM + BNT) * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Ls[DMA ? LST * SSTAGE : 2 * (BM + BNT) * LDK];
   typedef uint16_t AsT[2][DMA ? 1 : BM][LDK];
   typedef uint16_t BsT[2][DMA ? 1 : BNT][LDK];
   AsT& As = *reinterpret_cast<AsT*>(&Ls[0]);
@@ -263,7 +267,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 
   // split K: workgroup z covers [z * kchunk, (z + 1) * kchunk)
   const int kbeg = kz * a.kchunk;
-  const int nsteps = min(a.kchunk, a.K - kbeg) / BK;
+  const int nsteps = min(min(a.kchunk, a.K - kbeg) / BK, LDSST > 0 ? LDSST : 1 << 30);
   X += kbeg;
   if constexpr (KN) {
     W0 += (long long)kbeg * a.ldw;
@@ -279,7 +283,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr bool HAS_R = EPI == GE_RESID || EPI == GE_CONV;
   const bool want_r = EPI == GE_RESID || (EPI == GE_CONV && (a.flags & 4));
   // row-chunk epilogue through LDS (see below): 8 columns per 16-byte residual load and store
-  constexpr bool CAN_STAGE = NW == 1 && !GRP && BM * (BN + 8) + 4 * BN <= (DMA ? STAGES * SSTAGE : 2 * BM * LDK);
+  constexpr bool CAN_STAGE = NW == 1 && !GRP && BM * (BN + 8) + 4 * BN <= (DMA ? LST * SSTAGE : 2 * BM * LDK);
   const bool staged = CAN_STAGE && a.ksplit == 1 && (a.N & 7) == 0 && (a.ldo & 7) == 0 &&
                       (((size_t)a.out) & 15) == 0 && (!want_r || ((a.ldr & 7) == 0 && (((size_t)a.resid) & 15) == 0));
   uint32_t rr[HAS_R && !CAN_STAGE ? TJ : 1][HAS_R && !CAN_STAGE ? TI : 1][8];
@@ -832,6 +836,14 @@ GEMM_KERNEL_W4(k_gemm_f16_bias_m128n96, HS_F16, GE_BIAS, 1, 128, 96, 2)
   extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_convp_m##BM##n##BN##_k64d2(const GemmArgs a) {            \
     gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 2>(a);                                                   \
   }
+// one K step (1 x 1 convs over 64 channels): the LDS of one stage, 16 KB at 64 x 64, so up to
+// eight workgroups share a CU
+extern "C" __global__ void GM_ATTRS_CONV k_gemm_f16_conv_m64n64_k64d1(const GemmArgs a) {
+  gemm_body<HS_F16, GE_CONV, 1, 64, 64, false, 64, false, 2, 0, 2, 1>(a);
+}
+extern "C" __global__ void GM_ATTRS_CONV k_gemm_bf16_conv_m64n64_k64d1(const GemmArgs a) {
+  gemm_body<HS_BF16, GE_CONV, 1, 64, 64, false, 64, false, 2, 0, 2, 1>(a);
+}
 GEMM_CONV(f16, HS_F16, 128, 128, 4)
 GEMM_CONV(f16, HS_F16, 128, 64, 3)
 GEMM_CONV(f16, HS_F16, 64, 128, 3)

@@ -821,7 +821,8 @@ def _conv_chain_ir(N, Cin, H, W, C1, C2, k, stride, pad, add, dtype="float16"):
     (2, 64, 15, 17, 128, 96, 3, 2, 1, False, "k_gemm_f16_convg_m"),    # 3x3 stride 2, odd sizes, 96 channels
     (1, 64, 9, 9, 256, 128, 1, 2, 0, False, "k_gemm_f16_convg_m"),     # strided 1x1 (downsample)
     (2, 64, 8, 8, 1024, 256, 1, 1, 0, False, "k_gemm_f16_conv_m"),     # K = 1024, 32 tiles: split K + reduce
-    (16, 64, 64, 64, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m64n64_k64d2"),   # 4,096 short-K tiles: 64 x 64, 2 stages
+    (16, 64, 64, 64, 64, 256, 1, 1, 0, False, "k_gemm_f16_conv_m64n64_k64d1"),   # 4,096 tiles of one K step: 1 stage
+    (16, 64, 32, 32, 128, 256, 1, 1, 0, False, "k_gemm_f16_conv_m64n64_k64d2"),  # 2,048 tiles, K = 128: 2 stages
 ])
 def test_conv_chain_nhwc_gemm_vs_fp32(backend, N, Cin, H, W, C1, C2, k, stride, pad, add, kernel):
     """A conv reading the channels-last output of the previous one runs as an MFMA GEMM (gemm.hip):
