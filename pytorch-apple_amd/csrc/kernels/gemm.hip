@@ -120,10 +120,10 @@ template <int DT, int EPI, int NW, int BM, int BN, bool KN = false, int BK = GM_
           int STAGES = 0, int CV = 0, int WR = 2, int LDSST = 0>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   constexpr bool DMA = STAGES >= 2;
-  // LDSST (direct-to-LDS, > 0): LDS for only that many stages, for K ranges of at most LDSST steps
-  // (the host guarantees it; longer ranges are cut there rather than written past the buffer)
+  // LDSST 1 (direct-to-LDS): the LDS of one stage, each K step loaded and waited for in turn (other
+  // resident workgroups overlap the wait)
   constexpr int LST = LDSST > 0 ? LDSST : STAGES;
-  static_assert(LDSST == 0 || (DMA && LDSST < STAGES), "LDS stages");
+  static_assert(LDSST == 0 || (DMA && LDSST == 1), "LDS stages");
   static_assert(!DMA || (BK == 64 && !KN), "direct-to-LDS staging: BK 64, K-contiguous weights");
   static_assert(!CV || (DMA && NW == 1 && !GRP), "conv gather: direct-to-LDS, one weight");
   constexpr int LDK = BK + 8;             // padded LDS row (elements): fragment reads of 32 rows spread over the banks
@@ -267,7 +267,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 
   // split K: workgroup z covers [z * kchunk, (z + 1) * kchunk)
   const int kbeg = kz * a.kchunk;
-  const int nsteps = min(min(a.kchunk, a.K - kbeg) / BK, LDSST > 0 ? LDSST : 1 << 30);
+  const int nsteps = min(a.kchunk, a.K - kbeg) / BK;
   X += kbeg;
   if constexpr (KN) {
     W0 += (long long)kbeg * a.ldw;
@@ -404,8 +404,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
       }
       bsrc[q] = (const char*)wrow + ((ls ^ gm_swz(row)) * 16);
     }
-    auto issue = [&](int st) {   // stage st of the K loop into LDS buffer st % STAGES
-      const unsigned base = lds0 + (unsigned)((st % STAGES) * SSTAGE) * 2u;
+    auto issue = [&](int st) {   // stage st of the K loop into LDS buffer st % LST
+      const unsigned base = lds0 + (unsigned)((st % LST) * SSTAGE) * 2u;
       const long long kb = (long long)st * BK * 2;
       if constexpr (CV == 2) {   // chunk t of the K range: kernel row t / cpr, taps 2 (t % cpr), + 1
         const int cpr = a.cKW * a.cCin / 8;
@@ -472,15 +472,25 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
         load_stage_operands();
         stage_ops_loaded = true;
       }
+    if constexpr (LST == 1) {
+      for (int s = 0; s < nsteps; ++s) {
+        if (s > 0) __syncthreads();   // every wave is done with step s - 1's buffer
+        issue(s);
+        gm_vmcnt<0>();
+        __syncthreads();   // every wave's part of step s is in LDS
+        compute(0);
+      }
+    } else {
 #pragma unroll
-    for (int st = 0; st < STAGES - 1; ++st)
-      if (st < nsteps) issue(st);
-    for (int s = 0; s < nsteps; ++s) {
-      // stage s has landed when at most the stages issued after it are outstanding
-      gm_vmcnt_after<NI, STAGES - 2>(min(nsteps - 1 - s, STAGES - 2));
-      __syncthreads();   // every wave's part of stage s is in LDS; every wave is done with step s - 1
-      if (s + STAGES - 1 < nsteps) issue(s + STAGES - 1);   // into the buffer step s - 1 used
-      compute(s % STAGES);
+      for (int st = 0; st < STAGES - 1; ++st)
+        if (st < nsteps) issue(st);
+      for (int s = 0; s < nsteps; ++s) {
+        // stage s has landed when at most the stages issued after it are outstanding
+        gm_vmcnt_after<NI, STAGES - 2>(min(nsteps - 1 - s, STAGES - 2));
+        __syncthreads();   // every wave's part of stage s is in LDS; every wave is done with step s - 1
+        if (s + STAGES - 1 < nsteps) issue(s + STAGES - 1);   // into the buffer step s - 1 used
+        compute(s % STAGES);
+      }
     }
     gm_vmcnt<0>();
   }
@@ -836,8 +846,8 @@ GEMM_KERNEL_W4(k_gemm_f16_bias_m128n96, HS_F16, GE_BIAS, 1, 128, 96, 2)
   extern "C" __global__ void GM_ATTRS_CONV k_gemm_##DTN##_convp_m##BM##n##BN##_k64d2(const GemmArgs a) {            \
     gemm_body<DT, GE_CONV, 1, BM, BN, false, 64, false, 2, 2>(a);                                                   \
   }
-// one K step (1 x 1 convs over 64 channels): the LDS of one stage, 16 KB at 64 x 64, so up to
-// eight workgroups share a CU
+// short K (1 x 1 convs over few channels): the LDS of one stage, 16 KB at 64 x 64, so up to eight
+// workgroups share a CU
 extern "C" __global__ void GM_ATTRS_CONV k_gemm_f16_conv_m64n64_k64d1(const GemmArgs a) {
   gemm_body<HS_F16, GE_CONV, 1, 64, 64, false, 64, false, 2, 0, 2, 1>(a);
 }

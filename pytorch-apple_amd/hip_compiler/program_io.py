@@ -131,7 +131,7 @@ def lowering_settings(options: dict) -> dict:
         "conv_d2_max_k": subgraph_analyzer.CONV_D2_MAX_K,
         "conv_small_tile_max_k": subgraph_analyzer.CONV_SMALL_TILE_MAX_K,
         "conv_nfast": bool(subgraph_analyzer.CONV_NFAST),
-        "conv_d1": bool(subgraph_analyzer.CONV_D1),
+        "conv_d1_max_k": subgraph_analyzer.CONV_D1_MAX_K,
         "fuse_reduce_norm": bool(patterns.FUSE_REDUCE_NORM),
         "persistent_decode": (os.environ.get("HIPRT_PERSISTENT", "1") == "1") if options.get("persistent") is None
         else bool(options["persistent"]),

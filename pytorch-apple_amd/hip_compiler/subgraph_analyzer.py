@@ -47,7 +47,7 @@ GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
 CONV_D2_MAX_K = int(os.environ.get("HIPRT_CONV_D2_MAX_K", "1024"))   # convs up to this K: 2-stage staging
-CONV_D1 = os.environ.get("HIPRT_CONV_D1", "1") == "1"   # emit_conv_nhwc: one-stage kernels for K = 64
+CONV_D1_MAX_K = int(os.environ.get("HIPRT_CONV_D1_MAX_K", "64"))   # emit_conv_nhwc: one-stage 64x64 kernels up to this K
 CONV_SMALL_TILE_MAX_K = 512   # conv_gemm_tiling: 64 x 64 tiles for K up to this over many tiles
 CONV_NFAST = os.environ.get("HIPRT_CONV_NFAST", "1") == "1"   # conv tile order by operand sizes (emit_conv_nhwc)
 
@@ -1069,8 +1069,8 @@ class Lowering:
         # takes the 2-stage variant, whose smaller LDS footprint lets more workgroups share a CU
         # (the 56 x 56 3 x 3 convs, K = 576: 28 -> 25.5 us)
         stages = "d2" if K <= CONV_D2_MAX_K else "d"
-        if CONV_D1 and plain and K == 64 and (bm, bn_) == (64, 64) and ksplit == 1:
-            stages = "d1"   # one K step: one stage of LDS (16 KB), up to eight workgroups per CU
+        if plain and K <= CONV_D1_MAX_K and (bm, bn_) == (64, 64) and ksplit == 1:
+            stages = "d1"   # few K steps: one stage of LDS (16 KB), up to eight workgroups per CU
         kchunk = K
         if ksplit > 1:
             kchunk = ((K // 64 + ksplit - 1) // ksplit) * 64
