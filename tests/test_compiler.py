@@ -242,6 +242,22 @@ def test_resnet50_compiles_to_fused_convs():
     assert sum(1 for s in convs[1:] if "_convg_" in s.kernel) == 16 + 3   # 3 x 3 and the stride-2 1 x 1
     ks = [s.kernel for s in p.steps]
     assert "k_maxpool2d_nhwc_f16" in ks and "k_mean_nhwc_f16" in ks
+    # scheduling: tiles N-fastest (GEMM flag 16) exactly where the input outweighs the weights; short-K
+    # convs over >= 1,024 tiles on 64 x 64 tiles; K = 64 1 x 1 convs on the one-stage kernels
+    # (_k64d1), K <= 1,024 on two stages
+    for s in convs[1:]:
+        a = s.args
+        x_elems = a["M"] // (a["cHo"] * a["cWo"]) * a["cH"] * a["cW"] * a["cCin"]
+        assert bool(a["flags"] & 16) == (x_elems > a["N"] * a["K"]), s.params["nodes"]
+        tiles64 = -(-a["M"] // 64) * -(-a["N"] // 64)
+        if a["K"] <= 512 and tiles64 >= 1024:
+            assert s.params["tile"] == (64, 64), s.params["nodes"]
+        plain = "_conv_" in s.kernel
+        if plain and a["K"] == 64 and s.params["tile"] == (64, 64):
+            assert s.kernel.endswith("_k64d1")
+        elif a["K"] <= 1024:
+            assert s.kernel.endswith("_k64d2")
+    assert sum(1 for s in convs if s.kernel.endswith("_k64d1")) == 5   # the 56 x 56 64-channel 1 x 1 convs
     # HIPRT_CONV_NHWC=0 keeps every conv on the NCHW kernels
     import os
     os.environ["HIPRT_CONV_NHWC"] = "0"
