@@ -465,6 +465,7 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     advance.check()   # no step moved past the cache end
+    hexec.check()     # no persistent step timed out waiting for data (its tokens would be invalid)
     ms = elapsed * 1e3 / args.steps
     toks = args.steps / elapsed
     valid_avg = start + (args.steps + 1) / 2.0
@@ -559,11 +560,12 @@ def main() -> int:
         "metric": METRIC, "value": round(toks, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": round(toks / PUBLISHED_TOKS, 2), "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": "cfg3: Qwen2.5-1.5B-arch full decode step, batch 1, static KV cache 2048, "
+        "config": {"workload": f"cfg3: Qwen2.5-1.5B-arch full decode step, batch 1, static KV cache {S}, "
                                f"positions {start}..{start + args.steps - 1}, device-side greedy argmax",
                    "layers": cfg.layers, "hidden": cfg.hidden, "vocab": cfg.vocab, "max_cache_len": S,
                    "launches_per_step": len(program.steps), "compile_s": round(compile_s, 2),
                    "advance_in_step": folded_timed,
+                   "persistent_timeouts": 0,   # hexec.check() above raises on any
                    "host_input_tok_s": round(host_toks, 2),
                    "vs_baseline_ref": "reference CUDA path on RTX 3090 Ti, 30.0 tok/s at position 2048"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1),

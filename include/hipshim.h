@@ -94,6 +94,21 @@ int hs_argmax_rows(const void* x, int dtype, int64_t rows, int64_t cols, int64_t
  * return hipErrorInvalidValue. Calls that overlap on one GPU share that array and race. */
 int hs_argmax_rows_noalloc(const void* x, int dtype, int64_t rows, int64_t cols, int64_t* out, void* stream);
 
+/* Device facts for launches that need every workgroup resident at once (the persistent decode
+ * step): the current device's CU count, and how many workgroups of `fn` with `block` threads and
+ * `dyn_lds` bytes of dynamic LDS fit on one CU. No counterpart in the reference, whose CUDA path
+ * launches one kernel per IR op (cuda_runtime/cuda_executor.py:166-168) and never needs
+ * co-residency; they stand beside cupy.cuda.Device (cuda_runtime/cuda_backend.py:97-101). */
+int hs_device_cus(int* cus);
+int hs_occupancy(void* fn, uint32_t block, size_t dyn_lds, int* blocks_per_cu);
+
+/* `bytes` of zeroed, pinned, coherent host memory mapped into the device's address space: `host`
+ * for the CPU, `device` for kernels. A kernel reports a failure into it (the persistent decode
+ * step's timeout flag) and the host reads it without synchronising. Held until the process ends.
+ * No counterpart in the reference, which raises from host-side checks only
+ * (npu_runtime/dag_executor.py:319-323). */
+int hs_host_alloc_mapped(size_t bytes, void** host, void** device);
+
 /* sizeof() of the kernel argument struct with the given name (e.g. "LinearArgs"),
  * or 0 when unknown; lets the host check its ctypes mirrors. */
 size_t hs_argsize(const char* struct_name);

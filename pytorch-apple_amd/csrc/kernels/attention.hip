@@ -167,13 +167,35 @@ __device__ __forceinline__ float fl_dot2(uint32_t a, uint32_t b, float acc) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(fl_f16x2, a), __builtin_bit_cast(fl_f16x2, b), acc, false);
 }
 
-template <int DT, int W>
+// CHK (long caches): the workgroup first reads its split's mask values, and a split whose
+// positions are all -inf (closed: it contributes exactly nothing) writes an empty partial without
+// loading its K / V rows, so the rows read follow the open positions rather than the cache length.
+// The open splits pay one more memory latency (mask, then K / V).
+template <int DT, int W, bool CHK = false>
 __device__ __forceinline__ void flash_body(const FlashArgs& a) {
   __shared__ float osh[W][AT_D];
   __shared__ float msh[W], lsh[W];
   const int G = a.H / a.KVH;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int split = blockIdx.x, kvh = blockIdx.y, g = blockIdx.z;
+  if constexpr (CHK) {
+    bool open = false;
+    if (a.mask_dtype < 0) {
+      open = true;
+    } else if (threadIdx.x < FL_PW * W) {
+      const long long p = (long long)split * (FL_PW * W) + threadIdx.x;
+      open = p < a.S && ld_f(a.mask, p * a.mask_stride, a.mask_dtype) != -INFINITY;
+    }
+    if (!__syncthreads_or(open)) {
+      const long long part = (long long)(kvh * a.nsplit + split) * G + g;
+      if (threadIdx.x < AT_D) a.part_o[part * AT_D + threadIdx.x] = 0;
+      if (threadIdx.x == 0) {
+        a.part_ml[part * 2] = -INFINITY;
+        a.part_ml[part * 2 + 1] = 0.f;
+      }
+      return;
+    }
+  }
   const long long p0 = (long long)split * (FL_PW * W) + wave * FL_PW;   // this wave's first position
   const int kq = lane >> 2, kc = lane & 3;                         // K: position p0 + kq, dims kc*32..+32
   const long long last = a.S - 1;
@@ -271,6 +293,11 @@ __device__ __forceinline__ void flash_body(const FlashArgs& a) {
 
 extern "C" __global__ void __launch_bounds__(256) k_attn_flash(const FlashArgs a) { flash_body<HS_BF16, 4>(a); }
 extern "C" __global__ void __launch_bounds__(256) k_attn_flash_f16(const FlashArgs a) { flash_body<HS_F16, 4>(a); }
+// long caches: closed splits load no K / V rows
+extern "C" __global__ void __launch_bounds__(256) k_attn_flash_chk(const FlashArgs a) { flash_body<HS_BF16, 4, true>(a); }
+extern "C" __global__ void __launch_bounds__(256) k_attn_flash_chk_f16(const FlashArgs a) {
+  flash_body<HS_F16, 4, true>(a);
+}
 // 8 or 16 waves, 128 or 256 positions per split: 2x or 4x fewer partials, for a combine folded
 // into the next GEMV
 extern "C" __global__ void __launch_bounds__(512) k_attn_flash_w8(const FlashArgs a) { flash_body<HS_BF16, 8>(a); }

@@ -385,7 +385,8 @@ struct PersistArgs {
   long long kv_head_stride;   // elements between KV heads of a cache
   long long vocab;
   int L, hidden, inter, H, KVH, D;
-  int nsplit;                 // attention splits of 128 positions
+  int nsplit;                 // attention workgroups (slots) per query head; slot j walks the cache's
+                              // 128-position chunks j, j + nsplit, ... (those its mask leaves open)
   int nwg;                    // workgroups of the launch (all resident at once)
   int ids_dtype, pos_dtype, cpos_dtype, mask_dtype, add_dtype, n_dtype, out_dtype;
   int flags;                  // 1: q/k/v biases present
@@ -398,6 +399,10 @@ struct PersistArgs {
   long long* adv_cpos;        // cache_position [1]
   int* adv_flag;              // [0]: a step ran past the cache end
   int adv_mask_bytes, adv_pad;
+  int nchunk;                 // 128-position chunks of the cache: ceil(S / 128), at most 32 per slot
+  int rbo, rba;               // gate / up rows streamed through registers per o_proj / attention workgroup
+  int pad2;
+  int* host_err;              // null, or a host-visible word set to 1 when a wait times out
 };
 
 struct ArgmaxFinalizeArgs {   // out[m] = index of max over the `parts` keys of row m

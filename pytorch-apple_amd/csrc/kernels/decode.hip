@@ -15,17 +15,21 @@
 //   * The step tag is the launch count (1..65535, never 0; the exchange area starts zeroed):
 //     stale words from the previous step never match. Exchange slots are per layer, so a slot
 //     is written once per step.
-//   * Every wait is bounded: after 20 ms a workgroup records a timeout in the control word and
-//     goes on, so the launch always ends; the host checks the control word.
+//   * Every wait is bounded: after 20 ms a workgroup records a timeout in the control word (and
+//     in a host-visible word when the host passed one) and goes on, so the launch always ends; the
+//     host checks the flag. The step is correct only with every workgroup resident at once (one
+//     per CU): the host checks the device's CU count and the kernel's occupancy before using it.
 //   * Weights (and the K/V rows of past positions) do not depend on the step's activations, so
 //     each part issues its weight loads before it waits for its inputs: the wait overlaps the
 //     weight stream instead of following it.
 //
 // Work split (NWG workgroups of 8 waves; all resident at once, one per CU):
 //   A  q/k/v:      rows (H + 2 KVH) * D, at most 8 per workgroup, one per wave
-//   B  attention:  workgroup (query head, split) for split < nsplit (128 positions each); the G
-//                  heads of a KV head sit on one XCD and share its K/V rows in L2; partial (o / l, m, l)
-//   C  combine:    one workgroup per query head merges the head's split partials
+//   B  attention:  workgroup (query head, slot) for slot < nsplit; slot j reads the 128-position
+//                  chunks j, j + nsplit, ... that the mask leaves open (a chunk of -inf only is
+//                  skipped: found once per step); the G heads of a KV head share its K/V rows in
+//                  L2; partial (o / l, m, l)
+//   C  combine:    one workgroup per query head merges the head's slot partials
 //   D  o_proj:     hidden rows, at most 8 per workgroup, one per wave; + residual
 //   E  gate/up:    inter rows spread over workgroups and waves; SiLU(gate) * up
 //   F  down:       hidden rows, at most 8 per workgroup; the 8 waves split each row's K; + residual
@@ -40,7 +44,7 @@
 #define DEC_THREADS 512
 #define DEC_WAVES 8
 #define DEC_D 128
-#define DEC_SPL 128                   // positions per attention split: 8 waves x 16
+#define DEC_SPL 128                   // positions per attention chunk: 8 waves x 16
 #define DEC_MAXG 8                    // query heads per KV head, at most
 #define DEC_TIMEOUT 2000000ull        // 20 ms of the 100 MHz real-time counter
 #define DEC_OSTAGE 128                // o_proj or gate / up rows of one workgroup, at most
@@ -53,16 +57,11 @@
 #ifndef DEC_R4
 #define DEC_R4 2                      // lm_head rows per wave in each of its two rounds in flight
 #endif
-// gate/up rows an o_proj workgroup streams, at most (Qwen2.5-1.5B: 11 and 16 per attention
-// workgroup, 0.724 ms per step; the even split, 15 and 15: 0.733; 12: 0.725; 13-14: 0.734)
-#ifndef DEC_RBO
-#define DEC_RBO 11
-#endif
 #ifndef DEC_EARLY
 #define DEC_EARLY 1   // o_proj workgroups issue E's first ring rows with their o_proj rows (0: 0.730 ms, 1: 0.717)
 #endif
 #define DEC_NE(KC) ((KC) == 3 ? 24 : ((KC) == 2 ? 32 : 48))   // gate/up rows in LDS per attention workgroup
-#define DEC_SMEM (32 * (DEC_D + 4) * 2)   // per-part staging: the combine's partials of up to 32 splits
+#define DEC_SMEM (32 * (DEC_D + 4) * 2)   // per-part staging: the combine's partials of up to 32 slots
 
 typedef __attribute__((ext_vector_type(2))) __bf16 dec_bf16x2;
 typedef unsigned int dec_u32x4 __attribute__((ext_vector_type(4)));
@@ -130,17 +129,22 @@ __device__ __forceinline__ unsigned long long xget2(const uint32_t* p) {
   return __hip_atomic_load((unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void dec_fail(uint32_t* err) {
+// A wait timed out: the control word (read by the host after a synchronisation) and, when the
+// host passed one, a word in host memory that the host can read at any time.
+__device__ __forceinline__ void dec_fail(uint32_t* err, int* herr) {
   __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (herr != nullptr) __hip_atomic_store(herr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // Waits until the n words at src (n even, src 8-byte aligned) carry `tag` and copies their
-// payloads (bf16 bits) to dst. Thread t owns word pairs t + 512 j, j < NPT: all of its loads are
-// issued together, and only the pairs not yet current are loaded again, after a short sleep.
+// payloads (bf16 bits) to dst. Thread t owns word pairs t + NTH j, j < NPT: all of its loads are
+// issued together, and only the pairs not yet current are loaded again, after a short sleep (every
+// consumer re-reading every pair multiplies the traffic on the few memory channels that hold a
+// small exchange slot: 256 workgroups gathering the 8,960-word SiLU * up row took 4-5 us that way).
 // Returns after a __syncthreads(), so dst is complete for the whole workgroup.
 template <int NPT, int NTH = DEC_THREADS>
 __device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag, uint16_t* dst, uint32_t* err,
-                                        int tid) {
+                                        int* herr, int tid) {
   if (tid >= NTH) {   // waves outside the gathering set only meet the barrier
     __syncthreads();
     return;
@@ -161,12 +165,13 @@ __device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag
       ok = ok && ((v[j] & tmask) == want || tid + NTH * j >= np);
     if (ok) break;
     if (wall_clock64() - t0 > DEC_TIMEOUT) {
-      dec_fail(err);
+      dec_fail(err, herr);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-    for (int j = 0; j < NPT; ++j) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
+    for (int j = 0; j < NPT; ++j)
+      if ((v[j] & tmask) != want) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
   }
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
@@ -267,13 +272,13 @@ __device__ __forceinline__ void block_norm(const uint16_t* x, uint4 wv, int hid,
 // the layer's input row into xres: the token's embedding row (layer 0) or the exchange words
 template <int KC>
 __device__ __forceinline__ void load_x(const PersistArgs& a, int l, const uint32_t* xw, long long tok, uint32_t tag,
-                                       uint16_t* xres, uint32_t* err, int tid) {
+                                       uint16_t* xres, uint32_t* err, int* herr, int tid) {
   if (l == 0) {
     const int nch = a.hidden >> 3;
     if (tid < nch) *(uint4*)(xres + 8 * tid) = *(const uint4*)(a.emb + tok * a.hidden + 8 * tid);
     __syncthreads();
   } else {
-    xgather<(KC + 1) / 2>(xw, a.hidden, tag, xres, err, tid);
+    xgather<(KC + 1) / 2>(xw, a.hidden, tag, xres, err, herr, tid);
   }
 }
 
@@ -309,6 +314,7 @@ struct DecShared {
   __attribute__((aligned(16))) uint4 ebuf[NE * 2 * KC * 64];
   const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
   unsigned long long kred[DEC_WAVES];
+  uint32_t obw[DEC_WAVES];   // the open-chunk scan: each wave's bits
   // a part's results (o_proj rows, gate / up rows) staged here, then published with one store
   // instruction per 64 words: many single-word stores spread over the waves are acknowledged far
   // more slowly while the memory system is busy with the weight stream
@@ -359,7 +365,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   }
 
   // Roles. Workgroups b < NB (= H * nsplit) run attention: query head g = b / ntile of tile
-  // b % ntile (KV head, split of 128 positions). The other ND run o_proj (RD rows each), and the
+  // b % ntile (KV head, slot). Slot j takes the cache's 128-position chunks j, j + nsplit,
+  // j + 2 nsplit, ... The other ND run o_proj (RD rows each), and the
   // first H of them the combine of query head b - NB. An attention workgroup is done with its
   // latency-bound parts well before x1 exists, so it spends that time loading NE gate / up rows
   // into LDS, and takes NE more gate / up rows than the others; the rest are spread so that every
@@ -368,7 +375,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   const int NB = ntile * G, ND = NWG - NB;
   constexpr bool att = ROLE == 0;   // (the kernel entry picks the role instance from b)
   const int tile = b % ntile, gq = b / ntile;
-  const int kvh = tile / NT, split = tile % NT;
+  const int kvh = tile / NT, slot = tile % NT;
   constexpr bool comb = ROLE == 2;   // o_proj workgroups b in [NB, NB + H) also run the combine
   const int RD = (hid + ND - 1) / ND;                                   // <= 2 NE (checked on the host)
   // gate / up rows in LDS: NE on an attention workgroup; NEO behind the o_proj rows of an o_proj
@@ -376,11 +383,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   // the attention row); none on a combine workgroup, whose partials poll comes sooner
   const int NEO = max(2 * NE - RD, 0) / 2;
   const int NLC = att ? NE : (comb ? 0 : NEO);
-  // gate / up rows streamed: at most DEC_RBO by an o_proj workgroup (its stream starts only after
-  // o_proj), the rest spread over the attention workgroups
-  const int ringT = max(a.inter - NB * NE - (ND - H) * NEO, 0);
-  const int RBO = min((ringT + NWG - 1) / NWG, DEC_RBO);
-  const int RBA = (max(ringT - ND * RBO, 0) + NB - 1) / NB;
+  // gate / up rows streamed: RBO by an o_proj workgroup (its stream starts only after o_proj), RBA
+  // by an attention workgroup (the host's work split of the rows not held in LDS)
+  const int RBO = a.rbo, RBA = a.rba;
   const int e0 = att ? b * (NE + RBA)                                   // first gate / up row
                      : NB * (NE + RBA) + (b - NB) * RBO + max(b - NB - H, 0) * NEO;
   const int ecnt = max(min(NLC + (att ? RBA : RBO), a.inter - e0), 0);  // its rows
@@ -389,7 +394,42 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   // layer 0's tensors into LDS; each layer loads the next one's during its first part and stores
   // them in F, so no layer waits for its table at its start
   if (tid < 14) ptab[0][tid] = ((const void* const*)a.layers)[tid];
+  // The chunks this attention workgroup reads, the same for every layer: bit i stands for chunk
+  // slot + nsplit i, set when the mask opens a position of it (every chunk without a mask).
+  // Chunks whose positions are all -inf contribute exactly nothing to the softmax, so their K / V
+  // rows are never loaded; the loop over the open chunks is bounded by the mask, not by S.
+  // Wave w checks half a chunk per round (chunk 4 q + w / 2, positions 64 (w & 1) + lane), all
+  // eight rounds' loads issued together.
+  uint32_t ob = 0;
+  if constexpr (att) {
+    const int nch = (a.nchunk - slot + NT - 1) / NT;   // chunks of this slot (<= 32, checked on the host)
+    if (a.mask_dtype < 0) {
+      ob = nch >= 32 ? 0xFFFFFFFFu : ((1u << nch) - 1u);
+    } else {
+      FRaw mr[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const long long p = (long long)(slot + NT * (4 * q + (wave >> 1))) * DEC_SPL + 64 * (wave & 1) + lane;
+        mr[q] = ld_f_raw(a.mask, min(p, last), a.mask_dtype);
+      }
+      uint32_t bits = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = 4 * q + (wave >> 1);
+        const long long p = (long long)(slot + NT * i) * DEC_SPL + 64 * (wave & 1) + lane;
+        const bool open = i < nch && p <= last && ld_f_decode(mr[q], a.mask_dtype) != -INFINITY;
+        if (__ballot(open) != 0ull) bits |= 1u << i;
+      }
+      if (lane == 0) sh.obw[wave] = bits;
+    }
+  }
   __syncthreads();
+  if constexpr (att) {
+    if (a.mask_dtype >= 0) {
+#pragma unroll
+      for (int w8 = 0; w8 < DEC_WAVES; ++w8) ob |= sh.obw[w8];
+    }
+  }
 
   for (int l = 0; l < a.L; ++l) {
     const DecodeLayerPtrs P = dec_layer(ptab[l & 1]);
@@ -424,7 +464,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm1 + 8 * tid) : make_uint4(0, 0, 0, 0);
       __syncthreads();
       DEC_STAMP(l, 0);
-      load_x<KC>(a, l, XL, tok, tag, xres, err, tid);
+      load_x<KC>(a, l, XL, tok, tag, xres, err, a.host_err, tid);
       DEC_STAMP(l, 1);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
       if (has) {
@@ -481,108 +521,134 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       }
     }
 
-    // ---- the past positions' K / V rows and mask values for B: no dependency on this step's
-    // activations, so the K rows are issued before B waits for its q / k / v (after A, whose input
-    // poll would otherwise wait behind them); the V rows, needed last, are issued once q / k / v
-    // are in, so the poll does not wait behind them either and their latency overlaps the scores
-    uint4 kr[4];
-    FRaw mraw = {0, 0};
-    {
+    // ---- B: attention of one query head over the open chunks of its slot ----------------------------
+    // The first open chunk's K rows and mask values do not depend on this step's activations, so
+    // they are issued before B waits for its q / k / v (after A, whose input poll would otherwise
+    // wait behind them); its V rows, needed last, are issued once q / k / v are in, so the poll
+    // does not wait behind them either and their latency overlaps the scores. Further open chunks
+    // (caches longer than 128 nsplit positions) are loaded and folded in one after another: each
+    // wave keeps a running (max, sum, unnormalised output) over its 16 positions of every chunk.
+    if constexpr (att) {
       DEC_PART_IDS();
-      const long long p0 = (long long)split * DEC_SPL + wave * 16;
-      const int kq = lane >> 2, kc = lane & 3;
-      if (att) {
-        const uint16_t* Kb = P.kc + (long long)kvh * kvs;
-        if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(p0 + kq, last), a.mask_dtype);
-        const uint4* ks = (const uint4*)(Kb + min(p0 + kq, last) * DEC_D + kc * 32);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kr[j] = make_uint4(0, 0, 0, 0);
-      }
-    }
-
-    // ---- B: attention of one query head over one split of 128 positions ----------------------------
-    if (att) {
-      DEC_PART_IDS();
-      const long long p0 = (long long)split * DEC_SPL + wave * 16;
       const int kq = lane >> 2, kc = lane & 3;
       const int hq = kvh * G + gq;
       uint16_t* raw = (uint16_t*)smem;               // [3 * D]: q, k, v as produced
       const float* csh = rope_cs;                    // [64] cos, [64] sin (rounded, scaled)
       uint16_t* rot = (uint16_t*)(smem + 1536);      // [2 * D]: rotated q and k
       float* osh = (float*)(smem + 2048);            // [8][D] per-wave unnormalised outputs
-      __syncthreads();
-      xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, tid);
-      DEC_STAMP(l, 3);
-      uint32_t vr[16];
-      {
-        const uint16_t* Vb = P.vc + (long long)kvh * kvs;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(p0 + t, last) * DEC_D + 2 * lane);
-      }
-      if (tid < 128) {   // rotate_half RoPE: threads 0..63 q, 64..127 k
-        const int hs = tid >> 6, j = tid & 63;
-        const float x0 = bfh(raw[hs * DEC_D + j]), x1 = bfh(raw[hs * DEC_D + j + 64]);
-        const float c = csh[j], sn = csh[64 + j];
-        rot[hs * DEC_D + j] = f32_to_bf16(rb(rb(x0 * c) + rb(-x1 * sn)));
-        rot[hs * DEC_D + j + 64] = f32_to_bf16(rb(rb(x1 * c) + rb(x0 * sn)));
-      }
-      __syncthreads();
+      const uint16_t* Kb = P.kc + (long long)kvh * kvs;
+      const uint16_t* Vb = P.vc + (long long)kvh * kvs;
       const bool cin = cpos >= 0 && cpos < S;
-      if (cin && gq == 0 && cpos >= (long long)split * DEC_SPL && cpos < (long long)(split + 1) * DEC_SPL &&
-          tid < DEC_D) {   // this step's K / V row goes into the caches (index_copy at cache_position)
-        stg2(P.kc + (long long)kvh * kvs + cpos * DEC_D + tid, rot[DEC_D + tid]);
-        stg2(P.vc + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
-      }
-      // the wave holding that position uses the new K / V row (V chosen at its use below, so no
-      // branch joins the loaded V values, which would make the compiler wait for them here)
-      const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
-      const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
-      if (vnew && p0 + kq == cpos) {
-        const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kr[j] = kn[j];
-      }
-      const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
-      const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
-      const bool live = __ballot(mval != -INFINITY) != 0ull;
       float acc0 = 0.f, acc1 = 0.f, mw = -INFINITY, lw = 0.f;
-      if (live) {
-        const uint4* qq = (const uint4*)(rot + kc * 32);
-        float d = 0.f;
+      auto rope = [&]() {   // rotate_half RoPE: threads 0..63 q, 64..127 k
+        if (tid < 128) {
+          const int hs = tid >> 6, j = tid & 63;
+          const float x0 = bfh(raw[hs * DEC_D + j]), x1 = bfh(raw[hs * DEC_D + j + 64]);
+          const float c = csh[j], sn = csh[64 + j];
+          rot[hs * DEC_D + j] = f32_to_bf16(rb(rb(x0 * c) + rb(-x1 * sn)));
+          rot[hs * DEC_D + j + 64] = f32_to_bf16(rb(rb(x1 * c) + rb(x0 * sn)));
+        }
+        __syncthreads();
+        // this step's K / V row goes into the caches (index_copy at cache_position), by the
+        // first head's workgroup of the slot that holds the position, open or not
+        if (cin && gq == 0 && (int)((cpos / DEC_SPL) % NT) == slot && tid < DEC_D) {
+          stg2(P.kc + (long long)kvh * kvs + cpos * DEC_D + tid, rot[DEC_D + tid]);
+          stg2(P.vc + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
+        }
+      };
+      // one chunk folded into the wave's running softmax; p0: the wave's first position in it.
+      // The wave holding cache_position uses the new K / V row (V chosen at its use, so no branch
+      // joins the loaded V values, which would make the compiler wait for them there). For the
+      // first chunk (mw = -inf) the rescaling factor is 0 and the result is that of a one-pass
+      // softmax over the chunk.
+      auto fold = [&](const uint4 (&kin)[4], const uint32_t (&vr)[16], FRaw mraw, long long p0) {
+        uint4 kr[4] = {kin[0], kin[1], kin[2], kin[3]};
+        const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
+        const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
+        if (vnew && p0 + kq == cpos) {
+          const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint4 q4 = qq[j];
-          d = ddot2(q4.x, kr[j].x, d);
-          d = ddot2(q4.y, kr[j].y, d);
-          d = ddot2(q4.z, kr[j].z, d);
-          d = ddot2(q4.w, kr[j].w, d);
+          for (int j = 0; j < 4; ++j) kr[j] = kn[j];
         }
-        d += HS_DPP(d, HS_QUAD_XOR1);
-        d += HS_DPP(d, HS_QUAD_XOR2);
-        float sc = -INFINITY;
-        if (mval != -INFINITY) {
-          sc = rb(d);
-          sc = rb(sc * a.scale);
-          if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
-        }
-        float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
-        m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
-        m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
-        const float e = (sc == -INFINITY) ? 0.f : __expf(sc - m);
-        float ls = e + HS_DPP(e, HS_ROW_ROR4);
-        ls += HS_DPP(ls, HS_ROW_ROR8);
-        lw = (HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48));
-        mw = m;
+        const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
+        const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
+        const bool live = __ballot(mval != -INFINITY) != 0ull;
+        if (live) {
+          const uint4* qq = (const uint4*)(rot + kc * 32);
+          float d = 0.f;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-          const float p = HS_RL(e, 4 * t);
-          const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
-          acc0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), acc0);
-          acc1 = fmaf(p, bfh((uint16_t)(vt >> 16)), acc1);
+          for (int j = 0; j < 4; ++j) {
+            const uint4 q4 = qq[j];
+            d = ddot2(q4.x, kr[j].x, d);
+            d = ddot2(q4.y, kr[j].y, d);
+            d = ddot2(q4.z, kr[j].z, d);
+            d = ddot2(q4.w, kr[j].w, d);
+          }
+          d += HS_DPP(d, HS_QUAD_XOR1);
+          d += HS_DPP(d, HS_QUAD_XOR2);
+          float sc = -INFINITY;
+          if (mval != -INFINITY) {
+            sc = rb(d);
+            sc = rb(sc * a.scale);
+            if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
+          }
+          float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
+          m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
+          m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
+          const float mn = fmaxf(mw, m);
+          const float al = (mw == -INFINITY) ? 0.f : __expf(mw - mn);
+          const float e = (sc == -INFINITY) ? 0.f : __expf(sc - mn);
+          float ls = e + HS_DPP(e, HS_ROW_ROR4);
+          ls += HS_DPP(ls, HS_ROW_ROR8);
+          lw = lw * al + ((HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48)));
+          mw = mn;
+          acc0 *= al;
+          acc1 *= al;
+#pragma unroll
+          for (int t = 0; t < 16; ++t) {
+            const float p = HS_RL(e, 4 * t);
+            const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
+            acc0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), acc0);
+            acc1 = fmaf(p, bfh((uint16_t)(vt >> 16)), acc1);
+          }
         }
+      };
+      if (ob != 0) {   // workgroup-uniform
+        uint32_t rest = ob & (ob - 1);
+        const long long q0 = (long long)(slot + NT * __builtin_ctz(ob)) * DEC_SPL + wave * 16;
+        uint4 kr[4];
+        FRaw mraw = {0, 0};
+        if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(q0 + kq, last), a.mask_dtype);
+        const uint4* ks = (const uint4*)(Kb + min(q0 + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
+        __syncthreads();
+        xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, a.host_err, tid);
+        DEC_STAMP(l, 3);
+        uint32_t vr[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(q0 + t, last) * DEC_D + 2 * lane);
+        rope();
+        fold(kr, vr, mraw, q0);
+        while (rest != 0) {   // workgroup-uniform
+          const long long pc = (long long)(slot + NT * __builtin_ctz(rest)) * DEC_SPL + wave * 16;
+          rest &= rest - 1;
+          uint4 kr2[4];
+          uint32_t vr2[16];
+          FRaw m2 = {0, 0};
+          if (a.mask_dtype >= 0) m2 = ld_f_raw(a.mask, min(pc + kq, last), a.mask_dtype);
+          const uint4* ks2 = (const uint4*)(Kb + min(pc + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) kr2[j] = ldg16(ks2 + j);
+#pragma unroll
+          for (int t = 0; t < 16; ++t) vr2[t] = ldg4(Vb + min(pc + t, last) * DEC_D + 2 * lane);
+          fold(kr2, vr2, m2, pc);
+        }
+      } else {   // every chunk of this slot is closed: an empty partial
+        __syncthreads();
+        xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, a.host_err, tid);
+        DEC_STAMP(l, 3);
+        rope();
       }
       osh[wave * DEC_D + 2 * lane] = acc0;
       osh[wave * DEC_D + 2 * lane + 1] = acc1;
@@ -603,13 +669,13 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
           o = fmaf(f, osh[w8 * DEC_D + min(tid, DEC_D - 1)], o);
           L = fmaf(f, lv, L);
         }
-        // the head's split partial, one contiguous block: o / l (bf16), then m and l as four
+        // the head's slot partial, one contiguous block: o / l (bf16), then m and l as four
         // 16-bit halves
         const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
         const int e = tid - DEC_D;
         const uint16_t v = tid < DEC_D ? f32_to_bf16(L > 0.f ? o / L : 0.f)
                                        : (uint16_t)(((e < 2 ? mb : lb) >> ((e & 1) ? 0 : 16)) & 0xFFFFu);
-        xput(XL + X.part + ((long long)hq * NT + split) * (DEC_D + 4) + tid, v, tag);
+        xput(XL + X.part + ((long long)hq * NT + slot) * (DEC_D + 4) + tid, v, tag);
       }
       DEC_STAMP(l, 4);
       // this workgroup's first NL gate / up rows into LDS: its next wait (x1, in E) is some
@@ -622,7 +688,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       }
     }
 
-    // ---- C: combine the split partials of one query head (waves 0-3, 2 threads per dimension) ----------
+    // ---- C: combine the slot partials of one query head (waves 0-3, 2 threads per dimension) ----------
     if (comb) {
       DEC_PART_IDS();
       const int h = b - ntile * G;
@@ -630,7 +696,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       float* cw = red2;                 // [NT] weights e^(m_t - M) l_t / L (NT <= 32: red2 holds 64)
       __syncthreads();
       xgather<(32 * (DEC_D + 4) + 2 * 256 - 1) / (2 * 256), 256>(
-          XL + X.part + (long long)h * NT * (DEC_D + 4), NT * (DEC_D + 4), tag, pl, err, tid);
+          XL + X.part + (long long)h * NT * (DEC_D + 4), NT * (DEC_D + 4), tag, pl, err, a.host_err, tid);
       DEC_STAMP(l, 5);
       if (wave == 0) {
         float m = -INFINITY, lv = 0.f;
@@ -661,7 +727,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       dec_vmcnt0();   // this wave's o_proj rows have landed (long ago)
       __syncthreads();
       DEC_STAMP(l, 7);
-      xgather<(KC + 1) / 2 * 2, 256>(XL + X.att, H * DEC_D, tag, xs, err, tid);
+      xgather<(KC + 1) / 2 * 2, 256>(XL + X.att, H * DEC_D, tag, xs, err, a.host_err, tid);
       DEC_STAMP(l, 8);
       const unsigned char* ob = (const unsigned char*)ebuf;
       const int d0 = (b - NB) * RD;
@@ -730,7 +796,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       if (att && wave >= 4) dec_vmcnt0();   // waves outside the x1 gather: their LDS loads have landed
       __syncthreads();
       DEC_STAMP(l, 10);
-      xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, tid);
+      xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, a.host_err, tid);
       DEC_STAMP(l, 11);
 #pragma unroll
       for (int j = 0; j < RFE; ++j) load_down(j);
@@ -819,7 +885,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
 #pragma unroll
       for (int j = RFE; j < RF; ++j) load_down(j);
       DEC_STAMP(l, 13);
-      xgather<(IC * 4096 / 2 + 255) / 256, 256>(XL + X.h, a.inter, tag, hs, err, tid);
+      xgather<(IC * 4096 / 2 + DEC_THREADS - 1) / DEC_THREADS>(XL + X.h, a.inter, tag, hs, err, a.host_err, tid);
       DEC_STAMP(l, 14);
       float part[RF];
 #pragma unroll
@@ -874,7 +940,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     const uint4 nw = tid < (hid >> 3) ? *(const uint4*)(a.norm_f + 8 * tid) : make_uint4(0, 0, 0, 0);
     __syncthreads();
     DEC_STAMP(a.L, 0);
-    xgather<(KC + 1) / 2>(XF, hid, tag, xres, err, tid);
+    xgather<(KC + 1) / 2>(XF, hid, tag, xres, err, a.host_err, tid);
     DEC_STAMP(a.L, 1);
     block_norm(xres, nw, hid, a.eps_f, a.n_dtype, xs, red, tid);
     unsigned long long best = 0ull;
@@ -923,7 +989,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       unsigned long long v = xget2(keys + 2 * (long long)i);
       while ((uint32_t)(v >> 48) != tag) {
         if (wall_clock64() - t0 > DEC_TIMEOUT) {
-          dec_fail(err);
+          dec_fail(err, a.host_err);
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -972,7 +1038,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     else decode_body<KC, IC, EM, 1>(a, sh); \
   }
 
-DECODE_KERNEL(3, 3, 2)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 splits: 15 streamed rows)
+DECODE_KERNEL(3, 3, 2)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 slots: 16 streamed rows)
 DECODE_KERNEL(3, 3, 3)   // hidden 1536, up to 24 streamed gate/up rows per workgroup
 DECODE_KERNEL(3, 3, 4)   // hidden 1536, up to 32
 DECODE_KERNEL(3, 3, 6)   // hidden 1536, up to 48

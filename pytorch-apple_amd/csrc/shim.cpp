@@ -240,6 +240,36 @@ int hs_graph_destroy(void* graph_exec) {
   return 0;
 }
 
+int hs_device_cus(int* cus) {
+  int dev = 0;
+  HS_CHECK(hipGetDevice(&dev));
+  HS_CHECK(hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev));
+  return 0;
+}
+
+int hs_occupancy(void* fn, uint32_t block, size_t dyn_lds, int* blocks_per_cu) {
+  if (!fn || !blocks_per_cu) return fail_arg("hs_occupancy: null function or output");
+  HS_CHECK(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, (hipFunction_t)fn, (int)block,
+                                                              dyn_lds));
+  return 0;
+}
+
+int hs_host_alloc_mapped(size_t bytes, void** host, void** device) {
+  if (!host || !device || bytes == 0) return fail_arg("hs_host_alloc_mapped: null output or zero size");
+  void* h = nullptr;
+  HS_CHECK(hipHostMalloc(&h, bytes, hipHostMallocMapped | hipHostMallocCoherent));
+  std::memset(h, 0, bytes);
+  void* d = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&d, h, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(h);
+    return fail_hip(e, "hipHostGetDevicePointer");
+  }
+  *host = h;
+  *device = d;
+  return 0;
+}
+
 int hs_stream_create(void** stream) {
   hipStream_t s;
   HS_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));

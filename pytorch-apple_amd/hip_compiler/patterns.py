@@ -405,7 +405,10 @@ def _emit_flash_attention(low, q, k, v, mask, out, scale, H, kvh, S, add_dtype, 
     ins = [q, k, v] + ([mask] if mask else [])
     params = {"kv_heads": kvh, "q_per_kv": G, "seq_len": S, "head_dim": D, "nsplit": nsplit, "spl": spl,
               "nodes": names}
-    kname = {4: "k_attn_flash", 8: "k_attn_flash_w8", 16: "k_attn_flash_w16"}[waves] + \
+    # long caches (more than 32 splits): each split reads its mask first and skips its K / V rows
+    # when every position is -inf, so a 32k-position cache at position 2k reads 2k positions' rows
+    chk = waves == 4 and nsplit > 32 and mask is not None
+    kname = ("k_attn_flash_chk" if chk else {4: "k_attn_flash", 8: "k_attn_flash_w8", 16: "k_attn_flash_w16"}[waves]) + \
         ("" if dt == "bfloat16" else "_f16")
     low.emit(LaunchStep(kind="attention", kernel=kname, module="attention", arg_struct="FlashArgs",
                         args=args, grid=(nsplit, kvh, G), block=(64 * waves, 1, 1), inputs=ins,

@@ -3,7 +3,8 @@
 The fused lowering of a Qwen2-style decode step (one token, static KV caches) is a fixed
 sequence of launches: ``k_embedding``, then per layer ``k_qkv_rope*`` (RMSNorm, q/k/v, RoPE,
 K/V cache rows), ``k_attn_flash*`` (split-S attention), ``k_gemv_attn*_resid_r2`` (combine,
-o_proj, residual), ``k_gemv_norm_silu_r1`` (RMSNorm, gate/up, SiLU * up) and
+o_proj, residual; for long caches ``k_attn_combine`` then ``k_gemv_resid_r*``),
+``k_gemv_norm_silu_r1`` (RMSNorm, gate/up, SiLU * up) and
 ``k_gemv_resid_ks_r2`` / ``k_gemv_resid_r1`` (down_proj, residual), then ``k_gemv_norm_argmax_r4`` (final RMSNorm,
 lm_head, argmax keys) and ``k_argmax_finalize``. When the launch list is exactly that, with
 every layer reading what the previous launch wrote and dimensions the persistent kernel
@@ -14,6 +15,15 @@ boundaries. Anything else keeps the launch list unchanged.
 
 The launch reads the layers' tensors from a pointer table (``params["table"]``): 14 entries
 per layer (``TABLE_FIELDS``), resolved by the executor for each set of bound buffers.
+
+Attention runs on ``nsplit`` workgroups (slots) per query head, at most ``MAX_SLOTS``; slot j
+reads the cache's 128-position chunks j, j + nsplit, ... that the step's mask leaves open, so a
+cache of up to 32 * 128 * nsplit positions is one launch and the K/V rows read follow the open
+positions, not the cache length.
+
+The step is correct only when all ``NWG`` workgroups are resident at once (they wait for each
+other's data). ``fuse_decode_step`` asks ``resident_workgroups`` how many fit on the device and
+keeps the launch list when that is fewer; the executor checks again before it launches.
 
 The reference runs this step as one Python dispatch per IR op
 (`cuda_runtime/cuda_executor.py:136-176`); here the same IR ops become one launch.
@@ -28,19 +38,25 @@ from hip_compiler.program import DTYPE_CODE, LaunchStep, Ref, Storage
 NWG = 256            # workgroups of the launch: one per CU of an MI355X (all resident together)
 THREADS = 512
 D = 128
-SPL = 128            # positions per attention split
+SPL = 128            # positions per attention chunk
 MAX_G = 8            # query heads per KV head
-MAX_SPLITS = 32
+MAX_SLOTS = 16       # attention workgroups per query head
+MAX_CHUNKS_PER_SLOT = 32   # the kernel's open-chunk word (decode.hip ``ob``)
 VARIANTS = {1, 2, 3}     # hidden / 512 with a kernel instance (inter <= 4096 * that)
 E_LDS_ROWS = {1: 48, 2: 32, 3: 24}   # gate/up rows an attention workgroup holds in LDS (decode.hip DEC_NE)
-RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}
-O_RING_MAX = 11     # gate/up rows an o_proj workgroup streams, at most (decode.hip DEC_RBO)   # instances: gate/up rows per wave streamed through registers
+RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}   # kernel instances: gate/up rows per wave in registers
+# gate/up rows an o_proj workgroup streams, at most, while the attention workgroups can take the
+# rest (Qwen2.5-1.5B at 2048 positions: 11, and 16 per attention workgroup, 0.724 ms per step; the
+# even split, 15 and 15: 0.733; 12: 0.725; 13-14: 0.734)
+O_RING_MAX = 11
+OSTAGE = 128         # decode.hip DEC_OSTAGE: a workgroup's gate/up rows, staged
 
 TABLE_FIELDS = ("norm1", "wq", "bq", "wk", "bk", "wv", "bv", "kc", "vc", "wo", "norm2", "wg", "wu", "wd")
 
 QKV = ("k_qkv_rope_k1536", "k_qkv_rope")
-FLASH = ("k_attn_flash_w8", "k_attn_flash", "k_attn_flash_w16")
-OPROJ = ("k_gemv_attn16_resid_r2", "k_gemv_attn_resid_r2")
+FLASH = ("k_attn_flash_w8", "k_attn_flash", "k_attn_flash_w16", "k_attn_flash_chk")
+OPROJ = ("k_gemv_attn16_resid_r2", "k_gemv_attn_resid_r2")    # the combine folded in
+PLAIN = ("k_gemv_resid_r1", "k_gemv_resid_r2")                # after a k_attn_combine
 DOWN = ("k_gemv_resid_ks_r2", "k_gemv_resid_r1")
 
 
@@ -48,11 +64,80 @@ def enabled() -> bool:
     return os.environ.get("HIPRT_PERSISTENT", "1") == "1"
 
 
+def _device_resident(kernel: str) -> int | None:
+    """Workgroups of ``kernel`` (``THREADS`` threads) that the current device holds at once: CUs x
+    workgroups per CU. None when no GPU is visible (compiling on a CPU-only host)."""
+    try:
+        import torch
+
+        if not torch.cuda.is_available():
+            return None
+    except ImportError:
+        return None
+    from hip_runtime.hip_executor import resident_workgroups
+
+    return resident_workgroups(torch.cuda.current_device(), "decode", kernel, THREADS)
+
+
+# Replaceable hook (tests fake a smaller device through it).
+resident_workgroups = _device_resident
+
+
+def work_split(hidden: int, inter: int, H: int, nslot: int) -> dict | None:
+    """The kernel's division of a layer among the NWG workgroups (decode.hip ``decode_body``): NB
+    attention workgroups (each also holds NE gate/up rows in LDS), ND o_proj workgroups of RD rows
+    (those that run no combine also hold NEO gate/up rows in LDS); the gate/up rows left over are
+    streamed through registers, RBO by each o_proj workgroup and RBA by each attention workgroup;
+    EM is the kernel instance's register rows per wave. None when no instance fits."""
+    KC = hidden // 512
+    NB, NE = H * nslot, E_LDS_ROWS[KC]
+    ND = NWG - NB
+    if ND <= H:
+        return None
+    RD = -(-hidden // ND)
+    if RD > 2 * NE:   # the o_proj rows of one workgroup must fit its LDS
+        return None
+    NEO = max(2 * NE - RD, 0) // 2
+    ring = max(inter - NB * NE - (ND - H) * NEO, 0)
+    cap = 8 * max(RING_ROWS[KC])
+    RBO = min(-(-ring // NWG), O_RING_MAX)
+    RBO = max(RBO, -(-max(ring - NB * cap, 0) // ND))   # what the attention workgroups cannot take
+    RBA = -(-max(ring - ND * RBO, 0) // NB)
+    RB = max(RBA, RBO)
+    em = [e for e in RING_ROWS[KC] if 8 * e >= RB]
+    if not em or max(NE, NEO) + RB > OSTAGE:
+        return None
+    return dict(NB=NB, NE=NE, ND=ND, RD=RD, NEO=NEO, RBO=RBO, RBA=RBA, EM=em[0])
+
+
+def _parse_layers(steps: list[LaunchStep]):
+    """Per layer (qkv, flash, combine or None, o_proj, gate/up, down), or None."""
+    n = len(steps)
+    layers, i = [], 1
+    while i < n - 2:
+        if i + 4 >= n - 2 or steps[i].kernel not in QKV or steps[i + 1].kernel not in FLASH:
+            return None
+        j, c = i + 2, None
+        if steps[j].kernel == "k_attn_combine":
+            c, j = steps[j], j + 1
+        if j + 2 >= n - 2:
+            return None
+        o, g, d = steps[j], steps[j + 1], steps[j + 2]
+        if c is None and o.kernel not in OPROJ or c is not None and o.kernel not in PLAIN:
+            return None
+        if g.kernel != "k_gemv_norm_silu_r1" or d.kernel not in DOWN:
+            return None
+        layers.append((steps[i], steps[i + 1], c, o, g, d))
+        i = j + 3
+    return layers if i == n - 2 and layers else None
+
+
 def exchange_words(L: int, hidden: int, inter: int, H: int, KVH: int, nsplit: int) -> int:
     """32-bit words of the exchange area (decode.hip ``xlayout``): per layer the input row, each
-    query head's q row with its KV head's k and v rows, the attention partials (o[D] plus m and l as four half-words per split and
-    head), the combined attention row, the o_proj output and the SiLU * up row; then the final
-    row, one 64-bit argmax key per workgroup and two control words (step tag, timeout flag)."""
+    query head's q row with its KV head's k and v rows, the attention partials (o[D] plus m and l
+    as four half-words per slot and head), the combined attention row, the o_proj output and the
+    SiLU * up row; then the final row, one 64-bit argmax key per workgroup and two control words
+    (step tag, timeout flag)."""
     stride = hidden + H * 3 * D + H * nsplit * (D + 4) + H * D + hidden + inter
     stride += stride & 1
     return stride * L + hidden + 2 * NWG + 2
@@ -62,22 +147,34 @@ def _same(a, b) -> bool:
     return isinstance(a, Ref) and isinstance(b, Ref) and a == b
 
 
+def slots_for(S: int, hidden: int, inter: int, H: int) -> tuple[int, dict] | None:
+    """Attention slots per query head for an S-position cache (as many as fit, up to MAX_SLOTS and
+    one per chunk) with their work split, or None."""
+    nchunk = -(-S // SPL)
+    for nslot in range(min(nchunk, MAX_SLOTS), 0, -1):
+        if -(-nchunk // nslot) > MAX_CHUNKS_PER_SLOT:
+            return None
+        ws = work_split(hidden, inter, H, nslot)
+        if ws is not None:
+            return nslot, ws
+    return None
+
+
 def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> list[LaunchStep] | None:
-    """The one-launch form of ``steps``, or None when they are not a decode step it covers."""
+    """The one-launch form of ``steps``, or None when they are not a decode step it covers (or the
+    device cannot hold all of its workgroups at once)."""
     n = len(steps)
-    if n < 8 or (n - 3) % 5 != 0:
+    if n < 8:
         return None
-    L = (n - 3) // 5
     emb, lm, fin = steps[0], steps[-2], steps[-1]
     if emb.kernel != "k_embedding" or lm.kernel != "k_gemv_norm_argmax_r4" or fin.kernel != "k_argmax_finalize":
         return None
-    layers = [steps[1 + 5 * i: 6 + 5 * i] for i in range(L)]
-    for q, f, o, g, d in layers:
-        if (q.kernel not in QKV or f.kernel not in FLASH or o.kernel not in OPROJ or
-                g.kernel != "k_gemv_norm_silu_r1" or d.kernel not in DOWN):
-            return None
+    layers = _parse_layers(steps)
+    if layers is None:
+        return None
+    L = len(layers)
     ea, la, fa = emb.args, lm.args, fin.args
-    q0, f0, g0 = layers[0][0].args, layers[0][1].args, layers[0][3].args
+    q0, f0, g0 = layers[0][0].args, layers[0][1].args, layers[0][4].args
     hidden, H, KVH = int(q0["K"]), int(q0["H"]), int(q0["KVH"])
     inter, vocab, S = int(g0["N"]), int(la["N"]), int(f0["S"])
     if int(ea["n_ids"]) != 1 or int(ea["row_bytes"]) != 2 * hidden or int(ea["vocab"]) != vocab:
@@ -87,34 +184,26 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     KC = hidden // 512
     if H % KVH or H // KVH > MAX_G or inter % 8 or inter > 4096 * KC or (H + 2 * KVH) * D > 8 * NWG:
         return None
-    # attention runs one workgroup per (query head, split), the combine one per query head
-    if S % SPL or S // SPL > MAX_SPLITS or H * (S // SPL) + H > NWG or vocab >= 2 ** 32:
+    if vocab >= 2 ** 32:
         return None
-    nsplit = S // SPL
-    # the work split of decode.hip: NB attention workgroups (each also holds NE gate/up rows in
-    # LDS), ND o_proj workgroups of RD rows (those that run no combine also hold NEO gate/up rows
-    # in LDS); an o_proj workgroup streams RBO gate/up rows, an attention workgroup RBA
-    NB, NE = H * nsplit, E_LDS_ROWS[KC]
-    ND = NWG - NB
-    RD = -(-hidden // ND)
-    NEO = max(2 * NE - RD, 0) // 2
-    ring = max(inter - NB * NE - (ND - H) * NEO, 0)
-    RBO = min(-(-ring // NWG), O_RING_MAX)
-    RBA = -(-max(ring - ND * RBO, 0) // NB)
-    RB = max(RBA, RBO)
-    em = [e for e in RING_ROWS[KC] if 8 * e >= RB]
-    if RD > 2 * NE or not em or NE + RB > 128:   # decode.hip DEC_OSTAGE: a workgroup's rows, staged
+    sl = slots_for(S, hidden, inter, H)
+    if sl is None:
         return None
-    if nsplit * (D + 4) * 2 > 8192 * KC:   # the combine stages a head's partials in LDS
-        return None
+    nsplit, ws = sl
     shared = ("pos_ids", "cache_pos", "inv_freq")
     x = ea["out"]
     table: list = []
-    for q, f, o, g, d in layers:
+    for q, f, c, o, g, d in layers:
         qa, fl, oa, ga, da = q.args, f.args, o.args, g.args, d.args
+        if c is None:
+            attn_ok = _same(oa["attn_o"], fl["part_o"])
+        else:
+            ca = c.args
+            attn_ok = (_same(ca["part_o"], fl["part_o"]) and _same(ca["part_ml"], fl["part_ml"])
+                       and _same(oa["x"], ca["out"]) and oa.get("bias") is None)
         ok = (
-            _same(qa["x"], x) and _same(fl["q"], qa["q_out"]) and _same(fl["k"], qa["k_dst"])
-            and _same(fl["v"], qa["v_dst"]) and _same(oa["resid"], x) and _same(oa["attn_o"], fl["part_o"])
+            attn_ok and _same(qa["x"], x) and _same(fl["q"], qa["q_out"]) and _same(fl["k"], qa["k_dst"])
+            and _same(fl["v"], qa["v_dst"]) and _same(oa["resid"], x)
             and _same(ga["x"], oa["out"]) and _same(da["x"], ga["out"]) and _same(da["resid"], oa["out"])
             and all(_same(qa[k], q0[k]) for k in shared)
             and (int(qa["flags"]) | 2) == 63 and int(qa["flags"]) & 2 == int(q0["flags"]) & 2
@@ -145,6 +234,15 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
             and int(fa["out_dtype"]) in (DTYPE_CODE["int64"], DTYPE_CODE["int32"])
             and int(la["n_dtype"]) == int(q0["n_dtype"])):
         return None
+    # the table holds graph inputs (caches) and weights only: the executor resolves it per set of
+    # bound buffers, and arena storages get no offset of their own for it
+    for r in table:
+        if r is not None and storages[r.storage].kind not in ("input", "weight"):
+            return None
+    kernel = f"k_decode_step_k{KC}_i{KC}_e{ws['EM']}"
+    fit = resident_workgroups(kernel)
+    if fit is not None and fit < NWG:
+        return None
     words = exchange_words(L, hidden, inter, H, KVH, nsplit)
     xname = "decode_step.exchange"
     storages[xname] = Storage(xname, "persistent", words * 4, "uint8", zero_init=True)
@@ -158,12 +256,12 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
         mask_dtype=int(f0["mask_dtype"]) if mask is not None else -1, add_dtype=int(f0.get("add_dtype", 2)),
         n_dtype=int(q0["n_dtype"]), out_dtype=int(fa["out_dtype"]), flags=1 if int(q0["flags"]) & 2 else 0,
         eps=float(q0["eps"]), eps_f=float(la["eps"]), scale=float(f0["scale"]),
-        rope_scaling=float(q0["rope_scaling"]))
+        rope_scaling=float(q0["rope_scaling"]), nchunk=-(-S // SPL), rbo=ws["RBO"], rba=ws["RBA"])
     inputs = sorted({t for st in steps for t in st.inputs})
     outputs = [t for st in steps for t in st.outputs]
     step = LaunchStep(
-        kind="decode_step", kernel=f"k_decode_step_k{KC}_i{KC}_e{em[0]}", module="decode", arg_struct="PersistArgs",
+        kind="decode_step", kernel=kernel, module="decode", arg_struct="PersistArgs",
         args=args, grid=(NWG, 1, 1), block=(THREADS, 1, 1), inputs=inputs, outputs=outputs,
         params={"table": {"field": "layers", "entries": table}, "layers": L, "nsplit": nsplit,
-                "replaces": [st.kernel for st in steps], "exchange_words": words})
+                "replaces": [st.kernel for st in steps], "exchange_words": words, "work_split": ws})
     return [step]

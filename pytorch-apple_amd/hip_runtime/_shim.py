@@ -59,6 +59,9 @@ _SIGS = {
     "hs_argmax_rows": ([C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p],
                        C.c_int),
     "hs_argmax_rows_noalloc": ([C.c_void_p, C.c_int, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "hs_device_cus": ([C.POINTER(C.c_int)], C.c_int),
+    "hs_occupancy": ([C.c_void_p, C.c_uint32, C.c_size_t, C.POINTER(C.c_int)], C.c_int),
+    "hs_host_alloc_mapped": ([C.c_size_t, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)], C.c_int),
     "hs_argsize": ([C.c_char_p], C.c_size_t),
 }
 EXPORTED = tuple(_SIGS)

@@ -51,6 +51,43 @@ def module_cache(device_index: int) -> ModuleCache:
     return mc
 
 
+def resident_workgroups(device_index: int, module: str, kernel: str, threads: int, lds: int = 0) -> int:
+    """How many workgroups of ``kernel`` (``threads`` threads, ``lds`` bytes of dynamic LDS) the
+    device holds at once: its CU count times the kernel's workgroups per CU."""
+    lib = _shim.lib()
+    with torch.cuda.device(device_index):
+        mc = module_cache(device_index)
+        mc.ensure_builtin(module)
+        fn = mc.function(module, kernel)
+        cus, per = C.c_int(), C.c_int()
+        _shim.check(lib.hs_device_cus(C.byref(cus)), "device CU count")
+        _shim.check(lib.hs_occupancy(fn, threads, lds, C.byref(per)), f"occupancy of {kernel}")
+    return cus.value * per.value
+
+
+class _HostFlags:
+    """Host-visible 32-bit words that kernels set on failure (one per executor that needs one),
+    carved out of pinned, coherent, device-mapped pages that are never freed."""
+    PAGE = 4096
+
+    def __init__(self):
+        self._host = self._dev = 0
+        self._next = self.PAGE
+
+    def take(self) -> tuple[C.c_int, int]:
+        """(host view of the word, its device address)."""
+        if self._next + 4 > self.PAGE:
+            h, d = C.c_void_p(), C.c_void_p()
+            _shim.check(_shim.lib().hs_host_alloc_mapped(self.PAGE, C.byref(h), C.byref(d)), "host flag page")
+            self._host, self._dev, self._next = h.value, d.value, 0
+        off = self._next
+        self._next += 4
+        return C.c_int.from_address(self._host + off), self._dev + off
+
+
+_HOST_FLAGS: dict[int, _HostFlags] = {}
+
+
 class HIPExecutor:
     def __init__(self, program: HIPProgram, backend=None, use_graph: bool | None = None):
         self.program = program
@@ -109,7 +146,21 @@ class HIPExecutor:
         self._in_cache: OrderedDict[tuple, tuple] = OrderedDict()
         self._graphs: OrderedDict[tuple, int] = OrderedDict()   # (pointer set, advance) -> captured graph
         self._adv_ptr = 0                         # flag word of a decode advance folded into the launch
+        self._adv_bufs: tuple = ()                # its (mask, position, cache position, mask bytes)
         self._capture_stream = None
+        # a persistent decode step: every workgroup must be resident at once, and its timeout flag
+        # is mirrored into host memory, read on every launch without a synchronisation
+        self._hflag = None
+        for st, s in zip(program.steps, self._structs):
+            if st.kind != "decode_step":
+                continue
+            need = int(st.grid[0])
+            fit = resident_workgroups(self.device.index or 0, st.module, st.kernel, int(st.block[0]), int(st.lds))
+            if fit < need:
+                raise RuntimeError(f"persistent decode step {st.kernel} needs {need} workgroups resident at once; "
+                                   f"this device holds {fit} (compile with persistent=False, or HIPRT_PERSISTENT=0)")
+            flags = _HOST_FLAGS.setdefault(self.device.index or 0, _HostFlags())
+            self._hflag, s.host_err = flags.take()
         self._out_cache: dict[str, HIPBuffer] = {}
         for spec in program.output_specs:
             v = program.output_views[spec.name]
@@ -241,7 +292,12 @@ class HIPExecutor:
         return dict(zip(self._w_names, key[0])) | dict(zip(self._in_names, key[1]))
 
     def launch(self, inputs: dict, weights: dict, stream: int | None = None) -> None:
-        """Enqueue the whole program on ``stream`` (default: torch's current stream)."""
+        """Enqueue the whole program on ``stream`` (default: torch's current stream). Raises
+        ``RuntimeError`` first when an earlier persistent decode step of this executor reported a
+        timeout (its host-visible flag; no synchronisation needed)."""
+        if self._hflag is not None and self._hflag.value:
+            self._hflag.value = 0
+            raise RuntimeError(_TIMEOUT_MSG)
         key = self._pointer_key(inputs, weights)
         if stream is None:
             stream = _current_stream(self.device)
@@ -256,6 +312,8 @@ class HIPExecutor:
             if key != self._ext_key:
                 self._patch(self._ptrs_of(key), key)
                 self._ext_key = key
+            if self._adv_ptr:
+                self._check_advance(key, self._adv_bufs)
             if not self.use_graph:
                 _shim.check(lib.hs_replay(self._recs, self._n, stream), "replay")
                 return
@@ -273,6 +331,22 @@ class HIPExecutor:
                     self._table_bufs.pop(old_key, None)
         _shim.check(lib.hs_graph_launch(graph, stream), "graph launch")
 
+    def _check_advance(self, key: tuple, bufs: tuple) -> None:
+        """A folded advance moves the buffers this launch reads as its mask and positions, with the
+        mask's element size: anything else would move other buffers, or write 2-byte zeros into
+        a 4-byte mask."""
+        args = self.program.steps[0].args
+        ptrs = self._ptrs_of(key)
+        mask, pos, cpos, mbytes = bufs
+        want = {"mask": mask, "pos_ids": pos, "cache_pos": cpos}
+        for field, ptr in want.items():
+            ref = args[field]
+            got = None if ref is None else ptrs.get(ref.storage, -1) + ref.byte_offset
+            if got != ptr:
+                raise ValueError(f"the folded decode advance moves another buffer than the step's {field}")
+        if mbytes != {0: 4, 2: 2}.get(int(args["mask_dtype"]), -1):
+            raise ValueError("the folded decode advance's mask element size differs from the step's mask")
+
     def fold_advance(self, advance: "DecodeAdvance | None") -> bool:
         """Fold ``advance`` into this program's launch: a persistent decode step then moves its
         loop's position inputs to the next step itself, after its argmax (no second launch, and
@@ -289,27 +363,32 @@ class HIPExecutor:
             self._adv_ptr = 0
         else:
             a = advance._args
-            s.adv_mask, s.adv_pos, s.adv_cpos, s.adv_flag = a.mask, a.pos, a.cpos, a.overflow
-            s.adv_mask_bytes = a.mask_bytes
             if int(a.S) != int(self.program.steps[0].args["S"]):
                 raise ValueError("the advance's mask length differs from the step's cache length")
+            bufs = (int(a.mask), int(a.pos), int(a.cpos), int(a.mask_bytes))   # checked at launch
+            s.adv_mask, s.adv_pos, s.adv_cpos, s.adv_flag = a.mask, a.pos, a.cpos, a.overflow
+            s.adv_mask_bytes = a.mask_bytes
             self._adv_ptr = int(a.overflow)
+            self._adv_bufs = bufs
         return True
 
     def check(self) -> None:
         """Raise ``RuntimeError`` if a persistent decode step has recorded a timeout (one of its
         workgroups waited past its time limit for data from another: its results are not valid).
-        Synchronises with the device; clears the flag."""
+        Synchronises with the device; clears the flags."""
         for st in self.program.steps:
             if st.kind != "decode_step":
                 continue
             xs = self.program.storages[st.args["ll"].storage]
             off = xs.offset + (int(st.params["exchange_words"]) - 1) * 4
             flag = self.arena[off:off + 4].view(torch.int32)
-            if int(flag.item()):
+            dev = int(flag.item())
+            host = self._hflag is not None and self._hflag.value
+            if dev or host:
                 flag.zero_()
-                raise RuntimeError("persistent decode step: a workgroup timed out waiting for another's data; "
-                                   "the step's outputs are not valid (are all of its workgroups resident?)")
+                if self._hflag is not None:
+                    self._hflag.value = 0
+                raise RuntimeError(_TIMEOUT_MSG)
 
     def run(self, inputs: dict, weights: dict) -> dict[str, HIPBuffer]:
         self.launch(inputs, weights)
@@ -337,6 +416,11 @@ class HIPExecutor:
                 lib.hs_stream_destroy(self._capture_stream)
         except Exception:
             pass
+
+
+_TIMEOUT_MSG = ("persistent decode step: a workgroup timed out waiting for another's data, so the step's "
+                "outputs are not valid (the step needs every one of its workgroups resident at once: "
+                "is another kernel sharing the GPU?)")
 
 
 def _table_refs(step):

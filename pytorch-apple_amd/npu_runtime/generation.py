@@ -264,6 +264,14 @@ class GreedyGenerator:
             self.backend.synchronize()
             if b.get("advance") is not None:
                 b["advance"].check()
+        # a persistent decode step that timed out waiting for data (not all of its workgroups
+        # resident) produced invalid tokens: raise rather than return them
+        for dag in (self.prefill, self.decode):
+            for ex in getattr(dag, "npu_executors", {}).values():
+                check = getattr(ex, "check", None)
+                if check is not None:
+                    check()
+        if fast:
             got = hist[:steps].cpu().tolist()
             if eos_token_id is not None and eos_token_id in got:
                 got = got[:got.index(eos_token_id)]

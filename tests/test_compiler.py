@@ -82,9 +82,10 @@ def test_attention_block_is_three_launches_with_inplace_cache():
     sep = compile_subgraph(build_attention_ir(1025), fold_attention=False)
     assert kernels(sep) == ["k_qkv_rope_k1536", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
     assert sep.steps[1].args["nsplit"] == 17
-    # more than 16 splits of 256 do not fit the prologue: the separate combine is kept
+    # more than 16 splits of 256 do not fit the prologue: the separate combine is kept, and
+    # beyond 32 splits each split checks its mask before reading K / V
     long = compile_subgraph(build_attention_ir(4097))
-    assert kernels(long) == ["k_qkv_rope_k1536", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
+    assert kernels(long) == ["k_qkv_rope_k1536", "k_attn_flash_chk", "k_attn_combine", "k_gemv_bias_r1"]
     assert set(p.stats["mutated_inputs"]) == {"past_key_0", "past_value_0"}
     assert p.output_views["index_copy"].storage == "past_key_0"
     exact = compile_subgraph(build_attention_ir(1025), exact_attention=True)
@@ -312,3 +313,50 @@ def test_decode_step_becomes_one_persistent_launch():
     assert len(compile_subgraph(ir, fuse=False).steps) > 20
     pre = compile_subgraph(build_decode_ir(64, QwenConfig(layers=1), argmax=True, tokens=64))
     assert not any(s.kind == "decode_step" for s in pre.steps)
+
+
+def test_persistent_step_needs_every_workgroup_resident(monkeypatch):
+    """A device that holds fewer than the step's 256 workgroups at once keeps the launch list
+    (the step's workgroups wait for each other's data)."""
+    import hip_compiler.persistent as P
+    from hip_compiler import compile_subgraph
+    from irgen.qwen import QwenConfig, build_decode_ir
+
+    ir = build_decode_ir(2048, QwenConfig(layers=2), argmax=True)
+    monkeypatch.setattr(P, "resident_workgroups", lambda kernel: 128)
+    assert len(compile_subgraph(ir).steps) > 1
+    monkeypatch.setattr(P, "resident_workgroups", lambda kernel: 256)
+    assert [s.kind for s in compile_subgraph(ir).steps] == ["decode_step"]
+
+
+@pytest.mark.parametrize("S", [128, 1000, 2048, 2176, 4096, 32768, 65536])
+def test_persistent_step_covers_long_and_ragged_caches(S):
+    """One launch for caches up to 32 chunks per slot; the work split covers every gate/up row
+    exactly once (the kernel's e0 / ecnt arithmetic) and fits the kernel's LDS staging."""
+    import hip_compiler.persistent as P
+    from hip_compiler import compile_subgraph
+    from irgen.qwen import QwenConfig, build_decode_ir
+
+    cfg = QwenConfig(layers=1)
+    prog = compile_subgraph(build_decode_ir(S, cfg, argmax=True))
+    (st,) = prog.steps
+    ws, ns = st.params["work_split"], st.params["nsplit"]
+    assert st.args["nchunk"] == -(-S // 128) and -(-st.args["nchunk"] // ns) <= 32
+    NB, ND, NE, NEO, H = ws["NB"], ws["ND"], ws["NE"], ws["NEO"], cfg.heads
+    rows = []
+    for b in range(P.NWG):
+        att, comb = b < NB, NB <= b < NB + H
+        e0 = b * (NE + ws["RBA"]) if att else NB * (NE + ws["RBA"]) + (b - NB) * ws["RBO"] + max(b - NB - H, 0) * NEO
+        nlc = NE if att else (0 if comb else NEO)
+        ecnt = max(min(nlc + (ws["RBA"] if att else ws["RBO"]), cfg.intermediate - e0), 0)
+        rows += range(e0, e0 + ecnt)
+        assert ecnt - min(nlc, ecnt) <= 8 * ws["EM"]
+    assert sorted(rows) == list(range(cfg.intermediate))
+
+
+def test_persistent_step_rejects_caches_past_its_chunk_word():
+    from hip_compiler import compile_subgraph
+    from irgen.qwen import QwenConfig, build_decode_ir
+
+    prog = compile_subgraph(build_decode_ir(65536 + 128, QwenConfig(layers=1), argmax=True))
+    assert len(prog.steps) > 1

@@ -165,6 +165,34 @@ def test_generation_on_hip_follows_hf_teacher_forced(hf, backend):
     assert cut.tokens == res.tokens[:res.tokens.index(eos)]
 
 
+def test_generator_raises_when_the_decode_step_timed_out(hf, backend):
+    """A persistent decode step's timeout word (set from the host, as a timed-out workgroup sets
+    it) makes GreedyGenerator.generate raise instead of returning the step's tokens."""
+    import torch as _t
+
+    from irgen.hf_qwen import export_qwen, kv_mapping
+    from npu_runtime.generation import GreedyGenerator
+
+    m, d = hf
+    T = 32
+    pre = export_qwen(m, S, tokens=T, argmax=True)
+    dec = export_qwen(m, S, tokens=1, argmax=True)
+    dex = hip_executor(dec, d, backend)
+    gen = GreedyGenerator(hip_executor(pre, d, backend), dex, kv_mapping(pre, dec, 2, T, S), pre, dec,
+                          backend=backend)
+    (h,) = dex.npu_executors.values()
+    assert h.program.steps[0].kind == "decode_step"
+    prompt = [3, 14, 15, 92, 65]
+    print("[case] generator timeout report", flush=True)
+    ok = gen.generate(prompt, 4)
+    st = h.program.steps[0]
+    off = h.program.storages[st.args["ll"].storage].offset + (int(st.params["exchange_words"]) - 1) * 4
+    h.arena[off:off + 4].view(_t.int32).fill_(1)
+    with pytest.raises(RuntimeError, match="timed out"):
+        gen.generate(prompt, 4)
+    assert gen.generate(prompt, 4).tokens == ok.tokens   # cleared by the report
+
+
 def test_program_from_hipbin_runs_bit_identical(backend, tmp_path):
     """A decode program written to and read back from a ``.hipbin`` file produces the same
     bits as the freshly compiled one, and matches the CPU fallback (ATen) on the same

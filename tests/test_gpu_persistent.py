@@ -75,6 +75,15 @@ CASES = {
     "mini_s256_last": (dict(hidden=512, intermediate=1024, layers=3, heads=4, kv_heads=2, head_dim=128, vocab=4096), 256, 255),
     "real_dims_2l": (dict(layers=2), 2048, 1984),
     "real_dims_pos0": (dict(layers=1), 2048, 0),
+    # attention slots whose every chunk is closed (positions 0..100 open: slot 0 only)
+    "real_dims_pos100": (dict(layers=1), 2048, 100),
+    # a cache that is not a multiple of the 128-position chunk (the last chunk is partial)
+    "real_s1000_last": (dict(layers=1), 1000, 999),
+    # 32 chunks over 16 slots: every slot folds two chunks
+    "real_s4096_pos4000": (dict(layers=2), 4096, 4000),
+    # the reference's benchmark cache length: 17 open chunks of 256 (slot 0 folds two)
+    "real_s32768_pos2048": (dict(layers=2), 32768, 2048),
+    "real_s128": (dict(layers=1), 128, 77),
 }
 
 
@@ -260,3 +269,58 @@ def test_executor_sees_a_weight_replaced_in_its_dict_and_alternating_inputs(back
     ref = logits(fresh, xa)
     assert np.array_equal(got, ref)
     assert not np.array_equal(got, la)
+
+
+def test_persistent_step_reads_chunks_the_mask_opens_beyond_the_position(backend):
+    """A mask that also opens positions far past cache_position (chunks other slots hold, and a
+    chunk of slot 0's second round): those chunks are read and weigh in as on the CPU."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(layers=1)
+    S, pos = 32768, 1500
+    ir = build_decode_ir(S, cfg, argmax=True)
+    w = _host(make_weights(ir, cfg, device="cuda"))
+    xt = decode_inputs(S, pos, cfg)
+    m = xt["attention_mask"]
+    for p in (2048, 2100, 20000, 31000, 32767):   # chunk 16 (slot 0, round 2), 156, 242, 255
+        m[..., p] = 0.0
+    x = _host(xt)
+    print("[case] persistent decode step, S 32768, open positions past cache_position", flush=True)
+    ex = _executor(ir, backend, True)
+    ex.load_weights(w)
+    o = ex.execute({k: v.copy() for k, v in x.items()})
+    _hexec(ex).check()
+    got = {k: (v if isinstance(v, np.ndarray) else v.to_numpy()) for k, v in o.items()}
+    ref = _cpu(ir, x, w)
+    lg = ir["graph_outputs"][0]["name"]
+    _close(got[lg], ref[lg])
+    assert int(np.asarray(got["next_token"]).reshape(-1)[0]) == int(np.argmax(_f32(ref[lg]).reshape(-1)))
+
+
+def test_timeout_flags_raise_on_the_product_path(backend):
+    """The step's timeout words, set from the host after a normal step as a timed-out workgroup
+    would set them: the host-visible word makes the next execute() raise before launching, the
+    device word makes check() raise; both are cleared by the report."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(hidden=512, intermediate=1024, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=4096)
+    ir = build_decode_ir(128, cfg, argmax=True)
+    ex = _executor(ir, backend, True)
+    ex.load_weights(_host(make_weights(ir, cfg, device="cuda")))
+    x = _host(decode_inputs(128, 10, cfg))
+    print("[case] timeout flags", flush=True)
+    ex.execute({k: v.copy() for k, v in x.items()})
+    h = _hexec(ex)
+    h.check()
+    h._hflag.value = 1
+    with pytest.raises(RuntimeError, match="timed out"):
+        ex.execute({k: v.copy() for k, v in x.items()})
+    ex.execute({k: v.copy() for k, v in x.items()})   # reported once, then cleared
+    st = h.program.steps[0]
+    off = h.program.storages[st.args["ll"].storage].offset + (int(st.params["exchange_words"]) - 1) * 4
+    h.arena[off:off + 4].view(torch.int32).fill_(1)
+    with pytest.raises(RuntimeError, match="timed out"):
+        h.check()
+    h.check()
