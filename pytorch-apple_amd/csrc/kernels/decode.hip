@@ -51,8 +51,12 @@
 #ifndef DEC_ED
 #define DEC_ED 3                      // gate/up rows in flight per wave (2: 0.780 ms, 3: 0.766 ms per step)
 #endif
+// down_proj rows per workgroup issued as soon as x1 is in (before the gate / up arithmetic), of
+// its 2 KC: they land while E computes, so F streams fewer bytes after the SiLU * up row is out.
+// 0.714 -> 0.690 ms per step with 2 (1: 0.695, 3: 0.700, 4: 0.705, 6: 0.721: the h stores queue
+// behind the later ones)
 #ifndef DEC_RFE
-#define DEC_RFE 0                     // down_proj rows per workgroup issued before the gate / up arithmetic (1-4: no faster)
+#define DEC_RFE 2
 #endif
 #ifndef DEC_R4
 #define DEC_R4 2                      // lm_head rows per wave in each of its two rounds in flight
@@ -773,7 +777,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     // between the loads would sit in the same in-order completion count.
     // down_proj rows of F (rows b * RB + j): the first RFE are issued as soon as x1 is in, when
     // every load this workgroup issued before has landed, so they arrive during the gate / up
-    // arithmetic; the rest follow the h stores
+    // arithmetic (more of them would hold back the h stores behind them); the rest follow the
+    // h stores
     uint4 fw[RF][IC];
     auto load_down = [&](int j) {
       const int RB = (hid + NWG - 1) / NWG, K8 = a.inter >> 3, wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
@@ -880,8 +885,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       const int K8 = a.inter >> 3;
       uint16_t* hs = (uint16_t*)ebuf;   // (this layer's gate / up and o_proj rows are consumed)
       __syncthreads();
-      // the weights are issued only now: a CU's memory requests complete in order, so loads issued
-      // before the h stores would hold those stores back, and with them every workgroup's F
+      // the other weights are issued only now: a CU's memory requests complete in order, so loads
+      // issued before the h stores would hold those stores back, and with them every workgroup's F
 #pragma unroll
       for (int j = RFE; j < RF; ++j) load_down(j);
       DEC_STAMP(l, 13);
