@@ -51,12 +51,17 @@
 #ifndef DEC_ED
 #define DEC_ED 3                      // gate/up rows in flight per wave (2: 0.780 ms, 3: 0.766 ms per step)
 #endif
-// down_proj rows per workgroup issued as soon as x1 is in (before the gate / up arithmetic), of
-// its 2 KC: they land while E computes, so F streams fewer bytes after the SiLU * up row is out.
-// 0.714 -> 0.690 ms per step with 2 (1: 0.695, 3: 0.700, 4: 0.705, 6: 0.721: the h stores queue
-// behind the later ones)
+// down_proj rows per workgroup issued while E computes, of its 2 KC: they land before the h
+// stores, so F streams fewer bytes after the SiLU * up row is out. DEC_RFE_N of them are issued
+// once x1 is normalised, the rest once the LDS rows are summed (issuing a wave's loads stalls it
+// while the memory pipe is full, so they are spread over E). 0.714 -> 0.690 ms per step with 2
+// issued as soon as x1 is in (1: 0.695, 3: 0.700, 4: 0.705, 6: 0.721: the h stores queue behind
+// the later ones); 0.681 with 1 + 1 (2 + 1: 0.683, 2 + 2: 0.692, 2 + 0: 0.690, 0 + 2: 0.686)
 #ifndef DEC_RFE
 #define DEC_RFE 2
+#endif
+#ifndef DEC_RFE_N
+#define DEC_RFE_N 1
 #endif
 #ifndef DEC_R4
 #define DEC_R4 2                      // lm_head rows per wave in each of its two rounds in flight
@@ -775,8 +780,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     // re-reads its last one), so no loaded value flows through a branch join, which would make the
     // compiler wait for every load in flight. Results are published after the last row: a store
     // between the loads would sit in the same in-order completion count.
-    // down_proj rows of F (rows b * RB + j): the first RFE are issued as soon as x1 is in, when
-    // every load this workgroup issued before has landed, so they arrive during the gate / up
+    // down_proj rows of F (rows b * RB + j): the first RFE are issued during E, after x1 is in,
+    // when every load this workgroup issued before has landed, so they arrive during the gate / up
     // arithmetic (more of them would hold back the h stores behind them); the rest follow the
     // h stores
     uint4 fw[RF][IC];
@@ -803,9 +808,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       DEC_STAMP(l, 10);
       xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, a.host_err, tid);
       DEC_STAMP(l, 11);
-#pragma unroll
-      for (int j = 0; j < RFE; ++j) load_down(j);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
+#pragma unroll
+      for (int j = 0; j < (RFE < DEC_RFE_N ? RFE : DEC_RFE_N); ++j) load_down(j);
       uint4 xv[KC];
 #pragma unroll
       for (int c = 0; c < KC; ++c) xv[c] = *(const uint4*)(xs + c * 512 + lane * 8);
@@ -837,6 +842,8 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
           us[k] = i < NL ? u : 0.f;
         }
       }
+#pragma unroll
+      for (int j = DEC_RFE_N; j < RFE; ++j) load_down(j);
 #pragma unroll
       for (int k = 0; k < EM; ++k) {
         const int d = k % EP;
