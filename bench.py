@@ -410,9 +410,12 @@ def main() -> int:
 
     kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
     kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
-    masks = [decode_mask(S, p).to(dev) for p in range(start, S)]
-    pos_ids = [torch.tensor([[p]], dtype=torch.int64, device=dev) for p in range(start, S)]
-    cpos = [torch.tensor([p], dtype=torch.int64, device=dev) for p in range(start, S)]
+    # the positions the runs below visit (not the whole cache: at 32k positions that would be 2 GB
+    # of masks)
+    window = range(start, min(S, start + max(args.steps, args.warmup, args.cpu_steps) + 1))
+    masks = [decode_mask(S, p).to(dev) for p in window]
+    pos_ids = [torch.tensor([[p]], dtype=torch.int64, device=dev) for p in window]
+    cpos = [torch.tensor([p], dtype=torch.int64, device=dev) for p in window]
     from hip_runtime import HIPBuffer
 
     state = {k: backend.allocate_buffer(v) for k, v in x0.items()}

@@ -324,3 +324,37 @@ def test_timeout_flags_raise_on_the_product_path(backend):
     with pytest.raises(RuntimeError, match="timed out"):
         h.check()
     h.check()
+
+
+@pytest.mark.parametrize("persistent", [True, False])
+def test_rotary_attention_scaling_on_the_device(backend, persistent):
+    """A rotary node with ``attention_scaling`` (0.5): the kernels scale their cos / sin the way the
+    CPU fallback does (k_qkv_rope in the launch list, the persistent step's rotary factors)."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(layers=2)
+    S, pos = 2048, 1500
+    ir = build_decode_ir(S, cfg, argmax=True)
+    rot = [n for n in ir["nodes"] if n["op_type"] == "wrap_with_set_grad_enabled"]
+    assert rot
+    for n in rot:
+        n.setdefault("attrs", {})["attention_scaling"] = 0.5
+    w = _host(make_weights(ir, cfg, device="cuda"))
+    x = _host(decode_inputs(S, pos, cfg))
+    print(f"[case] rotary attention_scaling, persistent={persistent}", flush=True)
+    ex = _executor(ir, backend, persistent)
+    (prog,) = ex.npu_programs.values()
+    assert any(float(st.args.get("rope_scaling", 1.0)) == 0.5 for st in prog.steps)
+    ex.load_weights(w)
+    o = ex.execute({k: v.copy() for k, v in x.items()})
+    _hexec(ex).check()
+    got = {k: (v if isinstance(v, np.ndarray) else v.to_numpy()) for k, v in o.items()}
+    ref = _cpu(ir, x, w)
+    plain = _cpu(build_decode_ir(S, cfg, argmax=True), x, w)
+    lg = ir["graph_outputs"][0]["name"]
+    _close(got[lg], ref[lg])
+    for o_ in ir["graph_outputs"][1:-1]:   # the K rows written carry the scaled rotation
+        _close(np.asarray(got[o_["name"]])[:, :, pos], np.asarray(ref[o_["name"]])[:, :, pos])
+    k0 = ir["graph_outputs"][1]["name"]
+    assert not np.array_equal(np.asarray(ref[k0])[:, :, pos], np.asarray(plain[k0])[:, :, pos])

@@ -61,6 +61,44 @@ def test_rope_tables_closed_form():
     assert np.allclose(c[0], 1.0) and np.allclose(s[0], 0.0)
 
 
+def test_rotary_node_attention_scaling_branch():
+    """The rotary node's ``attention_scaling`` (transformers' dynamic / YaRN rope types scale cos
+    and sin): the oracle's branch against the closed form evaluated in float64 and rounded once
+    (at most one bf16 ulp apart: the float32 cos/sin may differ from float64 in the last fp32
+    ulp) and against the CPU fallback's ATen evaluation; the unscaled tables differ."""
+    import torch
+
+    from npu_runtime.aten_executor import run_node as aten_run_node
+
+    half, sc = 64, 0.7
+    inv = (1.0 / (1e6 ** (np.arange(half, dtype=np.float32) / half))).astype(np.float32)
+    pos = np.array([[0, 5, 1000, 2047, 32767]], dtype=np.int64)
+    node = {"name": "rot", "op_type": "wrap_with_set_grad_enabled",
+            "inputs": [{"name": "inv_freq", "shape": [half], "dtype": "float32"},
+                       {"name": "pos", "shape": [1, 5], "dtype": "int64"}],
+            "outputs": [{"name": "cos", "shape": [1, 5, 2 * half], "dtype": "bfloat16"},
+                        {"name": "sin", "shape": [1, 5, 2 * half], "dtype": "bfloat16"}],
+            "attrs": {"attention_scaling": sc}}
+    env = {"inv_freq": inv, "pos": pos}
+    R.run_node(node, env)
+    # the angle as HF forms it (float32 product), its cos / sin in float64, one rounding
+    f = (pos.reshape(-1)[:, None].astype(np.float32) * inv[None, :]).astype(np.float64)
+    emb = np.concatenate([f, f], 1)
+    for name, fn in (("cos", np.cos), ("sin", np.sin)):
+        got = np.asarray(env[name], np.float32).reshape(5, 2 * half)
+        exp = R.round_to(fn(emb) * sc, "bfloat16").reshape(5, 2 * half)
+        ulp = np.maximum(np.abs(exp) * 2.0 ** -7, 1e-6)
+        assert np.all(np.abs(got - exp) <= ulp), name
+        unscaled = R.round_to(fn(emb), "bfloat16").reshape(5, 2 * half)
+        assert not np.allclose(got, unscaled, atol=1e-3)            # the scaling is applied
+    tenv = {"inv_freq": torch.from_numpy(inv), "pos": torch.from_numpy(pos)}
+    aten_run_node(node, tenv)
+    for name in ("cos", "sin"):
+        a = tenv[name].float().numpy().reshape(5, 2 * half)
+        o = np.asarray(env[name], np.float32).reshape(5, 2 * half)
+        assert np.all(np.abs(a - o) <= np.maximum(np.abs(a) * 2.0 ** -7, 1e-6)), name
+
+
 def _brute_attention(Q, K, V, mask, scale):
     """tests/test_extended_kernels.py:621-640 in float64 (no intermediate rounding)."""
     out = np.zeros(Q.shape)
