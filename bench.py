@@ -327,6 +327,57 @@ def run_copy_probe(device_index: int, stream, mib: int = 512, repeats: int = 3) 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_ctx2048_hbm_traffic.md")
 
 
+STAMP_NAMES = ("A weights issued", "A x in", "A q/k/v published", "B q/k/v in", "B partial published",
+               "C partials in", "C attention row published", "D o_proj rows landed", "D attention row in",
+               "D x1 published", "E register rows issued", "E x1 in", "E h published", "F weights issued",
+               "F h in", "F x published")
+
+
+def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
+    """Per-part timeline of the persistent decode step from its progress stamps (decode.hip
+    DEC_STAMP: thread 0 of each workgroup records the 100 MHz real-time counter at fixed points of
+    each part). Runs ``steps`` steps without a graph (the stamp buffer is an argument the captured
+    graphs do not carry) and reads the last. Per stamp: the median over the workgroups that record
+    it, in µs after the layer's first workgroup has its input row, averaged over layers 2..L-3."""
+    import numpy as np
+    import torch
+
+    (st,) = hexec.program.steps
+    nwg, H, nsplit = int(st.grid[0]), int(st.args["H"]), int(st.args["nsplit"])
+    NB = H * nsplit
+    tr = torch.zeros(nwg * (L * 16 + 8), dtype=torch.int64, device=hexec.device)
+    s = hexec._structs[0]
+    s.trace = tr.data_ptr()
+    hexec.use_graph = False
+    try:
+        for _ in range(steps):
+            ex.execute(state)
+        torch.cuda.synchronize()
+    finally:
+        s.trace = None
+        hexec.use_graph = True
+    t = tr.cpu().numpy().reshape(nwg, L * 16 + 8).astype(np.float64) * 0.01   # 10 ns ticks -> µs
+    t -= t[:, L * 16 + 7].min()
+    b = np.arange(nwg)
+    att, comb = b < NB, (b >= NB) & (b < NB + H)
+    who = {3: att, 4: att, 5: comb, 6: comb, 7: ~att, 8: ~att, 9: ~att}
+    layers = range(2, L - 2)
+    med = {}
+    for k, name in enumerate(STAMP_NAMES):
+        vals = []
+        for l in layers:
+            v = t[:, l * 16 + k] - t[:, l * 16 + 1].min()
+            vals.append(np.median(v[who.get(k, np.ones(nwg, bool))]))
+        med[name] = round(float(np.mean(vals)), 2)
+    period = float(np.mean([t[:, (l + 1) * 16 + 1].min() - t[:, l * 16 + 1].min() for l in layers]))
+    g_in, g_done = t[:, L * 16 + 1], t[:, L * 16 + 2]
+    return {"layers_averaged": f"2..{L - 3}", "per_part_median_us": med, "layer_period_us": round(period, 2),
+            "first_layer_input_us": round(float(t[:, 1].min()), 2),
+            "lm_head_us": {"median": round(float(np.median(g_done - g_in.min())), 2),
+                           "last": round(float(g_done.max() - g_in.min()), 2)},
+            "kernel_us": round(float(t[0, L * 16 + 3]), 2)}
+
+
 def measured_traffic(kernel: str) -> int | None:
     """HBM bytes per launch of ``kernel`` from the committed FETCH_SIZE / WRITE_SIZE summary
     (lines ``traffic_bytes_per_launch <kernel> <bytes>``), or None when it has no entry."""
@@ -355,6 +406,8 @@ def main() -> int:
     ap.add_argument("--copy-probe-mib", type=int, default=512,
                     help="size of the k_copy calibration launches run after timing (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stamps", action="store_true",
+                    help="decode: add the persistent step's per-part timeline (its progress stamps) to the line")
     ap.add_argument("--no-fp32-parity", action="store_true",
                     help="skip grading the parity pass against a float32 evaluation of the same steps")
     ap.add_argument("--layers", type=int, default=28)
@@ -528,6 +581,10 @@ def main() -> int:
     log(f"dominant {dom}: {avg_ms * 1e3:.2f} us per launch ({achieved:.0f} GB/s); "
         f"{in_step_ms * 1e3:.2f} us with per-launch events inside the step")
     traffic = measured_traffic(dom)
+    stamps = None
+    if args.stamps and program.steps[0].kind == "decode_step":
+        stamps = decode_stamps(hexec, ex, dict(state), cfg.layers)
+        log(f"stamps: {stamps}")
 
     probe = None
     if args.copy_probe_mib > 0:
@@ -614,6 +671,8 @@ def main() -> int:
                           "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu,
     }
+    if stamps is not None:
+        line["stamps"] = stamps
     print(json.dumps(line), flush=True)
     return 0
 
