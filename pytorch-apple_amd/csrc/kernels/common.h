@@ -401,8 +401,13 @@ struct PersistArgs {
   int adv_mask_bytes, adv_pad;
   int nchunk;                 // 128-position chunks of the cache: ceil(S / 128), at most 32 per slot
   int rbo, rba;               // gate / up rows streamed through registers per o_proj / attention workgroup
-  int pad2;
+  int rows;                   // the attention step's o_proj rows per workgroup (unused by the decode step)
   int* host_err;              // null, or a host-visible word set to 1 when a wait times out
+  // the one-block attention step (k_attn_step_k*): its input row, output row and residual row
+  // (null: no residual); unused by the decode step
+  const uint16_t* xin;
+  uint16_t* out;
+  const uint16_t* resid;
 };
 
 struct ArgmaxFinalizeArgs {   // out[m] = index of max over the `parts` keys of row m

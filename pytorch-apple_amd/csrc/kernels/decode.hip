@@ -307,6 +307,243 @@ __device__ __forceinline__ DecodeLayerPtrs dec_layer(const void* const* t) {
   return P;
 }
 
+// The chunks of attention slot `slot`, the same for every layer: bit i stands for chunk
+// slot + nsplit i, set when the mask opens a position of it (every chunk without a mask).
+// Chunks whose positions are all -inf contribute exactly nothing to the softmax, so their K / V
+// rows are never loaded; the loop over the open chunks is bounded by the mask, not by S.
+// Wave w checks half a chunk per round (chunk 4 q + w / 2, positions 64 (w & 1) + lane), all
+// eight rounds' loads issued together. With a mask, each wave's bits go to obw[wave] and the
+// caller ORs them after a barrier (the return value is 0); without one the bits are returned.
+__device__ __forceinline__ uint32_t dec_scan_chunks(const PersistArgs& a, int slot, uint32_t* obw, int lane, int wave) {
+  const int NT = a.nsplit;
+  const long long last = a.S - 1;
+  const int nch = (a.nchunk - slot + NT - 1) / NT;   // chunks of this slot (<= 32, checked on the host)
+  if (a.mask_dtype < 0) return nch >= 32 ? 0xFFFFFFFFu : ((1u << nch) - 1u);
+  FRaw mr[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const long long p = (long long)(slot + NT * (4 * q + (wave >> 1))) * DEC_SPL + 64 * (wave & 1) + lane;
+    mr[q] = ld_f_raw(a.mask, min(p, last), a.mask_dtype);
+  }
+  uint32_t bits = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int i = 4 * q + (wave >> 1);
+    const long long p = (long long)(slot + NT * i) * DEC_SPL + 64 * (wave & 1) + lane;
+    const bool open = i < nch && p <= last && ld_f_decode(mr[q], a.mask_dtype) != -INFINITY;
+    if (__ballot(open) != 0ull) bits |= 1u << i;
+  }
+  if (lane == 0) obw[wave] = bits;
+  return 0u;
+}
+
+// ---- B: attention of one query head over the open chunks (ob) of its slot ---------------------------
+// The first open chunk's K rows and mask values do not depend on this step's activations, so
+// they are issued before B waits for its q / k / v (after A, whose input poll would otherwise
+// wait behind them); its V rows, needed last, are issued once q / k / v are in, so the poll
+// does not wait behind them either and their latency overlaps the scores. Further open chunks
+// (caches longer than 128 nsplit positions) are loaded and folded in one after another: each
+// wave keeps a running (max, sum, unnormalised output) over its 16 positions of every chunk.
+// qkvw: the head's exchange block (q | k | v); partw: the slot's partial; kcache / vcache: the
+// layer's caches (this step's row written by the slot's first head when the slot holds it).
+// VEARLY: the first chunk's V rows are issued with its K rows, before the wait (for a workgroup
+// with no other loads of its own in flight, whose wait would end after they land anyway).
+template <bool VEARLY = false>
+__device__ __forceinline__ void dec_attend(const PersistArgs& a, int l, uint16_t* kcache, uint16_t* vcache,
+                                           const uint32_t* qkvw, uint32_t* partw, uint32_t ob, int kvh, int gq,
+                                           int slot, long long cpos, uint32_t tag, uint32_t* err,
+                                           unsigned char* smem, const float* rope_cs, float* red, float* red2,
+                                           int tid, int lane, int wave) {
+  const int NT = a.nsplit;
+  const long long S = a.S, last = S - 1, kvs = a.kv_head_stride;
+  const int kq = lane >> 2, kc = lane & 3;
+  uint16_t* raw = (uint16_t*)smem;               // [3 * D]: q, k, v as produced
+  const float* csh = rope_cs;                    // [64] cos, [64] sin (rounded, scaled)
+  uint16_t* rot = (uint16_t*)(smem + 1536);      // [2 * D]: rotated q and k
+  float* osh = (float*)(smem + 2048);            // [8][D] per-wave unnormalised outputs
+  const uint16_t* Kb = kcache + (long long)kvh * kvs;
+  const uint16_t* Vb = vcache + (long long)kvh * kvs;
+  const bool cin = cpos >= 0 && cpos < S;
+  float acc0 = 0.f, acc1 = 0.f, mw = -INFINITY, lw = 0.f;
+  auto rope = [&]() {   // rotate_half RoPE: threads 0..63 q, 64..127 k
+    if (tid < 128) {
+      const int hs = tid >> 6, j = tid & 63;
+      const float x0 = bfh(raw[hs * DEC_D + j]), x1 = bfh(raw[hs * DEC_D + j + 64]);
+      const float c = csh[j], sn = csh[64 + j];
+      rot[hs * DEC_D + j] = f32_to_bf16(rb(rb(x0 * c) + rb(-x1 * sn)));
+      rot[hs * DEC_D + j + 64] = f32_to_bf16(rb(rb(x1 * c) + rb(x0 * sn)));
+    }
+    __syncthreads();
+    // this step's K / V row goes into the caches (index_copy at cache_position), by the
+    // first head's workgroup of the slot that holds the position, open or not
+    if (cin && gq == 0 && (int)((cpos / DEC_SPL) % NT) == slot && tid < DEC_D) {
+      stg2(kcache + (long long)kvh * kvs + cpos * DEC_D + tid, rot[DEC_D + tid]);
+      stg2(vcache + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
+    }
+  };
+  // one chunk folded into the wave's running softmax; p0: the wave's first position in it.
+  // The wave holding cache_position uses the new K / V row (V chosen at its use, so no branch
+  // joins the loaded V values, which would make the compiler wait for them there). For the
+  // first chunk (mw = -inf) the rescaling factor is 0 and the result is that of a one-pass
+  // softmax over the chunk.
+  auto fold = [&](const uint4 (&kin)[4], const uint32_t (&vr)[16], FRaw mraw, long long p0) {
+    uint4 kr[4] = {kin[0], kin[1], kin[2], kin[3]};
+    const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
+    const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
+    if (vnew && p0 + kq == cpos) {
+      const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kr[j] = kn[j];
+    }
+    const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
+    const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
+    const bool live = __ballot(mval != -INFINITY) != 0ull;
+    if (live) {
+      const uint4* qq = (const uint4*)(rot + kc * 32);
+      float d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 q4 = qq[j];
+        d = ddot2(q4.x, kr[j].x, d);
+        d = ddot2(q4.y, kr[j].y, d);
+        d = ddot2(q4.z, kr[j].z, d);
+        d = ddot2(q4.w, kr[j].w, d);
+      }
+      d += HS_DPP(d, HS_QUAD_XOR1);
+      d += HS_DPP(d, HS_QUAD_XOR2);
+      float sc = -INFINITY;
+      if (mval != -INFINITY) {
+        sc = rb(d);
+        sc = rb(sc * a.scale);
+        if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
+      }
+      float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
+      m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
+      m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
+      const float mn = fmaxf(mw, m);
+      const float al = (mw == -INFINITY) ? 0.f : __expf(mw - mn);
+      const float e = (sc == -INFINITY) ? 0.f : __expf(sc - mn);
+      float ls = e + HS_DPP(e, HS_ROW_ROR4);
+      ls += HS_DPP(ls, HS_ROW_ROR8);
+      lw = lw * al + ((HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48)));
+      mw = mn;
+      acc0 *= al;
+      acc1 *= al;
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const float p = HS_RL(e, 4 * t);
+        const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
+        acc0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), acc0);
+        acc1 = fmaf(p, bfh((uint16_t)(vt >> 16)), acc1);
+      }
+    }
+  };
+  if (ob != 0) {   // workgroup-uniform
+    uint32_t rest = ob & (ob - 1);
+    const long long q0 = (long long)(slot + NT * __builtin_ctz(ob)) * DEC_SPL + wave * 16;
+    uint4 kr[4];
+    FRaw mraw = {0, 0};
+    if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(q0 + kq, last), a.mask_dtype);
+    const uint4* ks = (const uint4*)(Kb + min(q0 + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
+    uint32_t vr[16];
+    if constexpr (VEARLY) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(q0 + t, last) * DEC_D + 2 * lane);
+    }
+    __syncthreads();
+    xgather<1>(qkvw, 3 * DEC_D, tag, raw, err, a.host_err, tid);
+    DEC_STAMP(l, 3);
+    if constexpr (!VEARLY) {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(q0 + t, last) * DEC_D + 2 * lane);
+    }
+    rope();
+    fold(kr, vr, mraw, q0);
+    while (rest != 0) {   // workgroup-uniform
+      const long long pc = (long long)(slot + NT * __builtin_ctz(rest)) * DEC_SPL + wave * 16;
+      rest &= rest - 1;
+      uint4 kr2[4];
+      uint32_t vr2[16];
+      FRaw m2 = {0, 0};
+      if (a.mask_dtype >= 0) m2 = ld_f_raw(a.mask, min(pc + kq, last), a.mask_dtype);
+      const uint4* ks2 = (const uint4*)(Kb + min(pc + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kr2[j] = ldg16(ks2 + j);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) vr2[t] = ldg4(Vb + min(pc + t, last) * DEC_D + 2 * lane);
+      fold(kr2, vr2, m2, pc);
+    }
+  } else {   // every chunk of this slot is closed: an empty partial
+    __syncthreads();
+    xgather<1>(qkvw, 3 * DEC_D, tag, raw, err, a.host_err, tid);
+    DEC_STAMP(l, 3);
+    rope();
+  }
+  osh[wave * DEC_D + 2 * lane] = acc0;
+  osh[wave * DEC_D + 2 * lane + 1] = acc1;
+  if (lane == 0) {
+    red[wave] = mw;
+    red2[wave] = lw;
+  }
+  __syncthreads();
+  if (tid < DEC_D + 4) {
+    float M = -INFINITY;
+#pragma unroll
+    for (int w8 = 0; w8 < DEC_WAVES; ++w8) M = fmaxf(M, red[w8]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int w8 = 0; w8 < DEC_WAVES; ++w8) {
+      const float lv = red2[w8];
+      const float f = lv > 0.f ? __expf(red[w8] - M) : 0.f;
+      o = fmaf(f, osh[w8 * DEC_D + min(tid, DEC_D - 1)], o);
+      L = fmaf(f, lv, L);
+    }
+    // the head's slot partial, one contiguous block: o / l (bf16), then m and l as four
+    // 16-bit halves
+    const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
+    const int e = tid - DEC_D;
+    const uint16_t v = tid < DEC_D ? f32_to_bf16(L > 0.f ? o / L : 0.f)
+                                   : (uint16_t)(((e < 2 ? mb : lb) >> ((e & 1) ? 0 : 16)) & 0xFFFFu);
+    xput(partw + tid, v, tag);
+  }
+}
+
+// ---- C: combine the slot partials of one query head (waves 0-3, 2 threads per dimension) ----------
+// partw: the head's nsplit partials; attw: the head's D words of the attention row.
+__device__ __forceinline__ void dec_combine(const PersistArgs& a, int l, const uint32_t* partw, uint32_t* attw,
+                                            uint32_t tag, uint32_t* err, unsigned char* smem, float* red2,
+                                            int tid, int lane, int wave) {
+  const int NT = a.nsplit;
+  uint16_t* pl = (uint16_t*)smem;   // [NT][D + 4]
+  float* cw = red2;                 // [NT] weights e^(m_t - M) l_t / L (NT <= 32: red2 holds 64)
+  __syncthreads();
+  xgather<(32 * (DEC_D + 4) + 2 * 256 - 1) / (2 * 256), 256>(partw, NT * (DEC_D + 4), tag, pl, err, a.host_err, tid);
+  DEC_STAMP(l, 5);
+  if (wave == 0) {
+    float m = -INFINITY, lv = 0.f;
+    if (lane < NT) {
+      const uint16_t* e = pl + lane * (DEC_D + 4) + DEC_D;
+      m = __uint_as_float(((uint32_t)e[0] << 16) | e[1]);
+      lv = __uint_as_float(((uint32_t)e[2] << 16) | e[3]);
+    }
+    const float M = wave_max(lv > 0.f ? m : -INFINITY);
+    const float f = lv > 0.f ? __expf(m - M) * lv : 0.f;
+    const float L = wave_sum(f);
+    if (lane < NT) cw[lane] = L > 0.f ? f / L : 0.f;
+  }
+  __syncthreads();
+  if (wave < 4) {
+    const int d = tid >> 1, q = tid & 1;
+    float sacc = 0.f;
+    for (int t = q; t < NT; t += 2) sacc = fmaf(cw[t], bfh(pl[t * (DEC_D + 4) + d]), sacc);
+    sacc += HS_DPP(sacc, HS_QUAD_XOR1);
+    if (q == 0) xput(attw + d, f32_to_bf16(sacc), tag);
+  }
+  DEC_STAMP(l, 6);
+}
+
 // ---------------------------------------------------------------- the step
 
 // The step's LDS, declared once per kernel (both role instances of decode_body use it).
@@ -403,35 +640,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   // layer 0's tensors into LDS; each layer loads the next one's during its first part and stores
   // them in F, so no layer waits for its table at its start
   if (tid < 14) ptab[0][tid] = ((const void* const*)a.layers)[tid];
-  // The chunks this attention workgroup reads, the same for every layer: bit i stands for chunk
-  // slot + nsplit i, set when the mask opens a position of it (every chunk without a mask).
-  // Chunks whose positions are all -inf contribute exactly nothing to the softmax, so their K / V
-  // rows are never loaded; the loop over the open chunks is bounded by the mask, not by S.
-  // Wave w checks half a chunk per round (chunk 4 q + w / 2, positions 64 (w & 1) + lane), all
-  // eight rounds' loads issued together.
+  // the open chunks this attention workgroup reads (the same for every layer)
   uint32_t ob = 0;
-  if constexpr (att) {
-    const int nch = (a.nchunk - slot + NT - 1) / NT;   // chunks of this slot (<= 32, checked on the host)
-    if (a.mask_dtype < 0) {
-      ob = nch >= 32 ? 0xFFFFFFFFu : ((1u << nch) - 1u);
-    } else {
-      FRaw mr[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const long long p = (long long)(slot + NT * (4 * q + (wave >> 1))) * DEC_SPL + 64 * (wave & 1) + lane;
-        mr[q] = ld_f_raw(a.mask, min(p, last), a.mask_dtype);
-      }
-      uint32_t bits = 0;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int i = 4 * q + (wave >> 1);
-        const long long p = (long long)(slot + NT * i) * DEC_SPL + 64 * (wave & 1) + lane;
-        const bool open = i < nch && p <= last && ld_f_decode(mr[q], a.mask_dtype) != -INFINITY;
-        if (__ballot(open) != 0ull) bits |= 1u << i;
-      }
-      if (lane == 0) sh.obw[wave] = bits;
-    }
-  }
+  if constexpr (att) ob = dec_scan_chunks(a, slot, sh.obw, lane, wave);
   __syncthreads();
   if constexpr (att) {
     if (a.mask_dtype >= 0) {
@@ -531,161 +742,12 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     }
 
     // ---- B: attention of one query head over the open chunks of its slot ----------------------------
-    // The first open chunk's K rows and mask values do not depend on this step's activations, so
-    // they are issued before B waits for its q / k / v (after A, whose input poll would otherwise
-    // wait behind them); its V rows, needed last, are issued once q / k / v are in, so the poll
-    // does not wait behind them either and their latency overlaps the scores. Further open chunks
-    // (caches longer than 128 nsplit positions) are loaded and folded in one after another: each
-    // wave keeps a running (max, sum, unnormalised output) over its 16 positions of every chunk.
     if constexpr (att) {
       DEC_PART_IDS();
-      const int kq = lane >> 2, kc = lane & 3;
       const int hq = kvh * G + gq;
-      uint16_t* raw = (uint16_t*)smem;               // [3 * D]: q, k, v as produced
-      const float* csh = rope_cs;                    // [64] cos, [64] sin (rounded, scaled)
-      uint16_t* rot = (uint16_t*)(smem + 1536);      // [2 * D]: rotated q and k
-      float* osh = (float*)(smem + 2048);            // [8][D] per-wave unnormalised outputs
-      const uint16_t* Kb = P.kc + (long long)kvh * kvs;
-      const uint16_t* Vb = P.vc + (long long)kvh * kvs;
-      const bool cin = cpos >= 0 && cpos < S;
-      float acc0 = 0.f, acc1 = 0.f, mw = -INFINITY, lw = 0.f;
-      auto rope = [&]() {   // rotate_half RoPE: threads 0..63 q, 64..127 k
-        if (tid < 128) {
-          const int hs = tid >> 6, j = tid & 63;
-          const float x0 = bfh(raw[hs * DEC_D + j]), x1 = bfh(raw[hs * DEC_D + j + 64]);
-          const float c = csh[j], sn = csh[64 + j];
-          rot[hs * DEC_D + j] = f32_to_bf16(rb(rb(x0 * c) + rb(-x1 * sn)));
-          rot[hs * DEC_D + j + 64] = f32_to_bf16(rb(rb(x1 * c) + rb(x0 * sn)));
-        }
-        __syncthreads();
-        // this step's K / V row goes into the caches (index_copy at cache_position), by the
-        // first head's workgroup of the slot that holds the position, open or not
-        if (cin && gq == 0 && (int)((cpos / DEC_SPL) % NT) == slot && tid < DEC_D) {
-          stg2(P.kc + (long long)kvh * kvs + cpos * DEC_D + tid, rot[DEC_D + tid]);
-          stg2(P.vc + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
-        }
-      };
-      // one chunk folded into the wave's running softmax; p0: the wave's first position in it.
-      // The wave holding cache_position uses the new K / V row (V chosen at its use, so no branch
-      // joins the loaded V values, which would make the compiler wait for them there). For the
-      // first chunk (mw = -inf) the rescaling factor is 0 and the result is that of a one-pass
-      // softmax over the chunk.
-      auto fold = [&](const uint4 (&kin)[4], const uint32_t (&vr)[16], FRaw mraw, long long p0) {
-        uint4 kr[4] = {kin[0], kin[1], kin[2], kin[3]};
-        const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
-        const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
-        if (vnew && p0 + kq == cpos) {
-          const uint4* kn = (const uint4*)(rot + DEC_D + kc * 32);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) kr[j] = kn[j];
-        }
-        const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
-        const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
-        const bool live = __ballot(mval != -INFINITY) != 0ull;
-        if (live) {
-          const uint4* qq = (const uint4*)(rot + kc * 32);
-          float d = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint4 q4 = qq[j];
-            d = ddot2(q4.x, kr[j].x, d);
-            d = ddot2(q4.y, kr[j].y, d);
-            d = ddot2(q4.z, kr[j].z, d);
-            d = ddot2(q4.w, kr[j].w, d);
-          }
-          d += HS_DPP(d, HS_QUAD_XOR1);
-          d += HS_DPP(d, HS_QUAD_XOR2);
-          float sc = -INFINITY;
-          if (mval != -INFINITY) {
-            sc = rb(d);
-            sc = rb(sc * a.scale);
-            if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
-          }
-          float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
-          m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
-          m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
-          const float mn = fmaxf(mw, m);
-          const float al = (mw == -INFINITY) ? 0.f : __expf(mw - mn);
-          const float e = (sc == -INFINITY) ? 0.f : __expf(sc - mn);
-          float ls = e + HS_DPP(e, HS_ROW_ROR4);
-          ls += HS_DPP(ls, HS_ROW_ROR8);
-          lw = lw * al + ((HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48)));
-          mw = mn;
-          acc0 *= al;
-          acc1 *= al;
-#pragma unroll
-          for (int t = 0; t < 16; ++t) {
-            const float p = HS_RL(e, 4 * t);
-            const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
-            acc0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), acc0);
-            acc1 = fmaf(p, bfh((uint16_t)(vt >> 16)), acc1);
-          }
-        }
-      };
-      if (ob != 0) {   // workgroup-uniform
-        uint32_t rest = ob & (ob - 1);
-        const long long q0 = (long long)(slot + NT * __builtin_ctz(ob)) * DEC_SPL + wave * 16;
-        uint4 kr[4];
-        FRaw mraw = {0, 0};
-        if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(q0 + kq, last), a.mask_dtype);
-        const uint4* ks = (const uint4*)(Kb + min(q0 + kq, last) * DEC_D + kc * 32);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
-        __syncthreads();
-        xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, a.host_err, tid);
-        DEC_STAMP(l, 3);
-        uint32_t vr[16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(q0 + t, last) * DEC_D + 2 * lane);
-        rope();
-        fold(kr, vr, mraw, q0);
-        while (rest != 0) {   // workgroup-uniform
-          const long long pc = (long long)(slot + NT * __builtin_ctz(rest)) * DEC_SPL + wave * 16;
-          rest &= rest - 1;
-          uint4 kr2[4];
-          uint32_t vr2[16];
-          FRaw m2 = {0, 0};
-          if (a.mask_dtype >= 0) m2 = ld_f_raw(a.mask, min(pc + kq, last), a.mask_dtype);
-          const uint4* ks2 = (const uint4*)(Kb + min(pc + kq, last) * DEC_D + kc * 32);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) kr2[j] = ldg16(ks2 + j);
-#pragma unroll
-          for (int t = 0; t < 16; ++t) vr2[t] = ldg4(Vb + min(pc + t, last) * DEC_D + 2 * lane);
-          fold(kr2, vr2, m2, pc);
-        }
-      } else {   // every chunk of this slot is closed: an empty partial
-        __syncthreads();
-        xgather<1>(XL + X.qkv + (long long)hq * 3 * DEC_D, 3 * DEC_D, tag, raw, err, a.host_err, tid);
-        DEC_STAMP(l, 3);
-        rope();
-      }
-      osh[wave * DEC_D + 2 * lane] = acc0;
-      osh[wave * DEC_D + 2 * lane + 1] = acc1;
-      if (lane == 0) {
-        red[wave] = mw;
-        red2[wave] = lw;
-      }
-      __syncthreads();
-      if (tid < DEC_D + 4) {
-        float M = -INFINITY;
-#pragma unroll
-        for (int w8 = 0; w8 < DEC_WAVES; ++w8) M = fmaxf(M, red[w8]);
-        float o = 0.f, L = 0.f;
-#pragma unroll
-        for (int w8 = 0; w8 < DEC_WAVES; ++w8) {
-          const float lv = red2[w8];
-          const float f = lv > 0.f ? __expf(red[w8] - M) : 0.f;
-          o = fmaf(f, osh[w8 * DEC_D + min(tid, DEC_D - 1)], o);
-          L = fmaf(f, lv, L);
-        }
-        // the head's slot partial, one contiguous block: o / l (bf16), then m and l as four
-        // 16-bit halves
-        const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
-        const int e = tid - DEC_D;
-        const uint16_t v = tid < DEC_D ? f32_to_bf16(L > 0.f ? o / L : 0.f)
-                                       : (uint16_t)(((e < 2 ? mb : lb) >> ((e & 1) ? 0 : 16)) & 0xFFFFu);
-        xput(XL + X.part + ((long long)hq * NT + slot) * (DEC_D + 4) + tid, v, tag);
-      }
+      dec_attend(a, l, P.kc, P.vc, XL + X.qkv + (long long)hq * 3 * DEC_D,
+                 XL + X.part + ((long long)hq * NT + slot) * (DEC_D + 4), ob, kvh, gq, slot, cpos, tag, err, smem,
+                 rope_cs, red, red2, tid, lane, wave);
       DEC_STAMP(l, 4);
       // this workgroup's first NL gate / up rows into LDS: its next wait (x1, in E) is some
       // microseconds away, and these land by then
@@ -697,37 +759,12 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       }
     }
 
-    // ---- C: combine the slot partials of one query head (waves 0-3, 2 threads per dimension) ----------
+    // ---- C: combine the slot partials of one query head ---------------------------------------------
     if (comb) {
       DEC_PART_IDS();
       const int h = b - ntile * G;
-      uint16_t* pl = (uint16_t*)smem;   // [NT][D + 4]
-      float* cw = red2;                 // [NT] weights e^(m_t - M) l_t / L (NT <= 32: red2 holds 64)
-      __syncthreads();
-      xgather<(32 * (DEC_D + 4) + 2 * 256 - 1) / (2 * 256), 256>(
-          XL + X.part + (long long)h * NT * (DEC_D + 4), NT * (DEC_D + 4), tag, pl, err, a.host_err, tid);
-      DEC_STAMP(l, 5);
-      if (wave == 0) {
-        float m = -INFINITY, lv = 0.f;
-        if (lane < NT) {
-          const uint16_t* e = pl + lane * (DEC_D + 4) + DEC_D;
-          m = __uint_as_float(((uint32_t)e[0] << 16) | e[1]);
-          lv = __uint_as_float(((uint32_t)e[2] << 16) | e[3]);
-        }
-        const float M = wave_max(lv > 0.f ? m : -INFINITY);
-        const float f = lv > 0.f ? __expf(m - M) * lv : 0.f;
-        const float L = wave_sum(f);
-        if (lane < NT) cw[lane] = L > 0.f ? f / L : 0.f;
-      }
-      __syncthreads();
-      if (wave < 4) {
-        const int d = tid >> 1, q = tid & 1;
-        float sacc = 0.f;
-        for (int t = q; t < NT; t += 2) sacc = fmaf(cw[t], bfh(pl[t * (DEC_D + 4) + d]), sacc);
-        sacc += HS_DPP(sacc, HS_QUAD_XOR1);
-        if (q == 0) xput(XL + X.att + (long long)h * DEC_D + d, f32_to_bf16(sacc), tag);
-      }
-      DEC_STAMP(l, 6);
+      dec_combine(a, l, XL + X.part + (long long)h * NT * (DEC_D + 4), XL + X.att + (long long)h * DEC_D, tag, err,
+                  smem, red2, tid, lane, wave);
     }
 
     // ---- D: o_proj + residual (o_proj workgroups; the rows from LDS) ------------------------------------
@@ -1057,3 +1094,207 @@ DECODE_KERNEL(3, 3, 6)   // hidden 1536, up to 48
 DECODE_KERNEL(1, 1, 1)   // hidden 512, up to 8
 DECODE_KERNEL(1, 1, 2)   // hidden 512, up to 16
 DECODE_KERNEL(2, 2, 4)   // hidden 1024, up to 32
+
+// ================================================================ one attention block, one launch
+//
+// k_attn_step_k<KC>: a graph that is one decode-token attention block (optional input RMSNorm,
+// q / k / v with optional biases, RoPE, the K / V rows written at cache_position, GQA attention
+// over the mask's open chunks, o_proj with optional residual) as one launch. Its launch list is
+// three dependent launches (q/k/v + RoPE + cache rows, split attention, combine + o_proj) around
+// ~12 MB at Qwen2.5-1.5B's shape, whose launch boundaries take most of the time. These are the
+// decode step's parts A-D for one layer, with the same exchange words, chunk walk and rounding
+// points:
+//   A  every workgroup: q / k / v rows b RB .. b RB + RB - 1 (RB <= 8), one per wave
+//   B  workgroups b < NB = H nsplit: (query head, KV head, slot) as in the decode step, its
+//      first chunk's K and V rows issued before it waits for q / k / v
+//   C  workgroups NB .. NB + H - 1: one head's partials combined into its D attention words
+//   D  workgroups NB + i, i < ceil(hidden / RD): o_proj rows i RD .. i RD + RD - 1 (loaded into
+//      LDS once A is out); + residual; out
+// Exchange words: [H][q | k | v], [H][nsplit][D + 4] partials, [H D] attention row, then the step
+// tag and the timeout flag. Workgroup NB writes the new step tag once it holds the whole
+// attention row: it depends on every workgroup's q / k / v rows, so every workgroup has read the
+// old tag by then. (Every o_proj workgroup combining all the partials itself instead, one
+// hand-off fewer, measured slower: 140 workgroups gathering 57 KB each.)
+#define AST_ROWS 32   // o_proj rows per workgroup, at most (its LDS)
+
+template <int KC>
+struct AttnShared {
+  __attribute__((aligned(16))) unsigned char smem[DEC_SMEM];   // B, C staging; the normalised x; the attention row
+  __attribute__((aligned(16))) uint16_t xres[512 * KC];        // the input row
+  __attribute__((aligned(16))) uint4 obuf[AST_ROWS * KC * 64];  // o_proj row i, chunk c: 1 KB at KC i + c
+  float red[DEC_WAVES * 8];
+  float red2[DEC_WAVES * DEC_MAXG];
+  float rope_cs[128];
+  const void* ptab[14];
+  uint32_t obw[DEC_WAVES];
+  uint16_t ostage[AST_ROWS];
+};
+
+template <int KC, int ROLE>
+__device__ __forceinline__ void attn_step_body(const PersistArgs& a, AttnShared<KC>& sh) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x, NWG = a.nwg;
+  const int hid = a.hidden, H = a.H, KVH = a.KVH, G = H / KVH, NT = a.nsplit;
+  const long long XP = (long long)H * 3 * DEC_D;                      // partials
+  const long long XA = XP + (long long)H * NT * (DEC_D + 4);          // attention row
+  uint32_t* ctl = a.ll + XA + (long long)H * DEC_D;                   // [0] step tag, [1] timeout flag
+  uint32_t* err = ctl + 1;
+  uint32_t tag = (__hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) & 0xFFFFu;
+  tag = tag == 0 ? 1u : tag;
+  const long long posr = ld_i(a.pos_ids, 0, a.pos_dtype);
+  const long long cpos = ld_i(a.cache_pos, 0, a.cpos_dtype);
+  uint16_t* xs = (uint16_t*)sh.smem;
+  DEC_STAMP(0, 0);
+  if (tid < 64) {   // rotary factors of this step's position, as in the decode step
+    float sf, cf;
+    sincos_rot(a.inv_freq[tid] * (float)posr, &sf, &cf);
+    sh.rope_cs[tid] = round_to(cf * a.rope_scaling, HS_BF16);
+    sh.rope_cs[64 + tid] = round_to(sf * a.rope_scaling, HS_BF16);
+  }
+  if (tid < 14) sh.ptab[tid] = ((const void* const*)a.layers)[tid];
+  constexpr bool ATT = ROLE == 0, COMB = ROLE == 2;
+  const int ntile = KVH * NT, NB = ntile * G;
+  const int tile = b % ntile, gq = b / ntile, kvh = tile / NT, slot = tile % NT;
+  const int RD = a.rows;                 // <= AST_ROWS (checked on the host)
+  const long long d0 = (long long)(b - NB) * RD;
+  uint32_t ob = 0;
+  if constexpr (ATT) ob = dec_scan_chunks(a, slot, sh.obw, lane, wave);
+  __syncthreads();
+  if constexpr (ATT) {
+    if (a.mask_dtype >= 0) {
+#pragma unroll
+      for (int w8 = 0; w8 < DEC_WAVES; ++w8) ob |= sh.obw[w8];
+    }
+  }
+  const DecodeLayerPtrs P = dec_layer(sh.ptab);
+
+  // ---- A: [RMSNorm], q / k / v rows (+ bias), published per query head ----------------------------
+  {
+    const int R = (H + 2 * KVH) * DEC_D, RB = (R + NWG - 1) / NWG;   // RB <= 8 (checked on the host)
+    const int r = b * RB + wave;
+    const bool has = wave < RB && r < R;
+    const uint16_t* W;
+    const uint16_t* B;
+    int rr;
+    if (r < H * DEC_D) {
+      W = P.wq; B = P.bq; rr = r;
+    } else if (r < (H + KVH) * DEC_D) {
+      rr = r - H * DEC_D; W = P.wk; B = P.bk;
+    } else {
+      rr = r - (H + KVH) * DEC_D; W = P.wv; B = P.bv;
+    }
+    const long long rl = has ? rr : 0;   // a wave without a row re-reads row 0 of q (unused)
+    const uint16_t* Wl = has ? W : P.wq;
+    const bool norm = P.norm1 != nullptr;
+    const int nch = hid >> 3;
+    const uint4 xv = tid < nch ? ldg16(a.xin + 8 * tid) : make_uint4(0, 0, 0, 0);
+    uint4 w[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) w[c] = ldw(Wl + rl * hid + c * 512 + lane * 8);
+    const uint16_t bias = (has && (a.flags & 1)) ? ldg2(B + rr) : (uint16_t)0;
+    const uint4 nw = (norm && tid < nch) ? ldg16(P.norm1 + 8 * tid) : make_uint4(0, 0, 0, 0);
+    if (tid < nch) *(uint4*)(sh.xres + 8 * tid) = xv;
+    __syncthreads();
+    DEC_STAMP(0, 1);
+    const uint16_t* xn = sh.xres;
+    if (norm) {
+      block_norm(sh.xres, nw, hid, a.eps, a.n_dtype, xs, sh.red, tid);
+      xn = xs;
+    }
+    if (has) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) acc = ddot8(*(const uint4*)(xn + c * 512 + lane * 8), w[c], acc);
+      acc = wave_sum(acc);
+      if (lane == 0) sh.ostage[wave] = f32_to_bf16(acc + bfh(bias));
+    }
+    __syncthreads();
+    // one store by wave 0: a k or v row goes into the blocks of all G heads that read it
+    if (wave == 0 && lane < RB * G) {
+      const int j = lane / G, g = lane % G, rj = b * RB + j;
+      if (rj < R) {
+        const int sj = rj < H * DEC_D ? 0 : (rj < (H + KVH) * DEC_D ? 1 : 2);
+        const int rrj = rj - (sj == 0 ? 0 : (sj == 1 ? H * DEC_D : (H + KVH) * DEC_D));
+        const int hq = sj == 0 ? rrj / DEC_D : (rrj / DEC_D) * G + g;
+        if (sj != 0 || g == 0) xput(a.ll + (long long)hq * 3 * DEC_D + sj * DEC_D + rrj % DEC_D, sh.ostage[j], tag);
+      }
+    }
+    DEC_STAMP(0, 2);
+  }
+
+  if constexpr (ATT) {
+    // ---- B ----
+    const int hq = kvh * G + gq;
+    dec_attend<true>(a, 0, P.kc, P.vc, a.ll + (long long)hq * 3 * DEC_D,
+                     a.ll + XP + ((long long)hq * NT + slot) * (DEC_D + 4), ob, kvh, gq, slot, cpos, tag, err,
+                     sh.smem, sh.rope_cs, sh.red, sh.red2, tid, lane, wave);
+    DEC_STAMP(0, 4);
+  } else {
+    // ---- D's o_proj rows into LDS; the residual values ----
+    const long long rmax = min(d0 + RD, (long long)hid) - 1;   // rows past the last re-read it
+    const unsigned base = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&sh.obuf[0];
+    for (int k = wave; k < RD * KC; k += DEC_WAVES) {
+      const long long r = max(min(d0 + k / KC, rmax), 0ll);
+      dec_dma16(P.wo + r * hid + (k % KC) * 512 + lane * 8, __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
+    }
+    const bool rin = a.resid != nullptr && tid < RD && d0 + tid < hid;
+    const uint16_t rv = rin ? ldg2(a.resid + d0 + tid) : (uint16_t)0;
+    // ---- C ----
+    if constexpr (COMB) {
+      const int h = b - NB;
+      dec_combine(a, 0, a.ll + XP + (long long)h * NT * (DEC_D + 4), a.ll + XA + (long long)h * DEC_D, tag, err,
+                  sh.smem, sh.red2, tid, lane, wave);
+    }
+    if (d0 >= hid) return;   // no o_proj rows (workgroup NB, which writes the tag, always has some)
+    dec_vmcnt0();   // this wave's o_proj rows have landed (the gather's barrier publishes them to all)
+    __syncthreads();
+    DEC_STAMP(0, 7);
+    xgather<(KC + 1) / 2 * 2, 256>(a.ll + XA, H * DEC_D, tag, xs, err, a.host_err, tid);
+    DEC_STAMP(0, 8);
+    if (b == NB && tid == 0) __hip_atomic_store(ctl, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // ---- D: o_proj [+ residual] -> out ----
+    const unsigned char* ow = (const unsigned char*)sh.obuf;
+    uint4 xa[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) xa[c] = *(const uint4*)(xs + c * 512 + lane * 8);
+    constexpr int MD = (AST_ROWS + DEC_WAVES - 1) / DEC_WAVES;   // rows per wave, at most: wave + 8 k
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = wave + DEC_WAVES * k;
+      v[k] = 0.f;
+      if (k < MD && i < RD && d0 + i < hid) {   // wave-uniform
+        uint4 wr[KC];
+#pragma unroll
+        for (int c = 0; c < KC; ++c) wr[c] = *(const uint4*)(ow + (i * KC + c) * 1024 + lane * 16);
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) acc = ddot8(xa[c], wr[c], acc);
+        v[k] = acc;
+      }
+    }
+    const float sum = wave_sum8(v, lane);   // lane 8 k: row wave + 8 k
+    const int i = wave + DEC_WAVES * (lane >> 3);
+    if ((lane & 7) == 0 && (lane >> 3) < MD && i < RD && d0 + i < hid) sh.ostage[i] = f32_to_bf16(sum);
+    __syncthreads();
+    if (tid < RD && d0 + tid < hid) {
+      uint16_t o = sh.ostage[tid];
+      if (rin) o = f32_to_bf16(bfh(rv) + bfh(o));
+      stg2(a.out + d0 + tid, o);
+    }
+    DEC_STAMP(0, 9);
+  }
+}
+
+#define ATTN_STEP_KERNEL(KC) \
+  extern "C" __global__ void __launch_bounds__(DEC_THREADS) k_attn_step_k##KC(const PersistArgs a) { \
+    __shared__ AttnShared<KC> sh; \
+    const int nb_ = a.H * a.nsplit; \
+    if ((int)blockIdx.x < nb_) attn_step_body<KC, 0>(a, sh); \
+    else if ((int)blockIdx.x < nb_ + a.H) attn_step_body<KC, 2>(a, sh); \
+    else attn_step_body<KC, 1>(a, sh); \
+  }
+
+ATTN_STEP_KERNEL(1)   // hidden 512
+ATTN_STEP_KERNEL(2)   // hidden 1024
+ATTN_STEP_KERNEL(3)   // hidden 1536 (Qwen2.5-1.5B)

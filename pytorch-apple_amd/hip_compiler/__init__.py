@@ -16,7 +16,7 @@ from __future__ import annotations
 from hip_compiler.buffer_planner import buffer_allocations, plan_arena
 from hip_compiler.op_support import get_hip_supported_ops, is_hip_op_supported
 from hip_compiler.persistent import enabled as persistent_enabled
-from hip_compiler.persistent import fuse_decode_step
+from hip_compiler.persistent import fuse_attention_step, fuse_decode_step
 from hip_compiler.program import HIPProgram, KernelSource, TView, contiguous_strides
 from hip_compiler.subgraph_analyzer import analyze_subgraph
 from npu_compiler.ir_reader import IRGraph, load_ir_from_dict
@@ -70,7 +70,7 @@ def compile_graph(graph: IRGraph, compute_dtype: str | None = None, *, inplace_i
         out_views[spec.name] = v
     steps = low.steps
     if fuse and (persistent if persistent is not None else persistent_enabled()):
-        steps = fuse_decode_step(low.steps, low.storages) or low.steps
+        steps = fuse_decode_step(low.steps, low.storages) or fuse_attention_step(low.steps, low.storages) or low.steps
     arena_bytes = plan_arena(steps, low.storages, {v.storage for v in out_views.values()})
     by_storage = {}
     for name, v in low.views.items():

@@ -25,8 +25,14 @@ The step is correct only when all ``NWG`` workgroups are resident at once (they 
 other's data). ``fuse_decode_step`` asks ``resident_workgroups`` how many fit on the device and
 keeps the launch list when that is fewer; the executor checks again before it launches.
 
+``fuse_attention_step`` does the same for a graph that is one decode-token attention block
+(the cfg2 block: q/k/v + RoPE + cache rows, split attention, combine + o_proj, optionally with
+the input RMSNorm and a residual): one launch of ``k_attn_step_k<KC>``, the decode step's
+attention parts for a single layer.
+
 The reference runs this step as one Python dispatch per IR op
-(`cuda_runtime/cuda_executor.py:136-176`); here the same IR ops become one launch.
+(`cuda_runtime/cuda_executor.py:136-176`, GQA attention at :226-273); here the same IR ops
+become one launch.
 """
 
 from __future__ import annotations
@@ -264,4 +270,115 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
         args=args, grid=(NWG, 1, 1), block=(THREADS, 1, 1), inputs=inputs, outputs=outputs,
         params={"table": {"field": "layers", "entries": table}, "layers": L, "nsplit": nsplit,
                 "replaces": [st.kernel for st in steps], "exchange_words": words, "work_split": ws})
+    return [step]
+
+
+# ---------------------------------------------------------------- one attention block, one launch
+
+AST_ROWS = 32        # decode.hip AST_ROWS: o_proj rows per workgroup, at most
+OPROJ_ATT = OPROJ + ("k_gemv_attn16_bias_r2", "k_gemv_attn_bias_r2")   # combine folded in, [+ residual]
+OPROJ_PLAIN = ("k_gemv_bias_r1", "k_gemv_bias_r4", "k_gemv_resid_r1", "k_gemv_resid_r2")
+
+
+def attention_slots(S: int, hidden: int, H: int) -> int | None:
+    """Attention slots per query head for ``k_attn_step`` over an S-position cache (as many as
+    fit, up to MAX_SLOTS and one per chunk), or None: the H nslot attention workgroups, the H
+    combine workgroups among the rest, and at most AST_ROWS o_proj rows for each of those."""
+    nchunk = -(-S // SPL)
+    for nslot in range(min(nchunk, MAX_SLOTS), 0, -1):
+        if -(-nchunk // nslot) > MAX_CHUNKS_PER_SLOT:
+            return None
+        nd = NWG - H * nslot
+        if nd > H and -(-hidden // nd) <= AST_ROWS:
+            return nslot
+    return None
+
+
+def attention_step_words(H: int, nsplit: int) -> int:
+    """32-bit words of ``k_attn_step``'s exchange area: per query head its q row with its KV head's
+    k and v rows, the slot partials (o[D], m, l as four half-words), the attention row, then the
+    step tag and the timeout flag."""
+    return H * 3 * D + H * nsplit * (D + 4) + H * D + 2
+
+
+def fuse_attention_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> list[LaunchStep] | None:
+    """The one-launch form (``k_attn_step_k<KC>``, csrc/kernels/decode.hip) of a launch list that is
+    exactly one decode-token attention block: ``k_qkv_rope*`` (optional RMSNorm and biases, RoPE on
+    q and k, both cache rows), ``k_attn_flash*`` and the o_proj GEMV with the combine folded in
+    (or ``k_attn_combine`` then a plain GEMV), with or without a residual. None otherwise, or when
+    the device cannot hold all of its workgroups at once."""
+    if len(steps) == 3:
+        q, f, o = steps
+        c = None
+        if o.kernel not in OPROJ_ATT:
+            return None
+    elif len(steps) == 4:
+        q, f, c, o = steps
+        if c.kernel != "k_attn_combine" or o.kernel not in OPROJ_PLAIN:
+            return None
+    else:
+        return None
+    if q.kernel not in QKV or f.kernel not in FLASH:
+        return None
+    qa, fl, oa = q.args, f.args, o.args
+    hidden, H, KVH, S = int(qa["K"]), int(qa["H"]), int(qa["KVH"]), int(fl["S"])
+    flags = int(qa["flags"])
+    if int(qa["D"]) != D or H * D != hidden or hidden % 512 or hidden // 512 not in VARIANTS:
+        return None
+    if H % KVH or H // KVH > MAX_G or (H + 2 * KVH) * D > 8 * NWG or flags & 60 != 60:
+        return None
+    if c is None:
+        attn_ok = _same(oa["attn_o"], fl["part_o"]) and _same(oa["attn_ml"], fl["part_ml"])
+    else:
+        ca = c.args
+        attn_ok = (_same(ca["part_o"], fl["part_o"]) and _same(ca["part_ml"], fl["part_ml"])
+                   and _same(oa["x"], ca["out"]))
+    resid = oa.get("resid")
+    ok = (
+        attn_ok and _same(fl["q"], qa["q_out"]) and _same(fl["k"], qa["k_dst"]) and _same(fl["v"], qa["v_dst"])
+        and isinstance(qa["x"], Ref) and isinstance(oa["out"], Ref) and (resid is None or isinstance(resid, Ref))
+        and ((flags & 1) == 0 or isinstance(qa["norm_w"], Ref))
+        and int(qa["cache_len"]) == S and int(qa["kv_head_stride"]) == int(fl["kv_head_stride"])
+        and int(fl["H"]) == H and int(fl["KVH"]) == KVH and int(fl["dtype"]) == DTYPE_CODE["bfloat16"]
+        and int(fl["q_head_stride"]) == D
+        and (fl["mask"] is None or (int(fl["mask_stride"]) == 1 and int(fl["mask_dtype"]) in (0, 2)))
+        and int(oa["N"]) == hidden and int(oa["K"]) == hidden and int(oa["M"]) == 1 and int(oa["flags"]) == 0
+        and oa.get("bias") is None and oa.get("w2") is None and oa.get("norm_w") is None
+    )
+    if not ok:
+        return None
+    nsplit = attention_slots(S, hidden, H)
+    if nsplit is None:
+        return None
+    bias = flags & 2
+    table = [qa["norm_w"] if flags & 1 else None, qa["wq"], qa["bq"] if bias else None, qa["wk"],
+             qa["bk"] if bias else None, qa["wv"], qa["bv"] if bias else None, qa["k_dst"], qa["v_dst"], oa["w"],
+             None, None, None, None]
+    for r in table:
+        if r is not None and storages[r.storage].kind not in ("input", "weight"):
+            return None
+    KC = hidden // 512
+    kernel = f"k_attn_step_k{KC}"
+    fit = resident_workgroups(kernel)
+    if fit is not None and fit < NWG:
+        return None
+    words = attention_step_words(H, nsplit)
+    xname = "attn_step.exchange"
+    storages[xname] = Storage(xname, "persistent", words * 4, "uint8", zero_init=True)
+    mask = fl["mask"]
+    args = dict(
+        layers=None, pos_ids=qa["pos_ids"], cache_pos=qa["cache_pos"], mask=mask, inv_freq=qa["inv_freq"],
+        ll=Ref(xname, 0), trace=None, S=S, kv_head_stride=int(qa["kv_head_stride"]), L=1, hidden=hidden, H=H,
+        KVH=KVH, D=D, nsplit=nsplit, nwg=NWG, pos_dtype=int(qa["pos_dtype"]), cpos_dtype=int(qa["cpos_dtype"]),
+        mask_dtype=int(fl["mask_dtype"]) if mask is not None else -1, add_dtype=int(fl.get("add_dtype", 2)),
+        n_dtype=int(qa["n_dtype"]), flags=1 if bias else 0, eps=float(qa["eps"]), scale=float(fl["scale"]),
+        rope_scaling=float(qa["rope_scaling"]), nchunk=-(-S // SPL), rows=-(-hidden // (NWG - H * nsplit)),
+        xin=qa["x"], out=oa["out"], resid=resid)
+    inputs = sorted({t for st in steps for t in st.inputs})
+    outputs = [t for st in steps for t in st.outputs]
+    step = LaunchStep(
+        kind="attn_step", kernel=kernel, module="decode", arg_struct="PersistArgs",
+        args=args, grid=(NWG, 1, 1), block=(THREADS, 1, 1), inputs=inputs, outputs=outputs,
+        params={"table": {"field": "layers", "entries": table}, "layers": 1, "nsplit": nsplit,
+                "replaces": [st.kernel for st in steps], "exchange_words": words})
     return [step]

@@ -148,16 +148,16 @@ class HIPExecutor:
         self._adv_ptr = 0                         # flag word of a decode advance folded into the launch
         self._adv_bufs: tuple = ()                # its (mask, position, cache position, mask bytes)
         self._capture_stream = None
-        # a persistent decode step: every workgroup must be resident at once, and its timeout flag
-        # is mirrored into host memory, read on every launch without a synchronisation
+        # a persistent step (PERSISTENT_KINDS): every workgroup must be resident at once, and its
+        # timeout flag is mirrored into host memory, read on every launch without a synchronisation
         self._hflag = None
         for st, s in zip(program.steps, self._structs):
-            if st.kind != "decode_step":
+            if st.kind not in PERSISTENT_KINDS:
                 continue
             need = int(st.grid[0])
             fit = resident_workgroups(self.device.index or 0, st.module, st.kernel, int(st.block[0]), int(st.lds))
             if fit < need:
-                raise RuntimeError(f"persistent decode step {st.kernel} needs {need} workgroups resident at once; "
+                raise RuntimeError(f"persistent step {st.kernel} needs {need} workgroups resident at once; "
                                    f"this device holds {fit} (compile with persistent=False, or HIPRT_PERSISTENT=0)")
             flags = _HOST_FLAGS.setdefault(self.device.index or 0, _HostFlags())
             self._hflag, s.host_err = flags.take()
@@ -293,7 +293,7 @@ class HIPExecutor:
 
     def launch(self, inputs: dict, weights: dict, stream: int | None = None) -> None:
         """Enqueue the whole program on ``stream`` (default: torch's current stream). Raises
-        ``RuntimeError`` first when an earlier persistent decode step of this executor reported a
+        ``RuntimeError`` first when an earlier persistent step of this executor reported a
         timeout (its host-visible flag; no synchronisation needed)."""
         if self._hflag is not None and self._hflag.value:
             self._hflag.value = 0
@@ -373,11 +373,11 @@ class HIPExecutor:
         return True
 
     def check(self) -> None:
-        """Raise ``RuntimeError`` if a persistent decode step has recorded a timeout (one of its
+        """Raise ``RuntimeError`` if a persistent step has recorded a timeout (one of its
         workgroups waited past its time limit for data from another: its results are not valid).
         Synchronises with the device; clears the flags."""
         for st in self.program.steps:
-            if st.kind != "decode_step":
+            if st.kind not in PERSISTENT_KINDS:
                 continue
             xs = self.program.storages[st.args["ll"].storage]
             off = xs.offset + (int(st.params["exchange_words"]) - 1) * 4
@@ -418,7 +418,12 @@ class HIPExecutor:
             pass
 
 
-_TIMEOUT_MSG = ("persistent decode step: a workgroup timed out waiting for another's data, so the step's "
+# launches whose workgroups wait for each other's data (all resident at once, bounded waits with
+# a timeout flag in the last exchange word): the persistent decode step and the one-launch
+# attention block
+PERSISTENT_KINDS = ("decode_step", "attn_step")
+
+_TIMEOUT_MSG = ("persistent step: a workgroup timed out waiting for another's data, so the step's "
                 "outputs are not valid (the step needs every one of its workgroups resident at once: "
                 "is another kernel sharing the GPU?)")
 

@@ -156,8 +156,10 @@ def build_mlp_ir(tokens: int, cfg: QwenConfig = QWEN2_5_1_5B) -> dict:
     return b.to_dict()
 
 
-def build_attention_ir(kv_len: int, cfg: QWEN2_5_1_5B.__class__ = QWEN2_5_1_5B) -> dict:
-    """cfg2: one decode-token attention block over a [1, KVH, kv_len, D] cache."""
+def build_attention_ir(kv_len: int, cfg: QWEN2_5_1_5B.__class__ = QWEN2_5_1_5B, residual: bool = False) -> dict:
+    """cfg2: one decode-token attention block over a [1, KVH, kv_len, D] cache. With
+    ``residual`` the block is a decoder layer's first half: input RMSNorm before it and the
+    block's input added to its output."""
     b = IRBuilder("Qwen2.5_Attention")
     x = b.input("hidden_states", [1, 1, cfg.hidden], cfg.dtype)
     mask = b.input("attention_mask", [1, 1, 1, kv_len], cfg.dtype)
@@ -166,7 +168,12 @@ def build_attention_ir(kv_len: int, cfg: QWEN2_5_1_5B.__class__ = QWEN2_5_1_5B) 
     pk = b.input("past_key_0", [1, cfg.kv_heads, kv_len, cfg.head_dim], cfg.dtype)
     pv = b.input("past_value_0", [1, cfg.kv_heads, kv_len, cfg.head_dim], cfg.dtype)
     cos, sin = rope_tables(b, cfg, pos)
-    out, kc, vc = attention_block(b, cfg, 0, x, cos, sin, mask, cpos, pk, pv)
+    h = x
+    if residual:
+        h = rmsnorm(b, x, b.weight("model.layers.0.input_layernorm.weight", [cfg.hidden], cfg.dtype), cfg.eps)
+    out, kc, vc = attention_block(b, cfg, 0, h, cos, sin, mask, cpos, pk, pv)
+    if residual:
+        out = b.op("aten.add.Tensor", [x, out])
     b.output(out, kc, vc)
     return b.to_dict()
 

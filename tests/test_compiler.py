@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from hip_compiler import compile_subgraph, get_hip_supported_ops, is_hip_op_supported
+from hip_compiler import persistent
 from hip_compiler import views as V
 from hip_compiler.program import ELEM_SIZE, Ref, TView, contiguous_strides
 from irgen.qwen import QwenConfig, build_attention_ir, build_decode_ir, build_mlp_ir
@@ -64,27 +65,61 @@ def test_rmsnorm_pattern_alone_is_one_kernel():
     assert abs(eps - 1e-6) < 1e-12
 
 
-def test_attention_block_is_three_launches_with_inplace_cache():
-    # default: 128-position splits (8 waves), combined in the o_proj prologue
+def test_attention_block_is_one_launch_by_default():
+    # the one-launch block: 9 slots of one 128-position chunk each for 12 heads (108 attention
+    # workgroups); 12 of the other 148 combine a head's partials, and 140 take 11 o_proj rows each
     p = compile_subgraph(build_attention_ir(1025))
+    assert kernels(p) == ["k_attn_step_k3"]
+    st = p.steps[0]
+    assert st.kind == "attn_step" and st.grid == (256, 1, 1) and st.block == (512, 1, 1)
+    assert st.params["nsplit"] == 9 and st.args["nchunk"] == 9 and st.args["rows"] == 11 and st.args["resid"] is None
+    assert st.params["replaces"] == ["k_qkv_rope_k1536", "k_attn_flash_w8", "k_gemv_attn16_bias_r2"]
+    assert st.params["exchange_words"] == 12 * 3 * 128 + 12 * 9 * 132 + 12 * 128 + 2
+    assert set(p.stats["mutated_inputs"]) == {"past_key_0", "past_value_0"}
+    assert p.output_views["index_copy"].storage == "past_key_0"
+    # long caches: 16 slots walking up to 32 chunks each; the separate-combine list is fused too
+    long = compile_subgraph(build_attention_ir(40000))
+    assert kernels(long) == ["k_attn_step_k3"] and long.steps[0].params["nsplit"] == 16
+    assert long.steps[0].params["replaces"][2:] == ["k_attn_combine", "k_gemv_bias_r1"]
+    # past 16 x 32 chunks, or off the kernel's shapes (hidden 2048), the launch list stays
+    assert len(compile_subgraph(build_attention_ir(65537)).steps) > 1
+    assert len(compile_subgraph(build_attention_ir(700, QwenConfig(hidden=2048, heads=16, kv_heads=2))).steps) == 3
+
+
+def test_attention_slots_leave_room_for_the_combine_and_o_proj():
+    for S in (1, 128, 129, 1025, 2048, 4096, 65536):
+        n = persistent.attention_slots(S, 1536, 12)
+        nchunk = -(-S // 128)
+        assert n == min(nchunk, 16) and -(-nchunk // n) <= 32
+        nd = 256 - 12 * n
+        assert nd > 12 and -(-1536 // nd) <= persistent.AST_ROWS
+    assert persistent.attention_slots(65537, 1536, 12) is None
+    # 20 heads, hidden 2560: 12 slots leave 16 workgroups (fewer than the 20 combines), 9 leave 76
+    # (34 o_proj rows each, more than 32); 8 leave 96 (27 rows)
+    assert persistent.attention_slots(4096, 2560, 20) == 8
+
+
+def test_attention_block_is_three_launches_with_inplace_cache():
+    # the launch list: 128-position splits (8 waves), combined in the o_proj prologue
+    p = compile_subgraph(build_attention_ir(1025), persistent=False)
     assert kernels(p) == ["k_qkv_rope_k1536", "k_attn_flash_w8", "k_gemv_attn16_bias_r2"]
     flash = p.steps[1]
     assert flash.args["nsplit"] == 9 and flash.block == (512, 1, 1) and flash.grid == (9, 2, 6)
     assert p.steps[2].args["attn_splits"] == 9 and p.steps[2].args["attn_heads"] == 12
     # up to 8 splits: the 8-split prologue
-    short = compile_subgraph(build_attention_ir(256))
+    short = compile_subgraph(build_attention_ir(256), persistent=False)
     assert kernels(short) == ["k_qkv_rope_k1536", "k_attn_flash_w8", "k_gemv_attn_bias_r2"]
     # 2048 < S <= 4096: 256-position splits (16 waves), at most 16 of them
-    mid = compile_subgraph(build_attention_ir(4096))
+    mid = compile_subgraph(build_attention_ir(4096), persistent=False)
     assert kernels(mid) == ["k_qkv_rope_k1536", "k_attn_flash_w16", "k_gemv_attn16_bias_r2"]
     assert mid.steps[1].args["nsplit"] == 16 and mid.steps[1].block == (1024, 1, 1)
     # separate combine kernel: 64-position splits
-    sep = compile_subgraph(build_attention_ir(1025), fold_attention=False)
+    sep = compile_subgraph(build_attention_ir(1025), fold_attention=False, persistent=False)
     assert kernels(sep) == ["k_qkv_rope_k1536", "k_attn_flash", "k_attn_combine", "k_gemv_bias_r1"]
     assert sep.steps[1].args["nsplit"] == 17
     # more than 16 splits of 256 do not fit the prologue: the separate combine is kept, and
     # beyond 32 splits each split checks its mask before reading K / V
-    long = compile_subgraph(build_attention_ir(4097))
+    long = compile_subgraph(build_attention_ir(4097), persistent=False)
     assert kernels(long) == ["k_qkv_rope_k1536", "k_attn_flash_chk", "k_attn_combine", "k_gemv_bias_r1"]
     assert set(p.stats["mutated_inputs"]) == {"past_key_0", "past_value_0"}
     assert p.output_views["index_copy"].storage == "past_key_0"

@@ -32,7 +32,8 @@ def close(got, ref, rtol=RTOL):
     return err / scale
 
 
-def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True, exact=False, fold=None):
+def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=True, exact=False, fold=None,
+            persistent=None):
     from hip_compiler import compile_subgraph, is_hip_op_supported
     from npu_compiler import partition
     from npu_runtime import DAGExecutor
@@ -40,7 +41,7 @@ def run_hip(ir, inputs, weights, backend, supported=None, force_cpu=(), fuse=Tru
     fn = supported or (lambda op, a=None: is_hip_op_supported(op, a) and op not in force_cpu)
     ex = DAGExecutor(partition(ir, fn), backend,
                      compile_fn=lambda sub: compile_subgraph(sub, fuse=fuse, exact_attention=exact,
-                                                             fold_attention=fold))
+                                                             fold_attention=fold, persistent=persistent))
     ex.load_weights(weights)
     out = ex.execute(inputs)
     return {k: (v if isinstance(v, np.ndarray) else v.to_numpy()) for k, v in out.items()}, ex
@@ -85,8 +86,11 @@ def test_mlp_block_cfg1(backend, tokens):
         close(got[name], run_ir(ir, x, w)[name])
 
 
-@pytest.mark.parametrize("exact", [False, True])
-def test_attention_block_cfg2(backend, exact):
+@pytest.mark.parametrize("mode", ["step", "list", "exact"])
+def test_attention_block_cfg2(backend, mode):
+    """cfg2 through its three lowerings: ``step`` the default one-launch block (k_attn_step),
+    ``list`` the launch list it replaces (q/k/v + RoPE + cache rows, flash, combine + o_proj),
+    ``exact`` the two-pass attention that repeats every CPU rounding point."""
     from irgen.qwen import build_attention_ir
     from irgen.workloads import attention_inputs, make_weights
     from oracle.numpy_ref import run_ir
@@ -94,8 +98,13 @@ def test_attention_block_cfg2(backend, exact):
     ir = build_attention_ir(1025)
     w = host(make_weights(ir))
     x = host(attention_inputs(1025))
-    got, ex = run_hip(ir, x, w, backend, exact=exact)
+    print(f"[case] attention block cfg2 {mode}", flush=True)
+    got, ex = run_hip(ir, x, w, backend, exact=mode == "exact", persistent=mode == "step")
     assert_all_npu(ex)
+    kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
+    assert (kernels == ["k_attn_step_k3"]) == (mode == "step"), kernels
+    for h in ex._npu_executors.values():
+        h.check()   # no workgroup of the one-launch block timed out
     ref = run_cpu(ir, x, w)
     orc = run_ir(ir, x, w)
     for k in got:
@@ -109,14 +118,15 @@ def test_attention_block_cfg2(backend, exact):
             assert np.array_equal(got[k][:, :, keep], src[:, :, keep])
 
 
-@pytest.mark.parametrize("mode", ["split", "fold", "exact"])
+@pytest.mark.parametrize("mode", ["split", "fold", "exact", "step"])
 @pytest.mark.parametrize("valid", [1, 10, 64, 65, 257, 1000])
 def test_decode_attention_kernel_vs_closed_form(backend, valid, mode):
     """The fused split-KV kernel against the closed form of tests/test_extended_kernels.py:621-640.
 
     ``split``: 64-position splits and a combine kernel; ``fold``: 128-position splits whose
     combine runs in the o_proj prologue (valid=1 leaves 7 of the 8 splits fully masked);
-    ``exact``: the two-pass path that repeats every CPU rounding point."""
+    ``exact``: the two-pass path that repeats every CPU rounding point; ``step``: the one-launch
+    block (k_attn_step: 8 slots of 128 positions, those the mask closes skipped)."""
     from irgen.qwen import QwenConfig, build_attention_ir
     from irgen.workloads import attention_inputs, decode_mask, make_weights
     from oracle.numpy_ref import run_ir
@@ -130,21 +140,26 @@ def test_decode_attention_kernel_vs_closed_form(backend, valid, mode):
     x["position_ids"][:] = valid - 1
     x["cache_position"][:] = valid - 1
     x = host(x)
-    got, ex = run_hip(ir, x, w, backend, exact=mode == "exact", fold=mode == "fold")
+    print(f"[case] decode attention {mode} valid {valid}", flush=True)
+    got, ex = run_hip(ir, x, w, backend, exact=mode == "exact", fold=mode == "fold", persistent=mode == "step")
     kernels = {st.kernel for p in ex.npu_programs.values() for st in p.steps}
     if mode == "fold":
         assert "k_attn_flash_w8" in kernels and "k_attn_combine" not in kernels
     elif mode == "split":
         assert "k_attn_flash" in kernels and "k_attn_combine" in kernels
+    elif mode == "step":
+        assert kernels == {"k_attn_step_k3"}
     orc = run_ir(ir, x, w)
     for k in got:
         if not k.startswith("index_copy"):
             close(got[k], orc[k])
 
 
+@pytest.mark.parametrize("step", [False, True])
 @pytest.mark.parametrize("valid", [5, 1500, 3000])
-def test_decode_attention_wide_splits_vs_closed_form(backend, valid):
-    """S = 3000: 256-position splits (16 waves), 12 of them, folded by the 16-split o_proj prologue."""
+def test_decode_attention_wide_splits_vs_closed_form(backend, valid, step):
+    """S = 3000: 256-position splits (16 waves), 12 of them, folded by the 16-split o_proj prologue;
+    or (``step``) the one-launch block, 16 slots over 24 chunks of 128 (8 slots fold two)."""
     from irgen.qwen import QwenConfig, build_attention_ir
     from irgen.workloads import attention_inputs, decode_mask, make_weights
     from oracle.numpy_ref import run_ir
@@ -157,9 +172,13 @@ def test_decode_attention_wide_splits_vs_closed_form(backend, valid):
     x["position_ids"][:] = valid - 1
     x["cache_position"][:] = valid - 1
     x = host(x)
-    got, ex = run_hip(ir, x, w, backend)
+    print(f"[case] wide decode attention valid {valid} step {step}", flush=True)
+    got, ex = run_hip(ir, x, w, backend, persistent=step)
     kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
-    assert "k_attn_flash_w16" in kernels and "k_gemv_attn16_bias_r2" in kernels
+    if step:
+        assert kernels == ["k_attn_step_k3"]
+    else:
+        assert "k_attn_flash_w16" in kernels and "k_gemv_attn16_bias_r2" in kernels
     orc = run_ir(ir, x, w)
     for k in got:
         if not k.startswith("index_copy"):
