@@ -348,14 +348,14 @@ def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
     tr = torch.zeros(nwg * (L * 16 + 8), dtype=torch.int64, device=hexec.device)
     s = hexec._structs[0]
     s.trace = tr.data_ptr()
-    hexec.use_graph = False
+    use_graph, hexec.use_graph = hexec.use_graph, False
     try:
         for _ in range(steps):
             ex.execute(state)
         torch.cuda.synchronize()
     finally:
         s.trace = None
-        hexec.use_graph = True
+        hexec.use_graph = use_graph
     t = tr.cpu().numpy().reshape(nwg, L * 16 + 8).astype(np.float64) * 0.01   # 10 ns ticks -> µs
     t -= t[:, L * 16 + 7].min()
     b = np.arange(nwg)

@@ -400,7 +400,8 @@ struct PersistArgs {
   int* adv_flag;              // [0]: a step ran past the cache end
   int adv_mask_bytes, adv_pad;
   int nchunk;                 // 128-position chunks of the cache: ceil(S / 128), at most 32 per slot
-  int rbo, rba;               // gate / up rows streamed through registers per o_proj / attention workgroup
+  int rbo, rba, rbc;          // gate / up rows streamed through registers per o_proj / attention / combine
+                              // workgroup
   int rows;                   // the attention step's o_proj rows per workgroup (unused by the decode step)
   int* host_err;              // null, or a host-visible word set to 1 when a wait times out
   // the one-block attention step (k_attn_step_k*): its input row, output row and residual row

@@ -629,11 +629,13 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   // the attention row); none on a combine workgroup, whose partials poll comes sooner
   const int NEO = max(2 * NE - RD, 0) / 2;
   const int NLC = att ? NE : (comb ? 0 : NEO);
-  // gate / up rows streamed: RBO by an o_proj workgroup (its stream starts only after o_proj), RBA
-  // by an attention workgroup (the host's work split of the rows not held in LDS)
-  const int RBO = a.rbo, RBA = a.rba;
+  // gate / up rows streamed (the host's work split of the rows not held in LDS): RBA by an
+  // attention workgroup, RBO by an o_proj workgroup (its stream starts only after o_proj), RBC by
+  // a combine workgroup (fewer: it runs the combine before its o_proj rows, and with RBO rows it
+  // published h and the next layer's rows last)
+  const int RBA = a.rba, RBC = a.rbc, RBO = comb ? RBC : a.rbo;
   const int e0 = att ? b * (NE + RBA)                                   // first gate / up row
-                     : NB * (NE + RBA) + (b - NB) * RBO + max(b - NB - H, 0) * NEO;
+                     : NB * (NE + RBA) + min(b - NB, H) * RBC + max(b - NB - H, 0) * (a.rbo + NEO);
   const int ecnt = max(min(NLC + (att ? RBA : RBO), a.inter - e0), 0);  // its rows
   const int NL = min(NLC, ecnt);                                        // of which in LDS
   const unsigned EOFF = att ? 0u : (unsigned)(RD * KC * 1024);          // where they sit in ebuf

@@ -55,6 +55,11 @@ RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}   # kernel instances: gate/up 
 # rest (Qwen2.5-1.5B at 2048 positions: 11, and 16 per attention workgroup, 0.724 ms per step; the
 # even split, 15 and 15: 0.733; 12: 0.725; 13-14: 0.734)
 O_RING_MAX = 11
+# gate/up rows a combine workgroup streams fewer than an o_proj workgroup: it waits for its head's
+# partials and runs the combine before its o_proj, so with the o_proj workgroups' share its h and
+# the next layer's rows were the last published (Qwen2.5-1.5B at 2048 positions: 11 - 4 = 7,
+# 0.670 ms per step against 0.673 with 11; 5 or 3 with one row more per o_proj workgroup: 0.674)
+C_RING_LESS = 4
 OSTAGE = 128         # decode.hip DEC_OSTAGE: a workgroup's gate/up rows, staged
 
 TABLE_FIELDS = ("norm1", "wq", "bq", "wk", "bk", "wv", "bv", "kc", "vc", "wo", "norm2", "wg", "wu", "wd")
@@ -93,8 +98,9 @@ def work_split(hidden: int, inter: int, H: int, nslot: int) -> dict | None:
     """The kernel's division of a layer among the NWG workgroups (decode.hip ``decode_body``): NB
     attention workgroups (each also holds NE gate/up rows in LDS), ND o_proj workgroups of RD rows
     (those that run no combine also hold NEO gate/up rows in LDS); the gate/up rows left over are
-    streamed through registers, RBO by each o_proj workgroup and RBA by each attention workgroup;
-    EM is the kernel instance's register rows per wave. None when no instance fits."""
+    streamed through registers, RBO by each o_proj workgroup that runs no combine, RBC by each of
+    the H combine workgroups and RBA by each attention workgroup; EM is the kernel instance's
+    register rows per wave. None when no instance fits."""
     KC = hidden // 512
     NB, NE = H * nslot, E_LDS_ROWS[KC]
     ND = NWG - NB
@@ -108,12 +114,13 @@ def work_split(hidden: int, inter: int, H: int, nslot: int) -> dict | None:
     cap = 8 * max(RING_ROWS[KC])
     RBO = min(-(-ring // NWG), O_RING_MAX)
     RBO = max(RBO, -(-max(ring - NB * cap, 0) // ND))   # what the attention workgroups cannot take
-    RBA = -(-max(ring - ND * RBO, 0) // NB)
+    RBC = max(RBO - C_RING_LESS, 0)
+    RBA = -(-max(ring - (ND - H) * RBO - H * RBC, 0) // NB)
     RB = max(RBA, RBO)
     em = [e for e in RING_ROWS[KC] if 8 * e >= RB]
     if not em or max(NE, NEO) + RB > OSTAGE:
         return None
-    return dict(NB=NB, NE=NE, ND=ND, RD=RD, NEO=NEO, RBO=RBO, RBA=RBA, EM=em[0])
+    return dict(NB=NB, NE=NE, ND=ND, RD=RD, NEO=NEO, RBO=RBO, RBC=RBC, RBA=RBA, EM=em[0])
 
 
 def _parse_layers(steps: list[LaunchStep]):
@@ -262,7 +269,7 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
         mask_dtype=int(f0["mask_dtype"]) if mask is not None else -1, add_dtype=int(f0.get("add_dtype", 2)),
         n_dtype=int(q0["n_dtype"]), out_dtype=int(fa["out_dtype"]), flags=1 if int(q0["flags"]) & 2 else 0,
         eps=float(q0["eps"]), eps_f=float(la["eps"]), scale=float(f0["scale"]),
-        rope_scaling=float(q0["rope_scaling"]), nchunk=-(-S // SPL), rbo=ws["RBO"], rba=ws["RBA"])
+        rope_scaling=float(q0["rope_scaling"]), nchunk=-(-S // SPL), rbo=ws["RBO"], rba=ws["RBA"], rbc=ws["RBC"])
     inputs = sorted({t for st in steps for t in st.inputs})
     outputs = [t for st in steps for t in st.outputs]
     step = LaunchStep(

@@ -39,7 +39,7 @@ _struct("PersistArgs", [("layers", P), ("emb", P), ("ids", P), ("pos_ids", P), (
                         ("out_dtype", I), ("flags", I), ("eps", F), ("eps_f", F), ("scale", F),
                         ("rope_scaling", F), ("adv_mask", P), ("adv_pos", P), ("adv_cpos", P), ("adv_flag", P),
                         ("adv_mask_bytes", I), ("adv_pad", I), ("nchunk", I), ("rbo", I), ("rba", I),
-                        ("rows", I), ("host_err", P), ("xin", P), ("out", P), ("resid", P)])
+                        ("rbc", I), ("rows", I), ("host_err", P), ("xin", P), ("out", P), ("resid", P)])
 _struct("CopyArgs", [("dst", P), ("src", P), ("n", LL), ("shape", LL * 6), ("sstride", LL * 6),
                      ("dstride", LL * 6), ("ndim", I), ("sdtype", I), ("ddtype", I), ("pad", I)])
 _struct("FillArgs", [("out", P), ("n", LL), ("value", C.c_double), ("dtype", I), ("pad", I)])

@@ -381,9 +381,10 @@ def test_persistent_step_covers_long_and_ragged_caches(S):
     rows = []
     for b in range(P.NWG):
         att, comb = b < NB, NB <= b < NB + H
-        e0 = b * (NE + ws["RBA"]) if att else NB * (NE + ws["RBA"]) + (b - NB) * ws["RBO"] + max(b - NB - H, 0) * NEO
+        e0 = (b * (NE + ws["RBA"]) if att else
+              NB * (NE + ws["RBA"]) + min(b - NB, H) * ws["RBC"] + max(b - NB - H, 0) * (ws["RBO"] + NEO))
         nlc = NE if att else (0 if comb else NEO)
-        ecnt = max(min(nlc + (ws["RBA"] if att else ws["RBO"]), cfg.intermediate - e0), 0)
+        ecnt = max(min(nlc + (ws["RBA"] if att else (ws["RBC"] if comb else ws["RBO"])), cfg.intermediate - e0), 0)
         rows += range(e0, e0 + ecnt)
         assert ecnt - min(nlc, ecnt) <= 8 * ws["EM"]
     assert sorted(rows) == list(range(cfg.intermediate))

@@ -258,6 +258,8 @@ def test_executor_keeps_one_graph_per_pointer_set(backend):
     ir = build_decode_ir(256, cfg, argmax=True)
     ex = DAGExecutor(partition(ir, is_hip_op_supported), backend, compile_fn=compile_subgraph)
     ex.load_weights(make_weights(ir, cfg, device="cuda"))
+    (hexec,) = ex._npu_executors.values()
+    hexec.use_graph = True   # (a one-launch program is launched directly by default)
     st = {k: backend.allocate_buffer(v.clone()) for k, v in decode_inputs(256, 100, cfg).items()}
     a = backend.allocate_buffer(torch.tensor([[11]]))
     b = backend.allocate_buffer(torch.tensor([[3000]]))
@@ -267,7 +269,6 @@ def test_executor_keeps_one_graph_per_pointer_set(backend):
         print("[case] graph per pointer set", flush=True)
         out = ex.execute({**st, "input_ids": ids})
         runs.append(out[lname].to_torch().clone())
-    (hexec,) = ex._npu_executors.values()
     assert len(hexec._graphs) == 2
     assert torch.equal(runs[0], runs[2])
     assert not torch.equal(runs[0], runs[1])
