@@ -972,12 +972,16 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   }
 
   // ---- G: final RMSNorm, lm_head, logits and argmax keys -------------------------------------------
+  // The vocabulary goes in rounds of 8 R4 rows, round k of workgroup b being rows (k NWG + b) 8 R4 ..:
+  // at any time the workgroups stream one contiguous window of the matrix. (Each workgroup's own
+  // contiguous 1/NWG of it took 67.2 us per step at Qwen2.5-1.5B's 467 MB, its slowest workgroup
+  // 71.0; interleaved: 63.8 and 67.0.)
   {
-      DEC_PART_IDS();
+    DEC_PART_IDS();
     uint32_t* XF = a.ll + X.stride * a.L;
-    const long long V = a.vocab, RB = (V + NWG - 1) / NWG, r0 = (long long)b * RB;
-    const long long rend = min(r0 + RB, V);
     constexpr int R4 = DEC_R4;   // rows per wave per round; two rounds in flight
+    const long long V = a.vocab, r0 = (long long)b * DEC_WAVES * R4, rend = V;
+    const long long GSTEP = (long long)NWG * DEC_WAVES * R4;
     uint4 wc[R4][KC], wn[R4][KC];
     auto issue = [&](uint4 (&w)[R4][KC], long long base) {
 #pragma unroll
@@ -995,9 +999,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     DEC_STAMP(a.L, 1);
     block_norm(xres, nw, hid, a.eps_f, a.n_dtype, xs, red, tid);
     unsigned long long best = 0ull;
-    for (long long base = r0; base < rend; base += (long long)DEC_WAVES * R4) {
-      const bool more = base + (long long)DEC_WAVES * R4 < rend;
-      if (more) issue(wn, base + (long long)DEC_WAVES * R4);
+    for (long long base = r0; base < rend; base += GSTEP) {
+      const bool more = base + GSTEP < rend;
+      if (more) issue(wn, base + GSTEP);
 #pragma unroll
       for (int i = 0; i < R4; ++i) {
         const long long r = base + wave + (long long)DEC_WAVES * i;
