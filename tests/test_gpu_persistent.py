@@ -173,6 +173,49 @@ def test_persistent_greedy_loop_follows_launch_list_and_wraps_step_tags(backend)
     assert runs[True]["toks"] == runs[False]["toks"]
 
 
+def test_one_launch_program_runs_without_a_graph_and_matches_the_graph_launch(backend):
+    """A one-launch program (the persistent step) is launched directly by default; the same
+    device-resident greedy loop, its inputs advanced inside the step, launched through a captured
+    HIP graph instead, gives the same tokens and bit-identical logits at every step."""
+    from irgen.qwen import QwenConfig, build_decode_ir
+    from irgen.workloads import decode_inputs, make_weights
+
+    cfg = QwenConfig(hidden=512, intermediate=1024, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=4096)
+    S, start, n = 256, 30, 8
+    ir = build_decode_ir(S, cfg, argmax=True)
+    w = make_weights(ir, cfg, device="cuda")
+    kv_in = [g["name"] for g in ir["graph_inputs"][4:]]
+    kv_out = [o["name"] for o in ir["graph_outputs"][1:-1]]
+    lg = ir["graph_outputs"][0]["name"]
+    runs = {}
+    for graph in (False, True):
+        ex = _executor(ir, backend, True)
+        ex.load_weights(w)
+        h = _hexec(ex)
+        assert h.use_graph is False   # the default for one launch
+        h.use_graph = graph
+        state = {k: backend.allocate_buffer(v) for k, v in decode_inputs(S, start, cfg, device="cuda").items()}
+        adv = backend.decode_advance(state["attention_mask"], state["position_ids"], state["cache_position"])
+        assert h.fold_advance(adv)
+        toks, logits = [], []
+        for s in range(n):
+            print(f"[case] one-launch loop graph={graph} step {s}", flush=True)
+            out = ex.execute(state)
+            toks.append(int(out["next_token"].native_handle.reshape(-1)[0].item()))
+            logits.append(out[lg].native_handle.clone())
+            state["input_ids"] = out["next_token"]
+            for i, o in zip(kv_in, kv_out):
+                state[i] = out[o]
+        torch.cuda.synchronize()
+        adv.check()
+        h.check()
+        assert (len(h._graphs) > 0) == graph   # graphs captured only when asked for
+        runs[graph] = (toks, logits)
+    assert runs[True][0] == runs[False][0]
+    for a, b in zip(runs[True][1], runs[False][1]):
+        assert torch.equal(a, b)
+
+
 def test_folded_advance_matches_separate_launches_and_reports_the_cache_end(backend):
     """``HIPExecutor.fold_advance``: the persistent step moves its own position inputs after each
     step. A greedy loop run that way gives the same tokens and bit-identical logits as the same
