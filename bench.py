@@ -344,7 +344,7 @@ def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
 
     (st,) = hexec.program.steps
     nwg, H, nsplit = int(st.grid[0]), int(st.args["H"]), int(st.args["nsplit"])
-    NB = H * nsplit
+    NB = (int(st.args["KVH"]) if st.params.get("kv_major") else H) * nsplit
     tr = torch.zeros(nwg * (L * 16 + 8), dtype=torch.int64, device=hexec.device)
     s = hexec._structs[0]
     s.trace = tr.data_ptr()

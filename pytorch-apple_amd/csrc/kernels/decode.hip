@@ -510,6 +510,223 @@ __device__ __forceinline__ void dec_attend(const PersistArgs& a, int l, uint16_t
   }
 }
 
+// ---- B, KV-head-major (long caches): the G query heads of one KV head over the open chunks of its slot
+// The head-major form gives every query head its own workgroups, so the G heads of a KV head each
+// read its K / V rows (from L2 after the first); over a long cache that is G times the rows per
+// workgroup (Qwen2.5-1.5B at 32,768 positions: 1 MB per workgroup and layer, ≈ 28 µs at the rate
+// one CU reads). Here workgroup (KV head, slot) reads each of its rows once and scores them for all
+// G heads: per chunk the K and V rows are loaded as in dec_attend, and each head keeps its own
+// running (max, sum, output) per wave. One partial per (query head, slot) as in dec_attend.
+// qw: the KV head's G exchange blocks [q_h | k | v] (one contiguous range); partw: the layer's
+// partials (query head h, slot s at (h NT + s) (D + 4)); osh: G x 8 waves x D floats of free LDS.
+__device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint16_t* kcache, uint16_t* vcache,
+                                              const uint32_t* qw, uint32_t* partw, uint32_t ob, int kvh, int slot,
+                                              long long cpos, uint32_t tag, uint32_t* err, unsigned char* smem,
+                                              float* osh, const float* rope_cs, float* red, float* red2, int tid,
+                                              int lane, int wave) {
+  const int NT = a.nsplit, G = a.H / a.KVH;
+  const long long S = a.S, last = S - 1, kvs = a.kv_head_stride;
+  const int kq = lane >> 2, kc = lane & 3;
+  uint16_t* raw = (uint16_t*)smem;                             // [G][3 D]: the G blocks as produced
+  uint16_t* rot = (uint16_t*)(smem + G * 3 * DEC_D * 2);       // [G + 1][D]: each head's rotated q, then k
+  const float* csh = rope_cs;
+  const uint16_t* Kb = kcache + (long long)kvh * kvs;
+  const uint16_t* Vb = vcache + (long long)kvh * kvs;
+  const bool cin = cpos >= 0 && cpos < S;
+  float acc0[DEC_MAXG], acc1[DEC_MAXG], mw[DEC_MAXG], lw[DEC_MAXG];
+#pragma unroll
+  for (int g = 0; g < DEC_MAXG; ++g) {
+    acc0[g] = acc1[g] = lw[g] = 0.f;
+    mw[g] = -INFINITY;
+  }
+  auto rope = [&]() {   // rotate_half RoPE of the G q rows and the k row
+    for (int i = tid; i < (G + 1) * 64; i += DEC_THREADS) {
+      const int hs = i >> 6, j = i & 63;
+      const uint16_t* src = hs < G ? raw + hs * 3 * DEC_D : raw + DEC_D;
+      const float x0 = bfh(src[j]), x1 = bfh(src[j + 64]);
+      const float c = csh[j], sn = csh[64 + j];
+      rot[hs * DEC_D + j] = f32_to_bf16(rb(rb(x0 * c) + rb(-x1 * sn)));
+      rot[hs * DEC_D + j + 64] = f32_to_bf16(rb(rb(x1 * c) + rb(x0 * sn)));
+    }
+    __syncthreads();
+    // this step's K / V row into the caches, by the workgroup of the slot that holds the position
+    if (cin && (int)((cpos / DEC_SPL) % NT) == slot && tid < DEC_D) {
+      stg2(kcache + (long long)kvh * kvs + cpos * DEC_D + tid, rot[G * DEC_D + tid]);
+      stg2(vcache + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
+    }
+  };
+  // one chunk folded into every head's running softmax (dec_attend's fold, per head)
+  auto fold = [&](const uint4 (&kin)[4], const uint32_t (&vr)[16], FRaw mraw, long long p0) {
+    uint4 kr[4] = {kin[0], kin[1], kin[2], kin[3]};
+    const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
+    const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
+    if (vnew && p0 + kq == cpos) {
+      const uint4* kn = (const uint4*)(rot + G * DEC_D + kc * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kr[j] = kn[j];
+    }
+    const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
+    const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
+    const bool live = __ballot(mval != -INFINITY) != 0ull;
+    if (!live) return;
+#pragma unroll
+    for (int g = 0; g < DEC_MAXG; ++g) {
+      if (g < G) {   // workgroup-uniform
+        const uint4* qq = (const uint4*)(rot + g * DEC_D + kc * 32);
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 q4 = qq[j];
+          d = ddot2(q4.x, kr[j].x, d);
+          d = ddot2(q4.y, kr[j].y, d);
+          d = ddot2(q4.z, kr[j].z, d);
+          d = ddot2(q4.w, kr[j].w, d);
+        }
+        d += HS_DPP(d, HS_QUAD_XOR1);
+        d += HS_DPP(d, HS_QUAD_XOR2);
+        float sc = -INFINITY;
+        if (mval != -INFINITY) {
+          sc = rb(d);
+          sc = rb(sc * a.scale);
+          if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
+        }
+        float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
+        m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
+        m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
+        const float mn = fmaxf(mw[g], m);
+        const float al = (mw[g] == -INFINITY) ? 0.f : __expf(mw[g] - mn);
+        const float e = (sc == -INFINITY) ? 0.f : __expf(sc - mn);
+        float ls = e + HS_DPP(e, HS_ROW_ROR4);
+        ls += HS_DPP(ls, HS_ROW_ROR8);
+        lw[g] = lw[g] * al + ((HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48)));
+        mw[g] = mn;
+        float o0 = acc0[g] * al, o1 = acc1[g] * al;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const float p = HS_RL(e, 4 * t);
+          const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
+          o0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), o0);
+          o1 = fmaf(p, bfh((uint16_t)(vt >> 16)), o1);
+        }
+        acc0[g] = o0;
+        acc1[g] = o1;
+      }
+    }
+  };
+  if (ob != 0) {   // workgroup-uniform
+    uint32_t rest = ob & (ob - 1);
+    const long long q0 = (long long)(slot + NT * __builtin_ctz(ob)) * DEC_SPL + wave * 16;
+    uint4 kr[4];
+    FRaw mraw = {0, 0};
+    if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(q0 + kq, last), a.mask_dtype);
+    const uint4* ks = (const uint4*)(Kb + min(q0 + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
+    __syncthreads();
+    xgather<3>(qw, G * 3 * DEC_D, tag, raw, err, a.host_err, tid);
+    DEC_STAMP(l, 3);
+    uint32_t vr[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(q0 + t, last) * DEC_D + 2 * lane);
+    rope();
+    fold(kr, vr, mraw, q0);
+    while (rest != 0) {   // workgroup-uniform
+      const long long pc = (long long)(slot + NT * __builtin_ctz(rest)) * DEC_SPL + wave * 16;
+      rest &= rest - 1;
+      uint4 kr2[4];
+      uint32_t vr2[16];
+      FRaw m2 = {0, 0};
+      if (a.mask_dtype >= 0) m2 = ld_f_raw(a.mask, min(pc + kq, last), a.mask_dtype);
+      const uint4* ks2 = (const uint4*)(Kb + min(pc + kq, last) * DEC_D + kc * 32);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) kr2[j] = ldg16(ks2 + j);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) vr2[t] = ldg4(Vb + min(pc + t, last) * DEC_D + 2 * lane);
+      fold(kr2, vr2, m2, pc);
+    }
+  } else {   // every chunk of this slot is closed: empty partials
+    __syncthreads();
+    xgather<3>(qw, G * 3 * DEC_D, tag, raw, err, a.host_err, tid);
+    DEC_STAMP(l, 3);
+    rope();
+  }
+#pragma unroll
+  for (int g = 0; g < DEC_MAXG; ++g) {
+    if (g < G) {
+      osh[(g * DEC_WAVES + wave) * DEC_D + 2 * lane] = acc0[g];
+      osh[(g * DEC_WAVES + wave) * DEC_D + 2 * lane + 1] = acc1[g];
+      if (lane == 0) {
+        red[wave * 8 + g] = mw[g];
+        red2[wave * DEC_MAXG + g] = lw[g];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < G * (DEC_D + 4); i += DEC_THREADS) {
+    const int g = i / (DEC_D + 4), e = i - g * (DEC_D + 4);
+    float M = -INFINITY;
+#pragma unroll
+    for (int w8 = 0; w8 < DEC_WAVES; ++w8) M = fmaxf(M, red[w8 * 8 + g]);
+    float o = 0.f, L = 0.f;
+#pragma unroll
+    for (int w8 = 0; w8 < DEC_WAVES; ++w8) {
+      const float lv = red2[w8 * DEC_MAXG + g];
+      const float f = lv > 0.f ? __expf(red[w8 * 8 + g] - M) : 0.f;
+      o = fmaf(f, osh[(g * DEC_WAVES + w8) * DEC_D + min(e, DEC_D - 1)], o);
+      L = fmaf(f, lv, L);
+    }
+    const uint32_t mb = __float_as_uint(M), lb = __float_as_uint(L);
+    const int e2 = e - DEC_D;
+    const uint16_t v = e < DEC_D ? f32_to_bf16(L > 0.f ? o / L : 0.f)
+                                 : (uint16_t)(((e2 < 2 ? mb : lb) >> ((e2 & 1) ? 0 : 16)) & 0xFFFFu);
+    const int hq = kvh * G + g;
+    xput(partw + ((long long)hq * NT + slot) * (DEC_D + 4) + e, v, tag);
+  }
+  __syncthreads();   // osh is free LDS of the caller's, which it refills next
+}
+
+// ---- C with more slots than the staging area holds (KV-head-major: NT up to 128) -----------------------
+// All NT partials in one gather by the whole workgroup, into pl (free LDS of the caller's: NT (D + 4)
+// halves), then the combine as dec_combine (weights e^(m_t - M) l_t / L, the o rows summed in slot
+// order). cw: NT floats of LDS.
+__device__ __forceinline__ void dec_combine_big(const PersistArgs& a, int l, const uint32_t* partw, uint32_t* attw,
+                                                uint32_t tag, uint32_t* err, uint16_t* pl, float* cw, int tid,
+                                                int lane, int wave) {
+  const int NT = a.nsplit;
+  __syncthreads();
+  xgather<(128 * (DEC_D + 4) / 2 + DEC_THREADS - 1) / DEC_THREADS>(partw, NT * (DEC_D + 4), tag, pl, err, a.host_err,
+                                                                 tid);
+  DEC_STAMP(l, 5);
+  if (wave == 0) {
+    float M = -INFINITY;
+    for (int t = lane; t < NT; t += 64) {
+      const uint16_t* e = pl + t * (DEC_D + 4) + DEC_D;
+      const float m = __uint_as_float(((uint32_t)e[0] << 16) | e[1]), lv = __uint_as_float(((uint32_t)e[2] << 16) | e[3]);
+      M = fmaxf(M, lv > 0.f ? m : -INFINITY);
+    }
+    M = wave_max(M);
+    float L = 0.f;
+    for (int t = lane; t < NT; t += 64) {
+      const uint16_t* e = pl + t * (DEC_D + 4) + DEC_D;
+      const float m = __uint_as_float(((uint32_t)e[0] << 16) | e[1]), lv = __uint_as_float(((uint32_t)e[2] << 16) | e[3]);
+      const float f = lv > 0.f ? __expf(m - M) * lv : 0.f;
+      cw[t] = f;
+      L += f;
+    }
+    L = wave_sum(L);
+    for (int t = lane; t < NT; t += 64) cw[t] = L > 0.f ? cw[t] / L : 0.f;
+  }
+  __syncthreads();
+  if (wave < 4) {
+    const int d = tid >> 1, q = tid & 1;
+    float sacc = 0.f;
+    for (int t = q; t < NT; t += 2) sacc = fmaf(cw[t], bfh(pl[t * (DEC_D + 4) + d]), sacc);
+    sacc += HS_DPP(sacc, HS_QUAD_XOR1);
+    if (q == 0) xput(attw + d, f32_to_bf16(sacc), tag);
+  }
+  DEC_STAMP(l, 6);
+}
+
 // ---- C: combine the slot partials of one query head (waves 0-3, 2 threads per dimension) ----------
 // partw: the head's nsplit partials; attw: the head's D words of the attention row.
 __device__ __forceinline__ void dec_combine(const PersistArgs& a, int l, const uint32_t* partw, uint32_t* attw,
@@ -560,6 +777,7 @@ struct DecShared {
   __attribute__((aligned(16))) uint4 ebuf[NE * 2 * KC * 64];
   const void* ptab[2][14];   // the current and the next layer's tensors (DecodeLayerPtrs)
   unsigned long long kred[DEC_WAVES];
+  float cwk[128];            // the combine's slot weights (KV-head-major: up to 128 slots)
   uint32_t obw[DEC_WAVES];   // the open-chunk scan: each wave's bits
   // a part's results (o_proj rows, gate / up rows) staged here, then published with one store
   // instruction per 64 words: many single-word stores spread over the waves are acknowledged far
@@ -572,7 +790,7 @@ struct DecShared {
 // rows per workgroup, at most (2 KC: hidden rows over 256 workgroups); EM: gate/up rows per wave
 // streamed through registers, at most; ED: those rows in flight per wave; NE: gate/up rows an
 // attention workgroup loads into LDS once its attention part is done.
-template <int KC, int IC, int EM, int ROLE, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC), int RFE = DEC_RFE>
+template <int KC, int IC, int EM, int ROLE, bool KVM, int RF = 2 * KC, int ED = DEC_ED, int NE = DEC_NE(KC), int RFE = DEC_RFE>
 __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, NE>& sh) {
   auto& smem = sh.smem;
   auto& xres = sh.xres;
@@ -617,10 +835,12 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   // latency-bound parts well before x1 exists, so it spends that time loading NE gate / up rows
   // into LDS, and takes NE more gate / up rows than the others; the rest are spread so that every
   // workgroup has about the same left to stream once x1 has arrived.
+  // (KVM, the KV-head-major attention of long caches: workgroup b < NB = KVH nsplit takes KV head
+  // b / nsplit, slot b % nsplit, for all G query heads)
   const int ntile = KVH * NT;
-  const int NB = ntile * G, ND = NWG - NB;
+  const int NB = KVM ? ntile : ntile * G, ND = NWG - NB;
   constexpr bool att = ROLE == 0;   // (the kernel entry picks the role instance from b)
-  const int tile = b % ntile, gq = b / ntile;
+  const int tile = b % ntile, gq = KVM ? 0 : b / ntile;
   const int kvh = tile / NT, slot = tile % NT;
   constexpr bool comb = ROLE == 2;   // o_proj workgroups b in [NB, NB + H) also run the combine
   const int RD = (hid + ND - 1) / ND;                                   // <= 2 NE (checked on the host)
@@ -746,10 +966,15 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     // ---- B: attention of one query head over the open chunks of its slot ----------------------------
     if constexpr (att) {
       DEC_PART_IDS();
-      const int hq = kvh * G + gq;
-      dec_attend(a, l, P.kc, P.vc, XL + X.qkv + (long long)hq * 3 * DEC_D,
-                 XL + X.part + ((long long)hq * NT + slot) * (DEC_D + 4), ob, kvh, gq, slot, cpos, tag, err, smem,
-                 rope_cs, red, red2, tid, lane, wave);
+      if constexpr (KVM) {   // (ebuf: its gate / up rows are loaded after this part)
+        dec_attend_kv(a, l, P.kc, P.vc, XL + X.qkv + (long long)kvh * G * 3 * DEC_D, XL + X.part, ob, kvh, slot,
+                      cpos, tag, err, smem, (float*)&ebuf[0], rope_cs, red, red2, tid, lane, wave);
+      } else {
+        const int hq = kvh * G + gq;
+        dec_attend(a, l, P.kc, P.vc, XL + X.qkv + (long long)hq * 3 * DEC_D,
+                   XL + X.part + ((long long)hq * NT + slot) * (DEC_D + 4), ob, kvh, gq, slot, cpos, tag, err, smem,
+                   rope_cs, red, red2, tid, lane, wave);
+      }
       DEC_STAMP(l, 4);
       // this workgroup's first NL gate / up rows into LDS: its next wait (x1, in E) is some
       // microseconds away, and these land by then
@@ -764,9 +989,13 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     // ---- C: combine the slot partials of one query head ---------------------------------------------
     if (comb) {
       DEC_PART_IDS();
-      const int h = b - ntile * G;
-      dec_combine(a, l, XL + X.part + (long long)h * NT * (DEC_D + 4), XL + X.att + (long long)h * DEC_D, tag, err,
-                  smem, red2, tid, lane, wave);
+      const int h = b - NB;
+      if constexpr (KVM)   // (its partials staged behind its o_proj rows: a combine workgroup holds no gate / up rows)
+        dec_combine_big(a, l, XL + X.part + (long long)h * NT * (DEC_D + 4), XL + X.att + (long long)h * DEC_D, tag,
+                        err, (uint16_t*)((unsigned char*)ebuf + EOFF), sh.cwk, tid, lane, wave);
+      else
+        dec_combine(a, l, XL + X.part + (long long)h * NT * (DEC_D + 4), XL + X.att + (long long)h * DEC_D, tag, err,
+                    smem, red2, tid, lane, wave);
     }
 
     // ---- D: o_proj + residual (o_proj workgroups; the rows from LDS) ------------------------------------
@@ -1088,9 +1317,18 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   extern "C" __global__ void __launch_bounds__(DEC_THREADS) k_decode_step_k##KC##_i##IC##_e##EM(const PersistArgs a) { \
     __shared__ DecShared<KC, DEC_NE(KC)> sh; \
     const int nb_ = a.H * a.nsplit; \
-    if ((int)blockIdx.x < nb_) decode_body<KC, IC, EM, 0>(a, sh); \
-    else if ((int)blockIdx.x < nb_ + a.H) decode_body<KC, IC, EM, 2>(a, sh); \
-    else decode_body<KC, IC, EM, 1>(a, sh); \
+    if ((int)blockIdx.x < nb_) decode_body<KC, IC, EM, 0, false>(a, sh); \
+    else if ((int)blockIdx.x < nb_ + a.H) decode_body<KC, IC, EM, 2, false>(a, sh); \
+    else decode_body<KC, IC, EM, 1, false>(a, sh); \
+  }
+// KV-head-major attention (long caches): nsplit slots per KV head, KVH nsplit attention workgroups
+#define DECODE_KERNEL_KV(KC, IC, EM) \
+  extern "C" __global__ void __launch_bounds__(DEC_THREADS) k_decode_step_k##KC##_i##IC##_e##EM##_kv(const PersistArgs a) { \
+    __shared__ DecShared<KC, DEC_NE(KC)> sh; \
+    const int nb_ = a.KVH * a.nsplit; \
+    if ((int)blockIdx.x < nb_) decode_body<KC, IC, EM, 0, true>(a, sh); \
+    else if ((int)blockIdx.x < nb_ + a.H) decode_body<KC, IC, EM, 2, true>(a, sh); \
+    else decode_body<KC, IC, EM, 1, true>(a, sh); \
   }
 
 DECODE_KERNEL(3, 3, 2)   // hidden 1536 (Qwen2.5-1.5B: inter 8960, 12 heads x 16 slots: 16 streamed rows)
@@ -1100,6 +1338,8 @@ DECODE_KERNEL(3, 3, 6)   // hidden 1536, up to 48
 DECODE_KERNEL(1, 1, 1)   // hidden 512, up to 8
 DECODE_KERNEL(1, 1, 2)   // hidden 512, up to 16
 DECODE_KERNEL(2, 2, 4)   // hidden 1024, up to 32
+DECODE_KERNEL_KV(3, 3, 2)   // hidden 1536, KV-head-major attention
+DECODE_KERNEL_KV(1, 1, 1)   // hidden 512, KV-head-major attention
 
 // ================================================================ one attention block, one launch
 //

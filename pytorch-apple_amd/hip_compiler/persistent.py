@@ -55,6 +55,15 @@ RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}   # kernel instances: gate/up 
 # rest (Qwen2.5-1.5B at 2048 positions: 11, and 16 per attention workgroup, 0.724 ms per step; the
 # even split, 15 and 15: 0.733; 12: 0.725; 13-14: 0.734)
 O_RING_MAX = 11
+# caches from this length on take the KV-head-major attention (decode.hip dec_attend_kv): one
+# workgroup per (KV head, slot) scores all G query heads of the K / V rows it reads, G times fewer
+# bytes per workgroup than one workgroup per (query head, slot), at G head-folds per chunk and a
+# combine of G times more partials. Measured (Qwen2.5-1.5B, positions near the cache end, tok/s
+# KV-major / head-major): 8,192: 1,100 / 1,199; 16,384: 941 / 967; 32,768: 812 / 697. The kernel
+# instances that have it, by (KC, EM)
+KV_MAJOR_MIN_S = int(os.environ.get("HIPRT_DECODE_KV_MIN_S", "24577"))
+KV_MAJOR = {(3, 2), (1, 1)}
+MAX_KV_SLOTS = 128    # decode.hip DecShared::cwk (the combine's slot weights)
 # gate/up rows a combine workgroup streams fewer than an o_proj workgroup: it waits for its head's
 # partials and runs the combine before its o_proj, so with the o_proj workgroups' share its h and
 # the next layer's rows were the last published (Qwen2.5-1.5B at 2048 positions: 11 - 4 = 7,
@@ -203,6 +212,12 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     if sl is None:
         return None
     nsplit, ws = sl
+    # KV-head-major: the same NB attention workgroups as G nsplit slots per KV head
+    G = H // KVH
+    kvm = (S >= KV_MAJOR_MIN_S and (KC, ws["EM"]) in KV_MAJOR and G * nsplit <= MAX_KV_SLOTS
+           and -(-(-(-S // SPL)) // (G * nsplit)) <= MAX_CHUNKS_PER_SLOT)
+    if kvm:
+        nsplit = G * nsplit
     shared = ("pos_ids", "cache_pos", "inv_freq")
     x = ea["out"]
     table: list = []
@@ -252,7 +267,7 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     for r in table:
         if r is not None and storages[r.storage].kind not in ("input", "weight"):
             return None
-    kernel = f"k_decode_step_k{KC}_i{KC}_e{ws['EM']}"
+    kernel = f"k_decode_step_k{KC}_i{KC}_e{ws['EM']}" + ("_kv" if kvm else "")
     fit = resident_workgroups(kernel)
     if fit is not None and fit < NWG:
         return None
@@ -276,7 +291,8 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
         kind="decode_step", kernel=kernel, module="decode", arg_struct="PersistArgs",
         args=args, grid=(NWG, 1, 1), block=(THREADS, 1, 1), inputs=inputs, outputs=outputs,
         params={"table": {"field": "layers", "entries": table}, "layers": L, "nsplit": nsplit,
-                "replaces": [st.kernel for st in steps], "exchange_words": words, "work_split": ws})
+                "replaces": [st.kernel for st in steps], "exchange_words": words, "work_split": ws,
+                "kv_major": kvm})
     return [step]
 
 

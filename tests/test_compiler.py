@@ -390,6 +390,26 @@ def test_persistent_step_covers_long_and_ragged_caches(S):
     assert sorted(rows) == list(range(cfg.intermediate))
 
 
+def test_long_caches_take_the_kv_head_major_attention():
+    """From KV_MAJOR_MIN_S positions the step scores the G query heads of a KV head in one workgroup:
+    G times the slots (the same attention workgroups), G times the partials in the exchange area."""
+    import hip_compiler.persistent as P
+    from hip_compiler import compile_subgraph
+    from irgen.qwen import QwenConfig, build_decode_ir
+
+    cfg = QwenConfig(layers=1)
+    G = cfg.heads // cfg.kv_heads
+    steps = {S: compile_subgraph(build_decode_ir(S, cfg, argmax=True)).steps for S in (16384, 32768)}
+    (short,), (long_,) = steps[16384], steps[32768]
+    assert not short.kernel.endswith("_kv") and long_.kernel.endswith("_kv") and long_.params["kv_major"]
+    assert 16384 < P.KV_MAJOR_MIN_S <= 32768
+    ns = int(long_.args["nsplit"])
+    assert ns == G * P.MAX_SLOTS and cfg.kv_heads * ns == long_.params["work_split"]["NB"]
+    assert -(-int(long_.args["nchunk"]) // ns) <= P.MAX_CHUNKS_PER_SLOT
+    assert long_.params["exchange_words"] == P.exchange_words(1, cfg.hidden, cfg.intermediate, cfg.heads,
+                                                              cfg.kv_heads, ns)
+
+
 def test_persistent_step_rejects_caches_past_its_chunk_word():
     from hip_compiler import compile_subgraph
     from irgen.qwen import QwenConfig, build_decode_ir

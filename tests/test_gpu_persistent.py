@@ -51,6 +51,10 @@ def _executor(ir, backend, persistent):
     kernels = [s.kernel for s in prog.steps]
     if persistent:
         assert len(kernels) == 1 and kernels[0].startswith("k_decode_step_"), kernels
+        import hip_compiler.persistent as P
+
+        S = int(prog.steps[0].args["S"])
+        assert kernels[0].endswith("_kv") == (S >= P.KV_MAJOR_MIN_S), kernels   # KV-head-major for long caches
     else:
         assert len(kernels) > 1
     return ex
@@ -84,15 +88,26 @@ CASES = {
     # the reference's benchmark cache length: 17 open chunks of 256 (slot 0 folds two)
     "real_s32768_pos2048": (dict(layers=2), 32768, 2048),
     "real_s128": (dict(layers=1), 128, 77),
+    # KV-head-major attention (taken by default from 24,577 positions; these cases lower the
+    # threshold): 64 chunks over 96 slots per KV head (slots 64..95 hold none), the position in
+    # the last chunk
+    "real_s8192_pos8000_kv": (dict(layers=2), 8192, 8000),
+    # ragged: 40 chunks, the last one partial, the last position
+    "real_s5000_last_kv": (dict(layers=1), 5000, 4999),
+    # G = 2: 32 slots per KV head, 2 chunks each
+    "mini_s8192_pos6000_kv": (dict(hidden=512, intermediate=1024, layers=2, heads=4, kv_heads=2, head_dim=128, vocab=4096), 8192, 6000),
 }
 
 
 @pytest.mark.parametrize("case", sorted(CASES))
-def test_persistent_step_vs_cpu_fallback_and_launch_list(backend, case):
+def test_persistent_step_vs_cpu_fallback_and_launch_list(backend, case, monkeypatch):
+    import hip_compiler.persistent as P
     from irgen.qwen import QwenConfig, build_decode_ir
     from irgen.workloads import decode_inputs, make_weights
 
     kw, S, pos = CASES[case]
+    if case.endswith("_kv"):
+        monkeypatch.setattr(P, "KV_MAJOR_MIN_S", 4097)
     cfg = QwenConfig(**kw)
     ir = build_decode_ir(S, cfg, argmax=True)
     w = _host(make_weights(ir, cfg, device="cuda"))
