@@ -361,6 +361,7 @@ __device__ __forceinline__ void dec_attend(const PersistArgs& a, int l, uint16_t
   const float* csh = rope_cs;                    // [64] cos, [64] sin (rounded, scaled)
   uint16_t* rot = (uint16_t*)(smem + 1536);      // [2 * D]: rotated q and k
   float* osh = (float*)(smem + 2048);            // [8][D] per-wave unnormalised outputs
+  // then each wave's 16 attention weights of its current chunk at smem + 6144: [8][16] floats
   const uint16_t* Kb = kcache + (long long)kvh * kvs;
   const uint16_t* Vb = vcache + (long long)kvh * kvs;
   const bool cin = cpos >= 0 && cpos < S;
@@ -429,9 +430,18 @@ __device__ __forceinline__ void dec_attend(const PersistArgs& a, int l, uint16_t
       mw = mn;
       acc0 *= al;
       acc1 *= al;
+      // the 16 positions' weights to every lane through the wave's own 64 bytes of LDS (one
+      // wave's LDS accesses complete in order); 16 lane reads would each stall on the scalar unit
+      float pv[16];
+      {
+        float* pb = (float*)(smem + 6144) + wave * 16;
+        if ((lane & 3) == 0) pb[lane >> 2] = e;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *(float4*)&pv[4 * j] = ((const float4*)pb)[j];
+      }
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
-        const float p = HS_RL(e, 4 * t);
+        const float p = pv[t];
         const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
         acc0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), acc0);
         acc1 = fmaf(p, bfh((uint16_t)(vt >> 16)), acc1);
@@ -601,9 +611,16 @@ __device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint1
         lw[g] = lw[g] * al + ((HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48)));
         mw[g] = mn;
         float o0 = acc0[g] * al, o1 = acc1[g] * al;
+        float pv[16];   // as in dec_attend, through LDS past the rotated rows
+        {
+          float* pb = (float*)(rot + (G + 1) * DEC_D) + wave * 16;
+          if ((lane & 3) == 0) pb[lane >> 2] = e;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) *(float4*)&pv[4 * j] = ((const float4*)pb)[j];
+        }
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-          const float p = HS_RL(e, 4 * t);
+          const float p = pv[t];
           const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
           o0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), o0);
           o1 = fmaf(p, bfh((uint16_t)(vt >> 16)), o1);

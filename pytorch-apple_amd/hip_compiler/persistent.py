@@ -59,11 +59,14 @@ O_RING_MAX = 11
 # workgroup per (KV head, slot) scores all G query heads of the K / V rows it reads, G times fewer
 # bytes per workgroup than one workgroup per (query head, slot), at G head-folds per chunk and a
 # combine of G times more partials. Measured (Qwen2.5-1.5B, positions near the cache end, tok/s
-# KV-major / head-major): 8,192: 1,100 / 1,199; 16,384: 941 / 967; 32,768: 812 / 697. The kernel
+# KV-major / head-major): 8,192: 1,100 / 1,199; 16,384: 941 / 967; 32,768: 840 / 697. The kernel
 # instances that have it, by (KC, EM)
 KV_MAJOR_MIN_S = int(os.environ.get("HIPRT_DECODE_KV_MIN_S", "24577"))
 KV_MAJOR = {(3, 2), (1, 1)}
 MAX_KV_SLOTS = 128    # decode.hip DecShared::cwk (the combine's slot weights)
+# query heads per KV head, at most, whose q / k / v rows, rotated rows and the 8 waves' chunk
+# weights fit the attention staging (decode.hip DEC_SMEM, 8,448 bytes: 1,024 G + 768)
+KV_MAX_G = 7
 # gate/up rows a combine workgroup streams fewer than an o_proj workgroup: it waits for its head's
 # partials and runs the combine before its o_proj, so with the o_proj workgroups' share its h and
 # the next layer's rows were the last published (Qwen2.5-1.5B at 2048 positions: 11 - 4 = 7,
@@ -214,7 +217,8 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     nsplit, ws = sl
     # KV-head-major: the same NB attention workgroups as G nsplit slots per KV head
     G = H // KVH
-    kvm = (S >= KV_MAJOR_MIN_S and (KC, ws["EM"]) in KV_MAJOR and G * nsplit <= MAX_KV_SLOTS
+    kvm = (S >= KV_MAJOR_MIN_S and (KC, ws["EM"]) in KV_MAJOR and G <= KV_MAX_G
+           and G * nsplit <= MAX_KV_SLOTS
            and -(-(-(-S // SPL)) // (G * nsplit)) <= MAX_CHUNKS_PER_SLOT)
     if kvm:
         nsplit = G * nsplit
