@@ -360,6 +360,8 @@ def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
     t -= t[:, L * 16 + 7].min()
     b = np.arange(nwg)
     att, comb = b < NB, (b >= NB) & (b < NB + H)
+    if st.params.get("slot_combine"):   # the attention workgroups run the combine
+        comb = att
     who = {3: att, 4: att, 5: comb, 6: comb, 7: ~att, 8: ~att, 9: ~att}
     layers = range(2, L - 2)
     med = {}

@@ -389,7 +389,7 @@ struct PersistArgs {
                               // 128-position chunks j, j + nsplit, ... (those its mask leaves open)
   int nwg;                    // workgroups of the launch (all resident at once)
   int ids_dtype, pos_dtype, cpos_dtype, mask_dtype, add_dtype, n_dtype, out_dtype;
-  int flags;                  // 1: q/k/v biases present
+  int flags;                  // 1: q/k/v biases present; 2: the attention workgroups run the combine
   float eps, eps_f, scale, rope_scaling;
   // optional in-kernel decode advance (adv_flag null: none). After the step, the next step's
   // inputs: p = adv_cpos + 1; adv_cpos = adv_pos = p; adv_mask[p] = 0 when p < S. A step that

@@ -125,6 +125,16 @@ __device__ __forceinline__ void stg2(void* p, uint16_t v) { *DEC_G(uint16_t, p) 
       a.trace[(long long)blockIdx.x * (a.L * 16 + 8) + (l) * 16 + (k)] = wall_clock64();         \
   } while (0)
 
+#ifndef DEC_PROBE_ROUNDS
+#define DEC_PROBE_ROUNDS 0
+#endif
+#define DEC_STAMPV(l, k, v)                                                                      \
+  do {                                                                                           \
+    if (DEC_PROBE_ROUNDS && a.trace != nullptr && threadIdx.x == 0)                              \
+      a.trace[(long long)blockIdx.x * (a.L * 16 + 8) + (l) * 16 + (k)] = (v);                    \
+  } while (0)
+#define DEC_STAMPT(l, k) do { if (!DEC_PROBE_ROUNDS) DEC_STAMP(l, k); } while (0)
+
 __device__ __forceinline__ float rb(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 __device__ __forceinline__ float bfh(uint16_t h) { return bf16_to_f32(h); }
 
@@ -152,12 +162,13 @@ __device__ __forceinline__ void dec_fail(uint32_t* err, int* herr) {
 // small exchange slot: 256 workgroups gathering the 8,960-word SiLU * up row took 4-5 us that way).
 // Returns after a __syncthreads(), so dst is complete for the whole workgroup.
 template <int NPT, int NTH = DEC_THREADS>
-__device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag, uint16_t* dst, uint32_t* err,
-                                        int* herr, int tid) {
+__device__ __forceinline__ int xgather(const uint32_t* src, int n, uint32_t tag, uint16_t* dst, uint32_t* err,
+                                       int* herr, int tid) {
   if (tid >= NTH) {   // waves outside the gathering set only meet the barrier
     __syncthreads();
-    return;
+    return 0;
   }
+  int rounds = 0;
   const int np = n >> 1;
   const unsigned long long want = ((unsigned long long)tag << 48) | ((unsigned long long)tag << 16);
   const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
@@ -178,6 +189,7 @@ __device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag
       break;
     }
     __builtin_amdgcn_s_sleep(1);
+    ++rounds;
 #pragma unroll
     for (int j = 0; j < NPT; ++j)
       if ((v[j] & tmask) != want) v[j] = xget2(src + 2 * min(tid + NTH * j, np - 1));
@@ -187,7 +199,12 @@ __device__ __forceinline__ void xgather(const uint32_t* src, int n, uint32_t tag
     const int i = tid + NTH * j;
     if (i < np) *(uint32_t*)(dst + 2 * i) = (uint32_t)(v[j] & 0xFFFFu) | (uint32_t)((v[j] >> 16) & 0xFFFF0000u);
   }
+#if DEC_PROBE_ROUNDS
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) rounds = max(rounds, __shfl_xor(rounds, o, 64));
+#endif
   __syncthreads();
+  return rounds;
 }
 
 // 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane (gfx950), from inline
@@ -198,6 +215,12 @@ __device__ __forceinline__ void dec_dma16(const void* g, unsigned lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 __device__ __forceinline__ void dec_vmcnt0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+#define DEC_STR2(x) #x
+#define DEC_STR(x) DEC_STR2(x)
+#define DEC_VMCNT(q) asm volatile("s_waitcnt vmcnt(" DEC_STR(q) ")" ::: "memory")
+#ifndef DEC_LDS_Q
+#define DEC_LDS_Q 0
+#endif
 
 // Word offsets of one layer's exchange slots (all even, so word pairs are 8-byte aligned).
 struct XLayout {
@@ -280,15 +303,15 @@ __device__ __forceinline__ void block_norm(const uint16_t* x, uint4 wv, int hid,
 
 // the layer's input row into xres: the token's embedding row (layer 0) or the exchange words
 template <int KC>
-__device__ __forceinline__ void load_x(const PersistArgs& a, int l, const uint32_t* xw, long long tok, uint32_t tag,
-                                       uint16_t* xres, uint32_t* err, int* herr, int tid) {
+__device__ __forceinline__ int load_x(const PersistArgs& a, int l, const uint32_t* xw, long long tok, uint32_t tag,
+                                      uint16_t* xres, uint32_t* err, int* herr, int tid) {
   if (l == 0) {
     const int nch = a.hidden >> 3;
     if (tid < nch) *(uint4*)(xres + 8 * tid) = *(const uint4*)(a.emb + tok * a.hidden + 8 * tid);
     __syncthreads();
-  } else {
-    xgather<(KC + 1) / 2>(xw, a.hidden, tag, xres, err, herr, tid);
+    return 0;
   }
+  return xgather<(KC + 1) / 2>(xw, a.hidden, tag, xres, err, herr, tid);
 }
 
 __device__ __forceinline__ unsigned long long key48(uint16_t hbits, unsigned idx) {
@@ -753,7 +776,9 @@ __device__ __forceinline__ void dec_combine(const PersistArgs& a, int l, const u
   uint16_t* pl = (uint16_t*)smem;   // [NT][D + 4]
   float* cw = red2;                 // [NT] weights e^(m_t - M) l_t / L (NT <= 32: red2 holds 64)
   __syncthreads();
-  xgather<(32 * (DEC_D + 4) + 2 * 256 - 1) / (2 * 256), 256>(partw, NT * (DEC_D + 4), tag, pl, err, a.host_err, tid);
+  const int crd = xgather<(32 * (DEC_D + 4) + 2 * 256 - 1) / (2 * 256), 256>(partw, NT * (DEC_D + 4), tag, pl, err,
+                                                                           a.host_err, tid);
+  DEC_STAMPV(l, 7, crd);
   DEC_STAMP(l, 5);
   if (wave == 0) {
     float m = -INFINITY, lv = 0.f;
@@ -774,6 +799,64 @@ __device__ __forceinline__ void dec_combine(const PersistArgs& a, int l, const u
     for (int t = q; t < NT; t += 2) sacc = fmaf(cw[t], bfh(pl[t * (DEC_D + 4) + d]), sacc);
     sacc += HS_DPP(sacc, HS_QUAD_XOR1);
     if (q == 0) xput(attw + d, f32_to_bf16(sacc), tag);
+  }
+  DEC_STAMP(l, 6);
+}
+
+// ---- C spread over the head's attention workgroups: slot j combines dims j DS .. j DS + DS - 1 ----
+// (DS = D / nsplit rounded up to even) of its head's nsplit partials, right after publishing its
+// own, and publishes those dims of the attention row. Each slot gathers only the (m, l) words and
+// its DS dims of every partial; the weights and sums are dec_combine's, in the same order, so the
+// row is the same bit for bit. No workgroup waits behind another's weight loads for the partials.
+__device__ __forceinline__ void dec_combine_slot(const PersistArgs& a, int l, const uint32_t* partw, uint32_t* attw,
+                                                 int slot, uint32_t tag, uint32_t* err, unsigned char* smem,
+                                                 float* red2, int tid, int lane, int wave) {
+  const int NT = a.nsplit;
+  const int DS = ((DEC_D + NT - 1) / NT + 1) & ~1, d0 = slot * DS, nd = min(DS, DEC_D - d0);
+  if (nd <= 0) return;   // (workgroup-uniform) a trailing slot with no dims
+  const int PW = DS / 2 + 2;        // 64-bit words per partial: DS / 2 of o, then (m, l)
+  uint16_t* pl = (uint16_t*)smem;   // [NT][DS + 4]
+  float* cw = red2;
+  __syncthreads();
+  {
+    const unsigned long long want = ((unsigned long long)tag << 48) | ((unsigned long long)tag << 16);
+    const unsigned long long tmask = 0xFFFF0000FFFF0000ull;
+    const bool mine = tid < NT * PW;
+    const int t = tid / PW, k = tid - t * PW;
+    const int off = t * (DEC_D + 4) + (k < DS / 2 ? min(d0 + 2 * k, DEC_D - 2) : DEC_D + 2 * (k - DS / 2));
+    unsigned long long v = mine ? xget2(partw + off) : want;
+    const unsigned long long t0 = wall_clock64();
+    while ((v & tmask) != want) {
+      if (wall_clock64() - t0 > DEC_TIMEOUT) {
+        dec_fail(err, a.host_err);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      v = xget2(partw + off);
+    }
+    if (mine) *(uint32_t*)(pl + t * (DS + 4) + 2 * k) = (uint32_t)(v & 0xFFFFu) | (uint32_t)((v >> 16) & 0xFFFF0000u);
+  }
+  __syncthreads();
+  DEC_STAMP(l, 5);
+  if (wave == 0) {
+    float m = -INFINITY, lv = 0.f;
+    if (lane < NT) {
+      const uint16_t* e = pl + lane * (DS + 4) + DS;
+      m = __uint_as_float(((uint32_t)e[0] << 16) | e[1]);
+      lv = __uint_as_float(((uint32_t)e[2] << 16) | e[3]);
+    }
+    const float M = wave_max(lv > 0.f ? m : -INFINITY);
+    const float f = lv > 0.f ? __expf(m - M) * lv : 0.f;
+    const float L = wave_sum(f);
+    if (lane < NT) cw[lane] = L > 0.f ? f / L : 0.f;
+    __builtin_amdgcn_wave_barrier();
+    for (int j = 0; j < nd; j += 32) {   // 32 dims per pass, two lanes each (every lane takes part)
+      const int dj = j + (lane >> 1), d = min(dj, nd - 1), q = lane & 1;
+      float sacc = 0.f;
+      for (int t = q; t < NT; t += 2) sacc = fmaf(cw[t], bfh(pl[t * (DS + 4) + d]), sacc);
+      sacc += HS_DPP(sacc, HS_QUAD_XOR1);
+      if (q == 0 && dj < nd) xput(attw + d0 + d, f32_to_bf16(sacc), tag);
+    }
   }
   DEC_STAMP(l, 6);
 }
@@ -827,10 +910,14 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
   uint32_t* err = ctl + 1;
   uint32_t tag = (__hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) & 0xFFFFu;
   tag = tag == 0 ? 1u : tag;
-  long long tok = ld_i(a.ids, 0, a.ids_dtype);
+  // the three inputs loaded together with no dtype switch (int64 or int32, checked on the host): a
+  // switch's branches would each wait for the load in flight, three cold round trips in a row
+  const IRaw tokw = ld_i_raw(a.ids, 0, a.ids_dtype), posw = ld_i_raw(a.pos_ids, 0, a.pos_dtype);
+  const IRaw cposw = ld_i_raw(a.cache_pos, 0, a.cpos_dtype);
+  long long tok = ld_i_decode(tokw, a.ids_dtype);
   tok = tok < 0 ? 0 : (tok >= a.vocab ? a.vocab - 1 : tok);   // ATen would raise; never read outside the table
-  const long long posr = ld_i(a.pos_ids, 0, a.pos_dtype);
-  const long long cpos = ld_i(a.cache_pos, 0, a.cpos_dtype);
+  const long long posr = ld_i_decode(posw, a.pos_dtype);
+  const long long cpos = ld_i_decode(cposw, a.cpos_dtype);
   const long long S = a.S, last = S - 1, kvs = a.kv_head_stride;
   uint16_t* xs = (uint16_t*)smem;
   DEC_STAMP(a.L, 7);
@@ -922,8 +1009,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       const uint16_t bias = (has && (a.flags & 1)) ? ldg2(B + rr) : (uint16_t)0;
       const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm1 + 8 * tid) : make_uint4(0, 0, 0, 0);
       __syncthreads();
-      DEC_STAMP(l, 0);
-      load_x<KC>(a, l, XL, tok, tag, xres, err, a.host_err, tid);
+      DEC_STAMPT(l, 0);
+      const int ard = load_x<KC>(a, l, XL, tok, tag, xres, err, a.host_err, tid);
+      DEC_STAMPV(l, 0, ard);
       DEC_STAMP(l, 1);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
       if (has) {
@@ -993,13 +1081,24 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
                    rope_cs, red, red2, tid, lane, wave);
       }
       DEC_STAMP(l, 4);
+      if constexpr (!KVM) {
+        if (a.flags & 2) {   // C by the head's attention workgroups (no combine workgroups)
+          const int hq = kvh * G + gq;
+          dec_combine_slot(a, l, XL + X.part + (long long)hq * NT * (DEC_D + 4), XL + X.att + (long long)hq * DEC_D,
+                           slot, tag, err, smem, red2, tid, lane, wave);
+        }
+      }
       // this workgroup's first NL gate / up rows into LDS: its next wait (x1, in E) is some
       // microseconds away, and these land by then
       const unsigned base = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&ebuf[0];
+      int nq = 0;
       for (int k = wave; k < NL * 2 * KC; k += DEC_WAVES) {
         const int i = k / (2 * KC), u = (k / KC) & 1, c = k % KC;
         dec_dma16((u ? P.wu : P.wg) + (long long)(e0 + i) * hid + c * 512 + lane * 8,
                   __builtin_amdgcn_readfirstlane(base + (unsigned)k * 1024u));
+        if constexpr (DEC_LDS_Q > 0) {
+          if (++nq >= DEC_LDS_Q) DEC_VMCNT(DEC_LDS_Q);
+        }
       }
     }
 
@@ -1020,8 +1119,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       DEC_PART_IDS();
       dec_vmcnt0();   // this wave's o_proj rows have landed (long ago)
       __syncthreads();
-      DEC_STAMP(l, 7);
-      xgather<(KC + 1) / 2 * 2, 256>(XL + X.att, H * DEC_D, tag, xs, err, a.host_err, tid);
+      DEC_STAMPT(l, 7);
+      const int drd = xgather<(KC + 1) / 2 * 2, 256>(XL + X.att, H * DEC_D, tag, xs, err, a.host_err, tid);
+      if constexpr (!comb) DEC_STAMPV(l, 7, drd);
       DEC_STAMP(l, 8);
       const unsigned char* ob = (const unsigned char*)ebuf;
       const int d0 = (b - NB) * RD;
@@ -1090,8 +1190,9 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       const uint4 nw = tid < (hid >> 3) ? ldg16(P.norm2 + 8 * tid) : make_uint4(0, 0, 0, 0);
       if (att && wave >= 4) dec_vmcnt0();   // waves outside the x1 gather: their LDS loads have landed
       __syncthreads();
-      DEC_STAMP(l, 10);
-      xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, a.host_err, tid);
+      DEC_STAMPT(l, 10);
+      const int erd = xgather<(KC + 1) / 2 * 2, 256>(XL + X.x1, hid, tag, xres, err, a.host_err, tid);
+      DEC_STAMPV(l, 10, erd);
       DEC_STAMP(l, 11);
       block_norm(xres, nw, hid, a.eps, a.n_dtype, xs, red, tid);
 #pragma unroll
@@ -1181,8 +1282,10 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
       // issued before the h stores would hold those stores back, and with them every workgroup's F
 #pragma unroll
       for (int j = RFE; j < RF; ++j) load_down(j);
-      DEC_STAMP(l, 13);
-      xgather<(IC * 4096 / 2 + DEC_THREADS - 1) / DEC_THREADS>(XL + X.h, a.inter, tag, hs, err, a.host_err, tid);
+      DEC_STAMPT(l, 13);
+      const int frd = xgather<(IC * 4096 / 2 + DEC_THREADS - 1) / DEC_THREADS>(XL + X.h, a.inter, tag, hs, err,
+                                                                               a.host_err, tid);
+      DEC_STAMPV(l, 13, frd);
       DEC_STAMP(l, 14);
       float part[RF];
 #pragma unroll
@@ -1335,7 +1438,7 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     __shared__ DecShared<KC, DEC_NE(KC)> sh; \
     const int nb_ = a.H * a.nsplit; \
     if ((int)blockIdx.x < nb_) decode_body<KC, IC, EM, 0, false>(a, sh); \
-    else if ((int)blockIdx.x < nb_ + a.H) decode_body<KC, IC, EM, 2, false>(a, sh); \
+    else if (!(a.flags & 2) && (int)blockIdx.x < nb_ + a.H) decode_body<KC, IC, EM, 2, false>(a, sh); \
     else decode_body<KC, IC, EM, 1, false>(a, sh); \
   }
 // KV-head-major attention (long caches): nsplit slots per KV head, KVH nsplit attention workgroups
@@ -1404,8 +1507,9 @@ __device__ __forceinline__ void attn_step_body(const PersistArgs& a, AttnShared<
   uint32_t* err = ctl + 1;
   uint32_t tag = (__hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u) & 0xFFFFu;
   tag = tag == 0 ? 1u : tag;
-  const long long posr = ld_i(a.pos_ids, 0, a.pos_dtype);
-  const long long cpos = ld_i(a.cache_pos, 0, a.cpos_dtype);
+  const IRaw posw = ld_i_raw(a.pos_ids, 0, a.pos_dtype), cposw = ld_i_raw(a.cache_pos, 0, a.cpos_dtype);
+  const long long posr = ld_i_decode(posw, a.pos_dtype);
+  const long long cpos = ld_i_decode(cposw, a.cpos_dtype);
   uint16_t* xs = (uint16_t*)sh.smem;
   DEC_STAMP(0, 0);
   if (tid < 64) {   // rotary factors of this step's position, as in the decode step

@@ -72,6 +72,10 @@ KV_MAX_G = 7
 # the next layer's rows were the last published (Qwen2.5-1.5B at 2048 positions: 11 - 4 = 7,
 # 0.670 ms per step against 0.673 with 11; 5 or 3 with one row more per o_proj workgroup: 0.674)
 C_RING_LESS = 4
+# the head-major attention without combine workgroups: slot j of a head, once its partial is out,
+# gathers dims j D / nsplit .. of all the head's partials and publishes them (decode.hip
+# dec_combine_slot); the 12 combine workgroups' partials poll waited behind their o_proj rows
+SLOT_COMBINE = os.environ.get("HIPRT_DECODE_SLOT_COMBINE", "0") == "1"
 OSTAGE = 128         # decode.hip DEC_OSTAGE: a workgroup's gate/up rows, staged
 
 TABLE_FIELDS = ("norm1", "wq", "bq", "wk", "bk", "wv", "bv", "kc", "vc", "wo", "norm2", "wg", "wu", "wd")
@@ -106,13 +110,15 @@ def _device_resident(kernel: str) -> int | None:
 resident_workgroups = _device_resident
 
 
-def work_split(hidden: int, inter: int, H: int, nslot: int) -> dict | None:
+def work_split(hidden: int, inter: int, H: int, nslot: int, comb: bool = True) -> dict | None:
     """The kernel's division of a layer among the NWG workgroups (decode.hip ``decode_body``): NB
     attention workgroups (each also holds NE gate/up rows in LDS), ND o_proj workgroups of RD rows
     (those that run no combine also hold NEO gate/up rows in LDS); the gate/up rows left over are
     streamed through registers, RBO by each o_proj workgroup that runs no combine, RBC by each of
     the H combine workgroups and RBA by each attention workgroup; EM is the kernel instance's
-    register rows per wave. None when no instance fits."""
+    register rows per wave. ``comb`` False: the attention workgroups run the combine, the first H
+    o_proj workgroups are like the others (RBC is then their stride in the gate/up rows, RBO +
+    NEO). None when no instance fits."""
     KC = hidden // 512
     NB, NE = H * nslot, E_LDS_ROWS[KC]
     ND = NWG - NB
@@ -122,12 +128,13 @@ def work_split(hidden: int, inter: int, H: int, nslot: int) -> dict | None:
     if RD > 2 * NE:   # the o_proj rows of one workgroup must fit its LDS
         return None
     NEO = max(2 * NE - RD, 0) // 2
-    ring = max(inter - NB * NE - (ND - H) * NEO, 0)
+    HC = H if comb else 0
+    ring = max(inter - NB * NE - (ND - HC) * NEO, 0)
     cap = 8 * max(RING_ROWS[KC])
     RBO = min(-(-ring // NWG), O_RING_MAX)
     RBO = max(RBO, -(-max(ring - NB * cap, 0) // ND))   # what the attention workgroups cannot take
-    RBC = max(RBO - C_RING_LESS, 0)
-    RBA = -(-max(ring - (ND - H) * RBO - H * RBC, 0) // NB)
+    RBC = max(RBO - C_RING_LESS, 0) if comb else RBO + NEO
+    RBA = -(-max(ring - (ND - HC) * RBO - HC * RBC, 0) // NB)
     RB = max(RBA, RBO)
     em = [e for e in RING_ROWS[KC] if 8 * e >= RB]
     if not em or max(NE, NEO) + RB > OSTAGE:
@@ -222,6 +229,10 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
            and -(-(-(-S // SPL)) // (G * nsplit)) <= MAX_CHUNKS_PER_SLOT)
     if kvm:
         nsplit = G * nsplit
+    # the head-major attention's workgroups combine their head's partials themselves
+    scomb = not kvm and SLOT_COMBINE and work_split(hidden, inter, H, nsplit, comb=False) is not None
+    if scomb:
+        ws = work_split(hidden, inter, H, nsplit, comb=False)
     shared = ("pos_ids", "cache_pos", "inv_freq")
     x = ea["out"]
     table: list = []
@@ -264,6 +275,8 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
     if not (_same(la["x"], x) and _same(fa["slot"], la["argmax_slot"]) and int(la["K"]) == hidden
             and int(la["M"]) == 1 and int(la["flags"]) == 0 and int(fa["rows"]) == 1
             and int(fa["out_dtype"]) in (DTYPE_CODE["int64"], DTYPE_CODE["int32"])
+            and all(int(d) in (DTYPE_CODE["int64"], DTYPE_CODE["int32"])   # the kernel's branch-free loads
+                    for d in (ea["ids_dtype"], q0["pos_dtype"], q0["cpos_dtype"]))
             and int(la["n_dtype"]) == int(q0["n_dtype"])):
         return None
     # the table holds graph inputs (caches) and weights only: the executor resolves it per set of
@@ -286,7 +299,8 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
         inter=inter, H=H, KVH=KVH, D=D, nsplit=nsplit, nwg=NWG, ids_dtype=int(ea["ids_dtype"]),
         pos_dtype=int(q0["pos_dtype"]), cpos_dtype=int(q0["cpos_dtype"]),
         mask_dtype=int(f0["mask_dtype"]) if mask is not None else -1, add_dtype=int(f0.get("add_dtype", 2)),
-        n_dtype=int(q0["n_dtype"]), out_dtype=int(fa["out_dtype"]), flags=1 if int(q0["flags"]) & 2 else 0,
+        n_dtype=int(q0["n_dtype"]), out_dtype=int(fa["out_dtype"]),
+        flags=(1 if int(q0["flags"]) & 2 else 0) | (2 if scomb else 0),
         eps=float(q0["eps"]), eps_f=float(la["eps"]), scale=float(f0["scale"]),
         rope_scaling=float(q0["rope_scaling"]), nchunk=-(-S // SPL), rbo=ws["RBO"], rba=ws["RBA"], rbc=ws["RBC"])
     inputs = sorted({t for st in steps for t in st.inputs})
@@ -296,7 +310,7 @@ def fuse_decode_step(steps: list[LaunchStep], storages: dict[str, Storage]) -> l
         args=args, grid=(NWG, 1, 1), block=(THREADS, 1, 1), inputs=inputs, outputs=outputs,
         params={"table": {"field": "layers", "entries": table}, "layers": L, "nsplit": nsplit,
                 "replaces": [st.kernel for st in steps], "exchange_words": words, "work_split": ws,
-                "kv_major": kvm})
+                "kv_major": kvm, "slot_combine": scomb})
     return [step]
 
 
@@ -371,6 +385,8 @@ def fuse_attention_step(steps: list[LaunchStep], storages: dict[str, Storage]) -
         and (fl["mask"] is None or (int(fl["mask_stride"]) == 1 and int(fl["mask_dtype"]) in (0, 2)))
         and int(oa["N"]) == hidden and int(oa["K"]) == hidden and int(oa["M"]) == 1 and int(oa["flags"]) == 0
         and oa.get("bias") is None and oa.get("w2") is None and oa.get("norm_w") is None
+        and all(int(d) in (DTYPE_CODE["int64"], DTYPE_CODE["int32"])   # the kernel's branch-free loads
+                for d in (qa["pos_dtype"], qa["cpos_dtype"]))
     )
     if not ok:
         return None

@@ -380,7 +380,7 @@ def test_persistent_step_covers_long_and_ragged_caches(S):
     NB, ND, NE, NEO, H = ws["NB"], ws["ND"], ws["NE"], ws["NEO"], cfg.heads
     rows = []
     for b in range(P.NWG):
-        att, comb = b < NB, NB <= b < NB + H
+        att, comb = b < NB, NB <= b < NB + H and not st.params["slot_combine"]
         e0 = (b * (NE + ws["RBA"]) if att else
               NB * (NE + ws["RBA"]) + min(b - NB, H) * ws["RBC"] + max(b - NB - H, 0) * (ws["RBO"] + NEO))
         nlc = NE if att else (0 if comb else NEO)
