@@ -74,7 +74,9 @@ KV_MAX_G = 7
 C_RING_LESS = 4
 # the head-major attention without combine workgroups: slot j of a head, once its partial is out,
 # gathers dims j D / nsplit .. of all the head's partials and publishes them (decode.hip
-# dec_combine_slot); the 12 combine workgroups' partials poll waited behind their o_proj rows
+# dec_combine_slot). Off: measured slower (Qwen2.5-1.5B at 2048 positions, 0.713 ms per step
+# against 0.666: the attention row is out sooner, but o_proj's poll for it returns no sooner and
+# the attention workgroups' gate / up rows, issued after the combine, land later)
 SLOT_COMBINE = os.environ.get("HIPRT_DECODE_SLOT_COMBINE", "0") == "1"
 OSTAGE = 128         # decode.hip DEC_OSTAGE: a workgroup's gate/up rows, staged
 
