@@ -34,6 +34,7 @@ from hip_runtime.kernels import STRUCTS, ModuleCache
 
 _MODULES: dict[int, ModuleCache] = {}
 MAX_GRAPHS = 8
+MAX_TABLES = 8   # pointer tables kept per executor without graphs (with graphs: all)
 
 
 def _current_stream(device: torch.device) -> int:
@@ -112,7 +113,9 @@ class HIPExecutor:
                                              if storages[r.storage].kind in ("input", "weight")})
         self._structs = []
         self._tables: list[tuple[object, str, list]] = []   # (struct, pointer field, entries)
-        self._table_bufs: dict[tuple, list] = {}             # pointer set -> device tables
+        # table values -> [(device table, its pinned host copy)]; pointer set -> table values
+        self._table_bufs: OrderedDict[tuple, list] = OrderedDict()
+        self._tkey_of: OrderedDict[tuple, tuple] = OrderedDict()
         self._fixups: list[tuple[object, str, int, str, int]] = []   # (struct, field, index, storage, byte_off)
         n = len(program.steps)
         self._recs = (_shim.LaunchRec * max(n, 1))()
@@ -142,6 +145,10 @@ class HIPExecutor:
         self._w_names = [n for n in self._ext_names if storages[n].kind == "weight"]
         self._in_names = [n for n in self._ext_names if storages[n].kind != "weight"]
         self._w_names_set = frozenset(self._w_names)
+        # each fixup's pointer as a position in the pointer set (weights, inputs): a launch with a
+        # new set patches its kernargs without building a name -> pointer map
+        pos = {n: (0, i) for i, n in enumerate(self._w_names)} | {n: (1, i) for i, n in enumerate(self._in_names)}
+        self._fix_pos = [(s, field, idx, *pos[storage], off) for s, field, idx, storage, off in self._fixups]
         self._w_src, self._w_snap, self._w_key = None, (), ()
         self._last_bufs: tuple | None = None      # input buffer objects of the previous launch
         self._last_in_key: tuple = ()
@@ -149,6 +156,7 @@ class HIPExecutor:
         self._graphs: OrderedDict[tuple, int] = OrderedDict()   # (pointer set, advance) -> captured graph
         self._adv_ptr = 0                         # flag word of a decode advance folded into the launch
         self._adv_bufs: tuple = ()                # its (mask, position, cache position, mask bytes)
+        self._adv_checked: tuple | None = None    # the (pointer set, advance) last checked
         self._capture_stream = None
         # a persistent step (PERSISTENT_KINDS): every workgroup must be resident at once, and its
         # timeout flag is mirrored into host memory, read on every launch without a synchronisation
@@ -191,41 +199,60 @@ class HIPExecutor:
         else:
             arr[idx] = val
 
-    def _patch(self, ptrs: dict[str, int], key: tuple) -> None:
-        for s, field, idx, storage, off in self._fixups:
-            val = ptrs[storage] + off
+    def _patch(self, key: tuple) -> None:
+        for s, field, idx, part, i, off in self._fix_pos:
+            val = key[part][i] + off
             if idx < 0:
                 setattr(s, field, val)
             else:
                 getattr(s, field)[idx] = val
         if self._tables:
-            self._fill_tables(ptrs, key)
+            self._fill_tables(key)
 
-    def _fill_tables(self, ptrs: dict[str, int], key: tuple) -> None:
+    def _fill_tables(self, key: tuple) -> None:
         """Pointer tables of the launches that read one (the persistent decode step's per-layer
-        tensors): resolved for this pointer set into a device array of its own, so that a graph
-        captured for another set keeps reading the table it was captured with."""
-        bufs = self._table_bufs.get(key)
-        if bufs is None:
+        tensors): one device array per set of table values. A table holds weights and caches
+        only, so calls that differ in other inputs (a decode loop's first token, then its own
+        argmax) share one and switch between them with no upload. A new set is uploaded from
+        pinned memory on the launch stream without waiting for the device; without graphs the
+        least recently used set beyond MAX_TABLES is freed after a synchronisation (a launch in
+        flight may still read it), and with graphs none is freed (a captured graph keeps reading
+        the table it was captured with)."""
+        tkey = self._tkey_of.get(key)
+        if tkey is None:
+            ptrs = self._ptrs_of(key)
             base = self.arena.data_ptr()
             storages = self.program.storages
-            bufs = []
+            vals = []
             for _, _, entries in self._tables:
-                vals = []
+                row = []
                 for r in entries:
                     if r is None:
-                        vals.append(0)
+                        row.append(0)
                     elif storages[r.storage].kind in ("arena", "persistent"):
-                        vals.append(base + storages[r.storage].offset + r.byte_offset)
+                        row.append(base + storages[r.storage].offset + r.byte_offset)
                     else:
-                        vals.append(ptrs[r.storage] + r.byte_offset)
-                host = torch.tensor([v - (1 << 64) if v >= (1 << 63) else v for v in vals], dtype=torch.int64)
-                bufs.append(host.to(self.device))
-            torch.cuda.current_stream(self.device).synchronize()
-            if not self.use_graph:   # without graphs only the current set's tables are read
-                self._table_bufs.clear()
-            self._table_bufs[key] = bufs
-        for (s, field, _), t in zip(self._tables, bufs):
+                        row.append(ptrs[r.storage] + r.byte_offset)
+                vals.append(tuple(row))
+            tkey = self._tkey_of[key] = tuple(vals)
+            while len(self._tkey_of) > 4 * MAX_TABLES:
+                self._tkey_of.popitem(last=False)
+        else:
+            self._tkey_of.move_to_end(key)
+        bufs = self._table_bufs.get(tkey)
+        if bufs is None:
+            bufs = []
+            for row in tkey:
+                host = torch.tensor([v - (1 << 64) if v >= (1 << 63) else v for v in row], dtype=torch.int64)
+                host = host.pin_memory()
+                bufs.append((host.to(self.device, non_blocking=True), host))
+            self._table_bufs[tkey] = bufs
+            if not self.use_graph and len(self._table_bufs) > MAX_TABLES:
+                torch.cuda.current_stream(self.device).synchronize()
+                self._table_bufs.popitem(last=False)
+        else:
+            self._table_bufs.move_to_end(tkey)
+        for (s, field, _), (t, _) in zip(self._tables, bufs):
             setattr(s, field, t.data_ptr())
 
     # ------------------------------------------------------------------ execution
@@ -312,10 +339,11 @@ class HIPExecutor:
             self._graphs.move_to_end(gkey)
         else:
             if key != self._ext_key:
-                self._patch(self._ptrs_of(key), key)
+                self._patch(key)
                 self._ext_key = key
-            if self._adv_ptr:
+            if self._adv_ptr and self._adv_checked != (key, self._adv_bufs):   # once per pointer set
                 self._check_advance(key, self._adv_bufs)
+                self._adv_checked = (key, self._adv_bufs)
             if not self.use_graph:
                 _shim.check(lib.hs_replay(self._recs, self._n, stream), "replay")
                 return
@@ -327,10 +355,8 @@ class HIPExecutor:
             _shim.check(lib.hs_graph_capture(self._recs, self._n, self._capture_stream, C.byref(g)), "graph capture")
             graph = self._graphs[gkey] = g.value
             while len(self._graphs) > MAX_GRAPHS:
-                (old_key, _), old = self._graphs.popitem(last=False)
+                _, old = self._graphs.popitem(last=False)
                 _shim.check(lib.hs_graph_destroy(old), "graph destroy")
-                if old_key != self._ext_key and all(k[0] != old_key for k in self._graphs):
-                    self._table_bufs.pop(old_key, None)
         _shim.check(lib.hs_graph_launch(graph, stream), "graph launch")
 
     def _check_advance(self, key: tuple, bufs: tuple) -> None:
