@@ -619,6 +619,161 @@ __device__ __forceinline__ void skinny_body(const GemvArgs& a) {
   }
 }
 
+// SILU with the RMSNorm of x folded in (k_skinny_silu_norm_*, M <= 16, K <= 1536 or 2048): SKN_W
+// waves per workgroup, one tile of 8 gate + 8 up rows each. The workgroup normalises the 16
+// activation rows once into LDS, laid out as the stages sk_stream's activation ring would hold
+// (stage s: 2 KB at s * 2 KB, chunk c of row r in slot c ^ (r & 7)), while the first weight
+// stages stream in; the waves then stream only their weights (RA stages ahead) and read their
+// activation fragments from that copy. The norm is the GEMV prologue's (rows_finish): fp32 sum of
+// squares, x * rsqrt(mean + eps) rounded to n_dtype, times the weight rounded to bf16.
+// LDS: 32 KMAX bytes of rows and SKN_W RA 2 KB of weight stages (KMAX = 1536: 144 KB, one
+// workgroup per CU with 96 KB of weights in flight). The activation rows are loaded before the
+// first weight stages, so the norm does not wait behind them (a CU's loads complete in order).
+// Measured at cfg1 T = 16 (the block, this kernel and the down GEMM): 8 waves of 6 stages 22.3 us;
+// 7 x 6 or 7 x 5 22.6, 8 x 7 22.9, 10 x 5 23.3, 6 x 7 23.4, 5 x 8 23.7, 4 x 8 or 4 x 12 (280
+// workgroups for 256 CUs) 30.0; the norm as a launch of its own before k_skinny_silu_mt1: 24.4-26.5.
+constexpr int SKN_W = 8, SKN_RA = 6;
+template <int KMAX, int RA, int SKN_W = SKN_W>
+__device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
+  constexpr int SKN_MAX_K = KMAX;
+  __shared__ uint4 xsr[16 * KMAX / 8];          // the normalised rows, stage layout
+  __shared__ uint4 ring[SKN_W][RA * 2 * 64];    // each wave's weight stages
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15, lr = lane >> 3;
+  const int K = a.K, ns = K >> 6, KC = K >> 9;   // stages of 64 k; 512-element chunks per row
+  const int tile = blockIdx.x * SKN_W + wave, n0 = tile * 8;
+  const bool live = n0 < a.N;                    // (wave-uniform) waves past N only normalise
+  const long long wrow = (long long)min(n0 + lr, a.N - 1) * K;
+  const uint16_t* wr[2] = {(const uint16_t*)a.w + wrow, (const uint16_t*)a.w2 + wrow};
+  const int cl = 8 * ((lane & 7) ^ (lane >> 3));
+  const int rot = (int)((unsigned)tile % (unsigned)ns);
+  const unsigned abase = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(sk_lds16*)ring[wave]);
+  auto issue_a = [&](int s, int slot) {   // visit s (clamped to the last) into slot
+    const int j = min(s, ns - 1) + rot, k = ((j >= ns ? j - ns : j) << 6) + cl;
+#pragma unroll
+    for (int j2 = 0; j2 < 2; ++j2) sk_dma16(wr[j2] + k, abase + (unsigned)(slot * 2 + j2) * 1024u);
+  };
+  // the norm: wave w takes rows NR w .. NR w + NR - 1 of the 16 (rows past M repeat row M - 1),
+  // lane l chunk 64 j + l of each (8 elements)
+  {
+    constexpr int MAXC = SKN_MAX_K / 512, NR = (16 + SKN_W - 1) / SKN_W;
+    uint4 xv[NR][MAXC], gv[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int k8 = min(c, KC - 1) * 64 + lane;
+      gv[c] = *(const uint4*)((const uint16_t*)a.norm_w + 8 * k8);
+#pragma unroll
+      for (int i = 0; i < NR; ++i)
+        xv[i][c] = *(const uint4*)((const uint16_t*)a.x + min((long long)min(NR * wave + i, 15), a.M - 1) * a.ldx + 8 * k8);
+    }
+    if (live) {
+#pragma unroll
+      for (int p = 0; p < RA; ++p) issue_a(p, p);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      if (NR * wave + i >= 16) break;   // (wave-uniform) past the 16 rows
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        if (c >= KC) break;
+        const uint32_t w4[4] = {xv[i][c].x, xv[i][c].y, xv[i][c].z, xv[i][c].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = bf16_to_f32((uint16_t)(w4[j] & 0xffffu)), hi = bf16_to_f32((uint16_t)(w4[j] >> 16));
+          acc = fmaf(lo, lo, acc);
+          acc = fmaf(hi, hi, acc);
+        }
+      }
+      const float tot = wave_sum(acc);
+      const float r = 1.0f / sqrtf(tot / (float)K + a.eps);
+      const int row = NR * wave + i;
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        if (c >= KC) break;
+        const uint32_t w4[4] = {xv[i][c].x, xv[i][c].y, xv[i][c].z, xv[i][c].w};
+        const uint32_t g4[4] = {gv[c].x, gv[c].y, gv[c].z, gv[c].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float m0 = round_to(bf16_to_f32((uint16_t)(w4[j] & 0xffffu)) * r, a.n_dtype);
+          const float m1 = round_to(bf16_to_f32((uint16_t)(w4[j] >> 16)) * r, a.n_dtype);
+          const uint16_t y0 = f32_to_bf16(bf16_to_f32((uint16_t)(g4[j] & 0xffffu)) * m0);
+          const uint16_t y1 = f32_to_bf16(bf16_to_f32((uint16_t)(g4[j] >> 16)) * m1);
+          o[j] = (uint32_t)y0 | ((uint32_t)y1 << 16);
+        }
+        const int k8 = c * 64 + lane, s = k8 >> 3, ch = k8 & 7;   // stage, chunk of the stage
+        xsr[s * 128 + (row >> 3) * 64 + (row & 7) * 8 + (ch ^ (row & 7))] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  sk_f32x4 acc = sk_f32x4{0.f, 0.f, 0.f, 0.f};
+  int fa[2], fb[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    fa[u] = (r16 >> 3) * 64 + (r16 & 7) * 8 + ((4 * u + q) ^ (r16 & 7));
+    fb[u] = (r16 >> 3) * 64 + (r16 & 7) * 8 + ((4 * u + q) ^ (r16 & 7));
+  }
+  const sk_lds16* rw = (const sk_lds16*)ring[wave];
+  const sk_lds16* xw = (const sk_lds16*)xsr;
+  for (int j0 = 0; j0 < ns; j0 += RA) {
+#pragma unroll
+    for (int p = 0; p < RA; ++p) {
+      sk_vmcnt<(RA - 1) * 2>();   // visit j0 + p has landed
+      const int v = j0 + p, jr = min(v, ns - 1) + rot, st = jr >= ns ? jr - ns : jr;
+      const unsigned ok = v < ns ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        uint4 av = rw[p * 128 + fa[u]];
+        av = make_uint4(av.x & ok, av.y & ok, av.z & ok, av.w & ok);
+        const uint4 bv = xw[st * 128 + fb[u]];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sk_bf16x8, av),
+                                                      __builtin_bit_cast(sk_bf16x8, bv), acc, 0, 0, 0);
+      }
+      sk_lgkm0();   // this slot's reads are done before it is refilled
+      issue_a(v + RA, p);
+    }
+  }
+  sk_vmcnt<0>();
+  float g[4], u[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    g[i] = acc[i];
+    u[i] = __shfl_xor(acc[i], 32, 64);
+  }
+  const int m = r16;
+  if (lane < 32 && m < a.M) {
+    uint16_t h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = min(n0 + 4 * q + i, a.N - 1);
+      float v = g[i], uu = u[i];
+      if (a.flags & 1) v += bf(a.bias, n);
+      if (a.flags & 4) uu += bf(a.bias2, n);
+      v = rbf(v);
+      uu = rbf(uu);
+      h[i] = f32_to_bf16(rbf(v / (1.f + expf(-v))) * uu);
+    }
+    uint16_t* o = (uint16_t*)a.out + (long long)m * a.ldo + n0 + 4 * q;
+    if (n0 + 4 * q + 3 < a.N && (((a.ldo | n0) & 3) == 0)) {
+      *(uint2*)o = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n0 + 4 * q + i < a.N) o[i] = h[i];
+    }
+  }
+}
+
+extern "C" __global__ void __launch_bounds__(64 * SKN_W) k_skinny_silu_norm_mt1_k1536(const GemvArgs a) {
+  skinny_silu_norm_body<1536, SKN_RA>(a);
+}
+extern "C" __global__ void __launch_bounds__(64 * SKN_W) k_skinny_silu_norm_mt1_k2048(const GemvArgs a) {
+  skinny_silu_norm_body<2048, SKN_RA>(a);
+}
+
 #define SKINNY_SILU(NAME, MT, RA, RB) \
   extern "C" __global__ void __launch_bounds__(64) NAME(const GemvArgs a) { skinny_silu_body<MT, RA, RB>(a); }
 #define SKINNY_KERNEL(NAME, EPI, MT, RW, RA, RB) \

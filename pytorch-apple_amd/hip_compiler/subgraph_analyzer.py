@@ -43,6 +43,10 @@ GEMM_MIN_M = 16
 # up to this many activation rows, bf16 linears take the skinny MFMA kernels (gemv.hip
 # k_skinny_*: every weight element read once and multiplied with all rows in one 16x16x32 MFMA)
 SKINNY_MAX_M = 32
+# the SiLU skinny kernel with the RMSNorm folded in (gemv.hip k_skinny_silu_norm_*): rows of at
+# most this many elements (its LDS copy of the 16 normalised rows), and its waves per workgroup
+SKINNY_NORM_MAX_K = 2048
+SKINNY_NORM_WAVES = 8
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
@@ -609,6 +613,40 @@ class Lowering:
                 params={"rows": M, "cols": N}))
             self.views[name] = t
 
+    def emit_skinny_silu_norm(self, x_name: str, w, w_name: str, w2: str, b_name: str | None, b2: str | None,
+                              out_name: str, out_shape, nodes: list[str]) -> bool:
+        """SiLU(x W^T) * (x W2^T) for at most 16 rows whose pending RMSNorm is folded in
+        (gemv.hip ``k_skinny_silu_norm_mt1_k*``: each workgroup of 8 waves normalises the rows into
+        LDS once, one 8 + 8-row tile per wave); False when ``x`` has no foldable norm or more rows."""
+        norm = self.foldable_norm(x_name, set(nodes))
+        if norm is None:
+            return False
+        N, K = w.shape
+        xr = self.aligned16(self.contiguous(norm["x"]), norm["x"])
+        M = xr.numel // K
+        if M > 16 or xr.numel != M * K:
+            return False
+        o = self.new_storage(out_name, out_shape, "bfloat16")
+        bias = self.contiguous(b_name) if b_name else None
+        wv2 = self.aligned16(self.contiguous(w2), w2)
+        bv2 = self.contiguous(b2) if b2 else None
+        kname = "k_skinny_silu_norm_mt1_k1536" if K <= 1536 else "k_skinny_silu_norm_mt1_k2048"
+        args = dict(x=self.ref(xr), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
+                    resid=None, w2=self.ref(wv2), bias2=self.ref(bv2) if bv2 else None,
+                    norm_w=self.ref(self.aligned16(self.contiguous(norm["w"]), norm["w"])), argmax_slot=None,
+                    attn_o=None, attn_ml=None, M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=float(norm["eps"]),
+                    n_dtype=DTYPE_CODE[norm["n_dtype"]], flags=(1 if bias else 0) | (4 if bv2 else 0),
+                    attn_heads=0, attn_kvh=0, attn_splits=0)
+        tiles = -(-N // 8)
+        self.emit(LaunchStep(
+            kind="gemm", kernel=kname, module="gemv", arg_struct="GemvArgs", args=args,
+            grid=(-(-tiles // SKINNY_NORM_WAVES), 1, 1), block=(64 * SKINNY_NORM_WAVES, 1, 1),
+            inputs=[norm["x"], w_name, w2, norm["w"]] + [t for t in (b_name, b2) if t], outputs=[out_name],
+            params={"M": M, "N": N, "K": K, "epilogue": "silu", "norm": True, "has_bias": bias is not None,
+                    "weights": 2, "transpose_b": True, "nodes": nodes, "mfma": True, "skinny": True}))
+        self.views[out_name] = o
+        return True
+
     def emit_gemm(self, x_name: str, w_name: str, b_name: str | None, out_name: str, out_shape, dtype: str, *,
                   epi: str, nodes: list[str], resid: str | None = None, w2: str | None = None,
                   b2: str | None = None) -> None:
@@ -617,6 +655,9 @@ class Lowering:
         bf16 rows take the skinny kernels instead."""
         w = self.aligned16(self.contiguous(w_name), w_name)
         N, K = w.shape
+        if (epi == "silu" and dtype == "bfloat16" and K % 64 == 0 and 512 <= K <= SKINNY_NORM_MAX_K and w2
+                and self.emit_skinny_silu_norm(x_name, w, w_name, w2, b_name, b2, out_name, out_shape, nodes)):
+            return
         x = self.aligned16(self.contiguous(x_name), x_name)
         M = x.numel // K
         o = self.new_storage(out_name, out_shape, dtype)
