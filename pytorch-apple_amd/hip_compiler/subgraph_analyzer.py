@@ -43,6 +43,10 @@ GEMM_MIN_M = 16
 # up to this many activation rows, bf16 linears take the skinny MFMA kernels (gemv.hip
 # k_skinny_*: every weight element read once and multiplied with all rows in one 16x16x32 MFMA)
 SKINNY_MAX_M = 32
+# from this many rows the bf16 linears take the skinny kernels rather than the streaming GEMVs,
+# which stream the weights once per 4 rows (cfg1 at T = 2 .. 15: 21-22 us per block against
+# 25-80 us)
+SKINNY_MIN_M = 2
 # the SiLU skinny kernel with the RMSNorm folded in (gemv.hip k_skinny_silu_norm_*): rows of at
 # most this many elements (its LDS copy of the 16 normalised rows), and its waves per workgroup
 SKINNY_NORM_MAX_K = 2048
@@ -173,6 +177,12 @@ def apply_alias(node: OpNode, v: TView) -> TView | None:
     if op == "aten.contiguous.default":
         return v if v.is_contiguous() else None
     return V.restride(v, out.shape)   # reshape / view / flatten / unsqueeze / squeeze
+
+
+def skinny_rows(M: int, K: int, dtype: str) -> bool:
+    """Rows a linear hands to the skinny MFMA kernels (gemv.hip ``k_skinny_*``: every weight
+    element read once and multiplied with up to 16 rows per MFMA) below the MFMA GEMM's range."""
+    return SKINNY_MIN_M <= M < GEMM_MIN_M and dtype == "bfloat16" and K % 64 == 0 and K >= 512
 
 
 @dataclass
@@ -512,7 +522,8 @@ class Lowering:
         Prefill-shaped calls (M >= GEMM_MIN_M) go to the MFMA GEMM instead."""
         w_view = self.view(w_name)
         n_out = numel(out_shape) // w_view.shape[0] if w_view.shape[0] else 0
-        if epi in ("bias", "resid", "silu") and n_out >= GEMM_MIN_M and w_view.shape[1] % 32 == 0:
+        if epi in ("bias", "resid", "silu") and (n_out >= GEMM_MIN_M and w_view.shape[1] % 32 == 0
+                                                 or skinny_rows(n_out, w_view.shape[1], "bfloat16")):
             self.emit_gemm(x_name, w_name, b_name, out_name, out_shape, "bfloat16", epi=epi, nodes=nodes,
                            resid=resid, w2=w2, b2=b2)
             return
@@ -735,7 +746,7 @@ class Lowering:
             if resid is not None:
                 raise NotImplementedError("residual epilogue on the generic path")
             return
-        if M >= GEMM_MIN_M and K % 32 == 0:
+        if M >= GEMM_MIN_M and K % 32 == 0 or skinny_rows(M, K, out_dtype):
             self.emit_gemm(x_name, w_name, b_name, out_name, out_shape, out_dtype,
                            epi="resid" if resid is not None else "bias", nodes=node_names, resid=resid)
             return
