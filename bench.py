@@ -338,7 +338,8 @@ def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
     DEC_STAMP: thread 0 of each workgroup records the 100 MHz real-time counter at fixed points of
     each part). Runs ``steps`` steps without a graph (the stamp buffer is an argument the captured
     graphs do not carry) and reads the last. Per stamp: the median over the workgroups that record
-    it, in µs after the layer's first workgroup has its input row, averaged over layers 2..L-3."""
+    it, in µs after the layer's first workgroup has its input row, averaged over layers 2..L-3
+    (and the minimum, median and maximum over those workgroups, averaged the same way)."""
     import numpy as np
     import torch
 
@@ -364,16 +365,19 @@ def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
         comb = att
     who = {3: att, 4: att, 5: comb, 6: comb, 7: ~att, 8: ~att, 9: ~att}
     layers = range(2, L - 2)
-    med = {}
+    med, spread = {}, {}
     for k, name in enumerate(STAMP_NAMES):
         vals = []
         for l in layers:
             v = t[:, l * 16 + k] - t[:, l * 16 + 1].min()
-            vals.append(np.median(v[who.get(k, np.ones(nwg, bool))]))
-        med[name] = round(float(np.mean(vals)), 2)
+            vals.append(np.percentile(v[who.get(k, np.ones(nwg, bool))], [0, 50, 100]))
+        m = np.mean(vals, axis=0)
+        med[name] = round(float(m[1]), 2)
+        spread[name] = [round(float(x), 2) for x in m]
     period = float(np.mean([t[:, (l + 1) * 16 + 1].min() - t[:, l * 16 + 1].min() for l in layers]))
     g_in, g_done = t[:, L * 16 + 1], t[:, L * 16 + 2]
-    return {"layers_averaged": f"2..{L - 3}", "per_part_median_us": med, "layer_period_us": round(period, 2),
+    return {"layers_averaged": f"2..{L - 3}", "per_part_median_us": med,
+            "per_part_min_median_max_us": spread, "layer_period_us": round(period, 2),
             "first_layer_input_us": round(float(t[:, 1].min()), 2),
             "lm_head_us": {"median": round(float(np.median(g_done - g_in.min())), 2),
                            "last": round(float(g_done.max() - g_in.min()), 2)},
