@@ -327,7 +327,7 @@ def run_copy_probe(device_index: int, stream, mib: int = 512, repeats: int = 3) 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_ctx2048_hbm_traffic.md")
 
 
-STAMP_NAMES = ("A weights issued", "A x in", "A q/k/v published", "B q/k/v in", "B partial published",
+STAMP_NAMES = ("A weights in", "A x in", "A q/k/v published", "B q/k/v in", "B partial published",
                "C partials in", "C attention row published", "D o_proj rows landed", "D attention row in",
                "D x1 published", "E register rows issued", "E x1 in", "E h published", "F weights issued",
                "F h in", "F x published")
