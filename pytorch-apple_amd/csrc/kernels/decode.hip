@@ -1329,8 +1329,12 @@ __device__ __forceinline__ void decode_body(const PersistArgs& a, DecShared<KC, 
     DEC_PART_IDS();
     uint32_t* XF = a.ll + X.stride * a.L;
     constexpr int R4 = DEC_R4;   // rows per wave per round; two rounds in flight
-    const long long V = a.vocab, r0 = (long long)b * DEC_WAVES * R4, rend = V;
     const long long GSTEP = (long long)NWG * DEC_WAVES * R4;
+    // the workgroups that take a share of the last, partial round are the last ones, not the
+    // first: workgroup 0 gathers every workgroup's argmax key once its own share is done
+    const long long V = a.vocab, rend = V;
+    const int xtra = (int)(((V % GSTEP) + DEC_WAVES * R4 - 1) / (DEC_WAVES * R4));   // workgroups with one more round
+    const long long r0 = (long long)((b + NWG - xtra) % NWG) * DEC_WAVES * R4;
     uint4 wc[R4][KC], wn[R4][KC];
     auto issue = [&](uint4 (&w)[R4][KC], long long base) {
 #pragma unroll
