@@ -619,7 +619,8 @@ __device__ __forceinline__ void skinny_body(const GemvArgs& a) {
   }
 }
 
-// SILU with the RMSNorm of x folded in (k_skinny_silu_norm_*, M <= 16, K <= 1536 or 2048): SKN_W
+// SILU with the RMSNorm of x folded in (k_skinny_silu_norm_*, M <= 16 and K <= 1536 or 2048, or
+// M <= 32 and K <= 1536 with two 16-row activation tiles, MT = 2, and 4 weight stages): SKN_W
 // waves per workgroup, one tile of 8 gate + 8 up rows each. The workgroup normalises the 16
 // activation rows once into LDS, laid out as the stages sk_stream's activation ring would hold
 // (stage s: 2 KB at s * 2 KB, chunk c of row r in slot c ^ (r & 7)), while the first weight
@@ -633,10 +634,10 @@ __device__ __forceinline__ void skinny_body(const GemvArgs& a) {
 // 7 x 6 or 7 x 5 22.6, 8 x 7 22.9, 10 x 5 23.3, 6 x 7 23.4, 5 x 8 23.7, 4 x 8 or 4 x 12 (280
 // workgroups for 256 CUs) 30.0; the norm as a launch of its own before k_skinny_silu_mt1: 24.4-26.5.
 constexpr int SKN_W = 8, SKN_RA = 6;
-template <int KMAX, int RA, int SKN_W = SKN_W>
+template <int KMAX, int RA, int SKN_W = SKN_W, int MT = 1>
 __device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
-  constexpr int SKN_MAX_K = KMAX;
-  __shared__ uint4 xsr[16 * KMAX / 8];          // the normalised rows, stage layout
+  constexpr int SKN_MAX_K = KMAX, ROWS = 16 * MT;
+  __shared__ uint4 xsr[ROWS * KMAX / 8];        // the normalised rows, stage layout (MT tiles per stage)
   __shared__ uint4 ring[SKN_W][RA * 2 * 64];    // each wave's weight stages
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15, lr = lane >> 3;
@@ -653,10 +654,10 @@ __device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
 #pragma unroll
     for (int j2 = 0; j2 < 2; ++j2) sk_dma16(wr[j2] + k, abase + (unsigned)(slot * 2 + j2) * 1024u);
   };
-  // the norm: wave w takes rows NR w .. NR w + NR - 1 of the 16 (rows past M repeat row M - 1),
+  // the norm: wave w takes rows NR w .. NR w + NR - 1 of the ROWS (rows past M repeat row M - 1),
   // lane l chunk 64 j + l of each (8 elements)
   {
-    constexpr int MAXC = SKN_MAX_K / 512, NR = (16 + SKN_W - 1) / SKN_W;
+    constexpr int MAXC = SKN_MAX_K / 512, NR = (ROWS + SKN_W - 1) / SKN_W;
     uint4 xv[NR][MAXC], gv[MAXC];
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
@@ -664,7 +665,7 @@ __device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
       gv[c] = *(const uint4*)((const uint16_t*)a.norm_w + 8 * k8);
 #pragma unroll
       for (int i = 0; i < NR; ++i)
-        xv[i][c] = *(const uint4*)((const uint16_t*)a.x + min((long long)min(NR * wave + i, 15), a.M - 1) * a.ldx + 8 * k8);
+        xv[i][c] = *(const uint4*)((const uint16_t*)a.x + min((long long)min(NR * wave + i, ROWS - 1), a.M - 1) * a.ldx + 8 * k8);
     }
     if (live) {
 #pragma unroll
@@ -672,7 +673,7 @@ __device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
     }
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      if (NR * wave + i >= 16) break;   // (wave-uniform) past the 16 rows
+      if (NR * wave + i >= ROWS) break;   // (wave-uniform) past the rows
       float acc = 0.f;
 #pragma unroll
       for (int c = 0; c < MAXC; ++c) {
@@ -703,13 +704,17 @@ __device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
           o[j] = (uint32_t)y0 | ((uint32_t)y1 << 16);
         }
         const int k8 = c * 64 + lane, s = k8 >> 3, ch = k8 & 7;   // stage, chunk of the stage
-        xsr[s * 128 + (row >> 3) * 64 + (row & 7) * 8 + (ch ^ (row & 7))] = make_uint4(o[0], o[1], o[2], o[3]);
+        const int tr = row & 15;                                  // row of its 16-row tile
+        xsr[(s * MT + (row >> 4)) * 128 + (tr >> 3) * 64 + (tr & 7) * 8 + (ch ^ (tr & 7))] =
+            make_uint4(o[0], o[1], o[2], o[3]);
       }
     }
   }
   __syncthreads();
   if (!live) return;
-  sk_f32x4 acc = sk_f32x4{0.f, 0.f, 0.f, 0.f};
+  sk_f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = sk_f32x4{0.f, 0.f, 0.f, 0.f};
   int fa[2], fb[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -728,45 +733,54 @@ __device__ __forceinline__ void skinny_silu_norm_body(const GemvArgs& a) {
       for (int u = 0; u < 2; ++u) {
         uint4 av = rw[p * 128 + fa[u]];
         av = make_uint4(av.x & ok, av.y & ok, av.z & ok, av.w & ok);
-        const uint4 bv = xw[st * 128 + fb[u]];
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sk_bf16x8, av),
-                                                      __builtin_bit_cast(sk_bf16x8, bv), acc, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const uint4 bv = xw[(st * MT + t) * 128 + fb[u]];
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sk_bf16x8, av),
+                                                           __builtin_bit_cast(sk_bf16x8, bv), acc[t], 0, 0, 0);
+        }
       }
       sk_lgkm0();   // this slot's reads are done before it is refilled
       issue_a(v + RA, p);
     }
   }
   sk_vmcnt<0>();
-  float g[4], u[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    g[i] = acc[i];
-    u[i] = __shfl_xor(acc[i], 32, 64);
-  }
-  const int m = r16;
-  if (lane < 32 && m < a.M) {
-    uint16_t h[4];
+  for (int t = 0; t < MT; ++t) {
+    float g[4], u[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int n = min(n0 + 4 * q + i, a.N - 1);
-      float v = g[i], uu = u[i];
-      if (a.flags & 1) v += bf(a.bias, n);
-      if (a.flags & 4) uu += bf(a.bias2, n);
-      v = rbf(v);
-      uu = rbf(uu);
-      h[i] = f32_to_bf16(rbf(v / (1.f + expf(-v))) * uu);
+      g[i] = acc[t][i];
+      u[i] = __shfl_xor(acc[t][i], 32, 64);
     }
-    uint16_t* o = (uint16_t*)a.out + (long long)m * a.ldo + n0 + 4 * q;
-    if (n0 + 4 * q + 3 < a.N && (((a.ldo | n0) & 3) == 0)) {
-      *(uint2*)o = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
-    } else {
+    const int m = t * 16 + r16;
+    if (lane < 32 && m < a.M) {
+      uint16_t h[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (n0 + 4 * q + i < a.N) o[i] = h[i];
+      for (int i = 0; i < 4; ++i) {
+        const int n = min(n0 + 4 * q + i, a.N - 1);
+        float v = g[i], uu = u[i];
+        if (a.flags & 1) v += bf(a.bias, n);
+        if (a.flags & 4) uu += bf(a.bias2, n);
+        v = rbf(v);
+        uu = rbf(uu);
+        h[i] = f32_to_bf16(rbf(v / (1.f + expf(-v))) * uu);
+      }
+      uint16_t* o = (uint16_t*)a.out + (long long)m * a.ldo + n0 + 4 * q;
+      if (n0 + 4 * q + 3 < a.N && (((a.ldo | n0) & 3) == 0)) {
+        *(uint2*)o = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n0 + 4 * q + i < a.N) o[i] = h[i];
+      }
     }
   }
 }
 
+extern "C" __global__ void __launch_bounds__(512) k_skinny_silu_norm_mt2_k1536(const GemvArgs a) {
+  skinny_silu_norm_body<1536, 4, 8, 2>(a);
+}
 extern "C" __global__ void __launch_bounds__(64 * SKN_W) k_skinny_silu_norm_mt1_k1536(const GemvArgs a) {
   skinny_silu_norm_body<1536, SKN_RA>(a);
 }

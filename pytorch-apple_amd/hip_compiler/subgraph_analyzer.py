@@ -626,8 +626,8 @@ class Lowering:
 
     def emit_skinny_silu_norm(self, x_name: str, w, w_name: str, w2: str, b_name: str | None, b2: str | None,
                               out_name: str, out_shape, nodes: list[str]) -> bool:
-        """SiLU(x W^T) * (x W2^T) for at most 16 rows whose pending RMSNorm is folded in
-        (gemv.hip ``k_skinny_silu_norm_mt1_k*``: each workgroup of 8 waves normalises the rows into
+        """SiLU(x W^T) * (x W2^T) for at most 32 rows whose pending RMSNorm is folded in
+        (gemv.hip ``k_skinny_silu_norm_mt*``: each workgroup of 8 waves normalises the rows into
         LDS once, one 8 + 8-row tile per wave); False when ``x`` has no foldable norm or more rows."""
         norm = self.foldable_norm(x_name, set(nodes))
         if norm is None:
@@ -635,13 +635,14 @@ class Lowering:
         N, K = w.shape
         xr = self.aligned16(self.contiguous(norm["x"]), norm["x"])
         M = xr.numel // K
-        if M > 16 or xr.numel != M * K:
+        if M > 32 or (M > 16 and K > 1536) or xr.numel != M * K:
             return False
         o = self.new_storage(out_name, out_shape, "bfloat16")
         bias = self.contiguous(b_name) if b_name else None
         wv2 = self.aligned16(self.contiguous(w2), w2)
         bv2 = self.contiguous(b2) if b2 else None
-        kname = "k_skinny_silu_norm_mt1_k1536" if K <= 1536 else "k_skinny_silu_norm_mt1_k2048"
+        kname = ("k_skinny_silu_norm_mt2_k1536" if M > 16 else
+                 "k_skinny_silu_norm_mt1_k1536" if K <= 1536 else "k_skinny_silu_norm_mt1_k2048")
         args = dict(x=self.ref(xr), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
                     resid=None, w2=self.ref(wv2), bias2=self.ref(bv2) if bv2 else None,
                     norm_w=self.ref(self.aligned16(self.contiguous(norm["w"]), norm["w"])), argmax_slot=None,
