@@ -324,7 +324,7 @@ def run_copy_probe(device_index: int, stream, mib: int = 512, repeats: int = 3) 
     return ms.value / repeats
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_ctx2048_hbm_traffic.md")
+TRAFFIC_GLOB = os.path.join(ROOT, "profiles", "*_hbm_traffic.md")
 
 
 STAMP_NAMES = ("A weights in", "A x in", "A q/k/v published", "B q/k/v in", "B partial published",
@@ -384,15 +384,18 @@ def decode_stamps(hexec, ex, state, L: int, steps: int = 6) -> dict:
             "kernel_us": round(float(t[0, L * 16 + 3]), 2)}
 
 
-def measured_traffic(kernel: str) -> int | None:
-    """HBM bytes per launch of ``kernel`` from the committed FETCH_SIZE / WRITE_SIZE summary
-    (lines ``traffic_bytes_per_launch <kernel> <bytes>``), or None when it has no entry."""
-    if not os.path.exists(TRAFFIC_FILE):
-        return None
-    for line in open(TRAFFIC_FILE):
-        parts = line.strip().strip("`").split()
-        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
-            return int(parts[2])
+def measured_traffic(kernel: str, workload: str | None = None) -> int | None:
+    """HBM bytes per launch of ``kernel`` from the committed FETCH_SIZE / WRITE_SIZE summaries
+    (lines ``traffic_bytes_per_launch <kernel> <bytes>``, or ``... <bytes> <workload>`` for a
+    figure measured on one workload's shapes), or None when none has an entry."""
+    import glob
+
+    for path in sorted(glob.glob(TRAFFIC_GLOB)):
+        for line in open(path):
+            parts = line.strip().strip("`").split()
+            if (len(parts) in (3, 4) and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel
+                    and (parts[3] if len(parts) == 4 else None) == workload):
+                return int(parts[2])
     return None
 
 
@@ -886,6 +889,11 @@ def main_block(args) -> int:
                "sample": f"the same graph through DAGExecutor's all-CPU plan (ATen bf16, {n} threads), median of 5 "
                          f"runs after 3 warmups: {med * 1e3:.2f} ms per run"}
         log(f"cpu: {cpu}")
+    # HBM bytes per step from the committed counter summaries of this workload's kernels (None
+    # unless every launch of the step has one)
+    tag = f"{args.workload}_t{args.tokens}" if args.workload == "mlp" else args.workload
+    per_launch = [measured_traffic(st.kernel, tag) for st in program.steps]
+    step_traffic = sum(per_launch) if all(v is not None for v in per_launch) else None
     line = {
         "metric": f"Qwen2.5-1.5B-shaped {args.workload} block bf16: achieved HBM GB/s vs peak ({unit_note})",
         "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -897,7 +905,7 @@ def main_block(args) -> int:
                    "kernels_in_step_event_us": {k: {"launches_per_step": len(per[k]),
                                                     "avg_us": round(ktimes[k] * 1e3, 3)} for k in per}},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": step_traffic},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
