@@ -600,7 +600,7 @@ def main() -> int:
     in_step_ms = time_in_step(hexec, lin, args.kernel_repeats, stream)
     log(f"dominant {dom}: {avg_ms * 1e3:.2f} us per launch ({achieved:.0f} GB/s); "
         f"{in_step_ms * 1e3:.2f} us with per-launch events inside the step")
-    traffic = measured_traffic(dom)
+    traffic = measured_traffic(dom, f"decode_s{S}")   # (the counter summary of this cache length)
     stamps = None
     if args.stamps and program.steps[0].kind == "decode_step":
         stamps = decode_stamps(hexec, ex, dict(state), cfg.layers)
