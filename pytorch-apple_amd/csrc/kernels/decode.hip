@@ -548,10 +548,19 @@ __device__ __forceinline__ void dec_attend(const PersistArgs& a, int l, uint16_t
 // read its K / V rows (from L2 after the first); over a long cache that is G times the rows per
 // workgroup (Qwen2.5-1.5B at 32,768 positions: 1 MB per workgroup and layer, ≈ 28 µs at the rate
 // one CU reads). Here workgroup (KV head, slot) reads each of its rows once and scores them for all
-// G heads: per chunk the K and V rows are loaded as in dec_attend, and each head keeps its own
-// running (max, sum, output) per wave. One partial per (query head, slot) as in dec_attend.
+// G heads at once on MFMA: per chunk each wave takes its 16 positions, S = K Q^T on
+// v_mfma_f32_16x16x32_bf16 (16 positions x 16 heads, the heads past G zero), the online softmax of
+// every head over the tile (a head's 16 scores sit in 4 registers of 4 lanes), and O += P V on
+// v_mfma_f32_16x16x16_bf16 (P rounded to bf16, as the CPU path rounds the probabilities before
+// P · V), V staged transposed through the wave's own LDS. Scores are rounded as in dec_attend
+// (bf16 of the dot product, of its scaled value, of the masked sum). One partial per (query head,
+// slot) as in dec_attend.
 // qw: the KV head's G exchange blocks [q_h | k | v] (one contiguous range); partw: the layer's
-// partials (query head h, slot s at (h NT + s) (D + 4)); osh: G x 8 waves x D floats of free LDS.
+// partials (query head h, slot s at (h NT + s) (D + 4)); osh: G x 8 waves x D floats of free LDS,
+// then 8 x 4 KB for the waves' transposed V tiles.
+typedef short dec_s16x4 __attribute__((ext_vector_type(4)));
+typedef float dec_f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((ext_vector_type(8))) __bf16 dec_bf16x8;
 __device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint16_t* kcache, uint16_t* vcache,
                                               const uint32_t* qw, uint32_t* partw, uint32_t ob, int kvh, int slot,
                                               long long cpos, uint32_t tag, uint32_t* err, unsigned char* smem,
@@ -559,19 +568,20 @@ __device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint1
                                               int lane, int wave) {
   const int NT = a.nsplit, G = a.H / a.KVH;
   const long long S = a.S, last = S - 1, kvs = a.kv_head_stride;
-  const int kq = lane >> 2, kc = lane & 3;
+  const int mq = lane >> 4, m16 = lane & 15;   // MFMA operand coordinates: k group, row / column
   uint16_t* raw = (uint16_t*)smem;                             // [G][3 D]: the G blocks as produced
   uint16_t* rot = (uint16_t*)(smem + G * 3 * DEC_D * 2);       // [G + 1][D]: each head's rotated q, then k
+  uint32_t* vt = (uint32_t*)(osh + G * DEC_WAVES * DEC_D) + wave * (DEC_D * 8);   // [D][16 positions] bf16
   const float* csh = rope_cs;
   const uint16_t* Kb = kcache + (long long)kvh * kvs;
   const uint16_t* Vb = vcache + (long long)kvh * kvs;
   const bool cin = cpos >= 0 && cpos < S;
-  float acc0[DEC_MAXG], acc1[DEC_MAXG], mw[DEC_MAXG], lw[DEC_MAXG];
+  // O[head 4 mq + r][dim 16 c + m16] in oacc[c][r]; the running max / sum of head m16
+  dec_f32x4 oacc[8];
 #pragma unroll
-  for (int g = 0; g < DEC_MAXG; ++g) {
-    acc0[g] = acc1[g] = lw[g] = 0.f;
-    mw[g] = -INFINITY;
-  }
+  for (int c = 0; c < 8; ++c) oacc[c] = dec_f32x4{0.f, 0.f, 0.f, 0.f};
+  float mwk = -INFINITY, lwk = 0.f;
+  uint4 qb[4];   // B of S = K Q^T: head m16's rotated q, dims 32 s + 8 mq .. (heads past G: zero)
   auto rope = [&]() {   // rotate_half RoPE of the G q rows and the k row
     for (int i = tid; i < (G + 1) * 64; i += DEC_THREADS) {
       const int hs = i >> 6, j = i & 63;
@@ -587,81 +597,104 @@ __device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint1
       stg2(kcache + (long long)kvh * kvs + cpos * DEC_D + tid, rot[G * DEC_D + tid]);
       stg2(vcache + (long long)kvh * kvs + cpos * DEC_D + tid, raw[2 * DEC_D + tid]);
     }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      qb[s4] = m16 < G ? *(const uint4*)(rot + m16 * DEC_D + 32 * s4 + 8 * mq) : make_uint4(0, 0, 0, 0);
   };
-  // one chunk folded into every head's running softmax (dec_attend's fold, per head)
-  auto fold = [&](const uint4 (&kin)[4], const uint32_t (&vr)[16], FRaw mraw, long long p0) {
+  // one chunk's 16 positions of this wave (p0 ..) folded into every head's running softmax.
+  // kin: the A operand (position p0 + m16, dims 32 s + 8 mq ..); vr: dims 2 lane, 2 lane + 1 of
+  // the 16 positions; mr: the mask values of positions p0 + 4 mq + r
+  auto fold = [&](const uint4 (&kin)[4], const uint32_t (&vr)[16], const FRaw (&mr)[4], long long p0) {
     uint4 kr[4] = {kin[0], kin[1], kin[2], kin[3]};
     const bool vnew = cin && cpos >= p0 && cpos < p0 + 16;
-    const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
-    if (vnew && p0 + kq == cpos) {
-      const uint4* kn = (const uint4*)(rot + G * DEC_D + kc * 32);
+    if (vnew && p0 + m16 == cpos) {   // this step's k row, not yet in the cache as read
 #pragma unroll
-      for (int j = 0; j < 4; ++j) kr[j] = kn[j];
+      for (int s4 = 0; s4 < 4; ++s4) kr[s4] = *(const uint4*)(rot + G * DEC_D + 32 * s4 + 8 * mq);
     }
-    const float mdec = a.mask_dtype < 0 ? 0.f : ld_f_decode(mraw, a.mask_dtype);
-    const float mval = (p0 + kq <= last) ? mdec : -INFINITY;
-    const bool live = __ballot(mval != -INFINITY) != 0ull;
-    if (!live) return;
+    float mval[4];
+    bool any = false;
 #pragma unroll
-    for (int g = 0; g < DEC_MAXG; ++g) {
-      if (g < G) {   // workgroup-uniform
-        const uint4* qq = (const uint4*)(rot + g * DEC_D + kc * 32);
-        float d = 0.f;
+    for (int r = 0; r < 4; ++r) {
+      const float md = a.mask_dtype < 0 ? 0.f : ld_f_decode(mr[r], a.mask_dtype);
+      mval[r] = (p0 + 4 * mq + r <= last) ? md : -INFINITY;
+      any = any || mval[r] != -INFINITY;
+    }
+    if (__ballot(any) == 0ull) return;   // every position of the tile closed
+    dec_f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint4 q4 = qq[j];
-          d = ddot2(q4.x, kr[j].x, d);
-          d = ddot2(q4.y, kr[j].y, d);
-          d = ddot2(q4.z, kr[j].z, d);
-          d = ddot2(q4.w, kr[j].w, d);
-        }
-        d += HS_DPP(d, HS_QUAD_XOR1);
-        d += HS_DPP(d, HS_QUAD_XOR2);
-        float sc = -INFINITY;
-        if (mval != -INFINITY) {
-          sc = rb(d);
-          sc = rb(sc * a.scale);
-          if (a.mask_dtype >= 0) sc = round_to(sc + mval, a.add_dtype);
-        }
-        float m = fmaxf(sc, HS_DPP(sc, HS_ROW_ROR4));
-        m = fmaxf(m, HS_DPP(m, HS_ROW_ROR8));
-        m = fmaxf(fmaxf(HS_RL(m, 0), HS_RL(m, 16)), fmaxf(HS_RL(m, 32), HS_RL(m, 48)));
-        const float mn = fmaxf(mw[g], m);
-        const float al = (mw[g] == -INFINITY) ? 0.f : __expf(mw[g] - mn);
-        const float e = (sc == -INFINITY) ? 0.f : __expf(sc - mn);
-        float ls = e + HS_DPP(e, HS_ROW_ROR4);
-        ls += HS_DPP(ls, HS_ROW_ROR8);
-        lw[g] = lw[g] * al + ((HS_RL(ls, 0) + HS_RL(ls, 16)) + (HS_RL(ls, 32) + HS_RL(ls, 48)));
-        mw[g] = mn;
-        float o0 = acc0[g] * al, o1 = acc1[g] * al;
-        float pv[16];   // as in dec_attend, through LDS past the rotated rows
-        {
-          float* pb = (float*)(rot + (G + 1) * DEC_D) + wave * 16;
-          if ((lane & 3) == 0) pb[lane >> 2] = e;
+    for (int s4 = 0; s4 < 4; ++s4)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dec_bf16x8, kr[s4]),
+                                                     __builtin_bit_cast(dec_bf16x8, qb[s4]), sacc, 0, 0, 0);
+    // sacc[r]: the score of position p0 + 4 mq + r for head m16
+    float sc[4], m = -INFINITY;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) *(float4*)&pv[4 * j] = ((const float4*)pb)[j];
-        }
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-          const float p = pv[t];
-          const uint32_t vt = (vnew && p0 + t == cpos) ? vn : vr[t];
-          o0 = fmaf(p, bfh((uint16_t)(vt & 0xffffu)), o0);
-          o1 = fmaf(p, bfh((uint16_t)(vt >> 16)), o1);
-        }
-        acc0[g] = o0;
-        acc1[g] = o1;
+    for (int r = 0; r < 4; ++r) {
+      float x = -INFINITY;
+      if (mval[r] != -INFINITY) {
+        x = rb(sacc[r]);
+        x = rb(x * a.scale);
+        if (a.mask_dtype >= 0) x = round_to(x + mval[r], a.add_dtype);
       }
+      sc[r] = x;
+      m = fmaxf(m, x);
     }
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const float mn = fmaxf(mwk, m);
+    const float al = (mwk == -INFINITY) ? 0.f : __expf(mwk - mn);
+    float e[4], ls = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e[r] = (sc[r] == -INFINITY) ? 0.f : __expf(sc[r] - mn);
+      ls += e[r];
+    }
+    ls += __shfl_xor(ls, 16, 64);
+    ls += __shfl_xor(ls, 32, 64);
+    lwk = lwk * al + ls;
+    mwk = mn;
+    // P as the A operand of O = P V: lane l holds P[head m16][position 4 mq + r], the layout S has
+    const dec_s16x4 pa = {(short)f32_to_bf16(e[0]), (short)f32_to_bf16(e[1]), (short)f32_to_bf16(e[2]),
+                          (short)f32_to_bf16(e[3])};
+    // O's rows are heads 4 mq + r: their rescale factors from the lanes that hold those heads
+    float alr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) alr[r] = __shfl(al, 4 * mq + r, 64);
+    // V transposed into the wave's LDS tile (the new v row in place of the cache's): dims 2 lane and
+    // 2 lane + 1, two positions per word; one wave's LDS accesses complete in order
+    const uint32_t vn = *(const uint32_t*)(raw + 2 * DEC_D + 2 * lane);
+#pragma unroll
+    for (int t = 0; t < 16; t += 2) {
+      const uint32_t v0 = (vnew && p0 + t == cpos) ? vn : vr[t];
+      const uint32_t v1 = (vnew && p0 + t + 1 == cpos) ? vn : vr[t + 1];
+      vt[(2 * lane) * 8 + t / 2] = (v0 & 0xFFFFu) | (v1 << 16);
+      vt[(2 * lane + 1) * 8 + t / 2] = (v0 >> 16) | (v1 & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) oacc[c][r] *= alr[r];
+      // B: V[positions 4 mq ..][dim 16 c + m16]
+      const uint2 vb = *(const uint2*)(vt + (16 * c + m16) * 8 + 2 * mq);
+      oacc[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(dec_s16x4, vb), oacc[c], 0, 0, 0);
+    }
+  };
+  auto kload = [&](uint4 (&kr)[4], long long p0) {   // the A operand rows of a tile
+    const uint16_t* kp = Kb + min(p0 + m16, last) * DEC_D + 8 * mq;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) kr[s4] = ldg16(kp + 32 * s4);
+  };
+  auto mload = [&](FRaw (&mr)[4], long long p0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mr[r] = a.mask_dtype >= 0 ? ld_f_raw(a.mask, min(p0 + 4 * mq + r, last), a.mask_dtype)
+                                                         : FRaw{0, 0};
   };
   if (ob != 0) {   // workgroup-uniform
     uint32_t rest = ob & (ob - 1);
     const long long q0 = (long long)(slot + NT * __builtin_ctz(ob)) * DEC_SPL + wave * 16;
     uint4 kr[4];
-    FRaw mraw = {0, 0};
-    if (a.mask_dtype >= 0) mraw = ld_f_raw(a.mask, min(q0 + kq, last), a.mask_dtype);
-    const uint4* ks = (const uint4*)(Kb + min(q0 + kq, last) * DEC_D + kc * 32);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kr[j] = ldg16(ks + j);
+    FRaw mr[4];
+    mload(mr, q0);
+    kload(kr, q0);
     __syncthreads();
     xgather<3>(qw, G * 3 * DEC_D, tag, raw, err, a.host_err, tid);
     DEC_STAMP(l, 3);
@@ -669,17 +702,15 @@ __device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint1
 #pragma unroll
     for (int t = 0; t < 16; ++t) vr[t] = ldg4(Vb + min(q0 + t, last) * DEC_D + 2 * lane);
     rope();
-    fold(kr, vr, mraw, q0);
+    fold(kr, vr, mr, q0);
     while (rest != 0) {   // workgroup-uniform
       const long long pc = (long long)(slot + NT * __builtin_ctz(rest)) * DEC_SPL + wave * 16;
       rest &= rest - 1;
       uint4 kr2[4];
       uint32_t vr2[16];
-      FRaw m2 = {0, 0};
-      if (a.mask_dtype >= 0) m2 = ld_f_raw(a.mask, min(pc + kq, last), a.mask_dtype);
-      const uint4* ks2 = (const uint4*)(Kb + min(pc + kq, last) * DEC_D + kc * 32);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) kr2[j] = ldg16(ks2 + j);
+      FRaw m2[4];
+      mload(m2, pc);
+      kload(kr2, pc);
 #pragma unroll
       for (int t = 0; t < 16; ++t) vr2[t] = ldg4(Vb + min(pc + t, last) * DEC_D + 2 * lane);
       fold(kr2, vr2, m2, pc);
@@ -690,16 +721,18 @@ __device__ __forceinline__ void dec_attend_kv(const PersistArgs& a, int l, uint1
     DEC_STAMP(l, 3);
     rope();
   }
+  // the wave's outputs of heads < G, and each head's (max, sum) from its lane m16 (of k group 0)
 #pragma unroll
-  for (int g = 0; g < DEC_MAXG; ++g) {
-    if (g < G) {
-      osh[(g * DEC_WAVES + wave) * DEC_D + 2 * lane] = acc0[g];
-      osh[(g * DEC_WAVES + wave) * DEC_D + 2 * lane + 1] = acc1[g];
-      if (lane == 0) {
-        red[wave * 8 + g] = mw[g];
-        red2[wave * DEC_MAXG + g] = lw[g];
-      }
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * mq + r;
+    if (h < G) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) osh[(h * DEC_WAVES + wave) * DEC_D + 16 * c + m16] = oacc[c][r];
     }
+  }
+  if (mq == 0 && m16 < G) {
+    red[wave * 8 + m16] = mwk;
+    red2[wave * DEC_MAXG + m16] = lwk;
   }
   __syncthreads();
   for (int i = tid; i < G * (DEC_D + 4); i += DEC_THREADS) {
