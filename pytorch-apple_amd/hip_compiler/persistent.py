@@ -56,12 +56,13 @@ RING_ROWS = {1: (1, 2), 2: (4,), 3: (2, 3, 4, 6)}   # kernel instances: gate/up 
 # even split, 15 and 15: 0.733; 12: 0.725; 13-14: 0.734)
 O_RING_MAX = 11
 # caches from this length on take the KV-head-major attention (decode.hip dec_attend_kv): one
-# workgroup per (KV head, slot) scores all G query heads of the K / V rows it reads, G times fewer
-# bytes per workgroup than one workgroup per (query head, slot), at G head-folds per chunk and a
-# combine of G times more partials. Measured (Qwen2.5-1.5B, positions near the cache end, tok/s
-# KV-major / head-major): 8,192: 1,100 / 1,199; 16,384: 941 / 967; 32,768: 840 / 697. The kernel
-# instances that have it, by (KC, EM)
-KV_MAJOR_MIN_S = int(os.environ.get("HIPRT_DECODE_KV_MIN_S", "24577"))
+# workgroup per (KV head, slot) scores all G query heads of the K / V rows it reads on MFMA, G times
+# fewer bytes per workgroup than one workgroup per (query head, slot), at a combine of G times more
+# partials. Measured (Qwen2.5-1.5B, positions 128 before the cache end, tok/s KV-major /
+# head-major): 8,192: 1,141 / 1,214; 10,240: 1,134 / 1,146; 12,288: 1,117 / 1,087; 14,336:
+# 1,034 / 1,035; 16,384: 1,026 / 987; 24,576: 1,005 / 827. The kernel instances that have it, by
+# (KC, EM)
+KV_MAJOR_MIN_S = int(os.environ.get("HIPRT_DECODE_KV_MIN_S", "12288"))
 KV_MAJOR = {(3, 2), (1, 1)}
 MAX_KV_SLOTS = 128    # decode.hip DecShared::cwk (the combine's slot weights)
 # query heads per KV head, at most, whose q / k / v rows, rotated rows and the 8 waves' chunk

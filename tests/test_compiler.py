@@ -405,10 +405,10 @@ def test_long_caches_take_the_kv_head_major_attention():
 
     cfg = QwenConfig(layers=1)
     G = cfg.heads // cfg.kv_heads
-    steps = {S: compile_subgraph(build_decode_ir(S, cfg, argmax=True)).steps for S in (16384, 32768)}
-    (short,), (long_,) = steps[16384], steps[32768]
+    steps = {S: compile_subgraph(build_decode_ir(S, cfg, argmax=True)).steps for S in (8192, 32768)}
+    (short,), (long_,) = steps[8192], steps[32768]
     assert not short.kernel.endswith("_kv") and long_.kernel.endswith("_kv") and long_.params["kv_major"]
-    assert 16384 < P.KV_MAJOR_MIN_S <= 32768
+    assert 8192 < P.KV_MAJOR_MIN_S <= 32768
     ns = int(long_.args["nsplit"])
     assert ns == G * P.MAX_SLOTS and cfg.kv_heads * ns == long_.params["work_split"]["NB"]
     assert -(-int(long_.args["nchunk"]) // ns) <= P.MAX_CHUNKS_PER_SLOT

@@ -88,7 +88,7 @@ CASES = {
     # the reference's benchmark cache length: 17 open chunks of 256 (slot 0 folds two)
     "real_s32768_pos2048": (dict(layers=2), 32768, 2048),
     "real_s128": (dict(layers=1), 128, 77),
-    # KV-head-major attention (taken by default from 24,577 positions; these cases lower the
+    # KV-head-major attention (taken by default from 12,288 positions; these cases lower the
     # threshold): 64 chunks over 96 slots per KV head (slots 64..95 hold none), the position in
     # the last chunk
     "real_s8192_pos8000_kv": (dict(layers=2), 8192, 8000),
