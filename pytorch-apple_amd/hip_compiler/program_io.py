@@ -122,7 +122,7 @@ def compiler_fingerprint() -> str:
 def lowering_settings(options: dict) -> dict:
     """The resolved values of every setting that changes the lowering besides the call's own
     options: environment switches read at compile time and module-level switches."""
-    from hip_compiler import patterns, subgraph_analyzer
+    from hip_compiler import patterns, persistent, subgraph_analyzer
 
     fold = options.get("fold_attention")
     return {
@@ -135,6 +135,10 @@ def lowering_settings(options: dict) -> dict:
         "fuse_reduce_norm": bool(patterns.FUSE_REDUCE_NORM),
         "persistent_decode": (os.environ.get("HIPRT_PERSISTENT", "1") == "1") if options.get("persistent") is None
         else bool(options["persistent"]),
+        "decode_kv_major_min_s": int(persistent.KV_MAJOR_MIN_S),
+        "decode_slot_combine": bool(persistent.SLOT_COMBINE),
+        "skinny_min_m": int(subgraph_analyzer.SKINNY_MIN_M),
+        "skinny_norm_max_k": int(subgraph_analyzer.SKINNY_NORM_MAX_K),
     }
 
 
