@@ -788,6 +788,162 @@ extern "C" __global__ void __launch_bounds__(64 * SKN_W) k_skinny_silu_norm_mt1_
   skinny_silu_norm_body<2048, SKN_RA>(a);
 }
 
+// SILU over up to 16 MT activation rows (k_wide_silu_mt*, MT = 4 or 8: 33 to 128 rows): a
+// workgroup of 4 waves owns TA tiles of 8 gate + 8 up rows (the tiles of k_skinny_silu_*) and all
+// MT activation tiles. A K stage of 64 is TA 2 KB of weight rows and MT 2 KB of activation rows
+// (1 KB = 8 rows x 128 B, chunk c of row r in slot c ^ (r & 7)); it lands in one of R LDS slots,
+// R - 1 stages ahead of the one being multiplied, its 2 TA + 2 MT loads dealt round-robin to the
+// 4 waves (UPW each; a wave with fewer repeats the stage's last load, so every wave waits for the
+// same count). Per stage a wave waits for its own loads of the stage, then one barrier makes the
+// whole stage visible and frees the slot read one stage before, which the next issue refills.
+// Wave w multiplies every weight tile of the stage by activation tiles w MT / 4 .. (w + 1) MT / 4
+// - 1. Every weight element is read from HBM once; the activation rows (L2-resident) once per
+// workgroup. Per CU that is 3 KB x K / 1536 per weight or activation row: at K = 1536, TA = 5,
+// MT = 8, 80 weight rows and 128 activation rows, 624 KB.
+template <int MT, int TA, int R>
+__device__ __forceinline__ void wide_silu_body(const GemvArgs& a) {
+  constexpr int TW = MT / 4, U = 2 * TA + 2 * MT, UPW = (U + 3) / 4, SLOT = U * 64;   // SLOT: uint4
+  static_assert(MT % 4 == 0 && R >= 2, "shape");
+  __shared__ uint4 ring[R * SLOT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15, lr = lane >> 3;
+  const int K = a.K, ns = K >> 6, p0 = blockIdx.x * TA * 8;   // stages; first output pair
+  const int cl = 8 * ((lane & 7) ^ lr);                        // this lane's source chunk (elements)
+  const uint16_t* src[UPW];
+  unsigned dst[UPW];
+  const unsigned base = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(sk_lds16*)ring);
+#pragma unroll
+  for (int j = 0; j < UPW; ++j) {
+    const int u = min(wave + 4 * j, U - 1);
+    if (u < 2 * TA) {   // weight tile u / 2, gate (u even) or up rows
+      const long long row = min(p0 + 8 * (u >> 1) + lr, a.N - 1);
+      src[j] = (const uint16_t*)((u & 1) ? a.w2 : a.w) + row * K + cl;
+    } else {            // activation tile (u - 2 TA) / 2, rows 8 ((u - 2 TA) & 1) ..
+      const int v = u - 2 * TA;
+      src[j] = (const uint16_t*)a.x + min((long long)(16 * (v >> 1) + 8 * (v & 1) + lr), a.M - 1) * a.ldx + cl;
+    }
+    dst[j] = __builtin_amdgcn_readfirstlane(base + (unsigned)u * 1024u);
+  }
+  auto issue = [&](int s) {   // stage s (clamped to the last) into slot s % R
+    const int k = min(s, ns - 1) << 6;
+    const unsigned so = (unsigned)(s % R) * (unsigned)SLOT * 16u;
+#pragma unroll
+    for (int j = 0; j < UPW; ++j) sk_dma16(src[j] + k, dst[j] + so);
+  };
+  int fa[2], fb[2];   // fragment slots (uint4) of MFMA step u within a 2-unit tile
+#pragma unroll
+  for (int u = 0; u < 2; ++u) fa[u] = fb[u] = (r16 >> 3) * 64 + (r16 & 7) * 8 + ((4 * u + q) ^ (r16 & 7));
+  sk_f32x4 acc[TA][TW];
+#pragma unroll
+  for (int t = 0; t < TA; ++t)
+#pragma unroll
+    for (int i = 0; i < TW; ++i) acc[t][i] = sk_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < R - 1; ++p) issue(p);
+  // The fragments of stage s are read from LDS while the MFMAs of stage s - 1 run on the
+  // registers read the step before (one wave per SIMD: nothing else hides the LDS latency).
+  const sk_lds16* rl = (const sk_lds16*)ring;
+  uint4 av[2][2][TA], bv[2][2][TW];   // [register set][k half][tile]
+  auto read = [&](int slot, int set) {
+    const sk_lds16* st = rl + slot * SLOT;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int i = 0; i < TW; ++i) bv[set][u][i] = st[(2 * TA + 2 * (wave * TW + i)) * 64 + fb[u]];
+#pragma unroll
+      for (int t = 0; t < TA; ++t) av[set][u][t] = st[2 * t * 64 + fa[u]];
+    }
+  };
+  auto mfma = [&](int set) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int t = 0; t < TA; ++t)
+#pragma unroll
+        for (int i = 0; i < TW; ++i)
+          acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sk_bf16x8, av[set][u][t]),
+                                                              __builtin_bit_cast(sk_bf16x8, bv[set][u][i]), acc[t][i], 0, 0, 0);
+  };
+  static_assert(R % 2 == 0, "register sets alternate with the stage parity");
+  for (int s0 = 0; s0 < ns; s0 += R) {
+#pragma unroll
+    for (int p = 0; p < R; ++p) {
+      if (s0 + p >= ns) break;   // (uniform)
+      sk_vmcnt<(R - 2) * UPW>();   // this wave's loads of stage s0 + p have landed
+      sk_lgkm0();                  // and its reads of the stage before are in registers
+      __syncthreads();             // every wave's: the stage is in LDS, slot (p - 1) % R is free
+      issue(s0 + p + R - 1);
+      read(p, p & 1);
+      if (s0 + p > 0) mfma((p & 1) ^ 1);   // stage s0 + p - 1
+    }
+  }
+  sk_lgkm0();
+  if ((ns - 1) & 1)   // (uniform) register set of the last stage, a constant index either way
+    mfma(1);
+  else
+    mfma(0);
+  sk_vmcnt<0>();   // the clamped tail loads land before the workgroup's LDS is released
+  // lanes 0..31 hold gate rows 4 q + i of the tile, lanes 32..63 the up rows of the same pairs
+#pragma unroll
+  for (int t = 0; t < TA; ++t) {
+    const int n0 = p0 + 8 * t;
+#pragma unroll
+    for (int i2 = 0; i2 < TW; ++i2) {
+      float g[4], u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[i] = acc[t][i2][i];
+        u[i] = __shfl_xor(acc[t][i2][i], 32, 64);
+      }
+      const int m = (wave * TW + i2) * 16 + r16;
+      if (lane < 32 && m < a.M && n0 < a.N) {
+        uint16_t h[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = min(n0 + 4 * q + i, a.N - 1);
+          float v = g[i], uu = u[i];
+          if (a.flags & 1) v += bf(a.bias, n);
+          if (a.flags & 4) uu += bf(a.bias2, n);
+          v = rbf(v);
+          uu = rbf(uu);
+          h[i] = f32_to_bf16(rbf(v / (1.f + expf(-v))) * uu);
+        }
+        uint16_t* o = (uint16_t*)a.out + (long long)m * a.ldo + n0 + 4 * q;
+        if (n0 + 4 * q + 3 < a.N && (((a.ldo | n0) & 3) == 0)) {
+          *(uint2*)o = make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n0 + 4 * q + i < a.N) o[i] = h[i];
+        }
+      }
+    }
+  }
+}
+
+// Measured on the cfg1 block (norm, this kernel, the down GEMM and its reduce) on MI355X, against
+// the 64 x 64 SiLU GEMM tiles it replaces: T = 48 31.1 us against 31.9, T = 64 31.3 / 31.9, T = 100
+// 37.6-38.1 / 38.7, T = 128 37.7-39.0 / 39.0-39.5 (4 stages; 6 stages 39.3-39.8). 3 or 4 weight
+// tiles per workgroup (374 or 280 workgroups) 47.1 and 50.5, 7 (160) 44.9. What bounds it is each
+// CU's intake of 624 KB at 30-37 GB/s: with the MFMAs taken out (loads and fragment reads only) the
+// block took 37.4 us, and overlapping the fragment reads with the previous stage's MFMAs (below)
+// did not change the time.
+#ifndef WIDE_TA
+#define WIDE_TA 5
+#endif
+#ifndef WIDE_R8
+#define WIDE_R8 4
+#endif
+#ifndef WIDE_R4
+#define WIDE_R4 8
+#endif
+extern "C" __global__ void __launch_bounds__(256) k_wide_silu_mt8(const GemvArgs a) {
+  wide_silu_body<8, WIDE_TA, WIDE_R8>(a);
+}
+extern "C" __global__ void __launch_bounds__(256) k_wide_silu_mt4(const GemvArgs a) {
+  wide_silu_body<4, WIDE_TA, WIDE_R4>(a);
+}
+
 #define SKINNY_SILU(NAME, MT, RA, RB) \
   extern "C" __global__ void __launch_bounds__(64) NAME(const GemvArgs a) { skinny_silu_body<MT, RA, RB>(a); }
 #define SKINNY_KERNEL(NAME, EPI, MT, RW, RA, RB) \

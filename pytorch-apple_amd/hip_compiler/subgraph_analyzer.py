@@ -51,6 +51,11 @@ SKINNY_MIN_M = 2
 # most this many elements (its LDS copy of the 16 normalised rows), and its waves per workgroup
 SKINNY_NORM_MAX_K = 2048
 SKINNY_NORM_WAVES = 8
+# gate/up with the SiLU * up epilogue from SKINNY_MAX_M + 1 to this many rows takes the wide
+# streaming kernel (gemv.hip k_wide_silu_mt4 / _mt8: 4 waves per workgroup over WIDE_TA tiles
+# of 8 output pairs and every activation row, weights read once); WIDE_TA must match the kernel's
+WIDE_MAX_M = int(os.environ.get("HIPRT_WIDE_MAX_M", "128"))
+WIDE_TA = 5
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
@@ -677,6 +682,22 @@ class Lowering:
         r = self.contiguous(resid) if resid else None
         wv2 = self.aligned16(self.contiguous(w2), w2) if w2 else None
         bv2 = self.contiguous(b2) if b2 else None
+        if (epi == "silu" and SKINNY_MAX_M < M <= WIDE_MAX_M and M <= 128 and dtype == "bfloat16"
+                and K % 64 == 0 and K >= 512):
+            # one workgroup of 4 waves per WIDE_TA tiles of 8 gate + 8 up rows, over every row
+            args = dict(x=self.ref(x), w=self.ref(w), bias=self.ref(bias) if bias else None, out=self.ref(o),
+                        resid=None, w2=self.ref(wv2), bias2=self.ref(bv2) if bv2 else None, norm_w=None,
+                        argmax_slot=None, attn_o=None, attn_ml=None, M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=0.0,
+                        n_dtype=0, flags=(1 if bias else 0) | (4 if bv2 else 0), attn_heads=0, attn_kvh=0,
+                        attn_splits=0)
+            self.emit(LaunchStep(
+                kind="gemm", kernel=f"k_wide_silu_mt{4 if M <= 64 else 8}", module="gemv", arg_struct="GemvArgs",
+                args=args, grid=(-(-N // (8 * WIDE_TA)), 1, 1), block=(256, 1, 1),
+                inputs=[x_name, w_name, w2] + [t for t in (b_name, b2) if t], outputs=[out_name],
+                params={"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None, "weights": 2,
+                        "transpose_b": True, "nodes": nodes, "mfma": True, "wide": True}))
+            self.views[out_name] = o
+            return
         if M <= SKINNY_MAX_M and dtype == "bfloat16" and K % 64 == 0 and K >= 512 and epi in ("bias", "resid", "silu"):
             # SiLU: one wave per tile of 8 gate + 8 up rows. Bias / residual: 8 waves per tile of
             # 16 output rows (8 when that gives fewer than 256 tiles), splitting K.

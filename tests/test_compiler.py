@@ -36,6 +36,20 @@ def test_mlp_block_fused_and_generic_step_lists():
     assert sum(1 for s in gen16.steps if s.kind == "gemm" and not s.params.get("reduce")) == 3
 
 
+def test_mlp_33_to_128_rows_take_the_wide_silu_kernel():
+    # 33-128 rows: the norm's launch, the wide SiLU kernel (4 waves, 5 tiles of 8 pairs per
+    # workgroup: 224 workgroups for 8960 pairs), then the down GEMM; 129 rows: the GEMM
+    from hip_compiler.subgraph_analyzer import WIDE_TA
+    for T, mt in ((33, 4), (64, 4), (65, 8), (128, 8)):
+        p = compile_subgraph(build_mlp_ir(T))
+        ks = kernels(p)
+        assert ks[0] == "k_rmsnorm_w" and ks[1] == f"k_wide_silu_mt{mt}", (T, ks)
+        st = p.steps[1]
+        assert st.grid == (-(-8960 // (8 * WIDE_TA)), 1, 1) == (224, 1, 1) and st.block == (256, 1, 1)
+        assert st.args["M"] == T and st.args["K"] == 1536 and st.args["w2"] is not None
+    assert not any(k.startswith("k_wide") for k in kernels(compile_subgraph(build_mlp_ir(129))))
+
+
 def test_prefill_mlp_is_norm_plus_two_mfma_gemms():
     p = compile_subgraph(build_mlp_ir(512))
     main = [s for s in p.steps if s.kind == "gemm" and not s.params.get("reduce")]

@@ -244,19 +244,24 @@ def test_views_materialised_bit_exact(backend, view):
     assert np.array_equal(np.ascontiguousarray(got[name]), np.ascontiguousarray(ref[name]))
 
 
-@pytest.mark.parametrize("case", ["bias_r8", "resid_r8", "bias_r16", "silu", "silu_bias", "resid_m24", "silu_m24"])
+@pytest.mark.parametrize("case", ["bias_r8", "resid_r8", "bias_r16", "silu", "silu_bias", "resid_m24", "silu_m24",
+                                  "wide_m33", "wide_m64_bias", "wide_m65", "wide_m128_k2048"])
 def test_skinny_linear_vs_cpu_fallback(backend, case):
     """The skinny MFMA kernels (16-32 activation rows, gemv.hip k_skinny_*): a linear with bias,
     a linear + residual add, and SiLU(gate) * up over two weights, against the CPU fallback;
     the output tile widths (8 / 16 rows, the short-N variant), one and two 16-row tiles, a
-    long K and an N that is not a multiple of the tile."""
+    long K and an N that is not a multiple of the tile. ``wide_*``: SiLU(gate) * up over 33-128
+    rows (k_wide_silu_mt4 / _mt8: rows past M repeat the last, N not a multiple of the
+    workgroup's 40 pairs nor of 8, biases, a K of 32 stages)."""
     from irgen.builder import IRBuilder
     from irgen.qwen import linear
 
     M, N, K, kind = {"bias_r8": (16, 1000, 768, "bias"), "resid_r8": (16, 1536, 8960, "resid"),
                      "bias_r16": (16, 4104, 512, "bias"), "silu": (16, 2056, 1536, "silu"),
                      "silu_bias": (16, 1032, 512, "silu_bias"), "resid_m24": (24, 1536, 2048, "resid"),
-                     "silu_m24": (24, 2048, 1536, "silu")}[case]
+                     "silu_m24": (24, 2048, 1536, "silu"), "wide_m33": (33, 1004, 1536, "silu"),
+                     "wide_m64_bias": (64, 1032, 512, "silu_bias"), "wide_m65": (65, 2056, 1536, "silu"),
+                     "wide_m128_k2048": (128, 8960, 2048, "silu")}[case]
     dt = "bfloat16"
     b = IRBuilder(f"skinny_{case}")
     x = b.input("x0", [M, K], dt)
@@ -286,6 +291,6 @@ def test_skinny_linear_vs_cpu_fallback(backend, case):
             xin[k] = (torch.from_numpy(_f(xin[k]) / np.sqrt(K)).to(torch.bfloat16).view(torch.int16).numpy()
                       .view(np.uint16))
     got, ref, kernels = _run(ir, xin, backend)
-    assert any(k.startswith("k_skinny_") for k in kernels), kernels
+    assert any(k.startswith("k_wide_silu_mt" if case.startswith("wide") else "k_skinny_") for k in kernels), kernels
     (name,) = got
     _close(got[name], ref[name])

@@ -68,11 +68,12 @@ def assert_all_npu(ex):
     assert all(s.target == "npu" for s in ex.plan.steps if isinstance(s, Partition))
 
 
-@pytest.mark.parametrize("tokens", [1, 11, 16, 24, 128])
+@pytest.mark.parametrize("tokens", [1, 11, 16, 24, 48, 100, 128, 129])
 def test_mlp_block_cfg1(backend, tokens):
     """cfg1 at each lowering: the streaming GEMVs (1), the skinny MFMA kernels with the RMSNorm
-    folded into the SiLU one (11: rows past M repeat the last; 16; 24: two 16-row tiles), the MFMA
-    GEMMs (128)."""
+    folded into the SiLU one (11: rows past M repeat the last; 16; 24: two 16-row tiles), the wide
+    SiLU kernel after the norm's launch (48: 4 activation tiles; 100, 128: 8), the MFMA GEMMs
+    (129)."""
     from irgen.qwen import build_mlp_ir
     from irgen.workloads import make_weights, mlp_inputs
     from oracle.numpy_ref import run_ir
@@ -84,6 +85,7 @@ def test_mlp_block_cfg1(backend, tokens):
     assert_all_npu(ex)
     kernels = [st.kernel for p in ex.npu_programs.values() for st in p.steps]
     assert (kernels[0].startswith("k_skinny_silu_norm")) == (2 <= tokens <= 32), kernels
+    assert any(k.startswith("k_wide_silu_mt") for k in kernels) == (32 < tokens <= 128), kernels
     ref = run_cpu(ir, x, w)
     (name,) = got
     close(got[name], ref[name])
