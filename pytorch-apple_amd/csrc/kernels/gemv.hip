@@ -800,14 +800,20 @@ extern "C" __global__ void __launch_bounds__(64 * SKN_W) k_skinny_silu_norm_mt1_
 // - 1. Every weight element is read from HBM once; the activation rows (L2-resident) once per
 // workgroup. Per CU that is 3 KB x K / 1536 per weight or activation row: at K = 1536, TA = 5,
 // MT = 8, 80 weight rows and 128 activation rows, 624 KB.
-template <int MT, int TA, int R>
+// HALVES = 2: the rows split in two halves of 16 MT between two workgroups over the same weight
+// tiles; workgroups b and b + 8 (dispatched to the same XCD, whose L2 then serves the second
+// reader of each weight row) take the halves of tile group (b / 16) 8 + b % 8.
+template <int MT, int TA, int R, int HALVES = 1>
 __device__ __forceinline__ void wide_silu_body(const GemvArgs& a) {
   constexpr int TW = MT / 4, U = 2 * TA + 2 * MT, UPW = (U + 3) / 4, SLOT = U * 64;   // SLOT: uint4
   static_assert(MT % 4 == 0 && R >= 2, "shape");
   __shared__ uint4 ring[R * SLOT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15, lr = lane >> 3;
-  const int K = a.K, ns = K >> 6, p0 = blockIdx.x * TA * 8;   // stages; first output pair
+  const int bx = (int)blockIdx.x;
+  const int grp = HALVES == 1 ? bx : ((bx >> 4) << 3) | (bx & 7), m0 = HALVES == 1 ? 0 : ((bx >> 3) & 1) * 16 * MT;
+  const int K = a.K, ns = K >> 6, p0 = grp * TA * 8;   // stages; first output pair
+  if (HALVES > 1 && (p0 >= a.N || m0 >= a.M)) return;   // (workgroup-uniform) past the tile groups or rows
   const int cl = 8 * ((lane & 7) ^ lr);                        // this lane's source chunk (elements)
   const uint16_t* src[UPW];
   unsigned dst[UPW];
@@ -820,7 +826,7 @@ __device__ __forceinline__ void wide_silu_body(const GemvArgs& a) {
       src[j] = (const uint16_t*)((u & 1) ? a.w2 : a.w) + row * K + cl;
     } else {            // activation tile (u - 2 TA) / 2, rows 8 ((u - 2 TA) & 1) ..
       const int v = u - 2 * TA;
-      src[j] = (const uint16_t*)a.x + min((long long)(16 * (v >> 1) + 8 * (v & 1) + lr), a.M - 1) * a.ldx + cl;
+      src[j] = (const uint16_t*)a.x + min((long long)(m0 + 16 * (v >> 1) + 8 * (v & 1) + lr), a.M - 1) * a.ldx + cl;
     }
     dst[j] = __builtin_amdgcn_readfirstlane(base + (unsigned)u * 1024u);
   }
@@ -895,7 +901,7 @@ __device__ __forceinline__ void wide_silu_body(const GemvArgs& a) {
         g[i] = acc[t][i2][i];
         u[i] = __shfl_xor(acc[t][i2][i], 32, 64);
       }
-      const int m = (wave * TW + i2) * 16 + r16;
+      const int m = m0 + (wave * TW + i2) * 16 + r16;
       if (lane < 32 && m < a.M && n0 < a.N) {
         uint16_t h[4];
 #pragma unroll
@@ -927,7 +933,9 @@ __device__ __forceinline__ void wide_silu_body(const GemvArgs& a) {
 // tiles per workgroup (374 or 280 workgroups) 47.1 and 50.5, 7 (160) 44.9. What bounds it is each
 // CU's intake of 624 KB at 30-37 GB/s: with the MFMAs taken out (loads and fragment reads only) the
 // block took 37.4 us, and overlapping the fragment reads with the previous stage's MFMAs (below)
-// did not change the time.
+// did not change the time. Two 64-row workgroups per tile group (HALVES = 2, k_wide_silu_mt4x2,
+// two per CU): the block at T = 100 36.9-37.2 us and at T = 128 37.8-38.1, against 37.6-38.1 and
+// 38.3-38.5 with one 128-row workgroup.
 #ifndef WIDE_TA
 #define WIDE_TA 5
 #endif
@@ -942,6 +950,12 @@ extern "C" __global__ void __launch_bounds__(256) k_wide_silu_mt8(const GemvArgs
 }
 extern "C" __global__ void __launch_bounds__(256) k_wide_silu_mt4(const GemvArgs a) {
   wide_silu_body<4, WIDE_TA, WIDE_R4>(a);
+}
+#ifndef WIDE_RH
+#define WIDE_RH 4
+#endif
+extern "C" __global__ void __launch_bounds__(256) k_wide_silu_mt4x2(const GemvArgs a) {
+  wide_silu_body<4, WIDE_TA, WIDE_RH, 2>(a);
 }
 
 #define SKINNY_SILU(NAME, MT, RA, RB) \

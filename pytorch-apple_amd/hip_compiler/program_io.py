@@ -140,6 +140,7 @@ def lowering_settings(options: dict) -> dict:
         "skinny_min_m": int(subgraph_analyzer.SKINNY_MIN_M),
         "skinny_norm_max_k": int(subgraph_analyzer.SKINNY_NORM_MAX_K),
         "wide_max_m": int(subgraph_analyzer.WIDE_MAX_M),
+        "wide_halves": bool(subgraph_analyzer.WIDE_HALVES),
     }
 
 

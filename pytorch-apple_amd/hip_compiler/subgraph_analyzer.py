@@ -56,6 +56,9 @@ SKINNY_NORM_WAVES = 8
 # of 8 output pairs and every activation row, weights read once); WIDE_TA must match the kernel's
 WIDE_MAX_M = int(os.environ.get("HIPRT_WIDE_MAX_M", "128"))
 WIDE_TA = 5
+# past 64 rows, two 64-row workgroups per group of weight tiles (k_wide_silu_mt4x2) instead of
+# one 128-row workgroup (k_wide_silu_mt8)
+WIDE_HALVES = os.environ.get("HIPRT_WIDE_HALVES", "1") == "1"
 GEMM_TARGET_WGS = 256    # workgroups a GEMM launch should reach (one per CU)
 GEMM_MIN_KCHUNK = 256    # smallest K range of one split-K workgroup
 GEMM_DMA_MAX_TILES = 1024   # tile grids at least this large keep register staging (gemm_tiling)
@@ -690,9 +693,15 @@ class Lowering:
                         argmax_slot=None, attn_o=None, attn_ml=None, M=M, ldx=K, ldo=N, ldr=N, N=N, K=K, eps=0.0,
                         n_dtype=0, flags=(1 if bias else 0) | (4 if bv2 else 0), attn_heads=0, attn_kvh=0,
                         attn_splits=0)
+            groups = -(-N // (8 * WIDE_TA))
+            if M > 64 and WIDE_HALVES:
+                # two workgroups per tile group, 64 rows each; b and b + 8 share a group
+                kname, grid = "k_wide_silu_mt4x2", (-(-groups // 8) * 16, 1, 1)
+            else:
+                kname, grid = f"k_wide_silu_mt{4 if M <= 64 else 8}", (groups, 1, 1)
             self.emit(LaunchStep(
-                kind="gemm", kernel=f"k_wide_silu_mt{4 if M <= 64 else 8}", module="gemv", arg_struct="GemvArgs",
-                args=args, grid=(-(-N // (8 * WIDE_TA)), 1, 1), block=(256, 1, 1),
+                kind="gemm", kernel=kname, module="gemv", arg_struct="GemvArgs",
+                args=args, grid=grid, block=(256, 1, 1),
                 inputs=[x_name, w_name, w2] + [t for t in (b_name, b2) if t], outputs=[out_name],
                 params={"M": M, "N": N, "K": K, "epilogue": epi, "has_bias": bias is not None, "weights": 2,
                         "transpose_b": True, "nodes": nodes, "mfma": True, "wide": True}))

@@ -38,14 +38,17 @@ def test_mlp_block_fused_and_generic_step_lists():
 
 def test_mlp_33_to_128_rows_take_the_wide_silu_kernel():
     # 33-128 rows: the norm's launch, the wide SiLU kernel (4 waves, 5 tiles of 8 pairs per
-    # workgroup: 224 workgroups for 8960 pairs), then the down GEMM; 129 rows: the GEMM
-    from hip_compiler.subgraph_analyzer import WIDE_TA
-    for T, mt in ((33, 4), (64, 4), (65, 8), (128, 8)):
+    # workgroup: 224 tile groups for 8960 pairs; past 64 rows two workgroups of 64 rows per
+    # group, 448 in all), then the down GEMM; 129 rows: the GEMM
+    from hip_compiler.subgraph_analyzer import WIDE_HALVES, WIDE_TA
+    assert -(-8960 // (8 * WIDE_TA)) == 224
+    for T, kn, g in ((33, "mt4", 224), (64, "mt4", 224), (65, "mt4x2" if WIDE_HALVES else "mt8", 448 if WIDE_HALVES else 224),
+                     (128, "mt4x2" if WIDE_HALVES else "mt8", 448 if WIDE_HALVES else 224)):
         p = compile_subgraph(build_mlp_ir(T))
         ks = kernels(p)
-        assert ks[0] == "k_rmsnorm_w" and ks[1] == f"k_wide_silu_mt{mt}", (T, ks)
+        assert ks[0] == "k_rmsnorm_w" and ks[1] == f"k_wide_silu_{kn}", (T, ks)
         st = p.steps[1]
-        assert st.grid == (-(-8960 // (8 * WIDE_TA)), 1, 1) == (224, 1, 1) and st.block == (256, 1, 1)
+        assert st.grid == (g, 1, 1) and st.block == (256, 1, 1)
         assert st.args["M"] == T and st.args["K"] == 1536 and st.args["w2"] is not None
     assert not any(k.startswith("k_wide") for k in kernels(compile_subgraph(build_mlp_ir(129))))
 

@@ -245,7 +245,7 @@ def test_views_materialised_bit_exact(backend, view):
 
 
 @pytest.mark.parametrize("case", ["bias_r8", "resid_r8", "bias_r16", "silu", "silu_bias", "resid_m24", "silu_m24",
-                                  "wide_m33", "wide_m64_bias", "wide_m65", "wide_m128_k2048"])
+                                  "wide_m33", "wide_m64_bias", "wide_m65", "wide_m128_k2048", "wide_m100_bias"])
 def test_skinny_linear_vs_cpu_fallback(backend, case):
     """The skinny MFMA kernels (16-32 activation rows, gemv.hip k_skinny_*): a linear with bias,
     a linear + residual add, and SiLU(gate) * up over two weights, against the CPU fallback;
@@ -261,7 +261,7 @@ def test_skinny_linear_vs_cpu_fallback(backend, case):
                      "silu_bias": (16, 1032, 512, "silu_bias"), "resid_m24": (24, 1536, 2048, "resid"),
                      "silu_m24": (24, 2048, 1536, "silu"), "wide_m33": (33, 1004, 1536, "silu"),
                      "wide_m64_bias": (64, 1032, 512, "silu_bias"), "wide_m65": (65, 2056, 1536, "silu"),
-                     "wide_m128_k2048": (128, 8960, 2048, "silu")}[case]
+                     "wide_m128_k2048": (128, 8960, 2048, "silu"), "wide_m100_bias": (100, 1004, 512, "silu_bias")}[case]
     dt = "bfloat16"
     b = IRBuilder(f"skinny_{case}")
     x = b.input("x0", [M, K], dt)
