@@ -38,7 +38,10 @@
 // Rounding points are those of the multi-kernel path (and of ATen on the CPU): RMSNorm
 // n = round(x * rsqrt(mean(x^2) + eps)), y = round(w * n); linear round(acc + b); RoPE
 // round(round(x c) + round(-x' s)); attention scores round(round(round(q.k) * scale) + mask);
-// residual round(r + round(acc)); SiLU*mul round(round(silu(round(g))) * round(u)).
+// residual round(r + round(acc)); SiLU*mul round(round(silu(round(g))) * round(u)). One
+// difference: the head-major attention (dec_attend) keeps the probabilities exp(s - m) in fp32
+// into P.V, where ATen's softmax rounds them to bf16 first; the KV-head-major form
+// (dec_attend_kv) rounds them to bf16, as its MFMA operand.
 #include "common.h"
 
 #define DEC_THREADS 512

@@ -245,8 +245,9 @@ def test_views_materialised_bit_exact(backend, view):
 
 
 @pytest.mark.parametrize("case", ["bias_r8", "resid_r8", "bias_r16", "silu", "silu_bias", "resid_m24", "silu_m24",
-                                  "wide_m33", "wide_m64_bias", "wide_m65", "wide_m128_k2048", "wide_m100_bias"])
-def test_skinny_linear_vs_cpu_fallback(backend, case):
+                                  "wide_m33", "wide_m64_bias", "wide_m65", "wide_m128_k2048", "wide_m100_bias",
+                                  "wide_m100_mt8"])
+def test_skinny_linear_vs_cpu_fallback(backend, case, monkeypatch):
     """The skinny MFMA kernels (16-32 activation rows, gemv.hip k_skinny_*): a linear with bias,
     a linear + residual add, and SiLU(gate) * up over two weights, against the CPU fallback;
     the output tile widths (8 / 16 rows, the short-N variant), one and two 16-row tiles, a
@@ -261,7 +262,11 @@ def test_skinny_linear_vs_cpu_fallback(backend, case):
                      "silu_bias": (16, 1032, 512, "silu_bias"), "resid_m24": (24, 1536, 2048, "resid"),
                      "silu_m24": (24, 2048, 1536, "silu"), "wide_m33": (33, 1004, 1536, "silu"),
                      "wide_m64_bias": (64, 1032, 512, "silu_bias"), "wide_m65": (65, 2056, 1536, "silu"),
-                     "wide_m128_k2048": (128, 8960, 2048, "silu"), "wide_m100_bias": (100, 1004, 512, "silu_bias")}[case]
+                     "wide_m128_k2048": (128, 8960, 2048, "silu"), "wide_m100_bias": (100, 1004, 512, "silu_bias"),
+                     "wide_m100_mt8": (100, 2056, 1536, "silu_bias")}[case]
+    if case.endswith("_mt8"):   # one 128-row workgroup per group of weight tiles (k_wide_silu_mt8)
+        from hip_compiler import subgraph_analyzer
+        monkeypatch.setattr(subgraph_analyzer, "WIDE_HALVES", False)
     dt = "bfloat16"
     b = IRBuilder(f"skinny_{case}")
     x = b.input("x0", [M, K], dt)
@@ -292,5 +297,7 @@ def test_skinny_linear_vs_cpu_fallback(backend, case):
                       .view(np.uint16))
     got, ref, kernels = _run(ir, xin, backend)
     assert any(k.startswith("k_wide_silu_mt" if case.startswith("wide") else "k_skinny_") for k in kernels), kernels
+    if case.endswith("_mt8"):
+        assert "k_wide_silu_mt8" in kernels, kernels
     (name,) = got
     _close(got[name], ref[name])
