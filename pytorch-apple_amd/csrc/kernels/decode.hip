@@ -59,9 +59,11 @@
 // once x1 is normalised, the rest once the LDS rows are summed (issuing a wave's loads stalls it
 // while the memory pipe is full, so they are spread over E). 0.714 -> 0.690 ms per step with 2
 // issued as soon as x1 is in (1: 0.695, 3: 0.700, 4: 0.705, 6: 0.721: the h stores queue behind
-// the later ones); 0.681 with 1 + 1 (2 + 1: 0.683, 2 + 2: 0.692, 2 + 0: 0.690, 0 + 2: 0.686)
+// the later ones); 0.681 with 1 + 1 (2 + 1: 0.683, 2 + 2: 0.692, 2 + 0: 0.690, 0 + 2: 0.686).
+// With the current schedule, 4 A/B rounds on one box, kernel µs per launch: 1 + 2 666.1-667.0,
+// 1 + 1 666.9-667.9, 2 + 1 667.5-668.7, 2 + 0 670.4-670.9, 1 + 3 679.0-679.8, 1 + 0 about 680.
 #ifndef DEC_RFE
-#define DEC_RFE 2
+#define DEC_RFE 3
 #endif
 #ifndef DEC_RFE_N
 #define DEC_RFE_N 1
