@@ -341,7 +341,7 @@ def test_persistent_step_reads_chunks_the_mask_opens_beyond_the_position(backend
     w = _host(make_weights(ir, cfg, device="cuda"))
     xt = decode_inputs(S, pos, cfg)
     m = xt["attention_mask"]
-    for p in (2048, 2100, 20000, 31000, 32767):   # chunk 16 (slot 0, round 2), 156, 242, 255
+    for p in (2048, 2100, 20000, 31000, 32767):   # chunk 16 (slot 0's second chunk), 156, 242, 255
         m[..., p] = 0.0
     x = _host(xt)
     print("[case] persistent decode step, S 32768, open positions past cache_position", flush=True)
